@@ -1,0 +1,182 @@
+#!/usr/bin/env python3
+"""Batch-1 decode benchmark of the fused HIP decode step (one MI355X).
+
+A step is one decode token of the configured model (default: the
+Llama-3.2-1B-shaped fp32 model, BASELINE cfg 2: 64-token prompt, then greedy
+decode).  Weights are seeded N(0, 0.02) synthetic weights in the reference's
+.bin layout, generated on the host and uploaded once; the prompt and
+`--warmup` decode steps run untimed, then exactly `--steps` decode steps are
+timed with HIP events on the engine's stream, with a stream synchronisation
+on both sides.  Prints one JSON line.
+
+  value          decode tok/s (whole job: one GPU)
+  achieved_GBps  algorithmic HBM bytes of the timed steps / time
+  roofline       the dominant kernel (W1/W3 + SwiGLU GEMV) alone: algorithmic
+                 bytes per launch / its average duration, from an eager pass
+                 with HIP events between consecutive launches
+  cpu_baseline   the CPU oracle (a restatement of the reference CPU path,
+                 "port") on a bounded sample of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "batch-1 decode tok/s + achieved HBM GB/s (% of peak), Llama-3.2-1B fp32"
+
+
+def dominant_kernel_bytes(cfg) -> int:
+    """Algorithmic bytes of one W1/W3+SwiGLU launch: both weight matrices
+    (plus their int8 scales), the RMSNorm weight and residual read, h written."""
+    D, F = cfg.dim, cfg.hidden_dim
+    if cfg.quant:
+        w = 2 * (F * D + (F * D // cfg.group_size) * 4)
+    else:
+        w = 2 * F * D * 4
+    return w + 2 * D * 4 + F * 4
+
+
+def cpu_baseline(K, cfg, img, seconds: float) -> dict:
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    m = O.Model(img, cfg.family, cfg.quant)
+    threads = O.lib.or_get_threads()
+    prompt = K.prompt_tokens(cfg, 4)
+    tok = int(prompt[0])
+    for pos in range(len(prompt) - 1):
+        m.step(int(prompt[pos]), pos)
+    tok = int(prompt[-1])
+    pos = len(prompt) - 1
+    n, t0 = 0, time.perf_counter()
+    while True:
+        lg = m.step(tok, pos)
+        tok = O.argmax(lg)
+        pos += 1
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or pos >= cfg.seq_len - 1:
+            break
+    return {
+        "value": round(n / el, 4),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} greedy decode steps after a 4-token prompt (positions 3..{pos - 1}), "
+                  f"{el:.1f} s, {threads} OpenMP threads",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=0, help="timed decode steps (default: config)")
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="llama32_1b")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is described in DESIGN.md, not built)", file=sys.stderr)
+        return 2
+
+    import kuiperllama_amd as K
+
+    if K.device_count() < 1:
+        print("bench.py: no HIP device", file=sys.stderr)
+        return 1
+    cfg = K.BASELINE[args.config]
+    steps = args.steps or cfg.decode_steps
+    P = cfg.prompt_len
+    if P + args.warmup + steps - 1 > cfg.seq_len:
+        print("bench.py: prompt + warmup + steps exceed the model's seq_len", file=sys.stderr)
+        return 1
+    t0 = time.time()
+    img = K.synth_image(cfg)
+    t_img = time.time() - t0
+    eng = K.Engine(img, cfg)
+    eng.set_graph(not args.no_graph)
+    t_load = time.time() - t0 - t_img
+    prompt = K.prompt_tokens(cfg)
+    print(f"# {K.device_name(0)}; image {img.nbytes / 1e9:.2f} GB in {t_img:.1f} s, "
+          f"upload {t_load:.1f} s", file=sys.stderr, flush=True)
+
+    wall0 = time.perf_counter()
+    toks, ms = eng.bench(prompt, args.warmup, steps)
+    wall = time.perf_counter() - wall0
+    tok_s = steps / (ms / 1e3)
+    first_pos = P - 1 + args.warmup
+    step_bytes = cfg.decode_bytes(first_pos, steps)
+    gbps = step_bytes / (ms / 1e3) / 1e9
+    print(f"# decode {steps} steps in {ms:.2f} ms ({tok_s:.1f} tok/s, {gbps:.0f} GB/s); "
+          f"call wall {wall:.2f} s", file=sys.stderr, flush=True)
+
+    prof = eng.profile(int(toks[-1]), first_pos, args.profile_steps)
+    per_step_eager = sum(v[0] * v[1] for v in prof.values()) / args.profile_steps
+    w13_ms = prof["w13"][0]
+    w13_bytes = dominant_kernel_bytes(cfg)
+    w13_gbps = w13_bytes / (w13_ms / 1e3) / 1e9
+    print("# eager per-kernel avg ms: " + ", ".join(f"{k} {v[0]:.4f} x{v[1]}" for k, v in prof.items())
+          + f"; eager step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(K, cfg, img, args.cpu_seconds)
+        print(f"# cpu baseline {cpu}", file=sys.stderr, flush=True)
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8w-f32" if cfg.quant else "f32",
+        "data": "synthetic: seeded N(0,0.02) weights in the reference .bin layout, seeded "
+                "uniform prompt ids",
+        "config": {
+            "workload": f"{cfg.name}: batch-1 greedy decode, {P}-token prompt then {steps} timed "
+                        f"decode steps (positions {first_pos}..{first_pos + steps - 1})",
+            "model": cfg.name,
+            "global_batch": 1,
+            "seq_len": cfg.seq_len,
+            "parallelism": "single GPU",
+            "graph": not args.no_graph,
+        },
+        "achieved_GBps": round(gbps, 1),
+        "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+        "bytes_per_token": int(step_bytes / steps),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_w13_swiglu (RMSNorm + W1/W3 GEMV + SwiGLU)",
+            "achieved": round(w13_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(w13_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "bytes_per_launch": w13_bytes,
+            "avg_launch_ms": round(w13_ms, 5),
+        },
+        "kernels_eager_ms": {k: round(v[0], 5) for k, v in prof.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

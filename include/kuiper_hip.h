@@ -1,0 +1,235 @@
+/*
+ * kuiper_hip.h -- C ABI of the MI355X (gfx950) backend for KuiperLLama's
+ * batch-1 token-generation loop.
+ *
+ * Conventions
+ *  - Plain pointers, sizes and an opaque stream handle (a hipStream_t passed
+ *    as void*; NULL means the library's default stream).  No C++ or torch
+ *    types cross this boundary.
+ *  - Every function returns int: 0 on success, a positive hipError_t value
+ *    for a runtime failure, or a negative KL_E* code for a rejected argument.
+ *    Nothing throws or aborts.  kl_error_string() names a code.
+ *  - All tensor pointers of the op-level entry points are device pointers,
+ *    fp32 unless stated, row-major, exactly as the reference kernels take them.
+ *  - Launches are asynchronous on the given stream unless stated.
+ *
+ * Reference interfaces each group replaces are cited as file:line, relative
+ * to the KuiperLLama checkout (kuiper/source/op/kernels/kernels_interface.h is
+ * abbreviated KI).
+ */
+#ifndef KUIPER_HIP_H_
+#define KUIPER_HIP_H_
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ---- */
+#define KL_OK 0
+#define KL_EINVAL (-1)    /* bad argument (shape, null pointer, range) */
+#define KL_ENOMEM (-2)    /* device allocation failed */
+#define KL_EFORMAT (-3)   /* malformed model image */
+#define KL_EUNSUPP (-4)   /* combination the backend does not implement */
+#define KL_ETOKEN (-5)    /* token id outside [0, vocab) */
+#define KL_EWORKSPACE (-6)/* caller workspace too small */
+
+/* Model families (the reference picks them with -DLLAMA3_SUPPORT /
+ * -DQWEN2_SUPPORT / -DQWEN3_SUPPORT, CMakeLists.txt:29-47; here at run time). */
+#define KL_FAMILY_LLAMA2 0 /* interleaved RoPE, theta 1e4, eps 1e-5 */
+#define KL_FAMILY_LLAMA3 1 /* rotate-half RoPE, theta 5e5, eps 1e-5 */
+#define KL_FAMILY_QWEN2 2  /* rotate-half, theta 1e6, eps 1e-6, q/k/v bias */
+#define KL_FAMILY_QWEN3 3  /* rotate-half, theta 1e6, eps 1e-6, per-head q/k RMSNorm */
+
+/* RoPE pairings: kernels/cpu/rope_kernel.cpp:98-121 (interleaved) and
+ * :18-42 / :58-82 (rotate-half). */
+#define KL_ROPE_INTERLEAVED 0
+#define KL_ROPE_HALF 1
+
+const char* kl_error_string(int code);
+
+/* ---------------------------------------------------------------------------
+ * Runtime: device selection, memory, streams, events.
+ * Replaces base::CUDADeviceAllocator (include/base/alloc.h:59-66,
+ * source/base/alloc_cu.cpp:7-112: allocate/release/memcpy/memset_zero),
+ * kernel::CudaConfig (include/base/cuda_config.h:6-13) and the cudaSetDevice /
+ * cudaStreamCreate calls of LLama2Model::init (source/model/llama3.cpp:116-123).
+ * ------------------------------------------------------------------------- */
+int kl_device_count(int* count);
+int kl_set_device(int device);
+int kl_device_name(int device, char* buf, int buf_len);
+int kl_malloc(void** ptr, size_t bytes);
+int kl_free(void* ptr);
+int kl_host_alloc(void** ptr, size_t bytes); /* pinned host memory */
+int kl_host_free(void* ptr);
+int kl_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int kl_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int kl_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int kl_memset_zero(void* ptr, size_t bytes, void* stream);
+int kl_stream_create(void** stream);
+int kl_stream_destroy(void* stream);
+int kl_stream_sync(void* stream);
+int kl_device_sync(void);
+int kl_event_create(void** event);
+int kl_event_destroy(void* event);
+int kl_event_record(void* event, void* stream);
+int kl_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ---------------------------------------------------------------------------
+ * Op-level kernels.  Each mirrors one reference kernel typedef (KI:6-47) with
+ * the Tensor arguments unpacked to device pointers and sizes.
+ * ------------------------------------------------------------------------- */
+
+/* MatmulKernel (KI:9-10; cuda/matmul_kernel.cu:89-109, cpu/matmul_kernel.cpp:5-41):
+ * y[r] = scale * sum_c W[r*cols + c] * x[c]. */
+int kl_gemv_f32(const float* x, const float* W, float* y, int rows, int cols, float scale,
+                void* stream);
+
+/* MatmulKernelQuant (KI:12-14; cuda/matmul_kernel.cu:111-134):
+ * y[r] = sum_c x[c] * scales[(r*cols + c) / group_size] * float(q[r*cols + c]).
+ * q is int8 [rows x cols]; scales fp32 [rows*cols / group_size]. */
+int kl_gemv_q8(const float* x, const int8_t* q, const float* scales, float* y, int rows, int cols,
+               int group_size, void* stream);
+
+/* Dequantised weights, out[i] = scales[i / group_size] * float(q[i]): the
+ * per-element product inside the reference int8 GEMV (cuda/matmul_kernel.cu:73). */
+int kl_dequant_q8(const int8_t* q, const float* scales, int64_t n, int group_size, float* out,
+                  void* stream);
+
+/* RMSNormKernel (KI:30-31; cpu/rmsnorm_kernel.cpp:4-33, cuda/rmsnorm_kernel.cu:110-136):
+ * y = w * (x / sqrt(mean(x^2) + eps)).  eps is a build flag in the reference
+ * (1e-5 Llama, 1e-6 Qwen); here an argument.  y may alias x. */
+int kl_rmsnorm(const float* x, const float* w, float* y, int n, float eps, void* stream);
+
+/* RMSNormKernelDim (KI:33-34; cuda/rmsnorm_kernel.cu:138-164): the same on each
+ * of `rows` rows of length n with one shared weight vector (Qwen3 q/k norm). */
+int kl_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n, float eps,
+                    void* stream);
+
+/* sin_cos_cache_calc_cpu (cpu/rope_kernel.cpp:4-16, :44-56, :84-96):
+ * sin/cos(pos * theta^(-d/hd)) for pos < seq_len, d < head_size, computed on
+ * the host with the same float formula as the reference CPU path and copied
+ * to the device tables [seq_len x head_size].  Synchronous. */
+int kl_sincos_table(int head_size, int seq_len, float theta, float* sin_dev, float* cos_dev);
+
+/* RoPEKernel (KI:36-39; cpu/rope_kernel.cpp:18-121): rotates q [dim] and the
+ * first kv_dim entries' pairs of k in place at position pos. */
+int kl_rope(int style, int dim, int kv_dim, int head_size, float* q, float* k, int pos,
+            const float* sin_cache, const float* cos_cache, void* stream);
+
+/* MHAKernel (KI:22-28; cpu/mha_kernel.cpp:5-61, cuda/mha_kernel.cu:109-127):
+ * per head h (kv head h / kv_mul): softmax_t((q_h . K_t) / sqrt(hd)) . V_t over
+ * t in [0, pos], caches [layers][seq_len][kv_dim].  The reference's score
+ * buffer [head_num x seq_len] becomes a split-K workspace of
+ * kl_mha_workspace_size() bytes (zero it once before first use; the kernel
+ * leaves its counters at zero). */
+int kl_mha_workspace_size(int head_num, int kv_mul, int seq_len, int head_size, size_t* bytes);
+int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+           int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
+           const float* key_cache, const float* value_cache, void* stream);
+
+/* SwigluKernel (KI:19-20; cpu/swiglu_kernel.cpp:3-23): out = a*sigmoid(a)*b. */
+int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream);
+
+/* AddKernel (KI:6-7; cpu/add_kernel.cpp:5-19): out = a + b. */
+int kl_add(const float* a, const float* b, float* out, int n, void* stream);
+
+/* EmbeddingKernel (KI:16-17; cpu/emb_kernel.cpp:4-29, cuda/emb_kernel.cu:23-48):
+ * out[i, :] = table[tokens[i], :] for i < n_tokens (no 512-token cap).
+ * tokens is a DEVICE int32 array; ids outside [0, vocab) leave their row
+ * untouched and set *bad_token_flag (device int32, may be NULL) to 1. */
+int kl_embedding(const int32_t* tokens, int n_tokens, const float* table, int vocab, int dim,
+                 float* out, int32_t* bad_token_flag, void* stream);
+
+/* Sampler::sample (include/sampler/sampler.h:10; argmax_sampler.cpp:5-13,
+ * cuda/argmax_kernel.cu:73-87): first index of the maximum of x[0..n).  The
+ * index is written to *out_index (device int32); workspace of
+ * kl_argmax_workspace_size() bytes, zeroed once before first use. */
+int kl_argmax_workspace_size(int n, size_t* bytes);
+int kl_argmax(const float* x, int n, int32_t* out_index, void* workspace, size_t workspace_bytes,
+              void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Synthetic model images in the reference's .bin formats (the byte layouts
+ * written by tools/export_llama.py:79-131 (fp32 v0), :134-210 (int8 g64),
+ * tools/export_qwen2.py:79-134 (bias after each of wq/wk/wv) and
+ * tools/export_qwen3.py:55-102 (8-int header)).  Matrices, embeddings and
+ * biases are N(0, stddev) from a counter-based generator keyed by (seed,
+ * tensor role, layer, element); norm weights are 1.0; the unused freq tables
+ * of the v0/Qwen2 layouts are written as zeros.  Host-only, no GPU needed.
+ * ------------------------------------------------------------------------- */
+typedef struct kl_model_spec {
+  int32_t family;     /* KL_FAMILY_* */
+  int32_t dim;        /* model width */
+  int32_t q_dim;      /* heads * head_size (== dim except Qwen3) */
+  int32_t hidden_dim; /* FFN width */
+  int32_t layers;
+  int32_t heads;
+  int32_t kv_heads;
+  int32_t vocab;
+  int32_t seq_len;
+  int32_t tied;       /* classifier = embedding (not for int8 or Qwen3) */
+  int32_t group_size; /* 0: fp32 image; >0: int8 per-group image (Llama layout) */
+} kl_model_spec;
+
+int kl_synth_image_size(const kl_model_spec* spec, int64_t* bytes);
+int kl_synth_image(const kl_model_spec* spec, uint64_t seed, float stddev, void* out,
+                   int64_t out_bytes, int n_threads);
+/* The same N(0, stddev) stream for one tensor role/layer, for tests. */
+int kl_synth_normal(uint64_t seed, int32_t role, int32_t layer, float stddev, float* out,
+                    int64_t n);
+/* The int8 quantiser of the image writer (export_llama.py:49-73). */
+int kl_quantize_q8(const float* w, int64_t n, int group_size, int8_t* q, float* scales);
+
+/* ---------------------------------------------------------------------------
+ * Decode engine: the whole per-token step of model::LLama2Model /
+ * Qwen2Model / Qwen3Model (source/model/llama3.cpp:146-166, :599-744;
+ * qwen2.cpp:205-225, :640-801; qwen3.cpp:147-167, :459-640) on fused gfx950
+ * kernels, replayed as one HIP graph per step.
+ * ------------------------------------------------------------------------- */
+typedef struct kl_engine kl_engine;
+
+/* Parses a reference-format image (model/model.cpp:41-141 plus the loaders
+ * model/llama3.cpp:183-422, qwen2.cpp:348-485, qwen3.cpp:186-299) from host
+ * memory and uploads it to the current device.  quant != 0 selects the int8
+ * layout.  The image may be freed after the call. */
+int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_engine** out);
+int kl_engine_destroy(kl_engine* e);
+/* dims: {dim, q_dim, kv_dim, hidden, layers, heads, kv_heads, vocab, seq_len, head_size} */
+int kl_engine_dims(const kl_engine* e, int32_t* out10);
+int kl_engine_weight_bytes(const kl_engine* e, int64_t* bytes);
+int kl_engine_set_graph(kl_engine* e, int enable);
+/* Model::predict (model/model.h:21-22, llama3.cpp:641-649): embed `token`,
+ * run every layer at `pos`, final norm, classifier and argmax.  Blocks until
+ * done; *next (may be NULL) receives the argmax, logits (host, may be NULL)
+ * the vocab logits. */
+int kl_engine_step(kl_engine* e, int32_t token, int32_t pos, int32_t* next, float* logits);
+/* The demo/main.cpp:5-47 greedy loop entirely on the device: P prompt tokens
+ * at positions 0..P-1, then n_new sampled tokens (out_tokens[n_new]).
+ * *decode_ms (may be NULL) receives the device time of the n_new sampled
+ * steps (positions P-1 .. P+n_new-2), measured with HIP events. */
+int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, int32_t* out_tokens,
+                       float* decode_ms);
+/* Benchmark run: like kl_engine_generate with n_warmup + n_timed sampled
+ * tokens, where *timed_ms is the device time (HIP events on the engine's
+ * stream) of the last n_timed steps only.  out_tokens[n_warmup + n_timed]. */
+int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, int n_timed,
+                    int32_t* out_tokens, float* timed_ms);
+/* Per-kernel timing: runs `steps` decode steps from (token, pos0) without the
+ * graph, with a HIP event recorded between consecutive launches on the
+ * engine's stream, and returns the average duration and launch count per
+ * kernel kind: [embed, qkv, attn, wo, w13, w2, cls]. */
+int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, float* avg_ms7,
+                      int32_t* counts7);
+/* Device pointers for inspection: logits [vocab], key/value caches
+ * [layers][seq_len][kv_dim]. */
+int kl_engine_buffers(const kl_engine* e, const float** logits, const float** key_cache,
+                      const float** value_cache);
+/* Stream the engine launches on (a hipStream_t as void*). */
+int kl_engine_stream(const kl_engine* e, void** stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KUIPER_HIP_H_ */

@@ -1,0 +1,94 @@
+// Device helpers shared by the op-level and fused decode kernels (gfx950,
+// wave64).  Vector types are clang ext_vector types so that 16-byte loads can
+// carry the nontemporal hint.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kl {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int i4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // four wave64s per workgroup
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// Streaming (read-once) weight loads: the nontemporal hint keeps them from
+// evicting the small, reused activation vectors from the caches.
+__device__ __forceinline__ f4 load_stream(const f4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ i4 load_stream(const i4* p) { return __builtin_nontemporal_load(p); }
+
+__device__ __forceinline__ float hsum(f4 v) { return (v.x + v.y) + (v.z + v.w); }
+
+// Butterfly sum over all 64 lanes; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Block-wide sum for a 256-thread block; `red` is LDS scratch of >= 4 floats.
+// Every thread receives the total.  Contains barriers: call uniformly.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) t += red[w];
+  return t;
+}
+
+// (value, index) argmax with the reference's tie rule: the lower index wins
+// among equal values (std::max_element keeps the first maximum).
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, kWave);
+    const int oi = __shfl_xor(i, off, kWave);
+    argmax_merge(v, i, ov, oi);
+  }
+}
+
+// RoPE rotation of one pair, written without contraction so that the result
+// is the same float expression the reference CPU path evaluates
+// (kernels/cpu/rope_kernel.cpp:37-38 / :115-118): v0*c - v1*s, v0*s + v1*c.
+__device__ __forceinline__ void rope_pair(float& v0, float& v1, float fcr, float fci) {
+#pragma clang fp contract(off)
+  const float a = v0 * fcr - v1 * fci;
+  const float b = v0 * fci + v1 * fcr;
+  v0 = a;
+  v1 = b;
+}
+
+// Signed bytes of a dword as floats.
+__device__ __forceinline__ void unpack_i8x4(int w, float* o) {
+  o[0] = static_cast<float>((w << 24) >> 24);
+  o[1] = static_cast<float>((w << 16) >> 24);
+  o[2] = static_cast<float>((w << 8) >> 24);
+  o[3] = static_cast<float>(w >> 24);
+}
+
+}  // namespace kl

@@ -1,0 +1,971 @@
+// Fused batch-1 decode engine for the Llama2 / Llama3 / Qwen2 / Qwen3 step of
+// the reference (model/llama3.cpp:146-166, :599-744; model/qwen2.cpp:205-225,
+// :640-801; model/qwen3.cpp:147-167, :459-640).
+//
+// One token step is 5 kernels per layer plus 2 per token, replayed as a HIP
+// graph:
+//   embed      x = E[token]                       (state.token, device resident)
+//   per layer
+//     qkv      RMSNorm(x) staged in LDS, [Wq;Wk;Wv] GEMV, + bias (Qwen2),
+//              q -> q buffer, k/v -> cache slot at state.pos
+//     attn     (q/k norm) + RoPE + split-K attention + cross-chunk merge
+//     wo       x += Wo . attn
+//     w13      RMSNorm(x) staged in LDS, W1 and W3 rows side by side,
+//              h = silu(W1 x) * (W3 x)
+//     w2       x += W2 . h
+//   cls        final RMSNorm staged in LDS, classifier GEMV, logits, argmax
+//              partials, last workgroup picks the token and advances state
+// Every kernel reads the position from device memory, so the captured graph
+// is position independent; between replays only the device state changes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "attn.hpp"
+#include "device.hpp"
+#include "gemv.hpp"
+#include "kuiper_hip.h"
+
+using namespace kl;
+
+namespace {
+
+struct StepState {
+  int32_t pos;         // position processed by the next replay
+  int32_t token;       // token embedded by the next replay
+  int32_t prompt_len;  // positions < prompt_len - 1 take their successor from the prompt
+  int32_t sampled;     // argmax of the last computed logits
+};
+
+inline int rc(hipError_t e) { return e == hipSuccess ? KL_OK : static_cast<int>(e); }
+
+// ---------------------------------------------------------------------------
+// Kernels.
+// ---------------------------------------------------------------------------
+
+// Stage the GEMV input vector in LDS; with a norm weight, apply RMSNorm on the
+// way (kernels/cpu/rmsnorm_kernel.cpp:30-32: w * (x / sqrt(mean(x^2) + eps))).
+// Contains barriers: every thread of the block must call it.
+__device__ __forceinline__ void stage_input(const float* __restrict__ x,
+                                            const float* __restrict__ nw, float eps, int n,
+                                            float* xs, float* red) {
+  if (nw) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+      const float v = x[i];
+      ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+    for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = nw[i] * (r * x[i]);
+  } else {
+    for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = x[i];
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_embed(const StepState* __restrict__ st,
+                                              const float* __restrict__ E, int D,
+                                              float* __restrict__ x) {
+  const float* src = E + static_cast<size_t>(st->token) * D;
+  for (int c = threadIdx.x; c < D; c += kBlock) x[c] = src[c];
+}
+
+struct QkvArgs {
+  const float* x;
+  const float* nw;
+  float eps;
+  int D, Dq, Dkv, chunk_shift;
+  WView wq, wk, wv;
+  const float *bq, *bk, *bv;
+  float* q_out;
+  float* kcache;  // layer base
+  float* vcache;  // layer base
+  const StepState* st;
+};
+
+template <bool Q8, int R, int U>
+__global__ __launch_bounds__(256) void k_qkv(QkvArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float red[kWavesPerBlock];
+  stage_input(a.x, a.nw, a.eps, a.D, xs, red);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pos = a.st->pos;
+  const int total = a.Dq + 2 * a.Dkv;
+  const int nblk = (total + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
+  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int row0 = (b * kWavesPerBlock + wave) * R;
+    if (row0 >= total) continue;
+    WView w;
+    const float* bias;
+    float* out;
+    int lr, seg_rows;
+    if (row0 < a.Dq) {
+      w = a.wq; bias = a.bq; out = a.q_out; lr = row0; seg_rows = a.Dq;
+    } else if (row0 < a.Dq + a.Dkv) {
+      w = a.wk; bias = a.bk; out = a.kcache + static_cast<size_t>(pos) * a.Dkv;
+      lr = row0 - a.Dq; seg_rows = a.Dkv;
+    } else {
+      w = a.wv; bias = a.bv; out = a.vcache + static_cast<size_t>(pos) * a.Dkv;
+      lr = row0 - a.Dq - a.Dkv; seg_rows = a.Dkv;
+    }
+    const int nr = min(R, seg_rows - lr);
+    float part[R];
+    gemv_rows<Q8, R, U>(w, a.D, a.chunk_shift, lr, nr, xs, part);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(part[r]);
+      if (lane == 0 && r < nr) out[lr + r] = bias ? v + bias[lr + r] : v;
+    }
+  }
+}
+
+// x[row] += W[row, :] . in   (output projection and down projection + residual)
+struct ResArgs {
+  const float* in;
+  int cols, rows, chunk_shift;
+  WView w;
+  float* x;
+};
+
+template <bool Q8, int R, int U>
+__global__ __launch_bounds__(256) void k_gemv_residual(ResArgs a) {
+  extern __shared__ float xs[];
+  stage_input(a.in, nullptr, 0.f, a.cols, xs, nullptr);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nblk = (a.rows + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
+  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int row0 = (b * kWavesPerBlock + wave) * R;
+    if (row0 >= a.rows) continue;
+    const int nr = min(R, a.rows - row0);
+    float part[R];
+    gemv_rows<Q8, R, U>(a.w, a.cols, a.chunk_shift, row0, nr, xs, part);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(part[r]);
+      if (lane == 0 && r < nr) a.x[row0 + r] = a.x[row0 + r] + v;
+    }
+  }
+}
+
+// h[r] = silu(W1[r] . xn) * (W3[r] . xn), xn = RMSNorm(x): each wave streams RH
+// rows of W1 and the same RH rows of W3 together.
+struct W13Args {
+  const float* x;
+  const float* nw;
+  float eps;
+  int D, F, chunk_shift;
+  WView w1, w3;
+  float* h;
+};
+
+template <bool Q8, int RH, int U>
+__global__ __launch_bounds__(256) void k_w13_swiglu(W13Args a) {
+  extern __shared__ float xs[];
+  __shared__ float red[kWavesPerBlock];
+  stage_input(a.x, a.nw, a.eps, a.D, xs, red);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nblk = (a.F + RH * kWavesPerBlock - 1) / (RH * kWavesPerBlock);
+  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int row0 = (b * kWavesPerBlock + wave) * RH;
+    if (row0 >= a.F) continue;
+    const int nr = min(RH, a.F - row0);
+    float pa[RH], pb[RH];
+    gemv_rows_pair<Q8, RH, U>(a.w1, a.w3, a.D, a.chunk_shift, row0, nr, xs, pa, pb);
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const float va = wave_sum(pa[r]);
+      const float vb = wave_sum(pb[r]);
+      if (lane == 0 && r < nr) {
+        // kernels/cpu/swiglu_kernel.cpp:21-22
+        const float s = va * (1.0f / (1.0f + expf(-va)));
+        a.h[row0 + r] = s * vb;
+      }
+    }
+  }
+}
+
+// Classifier + greedy sampling.
+struct ClsArgs {
+  const float* x;
+  const float* nw;
+  float eps;
+  int D, V, chunk_shift;
+  WView w;
+  float* logits;
+  float* pv;
+  int* pi;
+  unsigned int* counter;
+  StepState* st;
+  const int32_t* prompt;
+  int32_t* out_tokens;
+};
+
+template <bool Q8, int R, int U>
+__global__ __launch_bounds__(256) void k_cls_argmax(ClsArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float red[kWavesPerBlock];
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  __shared__ int s_last;
+  const int pos = a.st->pos;
+  const int P = a.st->prompt_len;
+  if (pos + 1 < P) {
+    // A prompt position whose successor is already known: the reference
+    // computes logits here and discards them (demo/main.cpp:20-22, is_prompt);
+    // only the device state advances.
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      a.st->token = a.prompt[pos + 1];
+      a.st->pos = pos + 1;
+    }
+    return;
+  }
+  stage_input(a.x, a.nw, a.eps, a.D, xs, red);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+  const int nblk = (a.V + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
+  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int row0 = (b * kWavesPerBlock + wave) * R;
+    if (row0 >= a.V) continue;
+    const int nr = min(R, a.V - row0);
+    float part[R];
+    gemv_rows<Q8, R, U>(a.w, a.D, a.chunk_shift, row0, nr, xs, part);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(part[r]);
+      if (r < nr) {
+        if (lane == 0) a.logits[row0 + r] = v;
+        argmax_merge(bv, bi, v, row0 + r);
+      }
+    }
+  }
+  // Every lane of a wave holds the same (bv, bi); merge the waves.
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+    a.pv[blockIdx.x] = bv;
+    a.pi[blockIdx.x] = bi;
+    __threadfence();
+    const unsigned int prev = atomicAdd(a.counter, 1u);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  bv = -INFINITY;
+  bi = INT_MAX;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kBlock)
+    argmax_merge(bv, bi, a.pv[b], a.pi[b]);
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+    a.st->sampled = bi;
+    a.st->token = bi;
+    a.out_tokens[pos] = bi;
+    a.st->pos = pos + 1;
+    *a.counter = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Model image parsing (host).  Offsets follow model/model.cpp:41-141 and the
+// loaders model/llama3.cpp:183-422 (fp32 / int8), model/qwen2.cpp:348-485
+// (bias after each of wq/wk/wv) and model/qwen3.cpp:186-299.
+// ---------------------------------------------------------------------------
+struct HostTensor {
+  const char* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+struct LayerHost {
+  HostTensor rms_att, rms_ffn, wq, wk, wv, wo, w1, w2, w3, sq, sk, sv, so, s1, s2, s3, bq, bk, bv,
+      qn, kn;
+};
+
+struct ImageLayout {
+  int family = 0, quant = 0, gs = 0;
+  int D = 0, Dq = 0, Dkv = 0, F = 0, L = 0, H = 0, KVH = 0, V = 0, S = 0, hd = 0;
+  bool tied = false;
+  HostTensor emb, rms_final, wcls, scls;
+  std::vector<LayerHost> layers;
+};
+
+int parse_image(const void* image, size_t size, int family, int quant, ImageLayout* out) {
+  if (!image || family < KL_FAMILY_LLAMA2 || family > KL_FAMILY_QWEN3) return KL_EINVAL;
+  const bool qwen3 = family == KL_FAMILY_QWEN3;
+  if (quant && family != KL_FAMILY_LLAMA2 && family != KL_FAMILY_LLAMA3) return KL_EUNSUPP;
+  const size_t header_ints = (qwen3 || quant) ? 8 : 7;
+  if (size < header_ints * 4) return KL_EFORMAT;
+  const int32_t* h = static_cast<const int32_t*>(image);
+  ImageLayout& m = *out;
+  m.family = family;
+  m.quant = quant;
+  const int32_t dim = h[0], hidden = h[1], vocab = h[5];
+  m.L = h[2];
+  m.H = h[3];
+  m.KVH = h[4];
+  m.S = h[6];
+  if (dim <= 0 || hidden <= 0 || m.L <= 0 || m.H <= 0 || m.KVH <= 0 || vocab == 0 || m.S <= 0 ||
+      dim % m.H != 0 || m.H % m.KVH != 0)
+    return KL_EFORMAT;
+  m.V = std::abs(vocab);
+  m.hd = dim / m.H;
+  m.Dq = dim;
+  m.Dkv = dim / m.H * m.KVH;
+  if (qwen3) {
+    m.D = hidden;
+    m.F = h[7];
+    m.tied = false;
+    if (m.F <= 0) return KL_EFORMAT;
+  } else {
+    m.D = dim;
+    m.F = hidden;
+    m.tied = vocab > 0;
+  }
+  if (quant) {
+    m.gs = h[7];
+    if (m.gs <= 0) return KL_EFORMAT;
+    if (m.tied) return KL_EUNSUPP;  // llama3.cpp:258-267 reads fp32 bytes as int8
+  }
+  const char* base = static_cast<const char*>(image) + header_ints * 4;
+  const size_t avail = size - header_ints * 4;
+  size_t off = 0;
+  bool overflow = false;
+  auto take = [&](size_t bytes) {
+    HostTensor t{base + off, bytes};
+    off += bytes;
+    if (off > avail) overflow = true;
+    return t;
+  };
+  auto f32 = [&](size_t n) { return take(n * 4); };
+  const size_t L = m.L, D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F, V = m.V;
+  m.layers.assign(L, LayerHost{});
+  if (quant) {
+    const size_t gs = m.gs;
+    auto q8 = [&](size_t n, HostTensor* w, HostTensor* s) {
+      if (n % gs != 0) overflow = true;
+      *w = take(n);
+      *s = f32(n / gs);
+    };
+    for (auto& l : m.layers) q8(Dq * D, &l.wq, &l.sq);
+    for (auto& l : m.layers) q8(Dkv * D, &l.wk, &l.sk);
+    for (auto& l : m.layers) q8(Dkv * D, &l.wv, &l.sv);
+    for (auto& l : m.layers) q8(D * Dq, &l.wo, &l.so);
+    for (auto& l : m.layers) q8(F * D, &l.w1, &l.s1);
+    for (auto& l : m.layers) q8(D * F, &l.w2, &l.s2);
+    for (auto& l : m.layers) q8(F * D, &l.w3, &l.s3);
+    q8(V * D, &m.wcls, &m.scls);
+    m.emb = f32(V * D);
+    for (auto& l : m.layers) l.rms_att = f32(D);
+    for (auto& l : m.layers) l.rms_ffn = f32(D);
+    m.rms_final = f32(D);
+  } else if (qwen3) {
+    for (auto& l : m.layers) l.rms_att = f32(D);
+    for (auto& l : m.layers) l.rms_ffn = f32(D);
+    m.rms_final = f32(D);
+    m.emb = f32(V * D);
+    for (auto& l : m.layers) l.wq = f32(Dq * D);
+    for (auto& l : m.layers) l.qn = f32(m.hd);
+    for (auto& l : m.layers) l.wk = f32(Dkv * D);
+    for (auto& l : m.layers) l.kn = f32(m.hd);
+    for (auto& l : m.layers) l.wv = f32(Dkv * D);
+    for (auto& l : m.layers) l.wo = f32(D * Dq);
+    for (auto& l : m.layers) l.w1 = f32(F * D);
+    for (auto& l : m.layers) l.w2 = f32(D * F);
+    for (auto& l : m.layers) l.w3 = f32(F * D);
+    m.wcls = f32(V * D);
+  } else {
+    const bool bias = family == KL_FAMILY_QWEN2;
+    m.emb = f32(V * D);
+    for (auto& l : m.layers) l.rms_att = f32(D);
+    for (auto& l : m.layers) {
+      l.wq = f32(Dq * D);
+      if (bias) l.bq = f32(Dq);
+    }
+    for (auto& l : m.layers) {
+      l.wk = f32(Dkv * D);
+      if (bias) l.bk = f32(Dkv);
+    }
+    for (auto& l : m.layers) {
+      l.wv = f32(Dkv * D);
+      if (bias) l.bv = f32(Dkv);
+    }
+    for (auto& l : m.layers) l.wo = f32(D * Dq);
+    for (auto& l : m.layers) l.rms_ffn = f32(D);
+    for (auto& l : m.layers) l.w1 = f32(F * D);
+    for (auto& l : m.layers) l.w2 = f32(D * F);
+    for (auto& l : m.layers) l.w3 = f32(F * D);
+    m.rms_final = f32(D);
+    f32(static_cast<size_t>(m.S) * m.hd);  // freq_cos + freq_sin, unused
+    if (!m.tied) m.wcls = f32(V * D);
+  }
+  if (overflow) return KL_EFORMAT;
+  return KL_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Engine.
+// ---------------------------------------------------------------------------
+struct LayerDev {
+  const float *rms_att, *rms_ffn, *bq, *bk, *bv, *qn, *kn;
+  WView wq, wk, wv, wo, w1, w2, w3;
+};
+
+struct kl_engine {
+  ImageLayout lay;  // host pointers are not kept valid after create
+  int family = 0, quant = 0, chunk_shift = 0;
+  float eps = 1e-5f, theta = 1e4f;
+  int rope_style = KL_ROPE_INTERLEAVED, transform = 1;
+  int cus = 256;
+  hipStream_t stream = nullptr;
+  char* arena = nullptr;
+  size_t arena_bytes = 0, weight_bytes = 0;
+  const float* emb = nullptr;
+  const float* rms_final = nullptr;
+  WView wcls{};
+  std::vector<LayerDev> layers;
+  float *sin_t = nullptr, *cos_t = nullptr, *kcache = nullptr, *vcache = nullptr;
+  float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+  float* attn_part = nullptr;
+  unsigned int* attn_counters = nullptr;
+  float* am_pv = nullptr;
+  int* am_pi = nullptr;
+  unsigned int* am_counter = nullptr;
+  StepState* st = nullptr;
+  StepState* st_host = nullptr;  // pinned staging
+  int32_t* prompt = nullptr;
+  int32_t* out_tokens = nullptr;
+  MhaPlan attn{};
+  int grid_cap = 1024;
+  bool use_graph = true;
+  hipGraphExec_t graph_exec = nullptr;
+  hipGraph_t graph = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace {
+
+// Tile choices (rows per wave R, 16-byte chunks in flight per row U).
+constexpr int kR = 2, kU = 4;    // qkv, residual GEMVs, classifier
+constexpr int kRH = 1, kUH = 4;  // W1/W3 pair: 2 rows per wave
+
+size_t lds_for(int n) { return static_cast<size_t>(n) * sizeof(float); }
+
+int grid_for(const kl_engine* e, int rows, int rows_per_block) {
+  const int nblk = (rows + rows_per_block - 1) / rows_per_block;
+  return std::max(1, std::min(nblk, e->grid_cap));
+}
+
+// Kernel kinds, in launch order within a layer; used by the profiler.
+enum KernelKind { kKEmbed = 0, kKQkv, kKAttn, kKWo, kKW13, kKW2, kKCls, kKinds };
+
+// With `marks` set (eager profiling only), an event is recorded on the
+// stream before every launch and after the last one; marks[i] then brackets
+// kernel i and kinds[i] names it.
+struct Marks {
+  std::vector<hipEvent_t>* ev;
+  std::vector<int>* kinds;
+};
+
+inline void mark(hipStream_t s, Marks* mk, int kind) {
+  if (!mk) return;
+  hipEvent_t ev;
+  if (hipEventCreate(&ev) != hipSuccess) return;
+  (void)hipEventRecord(ev, s);
+  mk->ev->push_back(ev);
+  mk->kinds->push_back(kind);
+}
+
+template <bool Q8>
+int launch_step_t(kl_engine* e, Marks* mk) {
+  const ImageLayout& m = e->lay;
+  hipStream_t s = e->stream;
+  const int rpb = kR * kWavesPerBlock;
+  mark(s, mk, kKEmbed);
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, s, e->st, e->emb, m.D, e->x);
+  const size_t kv_layer = static_cast<size_t>(m.S) * m.Dkv;
+  for (int l = 0; l < m.L; ++l) {
+    const LayerDev& L = e->layers[l];
+    QkvArgs qa{};
+    qa.x = e->x; qa.nw = L.rms_att; qa.eps = e->eps;
+    qa.D = m.D; qa.Dq = m.Dq; qa.Dkv = m.Dkv; qa.chunk_shift = e->chunk_shift;
+    qa.wq = L.wq; qa.wk = L.wk; qa.wv = L.wv; qa.bq = L.bq; qa.bk = L.bk; qa.bv = L.bv;
+    qa.q_out = e->q;
+    qa.kcache = e->kcache + l * kv_layer;
+    qa.vcache = e->vcache + l * kv_layer;
+    qa.st = e->st;
+    mark(s, mk, kKQkv);
+    hipLaunchKernelGGL((k_qkv<Q8, kR, kU>), dim3(grid_for(e, m.Dq + 2 * m.Dkv, rpb)),
+                       dim3(kBlock), lds_for(m.D), s, qa);
+
+    AttnArgs aa{};
+    aa.q = e->q;
+    aa.kcache = e->kcache + l * kv_layer;
+    aa.vcache = e->vcache + l * kv_layer;
+    aa.out = e->att;
+    aa.part = e->attn_part;
+    aa.counters = e->attn_counters;
+    aa.pos_ptr = &e->st->pos;
+    aa.kv_dim = m.Dkv;
+    aa.kv_mul = m.H / m.KVH;
+    aa.G = e->attn.G;
+    aa.min_chunk = e->attn.min_chunk;
+    aa.ch_max = e->attn.ch_max;
+    aa.transform = e->transform;
+    aa.rope_style = e->rope_style;
+    aa.sin_t = e->sin_t;
+    aa.cos_t = e->cos_t;
+    aa.qn = L.qn;
+    aa.kn = L.kn;
+    aa.qk_eps = 1e-6f;  // kernels/cuda/rmsnorm_kernel.cu:148
+    aa.scale = 1.f / std::sqrt(static_cast<float>(m.hd));
+    const dim3 ag(m.KVH * e->attn.G);
+    mark(s, mk, kKAttn);
+    switch (m.hd) {
+      case 32: hipLaunchKernelGGL(k_attn_decode<32>, ag, dim3(256), e->attn.lds_bytes, s, aa); break;
+      case 64: hipLaunchKernelGGL(k_attn_decode<64>, ag, dim3(256), e->attn.lds_bytes, s, aa); break;
+      case 128: hipLaunchKernelGGL(k_attn_decode<128>, ag, dim3(256), e->attn.lds_bytes, s, aa); break;
+      default: hipLaunchKernelGGL(k_attn_decode<256>, ag, dim3(256), e->attn.lds_bytes, s, aa); break;
+    }
+
+    ResArgs ra{};
+    ra.in = e->att; ra.cols = m.Dq; ra.rows = m.D; ra.chunk_shift = e->chunk_shift;
+    ra.w = L.wo; ra.x = e->x;
+    mark(s, mk, kKWo);
+    hipLaunchKernelGGL((k_gemv_residual<Q8, kR, kU>), dim3(grid_for(e, m.D, rpb)), dim3(kBlock),
+                       lds_for(m.Dq), s, ra);
+
+    W13Args wa{};
+    wa.x = e->x; wa.nw = L.rms_ffn; wa.eps = e->eps;
+    wa.D = m.D; wa.F = m.F; wa.chunk_shift = e->chunk_shift;
+    wa.w1 = L.w1; wa.w3 = L.w3; wa.h = e->h;
+    mark(s, mk, kKW13);
+    hipLaunchKernelGGL((k_w13_swiglu<Q8, kRH, kUH>),
+                       dim3(grid_for(e, m.F, kRH * kWavesPerBlock)), dim3(kBlock), lds_for(m.D), s,
+                       wa);
+
+    ResArgs rb{};
+    rb.in = e->h; rb.cols = m.F; rb.rows = m.D; rb.chunk_shift = e->chunk_shift;
+    rb.w = L.w2; rb.x = e->x;
+    mark(s, mk, kKW2);
+    hipLaunchKernelGGL((k_gemv_residual<Q8, kR, kU>), dim3(grid_for(e, m.D, rpb)), dim3(kBlock),
+                       lds_for(m.F), s, rb);
+  }
+  ClsArgs ca{};
+  ca.x = e->x; ca.nw = e->rms_final; ca.eps = e->eps;
+  ca.D = m.D; ca.V = m.V; ca.chunk_shift = e->chunk_shift;
+  ca.w = e->wcls; ca.logits = e->logits;
+  ca.pv = e->am_pv; ca.pi = e->am_pi; ca.counter = e->am_counter;
+  ca.st = e->st; ca.prompt = e->prompt; ca.out_tokens = e->out_tokens;
+  mark(s, mk, kKCls);
+  hipLaunchKernelGGL((k_cls_argmax<Q8, kR, kU>), dim3(grid_for(e, m.V, rpb)), dim3(kBlock),
+                     lds_for(m.D), s, ca);
+  mark(s, mk, kKinds);
+  return rc(hipGetLastError());
+}
+
+int launch_step(kl_engine* e, Marks* mk = nullptr) {
+  return e->quant ? launch_step_t<true>(e, mk) : launch_step_t<false>(e, mk);
+}
+
+int run_step(kl_engine* e) {
+  if (!e->use_graph) return launch_step(e);
+  if (!e->graph_exec) {
+    hipError_t err = hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal);
+    if (err != hipSuccess) return rc(err);
+    const int lrc = launch_step(e);
+    hipGraph_t g = nullptr;
+    err = hipStreamEndCapture(e->stream, &g);
+    if (lrc != KL_OK) {
+      if (g) (void)hipGraphDestroy(g);
+      return lrc;
+    }
+    if (err != hipSuccess) return rc(err);
+    err = hipGraphInstantiate(&e->graph_exec, g, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+      (void)hipGraphDestroy(g);
+      e->graph_exec = nullptr;
+      return rc(err);
+    }
+    e->graph = g;
+  }
+  return rc(hipGraphLaunch(e->graph_exec, e->stream));
+}
+
+void release(kl_engine* e) {
+  if (!e) return;
+  if (e->graph_exec) (void)hipGraphExecDestroy(e->graph_exec);
+  if (e->graph) (void)hipGraphDestroy(e->graph);
+  if (e->ev0) (void)hipEventDestroy(e->ev0);
+  if (e->ev1) (void)hipEventDestroy(e->ev1);
+  if (e->arena) (void)hipFree(e->arena);
+  if (e->st_host) (void)hipHostFree(e->st_host);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_engine** out) {
+  if (!out) return KL_EINVAL;
+  *out = nullptr;
+  ImageLayout lay;
+  int prc = parse_image(image, bytes, family, quant, &lay);
+  if (prc != KL_OK) return prc;
+  const int kv_mul = lay.H / lay.KVH;
+  if (!mha_shape_ok(lay.H, kv_mul, lay.hd)) return KL_EUNSUPP;
+  if (lay.D % 4 != 0 || lay.Dq % 4 != 0 || lay.F % 4 != 0) return KL_EUNSUPP;
+  int chunk_shift = 0;
+  if (quant) {
+    const int cpg = lay.gs / 16;
+    if (lay.gs % 16 != 0 || (cpg & (cpg - 1)) != 0 || lay.D % lay.gs != 0 ||
+        lay.Dq % lay.gs != 0 || lay.F % lay.gs != 0)
+      return KL_EUNSUPP;
+    while ((1 << chunk_shift) < cpg) ++chunk_shift;
+  }
+
+  kl_engine* e = new kl_engine();
+  e->lay = lay;
+  e->family = family;
+  e->quant = quant;
+  e->chunk_shift = chunk_shift;
+  switch (family) {
+    case KL_FAMILY_LLAMA2: e->eps = 1e-5f; e->theta = 10000.f; e->rope_style = KL_ROPE_INTERLEAVED; break;
+    case KL_FAMILY_LLAMA3: e->eps = 1e-5f; e->theta = 500000.f; e->rope_style = KL_ROPE_HALF; break;
+    case KL_FAMILY_QWEN2: e->eps = 1e-6f; e->theta = 1000000.f; e->rope_style = KL_ROPE_HALF; break;
+    default: e->eps = 1e-6f; e->theta = 1000000.f; e->rope_style = KL_ROPE_HALF; break;
+  }
+  e->transform = family == KL_FAMILY_QWEN3 ? 2 : 1;
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+    e->cus = prop.multiProcessorCount;
+  e->grid_cap = e->cus * 4;
+  if (const char* env = std::getenv("KL_GRID_PER_CU")) {
+    const int v = std::atoi(env);
+    if (v > 0) e->grid_cap = e->cus * v;
+  }
+  e->attn = mha_plan(lay.KVH, kv_mul, lay.S, lay.hd);
+
+  // Arena plan: every tensor 256-byte aligned.
+  size_t cursor = 0;
+  auto plan = [&](size_t bytes) {
+    const size_t at = cursor;
+    cursor += (bytes + 255) & ~size_t(255);
+    return at;
+  };
+  struct Slot {
+    const HostTensor* src;
+    size_t at;
+  };
+  std::vector<Slot> slots;
+  auto place = [&](const HostTensor& t) -> size_t {
+    if (!t.ptr) return SIZE_MAX;
+    const size_t at = plan(t.bytes);
+    slots.push_back({&t, at});
+    return at;
+  };
+  struct LayerOff {
+    size_t rms_att, rms_ffn, bq, bk, bv, qn, kn, wq, wk, wv, wo, w1, w2, w3, sq, sk, sv, so, s1, s2,
+        s3;
+  };
+  const size_t emb_at = place(e->lay.emb);
+  const size_t fin_at = place(e->lay.rms_final);
+  const size_t cls_at = e->lay.wcls.ptr ? place(e->lay.wcls) : SIZE_MAX;
+  const size_t scls_at = e->lay.scls.ptr ? place(e->lay.scls) : SIZE_MAX;
+  std::vector<LayerOff> lo(lay.L);
+  for (int l = 0; l < lay.L; ++l) {
+    const LayerHost& H = e->lay.layers[l];
+    LayerOff& o = lo[l];
+    o.rms_att = place(H.rms_att); o.rms_ffn = place(H.rms_ffn);
+    o.bq = place(H.bq); o.bk = place(H.bk); o.bv = place(H.bv);
+    o.qn = place(H.qn); o.kn = place(H.kn);
+    o.wq = place(H.wq); o.wk = place(H.wk); o.wv = place(H.wv); o.wo = place(H.wo);
+    o.w1 = place(H.w1); o.w2 = place(H.w2); o.w3 = place(H.w3);
+    o.sq = place(H.sq); o.sk = place(H.sk); o.sv = place(H.sv); o.so = place(H.so);
+    o.s1 = place(H.s1); o.s2 = place(H.s2); o.s3 = place(H.s3);
+  }
+  size_t wbytes = 0;
+  for (const Slot& sl : slots) wbytes += sl.src->bytes;
+  e->weight_bytes = wbytes;
+  const size_t S = lay.S, Dkv = lay.Dkv;
+  const size_t sin_at = plan(S * lay.hd * 4), cos_at = plan(S * lay.hd * 4);
+  const size_t kc_at = plan(static_cast<size_t>(lay.L) * S * Dkv * 4);
+  const size_t vc_at = plan(static_cast<size_t>(lay.L) * S * Dkv * 4);
+  const size_t x_at = plan(lay.D * 4), q_at = plan(lay.Dq * 4), att_at = plan(lay.Dq * 4);
+  const size_t h_at = plan(static_cast<size_t>(lay.F) * 4), lg_at = plan(static_cast<size_t>(lay.V) * 4);
+  const size_t part_at = plan(e->attn.part_floats * 4);
+  // Zero-initialised region: counters and state.
+  const size_t zero_begin = cursor;
+  const size_t actr_at = plan(lay.KVH * sizeof(unsigned int));
+  const size_t amc_at = plan(64);
+  const size_t st_at = plan(sizeof(StepState));
+  const size_t zero_end = cursor;
+  const int gmax = e->grid_cap;
+  const size_t pv_at = plan(gmax * 4), pi_at = plan(gmax * 4);
+  const size_t pr_at = plan(S * 4), ot_at = plan(S * 4);
+  e->arena_bytes = cursor;
+
+  hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+  if (err == hipSuccess) err = hipMalloc(&e->arena, e->arena_bytes);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    release(e);
+    return err == hipErrorOutOfMemory ? KL_ENOMEM : rc(err);
+  }
+  for (const Slot& sl : slots) {
+    err = hipMemcpy(e->arena + sl.at, sl.src->ptr, sl.src->bytes, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+      release(e);
+      return rc(err);
+    }
+  }
+  auto P = [&](size_t at) -> char* { return at == SIZE_MAX ? nullptr : e->arena + at; };
+  auto PF = [&](size_t at) { return reinterpret_cast<float*>(P(at)); };
+  e->emb = PF(emb_at);
+  e->rms_final = PF(fin_at);
+  if (quant) {
+    e->wcls = WView{P(cls_at), PF(scls_at)};
+  } else {
+    e->wcls = WView{lay.tied ? static_cast<const void*>(e->emb) : P(cls_at), nullptr};
+  }
+  e->layers.resize(lay.L);
+  for (int l = 0; l < lay.L; ++l) {
+    const LayerOff& o = lo[l];
+    LayerDev& d = e->layers[l];
+    d.rms_att = PF(o.rms_att); d.rms_ffn = PF(o.rms_ffn);
+    d.bq = PF(o.bq); d.bk = PF(o.bk); d.bv = PF(o.bv);
+    d.qn = PF(o.qn); d.kn = PF(o.kn);
+    d.wq = WView{P(o.wq), PF(o.sq)}; d.wk = WView{P(o.wk), PF(o.sk)};
+    d.wv = WView{P(o.wv), PF(o.sv)}; d.wo = WView{P(o.wo), PF(o.so)};
+    d.w1 = WView{P(o.w1), PF(o.s1)}; d.w2 = WView{P(o.w2), PF(o.s2)};
+    d.w3 = WView{P(o.w3), PF(o.s3)};
+  }
+  e->sin_t = PF(sin_at);
+  e->cos_t = PF(cos_at);
+  e->kcache = PF(kc_at);
+  e->vcache = PF(vc_at);
+  e->x = PF(x_at);
+  e->q = PF(q_at);
+  e->att = PF(att_at);
+  e->h = PF(h_at);
+  e->logits = PF(lg_at);
+  e->attn_part = PF(part_at);
+  e->attn_counters = reinterpret_cast<unsigned int*>(P(actr_at));
+  e->am_counter = reinterpret_cast<unsigned int*>(P(amc_at));
+  e->st = reinterpret_cast<StepState*>(P(st_at));
+  e->am_pv = PF(pv_at);
+  e->am_pi = reinterpret_cast<int*>(P(pi_at));
+  e->prompt = reinterpret_cast<int32_t*>(P(pr_at));
+  e->out_tokens = reinterpret_cast<int32_t*>(P(ot_at));
+  e->lay.layers.clear();  // host pointers are no longer needed
+  err = hipMemset(e->arena + zero_begin, 0, zero_end - zero_begin);
+  if (err == hipSuccess) err = hipMemset(e->kcache, 0, 2 * static_cast<size_t>(lay.L) * S * Dkv * 4);
+  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void**>(&e->st_host), sizeof(StepState), hipHostMallocDefault);
+  if (err == hipSuccess) err = hipEventCreate(&e->ev0);
+  if (err == hipSuccess) err = hipEventCreate(&e->ev1);
+  if (err != hipSuccess) {
+    release(e);
+    return rc(err);
+  }
+  const int trc = kl_sincos_table(lay.hd, lay.S, e->theta, e->sin_t, e->cos_t);
+  if (trc != KL_OK) {
+    release(e);
+    return trc;
+  }
+  *out = e;
+  return KL_OK;
+}
+
+int kl_engine_destroy(kl_engine* e) {
+  if (!e) return KL_EINVAL;
+  (void)hipStreamSynchronize(e->stream);
+  release(e);
+  return KL_OK;
+}
+
+int kl_engine_dims(const kl_engine* e, int32_t* o) {
+  if (!e || !o) return KL_EINVAL;
+  const ImageLayout& m = e->lay;
+  o[0] = m.D; o[1] = m.Dq; o[2] = m.Dkv; o[3] = m.F; o[4] = m.L;
+  o[5] = m.H; o[6] = m.KVH; o[7] = m.V; o[8] = m.S; o[9] = m.hd;
+  return KL_OK;
+}
+
+int kl_engine_weight_bytes(const kl_engine* e, int64_t* bytes) {
+  if (!e || !bytes) return KL_EINVAL;
+  *bytes = static_cast<int64_t>(e->weight_bytes);
+  return KL_OK;
+}
+
+int kl_engine_set_graph(kl_engine* e, int enable) {
+  if (!e) return KL_EINVAL;
+  e->use_graph = enable != 0;
+  return KL_OK;
+}
+
+int kl_engine_step(kl_engine* e, int32_t token, int32_t pos, int32_t* next, float* logits) {
+  if (!e) return KL_EINVAL;
+  if (pos < 0 || pos >= e->lay.S) return KL_EINVAL;
+  if (token < 0 || token >= e->lay.V) return KL_ETOKEN;
+  *e->st_host = StepState{pos, token, 0, 0};
+  hipError_t err =
+      hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  if (err != hipSuccess) return rc(err);
+  const int r = run_step(e);
+  if (r != KL_OK) return r;
+  if (logits) {
+    err = hipMemcpyAsync(logits, e->logits, sizeof(float) * e->lay.V, hipMemcpyDeviceToHost,
+                         e->stream);
+    if (err != hipSuccess) return rc(err);
+  }
+  err = hipMemcpyAsync(e->st_host, e->st, sizeof(StepState), hipMemcpyDeviceToHost, e->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+  if (err != hipSuccess) return rc(err);
+  if (next) *next = e->st_host->sampled;
+  return KL_OK;
+}
+
+int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, int32_t* out_tokens,
+                       float* decode_ms) {
+  if (!e || !prompt || !out_tokens || P <= 0 || n_new <= 0) return KL_EINVAL;
+  if (P + n_new - 1 > e->lay.S) return KL_EINVAL;
+  for (int i = 0; i < P; ++i)
+    if (prompt[i] < 0 || prompt[i] >= e->lay.V) return KL_ETOKEN;
+  hipError_t err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
+                                  e->stream);
+  if (err != hipSuccess) return rc(err);
+  *e->st_host = StepState{0, prompt[0], P, 0};
+  err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  if (err != hipSuccess) return rc(err);
+  // Prompt positions 0 .. P-2, then n_new sampled positions P-1 .. P+n_new-2.
+  for (int i = 0; i < P - 1; ++i) {
+    const int r = run_step(e);
+    if (r != KL_OK) return r;
+  }
+  err = hipEventRecord(e->ev0, e->stream);
+  if (err != hipSuccess) return rc(err);
+  for (int i = 0; i < n_new; ++i) {
+    const int r = run_step(e);
+    if (r != KL_OK) return r;
+  }
+  err = hipEventRecord(e->ev1, e->stream);
+  if (err == hipSuccess)
+    err = hipMemcpyAsync(out_tokens, e->out_tokens + (P - 1), sizeof(int32_t) * n_new,
+                         hipMemcpyDeviceToHost, e->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+  if (err != hipSuccess) return rc(err);
+  if (decode_ms) {
+    err = hipEventElapsedTime(decode_ms, e->ev0, e->ev1);
+    if (err != hipSuccess) return rc(err);
+  }
+  return KL_OK;
+}
+
+int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, int n_timed,
+                    int32_t* out_tokens, float* timed_ms) {
+  if (!e || !prompt || !out_tokens || !timed_ms || P <= 0 || n_warmup < 0 || n_timed <= 0)
+    return KL_EINVAL;
+  if (P + n_warmup + n_timed - 1 > e->lay.S) return KL_EINVAL;
+  for (int i = 0; i < P; ++i)
+    if (prompt[i] < 0 || prompt[i] >= e->lay.V) return KL_ETOKEN;
+  hipError_t err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
+                                  e->stream);
+  if (err != hipSuccess) return rc(err);
+  *e->st_host = StepState{0, prompt[0], P, 0};
+  err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  if (err != hipSuccess) return rc(err);
+  for (int i = 0; i < P - 1 + n_warmup; ++i) {
+    const int r = run_step(e);
+    if (r != KL_OK) return r;
+  }
+  err = hipStreamSynchronize(e->stream);
+  if (err == hipSuccess) err = hipEventRecord(e->ev0, e->stream);
+  if (err != hipSuccess) return rc(err);
+  for (int i = 0; i < n_timed; ++i) {
+    const int r = run_step(e);
+    if (r != KL_OK) return r;
+  }
+  err = hipEventRecord(e->ev1, e->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+  if (err == hipSuccess) err = hipEventElapsedTime(timed_ms, e->ev0, e->ev1);
+  if (err == hipSuccess)
+    err = hipMemcpy(out_tokens, e->out_tokens + (P - 1), sizeof(int32_t) * (n_warmup + n_timed),
+                    hipMemcpyDeviceToHost);
+  return rc(err);
+}
+
+int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, float* avg_ms,
+                      int32_t* counts) {
+  if (!e || !avg_ms || !counts || steps <= 0) return KL_EINVAL;
+  if (pos0 < 0 || pos0 + steps > e->lay.S) return KL_EINVAL;
+  if (token < 0 || token >= e->lay.V) return KL_ETOKEN;
+  for (int k = 0; k < kKinds; ++k) {
+    avg_ms[k] = 0.f;
+    counts[k] = 0;
+  }
+  *e->st_host = StepState{pos0, token, 0, 0};
+  hipError_t err =
+      hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  if (err != hipSuccess) return rc(err);
+  std::vector<hipEvent_t> ev;
+  std::vector<int> kinds;
+  Marks mk{&ev, &kinds};
+  int r = KL_OK;
+  for (int i = 0; i < steps && r == KL_OK; ++i) r = launch_step(e, &mk);
+  err = hipStreamSynchronize(e->stream);
+  if (r == KL_OK && err != hipSuccess) r = rc(err);
+  for (size_t i = 0; r == KL_OK && i + 1 < ev.size(); ++i) {
+    if (kinds[i] == kKinds) continue;  // end-of-step mark
+    float ms = 0.f;
+    err = hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+    if (err != hipSuccess) {
+      r = rc(err);
+      break;
+    }
+    avg_ms[kinds[i]] += ms;
+    counts[kinds[i]] += 1;
+  }
+  for (hipEvent_t x : ev) (void)hipEventDestroy(x);
+  if (r != KL_OK) return r;
+  for (int k = 0; k < kKinds; ++k)
+    if (counts[k]) avg_ms[k] /= static_cast<float>(counts[k]);
+  return KL_OK;
+}
+
+int kl_engine_buffers(const kl_engine* e, const float** logits, const float** key_cache,
+                      const float** value_cache) {
+  if (!e) return KL_EINVAL;
+  if (logits) *logits = e->logits;
+  if (key_cache) *key_cache = e->kcache;
+  if (value_cache) *value_cache = e->vcache;
+  return KL_OK;
+}
+
+int kl_engine_stream(const kl_engine* e, void** stream) {
+  if (!e || !stream) return KL_EINVAL;
+  *stream = e->stream;
+  return KL_OK;
+}
+
+}  // extern "C"

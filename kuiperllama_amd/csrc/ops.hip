@@ -1,0 +1,560 @@
+// Op-level C ABI: runtime (memory, streams, events) and one launcher per
+// reference kernel typedef (kuiper/source/op/kernels/kernels_interface.h:6-47).
+// Every launcher validates its arguments on the host, so a kernel is never
+// launched with a shape it does not handle.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "attn.hpp"
+#include "device.hpp"
+#include "gemv.hpp"
+#include "kuiper_hip.h"
+
+using namespace kl;
+
+namespace {
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+inline int rc(hipError_t e) { return e == hipSuccess ? KL_OK : static_cast<int>(e); }
+inline int launch_rc() { return rc(hipGetLastError()); }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// GEMV (MatmulKernel / MatmulKernelQuant).
+// ---------------------------------------------------------------------------
+constexpr int kGemvR = 2;  // rows per wave
+constexpr int kGemvU = 4;  // 16-byte chunks per row in flight per lane
+constexpr int kRowsPerBlock = kGemvR * kWavesPerBlock;
+
+template <int R, int U>
+__global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ x,
+                                                 const float* __restrict__ W, float* __restrict__ y,
+                                                 int rows, int cols, float scale) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nblk = (rows + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
+  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int row0 = (b * kWavesPerBlock + wave) * R;
+    if (row0 >= rows) continue;
+    const int nr = min(R, rows - row0);
+    float part[R];
+    gemv_rows<false, R, U>(WView{W, nullptr}, cols, 0, row0, nr, x, part);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(part[r]);
+      if (lane == 0 && r < nr) y[row0 + r] = v * scale;
+    }
+  }
+}
+
+// Any shape / alignment: one wave per row, scalar loads.
+__global__ __launch_bounds__(256) void k_gemv_f32_scalar(const float* __restrict__ x,
+                                                        const float* __restrict__ W,
+                                                        float* __restrict__ y, int rows, int cols,
+                                                        float scale) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int r = blockIdx.x * kWavesPerBlock + wave; r < rows; r += gridDim.x * kWavesPerBlock) {
+    const float* wr = W + static_cast<size_t>(r) * cols;
+    float acc = 0.f;
+    for (int c = lane; c < cols; c += kWave) acc += wr[c] * x[c];
+    acc = wave_sum(acc);
+    if (lane == 0) y[r] = acc * scale;
+  }
+}
+
+template <int R, int U>
+__global__ __launch_bounds__(256) void k_gemv_q8(const float* __restrict__ x,
+                                                const int8_t* __restrict__ W,
+                                                const float* __restrict__ S, float* __restrict__ y,
+                                                int rows, int cols, int chunk_shift) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nblk = (rows + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
+  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int row0 = (b * kWavesPerBlock + wave) * R;
+    if (row0 >= rows) continue;
+    const int nr = min(R, rows - row0);
+    float part[R];
+    gemv_rows<true, R, U>(WView{W, S}, cols, chunk_shift, row0, nr, x, part);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(part[r]);
+      if (lane == 0 && r < nr) y[row0 + r] = v;
+    }
+  }
+}
+
+// Any group size: per element (x * s) * q as the reference evaluates it.
+__global__ __launch_bounds__(256) void k_gemv_q8_scalar(const float* __restrict__ x,
+                                                       const int8_t* __restrict__ W,
+                                                       const float* __restrict__ S,
+                                                       float* __restrict__ y, int rows, int cols,
+                                                       int gs) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int r = blockIdx.x * kWavesPerBlock + wave; r < rows; r += gridDim.x * kWavesPerBlock) {
+    const size_t base = static_cast<size_t>(r) * cols;
+    float acc = 0.f;
+    for (int c = lane; c < cols; c += kWave) {
+      const size_t idx = base + c;
+      acc += (x[c] * S[idx / gs]) * static_cast<float>(W[idx]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[r] = acc;
+  }
+}
+
+__global__ void k_dequant_q8(const int8_t* __restrict__ q, const float* __restrict__ s, int64_t n,
+                             int gs, float* __restrict__ out) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[i] = s[i / gs] * static_cast<float>(q[i]);
+}
+
+int gemv_grid(int rows, int rows_per_block) {
+  const int nblk = (rows + rows_per_block - 1) / rows_per_block;
+  return std::max(1, std::min(nblk, 4096));
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_rmsnorm_1(const float* __restrict__ x,
+                                                   const float* __restrict__ w, float* y, int n,
+                                                   float eps) {
+  __shared__ float red[16];
+  __shared__ float s_r;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int k = 0; k < static_cast<int>(blockDim.x >> 6); ++k) t += red[k];
+    s_r = 1.f / sqrtf(t / static_cast<float>(n) + eps);
+  }
+  __syncthreads();
+  const float r = s_r;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = w[i] * (r * x[i]);
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x,
+                                                     const float* __restrict__ w, float* y,
+                                                     int rows, int n, float eps) {
+  __shared__ float red[kWavesPerBlock];
+  const int row = blockIdx.x;
+  const float* xr = x + static_cast<size_t>(row) * n;
+  float* yr = y + static_cast<size_t>(row) * n;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
+  ss = block_sum(ss, red);
+  const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+  for (int i = threadIdx.x; i < n; i += 256) yr[i] = (r * xr[i]) * w[i];
+}
+
+// ---------------------------------------------------------------------------
+// RoPE: one thread per rotated pair of q (and of k where the index < kv_dim).
+// ---------------------------------------------------------------------------
+__global__ void k_rope(int style, int dim, int kv_dim, int hd, float* q, float* k, int pos,
+                       const float* __restrict__ sin_t, const float* __restrict__ cos_t) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= dim / 2) return;
+  const int half = hd / 2;
+  int i0, i1, tab;
+  if (style == KL_ROPE_INTERLEAVED) {
+    i0 = 2 * p;
+    i1 = i0 + 1;
+    tab = i0 % hd;
+  } else {
+    const int head = p / half, j = p - head * half;
+    i0 = head * hd + j;
+    i1 = i0 + half;
+    tab = 2 * j;
+  }
+  const float fci = sin_t[static_cast<size_t>(pos) * hd + tab];
+  const float fcr = cos_t[static_cast<size_t>(pos) * hd + tab];
+  float v0 = q[i0], v1 = q[i1];
+  rope_pair(v0, v1, fcr, fci);
+  q[i0] = v0;
+  q[i1] = v1;
+  // k is rotated where the pair's first q index (interleaved) or the head's
+  // start (rotate-half) lies below kv_dim, as in the reference loops.
+  const int gate = style == KL_ROPE_INTERLEAVED ? i0 : (i0 - (i0 % hd));
+  if (gate < kv_dim) {
+    float w0 = k[i0], w1 = k[i1];
+    rope_pair(w0, w1, fcr, fci);
+    k[i0] = w0;
+    k[i1] = w1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise.
+// ---------------------------------------------------------------------------
+__global__ void k_swiglu(const float* __restrict__ a, const float* __restrict__ b, float* out,
+                         int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const float av = a[i];
+    const float s = av * (1.0f / (1.0f + expf(-av)));
+    out[i] = s * b[i];
+  }
+}
+
+__global__ void k_add(const float* __restrict__ a, const float* __restrict__ b, float* out, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    out[i] = a[i] + b[i];
+}
+
+// One workgroup per token row.
+__global__ __launch_bounds__(256) void k_embedding(const int32_t* __restrict__ tokens,
+                                                  const float* __restrict__ table, int vocab,
+                                                  int dim, float* __restrict__ out, int32_t* bad) {
+  const int i = blockIdx.x;
+  const int32_t t = tokens[i];
+  if (t < 0 || t >= vocab) {
+    if (threadIdx.x == 0 && bad) *bad = 1;
+    return;
+  }
+  const float* src = table + static_cast<size_t>(t) * dim;
+  float* dst = out + static_cast<size_t>(i) * dim;
+  for (int c = threadIdx.x; c < dim; c += 256) dst[c] = src[c];
+}
+
+// ---------------------------------------------------------------------------
+// Argmax: per-workgroup (value, index) partials, merged by the last workgroup
+// to arrive (arrival counter reset by that workgroup).
+// ---------------------------------------------------------------------------
+constexpr int kArgmaxMaxBlocks = 1024;
+
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int n,
+                                               int32_t* out_index, float* pv, int* pi,
+                                               unsigned int* counter) {
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  __shared__ int s_last;
+  float v = -INFINITY;
+  int idx = INT_MAX;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) argmax_merge(v, idx, x[i], i);
+  wave_argmax(v, idx);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = v;
+    si[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(v, idx, sv[w], si[w]);
+    pv[blockIdx.x] = v;
+    pi[blockIdx.x] = idx;
+    __threadfence();
+    const unsigned int prev = atomicAdd(counter, 1u);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  v = -INFINITY;
+  idx = INT_MAX;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256) argmax_merge(v, idx, pv[b], pi[b]);
+  wave_argmax(v, idx);
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = v;
+    si[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(v, idx, sv[w], si[w]);
+    *out_index = idx;
+    *counter = 0u;
+  }
+}
+
+int argmax_blocks(int n) { return std::max(1, std::min(kArgmaxMaxBlocks, (n + 4095) / 4096)); }
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* kl_error_string(int code) {
+  switch (code) {
+    case KL_OK: return "ok";
+    case KL_EINVAL: return "invalid argument";
+    case KL_ENOMEM: return "device out of memory";
+    case KL_EFORMAT: return "malformed model image";
+    case KL_EUNSUPP: return "unsupported configuration";
+    case KL_ETOKEN: return "token id out of range";
+    case KL_EWORKSPACE: return "workspace too small";
+    default:
+      if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+      return "unknown error";
+  }
+}
+
+int kl_device_count(int* count) {
+  if (!count) return KL_EINVAL;
+  return rc(hipGetDeviceCount(count));
+}
+int kl_set_device(int device) { return rc(hipSetDevice(device)); }
+int kl_device_name(int device, char* buf, int buf_len) {
+  if (!buf || buf_len <= 0) return KL_EINVAL;
+  hipDeviceProp_t prop;
+  const hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return rc(e);
+  snprintf(buf, buf_len, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+  return KL_OK;
+}
+int kl_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return KL_EINVAL;
+  *ptr = nullptr;
+  if (bytes == 0) return KL_OK;
+  const hipError_t e = hipMalloc(ptr, bytes);
+  if (e == hipErrorOutOfMemory) {
+    (void)hipGetLastError();
+    return KL_ENOMEM;
+  }
+  return rc(e);
+}
+int kl_free(void* ptr) { return ptr ? rc(hipFree(ptr)) : KL_OK; }
+int kl_host_alloc(void** ptr, size_t bytes) {
+  if (!ptr) return KL_EINVAL;
+  return rc(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+}
+int kl_host_free(void* ptr) { return ptr ? rc(hipHostFree(ptr)) : KL_OK; }
+int kl_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return KL_OK;
+  if (!dst || !src) return KL_EINVAL;
+  return rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+}
+int kl_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return KL_OK;
+  if (!dst || !src) return KL_EINVAL;
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream));
+  if (e != hipSuccess) return rc(e);
+  return rc(hipStreamSynchronize(as_stream(stream)));
+}
+int kl_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return KL_OK;
+  if (!dst || !src) return KL_EINVAL;
+  return rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+}
+int kl_memset_zero(void* ptr, size_t bytes, void* stream) {
+  if (bytes == 0) return KL_OK;
+  if (!ptr) return KL_EINVAL;
+  return rc(hipMemsetAsync(ptr, 0, bytes, as_stream(stream)));
+}
+int kl_stream_create(void** stream) {
+  if (!stream) return KL_EINVAL;
+  hipStream_t s = nullptr;
+  const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  *stream = s;
+  return rc(e);
+}
+int kl_stream_destroy(void* stream) { return stream ? rc(hipStreamDestroy(as_stream(stream))) : KL_OK; }
+int kl_stream_sync(void* stream) { return rc(hipStreamSynchronize(as_stream(stream))); }
+int kl_device_sync(void) { return rc(hipDeviceSynchronize()); }
+int kl_event_create(void** event) {
+  if (!event) return KL_EINVAL;
+  hipEvent_t e = nullptr;
+  const hipError_t err = hipEventCreate(&e);
+  *event = e;
+  return rc(err);
+}
+int kl_event_destroy(void* event) { return event ? rc(hipEventDestroy(static_cast<hipEvent_t>(event))) : KL_OK; }
+int kl_event_record(void* event, void* stream) {
+  if (!event) return KL_EINVAL;
+  return rc(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)));
+}
+int kl_event_elapsed_ms(void* start, void* stop, float* ms) {
+  if (!start || !stop || !ms) return KL_EINVAL;
+  const hipError_t e = hipEventSynchronize(static_cast<hipEvent_t>(stop));
+  if (e != hipSuccess) return rc(e);
+  return rc(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+}
+
+int kl_gemv_f32(const float* x, const float* W, float* y, int rows, int cols, float scale,
+                void* stream) {
+  if (!x || !W || !y || rows <= 0 || cols <= 0) return KL_EINVAL;
+  if (cols % 4 == 0 && aligned16(x) && aligned16(W)) {
+    hipLaunchKernelGGL((k_gemv_f32<kGemvR, kGemvU>), dim3(gemv_grid(rows, kRowsPerBlock)),
+                       dim3(256), 0, as_stream(stream), x, W, y, rows, cols, scale);
+  } else {
+    const int grid = std::max(1, std::min((rows + kWavesPerBlock - 1) / kWavesPerBlock, 4096));
+    hipLaunchKernelGGL(k_gemv_f32_scalar, dim3(grid), dim3(256), 0, as_stream(stream), x, W, y,
+                       rows, cols, scale);
+  }
+  return launch_rc();
+}
+
+int kl_gemv_q8(const float* x, const int8_t* q, const float* scales, float* y, int rows, int cols,
+               int group_size, void* stream) {
+  if (!x || !q || !scales || !y || rows <= 0 || cols <= 0 || group_size <= 0) return KL_EINVAL;
+  if ((static_cast<int64_t>(rows) * cols) % group_size != 0) return KL_EINVAL;
+  const int cpg = group_size / 16;
+  const bool vec = group_size % 16 == 0 && (cpg & (cpg - 1)) == 0 && cols % group_size == 0 &&
+                   aligned16(x) && aligned16(q);
+  if (vec) {
+    int shift = 0;
+    while ((1 << shift) < cpg) ++shift;
+    hipLaunchKernelGGL((k_gemv_q8<kGemvR, kGemvU>), dim3(gemv_grid(rows, kRowsPerBlock)),
+                       dim3(256), 0, as_stream(stream), x, q, scales, y, rows, cols, shift);
+  } else {
+    const int grid = std::max(1, std::min((rows + kWavesPerBlock - 1) / kWavesPerBlock, 4096));
+    hipLaunchKernelGGL(k_gemv_q8_scalar, dim3(grid), dim3(256), 0, as_stream(stream), x, q,
+                       scales, y, rows, cols, group_size);
+  }
+  return launch_rc();
+}
+
+int kl_dequant_q8(const int8_t* q, const float* scales, int64_t n, int group_size, float* out,
+                  void* stream) {
+  if (!q || !scales || !out || n <= 0 || group_size <= 0) return KL_EINVAL;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(k_dequant_q8, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     as_stream(stream), q, scales, n, group_size, out);
+  return launch_rc();
+}
+
+int kl_rmsnorm(const float* x, const float* w, float* y, int n, float eps, void* stream) {
+  if (!x || !w || !y || n <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_rmsnorm_1, dim3(1), dim3(1024), 0, as_stream(stream), x, w, y, n, eps);
+  return launch_rc();
+}
+
+int kl_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n, float eps,
+                    void* stream) {
+  if (!x || !w || !y || rows <= 0 || n <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(256), 0, as_stream(stream), x, w, y, rows, n,
+                     eps);
+  return launch_rc();
+}
+
+int kl_sincos_table(int head_size, int seq_len, float theta, float* sin_dev, float* cos_dev) {
+  if (head_size <= 0 || seq_len <= 0 || !sin_dev || !cos_dev) return KL_EINVAL;
+  const size_t n = static_cast<size_t>(head_size) * seq_len;
+  std::vector<float> s(n), c(n);
+  for (int pos = 0; pos < seq_len; ++pos) {
+    for (int d = 0; d < head_size; ++d) {
+      // Same float expression as kernels/cpu/rope_kernel.cpp:7-13.
+      const float freq =
+          1.0f / std::pow(theta, static_cast<float>(d) / static_cast<float>(head_size));
+      const float val = static_cast<float>(pos) * freq;
+      s[static_cast<size_t>(pos) * head_size + d] = std::sin(val);
+      c[static_cast<size_t>(pos) * head_size + d] = std::cos(val);
+    }
+  }
+  hipError_t e = hipMemcpy(sin_dev, s.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(cos_dev, c.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  return rc(e);
+}
+
+int kl_rope(int style, int dim, int kv_dim, int head_size, float* q, float* k, int pos,
+            const float* sin_cache, const float* cos_cache, void* stream) {
+  if (!q || !k || !sin_cache || !cos_cache || dim <= 0 || kv_dim < 0 || kv_dim > dim ||
+      head_size <= 0 || head_size % 2 != 0 || dim % head_size != 0 || kv_dim % head_size != 0 ||
+      pos < 0)
+    return KL_EINVAL;
+  if (style != KL_ROPE_INTERLEAVED && style != KL_ROPE_HALF) return KL_EINVAL;
+  const int pairs = dim / 2;
+  hipLaunchKernelGGL(k_rope, dim3((pairs + 255) / 256), dim3(256), 0, as_stream(stream), style, dim,
+                     kv_dim, head_size, q, k, pos, sin_cache, cos_cache);
+  return launch_rc();
+}
+
+int kl_mha_workspace_size(int head_num, int kv_mul, int seq_len, int head_size, size_t* bytes) {
+  if (!bytes || seq_len <= 0 || !mha_shape_ok(head_num, kv_mul, head_size)) return KL_EINVAL;
+  *bytes = mha_plan(head_num / kv_mul, kv_mul, seq_len, head_size).ws_bytes;
+  return KL_OK;
+}
+
+int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+           int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
+           const float* key_cache, const float* value_cache, void* stream) {
+  if (!out || !q || !workspace || !key_cache || !value_cache) return KL_EINVAL;
+  if (!mha_shape_ok(head_num, kv_mul, head_size)) return KL_EUNSUPP;
+  if (pos < 0 || pos >= seq_len || layer_index < 0) return KL_EINVAL;
+  const int kv_heads = head_num / kv_mul;
+  if (kv_dim != kv_heads * head_size) return KL_EINVAL;
+  const MhaPlan p = mha_plan(kv_heads, kv_mul, seq_len, head_size);
+  if (workspace_bytes < p.ws_bytes) return KL_EWORKSPACE;
+  AttnArgs a{};
+  const size_t layer_off = static_cast<size_t>(layer_index) * seq_len * kv_dim;
+  a.q = q;
+  a.kcache = const_cast<float*>(key_cache) + layer_off;
+  a.vcache = value_cache + layer_off;
+  a.out = out;
+  a.part = static_cast<float*>(workspace);
+  a.counters = reinterpret_cast<unsigned int*>(static_cast<char*>(workspace) +
+                                               ((p.part_floats * sizeof(float) + 255) & ~size_t(255)));
+  a.pos_ptr = nullptr;
+  a.pos_val = pos;
+  a.kv_dim = kv_dim;
+  a.kv_mul = kv_mul;
+  a.G = p.G;
+  a.min_chunk = p.min_chunk;
+  a.ch_max = p.ch_max;
+  a.transform = 0;
+  a.scale = 1.f / std::sqrt(static_cast<float>(head_size));
+  const dim3 grid(kv_heads * p.G), block(256);
+  switch (head_size) {
+    case 32: hipLaunchKernelGGL(k_attn_decode<32>, grid, block, p.lds_bytes, as_stream(stream), a); break;
+    case 64: hipLaunchKernelGGL(k_attn_decode<64>, grid, block, p.lds_bytes, as_stream(stream), a); break;
+    case 128: hipLaunchKernelGGL(k_attn_decode<128>, grid, block, p.lds_bytes, as_stream(stream), a); break;
+    default: hipLaunchKernelGGL(k_attn_decode<256>, grid, block, p.lds_bytes, as_stream(stream), a); break;
+  }
+  return launch_rc();
+}
+
+int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream) {
+  if (!a || !b || !out || n <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_swiglu, dim3(std::min((n + 255) / 256, 4096)), dim3(256), 0,
+                     as_stream(stream), a, b, out, n);
+  return launch_rc();
+}
+
+int kl_add(const float* a, const float* b, float* out, int n, void* stream) {
+  if (!a || !b || !out || n <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_add, dim3(std::min((n + 255) / 256, 4096)), dim3(256), 0, as_stream(stream),
+                     a, b, out, n);
+  return launch_rc();
+}
+
+int kl_embedding(const int32_t* tokens, int n_tokens, const float* table, int vocab, int dim,
+                 float* out, int32_t* bad_token_flag, void* stream) {
+  if (!tokens || !table || !out || n_tokens <= 0 || vocab <= 0 || dim <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_embedding, dim3(n_tokens), dim3(256), 0, as_stream(stream), tokens, table,
+                     vocab, dim, out, bad_token_flag);
+  return launch_rc();
+}
+
+int kl_argmax_workspace_size(int n, size_t* bytes) {
+  if (!bytes || n <= 0) return KL_EINVAL;
+  const int g = argmax_blocks(n);
+  *bytes = static_cast<size_t>(g) * (sizeof(float) + sizeof(int)) + 64;
+  return KL_OK;
+}
+
+int kl_argmax(const float* x, int n, int32_t* out_index, void* workspace, size_t workspace_bytes,
+              void* stream) {
+  if (!x || !out_index || !workspace || n <= 0) return KL_EINVAL;
+  size_t need = 0;
+  kl_argmax_workspace_size(n, &need);
+  if (workspace_bytes < need) return KL_EWORKSPACE;
+  const int g = argmax_blocks(n);
+  // Layout: counter (64 bytes reserved), values [g], indices [g].
+  char* ws = static_cast<char*>(workspace);
+  unsigned int* counter = reinterpret_cast<unsigned int*>(ws);
+  float* pv = reinterpret_cast<float*>(ws + 64);
+  int* pi = reinterpret_cast<int*>(ws + 64 + static_cast<size_t>(g) * sizeof(float));
+  hipLaunchKernelGGL(k_argmax, dim3(g), dim3(256), 0, as_stream(stream), x, n, out_index, pv, pi,
+                     counter);
+  return launch_rc();
+}
+
+}  // extern "C"

@@ -1,0 +1,547 @@
+// CPU parity oracle for the KuiperLLama batch-1 decode path.
+//
+// TEST INFRASTRUCTURE ONLY -- see oracle.h.  Built with g++ -O3
+// -ffp-contract=off (no fused multiply-add anywhere, so elementwise results
+// such as RoPE and int8 dequant are reproducible bit-for-bit), OpenMP over
+// independent rows/heads (each output element is still produced by one thread
+// in one fixed order, so results do not depend on the thread count).
+#include "oracle.h"
+
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+// Fixed-order fp32 dot product: 8 interleaved accumulators (lane c % 8),
+// folded pairwise, then the scalar tail.  The reference delegates this to
+// OpenBLAS sgemv through Armadillo (kernels/cpu/matmul_kernel.cpp:37-40),
+// whose internal order is not reproducible here; this order is the oracle's
+// own documented choice.
+inline float dot8(const float* a, const float* b, int n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int c = 0;
+  for (; c + 8 <= n; c += 8) {
+    for (int k = 0; k < 8; ++k) acc[k] += a[c + k] * b[c + k];
+  }
+  float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+  for (; c < n; ++c) s += a[c] * b[c];
+  return s;
+}
+
+// Armadillo's arrayops::accumulate order: two interleaved accumulators (even
+// and odd indices), summed at the end.  Used by arma::mean / arma::sum, i.e.
+// the CPU RMSNorm mean (kernels/cpu/rmsnorm_kernel.cpp:30) and the softmax sum
+// (kernels/cpu/softmax_kernel.cpp:13).
+inline float arma_accumulate(const float* x, int n) {
+  float acc1 = 0.f, acc2 = 0.f;
+  int i = 0, j = 1;
+  for (; j < n; i += 2, j += 2) {
+    acc1 += x[i];
+    acc2 += x[j];
+  }
+  if (i < n) acc1 += x[i];
+  return acc1 + acc2;
+}
+
+}  // namespace
+
+extern "C" {
+
+void or_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int or_get_threads(void) { return omp_get_max_threads(); }
+
+// kernels/cpu/matmul_kernel.cpp:5-41: y[r] = (sum_c x[c] * W[r, c]) * scale,
+// W row-major [rows x cols] (Armadillo views it as a cols x rows column-major
+// matrix and computes x^T * W^T).
+void or_gemv_f32(const float* x, const float* W, float* y, int rows, int cols, float scale) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) {
+    y[r] = dot8(W + (int64_t)r * cols, x, cols) * scale;
+  }
+}
+
+// CUDA-only semantics restated (kernels/cuda/matmul_kernel.cu:56-87; there is
+// no CPU int8 kernel, kernels_interfaces.cpp:54-61):
+//   y[r] = sum_c (x[c] * scales[(r*cols + c) / group_size]) * float(q[r*cols + c])
+// The group index is taken over the flattened matrix, as in the reference.
+void or_gemv_q8(const float* x, const int8_t* q, const float* scales, float* y, int rows, int cols,
+                int group_size) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) {
+    const int64_t base = (int64_t)r * cols;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int c = 0;
+    for (; c + 8 <= cols; c += 8) {
+      for (int k = 0; k < 8; ++k) {
+        const int64_t idx = base + c + k;
+        acc[k] += (x[c + k] * scales[idx / group_size]) * static_cast<float>(q[idx]);
+      }
+    }
+    float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+    for (; c < cols; ++c) {
+      const int64_t idx = base + c;
+      s += (x[c] * scales[idx / group_size]) * static_cast<float>(q[idx]);
+    }
+    y[r] = s;
+  }
+}
+
+// tools/export_llama.py:49-73 (quantize_q80): per contiguous group of
+// group_size values, scale = max|w| / 127 (fp32 divide), q = round-half-even
+// (w / scale) as int8.  An all-zero group (scale 0, where torch would produce
+// NaN) is defined here as q = 0.
+void or_quantize_q8(const float* w, int64_t n, int group_size, int8_t* q, float* scales) {
+  const int64_t groups = n / group_size;
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < groups; ++g) {
+    const float* wg = w + g * group_size;
+    float wmax = 0.f;
+    for (int i = 0; i < group_size; ++i) wmax = std::max(wmax, std::fabs(wg[i]));
+    const float scale = wmax / 127.0f;
+    scales[g] = scale;
+    for (int i = 0; i < group_size; ++i) {
+      float v = scale == 0.f ? 0.f : std::nearbyint(wg[i] / scale);
+      q[g * group_size + i] = static_cast<int8_t>(v);
+    }
+  }
+}
+
+// Dequantized value of the reference int8 layout: float(q) * scale, one fp32
+// multiply (kernels/cuda/matmul_kernel.cu:73 evaluates the same product).
+void or_dequant_q8(const int8_t* q, const float* scales, int64_t n, int group_size, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) out[i] = scales[i / group_size] * static_cast<float>(q[i]);
+}
+
+// kernels/cpu/rmsnorm_kernel.cpp:4-33:
+//   mean = mean(x^2) + eps; rsqrt = 1 / sqrt(mean); y = w % (rsqrt * x)
+void or_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
+  std::vector<float> sq(n);
+  for (int i = 0; i < n; ++i) sq[i] = x[i] * x[i];
+  const float mean = arma_accumulate(sq.data(), n) / static_cast<float>(n) + eps;
+  const float rsqrt = 1.f / std::sqrt(mean);
+  for (int i = 0; i < n; ++i) y[i] = w[i] * (rsqrt * x[i]);
+}
+
+// CUDA-only semantics restated (kernels/cuda/rmsnorm_kernel.cu:8-60, launched
+// by rmsnorm_kernel_cu_dim :138-164): the same normalisation applied to each
+// row of length n independently, with one weight vector of length n.  The
+// reference hard-codes eps = 1e-6 (:148); callers pass it explicitly here.
+void or_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n, float eps) {
+  for (int r = 0; r < rows; ++r) or_rmsnorm(x + (int64_t)r * n, w, y + (int64_t)r * n, n, eps);
+}
+
+// kernels/cpu/rope_kernel.cpp:4-16 / :44-56 / :84-96 (identical bodies, theta
+// 5e5 / 1e6 / 1e4 chosen by build flag):
+//   freq = 1 / pow(theta, d / hd); val = pos * freq; table = sinf/cosf(val)
+void or_sincos_table(int head_size, int seq_len, float theta, float* sin_cache, float* cos_cache) {
+  for (int pos = 0; pos < seq_len; ++pos) {
+    for (int d = 0; d < head_size; ++d) {
+      const float freq =
+          1.0f / std::pow(theta, static_cast<float>(d) / static_cast<float>(head_size));
+      const float val = static_cast<float>(pos) * freq;
+      sin_cache[pos * head_size + d] = std::sin(val);
+      cos_cache[pos * head_size + d] = std::cos(val);
+    }
+  }
+}
+
+// Interleaved style: kernels/cpu/rope_kernel.cpp:98-121 (pairs (i, i+1), table
+// index i % hd).  Rotate-half style: :18-42 and :58-82 (pairs (j, j + hd/2)
+// within each head, table index 2j).  k is rotated only where the q index is
+// below kv_dim.
+void or_rope(int style, int dim, int kv_dim, int head_size, float* q, float* k, int pos,
+             const float* sin_cache, const float* cos_cache) {
+  if (style == OR_ROPE_INTERLEAVED) {
+    for (int i = 0; i < dim; i += 2) {
+      const int hdim = i % head_size;
+      const float fci = sin_cache[pos * head_size + hdim];
+      const float fcr = cos_cache[pos * head_size + hdim];
+      const int rotn = i < kv_dim ? 2 : 1;
+      for (int v = 0; v < rotn; ++v) {
+        float* vec = v == 0 ? q : k;
+        const float v0 = vec[i];
+        const float v1 = vec[i + 1];
+        vec[i] = v0 * fcr - v1 * fci;
+        vec[i + 1] = v0 * fci + v1 * fcr;
+      }
+    }
+  } else {
+    const int half = head_size / 2;
+    for (int i = 0; i < dim; i += head_size) {
+      for (int j = 0; j < half; ++j) {
+        const float fci = sin_cache[pos * head_size + j * 2];
+        const float fcr = cos_cache[pos * head_size + j * 2];
+        const int rotn = i < kv_dim ? 2 : 1;
+        for (int v = 0; v < rotn; ++v) {
+          float* vec = v == 0 ? q : k;
+          const float v0 = vec[i + j];
+          const float v1 = vec[i + j + half];
+          vec[i + j] = v0 * fcr - v1 * fci;
+          vec[i + j + half] = v0 * fci + v1 * fcr;
+        }
+      }
+    }
+  }
+}
+
+// kernels/cpu/softmax_kernel.cpp:4-15: subtract the max (std::max_element),
+// expf, Armadillo sum, divide.
+void or_softmax(float* x, int n) {
+  const float mx = *std::max_element(x, x + n);
+  for (int i = 0; i < n; ++i) x[i] = std::exp(x[i] - mx);
+  const float sum = arma_accumulate(x, n);
+  for (int i = 0; i < n; ++i) x[i] = x[i] / sum;
+}
+
+// kernels/cpu/mha_kernel.cpp:5-61 with softmax_kernel.cpp:4-15 and
+// scale_sum_kernel.cpp:5-22.  Per head h (kv head h / kv_mul):
+//   s_t = (q_h . K_t) * (1/sqrt(hd)), t in [0, pos]; softmax; out_h = sum_t p_t V_t
+// accumulated in increasing t.  Caches are [layers][seq_len][kv_dim].
+void or_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+            int head_size, float* out, const float* q, float* score, const float* key_cache,
+            const float* value_cache) {
+  const int64_t layer_offset = (int64_t)layer_index * seq_len * kv_dim;
+  const float scale = 1.f / std::sqrt(static_cast<float>(head_size));
+#pragma omp parallel for schedule(static)
+  for (int h = 0; h < head_num; ++h) {
+    float* sh = score + (int64_t)h * seq_len;
+    const float* qh = q + (int64_t)h * head_size;
+    const int64_t head_off = (int64_t)(h / kv_mul) * head_size;
+    for (int t = 0; t <= pos; ++t) {
+      const float* kt = key_cache + layer_offset + (int64_t)t * kv_dim + head_off;
+      sh[t] = dot8(qh, kt, head_size) * scale;
+    }
+    or_softmax(sh, pos + 1);
+    float* oh = out + (int64_t)h * head_size;
+    for (int d = 0; d < head_size; ++d) oh[d] = 0.f;
+    for (int t = 0; t <= pos; ++t) {
+      const float* vt = value_cache + layer_offset + (int64_t)t * kv_dim + head_off;
+      const float p = sh[t];
+      for (int d = 0; d < head_size; ++d) oh[d] += p * vt[d];
+    }
+  }
+}
+
+// kernels/cpu/swiglu_kernel.cpp:3-23: a = a * (1 / (1 + exp(-a))); out = a * b.
+void or_swiglu(const float* a, const float* b, float* out, int n) {
+  for (int i = 0; i < n; ++i) {
+    const float s = a[i] * (1.0f / (1.0f + std::exp(-a[i])));
+    out[i] = s * b[i];
+  }
+}
+
+// kernels/cpu/add_kernel.cpp:5-19.
+void or_add(const float* a, const float* b, float* out, int n) {
+  for (int i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+// kernels/cpu/emb_kernel.cpp:4-29: out[i, :] = table[tokens[i], :].  The
+// reference rejects only token > vocab (:16), so token == vocab reads past
+// the table; the oracle rejects every id outside [0, vocab) and returns -1.
+int or_embedding(const int32_t* tokens, int n_tokens, const float* table, int vocab, int dim,
+                 float* out) {
+  for (int i = 0; i < n_tokens; ++i) {
+    const int32_t t = tokens[i];
+    if (t < 0 || t >= vocab) return -1;
+    std::memcpy(out + (int64_t)i * dim, table + (int64_t)t * dim, sizeof(float) * dim);
+  }
+  return 0;
+}
+
+// sampler/argmax_sampler.cpp:5-13: std::max_element, i.e. the first index of
+// the maximum (a later element replaces the best only if strictly greater).
+int64_t or_argmax(const float* x, int64_t n) {
+  int64_t best = 0;
+  for (int64_t i = 1; i < n; ++i) {
+    if (x[best] < x[i]) best = i;
+  }
+  return best;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Model restatement.
+// ---------------------------------------------------------------------------
+struct or_model {
+  int family = 0, quant = 0, group_size = 0;
+  int D = 0, Dq = 0, Dkv = 0, F = 0, L = 0, H = 0, KVH = 0, V = 0, S = 0, hd = 0;
+  bool tied = false;
+  float eps = 1e-5f, theta = 1e4f;
+  int rope_style = OR_ROPE_INTERLEAVED;
+  const float* emb = nullptr;
+  std::vector<const float*> rms_att, rms_ffn, q_norm, k_norm, bq, bk, bv;
+  const float* rms_final = nullptr;
+  // fp32 matrices or int8 matrices + scales
+  std::vector<const void*> wq, wk, wv, wo, w1, w2, w3;
+  std::vector<const float*> sq, sk, sv, so, s1, s2, s3;
+  const void* wcls = nullptr;
+  const float* scls = nullptr;
+  std::vector<float> sin_t, cos_t, kcache, vcache;
+  std::vector<float> x, xb, q, att, hb, hb2, score, logits;
+};
+
+namespace {
+
+void gemv_any(const or_model* m, const void* W, const float* s, const float* x, float* y,
+              int rows, int cols) {
+  if (m->quant) {
+    or_gemv_q8(x, static_cast<const int8_t*>(W), s, y, rows, cols, m->group_size);
+  } else {
+    or_gemv_f32(x, static_cast<const float*>(W), y, rows, cols, 1.f);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Parsing follows model/model.cpp:41-141 (header, derived dims, tied iff
+// vocab > 0) and the offset walks of model/llama3.cpp:183-422 (fp32 and int8),
+// model/qwen2.cpp:348-485 (bias after each of wq/wk/wv) and
+// model/qwen3.cpp:186-299 (8-int header, norms first, q/k norms, lm_head).
+or_model* or_model_open(const void* image, size_t size, int family, int quant, char* err,
+                        int err_len) {
+  auto fail = [&](const char* msg) -> or_model* {
+    if (err && err_len > 0) snprintf(err, err_len, "%s", msg);
+    return nullptr;
+  };
+  const bool qwen3 = family == OR_QWEN3;
+  const size_t header_ints = qwen3 ? 8 : (quant ? 8 : 7);
+  if (size < header_ints * 4) return fail("truncated header");
+  const int32_t* h = static_cast<const int32_t*>(image);
+  if (qwen3 && quant) return fail("qwen3 has no int8 layout");
+  if (family == OR_QWEN2 && quant) return fail("qwen2 int8 layout is not supported");
+  or_model* m = new or_model();
+  m->family = family;
+  m->quant = quant;
+  const int32_t dim = h[0], hidden = h[1];
+  m->L = h[2];
+  m->H = h[3];
+  m->KVH = h[4];
+  const int32_t vocab = h[5];
+  m->S = h[6];
+  if (dim <= 0 || hidden <= 0 || m->L <= 0 || m->H <= 0 || m->KVH <= 0 || vocab == 0 ||
+      m->S <= 0 || dim % m->H != 0 || m->H % m->KVH != 0) {
+    delete m;
+    return fail("bad header values");
+  }
+  m->V = std::abs(vocab);
+  m->hd = dim / m->H;
+  m->Dq = dim;
+  m->Dkv = dim * m->KVH / m->H;
+  if (qwen3) {
+    m->D = hidden;
+    m->F = h[7];
+    m->tied = false;
+  } else {
+    m->D = dim;
+    m->F = hidden;
+    m->tied = vocab > 0;
+  }
+  if (quant) {
+    m->group_size = h[7];
+    if (m->group_size <= 0) {
+      delete m;
+      return fail("bad group size");
+    }
+  }
+  switch (family) {
+    case OR_LLAMA2: m->eps = 1e-5f; m->theta = 10000.0f; m->rope_style = OR_ROPE_INTERLEAVED; break;
+    case OR_LLAMA3: m->eps = 1e-5f; m->theta = 500000.0f; m->rope_style = OR_ROPE_HALF; break;
+    case OR_QWEN2: m->eps = 1e-6f; m->theta = 1000000.0f; m->rope_style = OR_ROPE_HALF; break;
+    case OR_QWEN3: m->eps = 1e-6f; m->theta = 1000000.0f; m->rope_style = OR_ROPE_HALF; break;
+    default: delete m; return fail("unknown family");
+  }
+  const int L = m->L, D = m->D, Dq = m->Dq, Dkv = m->Dkv, F = m->F, V = m->V, S = m->S;
+  const char* base = static_cast<const char*>(image) + header_ints * 4;
+  const size_t avail = size - header_ints * 4;
+  size_t off = 0;  // bytes from the start of the weight area
+  bool overflow = false;
+  auto take = [&](size_t bytes) -> const char* {
+    const char* p = base + off;
+    off += bytes;
+    if (off > avail) overflow = true;
+    return p;
+  };
+  auto takef = [&](size_t n) { return reinterpret_cast<const float*>(take(n * 4)); };
+  m->rms_att.resize(L);
+  m->rms_ffn.resize(L);
+  m->wq.resize(L); m->wk.resize(L); m->wv.resize(L); m->wo.resize(L);
+  m->w1.resize(L); m->w2.resize(L); m->w3.resize(L);
+  if (quant) {
+    const int gs = m->group_size;
+    m->sq.resize(L); m->sk.resize(L); m->sv.resize(L); m->so.resize(L);
+    m->s1.resize(L); m->s2.resize(L); m->s3.resize(L);
+    auto takeq = [&](int64_t n, const void** w, const float** s) {
+      if (n % gs != 0) overflow = true;
+      *w = take(n);
+      *s = takef(n / gs);
+    };
+    for (int l = 0; l < L; ++l) takeq((int64_t)Dq * D, &m->wq[l], &m->sq[l]);
+    for (int l = 0; l < L; ++l) takeq((int64_t)Dkv * D, &m->wk[l], &m->sk[l]);
+    for (int l = 0; l < L; ++l) takeq((int64_t)Dkv * D, &m->wv[l], &m->sv[l]);
+    for (int l = 0; l < L; ++l) takeq((int64_t)D * Dq, &m->wo[l], &m->so[l]);
+    for (int l = 0; l < L; ++l) takeq((int64_t)F * D, &m->w1[l], &m->s1[l]);
+    for (int l = 0; l < L; ++l) takeq((int64_t)D * F, &m->w2[l], &m->s2[l]);
+    for (int l = 0; l < L; ++l) takeq((int64_t)F * D, &m->w3[l], &m->s3[l]);
+    if (m->tied) {
+      delete m;  // llama3.cpp:258-267 would reinterpret fp32 embedding bytes as int8
+      return fail("tied classifier in an int8 image is not supported");
+    }
+    takeq((int64_t)V * D, &m->wcls, &m->scls);
+    m->emb = takef((size_t)V * D);
+    for (int l = 0; l < L; ++l) m->rms_att[l] = takef(D);
+    for (int l = 0; l < L; ++l) m->rms_ffn[l] = takef(D);
+    m->rms_final = takef(D);
+  } else if (qwen3) {
+    for (int l = 0; l < L; ++l) m->rms_att[l] = takef(D);
+    for (int l = 0; l < L; ++l) m->rms_ffn[l] = takef(D);
+    m->rms_final = takef(D);
+    m->emb = takef((size_t)V * D);
+    m->q_norm.resize(L);
+    m->k_norm.resize(L);
+    for (int l = 0; l < L; ++l) m->wq[l] = takef((size_t)Dq * D);
+    for (int l = 0; l < L; ++l) m->q_norm[l] = takef(m->hd);
+    for (int l = 0; l < L; ++l) m->wk[l] = takef((size_t)Dkv * D);
+    for (int l = 0; l < L; ++l) m->k_norm[l] = takef(m->hd);
+    for (int l = 0; l < L; ++l) m->wv[l] = takef((size_t)Dkv * D);
+    for (int l = 0; l < L; ++l) m->wo[l] = takef((size_t)D * Dq);
+    for (int l = 0; l < L; ++l) m->w1[l] = takef((size_t)F * D);
+    for (int l = 0; l < L; ++l) m->w2[l] = takef((size_t)D * F);
+    for (int l = 0; l < L; ++l) m->w3[l] = takef((size_t)F * D);
+    m->wcls = takef((size_t)V * D);
+  } else {
+    const bool bias = family == OR_QWEN2;
+    m->emb = takef((size_t)V * D);
+    for (int l = 0; l < L; ++l) m->rms_att[l] = takef(D);
+    if (bias) {
+      m->bq.resize(L);
+      m->bk.resize(L);
+      m->bv.resize(L);
+    }
+    for (int l = 0; l < L; ++l) {
+      m->wq[l] = takef((size_t)Dq * D);
+      if (bias) m->bq[l] = takef(Dq);
+    }
+    for (int l = 0; l < L; ++l) {
+      m->wk[l] = takef((size_t)Dkv * D);
+      if (bias) m->bk[l] = takef(Dkv);
+    }
+    for (int l = 0; l < L; ++l) {
+      m->wv[l] = takef((size_t)Dkv * D);
+      if (bias) m->bv[l] = takef(Dkv);
+    }
+    for (int l = 0; l < L; ++l) m->wo[l] = takef((size_t)D * Dq);
+    for (int l = 0; l < L; ++l) m->rms_ffn[l] = takef(D);
+    for (int l = 0; l < L; ++l) m->w1[l] = takef((size_t)F * D);
+    for (int l = 0; l < L; ++l) m->w2[l] = takef((size_t)D * F);
+    for (int l = 0; l < L; ++l) m->w3[l] = takef((size_t)F * D);
+    m->rms_final = takef(D);
+    takef((size_t)S * m->hd);  // freq_cos + freq_sin tables, unused by the loaders
+    m->wcls = m->tied ? static_cast<const void*>(m->emb) : takef((size_t)V * D);
+  }
+  if (overflow) {
+    delete m;
+    return fail("image smaller than the layout its header describes");
+  }
+  m->sin_t.resize((size_t)S * m->hd);
+  m->cos_t.resize((size_t)S * m->hd);
+  or_sincos_table(m->hd, S, m->theta, m->sin_t.data(), m->cos_t.data());
+  m->kcache.assign((size_t)L * S * Dkv, 0.f);
+  m->vcache.assign((size_t)L * S * Dkv, 0.f);
+  m->x.resize(D);
+  m->xb.resize(std::max(D, Dq));
+  m->q.resize(Dq);
+  m->att.resize(D);
+  m->hb.resize(F);
+  m->hb2.resize(F);
+  m->score.resize((size_t)m->H * S);
+  m->logits.resize(V);
+  return m;
+}
+
+void or_model_close(or_model* m) { delete m; }
+
+void or_model_dims(const or_model* m, int32_t* o) {
+  o[0] = m->D; o[1] = m->Dq; o[2] = m->Dkv; o[3] = m->F; o[4] = m->L;
+  o[5] = m->H; o[6] = m->KVH; o[7] = m->V; o[8] = m->S; o[9] = m->hd;
+}
+
+// model/llama3.cpp:146-166 (forward), :599-744 (attention_rms, attention_qkv,
+// attention_mha, feed_forward, cls_logits); Qwen2 adds the bias add after each
+// of wq/wk/wv (op/matmul.cpp:74-77); Qwen3 applies the per-head q and k
+// RMSNorm between the projections and RoPE (model/qwen3.cpp:485-500).
+int or_model_step(or_model* m, int32_t token, int32_t pos, float* logits) {
+  if (pos < 0 || pos >= m->S) return -2;
+  if (or_embedding(&token, 1, m->emb, m->V, m->D, m->x.data()) != 0) return -1;
+  const int D = m->D, Dq = m->Dq, Dkv = m->Dkv, F = m->F, S = m->S, hd = m->hd;
+  float* x = m->x.data();
+  float* xb = m->xb.data();
+  for (int l = 0; l < m->L; ++l) {
+    or_rmsnorm(x, m->rms_att[l], xb, D, m->eps);
+    float* kslot = m->kcache.data() + ((size_t)l * S + pos) * Dkv;
+    float* vslot = m->vcache.data() + ((size_t)l * S + pos) * Dkv;
+    const bool q8 = m->quant != 0;
+    gemv_any(m, m->wq[l], q8 ? m->sq[l] : nullptr, xb, m->q.data(), Dq, D);
+    if (!m->bq.empty()) or_add(m->q.data(), m->bq[l], m->q.data(), Dq);
+    if (m->family == OR_QWEN3) {
+      or_rmsnorm_rows(m->q.data(), m->q_norm[l], m->q.data(), Dq / hd, hd, 1e-6f);
+    }
+    gemv_any(m, m->wk[l], q8 ? m->sk[l] : nullptr, xb, kslot, Dkv, D);
+    if (!m->bk.empty()) or_add(kslot, m->bk[l], kslot, Dkv);
+    if (m->family == OR_QWEN3) or_rmsnorm_rows(kslot, m->k_norm[l], kslot, Dkv / hd, hd, 1e-6f);
+    gemv_any(m, m->wv[l], q8 ? m->sv[l] : nullptr, xb, vslot, Dkv, D);
+    if (!m->bv.empty()) or_add(vslot, m->bv[l], vslot, Dkv);
+    or_rope(m->rope_style, Dq, Dkv, hd, m->q.data(), kslot, pos, m->sin_t.data(), m->cos_t.data());
+    or_mha(pos, m->H, l, S, Dkv, m->H / m->KVH, hd, xb, m->q.data(), m->score.data(),
+           m->kcache.data(), m->vcache.data());
+    gemv_any(m, m->wo[l], q8 ? m->so[l] : nullptr, xb, m->att.data(), D, Dq);
+    or_add(x, m->att.data(), x, D);
+    or_rmsnorm(x, m->rms_ffn[l], xb, D, m->eps);
+    gemv_any(m, m->w1[l], q8 ? m->s1[l] : nullptr, xb, m->hb.data(), F, D);
+    gemv_any(m, m->w3[l], q8 ? m->s3[l] : nullptr, xb, m->hb2.data(), F, D);
+    or_swiglu(m->hb.data(), m->hb2.data(), m->hb.data(), F);
+    gemv_any(m, m->w2[l], q8 ? m->s2[l] : nullptr, m->hb.data(), m->att.data(), D, F);
+    or_add(x, m->att.data(), x, D);
+  }
+  or_rmsnorm(x, m->rms_final, x, D, m->eps);
+  gemv_any(m, m->wcls, m->scls, x, m->logits.data(), m->V, D);
+  if (logits) std::memcpy(logits, m->logits.data(), sizeof(float) * m->V);
+  return 0;
+}
+
+// demo/main.cpp:5-47: prompt positions 0..P-2 run without sampling; from
+// position P-1 on, the current token is embedded, the step runs and the
+// argmax becomes the next token.  `next` starts at prompt[0]
+// (demo/main_qwen3.cpp:93), which keeps a 1-token prompt well defined.
+int or_model_generate(or_model* m, const int32_t* prompt, int P, int n_new, int32_t* out_tokens) {
+  if (P <= 0 || n_new <= 0) return 0;
+  int32_t next = prompt[0];
+  int n_out = 0;
+  const int total = P + n_new - 1;
+  for (int pos = 0; pos < total; ++pos) {
+    if (pos < P - 1) {
+      if (or_model_step(m, prompt[pos], pos, nullptr) != 0) return -1;
+      next = prompt[pos + 1];
+    } else {
+      if (or_model_step(m, next, pos, nullptr) != 0) return -1;
+      next = static_cast<int32_t>(or_argmax(m->logits.data(), m->V));
+      out_tokens[n_out++] = next;
+    }
+  }
+  return n_out;
+}
+
+void or_model_kv_row(const or_model* m, int layer, int pos, int which_v, float* out) {
+  const std::vector<float>& c = which_v ? m->vcache : m->kcache;
+  std::memcpy(out, c.data() + ((size_t)layer * m->S + pos) * m->Dkv, sizeof(float) * m->Dkv);
+}
+
+}  // extern "C"

@@ -1,0 +1,143 @@
+"""Whole-step parity of the fused decode engine against the CPU oracle.
+
+Bars (from the task's north star): per-step logits within 1e-4 relative
+(max |gpu - cpu| / max |cpu|), greedy tokens identical.  Greedy sequences are
+checked teacher-forced: both sides are fed the oracle's token at every step,
+so one near-tie cannot derail the rest of the comparison; any argmax
+disagreement must sit on a logit gap below the logits tolerance.
+"""
+import sys
+import time
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_RTOL = 1e-4
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def teacher_forced(K, O, cfg, img, prompt, n_new, graph=True):
+    eng = K.Engine(img, cfg)
+    eng.set_graph(graph)
+    om = O.Model(img, cfg.family, cfg.quant)
+    seq = [int(t) for t in prompt]
+    worst, mismatches = 0.0, []
+    for pos in range(len(prompt) + n_new - 1):
+        nxt, lg = eng.step(seq[pos], pos)
+        ref = om.step(seq[pos], pos)
+        r = rel(lg, ref)
+        worst = max(worst, r)
+        assert r < LOGIT_RTOL, (cfg.name, pos, r)
+        assert nxt == int(np.argmax(lg))  # the device argmax picks the first max
+        if pos >= len(prompt) - 1:
+            want = O.argmax(ref)
+            if nxt != want:
+                gap = abs(float(ref[nxt]) - float(ref[want]))
+                mismatches.append((pos, gap))
+                assert gap <= LOGIT_RTOL * np.max(np.abs(ref)), (cfg.name, pos, gap)
+            seq.append(want)
+    return eng, om, worst, mismatches
+
+
+@pytest.mark.parametrize("name", ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2",
+                                  "tiny_qwen3"])
+def test_tiny_models_step_parity(K, O, gpu, name):
+    cfg = K.TINY[name]
+    say("case", name)
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, cfg.decode_steps)
+    say(name, "worst logits rel err", worst, "argmax near-ties", mm)
+    assert not mm
+    # KV cache contents (K rotated) after the run
+    for layer, pos in ((0, 0), (cfg.layers - 1, 3), (cfg.layers - 1, cfg.prompt_len)):
+        for v in (False, True):
+            a, b = eng.kv_row(layer, pos, v), om.kv_row(layer, pos, v)
+            assert rel(a, b) < 1e-4
+
+
+@pytest.mark.parametrize("name", ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2",
+                                  "tiny_qwen3"])
+def test_tiny_models_generate_matches_oracle(K, O, gpu, name):
+    cfg = K.TINY[name]
+    say("case", name)
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    want = O.Model(img, cfg.family, cfg.quant).generate(prompt, cfg.decode_steps)
+    eng = K.Engine(img, cfg)
+    got, ms = eng.generate(prompt, cfg.decode_steps)
+    assert list(got) == list(want)
+    # a second run on the same engine (state fully device-driven) repeats it
+    got2, _ = eng.generate(prompt, cfg.decode_steps)
+    assert list(got2) == list(want)
+
+
+def test_graph_and_eager_agree_bitwise(K, O, gpu):
+    cfg = K.TINY["tiny_qwen3"]
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    a, b = K.Engine(img, cfg), K.Engine(img, cfg)
+    b.set_graph(False)
+    for pos, t in enumerate(list(prompt) + [5, 6, 7]):
+        na, la = a.step(int(t), pos)
+        nb, lb = b.step(int(t), pos)
+        assert na == nb and np.array_equal(la, lb)
+
+
+def test_engine_rejects_bad_tokens(K, gpu):
+    cfg = K.TINY["tiny_llama2"]
+    eng = K.Engine(K.synth_image(cfg), cfg)
+    with pytest.raises(K.KlError):
+        eng.step(cfg.vocab, 0)
+    with pytest.raises(K.KlError):
+        eng.step(0, cfg.seq_len)
+    with pytest.raises(K.KlError):
+        eng.generate(np.array([1, cfg.vocab], np.int32), 2)
+
+
+# ------------------------------------------- BASELINE shapes, full size -----
+def test_cfg1_llama2_110m_full(K, O, gpu):
+    """cfg 1 at full size: 16-token prompt + 128 greedy steps, teacher forced."""
+    cfg = K.BASELINE["llama2_110m"]
+    t = time.time()
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    say("cfg1 image", img.nbytes, time.time() - t)
+    eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, cfg.decode_steps)
+    say("cfg1 worst logits rel err", worst, "near-ties", mm, "t", time.time() - t)
+    got, _ = eng.generate(prompt, 64)
+    om2 = O.Model(img, cfg.family, cfg.quant)
+    assert list(got) == list(om2.generate(prompt, 64))
+
+
+def test_cfg2_llama32_1b_full(K, O, gpu):
+    """cfg 2 (north-star shape) at full size: first 64 greedy tokens."""
+    cfg = K.BASELINE["llama32_1b"]
+    t = time.time()
+    img = K.synth_image(cfg)
+    say("cfg2 image", img.nbytes, time.time() - t)
+    prompt = K.prompt_tokens(cfg, 16)
+    eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, 64)
+    say("cfg2 worst logits rel err", worst, "near-ties", mm, "t", time.time() - t)
+
+
+@pytest.mark.parametrize("name,steps", [("llama2_7b_q8", 6), ("qwen25_15b", 6), ("qwen3_4b", 4)])
+def test_other_baseline_shapes_full(K, O, gpu, name, steps):
+    """cfg 3 / 4 / 5 at full size, a few teacher-forced steps each."""
+    cfg = K.BASELINE[name]
+    t = time.time()
+    img = K.synth_image(cfg)
+    say(name, "image", img.nbytes, time.time() - t)
+    prompt = K.prompt_tokens(cfg, 4)
+    eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, steps)
+    say(name, "worst logits rel err", worst, "near-ties", mm, "t", time.time() - t)
