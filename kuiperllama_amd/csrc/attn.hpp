@@ -5,15 +5,18 @@
 // softmax over t, out_h = sum_t p_t V_t.  Caches are [seq_len][kv_dim] per
 // layer (the caller passes the layer base).
 //
-// Work split: one 256-thread workgroup per (kv head g, position chunk s).  A
-// workgroup serves all kv_mul query heads of its kv head, so every K/V row it
-// reads from HBM is used kv_mul times.  The chunk length adapts to the live
-// context (chunk = max(min_chunk, ceil((pos+1)/G))); workgroups past the last
-// chunk exit at once.  Each workgroup stores (o, m, l) for its chunk; the last
-// workgroup of a kv head to finish (an atomic arrival counter, reset by that
-// workgroup) merges the chunks with the usual rescaling
-// O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).  A single chunk writes the
-// output directly.
+// Work split: one 256-thread workgroup per (kv head g, chunk of PT
+// positions); the grid covers the whole cache and workgroups past the live
+// context exit at once.  A workgroup serves all kv_mul query heads of its kv
+// head, so each K/V row read from HBM is used kv_mul times.  Every K and V
+// load of the chunk is issued at kernel entry into registers (HD/4 lanes per
+// row, PT/(1024/HD) rows per lane), so the chunk costs one memory round trip;
+// q staging, q/k normalisation and RoPE overlap with it.  Each workgroup
+// stores (o, m, l) for its chunk with coherent stores; the last workgroup of
+// a kv head to finish (atomic arrival counter, reset by that workgroup) reads
+// them back with coherent loads and merges the chunks with
+// O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).  A single chunk writes
+// the output directly.
 //
 // With `transform` set, the kernel also applies what the reference runs
 // between the K/V projections and attention (model/llama3.cpp:634-638,
@@ -39,7 +42,7 @@ struct AttnArgs {
   unsigned int* counters;  // [kv_heads], zero between launches
   const int* pos_ptr;      // device position (fused path) or nullptr
   int pos_val;
-  int kv_dim, kv_mul, G, min_chunk, ch_max;
+  int kv_dim, kv_mul, G;   // G: chunk slots per kv head = ceil(seq_len / PT)
   int transform;           // 0: none, 1: RoPE, 2: per-head RMSNorm then RoPE
   int rope_style;          // 0 interleaved pairs, 1 rotate-half pairs
   const float* sin_t;      // [seq_len][HD]
@@ -50,31 +53,32 @@ struct AttnArgs {
   float scale;             // 1 / sqrt(HD)
 };
 
-__host__ __device__ inline size_t attn_lds_floats(int hd, int kv_mul, int ch_max) {
-  return static_cast<size_t>(kv_mul) * hd + static_cast<size_t>(kv_mul) * ch_max + hd +
-         2 * kAttnMaxKvMul + static_cast<size_t>(256 / hd) * kv_mul * hd;
+// Positions per workgroup for a head size (8 K and 8 V chunks per lane at
+// most: 64 VGPRs of prefetched cache).
+__host__ __device__ constexpr int attn_chunk(int hd) { return hd >= 256 ? 32 : 64; }
+
+__host__ __device__ inline size_t attn_lds_floats(int hd, int kv_mul) {
+  const int pt = attn_chunk(hd);
+  const int rpp = 256 / (hd / 4);
+  return static_cast<size_t>(kv_mul) * hd      // q
+         + static_cast<size_t>(kv_mul) * pt    // scores
+         + hd                                  // transformed K[pos]
+         + 2 * kAttnMaxKvMul                   // (m, l)
+         + static_cast<size_t>(rpp) * kv_mul * hd;  // PV reduction
 }
 
-// Split plan shared by the op-level launcher and the fused engine: about 256
-// workgroups in total (kv_heads * G), chunks of at least min_chunk positions.
+// Split plan shared by the op-level launcher and the fused engine.
 struct MhaPlan {
-  int G, min_chunk, ch_max;
+  int G;
   size_t part_floats, lds_bytes, ws_bytes;
 };
 
 inline MhaPlan mha_plan(int kv_heads, int kv_mul, int seq_len, int hd) {
   MhaPlan p;
-  p.min_chunk = 16;
-  int by_heads = 256 / (kv_heads > 0 ? kv_heads : 1);
-  if (by_heads < 1) by_heads = 1;
-  int by_len = (seq_len + p.min_chunk - 1) / p.min_chunk;
-  if (by_len < 1) by_len = 1;
-  p.G = by_heads < by_len ? by_heads : by_len;
-  int ch = (seq_len + p.G - 1) / p.G;
-  if (ch < p.min_chunk) ch = p.min_chunk;
-  p.ch_max = (ch + 3) & ~3;
+  const int pt = attn_chunk(hd);
+  p.G = (seq_len + pt - 1) / pt;
   p.part_floats = static_cast<size_t>(kv_heads) * p.G * kv_mul * (hd + 2);
-  p.lds_bytes = attn_lds_floats(hd, kv_mul, p.ch_max) * sizeof(float);
+  p.lds_bytes = attn_lds_floats(hd, kv_mul) * sizeof(float);
   p.ws_bytes = ((p.part_floats * sizeof(float) + 255) & ~size_t(255)) +
                static_cast<size_t>(kv_heads) * sizeof(unsigned int);
   return p;
@@ -88,37 +92,53 @@ inline bool mha_shape_ok(int head_num, int kv_mul, int hd) {
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
   static_assert(HD % 4 == 0 && HD <= 256 && (256 % HD) == 0, "head size");
-  extern __shared__ float lds[];
-  constexpr int TPR = HD / 4;     // threads per key row
-  constexpr int RPP = 256 / TPR;  // key rows per pass
-  constexpr int NTG = 256 / HD;   // position groups in the PV product
+  constexpr int PT = attn_chunk(HD);  // positions per workgroup
+  constexpr int TPR = HD / 4;         // lanes per key row (one f4 each)
+  constexpr int RPP = 256 / TPR;      // rows per pass
+  constexpr int NP = PT / RPP;        // passes: rows per lane
   constexpr int HALF = HD / 2;
+  static_assert(NP >= 1 && NP * RPP == PT, "chunk geometry");
+  extern __shared__ float lds[];
+  __shared__ int s_last;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int sub = tid % TPR;  // which f4 of the row
+  const int rr = tid / TPR;   // row within a pass
   const int g = blockIdx.x / a.G;
   const int s = blockIdx.x - g * a.G;
   const int kvm = a.kv_mul;
   const int pos = a.pos_ptr ? *a.pos_ptr : a.pos_val;
   const int n = pos + 1;
-  int chunk = (n + a.G - 1) / a.G;
-  if (chunk < a.min_chunk) chunk = a.min_chunk;
-  const int nsplit = (n + chunk - 1) / chunk;
+  const int nsplit = (n + PT - 1) / PT;
   if (s >= nsplit) return;  // uniform for the whole workgroup
-  const int t0 = s * chunk;
-  const int cnt = min(n, t0 + chunk) - t0;
+  const int t0 = s * PT;
+  const int cnt = min(n - t0, PT);
+  const bool own_pos = pos >= t0 && pos < t0 + cnt;
 
-  float* qs = lds;                    // [kvm][HD]
-  float* sc = qs + kvm * HD;          // [kvm][ch_max]
-  float* kp = sc + kvm * a.ch_max;    // [HD] transformed K[pos]
-  float* ml = kp + HD;                // [2 * kAttnMaxKvMul] (m, l)
-  float* red = ml + 2 * kAttnMaxKvMul;  // [NTG][kvm][HD]
-  __shared__ int s_last;
+  // 1. The chunk's K and V rows, straight into registers.
+  f4 kr[NP], vr[NP];
+  {
+    const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int tt = p * RPP + rr;
+      const size_t off = static_cast<size_t>(t0 + (tt < cnt ? tt : 0)) * a.kv_dim + col;
+      kr[p] = *reinterpret_cast<const f4*>(a.kcache + off);
+      vr[p] = *reinterpret_cast<const f4*>(a.vcache + off);
+    }
+  }
 
+  float* qs = lds;                 // [kvm][HD]
+  float* sc = qs + kvm * HD;       // [kvm][PT]
+  float* kp = sc + kvm * PT;       // [HD]
+  float* ml = kp + HD;             // [2 * kAttnMaxKvMul]
+  float* red = ml + 2 * kAttnMaxKvMul;  // [RPP][kvm][HD]
+
+  // 2. q of the group's heads (and its transforms), K[pos] transform.
   const float* qg = a.q + static_cast<size_t>(g) * kvm * HD;
   for (int i = tid; i < kvm * HD; i += 256) qs[i] = qg[i];
   __syncthreads();
-
   if (a.transform == 2) {
     // Per-head RMSNorm of q (kernels/cuda/rmsnorm_kernel.cu:8-60): one wave per head.
     for (int h = wave; h < kvm; h += kWavesPerBlock) {
@@ -142,9 +162,9 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
       qs[i0] = v0;
       qs[i1] = v1;
     }
-    // K[pos] of this kv head: done by wave 0 of the workgroup that owns pos,
-    // in registers (each lane holds whole pairs), then written to the cache.
-    if (wave == 0 && pos >= t0 && pos < t0 + cnt) {
+    // K[pos] of this kv head: wave 0 of the workgroup owning pos, in registers
+    // (each lane holds whole pairs), then written back to the cache.
+    if (wave == 0 && own_pos) {
       float* krow = a.kcache + static_cast<size_t>(pos) * a.kv_dim + static_cast<size_t>(g) * HD;
       constexpr int PPL = (HALF + kWave - 1) / kWave;  // pairs per lane
       float v0[PPL], v1[PPL];
@@ -185,45 +205,43 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
       }
     }
     __syncthreads();
+    if (own_pos) {
+      // The lane that prefetched K[pos] (raw) takes the transformed row.
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        if (t0 + p * RPP + rr == pos) kr[p] = reinterpret_cast<const f4*>(kp)[sub];
+    }
   }
 
-  // Scores: TPR lanes per key row, every row used for all kvm query heads.
+  // 3. Scores: TPR lanes per key row, each row used for all kvm query heads.
   {
-    const int sub = tid % TPR;
     const f4* q4 = reinterpret_cast<const f4*>(qs);
-    const int passes = (cnt + RPP - 1) / RPP;
-    for (int ps = 0; ps < passes; ++ps) {
-      const int tt = ps * RPP + tid / TPR;
-      const bool valid = tt < cnt;
-      const int t = t0 + (valid ? tt : 0);
-      const float* krow = (a.transform >= 1 && t == pos)
-                              ? kp
-                              : a.kcache + static_cast<size_t>(t) * a.kv_dim +
-                                    static_cast<size_t>(g) * HD;
-      const f4 k4 = reinterpret_cast<const f4*>(krow)[sub];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int tt = p * RPP + rr;
 #pragma unroll
       for (int h = 0; h < kAttnMaxKvMul; ++h) {
         if (h < kvm) {
-          float d = hsum(k4 * q4[h * TPR + sub]);
+          float d = hsum(kr[p] * q4[h * TPR + sub]);
           d = group_sum(d, TPR);
-          if (valid && sub == 0) sc[h * a.ch_max + tt] = d * a.scale;
+          if (sub == 0 && tt < cnt) sc[h * PT + tt] = d * a.scale;
         }
       }
     }
   }
   __syncthreads();
 
-  // Chunk-local softmax statistics, one wave per head.
+  // 4. Chunk-local softmax statistics, one wave per head.
   for (int h = wave; h < kvm; h += kWavesPerBlock) {
-    float* sh = sc + h * a.ch_max;
+    float* sh = sc + h * PT;
     float m = -INFINITY;
     for (int tt = lane; tt < cnt; tt += kWave) m = fmaxf(m, sh[tt]);
     m = wave_max(m);
     float l = 0.f;
     for (int tt = lane; tt < cnt; tt += kWave) {
-      const float p = expf(sh[tt] - m);
-      sh[tt] = p;
-      l += p;
+      const float e = expf(sh[tt] - m);
+      sh[tt] = e;
+      l += e;
     }
     l = wave_sum(l);
     if (lane == 0) {
@@ -233,82 +251,69 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
   }
   __syncthreads();
 
-  // o_h[d] = sum_t p_h[t] V_t[d]; NTG position groups, reduced through LDS.
-  const int d = tid % HD;
-  const int tg = tid / HD;
-  float o[kAttnMaxKvMul];
+  // 5. o_h = sum_t p_h[t] V_t: per-lane partials over its rows, then summed
+  //    over the RPP row slots through LDS.
 #pragma unroll
-  for (int h = 0; h < kAttnMaxKvMul; ++h) o[h] = 0.f;
-  for (int tt = tg; tt < cnt; tt += NTG) {
-    const float v =
-        a.vcache[static_cast<size_t>(t0 + tt) * a.kv_dim + static_cast<size_t>(g) * HD + d];
+  for (int h = 0; h < kAttnMaxKvMul; ++h) {
+    if (h < kvm) {
+      f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int h = 0; h < kAttnMaxKvMul; ++h)
-      if (h < kvm) o[h] += sc[h * a.ch_max + tt] * v;
-  }
-  if constexpr (NTG > 1) {
-#pragma unroll
-    for (int h = 0; h < kAttnMaxKvMul; ++h)
-      if (h < kvm) red[(tg * kvm + h) * HD + d] = o[h];
-    __syncthreads();
-    if (tg == 0) {
-#pragma unroll
-      for (int h = 0; h < kAttnMaxKvMul; ++h) {
-        if (h < kvm) {
-          float t = o[h];
-          for (int k = 1; k < NTG; ++k) t += red[(k * kvm + h) * HD + d];
-          o[h] = t;
-        }
+      for (int p = 0; p < NP; ++p) {
+        const int tt = p * RPP + rr;
+        if (tt < cnt) o += sc[h * PT + tt] * vr[p];
       }
+      reinterpret_cast<f4*>(red + (static_cast<size_t>(rr) * kvm + h) * HD)[sub] = o;
     }
-  }
-
-  float* outg = a.out + static_cast<size_t>(g) * kvm * HD;
-  if (nsplit == 1) {
-    if (tg == 0) {
-#pragma unroll
-      for (int h = 0; h < kAttnMaxKvMul; ++h)
-        if (h < kvm) outg[h * HD + d] = o[h] / ml[2 * h + 1];
-    }
-    return;
-  }
-
-  float* pg = a.part + static_cast<size_t>(g) * a.G * kvm * (HD + 2);
-  if (tg == 0) {
-    float* ps = pg + static_cast<size_t>(s) * kvm * (HD + 2);
-#pragma unroll
-    for (int h = 0; h < kAttnMaxKvMul; ++h) {
-      if (h < kvm) {
-        ps[h * (HD + 2) + d] = o[h];
-        if (d == 0) {
-          ps[h * (HD + 2) + HD] = ml[2 * h];
-          ps[h * (HD + 2) + HD + 1] = ml[2 * h + 1];
-        }
-      }
-    }
-    __threadfence();
   }
   __syncthreads();
+
+  float* outg = a.out + static_cast<size_t>(g) * kvm * HD;
+  float* pg = a.part + static_cast<size_t>(g) * a.G * kvm * (HD + 2);
+  for (int idx = tid; idx < kvm * HD; idx += 256) {
+    const int h = idx / HD, d = idx - h * HD;
+    float o = 0.f;
+    for (int k = 0; k < RPP; ++k) o += red[(static_cast<size_t>(k) * kvm + h) * HD + d];
+    if (nsplit == 1) {
+      outg[h * HD + d] = o / ml[2 * h + 1];
+    } else {
+      float* ps = pg + (static_cast<size_t>(s) * kvm + h) * (HD + 2);
+      store_coherent(ps + d, o);
+      if (d == 0) {
+        store_coherent(ps + HD, ml[2 * h]);
+        store_coherent(ps + HD + 1, ml[2 * h + 1]);
+      }
+    }
+  }
+  if (nsplit == 1) return;
+
+  wait_mem();
+  __syncthreads();
   if (tid == 0) {
-    const unsigned int prev = atomicAdd(a.counters + g, 1u);
+    const unsigned int prev = arrive(a.counters + g);
     s_last = (prev == static_cast<unsigned int>(nsplit - 1)) ? 1 : 0;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
+  // 6. Merge the chunks of this kv head.  The (m, l) pairs go through LDS
+  //    once; the o rows are read in one pass.
+  float* mls = red;  // reuse: [nsplit][kvm][2]
+  for (int i = tid; i < nsplit * kvm; i += 256) {
+    const float* pk = pg + static_cast<size_t>(i) * (HD + 2);
+    mls[2 * i] = load_coherent(pk + HD);
+    mls[2 * i + 1] = load_coherent(pk + HD + 1);
+  }
+  __syncthreads();
   for (int idx = tid; idx < kvm * HD; idx += 256) {
-    const int h = idx / HD, dd = idx - h * HD;
+    const int h = idx / HD, d = idx - h * HD;
     float M = -INFINITY;
-    for (int k = 0; k < nsplit; ++k)
-      M = fmaxf(M, pg[(static_cast<size_t>(k) * kvm + h) * (HD + 2) + HD]);
+    for (int k = 0; k < nsplit; ++k) M = fmaxf(M, mls[2 * (k * kvm + h)]);
     float L = 0.f, O = 0.f;
     for (int k = 0; k < nsplit; ++k) {
-      const float* pk = pg + (static_cast<size_t>(k) * kvm + h) * (HD + 2);
-      const float w = expf(pk[HD] - M);
-      L += pk[HD + 1] * w;
-      O += pk[dd] * w;
+      const float w = expf(mls[2 * (k * kvm + h)] - M);
+      L += mls[2 * (k * kvm + h) + 1] * w;
+      O += load_coherent(pg + (static_cast<size_t>(k) * kvm + h) * (HD + 2) + d) * w;
     }
-    outg[h * HD + dd] = O / L;
+    outg[h * HD + d] = O / L;
   }
   if (tid == 0) a.counters[g] = 0u;
 }

@@ -72,6 +72,32 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
+// Cross-workgroup hand-off without cache maintenance.  The L2 of an MI355X
+// XCD is not coherent with the other XCDs' L2s, and a device-scope fence
+// (__threadfence) writes back and invalidates the whole L2.  Instead, the few
+// words one workgroup passes to another go through agent-coherent (sc1)
+// stores and loads, the producer waits for its stores to complete
+// (wait_mem) before a device-scope atomic announces them, and the consumer,
+// having observed the atomic, reads them with coherent loads.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_coherent(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+// Device-scope arrival counter; returns the previous value.
+__device__ __forceinline__ unsigned int arrive(unsigned int* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // RoPE rotation of one pair, written without contraction so that the result
 // is the same float expression the reference CPU path evaluates
 // (kernels/cpu/rope_kernel.cpp:37-38 / :115-118): v0*c - v1*s, v0*s + v1*c.

@@ -46,149 +46,121 @@ struct StepState {
 inline int rc(hipError_t e) { return e == hipSuccess ? KL_OK : static_cast<int>(e); }
 
 // ---------------------------------------------------------------------------
-// Kernels.
+// Kernels.  Each GEMV-shaped kernel is run_tiles() with its own row map,
+// input staging and epilogue (see gemv.hpp); blockDim = 64 * KS * G.
 // ---------------------------------------------------------------------------
+constexpr int kRedFloats = 32;
 
-// Stage the GEMV input vector in LDS; with a norm weight, apply RMSNorm on the
-// way (kernels/cpu/rmsnorm_kernel.cpp:30-32: w * (x / sqrt(mean(x^2) + eps))).
-// Contains barriers: every thread of the block must call it.
-__device__ __forceinline__ void stage_input(const float* __restrict__ x,
-                                            const float* __restrict__ nw, float eps, int n,
-                                            float* xs, float* red) {
-  if (nw) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kBlock) {
-      const float v = x[i];
-      ss += v * v;
-    }
-    ss = block_sum(ss, red);
-    const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
-    for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = nw[i] * (r * x[i]);
-  } else {
-    for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = x[i];
-  }
-  __syncthreads();
-}
-
-__global__ __launch_bounds__(256) void k_embed(const StepState* __restrict__ st,
-                                              const float* __restrict__ E, int D,
-                                              float* __restrict__ x) {
-  const float* src = E + static_cast<size_t>(st->token) * D;
-  for (int c = threadIdx.x; c < D; c += kBlock) x[c] = src[c];
-}
-
+// [Wq; Wk; Wv] . RMSNorm(x); q -> q buffer, k/v -> cache slot at state.pos,
+// + bias (Qwen2).  Layer 0 reads its input straight from the embedding row of
+// state.token and workgroup 0 stores it as the residual stream x.
 struct QkvArgs {
   const float* x;
+  const float* emb;  // layer 0 only: embedding table
+  float* x_out;      // layer 0 only: residual stream
+  const StepState* st;
   const float* nw;
   float eps;
-  int D, Dq, Dkv, chunk_shift;
+  int D, Dq, Dkv;
+  ColGeom g;
   WView wq, wk, wv;
   const float *bq, *bk, *bv;
   float* q_out;
   float* kcache;  // layer base
   float* vcache;  // layer base
-  const StepState* st;
 };
 
-template <bool Q8, int R, int U>
-__global__ __launch_bounds__(256) void k_qkv(QkvArgs a) {
+template <bool Q8, int U>
+__global__ __launch_bounds__(512) void k_qkv(QkvArgs a) {
   extern __shared__ float xs[];
-  __shared__ float red[kWavesPerBlock];
-  stage_input(a.x, a.nw, a.eps, a.D, xs, red);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ float red[kRedFloats];
   const int pos = a.st->pos;
   const int total = a.Dq + 2 * a.Dkv;
-  const int nblk = (total + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
-  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int row0 = (b * kWavesPerBlock + wave) * R;
-    if (row0 >= total) continue;
-    WView w;
-    const float* bias;
-    float* out;
-    int lr, seg_rows;
-    if (row0 < a.Dq) {
-      w = a.wq; bias = a.bq; out = a.q_out; lr = row0; seg_rows = a.Dq;
-    } else if (row0 < a.Dq + a.Dkv) {
-      w = a.wk; bias = a.bk; out = a.kcache + static_cast<size_t>(pos) * a.Dkv;
-      lr = row0 - a.Dq; seg_rows = a.Dkv;
+  auto rows = [&](int u, int, WView& m, size_t& row) {
+    if (u < a.Dq) {
+      m = a.wq;
+      row = u;
+    } else if (u < a.Dq + a.Dkv) {
+      m = a.wk;
+      row = u - a.Dq;
     } else {
-      w = a.wv; bias = a.bv; out = a.vcache + static_cast<size_t>(pos) * a.Dkv;
-      lr = row0 - a.Dq - a.Dkv; seg_rows = a.Dkv;
+      m = a.wv;
+      row = u - a.Dq - a.Dkv;
     }
-    const int nr = min(R, seg_rows - lr);
-    float part[R];
-    gemv_rows<Q8, R, U>(w, a.D, a.chunk_shift, lr, nr, xs, part);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(part[r]);
-      if (lane == 0 && r < nr) out[lr + r] = bias ? v + bias[lr + r] : v;
+  };
+  auto stage = [&]() {
+    const float* x = a.emb ? a.emb + static_cast<size_t>(a.st->token) * a.D : a.x;
+    if (a.emb && blockIdx.x == 0)
+      for (int i = threadIdx.x; i < a.D; i += blockDim.x) a.x_out[i] = x[i];
+    stage_input(x, a.nw, a.eps, a.D, xs, red);
+  };
+  auto epi = [&](int u, const float (&v)[1]) {
+    if ((threadIdx.x & 63) != 0) return;
+    if (u < a.Dq) {
+      a.q_out[u] = a.bq ? v[0] + a.bq[u] : v[0];
+    } else if (u < a.Dq + a.Dkv) {
+      const int r = u - a.Dq;
+      a.kcache[static_cast<size_t>(pos) * a.Dkv + r] = a.bk ? v[0] + a.bk[r] : v[0];
+    } else {
+      const int r = u - a.Dq - a.Dkv;
+      a.vcache[static_cast<size_t>(pos) * a.Dkv + r] = a.bv ? v[0] + a.bv[r] : v[0];
     }
-  }
+  };
+  run_tiles<Q8, 1, U>(a.g, total, xs, red, rows, stage, epi);
 }
 
 // x[row] += W[row, :] . in   (output projection and down projection + residual)
 struct ResArgs {
   const float* in;
-  int cols, rows, chunk_shift;
+  int rows;
+  ColGeom g;
   WView w;
   float* x;
 };
 
-template <bool Q8, int R, int U>
-__global__ __launch_bounds__(256) void k_gemv_residual(ResArgs a) {
+template <bool Q8, int U>
+__global__ __launch_bounds__(512) void k_gemv_residual(ResArgs a) {
   extern __shared__ float xs[];
-  stage_input(a.in, nullptr, 0.f, a.cols, xs, nullptr);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nblk = (a.rows + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
-  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int row0 = (b * kWavesPerBlock + wave) * R;
-    if (row0 >= a.rows) continue;
-    const int nr = min(R, a.rows - row0);
-    float part[R];
-    gemv_rows<Q8, R, U>(a.w, a.cols, a.chunk_shift, row0, nr, xs, part);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(part[r]);
-      if (lane == 0 && r < nr) a.x[row0 + r] = a.x[row0 + r] + v;
-    }
-  }
+  __shared__ float red[kRedFloats];
+  auto rows = [&](int u, int, WView& m, size_t& row) {
+    m = a.w;
+    row = u;
+  };
+  auto stage = [&]() { stage_input(a.in, nullptr, 0.f, a.g.cols, xs, red); };
+  auto epi = [&](int u, const float (&v)[1]) {
+    if ((threadIdx.x & 63) == 0) a.x[u] = a.x[u] + v[0];
+  };
+  run_tiles<Q8, 1, U>(a.g, a.rows, xs, red, rows, stage, epi);
 }
 
-// h[r] = silu(W1[r] . xn) * (W3[r] . xn), xn = RMSNorm(x): each wave streams RH
-// rows of W1 and the same RH rows of W3 together.
+// h[r] = silu(W1[r] . xn) * (W3[r] . xn), xn = RMSNorm(x): a tile is row r of
+// W1 and row r of W3 (R = 2).
 struct W13Args {
   const float* x;
   const float* nw;
   float eps;
-  int D, F, chunk_shift;
+  int D, F;
+  ColGeom g;
   WView w1, w3;
   float* h;
 };
 
-template <bool Q8, int RH, int U>
-__global__ __launch_bounds__(256) void k_w13_swiglu(W13Args a) {
+template <bool Q8, int U>
+__global__ __launch_bounds__(512) void k_w13_swiglu(W13Args a) {
   extern __shared__ float xs[];
-  __shared__ float red[kWavesPerBlock];
-  stage_input(a.x, a.nw, a.eps, a.D, xs, red);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nblk = (a.F + RH * kWavesPerBlock - 1) / (RH * kWavesPerBlock);
-  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int row0 = (b * kWavesPerBlock + wave) * RH;
-    if (row0 >= a.F) continue;
-    const int nr = min(RH, a.F - row0);
-    float pa[RH], pb[RH];
-    gemv_rows_pair<Q8, RH, U>(a.w1, a.w3, a.D, a.chunk_shift, row0, nr, xs, pa, pb);
-#pragma unroll
-    for (int r = 0; r < RH; ++r) {
-      const float va = wave_sum(pa[r]);
-      const float vb = wave_sum(pb[r]);
-      if (lane == 0 && r < nr) {
-        // kernels/cpu/swiglu_kernel.cpp:21-22
-        const float s = va * (1.0f / (1.0f + expf(-va)));
-        a.h[row0 + r] = s * vb;
-      }
-    }
-  }
+  __shared__ float red[kRedFloats];
+  auto rows = [&](int u, int r, WView& m, size_t& row) {
+    m = r == 0 ? a.w1 : a.w3;
+    row = u;
+  };
+  auto stage = [&]() { stage_input(a.x, a.nw, a.eps, a.D, xs, red); };
+  auto epi = [&](int u, const float (&v)[2]) {
+    if ((threadIdx.x & 63) != 0) return;
+    // kernels/cpu/swiglu_kernel.cpp:21-22
+    const float s = v[0] * (1.0f / (1.0f + expf(-v[0])));
+    a.h[u] = s * v[1];
+  };
+  run_tiles<Q8, 2, U>(a.g, a.F, xs, red, rows, stage, epi);
 }
 
 // Classifier + greedy sampling.
@@ -196,7 +168,8 @@ struct ClsArgs {
   const float* x;
   const float* nw;
   float eps;
-  int D, V, chunk_shift;
+  int D, V;
+  ColGeom g;
   WView w;
   float* logits;
   float* pv;
@@ -207,12 +180,12 @@ struct ClsArgs {
   int32_t* out_tokens;
 };
 
-template <bool Q8, int R, int U>
-__global__ __launch_bounds__(256) void k_cls_argmax(ClsArgs a) {
+template <bool Q8, int U>
+__global__ __launch_bounds__(512) void k_cls_argmax(ClsArgs a) {
   extern __shared__ float xs[];
-  __shared__ float red[kWavesPerBlock];
-  __shared__ float sv[kWavesPerBlock];
-  __shared__ int si[kWavesPerBlock];
+  __shared__ float red[kRedFloats];
+  __shared__ float sv[16];
+  __shared__ int si[16];
   __shared__ int s_last;
   const int pos = a.st->pos;
   const int P = a.st->prompt_len;
@@ -226,26 +199,19 @@ __global__ __launch_bounds__(256) void k_cls_argmax(ClsArgs a) {
     }
     return;
   }
-  stage_input(a.x, a.nw, a.eps, a.D, xs, red);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   float bv = -INFINITY;
   int bi = INT_MAX;
-  const int nblk = (a.V + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
-  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int row0 = (b * kWavesPerBlock + wave) * R;
-    if (row0 >= a.V) continue;
-    const int nr = min(R, a.V - row0);
-    float part[R];
-    gemv_rows<Q8, R, U>(a.w, a.D, a.chunk_shift, row0, nr, xs, part);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(part[r]);
-      if (r < nr) {
-        if (lane == 0) a.logits[row0 + r] = v;
-        argmax_merge(bv, bi, v, row0 + r);
-      }
-    }
-  }
+  auto rows = [&](int u, int, WView& m, size_t& row) {
+    m = a.w;
+    row = u;
+  };
+  auto stage = [&]() { stage_input(a.x, a.nw, a.eps, a.D, xs, red); };
+  auto epi = [&](int u, const float (&v)[1]) {
+    if (lane == 0) a.logits[u] = v[0];
+    argmax_merge(bv, bi, v[0], u);
+  };
+  run_tiles<Q8, 1, U>(a.g, a.V, xs, red, rows, stage, epi);
   // Every lane of a wave holds the same (bv, bi); merge the waves.
   if (lane == 0) {
     sv[wave] = bv;
@@ -253,20 +219,19 @@ __global__ __launch_bounds__(256) void k_cls_argmax(ClsArgs a) {
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(bv, bi, sv[w], si[w]);
-    a.pv[blockIdx.x] = bv;
-    a.pi[blockIdx.x] = bi;
-    __threadfence();
-    const unsigned int prev = atomicAdd(a.counter, 1u);
+    for (int w = 1; w < nw; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+    store_coherent(a.pv + blockIdx.x, bv);
+    store_coherent(a.pi + blockIdx.x, bi);
+    wait_mem();
+    const unsigned int prev = arrive(a.counter);
     s_last = prev == gridDim.x - 1;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   bv = -INFINITY;
   bi = INT_MAX;
-  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kBlock)
-    argmax_merge(bv, bi, a.pv[b], a.pi[b]);
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += blockDim.x)
+    argmax_merge(bv, bi, load_coherent(a.pv + b), load_coherent(a.pi + b));
   wave_argmax(bv, bi);
   if (lane == 0) {
     sv[wave] = bv;
@@ -274,7 +239,7 @@ __global__ __launch_bounds__(256) void k_cls_argmax(ClsArgs a) {
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+    for (int w = 1; w < nw; ++w) argmax_merge(bv, bi, sv[w], si[w]);
     a.st->sampled = bi;
     a.st->token = bi;
     a.out_tokens[pos] = bi;
@@ -454,7 +419,13 @@ struct kl_engine {
   int32_t* prompt = nullptr;
   int32_t* out_tokens = nullptr;
   MhaPlan attn{};
-  int grid_cap = 1024;
+  int grid_cap = 2048;
+  struct GemvLaunch {
+    ColGeom g;
+    int U;
+    dim3 grid, block;
+    size_t lds;
+  } l_qkv, l_wo, l_w13, l_w2, l_cls;
   bool use_graph = true;
   hipGraphExec_t graph_exec = nullptr;
   hipGraph_t graph = nullptr;
@@ -463,15 +434,24 @@ struct kl_engine {
 
 namespace {
 
-// Tile choices (rows per wave R, 16-byte chunks in flight per row U).
-constexpr int kR = 2, kU = 4;    // qkv, residual GEMVs, classifier
-constexpr int kRH = 1, kUH = 4;  // W1/W3 pair: 2 rows per wave
-
-size_t lds_for(int n) { return static_cast<size_t>(n) * sizeof(float); }
-
-int grid_for(const kl_engine* e, int rows, int rows_per_block) {
-  const int nblk = (rows + rows_per_block - 1) / rows_per_block;
-  return std::max(1, std::min(nblk, e->grid_cap));
+// GEMV launch plan for `units` row units over `cols` columns: U = 4 chunks
+// per lane per slice (4 KiB of a row per wave) with KS waves per row, or U = 8
+// when a row would need more than kMaxKs slices; G rows per workgroup pass.
+// Measured on MI355X (cold HBM): 4 KiB tiles with split-K and a grid of two
+// workgroups per CU stream the 1 GB classifier at ~7 TB/s.
+kl_engine::GemvLaunch plan_gemv(const kl_engine* e, int units, int cols) {
+  kl_engine::GemvLaunch L;
+  const bool q8 = e->quant != 0;
+  const ColGeom g8 = make_geom(cols, q8, 8, e->lay.gs), g4 = make_geom(cols, q8, 4, e->lay.gs);
+  const bool use4 = g4.ks <= kMaxKs;
+  L.U = use4 ? 4 : 8;
+  L.g = use4 ? g4 : g8;
+  const int G = row_groups_for(L.g.ks);
+  const int nblk = (units + G - 1) / G;
+  L.grid = dim3(std::max(1, std::min(nblk, e->grid_cap)));
+  L.block = dim3(kWave * L.g.ks * G);
+  L.lds = static_cast<size_t>(cols) * sizeof(float);
+  return L;
 }
 
 // Kernel kinds, in launch order within a layer; used by the profiler.
@@ -494,27 +474,34 @@ inline void mark(hipStream_t s, Marks* mk, int kind) {
   mk->kinds->push_back(kind);
 }
 
+#define KL_GEMV_LAUNCH(KERNEL, Q8, L, S, ARGS)                                        \
+  do {                                                                                \
+    if ((L).U == 8)                                                                   \
+      hipLaunchKernelGGL((KERNEL<Q8, 8>), (L).grid, (L).block, (L).lds, (S), (ARGS)); \
+    else                                                                              \
+      hipLaunchKernelGGL((KERNEL<Q8, 4>), (L).grid, (L).block, (L).lds, (S), (ARGS)); \
+  } while (0)
+
 template <bool Q8>
 int launch_step_t(kl_engine* e, Marks* mk) {
   const ImageLayout& m = e->lay;
   hipStream_t s = e->stream;
-  const int rpb = kR * kWavesPerBlock;
-  mark(s, mk, kKEmbed);
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, s, e->st, e->emb, m.D, e->x);
   const size_t kv_layer = static_cast<size_t>(m.S) * m.Dkv;
   for (int l = 0; l < m.L; ++l) {
     const LayerDev& L = e->layers[l];
     QkvArgs qa{};
-    qa.x = e->x; qa.nw = L.rms_att; qa.eps = e->eps;
-    qa.D = m.D; qa.Dq = m.Dq; qa.Dkv = m.Dkv; qa.chunk_shift = e->chunk_shift;
+    qa.x = e->x;
+    qa.emb = l == 0 ? e->emb : nullptr;
+    qa.x_out = e->x;
+    qa.st = e->st;
+    qa.nw = L.rms_att; qa.eps = e->eps;
+    qa.D = m.D; qa.Dq = m.Dq; qa.Dkv = m.Dkv; qa.g = e->l_qkv.g;
     qa.wq = L.wq; qa.wk = L.wk; qa.wv = L.wv; qa.bq = L.bq; qa.bk = L.bk; qa.bv = L.bv;
     qa.q_out = e->q;
     qa.kcache = e->kcache + l * kv_layer;
     qa.vcache = e->vcache + l * kv_layer;
-    qa.st = e->st;
     mark(s, mk, kKQkv);
-    hipLaunchKernelGGL((k_qkv<Q8, kR, kU>), dim3(grid_for(e, m.Dq + 2 * m.Dkv, rpb)),
-                       dim3(kBlock), lds_for(m.D), s, qa);
+    KL_GEMV_LAUNCH(k_qkv, Q8, e->l_qkv, s, qa);
 
     AttnArgs aa{};
     aa.q = e->q;
@@ -527,8 +514,6 @@ int launch_step_t(kl_engine* e, Marks* mk) {
     aa.kv_dim = m.Dkv;
     aa.kv_mul = m.H / m.KVH;
     aa.G = e->attn.G;
-    aa.min_chunk = e->attn.min_chunk;
-    aa.ch_max = e->attn.ch_max;
     aa.transform = e->transform;
     aa.rope_style = e->rope_style;
     aa.sin_t = e->sin_t;
@@ -547,37 +532,30 @@ int launch_step_t(kl_engine* e, Marks* mk) {
     }
 
     ResArgs ra{};
-    ra.in = e->att; ra.cols = m.Dq; ra.rows = m.D; ra.chunk_shift = e->chunk_shift;
-    ra.w = L.wo; ra.x = e->x;
+    ra.in = e->att; ra.rows = m.D; ra.g = e->l_wo.g; ra.w = L.wo; ra.x = e->x;
     mark(s, mk, kKWo);
-    hipLaunchKernelGGL((k_gemv_residual<Q8, kR, kU>), dim3(grid_for(e, m.D, rpb)), dim3(kBlock),
-                       lds_for(m.Dq), s, ra);
+    KL_GEMV_LAUNCH(k_gemv_residual, Q8, e->l_wo, s, ra);
 
     W13Args wa{};
     wa.x = e->x; wa.nw = L.rms_ffn; wa.eps = e->eps;
-    wa.D = m.D; wa.F = m.F; wa.chunk_shift = e->chunk_shift;
+    wa.D = m.D; wa.F = m.F; wa.g = e->l_w13.g;
     wa.w1 = L.w1; wa.w3 = L.w3; wa.h = e->h;
     mark(s, mk, kKW13);
-    hipLaunchKernelGGL((k_w13_swiglu<Q8, kRH, kUH>),
-                       dim3(grid_for(e, m.F, kRH * kWavesPerBlock)), dim3(kBlock), lds_for(m.D), s,
-                       wa);
+    KL_GEMV_LAUNCH(k_w13_swiglu, Q8, e->l_w13, s, wa);
 
     ResArgs rb{};
-    rb.in = e->h; rb.cols = m.F; rb.rows = m.D; rb.chunk_shift = e->chunk_shift;
-    rb.w = L.w2; rb.x = e->x;
+    rb.in = e->h; rb.rows = m.D; rb.g = e->l_w2.g; rb.w = L.w2; rb.x = e->x;
     mark(s, mk, kKW2);
-    hipLaunchKernelGGL((k_gemv_residual<Q8, kR, kU>), dim3(grid_for(e, m.D, rpb)), dim3(kBlock),
-                       lds_for(m.F), s, rb);
+    KL_GEMV_LAUNCH(k_gemv_residual, Q8, e->l_w2, s, rb);
   }
   ClsArgs ca{};
   ca.x = e->x; ca.nw = e->rms_final; ca.eps = e->eps;
-  ca.D = m.D; ca.V = m.V; ca.chunk_shift = e->chunk_shift;
+  ca.D = m.D; ca.V = m.V; ca.g = e->l_cls.g;
   ca.w = e->wcls; ca.logits = e->logits;
   ca.pv = e->am_pv; ca.pi = e->am_pi; ca.counter = e->am_counter;
   ca.st = e->st; ca.prompt = e->prompt; ca.out_tokens = e->out_tokens;
   mark(s, mk, kKCls);
-  hipLaunchKernelGGL((k_cls_argmax<Q8, kR, kU>), dim3(grid_for(e, m.V, rpb)), dim3(kBlock),
-                     lds_for(m.D), s, ca);
+  KL_GEMV_LAUNCH(k_cls_argmax, Q8, e->l_cls, s, ca);
   mark(s, mk, kKinds);
   return rc(hipGetLastError());
 }
@@ -660,12 +638,27 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   hipDeviceProp_t prop;
   if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
     e->cus = prop.multiProcessorCount;
-  e->grid_cap = e->cus * 4;
+  e->grid_cap = e->cus * 2;
   if (const char* env = std::getenv("KL_GRID_PER_CU")) {
     const int v = std::atoi(env);
     if (v > 0) e->grid_cap = e->cus * v;
   }
   e->attn = mha_plan(lay.KVH, kv_mul, lay.S, lay.hd);
+  if (e->attn.G > 512) {
+    delete e;
+    return KL_EUNSUPP;  // the chunk merge keeps (m, l) of at most 512 chunks in LDS
+  }
+  e->l_qkv = plan_gemv(e, lay.Dq + 2 * lay.Dkv, lay.D);
+  e->l_wo = plan_gemv(e, lay.D, lay.Dq);
+  e->l_w13 = plan_gemv(e, lay.F, lay.D);
+  e->l_w2 = plan_gemv(e, lay.D, lay.F);
+  e->l_cls = plan_gemv(e, lay.V, lay.D);
+  for (const auto* L : {&e->l_qkv, &e->l_wo, &e->l_w13, &e->l_w2, &e->l_cls}) {
+    if (L->g.ks > kMaxKs) {
+      delete e;
+      return KL_EUNSUPP;
+    }
+  }
 
   // Arena plan: every tensor 256-byte aligned.
   size_t cursor = 0;

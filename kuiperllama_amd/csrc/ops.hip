@@ -28,28 +28,43 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // ---------------------------------------------------------------------------
 // GEMV (MatmulKernel / MatmulKernelQuant).
 // ---------------------------------------------------------------------------
-constexpr int kGemvR = 2;  // rows per wave
-constexpr int kGemvU = 4;  // 16-byte chunks per row in flight per lane
-constexpr int kRowsPerBlock = kGemvR * kWavesPerBlock;
+// Vector path: run_tiles() with x read straight from global memory (it is
+// small and cache resident), one wave per (row, 8 KiB slice).
+template <bool Q8, int U>
+__global__ __launch_bounds__(512) void k_gemv(const float* __restrict__ x, WView w, ColGeom g,
+                                             float* __restrict__ y, int rows, float scale) {
+  __shared__ float red[32];
+  auto rowfn = [&](int u, int, WView& m, size_t& row) {
+    m = w;
+    row = u;
+  };
+  auto stage = [] {};
+  auto epi = [&](int u, const float (&v)[1]) {
+    if ((threadIdx.x & 63) == 0) y[u] = v[0] * scale;
+  };
+  run_tiles<Q8, 1, U>(g, rows, x, red, rowfn, stage, epi);
+}
 
-template <int R, int U>
-__global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ x,
-                                                 const float* __restrict__ W, float* __restrict__ y,
-                                                 int rows, int cols, float scale) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nblk = (rows + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
-  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int row0 = (b * kWavesPerBlock + wave) * R;
-    if (row0 >= rows) continue;
-    const int nr = min(R, rows - row0);
-    float part[R];
-    gemv_rows<false, R, U>(WView{W, nullptr}, cols, 0, row0, nr, x, part);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(part[r]);
-      if (lane == 0 && r < nr) y[row0 + r] = v * scale;
-    }
+int launch_gemv(const float* x, WView w, float* y, int rows, int cols, bool q8, int group_size,
+                float scale, hipStream_t s) {
+  ColGeom g = make_geom(cols, q8, 4, group_size);
+  int U = 4;
+  if (g.ks > kMaxKs) {
+    g = make_geom(cols, q8, 8, group_size);
+    U = 8;
   }
+  if (g.ks > kMaxKs) return KL_EUNSUPP;
+  const int G = row_groups_for(g.ks);
+  const int grid = std::max(1, std::min((rows + G - 1) / G, 8192));
+  const dim3 block(kWave * g.ks * G);
+  if (q8) {
+    if (U == 8) hipLaunchKernelGGL((k_gemv<true, 8>), dim3(grid), block, 0, s, x, w, g, y, rows, scale);
+    else hipLaunchKernelGGL((k_gemv<true, 4>), dim3(grid), block, 0, s, x, w, g, y, rows, scale);
+  } else {
+    if (U == 8) hipLaunchKernelGGL((k_gemv<false, 8>), dim3(grid), block, 0, s, x, w, g, y, rows, scale);
+    else hipLaunchKernelGGL((k_gemv<false, 4>), dim3(grid), block, 0, s, x, w, g, y, rows, scale);
+  }
+  return launch_rc();
 }
 
 // Any shape / alignment: one wave per row, scalar loads.
@@ -64,27 +79,6 @@ __global__ __launch_bounds__(256) void k_gemv_f32_scalar(const float* __restrict
     for (int c = lane; c < cols; c += kWave) acc += wr[c] * x[c];
     acc = wave_sum(acc);
     if (lane == 0) y[r] = acc * scale;
-  }
-}
-
-template <int R, int U>
-__global__ __launch_bounds__(256) void k_gemv_q8(const float* __restrict__ x,
-                                                const int8_t* __restrict__ W,
-                                                const float* __restrict__ S, float* __restrict__ y,
-                                                int rows, int cols, int chunk_shift) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nblk = (rows + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
-  for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int row0 = (b * kWavesPerBlock + wave) * R;
-    if (row0 >= rows) continue;
-    const int nr = min(R, rows - row0);
-    float part[R];
-    gemv_rows<true, R, U>(WView{W, S}, cols, chunk_shift, row0, nr, x, part);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(part[r]);
-      if (lane == 0 && r < nr) y[row0 + r] = v;
-    }
   }
 }
 
@@ -112,11 +106,6 @@ __global__ void k_dequant_q8(const int8_t* __restrict__ q, const float* __restri
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
     out[i] = s[i / gs] * static_cast<float>(q[i]);
-}
-
-int gemv_grid(int rows, int rows_per_block) {
-  const int nblk = (rows + rows_per_block - 1) / rows_per_block;
-  return std::max(1, std::min(nblk, 4096));
 }
 
 // ---------------------------------------------------------------------------
@@ -248,18 +237,18 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < kWavesPerBlock; ++w) argmax_merge(v, idx, sv[w], si[w]);
-    pv[blockIdx.x] = v;
-    pi[blockIdx.x] = idx;
-    __threadfence();
-    const unsigned int prev = atomicAdd(counter, 1u);
+    store_coherent(pv + blockIdx.x, v);
+    store_coherent(pi + blockIdx.x, idx);
+    wait_mem();
+    const unsigned int prev = arrive(counter);
     s_last = prev == gridDim.x - 1;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   v = -INFINITY;
   idx = INT_MAX;
-  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256) argmax_merge(v, idx, pv[b], pi[b]);
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256)
+    argmax_merge(v, idx, load_coherent(pv + b), load_coherent(pi + b));
   wave_argmax(v, idx);
   if ((threadIdx.x & 63) == 0) {
     sv[wave] = v;
@@ -381,9 +370,8 @@ int kl_event_elapsed_ms(void* start, void* stop, float* ms) {
 int kl_gemv_f32(const float* x, const float* W, float* y, int rows, int cols, float scale,
                 void* stream) {
   if (!x || !W || !y || rows <= 0 || cols <= 0) return KL_EINVAL;
-  if (cols % 4 == 0 && aligned16(x) && aligned16(W)) {
-    hipLaunchKernelGGL((k_gemv_f32<kGemvR, kGemvU>), dim3(gemv_grid(rows, kRowsPerBlock)),
-                       dim3(256), 0, as_stream(stream), x, W, y, rows, cols, scale);
+  if (cols % 4 == 0 && aligned16(x) && aligned16(W) && cols <= kMaxKs * 2048) {
+    return launch_gemv(x, WView{W, nullptr}, y, rows, cols, false, 0, scale, as_stream(stream));
   } else {
     const int grid = std::max(1, std::min((rows + kWavesPerBlock - 1) / kWavesPerBlock, 4096));
     hipLaunchKernelGGL(k_gemv_f32_scalar, dim3(grid), dim3(256), 0, as_stream(stream), x, W, y,
@@ -398,12 +386,10 @@ int kl_gemv_q8(const float* x, const int8_t* q, const float* scales, float* y, i
   if ((static_cast<int64_t>(rows) * cols) % group_size != 0) return KL_EINVAL;
   const int cpg = group_size / 16;
   const bool vec = group_size % 16 == 0 && (cpg & (cpg - 1)) == 0 && cols % group_size == 0 &&
-                   aligned16(x) && aligned16(q);
+                   aligned16(x) && aligned16(q) && cols <= kMaxKs * 8192;
   if (vec) {
-    int shift = 0;
-    while ((1 << shift) < cpg) ++shift;
-    hipLaunchKernelGGL((k_gemv_q8<kGemvR, kGemvU>), dim3(gemv_grid(rows, kRowsPerBlock)),
-                       dim3(256), 0, as_stream(stream), x, q, scales, y, rows, cols, shift);
+    return launch_gemv(x, WView{q, scales}, y, rows, cols, true, group_size, 1.f,
+                       as_stream(stream));
   } else {
     const int grid = std::max(1, std::min((rows + kWavesPerBlock - 1) / kWavesPerBlock, 4096));
     hipLaunchKernelGGL(k_gemv_q8_scalar, dim3(grid), dim3(256), 0, as_stream(stream), x, q,
@@ -469,7 +455,9 @@ int kl_rope(int style, int dim, int kv_dim, int head_size, float* q, float* k, i
 
 int kl_mha_workspace_size(int head_num, int kv_mul, int seq_len, int head_size, size_t* bytes) {
   if (!bytes || seq_len <= 0 || !mha_shape_ok(head_num, kv_mul, head_size)) return KL_EINVAL;
-  *bytes = mha_plan(head_num / kv_mul, kv_mul, seq_len, head_size).ws_bytes;
+  const MhaPlan p = mha_plan(head_num / kv_mul, kv_mul, seq_len, head_size);
+  if (p.G > 512) return KL_EUNSUPP;
+  *bytes = p.ws_bytes;
   return KL_OK;
 }
 
@@ -482,6 +470,7 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
   const int kv_heads = head_num / kv_mul;
   if (kv_dim != kv_heads * head_size) return KL_EINVAL;
   const MhaPlan p = mha_plan(kv_heads, kv_mul, seq_len, head_size);
+  if (p.G > 512) return KL_EUNSUPP;
   if (workspace_bytes < p.ws_bytes) return KL_EWORKSPACE;
   AttnArgs a{};
   const size_t layer_off = static_cast<size_t>(layer_index) * seq_len * kv_dim;
@@ -497,8 +486,6 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
   a.kv_dim = kv_dim;
   a.kv_mul = kv_mul;
   a.G = p.G;
-  a.min_chunk = p.min_chunk;
-  a.ch_max = p.ch_max;
   a.transform = 0;
   a.scale = 1.f / std::sqrt(static_cast<float>(head_size));
   const dim3 grid(kv_heads * p.G), block(256);
