@@ -84,6 +84,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="first run one 256 MiB device-to-device copy, the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -95,6 +98,13 @@ def main() -> int:
     if K.device_count() < 1:
         print("bench.py: no HIP device", file=sys.stderr)
         return 1
+    if args.pmc_calibration:
+        n = 64 << 20
+        src, dst = K.DeviceArray(n, zero=True), K.DeviceArray(n)
+        K.check(K.lib.kl_memcpy_d2d(dst.ptr, src.ptr, src.nbytes, None), "kl_memcpy_d2d")
+        K.check(K.lib.kl_device_sync(), "kl_device_sync")
+        src.free()
+        dst.free()
     cfg = K.BASELINE[args.config]
     steps = args.steps or cfg.decode_steps
     P = cfg.prompt_len
