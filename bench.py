@@ -11,9 +11,12 @@ on both sides.  Prints one JSON line.
 
   value          decode tok/s (whole job: one GPU)
   achieved_GBps  algorithmic HBM bytes of the timed steps / time
-  roofline       the dominant kernel (W1/W3 + SwiGLU GEMV) alone: algorithmic
-                 bytes per launch / its average duration, from an eager pass
-                 with HIP events between consecutive launches
+  roofline       the dominant kernel: in the default persistent mode the
+                 whole-token kernel k_decode_persistent (one launch = one
+                 decode step, so its bytes are the step's algorithmic bytes);
+                 in --mode multi the W1/W3 + SwiGLU GEMV.  Achieved = bytes per
+                 launch / average launch duration, measured with HIP events
+                 around each launch on the engine's stream
   cpu_baseline   the CPU oracle (a restatement of the reference CPU path,
                  "port") on a bounded sample of the same workload
 """
@@ -84,6 +87,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--mode", choices=("persistent", "multi"), default="multi")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy, the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -116,6 +120,11 @@ def main() -> int:
     t_img = time.time() - t0
     eng = K.Engine(img, cfg)
     eng.set_graph(not args.no_graph)
+    eng.set_mode(K.MODE_MULTI if args.mode == "multi" else K.MODE_PERSISTENT)
+    persistent = eng.mode == K.MODE_PERSISTENT
+    if args.mode == "persistent" and not persistent:
+        print("bench.py: the persistent step does not fit this device; using --mode multi",
+              file=sys.stderr)
     t_load = time.time() - t0 - t_img
     prompt = K.prompt_tokens(cfg)
     print(f"# {K.device_name(0)}; image {img.nbytes / 1e9:.2f} GB in {t_img:.1f} s, "
@@ -131,13 +140,24 @@ def main() -> int:
     print(f"# decode {steps} steps in {ms:.2f} ms ({tok_s:.1f} tok/s, {gbps:.0f} GB/s); "
           f"call wall {wall:.2f} s", file=sys.stderr, flush=True)
 
-    prof = eng.profile(int(toks[-1]), first_pos, args.profile_steps)
+    # Per-launch durations: HIP events around every launch on the engine's
+    # stream, over --profile-steps more decode steps continuing the run.
+    prof_pos = first_pos + steps
+    if prof_pos + args.profile_steps > cfg.seq_len:
+        prof_pos = first_pos
+    prof = eng.profile(int(toks[-1]), prof_pos, args.profile_steps)
     per_step_eager = sum(v[0] * v[1] for v in prof.values()) / args.profile_steps
-    w13_ms = prof["w13"][0]
-    w13_bytes = dominant_kernel_bytes(cfg)
-    w13_gbps = w13_bytes / (w13_ms / 1e3) / 1e9
-    print("# eager per-kernel avg ms: " + ", ".join(f"{k} {v[0]:.4f} x{v[1]}" for k, v in prof.items())
-          + f"; eager step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
+    if persistent:
+        dom_name = "k_decode_persistent (whole decode step: every layer, classifier, argmax)"
+        dom_ms = prof["step"][0]
+        dom_bytes = cfg.decode_bytes(prof_pos, args.profile_steps) / args.profile_steps
+    else:
+        dom_name = "k_w13_swiglu (RMSNorm + W1/W3 GEMV + SwiGLU)"
+        dom_ms = prof["w13"][0]
+        dom_bytes = dominant_kernel_bytes(cfg)
+    dom_gbps = dom_bytes / (dom_ms / 1e3) / 1e9
+    print("# per-launch avg ms: " + ", ".join(f"{k} {v[0]:.4f} x{v[1]}" for k, v in prof.items() if v[1])
+          + f"; step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -165,23 +185,24 @@ def main() -> int:
             "global_batch": 1,
             "seq_len": cfg.seq_len,
             "parallelism": "single GPU",
-            "graph": not args.no_graph,
+            "mode": "persistent" if persistent else "multi",
+            "graph": (not args.no_graph) and not persistent,
         },
         "achieved_GBps": round(gbps, 1),
         "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
         "bytes_per_token": int(step_bytes / steps),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_w13_swiglu (RMSNorm + W1/W3 GEMV + SwiGLU)",
-            "achieved": round(w13_gbps, 1),
+            "kernel": dom_name,
+            "achieved": round(dom_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(w13_gbps / HBM_PEAK_GBPS, 4),
+            "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
             "traffic": None,
-            "bytes_per_launch": w13_bytes,
-            "avg_launch_ms": round(w13_ms, 5),
+            "bytes_per_launch": int(dom_bytes),
+            "avg_launch_ms": round(dom_ms, 5),
         },
-        "kernels_eager_ms": {k: round(v[0], 5) for k, v in prof.items()},
+        "launch_ms": {k: round(v[0], 5) for k, v in prof.items() if v[1]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

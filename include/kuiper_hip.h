@@ -34,6 +34,7 @@ extern "C" {
 #define KL_EUNSUPP (-4)   /* combination the backend does not implement */
 #define KL_ETOKEN (-5)    /* token id outside [0, vocab) */
 #define KL_EWORKSPACE (-6)/* caller workspace too small */
+#define KL_EDEVICE (-7)   /* the device step reported an error (barrier timeout, bad state) */
 
 /* Model families (the reference picks them with -DLLAMA3_SUPPORT /
  * -DQWEN2_SUPPORT / -DQWEN3_SUPPORT, CMakeLists.txt:29-47; here at run time). */
@@ -200,6 +201,22 @@ int kl_engine_destroy(kl_engine* e);
 int kl_engine_dims(const kl_engine* e, int32_t* out10);
 int kl_engine_weight_bytes(const kl_engine* e, int64_t* bytes);
 int kl_engine_set_graph(kl_engine* e, int enable);
+/* Execution mode of the step.  KL_MODE_MULTI (the default): 5 kernels per
+ * layer plus the classifier, replayed as a HIP graph (kl_engine_set_graph).
+ * KL_MODE_PERSISTENT (where the device can hold one 512-thread workgroup per
+ * CU): one cooperative launch per token runs every layer, with grid barriers
+ * between phases and each phase's weight loads issued before the preceding
+ * barrier.
+ * Both modes compute the same step; setting KL_MODE_PERSISTENT where it does
+ * not fit returns KL_EUNSUPP. */
+#define KL_MODE_PERSISTENT 0
+#define KL_MODE_MULTI 1
+int kl_engine_set_mode(kl_engine* e, int mode);
+int kl_engine_get_mode(const kl_engine* e, int* mode);
+/* Persistent-mode launch shape: workgroups, threads per workgroup, dynamic
+ * LDS bytes. */
+int kl_engine_launch_shape(const kl_engine* e, int32_t* workgroups, int32_t* threads,
+                           int64_t* lds_bytes);
 /* Model::predict (model/model.h:21-22, llama3.cpp:641-649): embed `token`,
  * run every layer at `pos`, final norm, classifier and argmax.  Blocks until
  * done; *next (may be NULL) receives the argmax, logits (host, may be NULL)
@@ -219,9 +236,20 @@ int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, in
 /* Per-kernel timing: runs `steps` decode steps from (token, pos0) without the
  * graph, with a HIP event recorded between consecutive launches on the
  * engine's stream, and returns the average duration and launch count per
- * kernel kind: [embed, qkv, attn, wo, w13, w2, cls]. */
-int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, float* avg_ms7,
-                      int32_t* counts7);
+ * kernel kind: [embed, qkv, attn, wo, w13, w2, cls, step]; in the persistent
+ * mode only `step` (the whole-token kernel) is used. */
+int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, float* avg_ms8,
+                      int32_t* counts8);
+/* Device-time trace of one persistent step (the reference's per-op profile,
+ * model/qwen2.cpp:16-68, measured on the device): runs the step for (token,
+ * pos) and returns ticks of the 100 MHz s_memrealtime clock, slot-major
+ * [n_slots][n_workgroups]: slot 0 = kernel entry, slots 2k+1 / 2k+2 = arrival
+ * at / release from grid barrier k (5 per layer: after QKV, attention, WO,
+ * W1/W3, W2), the last slot = end of the workgroup's last phase.  Unused
+ * slots are 0.  KL_EUNSUPP outside the persistent mode; KL_EWORKSPACE when
+ * max_ticks < n_slots * n_workgroups (the sizes are still returned). */
+int kl_engine_trace_step(kl_engine* e, int32_t token, int32_t pos, uint64_t* ticks,
+                         int64_t max_ticks, int32_t* n_slots, int32_t* n_workgroups);
 /* Device pointers for inspection: logits [vocab], key/value caches
  * [layers][seq_len][kv_dim]. */
 int kl_engine_buffers(const kl_engine* e, const float** logits, const float** key_cache,

@@ -16,11 +16,12 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import KlError, check, lib
+from ._lib import MODE_MULTI, MODE_PERSISTENT, KlError, check, lib
 from .configs import ALL, BASELINE, TINY, Config
 
 __all__ = [
     "ALL", "BASELINE", "TINY", "Config", "DeviceArray", "Engine", "KlError", "Stream",
+    "MODE_MULTI", "MODE_PERSISTENT",
     "synth_image", "synth_normal", "quantize_q8", "device_count",
 ]
 
@@ -162,6 +163,24 @@ class Engine:
     def set_graph(self, enable: bool):
         check(lib.kl_engine_set_graph(self.handle, int(enable)), "kl_engine_set_graph")
 
+    def set_mode(self, mode: int):
+        """_lib.MODE_PERSISTENT (one cooperative launch per token) or
+        _lib.MODE_MULTI (5 kernels per layer, graph-replayed)."""
+        check(lib.kl_engine_set_mode(self.handle, int(mode)), "kl_engine_set_mode")
+
+    @property
+    def mode(self) -> int:
+        m = C.c_int(-1)
+        check(lib.kl_engine_get_mode(self.handle, C.byref(m)), "kl_engine_get_mode")
+        return m.value
+
+    def launch_shape(self):
+        """(workgroups, threads, dynamic LDS bytes) of the persistent step."""
+        w, t, l = C.c_int32(0), C.c_int32(0), C.c_int64(0)
+        check(lib.kl_engine_launch_shape(self.handle, C.byref(w), C.byref(t), C.byref(l)),
+              "kl_engine_launch_shape")
+        return w.value, t.value, l.value
+
     def step(self, token: int, pos: int, want_logits: bool = True):
         nxt = C.c_int32(-1)
         logits = np.empty(self.vocab, np.float32) if want_logits else None
@@ -187,16 +206,29 @@ class Engine:
                                   out.ctypes.data, C.byref(ms)), "kl_engine_bench")
         return out, ms.value
 
-    KERNEL_KINDS = ("embed", "qkv", "attn", "wo", "w13", "w2", "cls")
+    KERNEL_KINDS = ("embed", "qkv", "attn", "wo", "w13", "w2", "cls", "step")
 
     def profile(self, token: int, pos0: int, steps: int) -> dict:
         """Average device time per kernel kind over `steps` eager decode steps
         (HIP events between consecutive launches on the engine's stream)."""
-        avg = (C.c_float * 7)()
-        cnt = (C.c_int32 * 7)()
+        avg = (C.c_float * 8)()
+        cnt = (C.c_int32 * 8)()
         check(lib.kl_engine_profile(self.handle, int(token), int(pos0), int(steps), avg, cnt),
               "kl_engine_profile")
         return {k: (float(avg[i]), int(cnt[i])) for i, k in enumerate(self.KERNEL_KINDS)}
+
+    def trace_step(self, token: int, pos: int) -> np.ndarray:
+        """Device-time trace of one persistent step: int64 ticks of the 100 MHz
+        clock, shape [slots, workgroups] (see kl_engine_trace_step)."""
+        ns, nw = C.c_int32(0), C.c_int32(0)
+        rc = lib.kl_engine_trace_step(self.handle, int(token), int(pos), None, 0, C.byref(ns),
+                                      C.byref(nw))
+        if rc not in (0, _lib.KL_EWORKSPACE):
+            check(rc, "kl_engine_trace_step")
+        out = np.zeros((ns.value, nw.value), np.uint64)
+        check(lib.kl_engine_trace_step(self.handle, int(token), int(pos), out.ctypes.data,
+                                       out.size, C.byref(ns), C.byref(nw)), "kl_engine_trace_step")
+        return out.astype(np.int64)
 
     def kv_row(self, layer: int, pos: int, which_v: bool) -> np.ndarray:
         lg, kc, vc = C.c_void_p(), C.c_void_p(), C.c_void_p()

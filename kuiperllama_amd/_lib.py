@@ -17,6 +17,8 @@ KL_EFORMAT = -3
 KL_EUNSUPP = -4
 KL_ETOKEN = -5
 KL_EWORKSPACE = -6
+KL_EDEVICE = -7
+MODE_PERSISTENT, MODE_MULTI = 0, 1
 
 FAMILY_LLAMA2, FAMILY_LLAMA3, FAMILY_QWEN2, FAMILY_QWEN3 = 0, 1, 2, 3
 ROPE_INTERLEAVED, ROPE_HALF = 0, 1
@@ -101,10 +103,14 @@ _SIGS = {
     "kl_engine_dims": (_i, [_p, _i32p]),
     "kl_engine_weight_bytes": (_i, [_p, _i64p]),
     "kl_engine_set_graph": (_i, [_p, _i]),
+    "kl_engine_set_mode": (_i, [_p, _i]),
+    "kl_engine_get_mode": (_i, [_p, C.POINTER(_i)]),
+    "kl_engine_launch_shape": (_i, [_p, _i32p, _i32p, _i64p]),
     "kl_engine_step": (_i, [_p, C.c_int32, C.c_int32, _i32p, _p]),
     "kl_engine_generate": (_i, [_p, _p, _i, _i, _p, _fp]),
     "kl_engine_bench": (_i, [_p, _p, _i, _i, _i, _p, _fp]),
     "kl_engine_profile": (_i, [_p, C.c_int32, C.c_int32, _i, _fp, _i32p]),
+    "kl_engine_trace_step": (_i, [_p, C.c_int32, C.c_int32, _p, C.c_int64, _i32p, _i32p]),
     "kl_engine_buffers": (_i, [_p, C.POINTER(_p), C.POINTER(_p), C.POINTER(_p)]),
     "kl_engine_stream": (_i, [_p, C.POINTER(_p)]),
 }

@@ -31,17 +31,14 @@
 #include "device.hpp"
 #include "gemv.hpp"
 #include "kuiper_hip.h"
+#include "persist.hpp"
 
 using namespace kl;
 
 namespace {
 
-struct StepState {
-  int32_t pos;         // position processed by the next replay
-  int32_t token;       // token embedded by the next replay
-  int32_t prompt_len;  // positions < prompt_len - 1 take their successor from the prompt
-  int32_t sampled;     // argmax of the last computed logits
-};
+typedef PStepState StepState;
+constexpr int kMaxPwgPerCu = 4;  // persistent workgroups per CU (KL_PWG_PER_CU)
 
 inline int rc(hipError_t e) { return e == hipSuccess ? KL_OK : static_cast<int>(e); }
 
@@ -430,6 +427,20 @@ struct kl_engine {
   hipGraphExec_t graph_exec = nullptr;
   hipGraph_t graph = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // Persistent step (persist.hpp): one cooperative launch per token.
+  int mode = KL_MODE_PERSISTENT;
+  bool persistent_ok = false;  // the persistent kernel fits this device and model
+  int nwg = 0;                 // workgroups (co-resident)
+  size_t p_lds = 0;
+  const void* p_kernel = nullptr;
+  PGemv* d_ph = nullptr;       // [4L + 1] phase descriptors (arena)
+  PAttn* d_at = nullptr;       // [L]
+  float* x_b = nullptr;        // second residual buffer
+  unsigned int* bar = nullptr;
+  unsigned int* bar_base = nullptr;
+  int* derr = nullptr;
+  int* derr_host = nullptr;    // pinned
+  PArgs pargs{};
 };
 
 namespace {
@@ -455,7 +466,7 @@ kl_engine::GemvLaunch plan_gemv(const kl_engine* e, int units, int cols) {
 }
 
 // Kernel kinds, in launch order within a layer; used by the profiler.
-enum KernelKind { kKEmbed = 0, kKQkv, kKAttn, kKWo, kKW13, kKW2, kKCls, kKinds };
+enum KernelKind { kKEmbed = 0, kKQkv, kKAttn, kKWo, kKW13, kKW2, kKCls, kKStep, kKinds, kKEnd };
 
 // With `marks` set (eager profiling only), an event is recorded on the
 // stream before every launch and after the last one; marks[i] then brackets
@@ -556,7 +567,7 @@ int launch_step_t(kl_engine* e, Marks* mk) {
   ca.st = e->st; ca.prompt = e->prompt; ca.out_tokens = e->out_tokens;
   mark(s, mk, kKCls);
   KL_GEMV_LAUNCH(k_cls_argmax, Q8, e->l_cls, s, ca);
-  mark(s, mk, kKinds);
+  mark(s, mk, kKEnd);
   return rc(hipGetLastError());
 }
 
@@ -564,7 +575,18 @@ int launch_step(kl_engine* e, Marks* mk = nullptr) {
   return e->quant ? launch_step_t<true>(e, mk) : launch_step_t<false>(e, mk);
 }
 
+// One persistent launch = one token.
+int launch_persistent(kl_engine* e, Marks* mk = nullptr) {
+  void* params[] = {&e->pargs};
+  mark(e->stream, mk, kKStep);
+  const hipError_t err = hipLaunchCooperativeKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads),
+                                                    params, e->p_lds, e->stream);
+  mark(e->stream, mk, kKEnd);
+  return rc(err);
+}
+
 int run_step(kl_engine* e) {
+  if (e->mode == KL_MODE_PERSISTENT) return launch_persistent(e);
   if (!e->use_graph) return launch_step(e);
   if (!e->graph_exec) {
     hipError_t err = hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal);
@@ -588,6 +610,175 @@ int run_step(kl_engine* e) {
   return rc(hipGraphLaunch(e->graph_exec, e->stream));
 }
 
+// Reads the device error word after the stream has been synchronised; on an
+// error, resets the barrier state so the engine can be used again.
+int check_device_error(kl_engine* e) {
+  if (e->mode != KL_MODE_PERSISTENT) return KL_OK;
+  hipError_t err = hipMemcpy(e->derr_host, e->derr, sizeof(int), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return rc(err);
+  if (*e->derr_host == 0) return KL_OK;
+  fprintf(stderr, "kuiper_hip: persistent step reported device error %d\n", *e->derr_host);
+  err = hipMemset(e->derr, 0, sizeof(int));
+  if (err == hipSuccess) err = hipMemset(e->bar, 0, sizeof(unsigned int));
+  if (err == hipSuccess) err = hipMemset(e->bar_base, 0, sizeof(unsigned int));
+  if (err == hipSuccess) err = hipMemset(e->am_counter, 0, sizeof(unsigned int));
+  if (err == hipSuccess) err = hipMemset(e->attn_counters, 0, e->lay.KVH * sizeof(unsigned int));
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  return err == hipSuccess ? KL_EDEVICE : rc(err);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent-step planning.
+// ---------------------------------------------------------------------------
+// Fills the geometry of one GEMV phase: rows split into one contiguous range
+// per workgroup, then (ks, rw) chosen to minimise the largest per-wave work,
+// counting a row reduction as half a chunk.  Returns the LDS floats the
+// phase's row partials need.
+size_t plan_phase(PGemv& p, int nwg, bool q8, int gs) {
+  const int total = p.paired ? p.rows[0] : p.rows[0] + p.rows[1] + p.rows[2];
+  p.rpw = (total + nwg - 1) / nwg;
+  p.cn16 = q8 ? p.cols / 16 : p.cols / 4;
+  p.cn = (p.cn16 + kWave - 1) / kWave;
+  p.gshift = 0;
+  if (q8)
+    while ((1 << p.gshift) < gs) ++p.gshift;
+  const int nloc = p.paired ? p.rpw * p.nsub : p.rpw;
+  double best = 1e30;
+  for (int ks = 1; ks <= kPWaves; ks *= 2) {
+    const int rw = kPWaves / ks;
+    const int nck = (p.cn + ks - 1) / ks;
+    const double cost = static_cast<double>((nloc + rw - 1) / rw) * (nck + 0.5);
+    if (cost < best - 1e-9) {
+      best = cost;
+      p.ks = ks;
+      p.rw = rw;
+      p.nck = nck;
+    }
+  }
+  return static_cast<size_t>(nloc) * p.ks;
+}
+
+template <bool Q8, int NB>
+const void* persistent_kernel(int hd) {
+  switch (hd) {
+    case 32: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 32>);
+    case 64: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 64>);
+    case 128: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 128>);
+    default: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 256>);
+  }
+}
+
+// Builds the phase descriptors and launch shape; leaves persistent_ok false
+// (and the multi-kernel mode selected) where the device cannot hold the grid.
+int setup_persistent(kl_engine* e) {
+  const ImageLayout& m = e->lay;
+  const bool q8 = e->quant != 0;
+  int nb = q8 ? 8 : 16;
+  if (const char* env = std::getenv("KL_PNB")) nb = std::atoi(env);
+  if (q8)
+    e->p_kernel = nb == 4 ? persistent_kernel<true, 4>(m.hd) : persistent_kernel<true, 8>(m.hd);
+  else
+    e->p_kernel = nb == 4   ? persistent_kernel<false, 4>(m.hd)
+                  : nb == 8 ? persistent_kernel<false, 8>(m.hd)
+                            : persistent_kernel<false, 16>(m.hd);
+  int per_cu = 1;
+  if (const char* env = std::getenv("KL_PWG_PER_CU"))
+    per_cu = std::min(kMaxPwgPerCu, std::max(1, std::atoi(env)));
+  e->nwg = e->cus * per_cu;
+  std::vector<PGemv> ph(4 * m.L + 1);
+  std::vector<PAttn> at(m.L);
+  size_t red_floats = 0;
+  int max_cols = 0;
+  for (int l = 0; l < m.L; ++l) {
+    const LayerDev& L = e->layers[l];
+    const size_t kv_layer = static_cast<size_t>(m.S) * m.Dkv;
+    PGemv& qkv = ph[4 * l + 0];
+    qkv = PGemv{};
+    qkv.w[0] = L.wq.w; qkv.w[1] = L.wk.w; qkv.w[2] = L.wv.w;
+    qkv.sc[0] = L.wq.s; qkv.sc[1] = L.wk.s; qkv.sc[2] = L.wv.s;
+    qkv.rows[0] = m.Dq; qkv.rows[1] = m.Dkv; qkv.rows[2] = m.Dkv;
+    qkv.nsub = 3; qkv.paired = 0; qkv.cols = m.D; qkv.epi = kEpiQkv;
+    qkv.in = l == 0 ? nullptr : e->x;
+    qkv.norm = L.rms_att;
+    qkv.out[0] = e->q; qkv.out[1] = e->kcache + l * kv_layer; qkv.out[2] = e->vcache + l * kv_layer;
+    qkv.bias[0] = L.bq; qkv.bias[1] = L.bk; qkv.bias[2] = L.bv;
+    PGemv& wo = ph[4 * l + 1];
+    wo = PGemv{};
+    wo.w[0] = L.wo.w; wo.sc[0] = L.wo.s; wo.rows[0] = m.D;
+    wo.nsub = 1; wo.cols = m.Dq; wo.epi = kEpiResid;
+    wo.in = e->att; wo.norm = nullptr;
+    wo.out[0] = e->x_b; wo.resid = l == 0 ? nullptr : e->x;
+    PGemv& w13 = ph[4 * l + 2];
+    w13 = PGemv{};
+    w13.w[0] = L.w1.w; w13.w[1] = L.w3.w; w13.sc[0] = L.w1.s; w13.sc[1] = L.w3.s;
+    w13.rows[0] = m.F; w13.rows[1] = m.F;
+    w13.nsub = 2; w13.paired = 1; w13.cols = m.D; w13.epi = kEpiSwiglu;
+    w13.in = e->x_b; w13.norm = L.rms_ffn; w13.out[0] = e->h;
+    PGemv& w2 = ph[4 * l + 3];
+    w2 = PGemv{};
+    w2.w[0] = L.w2.w; w2.sc[0] = L.w2.s; w2.rows[0] = m.D;
+    w2.nsub = 1; w2.cols = m.F; w2.epi = kEpiResid;
+    w2.in = e->h; w2.norm = nullptr; w2.out[0] = e->x; w2.resid = e->x_b;
+    at[l] = PAttn{e->kcache + l * kv_layer, e->vcache + l * kv_layer, L.qn, L.kn};
+  }
+  PGemv& cls = ph[4 * m.L];
+  cls = PGemv{};
+  cls.w[0] = e->wcls.w; cls.sc[0] = e->wcls.s; cls.rows[0] = m.V;
+  cls.nsub = 1; cls.cols = m.D; cls.epi = kEpiCls;
+  cls.in = e->x; cls.norm = e->rms_final; cls.out[0] = e->logits;
+  for (PGemv& p : ph) {
+    red_floats = std::max(red_floats, plan_phase(p, e->nwg, q8, m.gs));
+    max_cols = std::max(max_cols, p.cols);
+  }
+  const int red_off = (max_cols + 3) & ~3;
+  const size_t gemv_lds = (static_cast<size_t>(red_off) + red_floats) * sizeof(float);
+  const size_t attn_lds = attn_p_lds_floats(m.hd, m.H / m.KVH, e->attn.G) * sizeof(float);
+  e->p_lds = std::max(gemv_lds, attn_lds);
+  hipError_t err = hipMemcpy(e->d_ph, ph.data(), ph.size() * sizeof(PGemv), hipMemcpyHostToDevice);
+  if (err == hipSuccess)
+    err = hipMemcpy(e->d_at, at.data(), at.size() * sizeof(PAttn), hipMemcpyHostToDevice);
+  if (err != hipSuccess) return rc(err);
+
+  PArgs& a = e->pargs;
+  a = PArgs{};
+  a.ph = e->d_ph; a.at = e->d_at;
+  a.L = m.L; a.D = m.D; a.Dq = m.Dq; a.Dkv = m.Dkv; a.V = m.V; a.S = m.S;
+  a.kv_mul = m.H / m.KVH; a.KVH = m.KVH;
+  a.eps = e->eps; a.qk_eps = 1e-6f;  // kernels/cuda/rmsnorm_kernel.cu:148
+  a.scale = 1.f / std::sqrt(static_cast<float>(m.hd));
+  a.rope_style = e->rope_style; a.transform = e->transform;
+  a.sin_t = e->sin_t; a.cos_t = e->cos_t; a.emb = e->emb;
+  a.q = e->q; a.att = e->att; a.attn_part = e->attn_part; a.attn_cnt = e->attn_counters;
+  a.attn_G = e->attn.G;
+  a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
+  a.bar = e->bar; a.bar_base = e->bar_base; a.err = e->derr;
+  a.red_off = red_off;
+  a.st = e->st; a.prompt = e->prompt; a.out_tokens = e->out_tokens;
+
+  // The grid must be co-resident: one workgroup of 512 threads per CU (or
+  // KL_PWG_PER_CU) with this LDS.
+  if (e->p_lds > 64 * 1024) {
+    err = hipFuncSetAttribute(e->p_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(e->p_lds));
+    if (err != hipSuccess) {
+      (void)hipGetLastError();
+      return KL_OK;
+    }
+  }
+  int blocks = 0;
+  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, e->p_kernel, kPThreads, e->p_lds);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    return KL_OK;
+  }
+  e->persistent_ok = blocks >= per_cu;
+  e->mode = KL_MODE_MULTI;
+  if (const char* env = std::getenv("KL_ENGINE_MODE")) {
+    if (std::atoi(env) == KL_MODE_PERSISTENT && e->persistent_ok) e->mode = KL_MODE_PERSISTENT;
+  }
+  return KL_OK;
+}
+
 void release(kl_engine* e) {
   if (!e) return;
   if (e->graph_exec) (void)hipGraphExecDestroy(e->graph_exec);
@@ -596,6 +787,7 @@ void release(kl_engine* e) {
   if (e->ev1) (void)hipEventDestroy(e->ev1);
   if (e->arena) (void)hipFree(e->arena);
   if (e->st_host) (void)hipHostFree(e->st_host);
+  if (e->derr_host) (void)hipHostFree(e->derr_host);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -713,8 +905,13 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   const size_t actr_at = plan(lay.KVH * sizeof(unsigned int));
   const size_t amc_at = plan(64);
   const size_t st_at = plan(sizeof(StepState));
+  const size_t bar_at = plan(sizeof(unsigned int)), barb_at = plan(sizeof(unsigned int));
+  const size_t derr_at = plan(sizeof(int));
   const size_t zero_end = cursor;
-  const int gmax = e->grid_cap;
+  const int gmax = std::max(e->grid_cap, e->cus * kMaxPwgPerCu);
+  const size_t xb_at = plan(lay.D * 4);
+  const size_t ph_at = plan((4 * static_cast<size_t>(lay.L) + 1) * sizeof(PGemv));
+  const size_t at_at = plan(static_cast<size_t>(lay.L) * sizeof(PAttn));
   const size_t pv_at = plan(gmax * 4), pi_at = plan(gmax * 4);
   const size_t pr_at = plan(S * 4), ot_at = plan(S * 4);
   e->arena_bytes = cursor;
@@ -771,17 +968,25 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   e->am_pi = reinterpret_cast<int*>(P(pi_at));
   e->prompt = reinterpret_cast<int32_t*>(P(pr_at));
   e->out_tokens = reinterpret_cast<int32_t*>(P(ot_at));
+  e->x_b = PF(xb_at);
+  e->bar = reinterpret_cast<unsigned int*>(P(bar_at));
+  e->bar_base = reinterpret_cast<unsigned int*>(P(barb_at));
+  e->derr = reinterpret_cast<int*>(P(derr_at));
+  e->d_ph = reinterpret_cast<PGemv*>(P(ph_at));
+  e->d_at = reinterpret_cast<PAttn*>(P(at_at));
   e->lay.layers.clear();  // host pointers are no longer needed
   err = hipMemset(e->arena + zero_begin, 0, zero_end - zero_begin);
   if (err == hipSuccess) err = hipMemset(e->kcache, 0, 2 * static_cast<size_t>(lay.L) * S * Dkv * 4);
   if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void**>(&e->st_host), sizeof(StepState), hipHostMallocDefault);
+  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void**>(&e->derr_host), sizeof(int), hipHostMallocDefault);
   if (err == hipSuccess) err = hipEventCreate(&e->ev0);
   if (err == hipSuccess) err = hipEventCreate(&e->ev1);
   if (err != hipSuccess) {
     release(e);
     return rc(err);
   }
-  const int trc = kl_sincos_table(lay.hd, lay.S, e->theta, e->sin_t, e->cos_t);
+  int trc = kl_sincos_table(lay.hd, lay.S, e->theta, e->sin_t, e->cos_t);
+  if (trc == KL_OK) trc = setup_persistent(e);
   if (trc != KL_OK) {
     release(e);
     return trc;
@@ -811,6 +1016,34 @@ int kl_engine_weight_bytes(const kl_engine* e, int64_t* bytes) {
   return KL_OK;
 }
 
+int kl_engine_set_mode(kl_engine* e, int mode) {
+  if (!e) return KL_EINVAL;
+  if (mode == KL_MODE_PERSISTENT) {
+    if (!e->persistent_ok) return KL_EUNSUPP;
+  } else if (mode != KL_MODE_MULTI) {
+    return KL_EINVAL;
+  }
+  const hipError_t err = hipStreamSynchronize(e->stream);
+  if (err != hipSuccess) return rc(err);
+  e->mode = mode;
+  return KL_OK;
+}
+
+int kl_engine_get_mode(const kl_engine* e, int* mode) {
+  if (!e || !mode) return KL_EINVAL;
+  *mode = e->mode;
+  return KL_OK;
+}
+
+int kl_engine_launch_shape(const kl_engine* e, int32_t* workgroups, int32_t* threads,
+                           int64_t* lds_bytes) {
+  if (!e) return KL_EINVAL;
+  if (workgroups) *workgroups = e->nwg;
+  if (threads) *threads = kPThreads;
+  if (lds_bytes) *lds_bytes = static_cast<int64_t>(e->p_lds);
+  return KL_OK;
+}
+
 int kl_engine_set_graph(kl_engine* e, int enable) {
   if (!e) return KL_EINVAL;
   e->use_graph = enable != 0;
@@ -835,6 +1068,8 @@ int kl_engine_step(kl_engine* e, int32_t token, int32_t pos, int32_t* next, floa
   err = hipMemcpyAsync(e->st_host, e->st, sizeof(StepState), hipMemcpyDeviceToHost, e->stream);
   if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
   if (err != hipSuccess) return rc(err);
+  const int de = check_device_error(e);
+  if (de != KL_OK) return de;
   if (next) *next = e->st_host->sampled;
   return KL_OK;
 }
@@ -868,6 +1103,8 @@ int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, in
                          hipMemcpyDeviceToHost, e->stream);
   if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
   if (err != hipSuccess) return rc(err);
+  const int de = check_device_error(e);
+  if (de != KL_OK) return de;
   if (decode_ms) {
     err = hipEventElapsedTime(decode_ms, e->ev0, e->ev1);
     if (err != hipSuccess) return rc(err);
@@ -905,7 +1142,39 @@ int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, in
   if (err == hipSuccess)
     err = hipMemcpy(out_tokens, e->out_tokens + (P - 1), sizeof(int32_t) * (n_warmup + n_timed),
                     hipMemcpyDeviceToHost);
-  return rc(err);
+  if (err != hipSuccess) return rc(err);
+  return check_device_error(e);
+}
+
+int kl_engine_trace_step(kl_engine* e, int32_t token, int32_t pos, uint64_t* ticks,
+                         int64_t max_ticks, int32_t* n_slots, int32_t* n_workgroups) {
+  if (!e || !n_slots || !n_workgroups) return KL_EINVAL;
+  if (e->mode != KL_MODE_PERSISTENT) return KL_EUNSUPP;
+  if (pos < 0 || pos >= e->lay.S) return KL_EINVAL;
+  if (token < 0 || token >= e->lay.V) return KL_ETOKEN;
+  const int slots = 2 * 5 * e->lay.L + 2;
+  const size_t n = static_cast<size_t>(slots) * e->nwg;
+  *n_slots = slots;
+  *n_workgroups = e->nwg;
+  if (!ticks || static_cast<int64_t>(n) > max_ticks) return KL_EWORKSPACE;
+  unsigned long long* d = nullptr;
+  hipError_t err = hipMalloc(&d, n * sizeof(unsigned long long));
+  if (err != hipSuccess) return rc(err);
+  err = hipMemset(d, 0, n * sizeof(unsigned long long));
+  *e->st_host = StepState{pos, token, 0, 0};
+  if (err == hipSuccess)
+    err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  int r = rc(err);
+  if (r == KL_OK) {
+    e->pargs.trace = d;
+    r = launch_persistent(e);
+    e->pargs.trace = nullptr;
+  }
+  if (r == KL_OK) r = rc(hipStreamSynchronize(e->stream));
+  if (r == KL_OK) r = check_device_error(e);
+  if (r == KL_OK) r = rc(hipMemcpy(ticks, d, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  (void)hipFree(d);
+  return r;
 }
 
 int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, float* avg_ms,
@@ -925,11 +1194,14 @@ int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, floa
   std::vector<int> kinds;
   Marks mk{&ev, &kinds};
   int r = KL_OK;
-  for (int i = 0; i < steps && r == KL_OK; ++i) r = launch_step(e, &mk);
+  const bool pers = e->mode == KL_MODE_PERSISTENT;
+  for (int i = 0; i < steps && r == KL_OK; ++i)
+    r = pers ? launch_persistent(e, &mk) : launch_step(e, &mk);
   err = hipStreamSynchronize(e->stream);
   if (r == KL_OK && err != hipSuccess) r = rc(err);
+  if (r == KL_OK) r = check_device_error(e);
   for (size_t i = 0; r == KL_OK && i + 1 < ev.size(); ++i) {
-    if (kinds[i] == kKinds) continue;  // end-of-step mark
+    if (kinds[i] == kKEnd) continue;  // end-of-step mark
     float ms = 0.f;
     err = hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
     if (err != hipSuccess) {

@@ -280,6 +280,7 @@ const char* kl_error_string(int code) {
     case KL_EUNSUPP: return "unsupported configuration";
     case KL_ETOKEN: return "token id out of range";
     case KL_EWORKSPACE: return "workspace too small";
+    case KL_EDEVICE: return "device step error";
     default:
       if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
       return "unknown error";

@@ -26,9 +26,14 @@ def say(*a):
     sys.stdout.flush()
 
 
-def teacher_forced(K, O, cfg, img, prompt, n_new, graph=True):
+MODES = {"persistent": 0, "multi": 1}
+
+
+def teacher_forced(K, O, cfg, img, prompt, n_new, graph=True, mode=None):
     eng = K.Engine(img, cfg)
     eng.set_graph(graph)
+    if mode is not None:
+        eng.set_mode(mode)
     om = O.Model(img, cfg.family, cfg.quant)
     seq = [int(t) for t in prompt]
     worst, mismatches = 0.0, []
@@ -49,14 +54,17 @@ def teacher_forced(K, O, cfg, img, prompt, n_new, graph=True):
     return eng, om, worst, mismatches
 
 
+@pytest.mark.parametrize("mode", list(MODES))
 @pytest.mark.parametrize("name", ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2",
                                   "tiny_qwen3"])
-def test_tiny_models_step_parity(K, O, gpu, name):
+def test_tiny_models_step_parity(K, O, gpu, name, mode):
     cfg = K.TINY[name]
-    say("case", name)
+    say("case", name, mode)
     img = K.synth_image(cfg)
     prompt = K.prompt_tokens(cfg)
-    eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, cfg.decode_steps)
+    eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, cfg.decode_steps,
+                                        mode=MODES[mode])
+    assert eng.mode == MODES[mode]
     say(name, "worst logits rel err", worst, "argmax near-ties", mm)
     assert not mm
     # KV cache contents (K rotated) after the run
@@ -66,15 +74,17 @@ def test_tiny_models_step_parity(K, O, gpu, name):
             assert rel(a, b) < 1e-4
 
 
+@pytest.mark.parametrize("mode", list(MODES))
 @pytest.mark.parametrize("name", ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2",
                                   "tiny_qwen3"])
-def test_tiny_models_generate_matches_oracle(K, O, gpu, name):
+def test_tiny_models_generate_matches_oracle(K, O, gpu, name, mode):
     cfg = K.TINY[name]
-    say("case", name)
+    say("case", name, mode)
     img = K.synth_image(cfg)
     prompt = K.prompt_tokens(cfg)
     want = O.Model(img, cfg.family, cfg.quant).generate(prompt, cfg.decode_steps)
     eng = K.Engine(img, cfg)
+    eng.set_mode(MODES[mode])
     got, ms = eng.generate(prompt, cfg.decode_steps)
     assert list(got) == list(want)
     # a second run on the same engine (state fully device-driven) repeats it
@@ -87,11 +97,37 @@ def test_graph_and_eager_agree_bitwise(K, O, gpu):
     img = K.synth_image(cfg)
     prompt = K.prompt_tokens(cfg)
     a, b = K.Engine(img, cfg), K.Engine(img, cfg)
+    a.set_mode(K.MODE_MULTI)
+    b.set_mode(K.MODE_MULTI)
     b.set_graph(False)
     for pos, t in enumerate(list(prompt) + [5, 6, 7]):
         na, la = a.step(int(t), pos)
         nb, lb = b.step(int(t), pos)
         assert na == nb and np.array_equal(la, lb)
+
+
+def test_persistent_is_deterministic_and_close_to_multi(K, O, gpu):
+    """The persistent step sums each row in a fixed order: two engines (and two
+    runs) agree bit for bit; the multi-kernel step differs only in rounding."""
+    cfg = K.TINY["tiny_llama3"]
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    a, b, m = K.Engine(img, cfg), K.Engine(img, cfg), K.Engine(img, cfg)
+    a.set_mode(K.MODE_PERSISTENT)
+    b.set_mode(K.MODE_PERSISTENT)
+    wgs, threads, lds = a.launch_shape()
+    say("persistent launch", wgs, threads, lds)
+    assert wgs >= 1 and threads == 512 and lds > 0
+    m.set_mode(K.MODE_MULTI)
+    for pos, t in enumerate(list(prompt) + [11, 12, 13]):
+        na, la = a.step(int(t), pos)
+        nb, lb = b.step(int(t), pos)
+        nm, lm = m.step(int(t), pos)
+        assert na == nb and np.array_equal(la, lb)
+        assert rel(la, lm) < LOGIT_RTOL
+    ga, _ = a.generate(prompt, 16)
+    gb, _ = a.generate(prompt, 16)
+    assert list(ga) == list(gb)
 
 
 def test_engine_rejects_bad_tokens(K, gpu):
