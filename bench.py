@@ -87,7 +87,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--mode", choices=("persistent", "multi"), default="multi")
+    ap.add_argument("--mode", choices=("persistent", "multi"), default="persistent")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy, the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")

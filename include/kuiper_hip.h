@@ -201,12 +201,12 @@ int kl_engine_destroy(kl_engine* e);
 int kl_engine_dims(const kl_engine* e, int32_t* out10);
 int kl_engine_weight_bytes(const kl_engine* e, int64_t* bytes);
 int kl_engine_set_graph(kl_engine* e, int enable);
-/* Execution mode of the step.  KL_MODE_MULTI (the default): 5 kernels per
- * layer plus the classifier, replayed as a HIP graph (kl_engine_set_graph).
- * KL_MODE_PERSISTENT (where the device can hold one 512-thread workgroup per
- * CU): one cooperative launch per token runs every layer, with grid barriers
- * between phases and each phase's weight loads issued before the preceding
- * barrier.
+/* Execution mode of the step.  KL_MODE_PERSISTENT (the default where the
+ * device can hold one 512-thread workgroup per CU): one cooperative launch per
+ * token runs every layer; workgroups hand activations to each other through
+ * tagged stores (no grid barriers) and issue each phase's first weight loads
+ * before they wait for its input.  KL_MODE_MULTI: 5 kernels per layer plus the
+ * classifier, replayed as a HIP graph (kl_engine_set_graph).
  * Both modes compute the same step; setting KL_MODE_PERSISTENT where it does
  * not fit returns KL_EUNSUPP. */
 #define KL_MODE_PERSISTENT 0
@@ -243,10 +243,9 @@ int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, floa
 /* Device-time trace of one persistent step (the reference's per-op profile,
  * model/qwen2.cpp:16-68, measured on the device): runs the step for (token,
  * pos) and returns ticks of the 100 MHz s_memrealtime clock, slot-major
- * [n_slots][n_workgroups]: slot 0 = kernel entry, slots 2k+1 / 2k+2 = arrival
- * at / release from grid barrier k (5 per layer: after QKV, attention, WO,
- * W1/W3, W2), the last slot = end of the workgroup's last phase.  Unused
- * slots are 0.  KL_EUNSUPP outside the persistent mode; KL_EWORKSPACE when
+ * [n_slots][n_workgroups]: slot 0 = kernel entry; phase p (5 per layer: QKV,
+ * attention, WO, W1/W3, W2; then the classifier) has slot 2p+1 = its input
+ * staged and slot 2p+2 = its outputs stored.  Unused slots are 0.  KL_EUNSUPP outside the persistent mode; KL_EWORKSPACE when
  * max_ticks < n_slots * n_workgroups (the sizes are still returned). */
 int kl_engine_trace_step(kl_engine* e, int32_t token, int32_t pos, uint64_t* ticks,
                          int64_t max_ticks, int32_t* n_slots, int32_t* n_workgroups);

@@ -435,9 +435,9 @@ struct kl_engine {
   const void* p_kernel = nullptr;
   PGemv* d_ph = nullptr;       // [4L + 1] phase descriptors (arena)
   PAttn* d_at = nullptr;       // [L]
-  float* x_b = nullptr;        // second residual buffer
-  unsigned int* bar = nullptr;
-  unsigned int* bar_base = nullptr;
+  tagged_t *t_q = nullptr, *t_k = nullptr, *t_v = nullptr, *t_att = nullptr;  // tagged
+  tagged_t *t_xb = nullptr, *t_h = nullptr, *t_x = nullptr;                    //   hand-off
+  unsigned int* epoch = nullptr;
   int* derr = nullptr;
   int* derr_host = nullptr;    // pinned
   PArgs pargs{};
@@ -619,8 +619,6 @@ int check_device_error(kl_engine* e) {
   if (*e->derr_host == 0) return KL_OK;
   fprintf(stderr, "kuiper_hip: persistent step reported device error %d\n", *e->derr_host);
   err = hipMemset(e->derr, 0, sizeof(int));
-  if (err == hipSuccess) err = hipMemset(e->bar, 0, sizeof(unsigned int));
-  if (err == hipSuccess) err = hipMemset(e->bar_base, 0, sizeof(unsigned int));
   if (err == hipSuccess) err = hipMemset(e->am_counter, 0, sizeof(unsigned int));
   if (err == hipSuccess) err = hipMemset(e->attn_counters, 0, e->lay.KVH * sizeof(unsigned int));
   if (err == hipSuccess) err = hipDeviceSynchronize();
@@ -630,29 +628,36 @@ int check_device_error(kl_engine* e) {
 // ---------------------------------------------------------------------------
 // Persistent-step planning.
 // ---------------------------------------------------------------------------
-// Fills the geometry of one GEMV phase: rows split into one contiguous range
-// per workgroup, then (ks, rw) chosen to minimise the largest per-wave work,
-// counting a row reduction as half a chunk.  Returns the LDS floats the
-// phase's row partials need.
-size_t plan_phase(PGemv& p, int nwg, bool q8, int gs) {
+// Fills the geometry of one GEMV phase for segments of nb chunks: rows split
+// into balanced contiguous ranges, one per workgroup, then (ks, rw) chosen to
+// minimise the largest per-wave work, counting a row reduction as half a
+// chunk.  Returns the LDS floats the phase's row partials need.
+size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb) {
   const int total = p.paired ? p.rows[0] : p.rows[0] + p.rows[1] + p.rows[2];
-  p.rpw = (total + nwg - 1) / nwg;
+  const int rpw = (total + nwg - 1) / nwg;  // largest per-workgroup share
   p.cn16 = q8 ? p.cols / 16 : p.cols / 4;
   p.cn = (p.cn16 + kWave - 1) / kWave;
+  p.nseg = (p.cn + nb - 1) / nb;
   p.gshift = 0;
   if (q8)
     while ((1 << p.gshift) < gs) ++p.gshift;
-  const int nloc = p.paired ? p.rpw * p.nsub : p.rpw;
+  const int nloc = p.paired ? rpw * p.nsub : rpw;
   double best = 1e30;
-  for (int ks = 1; ks <= kPWaves; ks *= 2) {
+  int ks_lo = 1, ks_hi = kPWaves;
+  if (const char* env = std::getenv("KL_PKS")) {  // tuning: force the split-K factor
+    const int v = std::atoi(env);
+    if (v == 1 || v == 2 || v == 4 || v == 8) ks_lo = ks_hi = v;
+  }
+  for (int ks = ks_lo; ks <= ks_hi; ks *= 2) {
     const int rw = kPWaves / ks;
-    const int nck = (p.cn + ks - 1) / ks;
-    const double cost = static_cast<double>((nloc + rw - 1) / rw) * (nck + 0.5);
+    const int nsegw = (p.nseg + ks - 1) / ks;
+    double cost = static_cast<double>((nloc + rw - 1) / rw) * (nsegw * nb + 0.5);
+    if (!q8 && nsegw == 1) cost *= 0.97;  // the input slice stays in registers
     if (cost < best - 1e-9) {
       best = cost;
       p.ks = ks;
       p.rw = rw;
-      p.nck = nck;
+      p.nsegw = nsegw;
     }
   }
   return static_cast<size_t>(nloc) * p.ks;
@@ -673,18 +678,21 @@ const void* persistent_kernel(int hd) {
 int setup_persistent(kl_engine* e) {
   const ImageLayout& m = e->lay;
   const bool q8 = e->quant != 0;
-  int nb = q8 ? 8 : 16;
+  int nb = q8 ? 4 : 8;
   if (const char* env = std::getenv("KL_PNB")) nb = std::atoi(env);
   if (q8)
     e->p_kernel = nb == 4 ? persistent_kernel<true, 4>(m.hd) : persistent_kernel<true, 8>(m.hd);
   else
-    e->p_kernel = nb == 4   ? persistent_kernel<false, 4>(m.hd)
-                  : nb == 8 ? persistent_kernel<false, 8>(m.hd)
-                            : persistent_kernel<false, 16>(m.hd);
+    e->p_kernel = nb == 4 ? persistent_kernel<false, 4>(m.hd) : persistent_kernel<false, 8>(m.hd);
+  if (nb != 4 && nb != 8) nb = 8;
   int per_cu = 1;
   if (const char* env = std::getenv("KL_PWG_PER_CU"))
     per_cu = std::min(kMaxPwgPerCu, std::max(1, std::atoi(env)));
-  e->nwg = e->cus * per_cu;
+  // Every workgroup must own at least one row of every GEMV phase (the
+  // dataflow hand-off relies on it), so the grid is capped at the smallest
+  // phase's row count.
+  const int min_rows = std::min(std::min(m.D, m.F), std::min(m.Dq + 2 * m.Dkv, m.V));
+  e->nwg = std::min(e->cus * per_cu, min_rows);
   std::vector<PGemv> ph(4 * m.L + 1);
   std::vector<PAttn> at(m.L);
   size_t red_floats = 0;
@@ -698,42 +706,53 @@ int setup_persistent(kl_engine* e) {
     qkv.sc[0] = L.wq.s; qkv.sc[1] = L.wk.s; qkv.sc[2] = L.wv.s;
     qkv.rows[0] = m.Dq; qkv.rows[1] = m.Dkv; qkv.rows[2] = m.Dkv;
     qkv.nsub = 3; qkv.paired = 0; qkv.cols = m.D; qkv.epi = kEpiQkv;
-    qkv.in = l == 0 ? nullptr : e->x;
+    qkv.layer = l; qkv.in_layer = l - 1;
+    qkv.in = l == 0 ? nullptr : e->t_x;
     qkv.norm = L.rms_att;
-    qkv.out[0] = e->q; qkv.out[1] = e->kcache + l * kv_layer; qkv.out[2] = e->vcache + l * kv_layer;
+    qkv.out[0] = e->t_q; qkv.out[1] = e->t_k; qkv.out[2] = e->t_v;
+    qkv.vcache = e->vcache + l * kv_layer;
     qkv.bias[0] = L.bq; qkv.bias[1] = L.bk; qkv.bias[2] = L.bv;
     PGemv& wo = ph[4 * l + 1];
     wo = PGemv{};
     wo.w[0] = L.wo.w; wo.sc[0] = L.wo.s; wo.rows[0] = m.D;
     wo.nsub = 1; wo.cols = m.Dq; wo.epi = kEpiResid;
-    wo.in = e->att; wo.norm = nullptr;
-    wo.out[0] = e->x_b; wo.resid = l == 0 ? nullptr : e->x;
+    wo.layer = l; wo.in_layer = l;
+    wo.in = e->t_att; wo.norm = nullptr; wo.out[0] = e->t_xb;
     PGemv& w13 = ph[4 * l + 2];
     w13 = PGemv{};
     w13.w[0] = L.w1.w; w13.w[1] = L.w3.w; w13.sc[0] = L.w1.s; w13.sc[1] = L.w3.s;
     w13.rows[0] = m.F; w13.rows[1] = m.F;
     w13.nsub = 2; w13.paired = 1; w13.cols = m.D; w13.epi = kEpiSwiglu;
-    w13.in = e->x_b; w13.norm = L.rms_ffn; w13.out[0] = e->h;
+    w13.layer = l; w13.in_layer = l;
+    w13.in = e->t_xb; w13.norm = L.rms_ffn; w13.out[0] = e->t_h;
     PGemv& w2 = ph[4 * l + 3];
     w2 = PGemv{};
     w2.w[0] = L.w2.w; w2.sc[0] = L.w2.s; w2.rows[0] = m.D;
     w2.nsub = 1; w2.cols = m.F; w2.epi = kEpiResid;
-    w2.in = e->h; w2.norm = nullptr; w2.out[0] = e->x; w2.resid = e->x_b;
+    w2.layer = l; w2.in_layer = l;
+    w2.in = e->t_h; w2.norm = nullptr; w2.out[0] = e->t_x;
     at[l] = PAttn{e->kcache + l * kv_layer, e->vcache + l * kv_layer, L.qn, L.kn};
   }
   PGemv& cls = ph[4 * m.L];
   cls = PGemv{};
   cls.w[0] = e->wcls.w; cls.sc[0] = e->wcls.s; cls.rows[0] = m.V;
   cls.nsub = 1; cls.cols = m.D; cls.epi = kEpiCls;
-  cls.in = e->x; cls.norm = e->rms_final; cls.out[0] = e->logits;
+  cls.layer = m.L - 1; cls.in_layer = m.L - 1;
+  cls.in = e->t_x; cls.norm = e->rms_final; cls.logits = e->logits;
   for (PGemv& p : ph) {
-    red_floats = std::max(red_floats, plan_phase(p, e->nwg, q8, m.gs));
+    red_floats = std::max(red_floats, plan_phase(p, e->nwg, q8, m.gs, nb));
     max_cols = std::max(max_cols, p.cols);
   }
   const int red_off = (max_cols + 3) & ~3;
-  const size_t gemv_lds = (static_cast<size_t>(red_off) + red_floats) * sizeof(float);
+  const int xres_off = red_off + static_cast<int>((red_floats + 3) & ~size_t(3));
+  const int xres_floats = (m.D + e->nwg - 1) / e->nwg;
+  const size_t gemv_lds = (static_cast<size_t>(xres_off) + xres_floats) * sizeof(float);
   const size_t attn_lds = attn_p_lds_floats(m.hd, m.H / m.KVH, e->attn.G) * sizeof(float);
-  e->p_lds = std::max(gemv_lds, attn_lds);
+  // The residual rows must survive the attention phase, which uses LDS from 0.
+  const size_t xres_at = std::max(static_cast<size_t>(xres_off) * sizeof(float),
+                                  (attn_lds + 15) & ~size_t(15));
+  e->p_lds = xres_at + xres_floats * sizeof(float);
+  (void)gemv_lds;
   hipError_t err = hipMemcpy(e->d_ph, ph.data(), ph.size() * sizeof(PGemv), hipMemcpyHostToDevice);
   if (err == hipSuccess)
     err = hipMemcpy(e->d_at, at.data(), at.size() * sizeof(PAttn), hipMemcpyHostToDevice);
@@ -748,11 +767,13 @@ int setup_persistent(kl_engine* e) {
   a.scale = 1.f / std::sqrt(static_cast<float>(m.hd));
   a.rope_style = e->rope_style; a.transform = e->transform;
   a.sin_t = e->sin_t; a.cos_t = e->cos_t; a.emb = e->emb;
-  a.q = e->q; a.att = e->att; a.attn_part = e->attn_part; a.attn_cnt = e->attn_counters;
+  a.q = e->t_q; a.knew = e->t_k; a.vnew = e->t_v; a.att = e->t_att;
+  a.attn_part = e->attn_part; a.attn_cnt = e->attn_counters;
   a.attn_G = e->attn.G;
   a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
-  a.bar = e->bar; a.bar_base = e->bar_base; a.err = e->derr;
+  a.epoch = e->epoch; a.err = e->derr;
   a.red_off = red_off;
+  a.xres_off = static_cast<int>(xres_at / sizeof(float));
   a.st = e->st; a.prompt = e->prompt; a.out_tokens = e->out_tokens;
 
   // The grid must be co-resident: one workgroup of 512 threads per CU (or
@@ -772,9 +793,9 @@ int setup_persistent(kl_engine* e) {
     return KL_OK;
   }
   e->persistent_ok = blocks >= per_cu;
-  e->mode = KL_MODE_MULTI;
+  e->mode = e->persistent_ok ? KL_MODE_PERSISTENT : KL_MODE_MULTI;
   if (const char* env = std::getenv("KL_ENGINE_MODE")) {
-    if (std::atoi(env) == KL_MODE_PERSISTENT && e->persistent_ok) e->mode = KL_MODE_PERSISTENT;
+    if (std::atoi(env) == KL_MODE_MULTI) e->mode = KL_MODE_MULTI;
   }
   return KL_OK;
 }
@@ -905,11 +926,18 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   const size_t actr_at = plan(lay.KVH * sizeof(unsigned int));
   const size_t amc_at = plan(64);
   const size_t st_at = plan(sizeof(StepState));
-  const size_t bar_at = plan(sizeof(unsigned int)), barb_at = plan(sizeof(unsigned int));
+  const size_t epoch_at = plan(sizeof(unsigned int));
   const size_t derr_at = plan(sizeof(int));
+  // Tagged hand-off vectors: zeroed, so no stale element carries a live tag.
+  const size_t tq_at = plan(static_cast<size_t>(lay.Dq) * 8);
+  const size_t tk_at = plan(static_cast<size_t>(lay.Dkv) * 8);
+  const size_t tv_at = plan(static_cast<size_t>(lay.Dkv) * 8);
+  const size_t tatt_at = plan(static_cast<size_t>(lay.Dq) * 8);
+  const size_t txb_at = plan(static_cast<size_t>(lay.D) * 8);
+  const size_t th_at = plan(static_cast<size_t>(lay.F) * 8);
+  const size_t tx_at = plan(static_cast<size_t>(lay.D) * 8);
   const size_t zero_end = cursor;
   const int gmax = std::max(e->grid_cap, e->cus * kMaxPwgPerCu);
-  const size_t xb_at = plan(lay.D * 4);
   const size_t ph_at = plan((4 * static_cast<size_t>(lay.L) + 1) * sizeof(PGemv));
   const size_t at_at = plan(static_cast<size_t>(lay.L) * sizeof(PAttn));
   const size_t pv_at = plan(gmax * 4), pi_at = plan(gmax * 4);
@@ -968,10 +996,11 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   e->am_pi = reinterpret_cast<int*>(P(pi_at));
   e->prompt = reinterpret_cast<int32_t*>(P(pr_at));
   e->out_tokens = reinterpret_cast<int32_t*>(P(ot_at));
-  e->x_b = PF(xb_at);
-  e->bar = reinterpret_cast<unsigned int*>(P(bar_at));
-  e->bar_base = reinterpret_cast<unsigned int*>(P(barb_at));
+  e->epoch = reinterpret_cast<unsigned int*>(P(epoch_at));
   e->derr = reinterpret_cast<int*>(P(derr_at));
+  auto PT = [&](size_t at) { return reinterpret_cast<tagged_t*>(P(at)); };
+  e->t_q = PT(tq_at); e->t_k = PT(tk_at); e->t_v = PT(tv_at); e->t_att = PT(tatt_at);
+  e->t_xb = PT(txb_at); e->t_h = PT(th_at); e->t_x = PT(tx_at);
   e->d_ph = reinterpret_cast<PGemv*>(P(ph_at));
   e->d_at = reinterpret_cast<PAttn*>(P(at_at));
   e->lay.layers.clear();  // host pointers are no longer needed
@@ -1152,7 +1181,7 @@ int kl_engine_trace_step(kl_engine* e, int32_t token, int32_t pos, uint64_t* tic
   if (e->mode != KL_MODE_PERSISTENT) return KL_EUNSUPP;
   if (pos < 0 || pos >= e->lay.S) return KL_EINVAL;
   if (token < 0 || token >= e->lay.V) return KL_ETOKEN;
-  const int slots = 2 * 5 * e->lay.L + 2;
+  const int slots = 2 * 5 * e->lay.L + 3;
   const size_t n = static_cast<size_t>(slots) * e->nwg;
   *n_slots = slots;
   *n_workgroups = e->nwg;

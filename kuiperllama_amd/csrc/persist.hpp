@@ -2,42 +2,49 @@
 // reference forward (model/llama3.cpp:146-166, :599-744; qwen2.cpp:205-225;
 // qwen3.cpp:147-167) on every CU at once.
 //
-// Phases of one token, separated by grid barriers:
+// Phases of one token:
 //   per layer:  QKV GEMV -> attention -> WO GEMV -> W1/W3 GEMV -> W2 GEMV
 //   then:       classifier GEMV + argmax (sampled positions only)
 //
 // Why persistent: a decode step of Llama-3.2-1B streams 4.9 GB of weights in
 // 81 GEMV-shaped pieces, most of them 17-67 MB.  As separate kernels each pays
 // a launch, a ramp-up and a drain, and the small ones never reach full HBM
-// bandwidth.  Here every wave keeps streaming weights across phase
-// boundaries: weights do not depend on activations, so each wave issues the
-// loads of its first batch of the NEXT GEMV phase before it waits at the
-// barrier (and across the attention phase), and HBM stays busy while the
-// barrier, the activation hand-off and the attention run.
+// bandwidth.  Here every wave keeps streaming: weights do not depend on
+// activations, so each wave issues the loads of its first batch of the NEXT
+// GEMV phase before it waits for that phase's input (and across the attention
+// phase).
 //
-// GEMV phases.  The split dimension (output rows) is cut into one contiguous
-// range per workgroup.  Inside the workgroup, KS waves share a row (split-K)
-// and RW = 8 / KS row groups take rows round robin; the host planner picks KS
-// per phase.  A wave's work is a list of items = (local row, 1 KiB column
-// chunk): 64 lanes x 16 bytes (4 fp32 or 16 int8 weights per lane).  Items
-// are streamed through two register buffers of NB items each (double
-// buffering); a wave's partial sum for a row is reduced across the wave and
-// stored to LDS slot [row][k-slice], so the sum order is fixed (results are
-// bitwise reproducible).  The epilogue combines the KS slices per row.
+// Dataflow hand-off, no grid barriers.  Every activation that crosses
+// workgroups (q, the new K and V rows, the attention output, the residual
+// stream after WO and after W2, the FFN hidden vector) is stored as 64-bit
+// {value, tag} pairs with one agent-coherent (sc1) store; a consumer stages
+// its input by loading the pairs coherently and re-polling the elements whose
+// tag is not yet the current one.  The tag is unique per (launch, layer):
+// epoch * 128 + layer + 1, with `epoch` carried from launch to launch in
+// device memory.  One round trip (the producer's store, the consumer's load)
+// replaces barrier + staging load.  Safety of reuse: every workgroup owns at
+// least one row of every GEMV phase (the host caps the grid at the smallest
+// phase's row count), so no workgroup can start a phase before every
+// workgroup has finished the previous one; each tagged buffer is rewritten
+// only every fifth phase, long after its last reader.
 //
-// Hand-off between workgroups.  Activations written by one workgroup and read
-// by another (q, K/V rows, attention output, residual stream, FFN hidden
-// vector) are stored with agent-coherent (sc1) stores and read with coherent
-// loads, so no L2 of the eight XCDs can serve a stale copy; each thread drains
-// its stores before its workgroup arrives at the barrier.  Weights, norms and
-// tables are read-only during the launch and use ordinary (nontemporal) loads.
+// Residual stream.  WO and W2 both produce the D rows of the residual stream
+// with the same row split, so each workgroup keeps its own rows of x in LDS
+// and the residual adds read nothing from memory.
 //
-// Barrier.  A monotonically increasing arrival counter; barrier k of a launch
-// waits until the counter reaches base + (k+1) * gridDim.x, where base is
-// carried from launch to launch in device memory.  The wait is bounded: after
-// kSpinLimit polls the workgroup records an error and every later barrier of
-// the launch returns at once, so every wave always reaches the end of the
-// kernel; the host reports the error.
+// GEMV phases.  The split dimension (output rows) is cut into balanced
+// contiguous ranges, one per workgroup.  Inside the workgroup, KS waves share
+// a row (split-K) and RW = 8 / KS row groups take rows round robin; the host
+// planner picks KS per phase.  A wave's work is a list of items = (local row,
+// 1 KiB column chunk): 64 lanes x 16 bytes (4 fp32 or 16 int8 weights per
+// lane), streamed through two register buffers of NB items (double
+// buffering); a finished row's partial is reduced across the wave (DPP) and
+// stored to LDS slot [row][k-slice], so the sum order is fixed and results are
+// bitwise reproducible.
+//
+// Every wait is bounded: after kSpinLimit polls a workgroup records an error
+// and every later wait of the launch returns at once, so every wave always
+// reaches the end of the kernel; the host reports the error.
 #pragma once
 #include <math.h>
 
@@ -49,13 +56,16 @@ namespace kl {
 constexpr int kPThreads = 512;
 constexpr int kPWaves = kPThreads / kWave;
 constexpr int kSpinLimit = 1 << 22;
+constexpr int kTagLayers = 128;  // tag = epoch * kTagLayers + layer + 1
 
 // Error codes written to PArgs::err by the device.
-constexpr int kDevErrBarrier = 1;  // a barrier wait exceeded kSpinLimit polls
-constexpr int kDevErrPos = 2;      // position outside [0, seq_len)
-constexpr int kDevErrToken = 3;    // the sampler found no finite maximum
+constexpr int kDevErrWait = 1;   // a wait for another workgroup exceeded kSpinLimit polls
+constexpr int kDevErrPos = 2;    // position or token outside the model's range
+constexpr int kDevErrToken = 3;  // the sampler found no finite maximum
 
 enum : int { kEpiQkv = 0, kEpiResid = 1, kEpiSwiglu = 2, kEpiCls = 3 };
+
+typedef unsigned long long tagged_t;  // {float bits (low), tag (high)}
 
 // One GEMV phase (host-built, read-only in device memory).
 struct PGemv {
@@ -69,15 +79,18 @@ struct PGemv {
   int cn;                 // 1 KiB chunks per row (last one may be partial)
   int cn16;               // 16-byte lane units per row
   int gshift;             // int8 group size = 1 << gshift
-  int rpw;                // split-dimension rows per workgroup
   int ks, rw;             // waves per row (split-K), row groups; ks * rw == kPWaves
-  int nck;                // chunks per (row, k-slice) = ceil(cn / ks)
+  int nseg;               // segments (NB consecutive chunks) per row
+  int nsegw;              // segments per (row, wave) = ceil(nseg / ks)
   int epi;                // kEpi*
-  const float* in;        // input vector; nullptr: embedding row of the step's token
+  int layer;              // tags: this phase writes tag(layer), reads tag(in_layer)
+  int in_layer;
+  const tagged_t* in;     // tagged input vector; nullptr: embedding row of the token
   const float* norm;      // RMSNorm weight applied to the input, or nullptr
-  float* out[3];          // qkv: q, K cache layer base, V cache layer base; else out[0]
+  tagged_t* out[3];       // qkv: q, new K row, new V row; resid / swiglu: out[0]
+  float* vcache;          // qkv: V cache layer base (row pos kept for later tokens)
+  float* logits;          // classifier output
   const float* bias[3];   // qkv bias (Qwen2) or nullptr
-  const float* resid;     // kEpiResid: residual input; nullptr: embedding row of the token
 };
 
 struct PAttn {
@@ -103,28 +116,29 @@ struct PArgs {
   const float* sin_t;
   const float* cos_t;
   const float* emb;
-  const float* q;      // query [Dq] (QKV phase output)
-  float* att;          // attention output [Dq]
-  float* attn_part;    // split partials [KVH][G][kv_mul][HD + 2]
+  const tagged_t* q;       // QKV phase outputs (tagged)
+  const tagged_t* knew;
+  const tagged_t* vnew;
+  tagged_t* att;           // attention output [Dq] (tagged)
+  float* attn_part;        // split partials [KVH][G][kv_mul][HD + 2]
   unsigned int* attn_cnt;  // [KVH] arrival counters, zero between phases
-  int attn_G;          // chunk slots per kv head
-  float* am_pv;        // [gridDim] argmax partials
+  int attn_G;              // chunk slots per kv head
+  float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
-  unsigned int* am_cnt;    // argmax / end-of-step arrival counter
-  unsigned int* bar;       // grid barrier arrival counter
-  unsigned int* bar_base;  // counter value at the start of the next launch
+  unsigned int* am_cnt;    // end-of-step arrival counter
+  unsigned int* epoch;     // launch counter for tags
   int* err;
-  int red_off;         // LDS: the GEMV input vector at 0, row partials at red_off floats
+  int red_off;             // LDS floats: input vector at 0, row partials at red_off,
+  int xres_off;            //   own residual rows at xres_off
   PStepState* st;
   const int32_t* prompt;
   int32_t* out_tokens;
   // Optional device-time trace (nullptr: off).  Slot-major [slot][workgroup]
-  // of 100 MHz s_memrealtime ticks: slot 0 = kernel entry, slots 2k+1 / 2k+2 =
-  // arrival at / release from grid barrier k, slot 2 * n_barriers + 1 = end of
-  // the workgroup's last phase.
+  // of 100 MHz s_memrealtime ticks: slot 0 = kernel entry; phase p (5 per
+  // layer: QKV, attention, WO, W1/W3, W2; then the classifier) has slot 2p+1 =
+  // its input staged and slot 2p+2 = its outputs stored.
   unsigned long long* trace;
 };
-
 
 // ---------------------------------------------------------------------------
 // Address spaces.  Phase descriptors are read through the constant address
@@ -174,36 +188,38 @@ __device__ __forceinline__ T g_stream(const T* p) {
   return __builtin_nontemporal_load((const KL_GAS T*)(p));
 }
 
+__device__ __forceinline__ unsigned long long g_ld64(const tagged_t* p) {
+  return __hip_atomic_load((KL_GAS tagged_t*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void g_st_tagged(tagged_t* p, float v, unsigned int tag) {
+  const tagged_t x = (static_cast<tagged_t>(tag) << 32) | __float_as_uint(v);
+  __hip_atomic_store((KL_GAS tagged_t*)(p), x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned int tag_of(tagged_t x) { return static_cast<unsigned int>(x >> 32); }
+__device__ __forceinline__ float val_of(tagged_t x) {
+  return __uint_as_float(static_cast<unsigned int>(x));
+}
+
 __device__ __forceinline__ void trace_mark(const PArgs& a, int slot) {
   if (a.trace && threadIdx.x == 0)
     a.trace[static_cast<size_t>(slot) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 }
 
-// Grid barrier; `target` is this launch's running arrival target, `nbar` the
-// barrier's index within the launch (for the trace).
-__device__ __forceinline__ void grid_sync(const PArgs& a, unsigned int& target, int& nbar) {
-  target += gridDim.x;
-  wait_mem();
-  __syncthreads();
-  trace_mark(a, 2 * nbar + 1);
-  if (threadIdx.x == 0) {
-    if (g_ld(a.err) == 0) {
-      g_arrive(a.bar);
-      for (int spins = 0;; ++spins) {
-        const unsigned int c = g_ld(a.bar);
-        if (static_cast<int>(c - target) >= 0) break;
-        if ((spins & 255) == 255 && g_ld(a.err) != 0) break;
-        if (spins >= kSpinLimit) {
-          g_st(a.err, kDevErrBarrier);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
+// Loads a tagged element, re-polling until it carries `tag`.  Bounded: on
+// timeout (or once another workgroup has reported an error) returns whatever
+// value it holds.
+__device__ __forceinline__ float poll_tagged(const PArgs& a, const tagged_t* p, unsigned int tag) {
+  tagged_t x = g_ld64(p);
+  for (int spins = 0; tag_of(x) != tag; ++spins) {
+    if ((spins & 63) == 63 && g_ld(a.err) != 0) break;
+    if (spins >= kSpinLimit) {
+      g_st(a.err, kDevErrWait);
+      break;
     }
+    __builtin_amdgcn_s_sleep(1);
+    x = g_ld64(p);
   }
-  trace_mark(a, 2 * nbar + 2);
-  ++nbar;
-  __syncthreads();
+  return val_of(x);
 }
 
 // Sum over the 512 threads of the workgroup; `red` holds >= kPWaves floats.
@@ -218,26 +234,33 @@ __device__ __forceinline__ float block_sum_p(float v, float* red) {
   return t;
 }
 
-// Stages an activation vector into LDS (coherent loads unless it is constant
-// data such as an embedding row), applying RMSNorm when `nw` is set:
+// Stages a GEMV input vector into LDS: the tagged vector `src` (all n elements
+// polled until they carry `tag`), or the embedding row `emb_row` when src is
+// null; applies RMSNorm when `nw` is set:
 // y = w * (x * (1 / sqrt(mean(x^2) + eps))) (kernels/cpu/rmsnorm_kernel.cpp:30-32).
 // Ends with a workgroup barrier.
-__device__ __forceinline__ void stage_vec(const float* src, bool coherent, const float* nw,
-                                          float eps, int n, float* xs, float* red) {
+__device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, unsigned int tag,
+                                          const float* emb_row, const float* nw, float eps, int n,
+                                          float* xs, float* red) {
   float ss = 0.f;
   for (int b0 = 0; b0 < n; b0 += kPThreads * 8) {
-    float v[8];
+    tagged_t v[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int i = b0 + k * kPThreads + threadIdx.x;
-      v[k] = i < n ? (coherent ? g_ld(src + i) : g_rd(src + i)) : 0.f;
+      if (src)
+        v[k] = i < n ? g_ld64(src + i) : (static_cast<tagged_t>(tag) << 32);
+      else
+        v[k] = (static_cast<tagged_t>(tag) << 32) | __float_as_uint(i < n ? g_rd(emb_row + i) : 0.f);
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int i = b0 + k * kPThreads + threadIdx.x;
+      float x = val_of(v[k]);
+      if (tag_of(v[k]) != tag) x = poll_tagged(a, src + i, tag);
       if (i < n) {
-        xs[i] = v[k];
-        ss += v[k] * v[k];
+        xs[i] = x;
+        ss += x * x;
       }
     }
   }
@@ -249,44 +272,73 @@ __device__ __forceinline__ void stage_vec(const float* src, bool coherent, const
   __syncthreads();
 }
 
+// Lane-shifted copy of x through DPP (lanes without a source read 0).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_shift(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes with DPP row shifts and row broadcasts; the total is
+// valid in lane 63 only.
+__device__ __forceinline__ float wave_sum_to_63(float v) {
+  v += dpp_shift<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_shift<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_shift<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_shift<0x118, 0xf>(v);  // row_shr:8   -> lane 15 of each row holds the row sum
+  v += dpp_shift<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_shift<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // GEMV streaming.
+//
+// Unit of work: a segment = NB consecutive 1 KiB chunks of one row (64 lanes x
+// 16 bytes per chunk: 4 fp32 or 16 int8 weights per lane).  A wave owns the
+// segments (row rg + rw * jr, segment ksi + ks * js) of its workgroup's rows;
+// per segment it issues NB loads from one scalar row pointer, so all
+// bookkeeping is per segment, not per chunk.  Segments are double buffered in
+// registers.  When every wave always reads the same segment of its rows
+// (nsegw == 1), the matching slice of the fp32 input stays in registers for
+// the whole phase instead of being read from LDS per chunk.
 // ---------------------------------------------------------------------------
 template <bool Q8>
-struct PItem;
+struct PChunk;
 template <>
-struct PItem<false> {
+struct PChunk<false> {
   f4 w;
 };
 template <>
-struct PItem<true> {
+struct PChunk<true> {
   i4 w;
   float s;
 };
 
-// This workgroup's share of a phase and this wave's item geometry.
+// This workgroup's share of a phase and this wave's segment geometry.
 struct PGeom {
   int base;  // first split-dimension row of the workgroup
   int cnt;   // split-dimension rows of the workgroup
   int nloc;  // local rows (paired: cnt per sub-matrix)
-  int n_items;
+  int n_items;  // segments of this wave
   int rg, ksi;
 };
 
 __device__ __forceinline__ PGeom p_geom(PGp p) {
   PGeom g;
   // The wave index is uniform across the wave; readfirstlane lets the compiler
-  // keep every item's row/sub-matrix arithmetic (and the descriptor loads it
+  // keep every segment's row/sub-matrix arithmetic (and the descriptor loads it
   // drives) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   g.ksi = wave % p->ks;
   g.rg = wave / p->ks;
+  // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n).
   const int total = p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2];
-  g.base = blockIdx.x * p->rpw;
-  g.cnt = max(0, min(p->rpw, total - g.base));
+  const long long b = blockIdx.x, n = gridDim.x;
+  g.base = static_cast<int>(b * total / n);
+  g.cnt = static_cast<int>((b + 1) * total / n) - g.base;
   g.nloc = p->paired ? g.cnt * p->nsub : g.cnt;
   const int nrows = g.nloc > g.rg ? (g.nloc - g.rg + p->rw - 1) / p->rw : 0;
-  g.n_items = nrows * p->nck;
+  g.n_items = g.ksi < p->nseg ? nrows * p->nsegw : 0;
   return g;
 }
 
@@ -315,53 +367,62 @@ __device__ __forceinline__ void p_row(PGp p, const PGeom& g, int lr, int& sub, i
   }
 }
 
-// Item cursor: j-th item of the wave = (jr-th row of the wave, jc-th chunk).
+// Segment cursor: j-th segment of the wave = (jr-th row of the wave, js-th
+// segment of that row).
 struct PCur {
-  int j, jr, jc;
+  int j, jr, js;
 };
 
-__device__ __forceinline__ void p_advance(PCur& c, int nck) {
+__device__ __forceinline__ void p_advance(PCur& c, int nsegw) {
   ++c.j;
-  if (++c.jc == nck) {
-    c.jc = 0;
+  if (++c.js == nsegw) {
+    c.js = 0;
     ++c.jr;
   }
 }
 
-// Issues the loads of NB items starting at cursor c (advanced past them).
-// Every load is issued unconditionally (items past the wave's last one and
-// lanes past the row's end read a clamped, valid address; p_compute masks
-// them out), so the code is straight-line and the compiler can wait for each
-// item with an exact vmcnt instead of draining every outstanding load.
+// Issues the NB loads of the segment at cursor c (then advances it).  Every
+// load is issued (a wave without a segment left reads a clamped valid
+// address, lanes past the row's end read the row start; p_seg_compute masks
+// both), so the code is straight-line and each use waits with an exact vmcnt.
 template <bool Q8, int NB>
-__device__ __forceinline__ void p_issue(PGp p, const PGeom& g, PCur& c, PItem<Q8> (&buf)[NB]) {
+__device__ __forceinline__ void p_seg_issue(PGp p, const PGeom& g, PCur& c,
+                                            PChunk<Q8> (&buf)[NB]) {
   const int lane = threadIdx.x & 63;
-  const int nck = p->nck, rw = p->rw, ks = p->ks, cn = p->cn, cn16 = p->cn16, cols = p->cols;
-#pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    const bool item_ok = c.j < g.n_items;
-    int sub = 0, row = 0, chunk = 0;
-    if (item_ok) {
-      p_row(p, g, g.rg + rw * c.jr, sub, row);
-      chunk = g.ksi + ks * c.jc;
-    }
-    const int u = chunk * kWave + lane;  // 16-byte unit within the row
-    const int uc = (item_ok && chunk < cn && u < cn16) ? u : 0;
-    if constexpr (Q8) {
-      const size_t e = static_cast<size_t>(row) * cols + static_cast<size_t>(uc) * 16;
-      const int8_t* wp = static_cast<const int8_t*>(p->w[sub]);
-      buf[k].w = g_stream(reinterpret_cast<const i4*>(wp + e));
-      buf[k].s = g_rd(p->sc[sub] + (e >> p->gshift));
-    } else {
-      const float* wp = static_cast<const float*>(p->w[sub]) + static_cast<size_t>(row) * cols;
-      buf[k].w = g_stream(reinterpret_cast<const f4*>(wp) + uc);
-    }
-    p_advance(c, nck);
+  const bool item_ok = c.j < g.n_items;
+  int sub = 0, row = 0, seg = 0;
+  if (item_ok) {
+    p_row(p, g, g.rg + p->rw * c.jr, sub, row);
+    seg = g.ksi + p->ks * c.js;
   }
+  const int lim = item_ok ? p->cn16 : 0;  // valid 16-byte units of the row
+  const int u0 = seg * NB * kWave + lane;
+  const int cols = p->cols;
+  if constexpr (Q8) {
+    const int8_t* wp = static_cast<const int8_t*>(p->w[sub]) + static_cast<size_t>(row) * cols;
+    const float* sp = p->sc[sub];
+    const size_t e0 = static_cast<size_t>(row) * cols;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int u = u0 + k * kWave;
+      const int uc = u < lim ? u : 0;
+      buf[k].w = g_stream(reinterpret_cast<const i4*>(wp) + uc);
+      buf[k].s = g_rd(sp + ((e0 + static_cast<size_t>(uc) * 16) >> p->gshift));
+    }
+  } else {
+    const f4* wp = reinterpret_cast<const f4*>(static_cast<const float*>(p->w[sub]) +
+                                               static_cast<size_t>(row) * cols);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int u = u0 + k * kWave;
+      buf[k].w = g_stream(wp + (u < lim ? u : 0));
+    }
+  }
+  p_advance(c, p->nsegw);
 }
 
 template <bool Q8>
-__device__ __forceinline__ float p_dot(const PItem<Q8>& it, const float* xs, int u) {
+__device__ __forceinline__ float p_dot(const PChunk<Q8>& it, const float* xs, int u) {
   if constexpr (Q8) {
     const f4* xc = reinterpret_cast<const f4*>(xs) + 4 * u;
     float q[16];
@@ -379,68 +440,91 @@ __device__ __forceinline__ float p_dot(const PItem<Q8>& it, const float* xs, int
   }
 }
 
-// Consumes NB items starting at cursor c; a finished row's wave total goes to
-// red[local row * ks + k-slice].  Masked lanes and items contribute through a
-// select, never a branch around the load's use.
+// Consumes the segment at cursor c; a finished row's wave total goes to
+// red[local row * ks + k-slice].  xr holds the wave's input slice when xreg.
 template <bool Q8, int NB>
-__device__ __forceinline__ void p_compute(PGp p, const PGeom& g, PCur& c,
-                                          const PItem<Q8> (&buf)[NB], const float* xs, float* red,
-                                          float& acc) {
+__device__ __forceinline__ void p_seg_compute(PGp p, const PGeom& g, PCur& c,
+                                              const PChunk<Q8> (&buf)[NB], const float* xs,
+                                              const f4 (&xr)[NB], bool xreg, float* red,
+                                              float& acc) {
   const int lane = threadIdx.x & 63;
-  const int nck = p->nck, rw = p->rw, ks = p->ks, cn = p->cn, cn16 = p->cn16;
+  const bool item_ok = c.j < g.n_items;
+  const int seg = g.ksi + p->ks * c.js;
+  const int lim = item_ok ? p->cn16 : 0;
+  const int u0 = seg * NB * kWave + lane;
+  float part = 0.f;
+  if (!Q8 && xreg) {
+    f4 a4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    const bool item_ok = c.j < g.n_items;
-    const int chunk = g.ksi + ks * c.jc;
-    const int u = chunk * kWave + lane;
-    const bool ok = item_ok && chunk < cn && u < cn16;
-    const float d = p_dot<Q8>(buf[k], xs, ok ? u : 0);
-    acc += ok ? d : 0.f;
-    if (item_ok && c.jc == nck - 1) {
-      const float v = wave_sum(acc);
-      if (lane == 0) red[(g.rg + rw * c.jr) * ks + g.ksi] = v;
-      acc = 0.f;
+    for (int k = 0; k < NB; ++k) {
+      const f4 prod = reinterpret_cast<const f4&>(buf[k].w) * xr[k];
+      a4 += (u0 + k * kWave) < lim ? prod : f4{0.f, 0.f, 0.f, 0.f};
     }
-    p_advance(c, nck);
+    part = hsum(a4);
+  } else {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int u = u0 + k * kWave;
+      const bool ok = u < lim;
+      const float d = p_dot<Q8>(buf[k], xs, ok ? u : 0);
+      part += ok ? d : 0.f;
+    }
   }
+  acc += part;
+  if (item_ok && c.js == p->nsegw - 1) {
+    const float v = wave_sum_to_63(acc);
+    if (lane == 63) red[(g.rg + p->rw * c.jr) * p->ks + g.ksi] = v;
+    acc = 0.f;
+  }
+  p_advance(c, p->nsegw);
 }
 
 // Runs the streaming loop of one phase.  On entry, buffer A holds (in flight)
-// the wave's first NB items of p; on exit A holds (in flight) the first NB
-// items of `pn` (when pn is set).  Only A is live outside this function, so
-// the attention phase and the staging code have the registers of B to
+// the wave's first segment of p; on exit A holds (in flight) the first segment
+// of `pn` (when pn is set).  Only A is live outside this function, so the
+// attention phase and the staging code have the registers of B to
 // themselves.  Returns with LDS `red` holding every finished row of the
 // workgroup (after a workgroup barrier).
 template <bool Q8, int NB>
 __device__ __forceinline__ void p_stream(PGp p, const PGeom& g, PGp pn, const PGeom& gn,
-                                         PItem<Q8> (&A)[NB], const float* xs, float* red) {
-  PItem<Q8> B[NB];
-  const int nck = p->nck;
-  const int nb = (g.n_items + NB - 1) / NB;
-  PCur ci{NB, NB / nck, NB % nck};  // issue cursor: batch 1
-  PCur cc{0, 0, 0};                  // compute cursor
+                                         PChunk<Q8> (&A)[NB], const float* xs, float* red) {
+  PChunk<Q8> B[NB];
+  const int nb = g.n_items;
+  PCur ci{1, 1 / p->nsegw, 1 % p->nsegw};  // issue cursor: segment 1
+  PCur cc{0, 0, 0};                          // compute cursor
+  // The wave's input slice in registers when it always reads one segment.
+  const bool xreg = !Q8 && p->nsegw == 1;
+  f4 xr[NB];
+  if (!Q8) {
+    const int u0 = g.ksi * NB * kWave + (threadIdx.x & 63);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int u = u0 + k * kWave;
+      xr[k] = xreg && u < p->cn16 ? reinterpret_cast<const f4*>(xs)[u] : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
   float acc = 0.f;
   auto next_phase = [&]() {
     if (pn) {
       PCur c0{0, 0, 0};
-      p_issue<Q8, NB>(pn, gn, c0, A);
+      p_seg_issue<Q8, NB>(pn, gn, c0, A);
     }
   };
   for (int b = 0; b < nb; b += 2) {
-    // batch b is in A
+    // segment b is in A
     if (b + 1 < nb) {
-      p_issue<Q8, NB>(p, g, ci, B);
-      p_compute<Q8, NB>(p, g, cc, A, xs, red, acc);
+      p_seg_issue<Q8, NB>(p, g, ci, B);
+      p_seg_compute<Q8, NB>(p, g, cc, A, xs, xr, xreg, red, acc);
     } else {
-      p_compute<Q8, NB>(p, g, cc, A, xs, red, acc);
+      p_seg_compute<Q8, NB>(p, g, cc, A, xs, xr, xreg, red, acc);
       break;
     }
-    // batch b + 1 is in B; A is free
+    // segment b + 1 is in B; A is free
     if (b + 2 < nb)
-      p_issue<Q8, NB>(p, g, ci, A);
+      p_seg_issue<Q8, NB>(p, g, ci, A);
     else
       next_phase();
-    p_compute<Q8, NB>(p, g, cc, B, xs, red, acc);
+    p_seg_compute<Q8, NB>(p, g, cc, B, xs, xr, xreg, red, acc);
   }
   if (nb % 2 == 1 || nb == 0) next_phase();
   __syncthreads();
@@ -458,14 +542,17 @@ __device__ __forceinline__ float p_row_total(int ks, const float* red, int lr) {
 // optional Qwen3 per-head q/k RMSNorm (model/qwen3.cpp:485-500) and RoPE
 // (kernels/cpu/rope_kernel.cpp) applied first).  One item = (kv head, chunk
 // of PT positions); items are spread over the workgroups; the last chunk of a
-// kv head to finish merges the chunks.  LDS floats needed: attn_p_lds_floats.
+// kv head to finish merges the chunks.  Rows before pos come from the cache
+// (written by earlier launches); q and the new K/V rows come from the tagged
+// QKV outputs.  The chunk that holds pos writes the transformed K row to the
+// cache for later tokens.  LDS floats needed: attn_p_lds_floats.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int attn_p_rpp(int hd) { return kPThreads / (hd / 4); }
 
 __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul, int G) {
   const int pt = attn_chunk(hd);
-  const size_t head = static_cast<size_t>(kv_mul) * hd + static_cast<size_t>(kv_mul) * pt + hd +
-                      2 * kAttnMaxKvMul;
+  const size_t head = static_cast<size_t>(kv_mul) * hd + static_cast<size_t>(kv_mul) * pt +
+                      2 * static_cast<size_t>(hd) + 2 * kAttnMaxKvMul;
   const size_t pv = static_cast<size_t>(attn_p_rpp(hd)) * kv_mul * hd;
   const size_t merge = 2 * static_cast<size_t>(G) * kv_mul;
   return head + (pv > merge ? pv : merge);
@@ -473,7 +560,7 @@ __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul, int G) {
 
 template <int HD>
 __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, int pos,
-                                             float* lds) {
+                                             unsigned int tag, float* lds) {
   constexpr int PT = attn_chunk(HD);
   constexpr int TPR = HD / 4;
   constexpr int RPP = attn_p_rpp(HD);
@@ -497,8 +584,9 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
   const int items = a.KVH * nsplit;
   float* qs = lds;                      // [kvm][HD]
   float* sc = qs + kvm * HD;            // [kvm][PT]
-  float* kp = sc + kvm * PT;            // [HD]
-  float* ml = kp + HD;                  // [2 * kAttnMaxKvMul]
+  float* kp = sc + kvm * PT;            // [HD] K[pos] (transformed)
+  float* vp = kp + HD;                  // [HD] V[pos]
+  float* ml = vp + HD;                  // [2 * kAttnMaxKvMul]
   float* red = ml + 2 * kAttnMaxKvMul;  // [RPP][kvm][HD]; merge: [nsplit][kvm][2]
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int g = it / nsplit;
@@ -507,30 +595,30 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     const int cnt = min(n - t0, PT);
     const bool own_pos = pos >= t0 && pos < t0 + cnt;
 
-    // 1. The chunk's K and V rows into registers; row pos was written in this
-    //    launch (QKV phase) and is read coherently.
+    // 1. The chunk's cached K and V rows into registers (row pos is replaced
+    //    below by the new row).
     f4 kr[NP], vr[NP];
     {
       const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         const int tt = p * RPP + rr;
-        const int t = t0 + (tt < cnt ? tt : 0);
+        const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);
         const size_t off = static_cast<size_t>(t) * a.Dkv + col;
-        if (t == pos) {
-          kr[p] = f4{g_ld(kcache + off), g_ld(kcache + off + 1), g_ld(kcache + off + 2),
-                     g_ld(kcache + off + 3)};
-          vr[p] = f4{g_ld(vcache + off), g_ld(vcache + off + 1), g_ld(vcache + off + 2),
-                     g_ld(vcache + off + 3)};
-        } else {
-          kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
-          vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
-        }
+        kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
+        vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
       }
     }
-    // 2. q of the group's heads (coherent), q norm + RoPE in LDS; K[pos] transform.
+    // 2. q of the group's heads and (chunk of pos) the new K and V rows.
     for (int i = tid; i < kvm * HD; i += kPThreads)
-      qs[i] = g_ld(a.q + static_cast<size_t>(g) * kvm * HD + i);
+      qs[i] = poll_tagged(a, a.q + static_cast<size_t>(g) * kvm * HD + i, tag);
+    if (own_pos) {
+      for (int i = tid; i < 2 * HD; i += kPThreads) {
+        const tagged_t* src = i < HD ? a.knew : a.vnew;
+        const int d = i < HD ? i : i - HD;
+        kp[i] = poll_tagged(a, src + static_cast<size_t>(g) * HD + d, tag);  // kp, then vp
+      }
+    }
     __syncthreads();
     if (a.transform == 2) {
       for (int h = wave; h < kvm; h += kPWaves) {
@@ -540,65 +628,41 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         const float r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
         for (int d = lane; d < HD; d += kWave) qs[h * HD + d] = (r * qs[h * HD + d]) * g_rd(qn + d);
       }
+      if (own_pos && wave == kPWaves - 1) {
+        float ss = 0.f;
+        for (int d = lane; d < HD; d += kWave) ss += kp[d] * kp[d];
+        ss = wave_sum(ss);
+        const float r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
+        for (int d = lane; d < HD; d += kWave) kp[d] = (r * kp[d]) * g_rd(kn + d);
+      }
       __syncthreads();
     }
     if (a.transform >= 1) {
       const float* srow = a.sin_t + static_cast<size_t>(pos) * HD;
       const float* crow = a.cos_t + static_cast<size_t>(pos) * HD;
-      for (int p = tid; p < kvm * HALF; p += kPThreads) {
+      const int heads = own_pos ? kvm + 1 : kvm;  // head kvm = the new K row
+      for (int p = tid; p < heads * HALF; p += kPThreads) {
         const int h = p / HALF, j = p - h * HALF;
-        const int i0 = a.rope_style ? h * HD + j : h * HD + 2 * j;
-        const int i1 = a.rope_style ? i0 + HALF : i0 + 1;
-        float v0 = qs[i0], v1 = qs[i1];
+        float* v = h < kvm ? qs + h * HD : kp;
+        const int i0 = a.rope_style ? j : 2 * j;
+        const int i1 = a.rope_style ? j + HALF : 2 * j + 1;
+        float v0 = v[i0], v1 = v[i1];
         rope_pair(v0, v1, g_rd(crow + 2 * j), g_rd(srow + 2 * j));
-        qs[i0] = v0;
-        qs[i1] = v1;
-      }
-      if (wave == 0 && own_pos) {
-        float* krow = kcache + static_cast<size_t>(pos) * a.Dkv + static_cast<size_t>(g) * HD;
-        constexpr int PPL = (HALF + kWave - 1) / kWave;
-        float v0[PPL], v1[PPL];
-        float ss = 0.f;
-#pragma unroll
-        for (int k = 0; k < PPL; ++k) {
-          const int j = lane + k * kWave;
-          if (j < HALF) {
-            const int i0 = a.rope_style ? j : 2 * j;
-            const int i1 = a.rope_style ? j + HALF : 2 * j + 1;
-            v0[k] = g_ld(krow + i0);
-            v1[k] = g_ld(krow + i1);
-            ss += v0[k] * v0[k] + v1[k] * v1[k];
-          }
-        }
-        float r = 1.f;
-        if (a.transform == 2) {
-          ss = wave_sum(ss);
-          r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
-        }
-#pragma unroll
-        for (int k = 0; k < PPL; ++k) {
-          const int j = lane + k * kWave;
-          if (j < HALF) {
-            const int i0 = a.rope_style ? j : 2 * j;
-            const int i1 = a.rope_style ? j + HALF : 2 * j + 1;
-            float x0 = v0[k], x1 = v1[k];
-            if (a.transform == 2) {
-              x0 = (r * x0) * g_rd(kn + i0);
-              x1 = (r * x1) * g_rd(kn + i1);
-            }
-            rope_pair(x0, x1, g_rd(crow + 2 * j), g_rd(srow + 2 * j));
-            g_st(krow + i0, x0);
-            g_st(krow + i1, x1);
-            kp[i0] = x0;
-            kp[i1] = x1;
-          }
-        }
+        v[i0] = v0;
+        v[i1] = v1;
       }
       __syncthreads();
-      if (own_pos) {
+    }
+    if (own_pos) {
+      // The new rows join the chunk; K[pos] (transformed) goes to the cache.
+      float* krow = kcache + static_cast<size_t>(pos) * a.Dkv + static_cast<size_t>(g) * HD;
+      for (int d = tid; d < HD; d += kPThreads) krow[d] = kp[d];
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-          if (t0 + p * RPP + rr == pos) kr[p] = reinterpret_cast<const f4*>(kp)[sub];
+      for (int p = 0; p < NP; ++p) {
+        if (t0 + p * RPP + rr == pos) {
+          kr[p] = reinterpret_cast<const f4*>(kp)[sub];
+          vr[p] = reinterpret_cast<const f4*>(vp)[sub];
+        }
       }
     }
 
@@ -652,14 +716,14 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
       }
     }
     __syncthreads();
-    float* outg = a.att + static_cast<size_t>(g) * kvm * HD;
+    tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
     float* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
     for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
       const int h = idx / HD, d = idx - h * HD;
       float o = 0.f;
       for (int k = 0; k < RPP; ++k) o += red[(static_cast<size_t>(k) * kvm + h) * HD + d];
       if (nsplit == 1) {
-        g_st(outg + h * HD + d, o / ml[2 * h + 1]);
+        g_st_tagged(outg + h * HD + d, o / ml[2 * h + 1], tag);
       } else {
         float* ps = pg + (static_cast<size_t>(s) * kvm + h) * (HD + 2);
         g_st(ps + d, o);
@@ -696,7 +760,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
             L += mls[2 * (k * kvm + h) + 1] * w;
             O += g_ld(pg + (static_cast<size_t>(k) * kvm + h) * (HD + 2) + d) * w;
           }
-          g_st(outg + h * HD + d, O / L);
+          g_st_tagged(outg + h * HD + d, O / L, tag);
         }
         if (tid == 0) g_st(a.attn_cnt + g, 0u);
       }
@@ -706,10 +770,12 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 }
 
 // ---------------------------------------------------------------------------
-// Epilogues of the QKV, residual and SwiGLU phases.
+// Epilogues of the QKV, residual and SwiGLU phases.  `xres` holds this
+// workgroup's rows of the residual stream (the WO and W2 phases split the D
+// rows identically).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void p_epilogue(PGp p, const PGeom& g, const float* red, int pos,
-                                           const float* emb_row) {
+                                           unsigned int tag, float* xres) {
   const int ks = p->ks;
   const int epi = p->epi;
   if (epi == kEpiQkv) {
@@ -719,26 +785,24 @@ __device__ __forceinline__ void p_epilogue(PGp p, const PGeom& g, const float* r
       float v = p_row_total(ks, red, lr);
       const float* b = p->bias[sub];
       if (b) v = v + g_rd(b + row);
-      float* dst = sub == 0 ? p->out[0] + row
-                            : p->out[sub] + static_cast<size_t>(pos) * p->rows[1] + row;
-      g_st(dst, v);
+      g_st_tagged(p->out[sub] + row, v, tag);
+      if (sub == 2) p->vcache[static_cast<size_t>(pos) * p->rows[2] + row] = v;
     }
   } else if (epi == kEpiResid) {
-    const float* resid = p->resid;
-    float* out = p->out[0];
+    tagged_t* out = p->out[0];
     for (int lr = threadIdx.x; lr < g.nloc; lr += kPThreads) {
-      const int row = g.base + lr;
-      const float r = resid ? g_ld(resid + row) : g_rd(emb_row + row);
-      g_st(out + row, r + p_row_total(ks, red, lr));
+      const float x = xres[lr] + p_row_total(ks, red, lr);
+      xres[lr] = x;
+      g_st_tagged(out + g.base + lr, x, tag);
     }
   } else if (epi == kEpiSwiglu) {
-    float* out = p->out[0];
+    tagged_t* out = p->out[0];
     for (int lr = threadIdx.x; lr < g.cnt; lr += kPThreads) {
       const float a1 = p_row_total(ks, red, lr);
       const float a3 = p_row_total(ks, red, lr + g.cnt);
       // kernels/cpu/swiglu_kernel.cpp:21-22
       const float s = a1 * (1.0f / (1.0f + expf(-a1)));
-      g_st(out + g.base + lr, s * a3);
+      g_st_tagged(out + g.base + lr, s * a3, tag);
     }
   }
 }
@@ -761,38 +825,44 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     return;
   }
   const bool sample = pos + 1 >= st.prompt_len;
-  unsigned int target = g_rd(a.bar_base);
-  int nbar = 0;
-  trace_mark(a, 0);
+  const unsigned int epoch = g_rd(a.epoch);
   const float* emb_row = a.emb + static_cast<size_t>(token) * a.D;
   const PGp ph = (PGp)(a.ph);
   const int ncls = 4 * a.L;  // index of the classifier phase
   float* xs = lds;
   float* red = lds + a.red_off;
+  float* xres = lds + a.xres_off;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int slot = 0;
+  trace_mark(a, slot++);
 
-  PItem<Q8> A[NB];
+  PChunk<Q8> A[NB];
   {
     const PGeom g0 = p_geom(ph);
     PCur c0{0, 0, 0};
-    p_issue<Q8, NB>(ph, g0, c0, A);
+    p_seg_issue<Q8, NB>(ph, g0, c0, A);
+    // This workgroup's rows of the residual stream start as the embedding row.
+    const PGeom gr = p_geom(ph + 1);
+    for (int lr = threadIdx.x; lr < gr.nloc; lr += kPThreads) xres[lr] = g_rd(emb_row + gr.base + lr);
   }
   float bv = -INFINITY;
   int bi = INT_MAX;
   for (int k = 0; k <= ncls; ++k) {
     const PGp p = ph + k;
     const bool is_cls = k == ncls;
-    // The next GEMV phase (its first loads are issued before the barrier).
+    // The next GEMV phase (its first loads are issued before this phase ends).
     const PGp pn = k + 1 < ncls ? ph + k + 1 : (k + 1 == ncls && sample ? ph + ncls : nullptr);
     const PGeom g = p_geom(p);
     const PGeom gn = pn ? p_geom(pn) : PGeom{};
-    const float* in = p->in;
-    stage_vec(in ? in : emb_row, in != nullptr, p->norm, a.eps, p->cols, xs, sred);
+    const unsigned int tag_in = epoch * kTagLayers + p->in_layer + 1;
+    const unsigned int tag = epoch * kTagLayers + p->layer + 1;
+    stage_vec(a, p->in, tag_in, emb_row, p->norm, a.eps, p->cols, xs, sred);
+    trace_mark(a, slot++);
     p_stream<Q8, NB>(p, g, pn, gn, A, xs, red);
     if (is_cls) {
       // Logits (plain stores, read by the host after the launch) and this
       // workgroup's (max, first index) pair (sampler/argmax_sampler.cpp:5-13).
-      float* logits = p->out[0];
+      float* logits = p->logits;
       const int ks = p->ks;
       for (int lr = threadIdx.x; lr < g.nloc; lr += kPThreads) {
         const float v = p_row_total(ks, red, lr);
@@ -808,22 +878,24 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       if (threadIdx.x == 0) {
         for (int w = 1; w < kPWaves; ++w) argmax_merge(bv, bi, s_bv[w], s_bi[w]);
         g_st(a.am_pv + blockIdx.x, bv);
-        g_st(reinterpret_cast<int*>(a.am_pi) + blockIdx.x, bi);
+        g_st(a.am_pi + blockIdx.x, bi);
       }
+      trace_mark(a, slot++);
       break;
     }
-    p_epilogue(p, g, red, pos, emb_row);
+    p_epilogue(p, g, red, pos, tag, xres);
+    __syncthreads();  // red and xres are rewritten by the next phase
+    trace_mark(a, slot++);
     if (!pn) break;  // last layer of a prompt position: no classifier
-    grid_sync(a, target, nbar);
     if ((k & 3) == 0) {  // after QKV: attention of layer k / 4
-      attn_p_phase<HD>(a, a.at + (k >> 2), pos, lds);
-      grid_sync(a, target, nbar);
+      attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds);
+      trace_mark(a, slot++);
+      trace_mark(a, slot++);
     }
   }
 
   // End of step: the last workgroup to arrive samples (or takes the next
   // prompt token) and advances the device state for the next launch.
-  trace_mark(a, 2 * nbar + 1);
   wait_mem();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -837,7 +909,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     bv = -INFINITY;
     bi = INT_MAX;
     for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kPThreads)
-      argmax_merge(bv, bi, g_ld(a.am_pv + b), g_ld(reinterpret_cast<const int*>(a.am_pi) + b));
+      argmax_merge(bv, bi, g_ld(a.am_pv + b), g_ld(a.am_pi + b));
     wave_argmax(bv, bi);
     if (lane == 0) {
       s_bv[wave] = bv;
@@ -862,7 +934,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     ns.token = next;
     ns.pos = pos + 1;
     *a.st = ns;
-    *a.bar_base = target;
+    *a.epoch = epoch + 1;
     g_st(a.am_cnt, 0u);
   }
 }
