@@ -437,6 +437,7 @@ struct kl_engine {
   PAttn* d_at = nullptr;       // [L]
   tagged_t *t_q = nullptr, *t_k = nullptr, *t_v = nullptr, *t_att = nullptr;  // tagged
   tagged_t *t_xb = nullptr, *t_h = nullptr, *t_x = nullptr;                    //   hand-off
+  tagged_t* t_part = nullptr;  // attention split partials (tagged)
   unsigned int* epoch = nullptr;
   int* derr = nullptr;
   int* derr_host = nullptr;    // pinned
@@ -652,7 +653,7 @@ size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb) {
     const int rw = kPWaves / ks;
     const int nsegw = (p.nseg + ks - 1) / ks;
     double cost = static_cast<double>((nloc + rw - 1) / rw) * (nsegw * nb + 0.5);
-    if (!q8 && nsegw == 1) cost *= 0.97;  // the input slice stays in registers
+    if (!q8 && nsegw == 1) cost *= 0.9;  // the input slice stays in registers
     if (cost < best - 1e-9) {
       best = cost;
       p.ks = ks;
@@ -678,7 +679,7 @@ const void* persistent_kernel(int hd) {
 int setup_persistent(kl_engine* e) {
   const ImageLayout& m = e->lay;
   const bool q8 = e->quant != 0;
-  int nb = q8 ? 4 : 8;
+  int nb = 4;
   if (const char* env = std::getenv("KL_PNB")) nb = std::atoi(env);
   if (q8)
     e->p_kernel = nb == 4 ? persistent_kernel<true, 4>(m.hd) : persistent_kernel<true, 8>(m.hd);
@@ -768,7 +769,7 @@ int setup_persistent(kl_engine* e) {
   a.rope_style = e->rope_style; a.transform = e->transform;
   a.sin_t = e->sin_t; a.cos_t = e->cos_t; a.emb = e->emb;
   a.q = e->t_q; a.knew = e->t_k; a.vnew = e->t_v; a.att = e->t_att;
-  a.attn_part = e->attn_part; a.attn_cnt = e->attn_counters;
+  a.attn_part = e->t_part;
   a.attn_G = e->attn.G;
   a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
   a.epoch = e->epoch; a.err = e->derr;
@@ -936,6 +937,7 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   const size_t txb_at = plan(static_cast<size_t>(lay.D) * 8);
   const size_t th_at = plan(static_cast<size_t>(lay.F) * 8);
   const size_t tx_at = plan(static_cast<size_t>(lay.D) * 8);
+  const size_t tpart_at = plan(e->attn.part_floats * 8);
   const size_t zero_end = cursor;
   const int gmax = std::max(e->grid_cap, e->cus * kMaxPwgPerCu);
   const size_t ph_at = plan((4 * static_cast<size_t>(lay.L) + 1) * sizeof(PGemv));
@@ -1001,6 +1003,7 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   auto PT = [&](size_t at) { return reinterpret_cast<tagged_t*>(P(at)); };
   e->t_q = PT(tq_at); e->t_k = PT(tk_at); e->t_v = PT(tv_at); e->t_att = PT(tatt_at);
   e->t_xb = PT(txb_at); e->t_h = PT(th_at); e->t_x = PT(tx_at);
+  e->t_part = PT(tpart_at);
   e->d_ph = reinterpret_cast<PGemv*>(P(ph_at));
   e->d_at = reinterpret_cast<PAttn*>(P(at_at));
   e->lay.layers.clear();  // host pointers are no longer needed

@@ -120,8 +120,7 @@ struct PArgs {
   const tagged_t* knew;
   const tagged_t* vnew;
   tagged_t* att;           // attention output [Dq] (tagged)
-  float* attn_part;        // split partials [KVH][G][kv_mul][HD + 2]
-  unsigned int* attn_cnt;  // [KVH] arrival counters, zero between phases
+  tagged_t* attn_part;     // split partials [KVH][G][kv_mul][HD + 2] (tagged)
   int attn_G;              // chunk slots per kv head
   float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
@@ -238,10 +237,14 @@ __device__ __forceinline__ float block_sum_p(float v, float* red) {
 // polled until they carry `tag`), or the embedding row `emb_row` when src is
 // null; applies RMSNorm when `nw` is set:
 // y = w * (x * (1 / sqrt(mean(x^2) + eps))) (kernels/cpu/rmsnorm_kernel.cpp:30-32).
-// Ends with a workgroup barrier.
+// `prefetch()` issues the phase's first weight segment; it runs after the
+// first round of input loads is issued and before their results are used, so
+// waiting for the input never waits for the weights (loads complete in
+// order).  Ends with a workgroup barrier.
+template <class Prefetch>
 __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, unsigned int tag,
                                           const float* emb_row, const float* nw, float eps, int n,
-                                          float* xs, float* red) {
+                                          float* xs, float* red, Prefetch prefetch) {
   float ss = 0.f;
   for (int b0 = 0; b0 < n; b0 += kPThreads * 8) {
     tagged_t v[8];
@@ -253,6 +256,7 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
       else
         v[k] = (static_cast<tagged_t>(tag) << 32) | __float_as_uint(i < n ? g_rd(emb_row + i) : 0.f);
     }
+    if (b0 == 0) prefetch();
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int i = b0 + k * kPThreads + threadIdx.x;
@@ -288,6 +292,40 @@ __device__ __forceinline__ float wave_sum_to_63(float v) {
   v += dpp_shift<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
   v += dpp_shift<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
   return v;
+}
+
+// Sum over aligned groups of W lanes (W in 8, 16, 32, 64) with DPP butterflies
+// (quad_perm, half-row and row mirrors, row broadcasts): valid in lane W - 1
+// of each group (W <= 16: in every lane of the group).
+template <int W>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  v += dpp_shift<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v += dpp_shift<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v += dpp_shift<0x141, 0xf>(v);  // row_half_mirror: the two quads of each 8 lanes
+  if (W >= 16) v += dpp_shift<0x140, 0xf>(v);  // row_mirror: the two halves of each row
+  if (W >= 32) v += dpp_shift<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  if (W >= 64) v += dpp_shift<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Maximum over the 64 lanes, returned to every lane (uniform).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  auto mx = [](float a, float b) { return fmaxf(a, b); };
+  // -inf as the neutral element: shifted-in lanes read 0, so use mirrors and
+  // broadcasts whose sources are always valid lanes.
+  v = mx(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+  v = mx(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+  v = mx(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xf, 0xf, false)));
+  v = mx(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xf, 0xf, false)));
+  v = mx(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false)));
+  v = mx(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum over the 64 lanes, returned to every lane (uniform).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum_dpp<64>(v)), 63));
 }
 
 // ---------------------------------------------------------------------------
@@ -480,14 +518,12 @@ __device__ __forceinline__ void p_seg_compute(PGp p, const PGeom& g, PCur& c,
 }
 
 // Runs the streaming loop of one phase.  On entry, buffer A holds (in flight)
-// the wave's first segment of p; on exit A holds (in flight) the first segment
-// of `pn` (when pn is set).  Only A is live outside this function, so the
-// attention phase and the staging code have the registers of B to
-// themselves.  Returns with LDS `red` holding every finished row of the
-// workgroup (after a workgroup barrier).
+// the wave's first segment of p (issued by stage_vec).  Only A is live
+// outside this function.  Returns with LDS `red` holding every finished row
+// of the workgroup (after a workgroup barrier).
 template <bool Q8, int NB>
-__device__ __forceinline__ void p_stream(PGp p, const PGeom& g, PGp pn, const PGeom& gn,
-                                         PChunk<Q8> (&A)[NB], const float* xs, float* red) {
+__device__ __forceinline__ void p_stream(PGp p, const PGeom& g, PChunk<Q8> (&A)[NB],
+                                         const float* xs, float* red) {
   PChunk<Q8> B[NB];
   const int nb = g.n_items;
   PCur ci{1, 1 / p->nsegw, 1 % p->nsegw};  // issue cursor: segment 1
@@ -504,12 +540,6 @@ __device__ __forceinline__ void p_stream(PGp p, const PGeom& g, PGp pn, const PG
     }
   }
   float acc = 0.f;
-  auto next_phase = [&]() {
-    if (pn) {
-      PCur c0{0, 0, 0};
-      p_seg_issue<Q8, NB>(pn, gn, c0, A);
-    }
-  };
   for (int b = 0; b < nb; b += 2) {
     // segment b is in A
     if (b + 1 < nb) {
@@ -520,13 +550,9 @@ __device__ __forceinline__ void p_stream(PGp p, const PGeom& g, PGp pn, const PG
       break;
     }
     // segment b + 1 is in B; A is free
-    if (b + 2 < nb)
-      p_seg_issue<Q8, NB>(p, g, ci, A);
-    else
-      next_phase();
+    if (b + 2 < nb) p_seg_issue<Q8, NB>(p, g, ci, A);
     p_seg_compute<Q8, NB>(p, g, cc, B, xs, xr, xreg, red, acc);
   }
-  if (nb % 2 == 1 || nb == 0) next_phase();
   __syncthreads();
 }
 
@@ -541,8 +567,9 @@ __device__ __forceinline__ float p_row_total(int ks, const float* red, int lr) {
 // Attention phase (semantics of kernels/cpu/mha_kernel.cpp:5-61, with the
 // optional Qwen3 per-head q/k RMSNorm (model/qwen3.cpp:485-500) and RoPE
 // (kernels/cpu/rope_kernel.cpp) applied first).  One item = (kv head, chunk
-// of PT positions); items are spread over the workgroups; the last chunk of a
-// kv head to finish merges the chunks.  Rows before pos come from the cache
+// of PT positions); items are spread over the workgroups; every chunk writes
+// its partial (o, m, l) as tagged values and the workgroup that owns chunk 0
+// of the kv head merges them.  Rows before pos come from the cache
 // (written by earlier launches); q and the new K/V rows come from the tagged
 // QKV outputs.  The chunk that holds pos writes the transformed K row to the
 // cache for later tokens.  LDS floats needed: attn_p_lds_floats.
@@ -558,21 +585,71 @@ __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul, int G) {
   return head + (pv > merge ? pv : merge);
 }
 
+// What the attention of a layer needs that does not depend on the layer's
+// QKV output: this workgroup's first chunk of cached K and V rows, and the
+// Qwen3 q/k norm weights it applies.  Loaded at the start of the QKV phase, so
+// the loads complete while the QKV weights stream instead of queueing behind
+// the next phase's prefetch when attention starts.
+template <int HD>
+struct AttnPre {
+  static constexpr int NP = attn_chunk(HD) / attn_p_rpp(HD);
+  static constexpr int NW = HD >= kWave ? HD / kWave : 1;
+  f4 kr[NP], vr[NP];
+  float qn[NW], kn[NW];
+};
+
+template <int HD>
+__device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, int pos,
+                                              AttnPre<HD>& pre) {
+  constexpr int PT = attn_chunk(HD);
+  constexpr int TPR = HD / 4;
+  constexpr int RPP = attn_p_rpp(HD);
+  constexpr int NP = AttnPre<HD>::NP;
+  const KL_CAS PAttn* at = (const KL_CAS PAttn*)(atp);
+  const int n = pos + 1;
+  const int nsplit = (n + PT - 1) / PT;
+  const int it = blockIdx.x;
+  if (it >= a.KVH * nsplit) return;
+  const int g = it / nsplit;
+  const int s = it - g * nsplit;
+  const int t0 = s * PT;
+  const int cnt = min(n - t0, PT);
+  const int sub = threadIdx.x % TPR, rr = threadIdx.x / TPR;
+  const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
+  const float* kcache = at->kcache;
+  const float* vcache = at->vcache;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int tt = p * RPP + rr;
+    const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);  // row pos comes from QKV
+    const size_t off = static_cast<size_t>(t) * a.Dkv + col;
+    pre.kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
+    pre.vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
+  }
+  if (a.transform == 2) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+      const int d = lane + k * kWave;
+      pre.qn[k] = d < HD ? g_rd(at->qn + d) : 0.f;
+      pre.kn[k] = d < HD ? g_rd(at->kn + d) : 0.f;
+    }
+  }
+}
+
 template <int HD>
 __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, int pos,
-                                             unsigned int tag, float* lds) {
+                                             unsigned int tag, float* lds, int trace_slot,
+                                             const AttnPre<HD>& pre, float rope_c, float rope_s) {
   constexpr int PT = attn_chunk(HD);
   constexpr int TPR = HD / 4;
   constexpr int RPP = attn_p_rpp(HD);
   constexpr int NP = PT / RPP;
   constexpr int HALF = HD / 2;
   static_assert(NP >= 1 && NP * RPP == PT, "chunk geometry");
-  __shared__ int s_last;
   const KL_CAS PAttn* at = (const KL_CAS PAttn*)(atp);
   float* kcache = at->kcache;
   const float* vcache = at->vcache;
-  const float* qn = at->qn;
-  const float* kn = at->kn;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -598,7 +675,13 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     // 1. The chunk's cached K and V rows into registers (row pos is replaced
     //    below by the new row).
     f4 kr[NP], vr[NP];
-    {
+    if (it == static_cast<int>(blockIdx.x)) {  // loaded by attn_prefetch
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        kr[p] = pre.kr[p];
+        vr[p] = pre.vr[p];
+      }
+    } else {
       const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
@@ -620,26 +703,35 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
       }
     }
     __syncthreads();
+    if (it == static_cast<int>(blockIdx.x)) trace_mark(a, trace_slot);  // inputs arrived
     if (a.transform == 2) {
       for (int h = wave; h < kvm; h += kPWaves) {
         float ss = 0.f;
         for (int d = lane; d < HD; d += kWave) ss += qs[h * HD + d] * qs[h * HD + d];
         ss = wave_sum(ss);
         const float r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
-        for (int d = lane; d < HD; d += kWave) qs[h * HD + d] = (r * qs[h * HD + d]) * g_rd(qn + d);
+#pragma unroll
+        for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+          const int d = lane + k * kWave;
+          if (d < HD) qs[h * HD + d] = (r * qs[h * HD + d]) * pre.qn[k];
+        }
       }
       if (own_pos && wave == kPWaves - 1) {
         float ss = 0.f;
         for (int d = lane; d < HD; d += kWave) ss += kp[d] * kp[d];
         ss = wave_sum(ss);
         const float r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
-        for (int d = lane; d < HD; d += kWave) kp[d] = (r * kp[d]) * g_rd(kn + d);
+#pragma unroll
+        for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+          const int d = lane + k * kWave;
+          if (d < HD) kp[d] = (r * kp[d]) * pre.kn[k];
+        }
       }
       __syncthreads();
     }
     if (a.transform >= 1) {
-      const float* srow = a.sin_t + static_cast<size_t>(pos) * HD;
-      const float* crow = a.cos_t + static_cast<size_t>(pos) * HD;
+      // Every pair this thread rotates has j = tid % HALF (512 is a multiple
+      // of HALF), whose table entries rope_c / rope_s the kernel loaded once.
       const int heads = own_pos ? kvm + 1 : kvm;  // head kvm = the new K row
       for (int p = tid; p < heads * HALF; p += kPThreads) {
         const int h = p / HALF, j = p - h * HALF;
@@ -647,7 +739,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         const int i0 = a.rope_style ? j : 2 * j;
         const int i1 = a.rope_style ? j + HALF : 2 * j + 1;
         float v0 = v[i0], v1 = v[i1];
-        rope_pair(v0, v1, g_rd(crow + 2 * j), g_rd(srow + 2 * j));
+        rope_pair(v0, v1, rope_c, rope_s);
         v[i0] = v0;
         v[i1] = v1;
       }
@@ -676,8 +768,8 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         for (int h = 0; h < kAttnMaxKvMul; ++h) {
           if (h < kvm) {
             float d = hsum(kr[p] * q4[h * TPR + sub]);
-            d = group_sum(d, TPR);
-            if (sub == 0 && tt < cnt) sc[h * PT + tt] = d * a.scale;
+            d = group_sum_dpp<TPR>(d);
+            if (sub == TPR - 1 && tt < cnt) sc[h * PT + tt] = d * a.scale;
           }
         }
       }
@@ -688,14 +780,14 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
       float* sh = sc + h * PT;
       float m = -INFINITY;
       for (int tt = lane; tt < cnt; tt += kWave) m = fmaxf(m, sh[tt]);
-      m = wave_max(m);
+      m = wave_max_dpp(m);
       float l = 0.f;
       for (int tt = lane; tt < cnt; tt += kWave) {
         const float e = expf(sh[tt] - m);
         sh[tt] = e;
         l += e;
       }
-      l = wave_sum(l);
+      l = wave_sum_dpp(l);
       if (lane == 0) {
         ml[2 * h] = m;
         ml[2 * h + 1] = l;
@@ -717,55 +809,68 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     }
     __syncthreads();
     tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
-    float* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
+    tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
+    // Row slots summed in two halves (threads idx and idx + 256 of a pair of
+    // outputs), then combined through LDS.
+    {
+      const int half = tid >= kPThreads / 2;
+      for (int idx = tid - half * (kPThreads / 2); idx < kvm * HD; idx += kPThreads / 2) {
+        const int h = idx / HD, d = idx - h * HD;
+        float o = 0.f;
+#pragma unroll 8
+        for (int k = half * (RPP / 2); k < (half + 1) * (RPP / 2); ++k)
+          o += red[(static_cast<size_t>(k) * kvm + h) * HD + d];
+        if (half) red[(static_cast<size_t>(RPP / 2) * kvm + h) * HD + d] = o;  // slot RPP/2: upper sum
+        else red[(static_cast<size_t>(0) * kvm + h) * HD + d] = o;             // slot 0: lower sum
+      }
+    }
+    __syncthreads();
     for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
       const int h = idx / HD, d = idx - h * HD;
-      float o = 0.f;
-      for (int k = 0; k < RPP; ++k) o += red[(static_cast<size_t>(k) * kvm + h) * HD + d];
+      const float o = red[(static_cast<size_t>(0) * kvm + h) * HD + d] +
+                      red[(static_cast<size_t>(RPP / 2) * kvm + h) * HD + d];
       if (nsplit == 1) {
         g_st_tagged(outg + h * HD + d, o / ml[2 * h + 1], tag);
       } else {
-        float* ps = pg + (static_cast<size_t>(s) * kvm + h) * (HD + 2);
-        g_st(ps + d, o);
+        tagged_t* ps = pg + (static_cast<size_t>(s) * kvm + h) * (HD + 2);
+        g_st_tagged(ps + d, o, tag);
         if (d == 0) {
-          g_st(ps + HD, ml[2 * h]);
-          g_st(ps + HD + 1, ml[2 * h + 1]);
+          g_st_tagged(ps + HD, ml[2 * h], tag);
+          g_st_tagged(ps + HD + 1, ml[2 * h + 1], tag);
         }
-      }
-    }
-    if (nsplit > 1) {
-      wait_mem();
-      __syncthreads();
-      if (tid == 0) {
-        const unsigned int prev = g_arrive(a.attn_cnt + g);
-        s_last = prev == static_cast<unsigned int>(nsplit - 1) ? 1 : 0;
-      }
-      __syncthreads();
-      if (s_last) {
-        // 6. Merge the chunks of this kv head.
-        float* mls = red;  // [nsplit][kvm][2]
-        for (int i = tid; i < nsplit * kvm; i += kPThreads) {
-          const float* pk = pg + static_cast<size_t>(i) * (HD + 2);
-          mls[2 * i] = g_ld(pk + HD);
-          mls[2 * i + 1] = g_ld(pk + HD + 1);
-        }
-        __syncthreads();
-        for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
-          const int h = idx / HD, d = idx - h * HD;
-          float M = -INFINITY;
-          for (int k = 0; k < nsplit; ++k) M = fmaxf(M, mls[2 * (k * kvm + h)]);
-          float L = 0.f, O = 0.f;
-          for (int k = 0; k < nsplit; ++k) {
-            const float w = expf(mls[2 * (k * kvm + h)] - M);
-            L += mls[2 * (k * kvm + h) + 1] * w;
-            O += g_ld(pg + (static_cast<size_t>(k) * kvm + h) * (HD + 2) + d) * w;
-          }
-          g_st_tagged(outg + h * HD + d, O / L, tag);
-        }
-        if (tid == 0) g_st(a.attn_cnt + g, 0u);
       }
     }
     __syncthreads();  // LDS is reused by the next item
+  }
+  if (nsplit == 1) return;
+  // 6. The workgroup that owns chunk 0 of a kv head merges its chunks, once all
+  //    of this workgroup's own chunks are written (so it never waits on itself):
+  //    O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    const int g = it / nsplit;
+    if (it - g * nsplit != 0) continue;
+    const tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
+    float* mls = lds;  // [nsplit][kvm][2]
+    for (int i = tid; i < nsplit * kvm; i += kPThreads) {
+      const tagged_t* pk = pg + static_cast<size_t>(i) * (HD + 2);
+      mls[2 * i] = poll_tagged(a, pk + HD, tag);
+      mls[2 * i + 1] = poll_tagged(a, pk + HD + 1, tag);
+    }
+    __syncthreads();
+    tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
+    for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
+      const int h = idx / HD, d = idx - h * HD;
+      float M = -INFINITY;
+      for (int k = 0; k < nsplit; ++k) M = fmaxf(M, mls[2 * (k * kvm + h)]);
+      float L = 0.f, O = 0.f;
+      for (int k = 0; k < nsplit; ++k) {
+        const float w = expf(mls[2 * (k * kvm + h)] - M);
+        L += mls[2 * (k * kvm + h) + 1] * w;
+        O += poll_tagged(a, pg + (static_cast<size_t>(k) * kvm + h) * (HD + 2) + d, tag) * w;
+      }
+      g_st_tagged(outg + h * HD + d, O / L, tag);
+    }
+    __syncthreads();
   }
 }
 
@@ -834,13 +939,19 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   float* xres = lds + a.xres_off;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int slot = 0;
+  // RoPE table entries of this launch's position (every pair a thread
+  // rotates has j = tid % (HD / 2)).
+  float rope_c = 1.f, rope_s = 0.f;
+  if (a.transform >= 1) {
+    const int j = threadIdx.x % (HD / 2);
+    rope_c = g_rd(a.cos_t + static_cast<size_t>(pos) * HD + 2 * j);
+    rope_s = g_rd(a.sin_t + static_cast<size_t>(pos) * HD + 2 * j);
+  }
+  AttnPre<HD> pre;
   trace_mark(a, slot++);
 
   PChunk<Q8> A[NB];
   {
-    const PGeom g0 = p_geom(ph);
-    PCur c0{0, 0, 0};
-    p_seg_issue<Q8, NB>(ph, g0, c0, A);
     // This workgroup's rows of the residual stream start as the embedding row.
     const PGeom gr = p_geom(ph + 1);
     for (int lr = threadIdx.x; lr < gr.nloc; lr += kPThreads) xres[lr] = g_rd(emb_row + gr.base + lr);
@@ -850,15 +961,18 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   for (int k = 0; k <= ncls; ++k) {
     const PGp p = ph + k;
     const bool is_cls = k == ncls;
-    // The next GEMV phase (its first loads are issued before this phase ends).
+    // The next GEMV phase (none after the last layer of a prompt position).
     const PGp pn = k + 1 < ncls ? ph + k + 1 : (k + 1 == ncls && sample ? ph + ncls : nullptr);
     const PGeom g = p_geom(p);
-    const PGeom gn = pn ? p_geom(pn) : PGeom{};
     const unsigned int tag_in = epoch * kTagLayers + p->in_layer + 1;
     const unsigned int tag = epoch * kTagLayers + p->layer + 1;
-    stage_vec(a, p->in, tag_in, emb_row, p->norm, a.eps, p->cols, xs, sred);
+    if ((k & 3) == 0 && !is_cls) attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
+    stage_vec(a, p->in, tag_in, emb_row, p->norm, a.eps, p->cols, xs, sred, [&]() {
+      PCur c0{0, 0, 0};
+      p_seg_issue<Q8, NB>(p, g, c0, A);
+    });
     trace_mark(a, slot++);
-    p_stream<Q8, NB>(p, g, pn, gn, A, xs, red);
+    p_stream<Q8, NB>(p, g, A, xs, red);
     if (is_cls) {
       // Logits (plain stores, read by the host after the launch) and this
       // workgroup's (max, first index) pair (sampler/argmax_sampler.cpp:5-13).
@@ -888,8 +1002,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     trace_mark(a, slot++);
     if (!pn) break;  // last layer of a prompt position: no classifier
     if ((k & 3) == 0) {  // after QKV: attention of layer k / 4
-      attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds);
-      trace_mark(a, slot++);
+      if (static_cast<int>(blockIdx.x) >= a.KVH * ((pos + attn_chunk(HD)) / attn_chunk(HD)))
+        trace_mark(a, slot);  // no attention item: "inputs arrived" = now
+      attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds, slot, pre, rope_c, rope_s);
+      ++slot;
       trace_mark(a, slot++);
     }
   }
