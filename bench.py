@@ -25,6 +25,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -44,6 +45,28 @@ def dominant_kernel_bytes(cfg) -> int:
     else:
         w = 2 * F * D * 4
     return w + 2 * D * 4 + F * 4
+
+
+def measured_traffic(kernel: str, config: str, mode: str):
+    """HBM bytes per launch of `kernel` on `config` in `mode`, as recorded by
+    the rocprofv3 PMC summaries under profiles/ (FETCH_SIZE + WRITE_SIZE,
+    calibrated against a copy kernel of known size).  The counters cannot be
+    read in the same run as the timing, so the figure comes from those
+    committed runs of this same command; None when no summary covers it."""
+    pat = re.compile(r"measured: kernel=(\S+) config=(\S+) mode=(\S+) "
+                     r"traffic_bytes_per_launch=(\d+)")
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None, None
+    for name in sorted(os.listdir(pdir)):
+        if not name.endswith("_pmc.txt"):
+            continue
+        with open(os.path.join(pdir, name)) as f:
+            for line in f:
+                m = pat.search(line)
+                if m and m.group(1) == kernel and m.group(2) == config and m.group(3) == mode:
+                    return int(m.group(4)), "profiles/" + name
+    return None, None
 
 
 def cpu_baseline(K, cfg, img, seconds: float) -> dict:
@@ -156,6 +179,8 @@ def main() -> int:
         dom_ms = prof["w13"][0]
         dom_bytes = dominant_kernel_bytes(cfg)
     dom_gbps = dom_bytes / (dom_ms / 1e3) / 1e9
+    traffic, traffic_src = measured_traffic("k_decode_persistent" if persistent else "k_w13_swiglu",
+                                            cfg.name, "persistent" if persistent else "multi")
     print("# per-launch avg ms: " + ", ".join(f"{k} {v[0]:.4f} x{v[1]}" for k, v in prof.items() if v[1])
           + f"; step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
 
@@ -187,6 +212,8 @@ def main() -> int:
             "parallelism": "single GPU",
             "mode": "persistent" if persistent else "multi",
             "graph": (not args.no_graph) and not persistent,
+            "launch": ("cooperative" if os.environ.get("KL_PERSISTENT_LAUNCH") == "cooperative"
+                       else "plain") if persistent else "stream",
         },
         "achieved_GBps": round(gbps, 1),
         "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
@@ -198,7 +225,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "bytes_per_launch": int(dom_bytes),
             "avg_launch_ms": round(dom_ms, 5),
         },

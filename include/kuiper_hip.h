@@ -205,7 +205,11 @@ int kl_engine_set_graph(kl_engine* e, int enable);
  * device can hold one 512-thread workgroup per CU): one cooperative launch per
  * token runs every layer; workgroups hand activations to each other through
  * tagged stores (no grid barriers) and issue each phase's first weight loads
- * before they wait for its input.  KL_MODE_MULTI: 5 kernels per layer plus the
+ * before they wait for its input.  The grid (one workgroup per CU) is launched
+ * with hipLaunchKernel where the occupancy query shows it co-resident, else
+ * cooperatively; every device-side wait is bounded and a timeout surfaces as
+ * KL_EDEVICE (environment KL_PERSISTENT_LAUNCH=cooperative forces the
+ * cooperative launch).  KL_MODE_MULTI: 5 kernels per layer plus the
  * classifier, replayed as a HIP graph (kl_engine_set_graph).
  * Both modes compute the same step; setting KL_MODE_PERSISTENT where it does
  * not fit returns KL_EUNSUPP. */

@@ -1,0 +1,196 @@
+// Models of the host API: Model (the reference's include/model/model.h:14-94)
+// and LLama2Model / Qwen2Model / Qwen3Model (include/model/llama3.h:33-74,
+// qwen2.h:42-87, qwen3.h:48-89).  init(kDeviceHIP) mmaps a reference-format
+// .bin file, wraps the weights as layers and moves them to the device;
+// predict() runs the reference's layer-by-layer forward on the HIP kernels.
+// set_fused(true) runs predict() on the fused decode engine of the C ABI
+// (kl_engine_*) instead, from the same mapped file.
+//
+// Differences from the reference, by design:
+//  * the model family (RoPE pairing and theta, RMSNorm eps, Qwen2 bias, Qwen3
+//    q/k norm, header size) is a constructor argument instead of a build flag;
+//  * the tokenizer is optional: prompts are token ids (encode/decode report
+//    that no tokenizer is loaded);
+//  * kDeviceCPU is refused: the CPU kernels are the reference's own.
+#pragma once
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kuiper/hip_config.h"
+#include "kuiper/kernels.h"
+#include "kuiper/layer.h"
+#include "kuiper/tensor.h"
+
+struct kl_engine;
+
+namespace model {
+
+enum class ModelFamily : int32_t {
+  kLlama2 = 0,  // interleaved RoPE, theta 1e4, eps 1e-5 (no build flag)
+  kLlama3 = 1,  // rotate-half RoPE, theta 5e5, eps 1e-5 (LLAMA3_SUPPORT)
+  kQwen2 = 2,   // rotate-half, theta 1e6, eps 1e-6, q/k/v bias (QWEN2_SUPPORT)
+  kQwen3 = 3,   // rotate-half, theta 1e6, eps 1e-6, per-head q/k RMSNorm (QWEN3_SUPPORT)
+};
+
+// The .bin header (include/model/config.h:4-15): 7 int32, plus the group size
+// for int8 images; Qwen3 images carry 8 int32 {q_dim, dim, layers, heads,
+// kv_heads, vocab, seq_len, ffn_dim}.
+struct ModelConfig {
+  int32_t dim = 0;
+  int32_t hidden_dim = 0;
+  int32_t layer_num = 0;
+  int32_t head_num = 0;
+  int32_t kv_head_num = 0;
+  int32_t vocab_size = 0;
+  int32_t seq_len = 0;
+};
+
+// Derived sizes (model/model.cpp:113-141).  dim_ is the model width,
+// q_dim_ = head_num * head_size (equal to dim_ except Qwen3), hidden_dim_ the
+// FFN width.
+struct TransformerConfig {
+  int32_t kv_dim_ = 0;
+  int32_t kv_mul_ = 0;
+  int32_t head_size_ = 0;
+  int32_t vocab_size_ = 0;
+  int32_t dim_ = 0;
+  int32_t q_dim_ = 0;
+  int32_t hidden_dim_ = 0;
+  int32_t layer_num_ = 0;
+  int32_t head_num_ = 0;
+  int32_t kv_head_num_ = 0;
+  int32_t seq_len_ = 0;
+  bool is_shared_weight_ = false;
+};
+
+// A read-only mapping of the model file (model/raw_model_data.cpp).
+struct RawModelData {
+  int32_t fd = -1;
+  size_t file_size = 0;
+  void* data = nullptr;
+  const int8_t* weight_data = nullptr;  // first byte after the header
+  ~RawModelData();
+};
+
+struct DecoderLayers {
+  std::shared_ptr<op::Layer> add_layer_, rope_layer_, swiglu_layer_, mha_layer_;
+  std::vector<std::shared_ptr<op::Layer>> wq_layers_, wk_layers_, wv_layers_, wo_layers_;
+  std::vector<std::shared_ptr<op::Layer>> w1_layers_, w2_layers_, w3_layers_;
+  // 0..L-1 attention norms, L..2L-1 FFN norms, 2L the final norm; Qwen3:
+  // 2L+1..3L q norms, 3L+1..4L k norms.
+  std::vector<std::shared_ptr<op::Layer>> rmsnorm_layers_;
+  std::shared_ptr<op::Layer> cls_layer_, embedding_layer_;
+  void to_hip(const std::shared_ptr<kernel::HipConfig>& config);
+};
+
+class Model {
+ public:
+  explicit Model(base::TokenizerType tokenizer_type, base::ModelType model_type,
+                 std::string token_path, std::string model_path, bool is_quant_model,
+                 ModelFamily family);
+  virtual ~Model();
+
+  base::Status init(base::DeviceType device_type);
+  // One token: forward() then, unless is_prompt, greedy sampling into next
+  // (-1 for prompt positions), as llama3.cpp:641-649.
+  base::Status predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                       bool is_prompt, int& next) const;
+  base::Status forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                       int& next) const;
+
+  base::ModelType model_type() const { return model_type_; }
+  ModelFamily family() const { return family_; }
+  const std::string& token_path() const { return token_path_; }
+  const std::string& model_path() const { return model_path_; }
+  const TransformerConfig& config() const { return *config_; }
+  tensor::Tensor& get_buffer(ModelBufferType buffer_idx);
+  const tensor::Tensor& get_buffer(ModelBufferType buffer_idx) const;
+
+  bool is_sentence_ending(int32_t token_idx) const;
+  std::string decode(int32_t token_idx) const;
+  std::string decode(std::vector<int32_t> token_idxs) const;
+  std::vector<int32_t> encode(const std::string& sentence) const;
+
+  // K and V cache rows of (layer, position) as device tensors [kv_dim].
+  std::pair<tensor::Tensor, tensor::Tensor> slice_kv_cache(int32_t layer_idx,
+                                                           int32_t token_pos) const;
+  // Embeds tokens (all at once) into kInputEmbeddings.
+  op::EmbeddingOutput embedding(const std::vector<int>& tokens) const;
+  // The residual-stream input of a step: row pos of the prompt embeddings
+  // (is_prompt) or row 0 (the single decoded token), as model.cpp:240-265.
+  tensor::Tensor fill_input(const tensor::Tensor& pos_tensor,
+                            const op::EmbeddingOutput& embedding_output, bool is_prompt) const;
+
+  // Fused decode engine (one persistent launch per token); predict() uses it
+  // when enabled.  The engine is created on first use from the mapped file.
+  base::Status set_fused(bool enable);
+  bool is_fused() const { return fused_; }
+  // The greedy loop of demo/main.cpp:5-47: P prompt tokens, then n_new
+  // sampled tokens written to out (fused: entirely on the device).
+  base::Status generate(const std::vector<int32_t>& prompt, int32_t n_new,
+                        std::vector<int32_t>& out) const;
+  std::shared_ptr<kernel::HipConfig> hip_config() const { return hip_config_; }
+
+ protected:
+  base::Status insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor);
+  base::Status read_model_file();
+  base::Status generate_model_infos(const ModelConfig& config, int32_t extra);
+  base::Status create_layers();
+  void create_param_layers();
+  void create_param_quant_layers();
+  void create_nonparam_layers();
+  void init_mem();
+  void attention_rms(int32_t layer_idx, const tensor::Tensor& input) const;
+  void attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const;
+  void attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const;
+  void feed_forward(int32_t layer_idx, const tensor::Tensor& input) const;
+  void cls_logits(const tensor::Tensor& input) const;
+  int32_t post_processing(const tensor::Tensor& pos, bool is_prompt) const;
+
+  int32_t group_size_ = 1;
+  bool is_quant_model_ = false;
+  ModelFamily family_ = ModelFamily::kLlama2;
+  std::unique_ptr<TransformerConfig> config_;
+  std::string token_path_;
+  std::string model_path_;
+  std::map<ModelBufferType, tensor::Tensor> buffers_;
+  std::unique_ptr<sampler::Sampler> sampler_;
+  std::shared_ptr<RawModelData> raw_model_data_;
+  base::DeviceType device_type_ = base::DeviceType::kDeviceUnknown;
+  base::ModelType model_type_ = base::ModelType::kModelTypeUnknown;
+  base::TokenizerType tokenizer_type_ = base::TokenizerType::kEncodeUnknown;
+  std::shared_ptr<kernel::HipConfig> hip_config_;
+  std::unique_ptr<DecoderLayers> layers_;
+  bool fused_ = false;
+  kl_engine* engine_ = nullptr;
+};
+
+// Llama2 (default) and Llama3 (family kLlama3) checkpoints.
+class LLama2Model : public Model {
+ public:
+  explicit LLama2Model(base::TokenizerType tokenizer_type, std::string token_path,
+                       std::string model_path, bool is_quant_model,
+                       ModelFamily family = ModelFamily::kLlama2)
+      : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
+              std::move(model_path), is_quant_model, family) {}
+};
+
+class Qwen2Model : public Model {
+ public:
+  explicit Qwen2Model(base::TokenizerType tokenizer_type, std::string token_path,
+                      std::string model_path, bool is_quant_model)
+      : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
+              std::move(model_path), is_quant_model, ModelFamily::kQwen2) {}
+};
+
+class Qwen3Model : public Model {
+ public:
+  explicit Qwen3Model(base::TokenizerType tokenizer_type, std::string token_path,
+                      std::string model_path, bool is_quant_model)
+      : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
+              std::move(model_path), is_quant_model, ModelFamily::kQwen3) {}
+};
+
+}  // namespace model

@@ -1,0 +1,682 @@
+// Model, the layer-by-layer decode step on the HIP kernels, and the fused
+// path on the persistent decode engine (the reference's source/model/
+// {model,llama3,qwen2,qwen3}.cpp and demo/main.cpp, for kDeviceHIP).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "kuiper/model.h"
+#include "kuiper_hip.h"
+
+namespace model {
+
+RawModelData::~RawModelData() {
+  if (data != nullptr && data != MAP_FAILED) munmap(data, file_size);
+  if (fd != -1) close(fd);
+}
+
+void DecoderLayers::to_hip(const std::shared_ptr<kernel::HipConfig>& config) {
+  auto move = [&](const std::shared_ptr<op::Layer>& layer) {
+    if (!layer) return;
+    layer->set_hip_config(config);
+    layer->to_hip();
+  };
+  move(add_layer_);
+  move(rope_layer_);
+  move(swiglu_layer_);
+  move(mha_layer_);
+  move(cls_layer_);
+  move(embedding_layer_);
+  for (auto* group : {&wq_layers_, &wk_layers_, &wv_layers_, &wo_layers_, &w1_layers_,
+                      &w2_layers_, &w3_layers_, &rmsnorm_layers_})
+    for (auto& layer : *group) move(layer);
+}
+
+namespace {
+kernel::KernelTraits traits_of(ModelFamily family) {
+  kernel::KernelTraits t;
+  switch (family) {
+    case ModelFamily::kLlama2: t.rope_style = KL_ROPE_INTERLEAVED; t.rope_theta = 1e4f; t.rms_eps = 1e-5f; break;
+    case ModelFamily::kLlama3: t.rope_style = KL_ROPE_HALF; t.rope_theta = 5e5f; t.rms_eps = 1e-5f; break;
+    case ModelFamily::kQwen2:
+    case ModelFamily::kQwen3: t.rope_style = KL_ROPE_HALF; t.rope_theta = 1e6f; t.rms_eps = 1e-6f; break;
+  }
+  t.rms_dim_eps = 1e-6f;
+  return t;
+}
+}  // namespace
+
+Model::Model(base::TokenizerType tokenizer_type, base::ModelType model_type,
+             std::string token_path, std::string model_path, bool is_quant_model,
+             ModelFamily family)
+    : is_quant_model_(is_quant_model),
+      family_(family),
+      token_path_(std::move(token_path)),
+      model_path_(std::move(model_path)),
+      model_type_(model_type),
+      tokenizer_type_(tokenizer_type) {}
+
+Model::~Model() {
+  if (engine_) kl_engine_destroy(engine_);
+  engine_ = nullptr;
+  // Layers and buffers release their device memory before the stream goes.
+  layers_.reset();
+  buffers_.clear();
+  sampler_.reset();
+}
+
+// llama3.cpp:111-145 for kDeviceHIP.  The tokenizer is optional (token ids in
+// and out), so an empty token_path is accepted.
+base::Status Model::init(base::DeviceType device_type) {
+  if (device_type != base::DeviceType::kDeviceHIP)
+    return base::error::InvalidArgument(
+        "This backend runs on kDeviceHIP only; the CPU and CUDA paths are the reference's.");
+  if (is_quant_model_ && family_ != ModelFamily::kLlama2 && family_ != ModelFamily::kLlama3)
+    return base::error::InvalidArgument("int8 images exist for the Llama layouts only.");
+  device_type_ = device_type;
+  // The file is parsed and sized before any device work, so a bad path or
+  // image is reported without touching the GPU.
+  base::Status s = read_model_file();
+  if (!s) return s;
+  s = create_layers();
+  if (!s) return s;
+  if (kl_set_device(0) != KL_OK) return base::error::InternalError("kl_set_device(0) failed.");
+  hip_config_ = std::make_shared<kernel::HipConfig>();
+  if (hip_config_->create() != KL_OK)
+    return base::error::InternalError("The HIP stream could not be created.");
+  kernel::set_kernel_traits(traits_of(family_));
+  init_mem();
+  kernel::sin_cos_cache_calc_hip(config_->head_size_, config_->seq_len_,
+                                 get_buffer(ModelBufferType::kSinCache),
+                                 get_buffer(ModelBufferType::kCosCache));
+  sampler_ = std::make_unique<sampler::ArgmaxSampler>(device_type_);
+  return base::error::Success();
+}
+
+// model.cpp:41-111: header, optional group size, then mmap of the whole file.
+// Qwen3 images carry an eighth header int (the FFN width).
+base::Status Model::read_model_file() {
+  if (model_path_.empty())
+    return base::error::PathNotValid("Failed to open the weight file, the model path is empty!");
+  auto raw = std::make_shared<RawModelData>();
+  raw->fd = open(model_path_.c_str(), O_RDONLY);
+  if (raw->fd == -1)
+    return base::error::PathNotValid("Failed to open the weight file " + model_path_ +
+                                     " may be the path does not exist!");
+  struct stat st;
+  if (fstat(raw->fd, &st) == -1)
+    return base::error::ModelParseError("Failed to retrieve the file size of " + model_path_);
+  raw->file_size = static_cast<size_t>(st.st_size);
+  const bool qwen3 = family_ == ModelFamily::kQwen3;
+  const size_t header_ints = 7 + ((qwen3 || is_quant_model_) ? 1 : 0);
+  if (raw->file_size < header_ints * sizeof(int32_t))
+    return base::error::ModelParseError(
+        "Failed to retrieve the configuration information from the model file.");
+  raw->data = mmap(nullptr, raw->file_size, PROT_READ, MAP_PRIVATE, raw->fd, 0);
+  if (raw->data == MAP_FAILED || raw->data == nullptr) {
+    raw->data = nullptr;
+    return base::error::ModelParseError("Failed to map the weight file " + model_path_ +
+                                        " into memory.");
+  }
+  const int32_t* h = static_cast<const int32_t*>(raw->data);
+  ModelConfig config;
+  config.dim = h[0];
+  config.hidden_dim = h[1];
+  config.layer_num = h[2];
+  config.head_num = h[3];
+  config.kv_head_num = h[4];
+  config.vocab_size = h[5];
+  config.seq_len = h[6];
+  int32_t extra = 0;
+  if (is_quant_model_) group_size_ = h[7];
+  if (qwen3) extra = h[7];
+  base::Status s = generate_model_infos(config, extra);
+  if (!s) return s;
+  if (is_quant_model_ && group_size_ <= 0)
+    return base::error::ModelParseError(
+        "Failed to retrieve the group size information from the model file.");
+  raw->weight_data = static_cast<const int8_t*>(raw->data) + header_ints * sizeof(int32_t);
+  raw_model_data_ = raw;
+  return base::error::Success();
+}
+
+// model.cpp:113-141 (Qwen3: qwen3.cpp's header {q_dim, dim, ..., ffn}).
+base::Status Model::generate_model_infos(const ModelConfig& c, int32_t extra) {
+  if (c.dim <= 0 || c.hidden_dim <= 0 || c.layer_num <= 0 || c.head_num <= 0 ||
+      c.kv_head_num <= 0 || c.vocab_size == 0 || c.seq_len <= 0 || c.dim % c.head_num != 0 ||
+      c.head_num % c.kv_head_num != 0)
+    return base::error::ModelParseError("The model header is not valid.");
+  auto cfg = std::make_unique<TransformerConfig>();
+  cfg->layer_num_ = c.layer_num;
+  cfg->head_num_ = c.head_num;
+  cfg->kv_head_num_ = c.kv_head_num;
+  cfg->seq_len_ = c.seq_len;
+  cfg->head_size_ = c.dim / c.head_num;
+  cfg->kv_dim_ = c.dim * c.kv_head_num / c.head_num;
+  cfg->kv_mul_ = c.head_num / c.kv_head_num;
+  cfg->q_dim_ = c.dim;
+  if (family_ == ModelFamily::kQwen3) {
+    if (extra <= 0) return base::error::ModelParseError("The Qwen3 FFN width is not valid.");
+    cfg->dim_ = c.hidden_dim;  // the model width
+    cfg->hidden_dim_ = extra;  // the FFN width
+    cfg->is_shared_weight_ = false;
+  } else {
+    cfg->dim_ = c.dim;
+    cfg->hidden_dim_ = c.hidden_dim;
+    cfg->is_shared_weight_ = c.vocab_size > 0;
+  }
+  cfg->vocab_size_ = std::abs(c.vocab_size);
+  config_ = std::move(cfg);
+  return base::error::Success();
+}
+
+// Walks the weight region in file order (llama3.cpp:183-422, qwen2.cpp:348-485,
+// qwen3.cpp:186-299), wrapping each tensor as an external CPU weight.
+void Model::create_param_layers() {
+  const auto& c = *config_;
+  const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+                V = c.vocab_size_, hd = c.head_size_;
+  const auto cpu = base::DeviceType::kDeviceCPU;
+  const auto dev = device_type_;
+  const float* p = reinterpret_cast<const float*>(raw_model_data_->weight_data);
+  auto& ly = *layers_;
+  auto matmul = [&](int32_t rows, int32_t cols, bool bias = false) {
+    auto m = std::make_shared<op::MatmulLayer>(dev, rows, cols, false, bias);
+    m->set_weight(0, {rows, cols}, p, cpu);
+    p += static_cast<size_t>(rows) * cols;
+    if (bias) {
+      int32_t n = rows;
+      m->set_bias(0, n, p, cpu);
+      p += rows;
+    }
+    return m;
+  };
+  auto norm = [&](int32_t n) {
+    auto r = std::make_shared<op::RmsNormLayer>(dev, n);
+    r->set_weight(0, {n}, p, cpu);
+    p += n;
+    return r;
+  };
+  auto embedding = [&]() {
+    auto e = std::make_shared<op::EmbeddingLayer>(dev, D, c.seq_len_, V);
+    e->set_weight(0, {V, D}, p, cpu);
+    p += static_cast<size_t>(V) * D;
+    return e;
+  };
+
+  if (family_ == ModelFamily::kQwen3) {
+    for (int32_t i = 0; i < 2 * L + 1; ++i) ly.rmsnorm_layers_.push_back(norm(D));
+    ly.embedding_layer_ = embedding();
+    std::vector<std::shared_ptr<op::Layer>> qn, kn;
+    for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(matmul(Dq, D));
+    for (int32_t l = 0; l < L; ++l) qn.push_back(norm(hd));
+    for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(matmul(Dkv, D));
+    for (int32_t l = 0; l < L; ++l) kn.push_back(norm(hd));
+    for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(matmul(Dkv, D));
+    for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(matmul(D, Dq));
+    for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(matmul(F, D));
+    for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(matmul(D, F));
+    for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(matmul(F, D));
+    ly.cls_layer_ = matmul(V, D);
+    for (auto& x : qn) ly.rmsnorm_layers_.push_back(x);
+    for (auto& x : kn) ly.rmsnorm_layers_.push_back(x);
+    return;
+  }
+  const bool bias = family_ == ModelFamily::kQwen2;
+  ly.embedding_layer_ = embedding();
+  std::vector<std::shared_ptr<op::Layer>> att, ffn;
+  for (int32_t l = 0; l < L; ++l) att.push_back(norm(D));
+  for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(matmul(Dq, D, bias));
+  for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(matmul(Dkv, D, bias));
+  for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(matmul(Dkv, D, bias));
+  for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(matmul(D, Dq));
+  for (int32_t l = 0; l < L; ++l) ffn.push_back(norm(D));
+  for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(matmul(F, D));
+  for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(matmul(D, F));
+  for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(matmul(F, D));
+  auto final_norm = norm(D);
+  p += static_cast<size_t>(c.seq_len_) * hd;  // freq_cis_real + freq_cis_imag, unused
+  if (c.is_shared_weight_) {
+    auto cls = std::make_shared<op::MatmulLayer>(dev, V, D);
+    cls->set_weight(0, {V, D},
+                    std::static_pointer_cast<op::LayerParam>(ly.embedding_layer_)
+                        ->get_weight(0)
+                        .ptr<float>(),
+                    cpu);
+    ly.cls_layer_ = cls;
+  } else {
+    ly.cls_layer_ = matmul(V, D);
+  }
+  for (auto& x : att) ly.rmsnorm_layers_.push_back(x);
+  for (auto& x : ffn) ly.rmsnorm_layers_.push_back(x);
+  ly.rmsnorm_layers_.push_back(final_norm);
+}
+
+// llama3.cpp:183-287: int8 matrices, each followed by its fp32 group scales,
+// then the fp32 embedding and norm weights.
+void Model::create_param_quant_layers() {
+  const auto& c = *config_;
+  const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+                V = c.vocab_size_;
+  const auto cpu = base::DeviceType::kDeviceCPU;
+  const auto dev = device_type_;
+  const int8_t* p = raw_model_data_->weight_data;
+  auto& ly = *layers_;
+  auto qmatmul = [&](int32_t rows, int32_t cols) {
+    auto m = std::make_shared<op::MatmulLayer>(dev, rows, cols, true);
+    m->set_group_size(group_size_);
+    m->set_weight(0, {rows, cols}, p, cpu);
+    p += static_cast<size_t>(rows) * cols + m->get_scale_num() * sizeof(float);
+    return m;
+  };
+  for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(qmatmul(Dq, D));
+  for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(qmatmul(Dkv, D));
+  for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(qmatmul(Dkv, D));
+  for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(qmatmul(D, Dq));
+  for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(qmatmul(F, D));
+  for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(qmatmul(D, F));
+  for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(qmatmul(F, D));
+  ly.cls_layer_ = qmatmul(V, D);
+  const float* f = reinterpret_cast<const float*>(p);
+  auto emb = std::make_shared<op::EmbeddingLayer>(dev, D, c.seq_len_, V);
+  emb->set_weight(0, {V, D}, f, cpu);
+  f += static_cast<size_t>(V) * D;
+  ly.embedding_layer_ = emb;
+  for (int32_t i = 0; i < 2 * L + 1; ++i) {
+    auto r = std::make_shared<op::RmsNormLayer>(dev, D);
+    r->set_weight(0, {D}, f, cpu);
+    f += D;
+    ly.rmsnorm_layers_.push_back(r);
+  }
+}
+
+void Model::create_nonparam_layers() {
+  const auto& c = *config_;
+  auto& ly = *layers_;
+  ly.rope_layer_ = std::make_shared<op::RoPELayer>(device_type_, c.q_dim_, c.kv_dim_, c.head_size_);
+  ly.mha_layer_ = std::make_shared<op::MultiHeadAttention>(
+      device_type_, 0, c.kv_mul_, c.kv_dim_, c.seq_len_, c.head_num_, c.head_size_);
+  ly.add_layer_ = std::make_shared<op::VecAddLayer>(device_type_);
+  ly.swiglu_layer_ = std::make_shared<op::SwiGLULayer>(device_type_, c.hidden_dim_);
+}
+
+// llama3.cpp:499-575: sizes the image, creates every layer and checks them.
+base::Status Model::create_layers() {
+  const auto& c = *config_;
+  const size_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+               V = c.vocab_size_, hd = c.head_size_;
+  size_t need = 0;  // bytes after the header
+  if (is_quant_model_) {
+    if (c.is_shared_weight_)
+      return base::error::ModelParseError(
+          "A tied classifier is not defined for int8 images (the classifier is int8).");
+    const size_t gs = group_size_;
+    auto q8 = [&](size_t n) { return n + (n / gs) * 4; };
+    for (size_t n : {Dq * D, Dkv * D, Dkv * D, D * Dq, F * D, D * F, F * D})
+      if (n % gs) return base::error::ModelParseError("A matrix is not a multiple of the group size.");
+    need = L * (q8(Dq * D) + 2 * q8(Dkv * D) + q8(D * Dq) + 2 * q8(F * D) + q8(D * F)) +
+           q8(V * D) + 4 * (V * D + (2 * L + 1) * D);
+  } else if (family_ == ModelFamily::kQwen3) {
+    need = 4 * ((2 * L + 1) * D + V * D + L * (Dq * D + 2 * hd + 2 * Dkv * D + D * Dq +
+                                               3 * F * D) + V * D);
+  } else {
+    const size_t b = family_ == ModelFamily::kQwen2 ? (Dq + 2 * Dkv) : 0;
+    need = 4 * (V * D + L * (2 * D + Dq * D + 2 * Dkv * D + D * Dq + 3 * F * D + b) + D +
+                static_cast<size_t>(c.seq_len_) * hd + (c.is_shared_weight_ ? 0 : V * D));
+  }
+  const size_t have = raw_model_data_->file_size -
+                      (raw_model_data_->weight_data - static_cast<const int8_t*>(raw_model_data_->data));
+  if (need > have)
+    return base::error::ModelParseError("The weight file is shorter than its header implies.");
+
+  layers_ = std::make_unique<DecoderLayers>();
+  if (is_quant_model_) create_param_quant_layers();
+  else create_param_layers();
+  create_nonparam_layers();
+
+  auto& ly = *layers_;
+  if (!ly.embedding_layer_)
+    return base::error::InternalError("Create the embedding layer for the llama model failed!");
+  const size_t norms = family_ == ModelFamily::kQwen3 ? 4 * L + 1 : 2 * L + 1;
+  if (ly.rmsnorm_layers_.size() != norms)
+    return base::error::InternalError("Create the rmsnorm layers for the llama model failed!");
+  if (ly.wq_layers_.size() != L || ly.wk_layers_.size() != L || ly.wv_layers_.size() != L ||
+      ly.wo_layers_.size() != L)
+    return base::error::InternalError("Create the attention matmul layers for the llama model failed!");
+  if (ly.w1_layers_.size() != L || ly.w2_layers_.size() != L || ly.w3_layers_.size() != L)
+    return base::error::InternalError("Create the feedforward matmul layers for the llama model failed!");
+  if (!ly.cls_layer_ || !ly.rope_layer_ || !ly.mha_layer_ || !ly.add_layer_ || !ly.swiglu_layer_)
+    return base::error::InternalError("Create the llama model layers failed!");
+  return base::error::Success();
+}
+
+base::Status Model::insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor) {
+  if (buffers_.count(buffer_idx) > 0)
+    return base::error::KeyHasExits(std::to_string(int(buffer_idx)) +
+                                    " has exits in the buffers");
+  if (tensor.is_empty()) return base::error::InvalidArgument("The tensor is empty for inserting buffer.");
+  buffers_.insert({buffer_idx, tensor});
+  return base::error::Success();
+}
+
+tensor::Tensor& Model::get_buffer(ModelBufferType buffer_idx) {
+  KUIPER_CHECK(buffers_.count(buffer_idx) > 0, "buffer " + std::to_string(int(buffer_idx)));
+  return buffers_.at(buffer_idx);
+}
+
+const tensor::Tensor& Model::get_buffer(ModelBufferType buffer_idx) const {
+  KUIPER_CHECK(buffers_.count(buffer_idx) > 0, "buffer " + std::to_string(int(buffer_idx)));
+  return buffers_.at(buffer_idx);
+}
+
+// llama3.cpp:424-497 (Qwen3: qwen3.cpp:301-380): moves the layers to the
+// device and lays out the step's buffers with the reference's aliases.  The
+// score buffer is also the attention kernel's split-K workspace, so it holds
+// max(head_num x seq_len floats, the kernel's workspace) and starts zeroed.
+void Model::init_mem() {
+  const auto& c = *config_;
+  auto alloc = base::HIPDeviceAllocatorFactory::get_instance();
+  auto alloc_cpu = base::CPUDeviceAllocatorFactory::get_instance();
+  layers_->to_hip(hip_config_);
+  void* stream = hip_config_->stream;
+  using T = tensor::Tensor;
+  using DT = base::DataType;
+
+  T input_tokens(DT::kDataTypeInt32, 1, true, alloc_cpu);
+  T input_embeddings(DT::kDataTypeFp32, 1, c.dim_, true, alloc);
+  T sin_cache(DT::kDataTypeFp32, c.head_size_ * c.seq_len_, true, alloc);
+  T cos_cache(DT::kDataTypeFp32, c.head_size_ * c.seq_len_, true, alloc);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kSinCache, sin_cache));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kCosCache, cos_cache));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kInputTokens, input_tokens));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kInputEmbeddings, input_embeddings));
+
+  const bool qwen3 = family_ == ModelFamily::kQwen3;
+  T rms_output(DT::kDataTypeFp32, c.dim_, true, alloc);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kOutputRMSNorm, rms_output));
+  if (qwen3) {
+    T out_mha(DT::kDataTypeFp32, c.q_dim_, true, alloc);
+    STATUS_CHECK(insert_buffer(ModelBufferType::kOutputMHA, out_mha));
+  } else {
+    STATUS_CHECK(insert_buffer(ModelBufferType::kOutputMHA, rms_output));
+  }
+  STATUS_CHECK(insert_buffer(ModelBufferType::kW2Output, rms_output));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kFFNRMSNorm, rms_output));
+
+  T w1_output(DT::kDataTypeFp32, c.hidden_dim_, true, alloc);
+  T w3_output(DT::kDataTypeFp32, c.hidden_dim_, true, alloc);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kW1Output, w1_output));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kW3Output, w3_output));
+
+  T key_cache(DT::kDataTypeFp32, c.layer_num_, c.seq_len_, c.kv_dim_, true, alloc);
+  T value_cache(DT::kDataTypeFp32, c.layer_num_, c.seq_len_, c.kv_dim_, true, alloc);
+  KUIPER_CHECK(!key_cache.is_empty() && !value_cache.is_empty(), "KV cache allocation");
+  alloc->memset_zero(key_cache.ptr<void>(), key_cache.byte_size(), stream);
+  alloc->memset_zero(value_cache.ptr<void>(), value_cache.byte_size(), stream);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kKeyCache, key_cache));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kValueCache, value_cache));
+
+  T query(DT::kDataTypeFp32, c.q_dim_, true, alloc);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kQuery, query));
+
+  T pos_tensor(DT::kDataTypeInt32, 1, true, alloc_cpu);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kInputPos, pos_tensor));
+
+  const size_t ws = kernel::mha_workspace_bytes(c.head_num_, c.kv_mul_, c.seq_len_, c.head_size_);
+  int32_t score_cols = c.seq_len_;
+  while (static_cast<size_t>(c.head_num_) * score_cols * sizeof(float) < ws) ++score_cols;
+  T attn(DT::kDataTypeFp32, c.head_num_, score_cols, true, alloc);
+  alloc->memset_zero(attn.ptr<void>(), attn.byte_size(), stream);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kScoreStorage, attn));
+  if (qwen3) {
+    T attn_output(DT::kDataTypeFp32, c.dim_, true, alloc);
+    STATUS_CHECK(insert_buffer(ModelBufferType::kAttnOutput, attn_output));
+  } else {
+    STATUS_CHECK(insert_buffer(ModelBufferType::kAttnOutput, query));
+  }
+
+  T forward_output(DT::kDataTypeFp32, c.vocab_size_, true, alloc);
+  T forward_output_cpu(DT::kDataTypeFp32, c.vocab_size_, true, alloc_cpu);
+  STATUS_CHECK(insert_buffer(ModelBufferType::kForwardOutputCPU, forward_output_cpu));
+  STATUS_CHECK(insert_buffer(ModelBufferType::kForwardOutput, forward_output));
+  KUIPER_CHECK(kl_stream_sync(stream) == KL_OK, "init_mem sync");
+}
+
+std::pair<tensor::Tensor, tensor::Tensor> Model::slice_kv_cache(int32_t layer_idx,
+                                                                int32_t token_pos) const {
+  const auto& c = *config_;
+  KUIPER_CHECK(layer_idx >= 0 && layer_idx < c.layer_num_ && token_pos >= 0 &&
+                   token_pos < c.seq_len_,
+               "KV slot out of range");
+  const int64_t offset = (static_cast<int64_t>(layer_idx) * c.seq_len_ + token_pos) * c.kv_dim_;
+  float* k = const_cast<float*>(get_buffer(ModelBufferType::kKeyCache).ptr<float>(offset));
+  float* v = const_cast<float*>(get_buffer(ModelBufferType::kValueCache).ptr<float>(offset));
+  tensor::Tensor key(base::DataType::kDataTypeFp32, c.kv_dim_, false, nullptr, k);
+  tensor::Tensor val(base::DataType::kDataTypeFp32, c.kv_dim_, false, nullptr, v);
+  key.set_device_type(device_type_);
+  val.set_device_type(device_type_);
+  return {key, val};
+}
+
+// llama3.cpp:577-597
+op::EmbeddingOutput Model::embedding(const std::vector<int>& tokens) const {
+  KUIPER_CHECK(!tokens.empty(), "no tokens to embed");
+  auto* self = const_cast<Model*>(this);
+  tensor::Tensor& input_tokens = self->get_buffer(ModelBufferType::kInputTokens);
+  tensor::Tensor& input_embeddings = self->get_buffer(ModelBufferType::kInputEmbeddings);
+  const int32_t n = static_cast<int32_t>(tokens.size());
+  if (input_tokens.size() != tokens.size()) {
+    input_tokens.reshape({n});
+    input_embeddings.reshape({n, config_->dim_});
+  }
+  for (int32_t i = 0; i < n; ++i) input_tokens.index<int32_t>(i) = tokens[i];
+  tensor::Tensor input_token_num(base::DataType::kDataTypeInt32, n);
+  STATUS_CHECK(layers_->embedding_layer_->forward(input_tokens, input_token_num, input_embeddings));
+  return op::EmbeddingOutput(input_tokens, input_embeddings, input_token_num);
+}
+
+// model.cpp:240-265
+tensor::Tensor Model::fill_input(const tensor::Tensor& pos_tensor,
+                                 const op::EmbeddingOutput& embedding_output,
+                                 bool is_prompt) const {
+  const int32_t pos = pos_tensor.index<int32_t>(0);
+  const int32_t index = is_prompt ? pos : 0;
+  const auto& emb = embedding_output.input_embeddings;
+  KUIPER_CHECK(index >= 0 && static_cast<size_t>(index + 1) * config_->dim_ <= emb.size(),
+               "fill_input row out of range");
+  auto buffer = std::make_shared<base::Buffer>(
+      config_->dim_ * sizeof(float), nullptr,
+      const_cast<float*>(emb.ptr<float>(static_cast<int64_t>(index) * config_->dim_)), true);
+  tensor::Tensor input(base::DataType::kDataTypeFp32, config_->dim_);
+  input.assign(buffer);
+  input.set_device_type(device_type_);
+  return input;
+}
+
+// The layer-by-layer step (llama3.cpp:146-166, :599-744; qwen2/qwen3 alike).
+void Model::attention_rms(int32_t layer_idx, const tensor::Tensor& input) const {
+  STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx)->forward(
+      input, get_buffer(ModelBufferType::kOutputRMSNorm)));
+}
+
+void Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
+  const auto& c = *config_;
+  tensor::Tensor query = get_buffer(ModelBufferType::kQuery);
+  const int32_t pos = pos_tensor.index<int32_t>(0);
+  auto [key, val] = slice_kv_cache(layer_idx, pos);
+  const tensor::Tensor& rms = get_buffer(ModelBufferType::kOutputRMSNorm);
+  STATUS_CHECK(layers_->wq_layers_.at(layer_idx)->forward(rms, query));
+  if (family_ == ModelFamily::kQwen3) {
+    // Per-head q/k RMSNorm (qwen3.cpp:485-500).
+    query.reshape({c.q_dim_ / c.head_size_, c.head_size_});
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 2 * c.layer_num_ + 1)->forward(query, query));
+    query.reshape({c.q_dim_});
+    STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key));
+    key.reshape({c.kv_dim_ / c.head_size_, c.head_size_});
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 3 * c.layer_num_ + 1)->forward(key, key));
+    key.reshape({c.kv_dim_});
+  } else {
+    STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key));
+  }
+  STATUS_CHECK(layers_->wv_layers_.at(layer_idx)->forward(rms, val));
+  STATUS_CHECK(layers_->rope_layer_->forward(query, key, pos_tensor,
+                                             get_buffer(ModelBufferType::kSinCache),
+                                             get_buffer(ModelBufferType::kCosCache),
+                                             tensor::Tensor{}));
+}
+
+void Model::attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
+  const tensor::Tensor& mha_output = get_buffer(ModelBufferType::kOutputMHA);
+  auto mha = std::static_pointer_cast<op::MultiHeadAttention>(layers_->mha_layer_);
+  mha->set_pos(pos_tensor.index<int32_t>(0));
+  mha->set_layer_idx(layer_idx);
+  STATUS_CHECK(mha->forward(get_buffer(ModelBufferType::kQuery),
+                            get_buffer(ModelBufferType::kScoreStorage),
+                            get_buffer(ModelBufferType::kKeyCache),
+                            get_buffer(ModelBufferType::kValueCache), mha_output));
+  STATUS_CHECK(layers_->wo_layers_.at(layer_idx)->forward(
+      mha_output, get_buffer(ModelBufferType::kAttnOutput)));
+}
+
+void Model::feed_forward(int32_t layer_idx, const tensor::Tensor& input) const {
+  const auto& c = *config_;
+  STATUS_CHECK(layers_->add_layer_->forward(input, get_buffer(ModelBufferType::kAttnOutput), input));
+  const tensor::Tensor& ffn_norm = get_buffer(ModelBufferType::kFFNRMSNorm);
+  STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + c.layer_num_)->forward(input, ffn_norm));
+  const tensor::Tensor& w1 = get_buffer(ModelBufferType::kW1Output);
+  const tensor::Tensor& w3 = get_buffer(ModelBufferType::kW3Output);
+  STATUS_CHECK(layers_->w1_layers_.at(layer_idx)->forward(ffn_norm, w1));
+  STATUS_CHECK(layers_->w3_layers_.at(layer_idx)->forward(ffn_norm, w3));
+  STATUS_CHECK(layers_->swiglu_layer_->forward(w1, w3, w1));
+  const tensor::Tensor& w2 = get_buffer(ModelBufferType::kW2Output);
+  STATUS_CHECK(layers_->w2_layers_.at(layer_idx)->forward(w1, w2));
+  STATUS_CHECK(layers_->add_layer_->forward(input, w2, input));
+}
+
+void Model::cls_logits(const tensor::Tensor& input) const {
+  STATUS_CHECK(layers_->rmsnorm_layers_.at(2 * config_->layer_num_)->forward(input, input));
+  STATUS_CHECK(layers_->cls_layer_->forward(input, get_buffer(ModelBufferType::kForwardOutput)));
+}
+
+int32_t Model::post_processing(const tensor::Tensor&, bool is_prompt) const {
+  const tensor::Tensor& out = get_buffer(ModelBufferType::kForwardOutput);
+  if (is_prompt) return -1;
+  return static_cast<int32_t>(sampler_->sample(out.ptr<float>(), out.size(), hip_config_->stream));
+}
+
+base::Status Model::forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                            int&) const {
+  if (input.is_empty()) return base::error::InvalidArgument("The input tensor is empty.");
+  const int32_t pos = pos_tensor.index<int32_t>(0);
+  if (pos < 0 || pos >= config_->seq_len_)
+    return base::error::InvalidArgument("The position is outside the sequence length.");
+  for (int32_t l = 0; l < config_->layer_num_; ++l) {
+    attention_rms(l, input);
+    attention_qkv(l, pos_tensor);
+    attention_mha(l, pos_tensor);
+    feed_forward(l, input);
+  }
+  cls_logits(input);
+  return base::error::Success();
+}
+
+// llama3.cpp:641-649.  Fused: the token is the one embedding() stored for
+// this input row (fill_input's row of kInputEmbeddings), and the engine runs
+// the whole step in one launch; its logits are copied into kForwardOutput.
+base::Status Model::predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                            bool is_prompt, int& next) const {
+  if (!fused_) {
+    base::Status s = forward(input, pos_tensor, next);
+    if (!s) return s;
+    next = post_processing(pos_tensor, is_prompt);
+    return base::error::Success();
+  }
+  const int32_t pos = pos_tensor.index<int32_t>(0);
+  if (pos < 0 || pos >= config_->seq_len_)
+    return base::error::InvalidArgument("The position is outside the sequence length.");
+  const int32_t row = is_prompt ? pos : 0;
+  const tensor::Tensor& tokens = get_buffer(ModelBufferType::kInputTokens);
+  const tensor::Tensor& emb = get_buffer(ModelBufferType::kInputEmbeddings);
+  if (row >= static_cast<int32_t>(tokens.size()) ||
+      input.ptr<float>() != emb.ptr<float>(static_cast<int64_t>(row) * config_->dim_))
+    return base::error::InvalidArgument(
+        "The fused step takes the input row that fill_input() returned for embedding().");
+  int32_t sampled = -1;
+  int rc = kl_engine_step(engine_, tokens.index<int32_t>(row), pos, &sampled, nullptr);
+  if (rc != KL_OK) return base::error::InternalError(std::string("kl_engine_step: ") + kl_error_string(rc));
+  const float* d_logits = nullptr;
+  kl_engine_buffers(engine_, &d_logits, nullptr, nullptr);
+  const tensor::Tensor& out = get_buffer(ModelBufferType::kForwardOutput);
+  rc = kl_memcpy_d2d(const_cast<float*>(out.ptr<float>()), d_logits, out.byte_size(),
+                     hip_config_->stream);
+  if (rc == KL_OK) rc = kl_stream_sync(hip_config_->stream);
+  if (rc != KL_OK) return base::error::InternalError("logits copy failed");
+  next = is_prompt ? -1 : sampled;
+  return base::error::Success();
+}
+
+// Creates the engine from the mapped image on first use.  Switching modes
+// starts a new sequence: each path keeps its own KV cache.
+base::Status Model::set_fused(bool enable) {
+  if (!raw_model_data_) return base::error::InvalidArgument("init() has not run.");
+  if (enable && !engine_) {
+    int rc = kl_engine_create(raw_model_data_->data, raw_model_data_->file_size,
+                              static_cast<int>(family_), is_quant_model_ ? 1 : 0, &engine_);
+    if (rc != KL_OK) {
+      engine_ = nullptr;
+      return base::error::InternalError(std::string("kl_engine_create: ") + kl_error_string(rc));
+    }
+  }
+  fused_ = enable;
+  return base::error::Success();
+}
+
+// demo/main.cpp:5-47 without the tokenizer: positions 0..P-2 are prompt steps,
+// position P-1 feeds the last prompt token through the decode branch, and
+// n_new tokens are sampled (no end-of-sequence stop: there is no tokenizer).
+// Fused: the whole loop runs on the device (kl_engine_generate).
+base::Status Model::generate(const std::vector<int32_t>& prompt, int32_t n_new,
+                             std::vector<int32_t>& out) const {
+  const int32_t P = static_cast<int32_t>(prompt.size());
+  if (P < 1 || n_new < 1 || P + n_new - 1 > config_->seq_len_)
+    return base::error::InvalidArgument("prompt + new tokens must fit the sequence length.");
+  out.assign(n_new, -1);
+  if (fused_) {
+    int rc = kl_engine_generate(engine_, prompt.data(), P, n_new, out.data(), nullptr);
+    if (rc != KL_OK) return base::error::InternalError(std::string("kl_engine_generate: ") + kl_error_string(rc));
+    return base::error::Success();
+  }
+  const op::EmbeddingOutput prompt_embedding = embedding(prompt);
+  tensor::Tensor pos_tensor = get_buffer(ModelBufferType::kInputPos);
+  int next = -1;
+  for (int32_t pos = 0; pos < P - 1; ++pos) {
+    pos_tensor.index<int32_t>(0) = pos;
+    base::Status s = predict(fill_input(pos_tensor, prompt_embedding, true), pos_tensor, true, next);
+    if (!s) return s;
+  }
+  int32_t token = prompt[P - 1];
+  for (int32_t i = 0; i < n_new; ++i) {
+    const int32_t pos = P - 1 + i;
+    pos_tensor.index<int32_t>(0) = pos;
+    const op::EmbeddingOutput emb = embedding({token});
+    base::Status s = predict(fill_input(pos_tensor, emb, false), pos_tensor, false, next);
+    if (!s) return s;
+    out[i] = next;
+    token = next;
+  }
+  return base::error::Success();
+}
+
+bool Model::is_sentence_ending(int32_t) const { return false; }
+std::string Model::decode(int32_t) const { return std::string(); }
+std::string Model::decode(std::vector<int32_t>) const { return std::string(); }
+std::vector<int32_t> Model::encode(const std::string&) const {
+  std::fprintf(stderr, "kuiper: no tokenizer is loaded; pass token ids\n");
+  return {};
+}
+
+}  // namespace model
