@@ -1,4 +1,4 @@
-// Persistent decode step: one cooperative launch runs a whole token of the
+// Persistent decode step: one launch runs a whole token of the
 // reference forward (model/llama3.cpp:146-166, :599-744; qwen2.cpp:205-225;
 // qwen3.cpp:147-167) on every CU at once.
 //

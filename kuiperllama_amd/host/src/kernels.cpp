@@ -1,6 +1,7 @@
 // kDeviceHIP kernel adapters: each unpacks the reference kernel signature
 // (source/op/kernels/kernels_interface.h:6-47) into one call of the C ABI.  A
 // failed call is fatal, as a failed CHECK inside the reference's kernels is.
+#include <algorithm>
 #include <string>
 
 #include "kuiper/alloc.h"
@@ -77,6 +78,27 @@ void matmul_q8_hip(const tensor::Tensor& input, const tensor::Tensor& weight,
            "kl_gemv_q8");
 }
 
+// Device staging area for token ids, grown to the largest prompt seen and
+// kept for the process (the reference clones the ids into a fresh device
+// tensor on every call, emb_kernel.cu:33-35).
+struct IdStage {
+  int32_t* ptr = nullptr;
+  size_t count = 0;
+};
+IdStage g_ids;
+
+int32_t* stage_ids(size_t n) {
+  if (n > g_ids.count) {
+    void* p = nullptr;
+    const size_t cap = std::max<size_t>(n, 512);
+    check_rc(kl_malloc(&p, cap * sizeof(int32_t)), "kl_malloc (token staging)");
+    if (g_ids.ptr) kl_free(g_ids.ptr);
+    g_ids.ptr = static_cast<int32_t*>(p);
+    g_ids.count = cap;
+  }
+  return g_ids.ptr;
+}
+
 // kernels/cuda/emb_kernel.cu:23-48: the token ids arrive in host memory, are
 // range-checked on the host (kernels/cpu/emb_kernel.cpp:18-20 CHECKs them) and
 // staged to the device.
@@ -90,22 +112,27 @@ void embedding_hip(const tensor::Tensor& input, const tensor::Tensor& weight,
   const int dim = weight.get_dim(1);
   const int n = as_int(input.size());
   KUIPER_CHECK(output.size() >= static_cast<size_t>(n) * dim, "embedding output too small");
-  tensor::Tensor ids = input;
+  const int32_t* ids = nullptr;
   if (input.device_type() == base::DeviceType::kDeviceCPU) {
     for (int i = 0; i < n; ++i) {
       const int32_t t = input.index<int32_t>(i);
       KUIPER_CHECK(t >= 0 && t < vocab_size, "Token index is greater than vocab size.");
     }
-    ids = input.clone();
-    ids.to_hip(stream);
+    int32_t* staged = stage_ids(n);
+    check_rc(kl_memcpy_h2d(staged, input.ptr<int32_t>(), n * sizeof(int32_t), stream),
+             "kl_memcpy_h2d");
+    ids = staged;
   } else {
     require_hip(input, "embedding input");
+    ids = input.ptr<int32_t>();
   }
-  check_rc(kl_embedding(ids.ptr<int32_t>(), n, weight.ptr<float>(), vocab_size, dim,
+  check_rc(kl_embedding(ids, n, weight.ptr<float>(), vocab_size, dim,
                         const_cast<float*>(output.ptr<float>()), nullptr, stream),
            "kl_embedding");
+  // The host ids may change after return and the staging area is reused by
+  // the next call, possibly on another stream.
   if (input.device_type() == base::DeviceType::kDeviceCPU)
-    check_rc(kl_stream_sync(stream), "kl_stream_sync");  // ids is freed on return
+    check_rc(kl_stream_sync(stream), "kl_stream_sync");
 }
 
 // kernels/cpu/swiglu_kernel.cpp:3-23
