@@ -130,6 +130,31 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
            int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
            const float* key_cache, const float* value_cache, void* stream);
 
+/* ---- Batched prompt prefill (no reference counterpart: the reference runs
+ * the prompt token by token, demo/main.cpp:20-22, and MatmulLayer accepts
+ * only a 1-D input, op/matmul.cpp:20).  Row-major, fp32, device pointers. ---- */
+
+/* C[M x N] = A[M x K] . W[N x K]^T (+ bias[N]) (+ C when accumulate != 0): the
+ * MatmulKernel product (KI:9-10) for M input rows at once, on the matrix cores
+ * (v_mfma_f32_32x32x2f32).  lda, ldw, ldc are row strides in floats.  Needs
+ * K, lda, ldw multiples of 4 and A, W 16-byte aligned (else KL_EUNSUPP). */
+int kl_gemm_f32(const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
+                int ldc, const float* bias, int accumulate, void* stream);
+
+/* RoPEKernel (KI:36-39) on n_pos rows: row r of q (stride ldq) and of k
+ * (stride ldk) rotated at position pos0 + r. */
+int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ldq, float* k,
+                 int ldk, int pos0, int n_pos, const float* sin_cache, const float* cos_cache,
+                 void* stream);
+
+/* MHAKernel (KI:22-28) for query positions pos0 .. pos0+n_pos-1 at once:
+ * row r of q (stride ldq, head_num*head_size floats) attends key/value rows
+ * 0 .. pos0+r of one layer's caches ([seq_len][kv_dim]), causal; out row r
+ * (stride ldo).  head_size 32, 64 or 128 (else KL_EUNSUPP). */
+int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
+                    int ldq, const float* key_cache, const float* value_cache, int kv_dim,
+                    float* out, int ldo, void* stream);
+
 /* SwigluKernel (KI:19-20; cpu/swiglu_kernel.cpp:3-23): out = a*sigmoid(a)*b. */
 int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream);
 
@@ -237,6 +262,24 @@ int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, in
  * stream) of the last n_timed steps only.  out_tokens[n_warmup + n_timed]. */
 int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, int n_timed,
                     int32_t* out_tokens, float* timed_ms);
+/* Batched prompt prefill: positions 0 .. P-1 of `prompt` through every layer
+ * at once (row RMSNorm, MFMA GEMMs, batched q/k norm and RoPE, causal
+ * attention, SwiGLU), K and V rows written to the caches, then the final norm,
+ * classifier and argmax of position P-1: *next (may be NULL) receives the
+ * greedy token, logits (host, may be NULL) the vocab logits of position P-1.
+ * Same result as P kl_engine_step calls up to float rounding; a following
+ * kl_engine_step(e, *next, P, ...) continues the sequence.  Chunks of at most
+ * 1024 positions.  KL_EUNSUPP for int8 images and head sizes other than 32,
+ * 64, 128.  Blocks until done; *prefill_ms (may be NULL) receives its device
+ * time. */
+int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next, float* logits,
+                      float* prefill_ms);
+/* When enabled (default off), kl_engine_generate runs prompts of 2 or more
+ * tokens through kl_engine_prefill; out_tokens[0] is then the prefill's token
+ * and *decode_ms covers the n_new - 1 decode steps that follow.  Returns
+ * KL_EUNSUPP (and stays off) where the prefill does not support the model. */
+int kl_engine_set_prefill(kl_engine* e, int enable);
+
 /* Per-kernel timing: runs `steps` decode steps from (token, pos0) without the
  * graph, with a HIP event recorded between consecutive launches on the
  * engine's stream, and returns the average duration and launch count per

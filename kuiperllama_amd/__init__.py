@@ -196,6 +196,22 @@ class Engine:
                                      C.byref(ms)), "kl_engine_generate")
         return out, ms.value
 
+    def prefill(self, prompt, want_logits: bool = True):
+        """Batched prefill of the whole prompt (kl_engine_prefill): returns
+        (next token, logits of the last position, device ms)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        nxt = C.c_int32(-1)
+        logits = np.empty(self.vocab, np.float32) if want_logits else None
+        ms = C.c_float(0.0)
+        check(lib.kl_engine_prefill(self.handle, p.ctypes.data, p.size, C.byref(nxt),
+                                    logits.ctypes.data if want_logits else None, C.byref(ms)),
+              "kl_engine_prefill")
+        return nxt.value, logits, ms.value
+
+    def set_prefill(self, enable: bool):
+        """Whether generate() runs the prompt through the batched prefill."""
+        check(lib.kl_engine_set_prefill(self.handle, int(enable)), "kl_engine_set_prefill")
+
     def bench(self, prompt, n_warmup: int, n_timed: int):
         """Prompt + n_warmup untimed decode steps, then n_timed decode steps
         timed with HIP events on the engine's stream.  Returns (tokens, ms)."""

@@ -89,6 +89,9 @@ _SIGS = {
     "kl_rope": (_i, [_i, _i, _i, _i, _p, _p, _i, _p, _p, _p]),
     "kl_mha_workspace_size": (_i, [_i, _i, _i, _i, C.POINTER(_sz)]),
     "kl_mha": (_i, [_i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _sz, _p, _p, _p]),
+    "kl_gemm_f32": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
+    "kl_rope_rows": (_i, [_i, _i, _i, _i, _p, _i, _p, _i, _i, _i, _p, _p, _p]),
+    "kl_attn_prefill": (_i, [_i, _i, _i, _i, _i, _p, _i, _p, _p, _i, _p, _i, _p]),
     "kl_swiglu": (_i, [_p, _p, _p, _i, _p]),
     "kl_add": (_i, [_p, _p, _p, _i, _p]),
     "kl_embedding": (_i, [_p, _i, _p, _i, _i, _p, _p, _p]),
@@ -109,6 +112,8 @@ _SIGS = {
     "kl_engine_step": (_i, [_p, C.c_int32, C.c_int32, _i32p, _p]),
     "kl_engine_generate": (_i, [_p, _p, _i, _i, _p, _fp]),
     "kl_engine_bench": (_i, [_p, _p, _i, _i, _i, _p, _fp]),
+    "kl_engine_prefill": (_i, [_p, _p, _i, _i32p, _p, _fp]),
+    "kl_engine_set_prefill": (_i, [_p, _i]),
     "kl_engine_profile": (_i, [_p, C.c_int32, C.c_int32, _i, _fp, _i32p]),
     "kl_engine_trace_step": (_i, [_p, C.c_int32, C.c_int32, _p, C.c_int64, _i32p, _i32p]),
     "kl_engine_buffers": (_i, [_p, C.POINTER(_p), C.POINTER(_p), C.POINTER(_p)]),

@@ -450,6 +450,17 @@ struct kl_engine {
   int* derr = nullptr;
   int* derr_host = nullptr;    // pinned
   PArgs pargs{};
+  // Batched prompt prefill (kl_engine_prefill): scratch for one chunk of
+  // rows, allocated on first use.
+  bool use_prefill = false;
+  int pf_rows = 0;              // rows the scratch holds
+  char* pf_buf = nullptr;       // one allocation for everything below
+  float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
+  float *pf_h1 = nullptr, *pf_h3 = nullptr, *pf_xlast = nullptr;
+  int32_t* pf_tok = nullptr;    // [seq_len] prompt ids
+  int32_t* pf_next = nullptr;
+  void* pf_am = nullptr;        // argmax workspace (zeroed once)
+  size_t pf_am_bytes = 0;
 };
 
 namespace {
@@ -822,6 +833,7 @@ void release(kl_engine* e) {
   if (e->ev0) (void)hipEventDestroy(e->ev0);
   if (e->ev1) (void)hipEventDestroy(e->ev1);
   if (e->arena) (void)hipFree(e->arena);
+  if (e->pf_buf) (void)hipFree(e->pf_buf);
   if (e->st_host) (void)hipHostFree(e->st_host);
   if (e->derr_host) (void)hipHostFree(e->derr_host);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -1120,12 +1132,195 @@ int kl_engine_step(kl_engine* e, int32_t token, int32_t pos, int32_t* next, floa
   return KL_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+constexpr int kPrefillChunk = 1024;  // rows per prefill pass
+
+bool prefill_supported(const kl_engine* e) {
+  const int hd = e->lay.hd;
+  return !e->quant && (hd == 32 || hd == 64 || hd == 128);
+}
+
+// Allocates the prefill scratch for `rows` rows (once; grows if needed).
+int prefill_scratch(kl_engine* e, int rows) {
+  if (rows <= e->pf_rows) return KL_OK;
+  const ImageLayout& m = e->lay;
+  size_t am = 0;
+  int r = kl_argmax_workspace_size(m.V, &am);
+  if (r != KL_OK) return r;
+  auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+  const size_t R = rows;
+  const size_t sz_x = al(R * m.D * 4), sz_q = al(R * m.Dq * 4), sz_h = al(R * m.F * 4);
+  const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + al(m.D * 4) + al(m.S * 4) + al(256) + al(am);
+  char* buf = nullptr;
+  hipError_t err = hipMalloc(&buf, total);
+  if (err != hipSuccess) return KL_ENOMEM;
+  if (e->pf_buf) (void)hipFree(e->pf_buf);
+  e->pf_buf = buf;
+  size_t off = 0;
+  auto take = [&](size_t b) {
+    char* p = buf + off;
+    off += b;
+    return p;
+  };
+  e->pf_x = reinterpret_cast<float*>(take(sz_x));
+  e->pf_xn = reinterpret_cast<float*>(take(sz_x));
+  e->pf_q = reinterpret_cast<float*>(take(sz_q));
+  e->pf_att = reinterpret_cast<float*>(take(sz_q));
+  e->pf_h1 = reinterpret_cast<float*>(take(sz_h));
+  e->pf_h3 = reinterpret_cast<float*>(take(sz_h));
+  e->pf_xlast = reinterpret_cast<float*>(take(al(m.D * 4)));
+  e->pf_tok = reinterpret_cast<int32_t*>(take(al(m.S * 4)));
+  e->pf_next = reinterpret_cast<int32_t*>(take(al(256)));
+  e->pf_am = take(al(am));
+  e->pf_am_bytes = am;
+  e->pf_rows = rows;
+  err = hipMemsetAsync(e->pf_am, 0, am, e->stream);
+  return err == hipSuccess ? KL_OK : rc(err);
+}
+
+// Positions pos0 .. pos0+n-1 through every layer; leaves the residual rows in
+// pf_x and the K/V rows in the caches.
+int prefill_chunk(kl_engine* e, int pos0, int n) {
+  const ImageLayout& m = e->lay;
+  const int D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F, H = m.H, KVH = m.KVH, hd = m.hd;
+  void* st = e->stream;
+  const size_t kv_layer = static_cast<size_t>(m.S) * Dkv;
+  int r = kl_embedding(e->pf_tok + pos0, n, e->emb, m.V, D, e->pf_x, nullptr, st);
+#define PF(call)          \
+  do {                    \
+    if (r == KL_OK) r = (call); \
+  } while (0)
+  for (int l = 0; l < m.L && r == KL_OK; ++l) {
+    const LayerDev& Ld = e->layers[l];
+    float* kc = e->kcache + l * kv_layer;
+    float* vc = e->vcache + l * kv_layer;
+    float* krow = kc + static_cast<size_t>(pos0) * Dkv;
+    float* vrow = vc + static_cast<size_t>(pos0) * Dkv;
+    const float* wq = static_cast<const float*>(Ld.wq.w);
+    const float* wk = static_cast<const float*>(Ld.wk.w);
+    const float* wv = static_cast<const float*>(Ld.wv.w);
+    const float* wo = static_cast<const float*>(Ld.wo.w);
+    const float* w1 = static_cast<const float*>(Ld.w1.w);
+    const float* w2 = static_cast<const float*>(Ld.w2.w);
+    const float* w3 = static_cast<const float*>(Ld.w3.w);
+    // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
+    PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
+    PF(kl_gemm_f32(e->pf_xn, wq, e->pf_q, n, Dq, D, D, D, Dq, Ld.bq, 0, st));
+    PF(kl_gemm_f32(e->pf_xn, wk, krow, n, Dkv, D, D, D, Dkv, Ld.bk, 0, st));
+    PF(kl_gemm_f32(e->pf_xn, wv, vrow, n, Dkv, D, D, D, Dkv, Ld.bv, 0, st));
+    if (e->transform == 2) {  // Qwen3 per-head q/k RMSNorm, eps 1e-6
+      PF(kl_rmsnorm_rows(e->pf_q, Ld.qn, e->pf_q, n * H, hd, 1e-6f, st));
+      PF(kl_rmsnorm_rows(krow, Ld.kn, krow, n * KVH, hd, 1e-6f, st));
+    }
+    PF(kl_rope_rows(e->rope_style, Dq, Dkv, hd, e->pf_q, Dq, krow, Dkv, pos0, n, e->sin_t,
+                    e->cos_t, st));
+    // attention_mha (llama3.cpp:651-669), then x += Wo . att
+    PF(kl_attn_prefill(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, st));
+    PF(kl_gemm_f32(e->pf_att, wo, e->pf_x, n, D, Dq, Dq, Dq, D, nullptr, 1, st));
+    // feed_forward (llama3.cpp:671-719)
+    PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
+    PF(kl_gemm_f32(e->pf_xn, w1, e->pf_h1, n, F, D, D, D, F, nullptr, 0, st));
+    PF(kl_gemm_f32(e->pf_xn, w3, e->pf_h3, n, F, D, D, D, F, nullptr, 0, st));
+    PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
+    PF(kl_gemm_f32(e->pf_h1, w2, e->pf_x, n, D, F, F, F, D, nullptr, 1, st));
+  }
+#undef PF
+  return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kl_engine_set_prefill(kl_engine* e, int enable) {
+  if (!e) return KL_EINVAL;
+  if (enable && !prefill_supported(e)) return KL_EUNSUPP;
+  e->use_prefill = enable != 0;
+  return KL_OK;
+}
+
+int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next, float* logits,
+                      float* prefill_ms) {
+  if (!e || !prompt || P <= 0) return KL_EINVAL;
+  const ImageLayout& m = e->lay;
+  if (P > m.S) return KL_EINVAL;
+  for (int i = 0; i < P; ++i)
+    if (prompt[i] < 0 || prompt[i] >= m.V) return KL_ETOKEN;
+  if (!prefill_supported(e)) return KL_EUNSUPP;
+  int r = prefill_scratch(e, std::min(P, kPrefillChunk));
+  if (r != KL_OK) return r;
+  hipError_t err = hipMemcpyAsync(e->pf_tok, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
+                                  e->stream);
+  if (err == hipSuccess) err = hipEventRecord(e->ev0, e->stream);
+  if (err != hipSuccess) return rc(err);
+  int last_n = 0;
+  for (int pos0 = 0; pos0 < P && r == KL_OK; pos0 += kPrefillChunk) {
+    last_n = std::min(kPrefillChunk, P - pos0);
+    r = prefill_chunk(e, pos0, last_n);
+  }
+  // cls_logits + post_processing of position P-1 (llama3.cpp:721-744)
+  if (r == KL_OK)
+    r = kl_rmsnorm(e->pf_x + static_cast<size_t>(last_n - 1) * m.D, e->rms_final, e->pf_xlast, m.D,
+                   e->eps, e->stream);
+  if (r == KL_OK)
+    r = kl_gemv_f32(e->pf_xlast, static_cast<const float*>(e->wcls.w), e->logits, m.V, m.D, 1.f,
+                    e->stream);
+  if (r == KL_OK) r = kl_argmax(e->logits, m.V, e->pf_next, e->pf_am, e->pf_am_bytes, e->stream);
+  if (r != KL_OK) return r;
+  err = hipEventRecord(e->ev1, e->stream);
+  int32_t nx = -1;
+  if (err == hipSuccess)
+    err = hipMemcpyAsync(&nx, e->pf_next, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream);
+  if (err == hipSuccess && logits)
+    err = hipMemcpyAsync(logits, e->logits, sizeof(float) * m.V, hipMemcpyDeviceToHost, e->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+  if (err == hipSuccess && prefill_ms) err = hipEventElapsedTime(prefill_ms, e->ev0, e->ev1);
+  if (err != hipSuccess) return rc(err);
+  if (next) *next = nx;
+  return KL_OK;
+}
+
 int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, int32_t* out_tokens,
                        float* decode_ms) {
   if (!e || !prompt || !out_tokens || P <= 0 || n_new <= 0) return KL_EINVAL;
   if (P + n_new - 1 > e->lay.S) return KL_EINVAL;
   for (int i = 0; i < P; ++i)
     if (prompt[i] < 0 || prompt[i] >= e->lay.V) return KL_ETOKEN;
+  if (e->use_prefill && P >= 2) {
+    // The prompt in one batched pass; its token is the first of out_tokens,
+    // the device loop continues at position P.
+    int32_t first = -1;
+    int r = kl_engine_prefill(e, prompt, P, &first, nullptr, nullptr);
+    if (r != KL_OK) return r;
+    out_tokens[0] = first;
+    if (decode_ms) *decode_ms = 0.f;
+    if (n_new == 1) return KL_OK;
+    *e->st_host = StepState{P, first, P, first};
+    hipError_t err =
+        hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+    if (err == hipSuccess) err = hipEventRecord(e->ev0, e->stream);
+    if (err != hipSuccess) return rc(err);
+    for (int i = 0; i < n_new - 1; ++i) {
+      r = run_step(e);
+      if (r != KL_OK) return r;
+    }
+    err = hipEventRecord(e->ev1, e->stream);
+    if (err == hipSuccess)
+      err = hipMemcpyAsync(out_tokens + 1, e->out_tokens + P, sizeof(int32_t) * (n_new - 1),
+                           hipMemcpyDeviceToHost, e->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+    if (err != hipSuccess) return rc(err);
+    const int de = check_device_error(e);
+    if (de != KL_OK) return de;
+    if (decode_ms) {
+      err = hipEventElapsedTime(decode_ms, e->ev0, e->ev1);
+      if (err != hipSuccess) return rc(err);
+    }
+    return KL_OK;
+  }
   hipError_t err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
                                   e->stream);
   if (err != hipSuccess) return rc(err);

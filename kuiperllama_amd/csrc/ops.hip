@@ -13,7 +13,9 @@
 
 #include "attn.hpp"
 #include "device.hpp"
+#include "gemm.hpp"
 #include "gemv.hpp"
+#include "prefill.hpp"
 #include "kuiper_hip.h"
 
 using namespace kl;
@@ -148,10 +150,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // RoPE: one thread per rotated pair of q (and of k where the index < kv_dim).
 // ---------------------------------------------------------------------------
-__global__ void k_rope(int style, int dim, int kv_dim, int hd, float* q, float* k, int pos,
-                       const float* __restrict__ sin_t, const float* __restrict__ cos_t) {
-  const int p = blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= dim / 2) return;
+// Rotates pair p of q (and of k where the reference does) at position pos.
+__device__ __forceinline__ void rope_one(int style, int kv_dim, int hd, float* q, float* k, int pos,
+                                         int p, const float* __restrict__ sin_t,
+                                         const float* __restrict__ cos_t) {
   const int half = hd / 2;
   int i0, i1, tab;
   if (style == KL_ROPE_INTERLEAVED) {
@@ -179,6 +181,23 @@ __global__ void k_rope(int style, int dim, int kv_dim, int hd, float* q, float* 
     k[i0] = w0;
     k[i1] = w1;
   }
+}
+
+__global__ void k_rope(int style, int dim, int kv_dim, int hd, float* q, float* k, int pos,
+                       const float* __restrict__ sin_t, const float* __restrict__ cos_t) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < dim / 2) rope_one(style, kv_dim, hd, q, k, pos, p, sin_t, cos_t);
+}
+
+// Rows r < n of q (stride ldq) and k (stride ldk) at positions pos0 + r.
+__global__ void k_rope_rows(int style, int dim, int kv_dim, int hd, float* q, int ldq, float* k,
+                            int ldk, int pos0, int n, const float* __restrict__ sin_t,
+                            const float* __restrict__ cos_t) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.y;
+  if (p < dim / 2 && r < n)
+    rope_one(style, kv_dim, hd, q + static_cast<size_t>(r) * ldq, k + static_cast<size_t>(r) * ldk,
+             pos0 + r, p, sin_t, cos_t);
 }
 
 // ---------------------------------------------------------------------------
@@ -497,6 +516,84 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
     default: hipLaunchKernelGGL(k_attn_decode<256>, grid, block, p.lds_bytes, as_stream(stream), a); break;
   }
   return launch_rc();
+}
+
+int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ldq, float* k,
+                 int ldk, int pos0, int n_pos, const float* sin_cache, const float* cos_cache,
+                 void* stream) {
+  if (!q || !k || !sin_cache || !cos_cache || dim <= 0 || kv_dim < 0 || kv_dim > dim ||
+      head_size <= 0 || head_size % 2 != 0 || dim % head_size != 0 || kv_dim % head_size != 0 ||
+      pos0 < 0 || n_pos <= 0 || n_pos > 65535 || ldq < dim || ldk < kv_dim)
+    return KL_EINVAL;
+  if (style != KL_ROPE_INTERLEAVED && style != KL_ROPE_HALF) return KL_EINVAL;
+  const int pairs = dim / 2;
+  hipLaunchKernelGGL(k_rope_rows, dim3((pairs + 255) / 256, n_pos), dim3(256), 0, as_stream(stream),
+                     style, dim, kv_dim, head_size, q, ldq, k, ldk, pos0, n_pos, sin_cache,
+                     cos_cache);
+  return launch_rc();
+}
+
+int kl_gemm_f32(const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
+                int ldc, const float* bias, int accumulate, void* stream) {
+  if (!A || !W || !C || M <= 0 || N <= 0 || K <= 0 || lda < K || ldw < K || ldc < N)
+    return KL_EINVAL;
+  // 16-byte operand loads: rows must start 16-byte aligned.
+  if (K % 4 || lda % 4 || ldw % 4 || !aligned16(A) || !aligned16(W)) return KL_EUNSUPP;
+  const hipStream_t st = as_stream(stream);
+  const long long big = static_cast<long long>((M + 127) / 128) * ((N + 127) / 128);
+  if (big >= 256) {
+    const int tm = (M + 127) / 128, tn = (N + 127) / 128;
+    hipLaunchKernelGGL((k_gemm_f32<2, 2, 2, 2>), dim3(tm * tn), dim3(256), 0, st, A, W, C, bias, M,
+                       N, K, lda, ldw, ldc, accumulate, tm);
+  } else {
+    const int tm = (M + 63) / 64, tn = (N + 63) / 64;
+    hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(tm * tn), dim3(256), 0, st, A, W, C, bias, M,
+                       N, K, lda, ldw, ldc, accumulate, tm);
+  }
+  return launch_rc();
+}
+
+}  // extern "C"
+
+namespace {
+template <int HD>
+int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
+                        int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st) {
+  const size_t lds = attn_prefill_lds_bytes(HD);
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_prefill<HD>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return rc(e);
+    attr_set = true;
+  }
+  const float scale = 1.f / std::sqrt(static_cast<float>(HD));
+  hipLaunchKernelGGL(k_attn_prefill<HD>, dim3((n + kPrefillQB - 1) / kPrefillQB, heads), dim3(256),
+                     lds, st, q, ldq, kc, vc, kv_dim, kv_mul, out, ldo, pos0, n, scale);
+  return launch_rc();
+}
+}  // namespace
+
+extern "C" {
+
+int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
+                    int ldq, const float* key_cache, const float* value_cache, int kv_dim,
+                    float* out, int ldo, void* stream) {
+  if (!q || !key_cache || !value_cache || !out || pos0 < 0 || n_pos <= 0 || n_pos > 65535 * 64 ||
+      head_num <= 0 || kv_mul <= 0 || head_num % kv_mul != 0 ||
+      kv_dim != head_num / kv_mul * head_size || ldq < head_num * head_size ||
+      ldo < head_num * head_size)
+    return KL_EINVAL;
+  if (ldq % 4 || kv_dim % 4 || !aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache))
+    return KL_EUNSUPP;
+  const hipStream_t st = as_stream(stream);
+  switch (head_size) {
+    case 32: return attn_prefill_launch<32>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
+    case 64: return attn_prefill_launch<64>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
+    case 128: return attn_prefill_launch<128>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
+    default: return KL_EUNSUPP;
+  }
 }
 
 int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream) {

@@ -204,21 +204,32 @@ __device__ __forceinline__ void trace_mark(const PArgs& a, int slot) {
     a.trace[static_cast<size_t>(slot) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 }
 
-// Loads a tagged element, re-polling until it carries `tag`.  Bounded: on
-// timeout (or once another workgroup has reported an error) returns whatever
-// value it holds.
-__device__ __forceinline__ float poll_tagged(const PArgs& a, const tagged_t* p, unsigned int tag) {
-  tagged_t x = g_ld64(p);
-  for (int spins = 0; tag_of(x) != tag; ++spins) {
+// Re-polls, all together, the elements k of `v` (E values already loaded once
+// from addr(k), valid where bit k of `valid` is set) that do not yet carry
+// `tag`, until every one does: one round trip per retry however many are
+// stale.  Bounded: after kSpinLimit retries (or once another workgroup has
+// reported an error) it records the error and returns with what it holds.
+template <int E, class Addr>
+__device__ __forceinline__ void poll_many(const PArgs& a, unsigned int tag, Addr addr,
+                                          unsigned int valid, tagged_t (&v)[E]) {
+  unsigned int pend = 0;
+#pragma unroll
+  for (int k = 0; k < E; ++k)
+    if (((valid >> k) & 1u) && tag_of(v[k]) != tag) pend |= 1u << k;
+  for (int spins = 0; pend != 0; ++spins) {
     if ((spins & 63) == 63 && g_ld(a.err) != 0) break;
     if (spins >= kSpinLimit) {
       g_st(a.err, kDevErrWait);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
-    x = g_ld64(p);
+#pragma unroll
+    for (int k = 0; k < E; ++k)
+      if ((pend >> k) & 1u) v[k] = g_ld64(addr(k));
+#pragma unroll
+    for (int k = 0; k < E; ++k)
+      if (((pend >> k) & 1u) && tag_of(v[k]) == tag) pend &= ~(1u << k);
   }
-  return val_of(x);
 }
 
 // Sum over the 512 threads of the workgroup; `red` holds >= kPWaves floats.
@@ -246,6 +257,7 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
                                           const float* emb_row, const float* nw, float eps, int n,
                                           float* xs, float* red, Prefetch prefetch) {
   float ss = 0.f;
+  float wv[8];  // norm weights of the first round, loaded before the prefetch
   for (int b0 = 0; b0 < n; b0 += kPThreads * 8) {
     tagged_t v[8];
 #pragma unroll
@@ -256,13 +268,32 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
       else
         v[k] = (static_cast<tagged_t>(tag) << 32) | __float_as_uint(i < n ? g_rd(emb_row + i) : 0.f);
     }
-    if (b0 == 0) prefetch();
+    if (b0 == 0) {
+      if (nw) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int i = k * kPThreads + threadIdx.x;
+          wv[k] = g_rd(nw + (i < n ? i : 0));
+        }
+      }
+      // Keep the prefetch behind the input and norm-weight loads: loads
+      // complete in order, so using those never waits for the weights.
+      __builtin_amdgcn_sched_barrier(0);
+      prefetch();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (src) {
+      unsigned int valid = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (b0 + k * kPThreads + static_cast<int>(threadIdx.x) < n) valid |= 1u << k;
+      poll_many<8>(a, tag, [&](int k) { return src + b0 + k * kPThreads + threadIdx.x; }, valid, v);
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int i = b0 + k * kPThreads + threadIdx.x;
-      float x = val_of(v[k]);
-      if (tag_of(v[k]) != tag) x = poll_tagged(a, src + i, tag);
       if (i < n) {
+        const float x = val_of(v[k]);
         xs[i] = x;
         ss += x * x;
       }
@@ -271,7 +302,12 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
   if (nw) {
     ss = block_sum_p(ss, red);
     const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
-    for (int i = threadIdx.x; i < n; i += kPThreads) xs[i] = g_rd(nw + i) * (r * xs[i]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = k * kPThreads + threadIdx.x;
+      if (i < n) xs[i] = wv[k] * (r * xs[i]);
+    }
+    for (int i = kPThreads * 8 + threadIdx.x; i < n; i += kPThreads) xs[i] = g_rd(nw + i) * (r * xs[i]);
   }
   __syncthreads();
 }
@@ -518,7 +554,7 @@ __device__ __forceinline__ void p_seg_compute(PGp p, const PGeom& g, PCur& c,
 }
 
 // Runs the streaming loop of one phase.  On entry, buffer A holds (in flight)
-// the wave's first segment of p (issued by stage_vec).  Only A is live
+// the wave's first segment of p (issued by stage_vec); B is the second buffer.  Only A is live
 // outside this function.  Returns with LDS `red` holding every finished row
 // of the workgroup (after a workgroup barrier).
 template <bool Q8, int NB>
@@ -540,17 +576,15 @@ __device__ __forceinline__ void p_stream(PGp p, const PGeom& g, PChunk<Q8> (&A)[
     }
   }
   float acc = 0.f;
+  // Every step issues the next segment into the buffer computed in the step
+  // before, then consumes the other.  Issues are unconditional (past the
+  // wave's last segment they read one clamped valid address and are never
+  // consumed), so each consume waits with an exact vmcnt.
   for (int b = 0; b < nb; b += 2) {
-    // segment b is in A
-    if (b + 1 < nb) {
-      p_seg_issue<Q8, NB>(p, g, ci, B);
-      p_seg_compute<Q8, NB>(p, g, cc, A, xs, xr, xreg, red, acc);
-    } else {
-      p_seg_compute<Q8, NB>(p, g, cc, A, xs, xr, xreg, red, acc);
-      break;
-    }
-    // segment b + 1 is in B; A is free
-    if (b + 2 < nb) p_seg_issue<Q8, NB>(p, g, ci, A);
+    p_seg_issue<Q8, NB>(p, g, ci, B);
+    p_seg_compute<Q8, NB>(p, g, cc, A, xs, xr, xreg, red, acc);
+    if (b + 1 >= nb) break;
+    p_seg_issue<Q8, NB>(p, g, ci, A);
     p_seg_compute<Q8, NB>(p, g, cc, B, xs, xr, xreg, red, acc);
   }
   __syncthreads();
@@ -692,14 +726,35 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
       }
     }
-    // 2. q of the group's heads and (chunk of pos) the new K and V rows.
-    for (int i = tid; i < kvm * HD; i += kPThreads)
-      qs[i] = poll_tagged(a, a.q + static_cast<size_t>(g) * kvm * HD + i, tag);
-    if (own_pos) {
-      for (int i = tid; i < 2 * HD; i += kPThreads) {
-        const tagged_t* src = i < HD ? a.knew : a.vnew;
-        const int d = i < HD ? i : i - HD;
-        kp[i] = poll_tagged(a, src + static_cast<size_t>(g) * HD + d, tag);  // kp, then vp
+    // 2. q of the group's heads and (chunk of pos) the new K and V rows, polled
+    //    together (element e < kvm * HD is q, the next 2 * HD are K then V).
+    {
+      const int nq = kvm * HD, ne = nq + (own_pos ? 2 * HD : 0);
+      const tagged_t* qg = a.q + static_cast<size_t>(g) * kvm * HD;
+      auto addr = [&](int e) -> const tagged_t* {
+        if (e < nq) return qg + e;
+        e -= nq;
+        return (e < HD ? a.knew : a.vnew) + static_cast<size_t>(g) * HD + (e < HD ? e : e - HD);
+      };
+      for (int e0 = tid; e0 < ne; e0 += 4 * kPThreads) {
+        tagged_t v[4];
+        unsigned int valid = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int e = e0 + k * kPThreads;
+          if (e < ne) valid |= 1u << k;
+          v[k] = g_ld64(addr(e < ne ? e : 0));
+        }
+        poll_many<4>(a, tag, [&](int k) {
+          const int e = e0 + k * kPThreads;
+          return addr(e < ne ? e : 0);
+        }, valid, v);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int e = e0 + k * kPThreads;
+          if (e < nq) qs[e] = val_of(v[k]);
+          else if (e < ne) kp[e - nq] = val_of(v[k]);  // kp, then vp
+        }
       }
     }
     __syncthreads();
@@ -853,8 +908,10 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     float* mls = lds;  // [nsplit][kvm][2]
     for (int i = tid; i < nsplit * kvm; i += kPThreads) {
       const tagged_t* pk = pg + static_cast<size_t>(i) * (HD + 2);
-      mls[2 * i] = poll_tagged(a, pk + HD, tag);
-      mls[2 * i + 1] = poll_tagged(a, pk + HD + 1, tag);
+      tagged_t v[2] = {g_ld64(pk + HD), g_ld64(pk + HD + 1)};
+      poll_many<2>(a, tag, [&](int k) { return pk + HD + k; }, 3u, v);
+      mls[2 * i] = val_of(v[0]);
+      mls[2 * i + 1] = val_of(v[1]);
     }
     __syncthreads();
     tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
@@ -863,10 +920,28 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
       float M = -INFINITY;
       for (int k = 0; k < nsplit; ++k) M = fmaxf(M, mls[2 * (k * kvm + h)]);
       float L = 0.f, O = 0.f;
-      for (int k = 0; k < nsplit; ++k) {
-        const float w = expf(mls[2 * (k * kvm + h)] - M);
-        L += mls[2 * (k * kvm + h) + 1] * w;
-        O += poll_tagged(a, pg + (static_cast<size_t>(k) * kvm + h) * (HD + 2) + d, tag) * w;
+      // The chunks' partial outputs, 8 at a time, polled together.
+      for (int k0 = 0; k0 < nsplit; k0 += 8) {
+        auto addr = [&](int k) {
+          const int kk = k0 + k < nsplit ? k0 + k : 0;
+          return pg + (static_cast<size_t>(kk) * kvm + h) * (HD + 2) + d;
+        };
+        tagged_t v[8];
+        unsigned int valid = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (k0 + k < nsplit) valid |= 1u << k;
+          v[k] = g_ld64(addr(k));
+        }
+        poll_many<8>(a, tag, addr, valid, v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (k0 + k < nsplit) {
+            const float w = expf(mls[2 * ((k0 + k) * kvm + h)] - M);
+            L += mls[2 * ((k0 + k) * kvm + h) + 1] * w;
+            O += val_of(v[k]) * w;
+          }
+        }
       }
       g_st_tagged(outg + h * HD + d, O / L, tag);
     }

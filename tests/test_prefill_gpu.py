@@ -1,0 +1,220 @@
+"""Batched prompt prefill: the MFMA GEMM, batched RoPE and causal attention
+ops, and kl_engine_prefill, against the CPU oracle (which, like the
+reference, runs the prompt token by token).
+
+Bars: GEMM rows within the fp32 GEMV bound of the oracle's MatmulKernel on the
+same row; RoPE rows bit-exact (elementwise); attention within 2e-5 of the
+oracle's MHA at each position; whole-prompt logits within 1e-4 relative
+(max |gpu - cpu| / max |cpu|) and the greedy tokens identical.  At full size
+(cfg 5: 512-token prompt, cfg 4: 4000-position fill) the oracle is too slow
+for the whole prompt, so the prefill is checked against the engine's own
+step-by-step path, which the decode tests pin to the oracle.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_RTOL = 1e-4
+
+
+def D(K, a):
+    return K.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+def ok(rc, what="call"):
+    assert rc == 0, f"{what}: rc={rc}"
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def gemm(K, A, W, bias=None, C0=None):
+    M, Kd = A.shape
+    N = W.shape[0]
+    dA, dW = D(K, A), D(K, W)
+    dC = D(K, C0) if C0 is not None else K.DeviceArray(M * N)
+    db = D(K, bias) if bias is not None else None
+    ok(K.lib.kl_gemm_f32(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, Kd, Kd, N, db.ptr if db else None,
+                         int(C0 is not None), None), "kl_gemm_f32")
+    return dC.numpy().reshape(M, N)
+
+
+# ---------------------------------------------------------------- GEMM ------
+def test_gemm_kat_exact(K, O, gpu):
+    # test_load.cpp:49-105 and test_cu_matmul.cpp's 4x4 arange, as GEMM rows.
+    W = np.arange(2048, dtype=np.float32).reshape(16, 128)
+    y = gemm(K, np.ones((3, 128), np.float32), W)
+    for r in range(3):
+        for i, v in {0: 8128, 1: 24512, 14: 237504, 15: 253888}.items():
+            assert y[r, i] == v
+    W4 = np.arange(16, dtype=np.float32).reshape(4, 4)
+    y = gemm(K, np.arange(4, dtype=np.float32).reshape(1, 4), W4)
+    assert list(y[0]) == [14, 38, 62, 86]
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 3, 4), (5, 37, 12), (64, 64, 64), (77, 300, 256),
+                                    (512, 1024, 2560), (130, 2560, 4096), (512, 9728, 512),
+                                    (1000, 256, 1536)])
+def test_gemm_vs_oracle_rows(K, O, gpu, M, N, Kd):
+    rng = np.random.default_rng(M * 7 + N + Kd)
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    W = (rng.standard_normal((N, Kd)) * 0.02).astype(np.float32)
+    y = gemm(K, A, W)
+    rows = sorted(set(np.linspace(0, M - 1, min(M, 24)).astype(int)))
+    for m in rows:
+        ref = O.gemv_f32(A[m], W)
+        tol = 4e-7 * np.sqrt(Kd) * (np.abs(W) @ np.abs(A[m])).max() + 1e-30
+        assert np.max(np.abs(y[m] - ref)) <= tol, (m, np.max(np.abs(y[m] - ref)), tol)
+
+
+def test_gemm_bias_and_accumulate(K, O, gpu):
+    rng = np.random.default_rng(5)
+    M, N, Kd = 70, 200, 96
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    W = rng.standard_normal((N, Kd)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    yb = gemm(K, A, W, bias=b)      # matmul.cpp:74-77: y = W x, then y += b
+    ya = gemm(K, A, W, C0=C0)       # llama3.cpp:682-683: x = x + W x'
+    for m in range(M):
+        g = O.gemv_f32(A[m], W)
+        tol = 4e-7 * np.sqrt(Kd) * (np.abs(W) @ np.abs(A[m])).max()
+        assert np.max(np.abs(yb[m] - O.add(g, b))) <= tol + 1e-6
+        assert np.max(np.abs(ya[m] - O.add(C0[m], g))) <= tol + 1e-6
+
+
+def test_gemm_rejects_unaligned_k(K, gpu):
+    buf = K.DeviceArray(64)
+    assert K.lib.kl_gemm_f32(buf.ptr, buf.ptr, buf.ptr, 2, 2, 3, 3, 3, 2, None, 0, None) == -4
+    assert K.lib.kl_gemm_f32(buf.ptr, buf.ptr, buf.ptr, 0, 2, 4, 4, 4, 2, None, 0, None) == -1
+
+
+# ---------------------------------------------------------------- RoPE ------
+@pytest.mark.parametrize("style,dim,kv,hd,pos0,n", [(0, 768, 768, 64, 0, 16), (1, 2048, 512, 64, 5, 33),
+                                                    (1, 4096, 1024, 128, 0, 70)])
+def test_rope_rows_bit_exact(K, O, gpu, style, dim, kv, hd, pos0, n):
+    S = pos0 + n
+    s, c = O.sincos_table(hd, S, 1e4 if style == 0 else 1e6)
+    rng = np.random.default_rng(dim + n)
+    q = rng.standard_normal((n, dim)).astype(np.float32)
+    k = rng.standard_normal((n, kv)).astype(np.float32)
+    dq, dk, dsn, dcs = D(K, q), D(K, k), D(K, s), D(K, c)
+    ok(K.lib.kl_rope_rows(style, dim, kv, hd, dq.ptr, dim, dk.ptr, kv, pos0, n, dsn.ptr, dcs.ptr,
+                          None))
+    gq, gk = dq.numpy().reshape(n, dim), dk.numpy().reshape(n, kv)
+    for r in range(n):
+        rq, rk = O.rope(style, dim, kv, hd, q[r], k[r], pos0 + r, s, c)
+        assert np.array_equal(gq[r], rq) and np.array_equal(gk[r], rk), r
+
+
+# ----------------------------------------------------------- attention ------
+@pytest.mark.parametrize("H,kvm,hd,S,pos0,n", [(12, 1, 64, 160, 0, 143), (32, 4, 128, 256, 0, 200),
+                                              (4, 2, 32, 80, 17, 50), (12, 6, 128, 4096, 3900, 100),
+                                              (8, 8, 64, 70, 0, 1)])
+def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
+    rng = np.random.default_rng(H * S + pos0 + n)
+    kvd = H // kvm * hd
+    kc = rng.standard_normal((1, S, kvd)).astype(np.float32)
+    vc = rng.standard_normal((1, S, kvd)).astype(np.float32)
+    q = rng.standard_normal((n, H * hd)).astype(np.float32)
+    dk, dv, dq, do = D(K, kc.ravel()), D(K, vc.ravel()), D(K, q), K.DeviceArray(n * H * hd)
+    ok(K.lib.kl_attn_prefill(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd, do.ptr,
+                             H * hd, None), "kl_attn_prefill")
+    out = do.numpy().reshape(n, H * hd)
+    rows = sorted(set(np.linspace(0, n - 1, min(n, 16)).astype(int)))
+    for r in rows:
+        ref = O.mha(pos0 + r, H, 0, S, kvd, kvm, hd, q[r], kc, vc)
+        assert np.max(np.abs(out[r] - ref)) < 2e-5, r
+    if pos0 == 0:  # position 0 attends only key 0: V0 exactly up to the 1/l factor (l = 1)
+        for h in range(H):
+            g = h // kvm
+            assert np.allclose(out[0, h * hd:(h + 1) * hd], vc[0, 0, g * hd:(g + 1) * hd], rtol=0,
+                               atol=1e-7)
+
+
+# ------------------------------------------------------- whole prompt -------
+FP32_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3"]
+
+
+@pytest.mark.parametrize("name", FP32_TINY)
+def test_engine_prefill_vs_oracle(K, O, gpu, name):
+    cfg = K.TINY[name]
+    img = K.synth_image(cfg)
+    P = min(40, cfg.seq_len - 10)
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    eng = K.Engine(img, cfg)
+    nxt, lg, ms = eng.prefill(prompt)
+    om = O.Model(img, cfg.family, cfg.quant)
+    for pos in range(P - 1):
+        om.step(prompt[pos], pos)
+    ref = om.step(prompt[P - 1], P - 1)
+    r = rel(lg, ref)
+    print(f"{name}: prefill P={P} logits rel err {r:.2e}, {ms:.3f} ms", flush=True)
+    assert r < LOGIT_RTOL
+    assert nxt == int(np.argmax(lg))
+    want = O.argmax(ref)
+    if nxt != want:
+        assert abs(float(ref[nxt]) - float(ref[want])) <= LOGIT_RTOL * np.max(np.abs(ref))
+    # The cache rows the prefill wrote are the ones the step path writes.
+    for layer in (0, cfg.layers - 1):
+        for pos in (0, P // 2, P - 1):
+            for which_v in (False, True):
+                a, b = eng.kv_row(layer, pos, which_v), om.kv_row(layer, pos, which_v)
+                assert np.max(np.abs(a - b)) <= 1e-5 * max(np.max(np.abs(b)), 1.0)
+    # Decoding continues from the prefilled cache (teacher-forced on the oracle's tokens).
+    tok = want
+    for pos in range(P, P + 4):
+        n2, lg2 = eng.step(tok, pos)
+        ref2 = om.step(tok, pos)
+        assert rel(lg2, ref2) < LOGIT_RTOL
+        tok = O.argmax(ref2)
+
+
+@pytest.mark.parametrize("name", FP32_TINY)
+def test_generate_with_prefill_matches_oracle(K, O, gpu, name):
+    cfg = K.TINY[name]
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg, 12)
+    eng = K.Engine(img, cfg)
+    eng.set_prefill(True)
+    got, _ = eng.generate(prompt, 10)
+    want = O.Model(img, cfg.family, cfg.quant).generate(prompt, 10)
+    assert list(got) == list(want)
+
+
+def test_prefill_unsupported_for_int8(K, gpu):
+    cfg = K.TINY["tiny_q8"]
+    eng = K.Engine(K.synth_image(cfg), cfg)
+    assert K.lib.kl_engine_set_prefill(eng.handle, 1) == -4
+    p = np.ascontiguousarray(K.prompt_tokens(cfg, 4), np.int32)
+    assert K.lib.kl_engine_prefill(eng.handle, p.ctypes.data, 4, None, None, None) == -4
+
+
+@pytest.mark.parametrize("name,P", [("qwen3_4b", 512), ("qwen25_15b", 4000)])
+def test_full_size_prefill_vs_steps(K, gpu, name, P):
+    cfg = K.BASELINE[name]
+    img = K.synth_image(cfg)
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    eng = K.Engine(img, cfg)
+    nxt, lg, ms = eng.prefill(prompt)
+    print(f"{name}: prefill of {P} tokens in {ms:.1f} ms", flush=True)
+    ref_eng = K.Engine(img, cfg)
+    for pos in range(P - 1):
+        ref_eng.step(prompt[pos], pos, want_logits=False)
+    n_ref, ref = ref_eng.step(prompt[P - 1], P - 1)
+    r = rel(lg, ref)
+    print(f"{name}: logits rel err vs step path {r:.2e}", flush=True)
+    assert r < LOGIT_RTOL
+    if nxt != n_ref:
+        assert abs(float(ref[nxt]) - float(ref[n_ref])) <= LOGIT_RTOL * np.max(np.abs(ref))
+    # Both continue identically for a few decode steps from the same token.
+    tok = n_ref
+    for pos in range(P, P + 3):
+        a, la = eng.step(tok, pos)
+        b, lb = ref_eng.step(tok, pos)
+        assert rel(la, lb) < LOGIT_RTOL
+        tok = b
