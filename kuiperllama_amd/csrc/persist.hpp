@@ -9,10 +9,12 @@
 // Why persistent: a decode step of Llama-3.2-1B streams 4.9 GB of weights in
 // 81 GEMV-shaped pieces, most of them 17-67 MB.  As separate kernels each pays
 // a launch, a ramp-up and a drain, and the small ones never reach full HBM
-// bandwidth.  Here every wave keeps streaming: weights do not depend on
-// activations, so each wave issues the loads of its first batch of the NEXT
-// GEMV phase before it waits for that phase's input (and across the attention
-// phase).
+// bandwidth.  Here the 81 phases follow each other inside one launch, and a
+// workgroup starts a phase the moment its input vector is complete (no grid
+// barrier), so the chip streams weights nearly continuously.  The phase's first
+// weight loads are issued right after its input is staged, not before the wait:
+// a burst of every workgroup's prefetch at each hand-off was measured to delay
+// the hand-off itself by more than it saved.
 //
 // Dataflow hand-off, no grid barriers.  Every activation that crosses
 // workgroups (q, the new K and V rows, the attention output, the residual
@@ -248,16 +250,16 @@ __device__ __forceinline__ float block_sum_p(float v, float* red) {
 // polled until they carry `tag`), or the embedding row `emb_row` when src is
 // null; applies RMSNorm when `nw` is set:
 // y = w * (x * (1 / sqrt(mean(x^2) + eps))) (kernels/cpu/rmsnorm_kernel.cpp:30-32).
-// `prefetch()` issues the phase's first weight segment; it runs after the
-// first round of input loads is issued and before their results are used, so
-// waiting for the input never waits for the weights (loads complete in
-// order).  Ends with a workgroup barrier.
-template <class Prefetch>
+// No weight loads are in flight while the input is polled: the phase's first
+// weight segment is issued after the staging (measured: issuing it before
+// the wait slows the hand-off more than it saves, because every workgroup's
+// burst of prefetches queues ahead of the polls in the memory system).
+// Ends with a workgroup barrier.
 __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, unsigned int tag,
                                           const float* emb_row, const float* nw, float eps, int n,
-                                          float* xs, float* red, Prefetch prefetch) {
+                                          float* xs, float* red) {
   float ss = 0.f;
-  float wv[8];  // norm weights of the first round, loaded before the prefetch
+  float wv[8];  // norm weights of the first round
   for (int b0 = 0; b0 < n; b0 += kPThreads * 8) {
     tagged_t v[8];
 #pragma unroll
@@ -268,19 +270,12 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
       else
         v[k] = (static_cast<tagged_t>(tag) << 32) | __float_as_uint(i < n ? g_rd(emb_row + i) : 0.f);
     }
-    if (b0 == 0) {
-      if (nw) {
+    if (b0 == 0 && nw) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int i = k * kPThreads + threadIdx.x;
-          wv[k] = g_rd(nw + (i < n ? i : 0));
-        }
+      for (int k = 0; k < 8; ++k) {
+        const int i = k * kPThreads + threadIdx.x;
+        wv[k] = g_rd(nw + (i < n ? i : 0));
       }
-      // Keep the prefetch behind the input and norm-weight loads: loads
-      // complete in order, so using those never waits for the weights.
-      __builtin_amdgcn_sched_barrier(0);
-      prefetch();
-      __builtin_amdgcn_sched_barrier(0);
     }
     if (src) {
       unsigned int valid = 0;
@@ -554,7 +549,7 @@ __device__ __forceinline__ void p_seg_compute(PGp p, const PGeom& g, PCur& c,
 }
 
 // Runs the streaming loop of one phase.  On entry, buffer A holds (in flight)
-// the wave's first segment of p (issued by stage_vec); B is the second buffer.  Only A is live
+// the wave's first segment of p; B is the second buffer.  Only A is live
 // outside this function.  Returns with LDS `red` holding every finished row
 // of the workgroup (after a workgroup barrier).
 template <bool Q8, int NB>
@@ -622,8 +617,8 @@ __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul, int G) {
 // What the attention of a layer needs that does not depend on the layer's
 // QKV output: this workgroup's first chunk of cached K and V rows, and the
 // Qwen3 q/k norm weights it applies.  Loaded at the start of the QKV phase, so
-// the loads complete while the QKV weights stream instead of queueing behind
-// the next phase's prefetch when attention starts.
+// the loads complete while the QKV weights stream instead of adding a round
+// trip when attention starts.
 template <int HD>
 struct AttnPre {
   static constexpr int NP = attn_chunk(HD) / attn_p_rpp(HD);
@@ -1042,11 +1037,12 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     const unsigned int tag_in = epoch * kTagLayers + p->in_layer + 1;
     const unsigned int tag = epoch * kTagLayers + p->layer + 1;
     if ((k & 3) == 0 && !is_cls) attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
-    stage_vec(a, p->in, tag_in, emb_row, p->norm, a.eps, p->cols, xs, sred, [&]() {
+    stage_vec(a, p->in, tag_in, emb_row, p->norm, a.eps, p->cols, xs, sred);
+    trace_mark(a, slot++);
+    {
       PCur c0{0, 0, 0};
       p_seg_issue<Q8, NB>(p, g, c0, A);
-    });
-    trace_mark(a, slot++);
+    }
     p_stream<Q8, NB>(p, g, A, xs, red);
     if (is_cls) {
       // Logits (plain stores, read by the host after the launch) and this
