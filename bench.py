@@ -69,6 +69,29 @@ def measured_traffic(kernel: str, config: str, mode: str):
     return None, None
 
 
+MFMA_FP32_PEAK_TFLOPS = 157.3
+
+
+def measure_prefill(K, cfg, reps: int = 3) -> dict:
+    """Batched prefill of the config's prompt (kl_engine_prefill), device time
+    from HIP events inside the call; best of `reps` after one warm-up.  The
+    roofline is the fp32 matrix-core peak."""
+    img = K.synth_image(cfg)
+    eng = K.Engine(img, cfg)
+    prompt = K.prompt_tokens(cfg)
+    P = len(prompt)
+    eng.prefill(prompt, want_logits=False)
+    times = [eng.prefill(prompt, want_logits=False)[2] for _ in range(reps)]
+    ms = min(times)
+    fl = cfg.prefill_flops(P)
+    tf = fl / (ms / 1e3) / 1e12
+    return {"config": cfg.name, "tokens": P, "ms": round(ms, 3),
+            "tok_s": round(P / (ms / 1e3), 1), "tflops": round(tf, 2),
+            "bound": "mfma", "peak_tflops": MFMA_FP32_PEAK_TFLOPS,
+            "frac": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "flops": int(fl),
+            "dtype": "f32"}
+
+
 def cpu_baseline(K, cfg, img, seconds: float) -> dict:
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -111,6 +134,9 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--mode", choices=("persistent", "multi"), default="persistent")
+    ap.add_argument("--prefill-config", default="",
+                    help="also time the batched prefill of this config's prompt (e.g. qwen3_4b: "
+                         "512 tokens) and report it under 'prefill'")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy, the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -184,6 +210,12 @@ def main() -> int:
     print("# per-launch avg ms: " + ", ".join(f"{k} {v[0]:.4f} x{v[1]}" for k, v in prof.items() if v[1])
           + f"; step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
 
+    prefill = None
+    if args.prefill_config:
+        del eng
+        prefill = measure_prefill(K, K.BASELINE[args.prefill_config])
+        print(f"# prefill {prefill}", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(K, cfg, img, args.cpu_seconds)
@@ -233,6 +265,8 @@ def main() -> int:
         "launch_ms": {k: round(v[0], 5) for k, v in prof.items() if v[1]},
         "cpu_baseline": cpu,
     }
+    if prefill is not None:
+        out["prefill"] = prefill
     print(json.dumps(out), flush=True)
     return 0
 

@@ -92,6 +92,17 @@ class Config:
         plus the new row written."""
         return 2 * self.layers * self.kv_dim * 4 * (pos + 1) + 2 * self.layers * self.kv_dim * 4
 
+    def prefill_flops(self, n: int) -> int:
+        """Algorithmic FLOPs of a batched prefill of positions 0 .. n-1: the
+        seven projections of every layer on n rows (2 flops per weight per
+        row), causal attention (q.k and p.v over t <= position: 4 * heads *
+        head_size * (pos + 1) per position and layer) and the classifier of
+        the last position."""
+        D, Dq, Dkv, F, L = self.dim, self.qd, self.kv_dim, self.hidden_dim, self.layers
+        proj = L * (Dq * D + 2 * Dkv * D + D * Dq + 3 * F * D)
+        attn = L * 4 * self.heads * self.head_size * (n * (n + 1) // 2)
+        return 2 * proj * n + attn + 2 * self.vocab * D
+
     def decode_bytes(self, first_pos: int, steps: int) -> int:
         """Algorithmic HBM bytes of `steps` decode steps at positions
         first_pos .. first_pos + steps - 1."""

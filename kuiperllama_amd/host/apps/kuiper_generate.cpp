@@ -1,0 +1,285 @@
+// kuiper_generate: the generate/serve driver of the reference demos
+// (demo/main.cpp:5-47, demo/main_qwen.cpp:198-284 and :404-452) on the
+// MI355X backend, through the C++ host API (model::Model on kDeviceHIP).
+//
+// Prompts and responses are token ids (no tokenizer in this backend):
+//
+//   kuiper_generate [options] <model.bin> <ids> [max_new_tokens]
+//       ids: comma- or space-separated prompt token ids.  Prints
+//       [RESPONSE_START] / generated ids / [RESPONSE_END] on stdout and
+//       [STATS] steps=.. duration=.. steps_per_s=.. on stderr.
+//   kuiper_generate --serve [options] <model.bin> [max_new_tokens]
+//       prints [READY]; then for each block of lines between [PROMPT_START]
+//       and [PROMPT_END] (token ids) prints one response as above; [EXIT] or
+//       end of input stops.
+//
+// Options: --family llama2|llama3|qwen2|qwen3 (default llama2), --quant (int8
+// image), --layered (the layer-by-layer path instead of the fused engine),
+// --prefill (the whole prompt in one batched pass; fused only), --eos ID
+// (end-of-sequence id, repeatable).
+//
+// Generation follows main_qwen.cpp: prompt positions advance without
+// sampling; in the decode phase only, generation stops at an end-of-sequence
+// id, after 24 identical tokens in a row, or when the last 12 tokens repeat
+// the 12 before them.  (The reference's rule on decoded tail text needs a
+// tokenizer and is not applied.)
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <iostream>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "kuiper/model.h"
+
+namespace {
+
+struct Options {
+  model::ModelFamily family = model::ModelFamily::kLlama2;
+  bool quant = false;
+  bool layered = false;
+  bool prefill = false;
+  std::vector<int32_t> eos;
+};
+
+struct GenerationResult {
+  std::vector<int32_t> response;
+  int32_t steps = 0;
+};
+
+std::vector<int32_t> parse_ids(const std::string& text, bool* ok) {
+  std::vector<int32_t> ids;
+  std::string t = text;
+  for (char& c : t)
+    if (c == ',') c = ' ';
+  std::istringstream in(t);
+  std::string w;
+  *ok = true;
+  while (in >> w) {
+    char* end = nullptr;
+    const long v = std::strtol(w.c_str(), &end, 10);
+    if (*end != '\0' || v < 0 || v > 0x7fffffffL) {
+      *ok = false;
+      return {};
+    }
+    ids.push_back(static_cast<int32_t>(v));
+  }
+  return ids;
+}
+
+// main_qwen.cpp:198-284 with token ids.
+GenerationResult generate(const model::Model& m, const std::vector<int32_t>& prompt, int max_new,
+                          bool use_prefill) {
+  GenerationResult r;
+  const int32_t P = static_cast<int32_t>(prompt.size());
+  const int32_t total_steps =
+      std::min<int32_t>(P + std::max(1, max_new), m.config().seq_len_);
+  tensor::Tensor pos_tensor = m.get_buffer(model::ModelBufferType::kInputPos);
+  std::vector<int32_t> words(prompt.begin(), prompt.begin() + 1);
+  int32_t pos = 0, next = prompt[0], last = -1, same_run = 0;
+  bool is_prompt = true;
+  if (use_prefill && P >= 2) {
+    // The prompt in one batched pass: the loop resumes at the first sampled
+    // token, as if positions 0 .. P-1 had run one by one.
+    int nx = -1;
+    STATUS_CHECK(m.prefill(prompt, nx));
+    words.assign(prompt.begin(), prompt.end());
+    next = nx;
+    pos = P;
+    is_prompt = false;
+    if (!m.is_sentence_ending(next)) {
+      words.push_back(next);
+      r.response.push_back(next);
+      last = next;
+      same_run = 1;
+    } else {
+      r.steps = pos;
+      return r;
+    }
+  } else {
+    const op::EmbeddingOutput prompt_embedding = m.embedding(prompt);
+    while (pos < total_steps && pos < P - 1) {
+      pos_tensor.index<int32_t>(0) = pos;
+      STATUS_CHECK(m.predict(m.fill_input(pos_tensor, prompt_embedding, true), pos_tensor, true,
+                             next));
+      next = prompt[pos + 1];
+      words.push_back(next);
+      ++pos;
+    }
+  }
+  while (pos < total_steps) {
+    pos_tensor.index<int32_t>(0) = pos;
+    is_prompt = false;
+    const op::EmbeddingOutput emb = m.embedding({next});
+    STATUS_CHECK(m.predict(m.fill_input(pos_tensor, emb, false), pos_tensor, false, next));
+    if (m.is_sentence_ending(next)) break;
+    words.push_back(next);
+    r.response.push_back(next);
+    // 1) the same token 24 times in a row
+    if (next == last) {
+      ++same_run;
+    } else {
+      last = next;
+      same_run = 1;
+    }
+    if (same_run >= 24) break;
+    // 3) the last 12 tokens repeat the 12 before them
+    constexpr int kRepeatWindow = 12;
+    if (words.size() >= static_cast<size_t>(P + kRepeatWindow * 2)) {
+      bool repeated = true;
+      auto e = words.end();
+      for (int i = 0; i < kRepeatWindow && repeated; ++i)
+        repeated = *(e - 1 - i) == *(e - 1 - kRepeatWindow - i);
+      if (repeated) break;
+    }
+    ++pos;
+  }
+  (void)is_prompt;
+  r.steps = pos;
+  return r;
+}
+
+// main_qwen.cpp:378-387
+void print_result(const GenerationResult& r, double duration_sec, bool print_stats) {
+  const double sps = duration_sec > 0 ? static_cast<double>(r.steps) / duration_sec : 0.0;
+  std::printf("[RESPONSE_START]\n");
+  for (size_t i = 0; i < r.response.size(); ++i)
+    std::printf("%s%d", i ? " " : "", r.response[i]);
+  std::printf("\n[RESPONSE_END]\n");
+  std::fflush(stdout);
+  if (print_stats) {
+    std::fprintf(stderr, "[STATS] steps=%d duration=%.6f steps_per_s=%.6f\n", r.steps,
+                 duration_sec, sps);
+    std::fflush(stderr);
+  }
+}
+
+std::unique_ptr<model::Model> load(const std::string& path, const Options& o) {
+  std::unique_ptr<model::Model> m;
+  switch (o.family) {
+    case model::ModelFamily::kQwen2:
+      m = std::make_unique<model::Qwen2Model>(base::TokenizerType::kEncodeBpe, "", path, o.quant);
+      break;
+    case model::ModelFamily::kQwen3:
+      m = std::make_unique<model::Qwen3Model>(base::TokenizerType::kEncodeBpe, "", path, o.quant);
+      break;
+    default:
+      m = std::make_unique<model::LLama2Model>(base::TokenizerType::kEncodeSpe, "", path, o.quant,
+                                               o.family);
+  }
+  const base::Status s = m->init(base::DeviceType::kDeviceHIP);
+  if (!s) {
+    std::fprintf(stderr, "kuiper_generate: init failed (%d): %s\n", int(s), s.get_err_msg().c_str());
+    return nullptr;
+  }
+  if (!o.layered) STATUS_CHECK(m->set_fused(true));
+  m->set_eos_tokens(o.eos);
+  return m;
+}
+
+int usage(const char* prog) {
+  std::fprintf(stderr,
+               "Usage:\n  %s [options] <model.bin> <ids> [max_new_tokens]\n"
+               "  %s --serve [options] <model.bin> [max_new_tokens]\n"
+               "Options: --family llama2|llama3|qwen2|qwen3, --quant, --layered, --prefill, "
+               "--eos ID\n",
+               prog, prog);
+  return 2;
+}
+
+int parse_max(const char* s) {
+  const int v = std::atoi(s);
+  return v > 0 ? v : 128;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  Options o;
+  bool serve = false;
+  std::vector<std::string> pos_args;
+  for (int i = 1; i < argc; ++i) {
+    const std::string a = argv[i];
+    if (a == "--serve") {
+      serve = true;
+    } else if (a == "--quant") {
+      o.quant = true;
+    } else if (a == "--layered") {
+      o.layered = true;
+    } else if (a == "--prefill") {
+      o.prefill = true;
+    } else if (a == "--eos" && i + 1 < argc) {
+      o.eos.push_back(std::atoi(argv[++i]));
+    } else if (a == "--family" && i + 1 < argc) {
+      const std::string f = argv[++i];
+      if (f == "llama2") o.family = model::ModelFamily::kLlama2;
+      else if (f == "llama3") o.family = model::ModelFamily::kLlama3;
+      else if (f == "qwen2") o.family = model::ModelFamily::kQwen2;
+      else if (f == "qwen3") o.family = model::ModelFamily::kQwen3;
+      else return usage(argv[0]);
+    } else if (a.size() > 2 && a[0] == '-' && a[1] == '-') {
+      return usage(argv[0]);
+    } else {
+      pos_args.push_back(a);
+    }
+  }
+  if (o.prefill && o.layered) {
+    std::fprintf(stderr, "kuiper_generate: --prefill runs on the fused engine, not --layered\n");
+    return 2;
+  }
+  if (serve) {
+    if (pos_args.empty() || pos_args.size() > 2) return usage(argv[0]);
+    const int max_steps = pos_args.size() == 2 ? parse_max(pos_args[1].c_str()) : 128;
+    auto m = load(pos_args[0], o);
+    if (!m) return 1;
+    if (o.prefill) STATUS_CHECK(m->set_prefill(true));
+    std::cout << "[READY]" << std::endl;
+    std::string line;
+    while (std::getline(std::cin, line)) {
+      if (line == "[EXIT]") break;
+      if (line != "[PROMPT_START]") continue;
+      std::string text;
+      bool has_end = false;
+      while (std::getline(std::cin, line)) {
+        if (line == "[PROMPT_END]") {
+          has_end = true;
+          break;
+        }
+        text += " " + line;
+      }
+      if (!has_end) break;
+      bool ok = false;
+      const std::vector<int32_t> prompt = parse_ids(text, &ok);
+      if (!ok || prompt.empty()) {
+        std::printf("[ERROR] the prompt must be token ids\n");
+        std::fflush(stdout);
+        continue;
+      }
+      const auto t0 = std::chrono::steady_clock::now();
+      const GenerationResult r = generate(*m, prompt, max_steps, o.prefill);
+      const double dt =
+          std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+      print_result(r, dt, false);
+    }
+    return 0;
+  }
+  if (pos_args.size() < 2 || pos_args.size() > 3) return usage(argv[0]);
+  bool ok = false;
+  const std::vector<int32_t> prompt = parse_ids(pos_args[1], &ok);
+  if (!ok || prompt.empty()) {
+    std::fprintf(stderr, "kuiper_generate: the prompt must be token ids\n");
+    return 2;
+  }
+  const int max_steps = pos_args.size() == 3 ? parse_max(pos_args[2].c_str()) : 128;
+  auto m = load(pos_args[0], o);
+  if (!m) return 1;
+  if (o.prefill) STATUS_CHECK(m->set_prefill(true));
+  const auto t0 = std::chrono::steady_clock::now();
+  const GenerationResult r = generate(*m, prompt, max_steps, o.prefill);
+  const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  print_result(r, dt, true);
+  return 0;
+}

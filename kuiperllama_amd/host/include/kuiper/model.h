@@ -131,6 +131,15 @@ class Model {
   // sampled tokens written to out (fused: entirely on the device).
   base::Status generate(const std::vector<int32_t>& prompt, int32_t n_new,
                         std::vector<int32_t>& out) const;
+  // Fused only: the whole prompt in one batched pass (kl_engine_prefill);
+  // next receives the greedy token after the prompt and kForwardOutput the
+  // logits of its last position.  Decoding continues with predict() at
+  // position prompt.size().  generate() uses it when set_prefill(true).
+  base::Status prefill(const std::vector<int32_t>& prompt, int& next) const;
+  base::Status set_prefill(bool enable);
+  // End-of-sequence ids for is_sentence_ending() (the tokenizer's EOS in the
+  // reference, encode.cpp; here given explicitly since prompts are ids).
+  void set_eos_tokens(std::vector<int32_t> ids) { eos_tokens_ = std::move(ids); }
   std::shared_ptr<kernel::HipConfig> hip_config() const { return hip_config_; }
 
  protected:
@@ -164,6 +173,8 @@ class Model {
   std::shared_ptr<kernel::HipConfig> hip_config_;
   std::unique_ptr<DecoderLayers> layers_;
   bool fused_ = false;
+  bool prefill_ = false;
+  std::vector<int32_t> eos_tokens_;
   kl_engine* engine_ = nullptr;
 };
 

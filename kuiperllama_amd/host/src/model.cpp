@@ -671,7 +671,41 @@ base::Status Model::generate(const std::vector<int32_t>& prompt, int32_t n_new,
   return base::error::Success();
 }
 
-bool Model::is_sentence_ending(int32_t) const { return false; }
+base::Status Model::set_prefill(bool enable) {
+  if (enable && !fused_) return base::error::InvalidArgument("prefill needs set_fused(true)");
+  const int rc = kl_engine_set_prefill(engine_, enable ? 1 : 0);
+  if (rc != KL_OK)
+    return base::error::FunctionNotImplement(std::string("kl_engine_set_prefill: ") +
+                                             kl_error_string(rc));
+  prefill_ = enable;
+  return base::error::Success();
+}
+
+base::Status Model::prefill(const std::vector<int32_t>& prompt, int& next) const {
+  if (!fused_ || !engine_) return base::error::InvalidArgument("prefill needs set_fused(true)");
+  if (prompt.empty() || static_cast<int32_t>(prompt.size()) > config_->seq_len_)
+    return base::error::InvalidArgument("The prompt does not fit the sequence length.");
+  int32_t nx = -1;
+  int rc = kl_engine_prefill(engine_, prompt.data(), static_cast<int>(prompt.size()), &nx, nullptr,
+                             nullptr);
+  if (rc != KL_OK)
+    return base::error::InternalError(std::string("kl_engine_prefill: ") + kl_error_string(rc));
+  const float* d_logits = nullptr;
+  kl_engine_buffers(engine_, &d_logits, nullptr, nullptr);
+  const tensor::Tensor& out = get_buffer(ModelBufferType::kForwardOutput);
+  rc = kl_memcpy_d2d(const_cast<float*>(out.ptr<float>()), d_logits, out.byte_size(),
+                     hip_config_->stream);
+  if (rc == KL_OK) rc = kl_stream_sync(hip_config_->stream);
+  if (rc != KL_OK) return base::error::InternalError("logits copy failed");
+  next = nx;
+  return base::error::Success();
+}
+
+bool Model::is_sentence_ending(int32_t token_idx) const {
+  for (int32_t e : eos_tokens_)
+    if (e == token_idx) return true;
+  return false;
+}
 std::string Model::decode(int32_t) const { return std::string(); }
 std::string Model::decode(std::vector<int32_t>) const { return std::string(); }
 std::vector<int32_t> Model::encode(const std::string&) const {
