@@ -136,10 +136,25 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
 
 /* C[M x N] = A[M x K] . W[N x K]^T (+ bias[N]) (+ C when accumulate != 0): the
  * MatmulKernel product (KI:9-10) for M input rows at once, on the matrix cores
- * (v_mfma_f32_32x32x2f32).  lda, ldw, ldc are row strides in floats.  Needs
+ * (v_mfma_f32_32x32x2f32, 64 x 64 workgroup tiles).  lda, ldw, ldc are row strides in floats.  Needs
  * K, lda, ldw multiples of 4 and A, W 16-byte aligned (else KL_EUNSUPP). */
 int kl_gemm_f32(const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
                 int ldc, const float* bias, int accumulate, void* stream);
+
+/* The same product for up to 3 outputs over one A in one launch (the Q, K
+ * and V projections): C[i][M x N[i]] (+)= A . W[i]^T (+ bias[i]); bias may be
+ * NULL (or hold NULL entries). */
+int kl_gemm_f32_grouped(const float* A, int M, int K, int lda, int n_seg, const float* const* W,
+                        float* const* C, const float* const* bias, const int* N, const int* ldw,
+                        const int* ldc, int accumulate, void* stream);
+
+/* kl_gemm_f32 with K divided among `splits` (1..16) workgroup slices for
+ * narrow outputs: partial products go to the caller's workspace
+ * (>= splits*M*N floats, else KL_EWORKSPACE) and are summed in slice order
+ * before bias and accumulate apply.  No allocation. */
+int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, int K, int lda,
+                       int ldw, int ldc, const float* bias, int accumulate, int splits,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* RoPEKernel (KI:36-39) on n_pos rows: row r of q (stride ldq) and of k
  * (stride ldk) rotated at position pos0 + r. */

@@ -457,6 +457,7 @@ struct kl_engine {
   char* pf_buf = nullptr;       // one allocation for everything below
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
   float *pf_h1 = nullptr, *pf_h3 = nullptr, *pf_xlast = nullptr;
+  float* pf_ws = nullptr;       // split-K partials [kPrefillMaxSplits][rows][dim]
   int32_t* pf_tok = nullptr;    // [seq_len] prompt ids
   int32_t* pf_next = nullptr;
   void* pf_am = nullptr;        // argmax workspace (zeroed once)
@@ -1137,6 +1138,16 @@ int kl_engine_step(kl_engine* e, int32_t token, int32_t pos, int32_t* next, floa
 namespace {
 
 constexpr int kPrefillChunk = 1024;  // rows per prefill pass
+constexpr int kPrefillMaxSplits = 4;
+
+// Split-K factor for a GEMM of rows x n outputs over k: enough workgroup
+// tiles (64 x 64) to fill the chip, each split keeping >= 32 k blocks.
+int prefill_splits(int rows, int n, int k) {
+  const long long tiles = static_cast<long long>((rows + 63) / 64) * ((n + 63) / 64);
+  int s = 1;
+  while (s < kPrefillMaxSplits && tiles * s < 1024 && k / 16 / (2 * s) >= 32) s *= 2;
+  return s;
+}
 
 bool prefill_supported(const kl_engine* e) {
   const int hd = e->lay.hd;
@@ -1153,7 +1164,9 @@ int prefill_scratch(kl_engine* e, int rows) {
   auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t R = rows;
   const size_t sz_x = al(R * m.D * 4), sz_q = al(R * m.Dq * 4), sz_h = al(R * m.F * 4);
-  const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + al(m.D * 4) + al(m.S * 4) + al(256) + al(am);
+  const size_t sz_ws = al(static_cast<size_t>(kPrefillMaxSplits) * R * m.D * 4);
+  const size_t total =
+      2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(m.D * 4) + al(m.S * 4) + al(256) + al(am);
   char* buf = nullptr;
   hipError_t err = hipMalloc(&buf, total);
   if (err != hipSuccess) return KL_ENOMEM;
@@ -1171,6 +1184,7 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_att = reinterpret_cast<float*>(take(sz_q));
   e->pf_h1 = reinterpret_cast<float*>(take(sz_h));
   e->pf_h3 = reinterpret_cast<float*>(take(sz_h));
+  e->pf_ws = reinterpret_cast<float*>(take(sz_ws));
   e->pf_xlast = reinterpret_cast<float*>(take(al(m.D * 4)));
   e->pf_tok = reinterpret_cast<int32_t*>(take(al(m.S * 4)));
   e->pf_next = reinterpret_cast<int32_t*>(take(al(256)));
@@ -1208,9 +1222,13 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     const float* w3 = static_cast<const float*>(Ld.w3.w);
     // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
-    PF(kl_gemm_f32(e->pf_xn, wq, e->pf_q, n, Dq, D, D, D, Dq, Ld.bq, 0, st));
-    PF(kl_gemm_f32(e->pf_xn, wk, krow, n, Dkv, D, D, D, Dkv, Ld.bk, 0, st));
-    PF(kl_gemm_f32(e->pf_xn, wv, vrow, n, Dkv, D, D, D, Dkv, Ld.bv, 0, st));
+    {  // q, k and v in one grouped launch; k and v straight into the cache rows
+      const float* W[3] = {wq, wk, wv};
+      float* Cs[3] = {e->pf_q, krow, vrow};
+      const float* B[3] = {Ld.bq, Ld.bk, Ld.bv};
+      const int N[3] = {Dq, Dkv, Dkv}, LW[3] = {D, D, D}, LC[3] = {Dq, Dkv, Dkv};
+      PF(kl_gemm_f32_grouped(e->pf_xn, n, D, D, 3, W, Cs, B, N, LW, LC, 0, st));
+    }
     if (e->transform == 2) {  // Qwen3 per-head q/k RMSNorm, eps 1e-6
       PF(kl_rmsnorm_rows(e->pf_q, Ld.qn, e->pf_q, n * H, hd, 1e-6f, st));
       PF(kl_rmsnorm_rows(krow, Ld.kn, krow, n * KVH, hd, 1e-6f, st));
@@ -1219,13 +1237,20 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
                     e->cos_t, st));
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     PF(kl_attn_prefill(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, st));
-    PF(kl_gemm_f32(e->pf_att, wo, e->pf_x, n, D, Dq, Dq, Dq, D, nullptr, 1, st));
+    const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
+    PF(kl_gemm_f32_splitk(e->pf_att, wo, e->pf_x, n, D, Dq, Dq, Dq, D, nullptr, 1,
+                          prefill_splits(n, D, Dq), e->pf_ws, ws_bytes, st));
     // feed_forward (llama3.cpp:671-719)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
-    PF(kl_gemm_f32(e->pf_xn, w1, e->pf_h1, n, F, D, D, D, F, nullptr, 0, st));
-    PF(kl_gemm_f32(e->pf_xn, w3, e->pf_h3, n, F, D, D, D, F, nullptr, 0, st));
+    {
+      const float* W[2] = {w1, w3};
+      float* Cs[2] = {e->pf_h1, e->pf_h3};
+      const int N[2] = {F, F}, LW[2] = {D, D}, LC[2] = {F, F};
+      PF(kl_gemm_f32_grouped(e->pf_xn, n, D, D, 2, W, Cs, nullptr, N, LW, LC, 0, st));
+    }
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
-    PF(kl_gemm_f32(e->pf_h1, w2, e->pf_x, n, D, F, F, F, D, nullptr, 1, st));
+    PF(kl_gemm_f32_splitk(e->pf_h1, w2, e->pf_x, n, D, F, F, F, D, nullptr, 1,
+                          prefill_splits(n, D, F), e->pf_ws, ws_bytes, st));
   }
 #undef PF
   return r;

@@ -16,6 +16,11 @@
 // with two ds_read_b128: MFMA step s uses, in lane l, column 8 (l / 32) + s.
 // The same permutation applies to both operands, so every product
 // A[m][k] W[n][k] is formed exactly once.
+//
+// Grouped launches compute up to three outputs over the same A (the Q, K and V
+// projections) in one grid, and split-K divides the K blocks among
+// blockIdx.y with a fixed-order reduction, so that narrow outputs (few tiles)
+// still fill the chip.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -28,12 +33,33 @@ typedef float gf16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmBK = 16;
 constexpr int kGemmLDK = kGemmBK + 4;  // padded LDS row (floats)
+constexpr int kGemmMaxSeg = 3;
+
+// One output of a grouped GEMM: C_s = A . W_s^T (+ bias_s) over the same A.
+struct GemmSeg {
+  const float* W;
+  float* C;
+  const float* bias;
+  int N, ldw, ldc;
+  int tile0;  // first workgroup tile of this segment
+};
+
+struct GemmArgs {
+  const float* A;
+  int M, K, lda;
+  int accumulate;  // C += product (else C = product)
+  int tiles_m;
+  int nseg;
+  GemmSeg seg[kGemmMaxSeg];
+  // Split-K (one segment only): blockIdx.y = split; the partial products go
+  // to ws[split][M][N] and k_gemm_reduce applies bias and accumulate.
+  float* ws;
+  int splits;
+};
 
 template <int WM, int WN, int TM, int TN>
-__global__ __launch_bounds__(WM * WN * 64) void k_gemm_f32(
-    const float* __restrict__ A, const float* __restrict__ W, float* __restrict__ C,
-    const float* __restrict__ bias, int M, int N, int K, int lda, int ldw, int ldc,
-    int accumulate, int tiles_m) {
+__global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm_f32(
+    GemmArgs g) {
   constexpr int BM = WM * TM * 32, BN = WN * TN * 32, BK = kGemmBK, LDK = kGemmLDK;
   constexpr int NT = WM * WN * 64;
   constexpr int A4 = BM * BK / 4, W4 = BN * BK / 4;  // float4s per tile
@@ -42,44 +68,77 @@ __global__ __launch_bounds__(WM * WN * 64) void k_gemm_f32(
   __shared__ __align__(16) float Ws[2][BN * LDK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
+  // Segment of this tile (uniform per workgroup).
+  int sidx = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i < g.nseg && static_cast<int>(blockIdx.x) >= g.seg[i].tile0) sidx = i;
+  const float* __restrict__ A = g.A;
+  const float* __restrict__ W = g.seg[0].W;
+  float* C = g.seg[0].C;
+  const float* bias = g.seg[0].bias;
+  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i == sidx) {
+      W = g.seg[i].W;
+      C = g.seg[i].C;
+      bias = g.seg[i].bias;
+      N = g.seg[i].N;
+      ldw = g.seg[i].ldw;
+      ldc = g.seg[i].ldc;
+      tile0 = g.seg[i].tile0;
+    }
+  const int M = g.M, K = g.K, lda = g.lda;
   // Tiles along M are adjacent in launch order, so the workgroups that share
   // a W tile run together and read it from cache.
-  const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+  const int local = static_cast<int>(blockIdx.x) - tile0;
+  const int tm = local % g.tiles_m, tn = local / g.tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
+  // K range of this split, in whole blocks.
+  const int nkt = (K + BK - 1) / BK;
+  const int kb0 = static_cast<int>(blockIdx.y) * nkt / g.splits;
+  const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
 
+  // The next block's loads land in ra/rw while the current block's MFMAs run;
+  // out-of-range elements are zeroed when the registers are written to LDS
+  // (after the MFMAs), so no wait is forced at load time.
   gf4 ra[LA], rw[LW];
+  unsigned int oka = 0, okw = 0;
   auto gload = [&](int k0) {
+    oka = okw = 0;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int idx = tid + i * NT;
       const int r = idx >> 2, c = (idx & 3) * 4;
       const int m = m0 + r, k = k0 + c;
-      const bool ok = idx < A4 && m < M && k < K;
-      const gf4 v = *reinterpret_cast<const gf4*>(A + static_cast<size_t>(ok ? m : 0) * lda +
-                                                  (ok ? k : 0));
-      ra[i] = ok ? v : gf4{0.f, 0.f, 0.f, 0.f};
+      const bool ok = (A4 % NT == 0 || idx < A4) && m < M && k < K;
+      oka |= ok ? 1u << i : 0u;
+      ra[i] = *reinterpret_cast<const gf4*>(A + static_cast<size_t>(ok ? m : 0) * lda + (ok ? k : 0));
     }
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
       const int idx = tid + i * NT;
       const int r = idx >> 2, c = (idx & 3) * 4;
       const int n = n0 + r, k = k0 + c;
-      const bool ok = idx < W4 && n < N && k < K;
-      const gf4 v = *reinterpret_cast<const gf4*>(W + static_cast<size_t>(ok ? n : 0) * ldw +
-                                                  (ok ? k : 0));
-      rw[i] = ok ? v : gf4{0.f, 0.f, 0.f, 0.f};
+      const bool ok = (W4 % NT == 0 || idx < W4) && n < N && k < K;
+      okw |= ok ? 1u << i : 0u;
+      rw[i] = *reinterpret_cast<const gf4*>(W + static_cast<size_t>(ok ? n : 0) * ldw + (ok ? k : 0));
     }
   };
   auto sstore = [&](int buf) {
+    const gf4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int idx = tid + i * NT;
-      if (idx < A4) *reinterpret_cast<gf4*>(&As[buf][(idx >> 2) * LDK + (idx & 3) * 4]) = ra[i];
+      if (A4 % NT == 0 || idx < A4)
+        *reinterpret_cast<gf4*>(&As[buf][(idx >> 2) * LDK + (idx & 3) * 4]) = ((oka >> i) & 1u) ? ra[i] : z;
     }
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
       const int idx = tid + i * NT;
-      if (idx < W4) *reinterpret_cast<gf4*>(&Ws[buf][(idx >> 2) * LDK + (idx & 3) * 4]) = rw[i];
+      if (W4 % NT == 0 || idx < W4)
+        *reinterpret_cast<gf4*>(&Ws[buf][(idx >> 2) * LDK + (idx & 3) * 4]) = ((okw >> i) & 1u) ? rw[i] : z;
     }
   };
 
@@ -89,14 +148,15 @@ __global__ __launch_bounds__(WM * WN * 64) void k_gemm_f32(
 #pragma unroll
     for (int b = 0; b < TN; ++b) acc[a][b] = gf16{};
 
-  const int nk = (K + BK - 1) / BK;
-  gload(0);
-  sstore(0);
+  if (kb0 < kb1) {
+    gload(kb0 * BK);
+    sstore(0);
+  }
   __syncthreads();
   const int kc = 8 * (lane >> 5);  // this lane's 8 columns of a k block
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+  for (int kt = kb0; kt < kb1; ++kt) {
+    const int cur = (kt - kb0) & 1;
+    if (kt + 1 < kb1) gload((kt + 1) * BK);
     gf4 af[TM][2], bf[TN][2];
 #pragma unroll
     for (int a = 0; a < TM; ++a) {
@@ -118,10 +178,11 @@ __global__ __launch_bounds__(WM * WN * 64) void k_gemm_f32(
         for (int b = 0; b < TN; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s >> 2][s & 3],
                                                            bf[b][s >> 2][s & 3], acc[a][b], 0, 0, 0);
-    if (kt + 1 < nk) sstore(cur ^ 1);
+    if (kt + 1 < kb1) sstore(cur ^ 1);
     __syncthreads();
   }
 
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * M * N : nullptr;
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -132,12 +193,33 @@ __global__ __launch_bounds__(WM * WN * 64) void k_gemm_f32(
         const int n = n0 + wn * TN * 32 + b * 32 + (lane & 31);
         if (m < M && n < N) {
           float v = acc[a][b][r];
-          if (bias) v += bias[n];
-          float* cp = C + static_cast<size_t>(m) * ldc + n;
-          if (accumulate) v = *cp + v;
-          *cp = v;
+          if (wsp) {
+            wsp[static_cast<size_t>(m) * N + n] = v;
+          } else {
+            if (bias) v += bias[n];
+            float* cp = C + static_cast<size_t>(m) * ldc + n;
+            if (g.accumulate) v = *cp + v;
+            *cp = v;
+          }
         }
       }
+}
+
+// C = sum of the split partials in split order (+ bias) (+ C).
+__global__ void k_gemm_reduce(const float* __restrict__ ws, int splits, int M, int N,
+                              float* __restrict__ C, int ldc, const float* __restrict__ bias,
+                              int accumulate) {
+  const size_t total = static_cast<size_t>(M) * N;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    float v = ws[i];
+    for (int s = 1; s < splits; ++s) v += ws[static_cast<size_t>(s) * total + i];
+    const int m = static_cast<int>(i / N), n = static_cast<int>(i - static_cast<size_t>(m) * N);
+    if (bias) v += bias[n];
+    float* cp = C + static_cast<size_t>(m) * ldc + n;
+    if (accumulate) v = *cp + v;
+    *cp = v;
+  }
 }
 
 }  // namespace kl

@@ -533,24 +533,85 @@ int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ld
   return launch_rc();
 }
 
+}  // extern "C"
+
+namespace {
+constexpr int kGemmTile = 64;  // workgroup tile (2 x 2 waves of 32 x 32)
+
+bool gemm_shape_ok(const float* A, int M, int K, int lda) {
+  return A && M > 0 && K > 0 && lda >= K;
+}
+
+// C_s (+)= A . W_s^T (+ bias_s) for nseg outputs in one grid; splits > 1
+// (nseg == 1) divides K among blockIdx.y into ws[splits][M][N] and reduces.
+int gemm_launch(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs, int accumulate,
+                float* ws, int splits, hipStream_t st) {
+  if (K % 4 || lda % 4 || !aligned16(A)) return KL_EUNSUPP;
+  GemmArgs g{};
+  g.A = A;
+  g.M = M;
+  g.K = K;
+  g.lda = lda;
+  g.accumulate = accumulate;
+  g.nseg = nseg;
+  g.ws = ws;
+  g.splits = splits;
+  g.tiles_m = (M + kGemmTile - 1) / kGemmTile;
+  long long tiles = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const GemmSeg& sg = segs[i];
+    if (!sg.W || !sg.C || sg.N <= 0 || sg.ldw < K || sg.ldc < sg.N) return KL_EINVAL;
+    if (sg.ldw % 4 || !aligned16(sg.W)) return KL_EUNSUPP;
+    g.seg[i] = sg;
+    g.seg[i].tile0 = static_cast<int>(tiles);
+    tiles += static_cast<long long>(g.tiles_m) * ((sg.N + kGemmTile - 1) / kGemmTile);
+  }
+  if (tiles > INT_MAX) return KL_EUNSUPP;
+  hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(static_cast<unsigned>(tiles), splits), dim3(256),
+                     0, st, g);
+  int r = launch_rc();
+  if (r != KL_OK || splits == 1) return r;
+  const GemmSeg& sg = segs[0];
+  const size_t total = static_cast<size_t>(M) * sg.N;
+  const int grid = static_cast<int>(std::min<size_t>((total + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_gemm_reduce, dim3(grid), dim3(256), 0, st, ws, splits, M, sg.N, sg.C, sg.ldc,
+                     sg.bias, accumulate);
+  return launch_rc();
+}
+}  // namespace
+
+extern "C" {
+
 int kl_gemm_f32(const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
                 int ldc, const float* bias, int accumulate, void* stream) {
-  if (!A || !W || !C || M <= 0 || N <= 0 || K <= 0 || lda < K || ldw < K || ldc < N)
+  if (!gemm_shape_ok(A, M, K, lda) || !W || !C || N <= 0 || ldw < K || ldc < N) return KL_EINVAL;
+  const GemmSeg sg{W, C, bias, N, ldw, ldc, 0};
+  return gemm_launch(A, M, K, lda, 1, &sg, accumulate, nullptr, 1, as_stream(stream));
+}
+
+int kl_gemm_f32_grouped(const float* A, int M, int K, int lda, int n_seg, const float* const* W,
+                        float* const* C, const float* const* bias, const int* N, const int* ldw,
+                        const int* ldc, int accumulate, void* stream) {
+  if (!gemm_shape_ok(A, M, K, lda) || n_seg < 1 || n_seg > kGemmMaxSeg || !W || !C || !N || !ldw ||
+      !ldc)
     return KL_EINVAL;
-  // 16-byte operand loads: rows must start 16-byte aligned.
-  if (K % 4 || lda % 4 || ldw % 4 || !aligned16(A) || !aligned16(W)) return KL_EUNSUPP;
-  const hipStream_t st = as_stream(stream);
-  const long long big = static_cast<long long>((M + 127) / 128) * ((N + 127) / 128);
-  if (big >= 256) {
-    const int tm = (M + 127) / 128, tn = (N + 127) / 128;
-    hipLaunchKernelGGL((k_gemm_f32<2, 2, 2, 2>), dim3(tm * tn), dim3(256), 0, st, A, W, C, bias, M,
-                       N, K, lda, ldw, ldc, accumulate, tm);
-  } else {
-    const int tm = (M + 63) / 64, tn = (N + 63) / 64;
-    hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(tm * tn), dim3(256), 0, st, A, W, C, bias, M,
-                       N, K, lda, ldw, ldc, accumulate, tm);
-  }
-  return launch_rc();
+  GemmSeg segs[kGemmMaxSeg];
+  for (int i = 0; i < n_seg; ++i)
+    segs[i] = GemmSeg{W[i], C[i], bias ? bias[i] : nullptr, N[i], ldw[i], ldc[i], 0};
+  return gemm_launch(A, M, K, lda, n_seg, segs, accumulate, nullptr, 1, as_stream(stream));
+}
+
+int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, int K, int lda,
+                       int ldw, int ldc, const float* bias, int accumulate, int splits,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (!gemm_shape_ok(A, M, K, lda) || !W || !C || N <= 0 || ldw < K || ldc < N || splits < 1 ||
+      splits > 16)
+    return KL_EINVAL;
+  if (splits > 1 && (!workspace || workspace_bytes < static_cast<size_t>(splits) * M * N * sizeof(float)))
+    return KL_EWORKSPACE;
+  const GemmSeg sg{W, C, bias, N, ldw, ldc, 0};
+  return gemm_launch(A, M, K, lda, 1, &sg, accumulate, static_cast<float*>(workspace), splits,
+                     as_stream(stream));
 }
 
 }  // extern "C"

@@ -87,6 +87,49 @@ def test_gemm_bias_and_accumulate(K, O, gpu):
         assert np.max(np.abs(ya[m] - O.add(C0[m], g))) <= tol + 1e-6
 
 
+def test_gemm_grouped_matches_single(K, O, gpu):
+    """Three outputs over one A (the Q, K, V projections) in one launch."""
+    rng = np.random.default_rng(9)
+    M, Kd = 90, 160
+    Ns = [256, 64, 64]
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    Ws = [(rng.standard_normal((n, Kd)) * 0.05).astype(np.float32) for n in Ns]
+    bs = [rng.standard_normal(n).astype(np.float32) for n in Ns]
+    dA = D(K, A)
+    dW = [D(K, w) for w in Ws]
+    dC = [K.DeviceArray(M * n) for n in Ns]
+    db = [D(K, b) for b in bs]
+    P3 = C.c_void_p * 3
+    I3 = C.c_int * 3
+    ok(K.lib.kl_gemm_f32_grouped(dA.ptr, M, Kd, Kd, 3, P3(*[w.ptr for w in dW]),
+                                 P3(*[c.ptr for c in dC]), P3(*[b.ptr for b in db]), I3(*Ns),
+                                 I3(Kd, Kd, Kd), I3(*Ns), 0, None), "grouped")
+    for w, b, c, n in zip(Ws, bs, dC, Ns):
+        y = c.numpy().reshape(M, n)
+        assert np.array_equal(y, gemm(K, A, w, bias=b))  # same kernel, same order
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
+def test_gemm_splitk_vs_oracle(K, O, gpu, splits):
+    rng = np.random.default_rng(splits)
+    M, N, Kd = 100, 192, 1024
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    W = (rng.standard_normal((N, Kd)) * 0.02).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    dA, dW, dC = D(K, A), D(K, W), D(K, C0)
+    ws = K.DeviceArray(splits * M * N)
+    ok(K.lib.kl_gemm_f32_splitk(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, Kd, Kd, N, None, 1, splits,
+                                ws.ptr, ws.nbytes, None), "splitk")
+    y = dC.numpy().reshape(M, N)
+    for m in range(0, M, 7):
+        g = O.gemv_f32(A[m], W)
+        tol = 4e-7 * np.sqrt(Kd) * (np.abs(W) @ np.abs(A[m])).max() + 1e-6
+        assert np.max(np.abs(y[m] - O.add(C0[m], g))) <= tol
+    if splits > 1:  # a workspace too small is refused before any launch
+        assert K.lib.kl_gemm_f32_splitk(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, Kd, Kd, N, None, 1,
+                                        splits, ws.ptr, ws.nbytes - 4, None) == -6
+
+
 def test_gemm_rejects_unaligned_k(K, gpu):
     buf = K.DeviceArray(64)
     assert K.lib.kl_gemm_f32(buf.ptr, buf.ptr, buf.ptr, 2, 2, 3, 3, 3, 2, None, 0, None) == -4
