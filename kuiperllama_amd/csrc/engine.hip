@@ -442,6 +442,10 @@ struct kl_engine {
   size_t p_lds = 0;
   const void* p_kernel = nullptr;
   PGemv* d_ph = nullptr;       // [4L + 1] phase descriptors (arena)
+  // Row split per workgroup, weighted by measured streaming speed (empty:
+  // balanced).  d_split holds 4 tables of nwg + 1 row offsets: QKV rows, D, F, V.
+  std::vector<double> wg_weight;
+  int* d_split = nullptr;
   PAttn* d_at = nullptr;       // [L]
   tagged_t *t_q = nullptr, *t_k = nullptr, *t_v = nullptr, *t_att = nullptr;  // tagged
   tagged_t *t_xb = nullptr, *t_h = nullptr, *t_x = nullptr;                    //   hand-off
@@ -656,9 +660,12 @@ int check_device_error(kl_engine* e) {
 // into balanced contiguous ranges, one per workgroup, then (ks, rw) chosen to
 // minimise the largest per-wave work, counting a row reduction as half a
 // chunk.  Returns the LDS floats the phase's row partials need.
-size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb) {
+// The split-K factor is chosen for the balanced share, so a row's summation
+// order (and so every result bit) does not depend on the measured split;
+// `max_share` (the largest weighted share, or 0) only sizes the LDS slots.
+size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb, int max_share) {
   const int total = p.paired ? p.rows[0] : p.rows[0] + p.rows[1] + p.rows[2];
-  const int rpw = (total + nwg - 1) / nwg;  // largest per-workgroup share
+  const int rpw = (total + nwg - 1) / nwg;  // balanced per-workgroup share
   p.cn16 = q8 ? p.cols / 16 : p.cols / 4;
   p.cn = (p.cn16 + kWave - 1) / kWave;
   p.nseg = (p.cn + nb - 1) / nb;
@@ -684,7 +691,8 @@ size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb) {
       p.nsegw = nsegw;
     }
   }
-  return static_cast<size_t>(nloc) * p.ks;
+  const int rmax = std::max(rpw, max_share);
+  return static_cast<size_t>(p.paired ? rmax * p.nsub : rmax) * p.ks;
 }
 
 template <bool Q8, int NB>
@@ -695,6 +703,31 @@ const void* persistent_kernel(int hd) {
     case 128: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 128>);
     default: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 256>);
   }
+}
+
+// Row offsets [nwg + 1] for `total` rows with shares proportional to w (every
+// workgroup keeps at least one row: the tagged hand-off relies on it).
+std::vector<int> weighted_split(int total, const std::vector<double>& w) {
+  const int n = static_cast<int>(w.size());
+  std::vector<int> off(n + 1, 0);
+  double sum = 0.0;
+  for (double x : w) sum += x;
+  double acc = 0.0;
+  for (int b = 0; b < n; ++b) {
+    acc += w[b];
+    int e = static_cast<int>(std::llround(acc / sum * total));
+    e = std::max(e, off[b] + 1);              // at least one row
+    e = std::min(e, total - (n - 1 - b));      // leave one for each later workgroup
+    off[b + 1] = e;
+  }
+  off[n] = total;
+  return off;
+}
+
+int max_share(const std::vector<int>& off) {
+  int m = 0;
+  for (size_t b = 0; b + 1 < off.size(); ++b) m = std::max(m, off[b + 1] - off[b]);
+  return m;
 }
 
 // Builds the phase descriptors and launch shape; leaves persistent_ok false
@@ -757,19 +790,56 @@ int setup_persistent(kl_engine* e) {
     w2.in = e->t_h; w2.norm = nullptr; w2.out[0] = e->t_x;
     at[l] = PAttn{e->kcache + l * kv_layer, e->vcache + l * kv_layer, L.qn, L.kn};
   }
+  // Weighted splits (after calibration) for the four split dimensions.
+  const bool weighted = static_cast<int>(e->wg_weight.size()) == e->nwg;
+  int share_qkv = 0, share_d = 0, share_f = 0, share_v = 0;
+  if (weighted) {
+    const std::vector<int> sq = weighted_split(m.Dq + 2 * m.Dkv, e->wg_weight);
+    const std::vector<int> sd = weighted_split(m.D, e->wg_weight);
+    const std::vector<int> sf = weighted_split(m.F, e->wg_weight);
+    const std::vector<int> sv = weighted_split(m.V, e->wg_weight);
+    share_qkv = max_share(sq);
+    share_d = max_share(sd);
+    share_f = max_share(sf);
+    share_v = max_share(sv);
+    const size_t per = static_cast<size_t>(e->nwg) + 1;
+    if (!e->d_split) {
+      hipError_t err = hipMalloc(&e->d_split, 4 * per * sizeof(int));
+      if (err != hipSuccess) return rc(err);
+    }
+    std::vector<int> all;
+    for (const auto* t : {&sq, &sd, &sf, &sv}) all.insert(all.end(), t->begin(), t->end());
+    hipError_t err = hipMemcpy(e->d_split, all.data(), all.size() * sizeof(int), hipMemcpyHostToDevice);
+    if (err != hipSuccess) return rc(err);
+    for (int l = 0; l < m.L; ++l) {
+      ph[4 * l + 0].split = e->d_split;
+      ph[4 * l + 1].split = e->d_split + per;
+      ph[4 * l + 2].split = e->d_split + 2 * per;
+      ph[4 * l + 3].split = e->d_split + per;
+    }
+  }
   PGemv& cls = ph[4 * m.L];
   cls = PGemv{};
   cls.w[0] = e->wcls.w; cls.sc[0] = e->wcls.s; cls.rows[0] = m.V;
   cls.nsub = 1; cls.cols = m.D; cls.epi = kEpiCls;
   cls.layer = m.L - 1; cls.in_layer = m.L - 1;
   cls.in = e->t_x; cls.norm = e->rms_final; cls.logits = e->logits;
-  for (PGemv& p : ph) {
-    red_floats = std::max(red_floats, plan_phase(p, e->nwg, q8, m.gs, nb));
+  if (weighted) cls.split = e->d_split + 3 * (static_cast<size_t>(e->nwg) + 1);
+  for (size_t i = 0; i < ph.size(); ++i) {
+    PGemv& p = ph[i];
+    int share = 0;
+    if (weighted) {
+      if (i + 1 == ph.size()) share = share_v;         // classifier
+      else if (i % 4 == 0) share = share_qkv;          // QKV
+      else if (i % 4 == 2) share = share_f;            // W1/W3
+      else share = share_d;                            // WO, W2
+    }
+    red_floats = std::max(red_floats, plan_phase(p, e->nwg, q8, m.gs, nb, share));
     max_cols = std::max(max_cols, p.cols);
   }
   const int red_off = (max_cols + 3) & ~3;
   const int xres_off = red_off + static_cast<int>((red_floats + 3) & ~size_t(3));
-  const int xres_floats = (m.D + e->nwg - 1) / e->nwg;
+  const int xres_floats = weighted ? share_d : (m.D + e->nwg - 1) / e->nwg;
   const size_t gemv_lds = (static_cast<size_t>(xres_off) + xres_floats) * sizeof(float);
   const size_t attn_lds = attn_p_lds_floats(m.hd, m.H / m.KVH, e->attn.G) * sizeof(float);
   // The residual rows must survive the attention phase, which uses LDS from 0.
@@ -835,10 +905,77 @@ void release(kl_engine* e) {
   if (e->ev1) (void)hipEventDestroy(e->ev1);
   if (e->arena) (void)hipFree(e->arena);
   if (e->pf_buf) (void)hipFree(e->pf_buf);
+  if (e->d_split) (void)hipFree(e->d_split);
   if (e->st_host) (void)hipHostFree(e->st_host);
   if (e->derr_host) (void)hipHostFree(e->derr_host);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
+}
+
+}  // namespace
+
+namespace {
+
+// One traced persistent step (token, pos): ticks [2 * 5 * L + 3][nwg].
+int trace_once(kl_engine* e, int32_t token, int32_t pos, unsigned long long* ticks) {
+  const size_t n = static_cast<size_t>(2 * 5 * e->lay.L + 3) * e->nwg;
+  unsigned long long* d = nullptr;
+  hipError_t err = hipMalloc(&d, n * sizeof(unsigned long long));
+  if (err != hipSuccess) return rc(err);
+  err = hipMemset(d, 0, n * sizeof(unsigned long long));
+  *e->st_host = StepState{pos, token, 0, 0};
+  if (err == hipSuccess)
+    err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  int r = rc(err);
+  if (r == KL_OK) {
+    e->pargs.trace = d;
+    r = launch_persistent(e);
+    e->pargs.trace = nullptr;
+  }
+  if (r == KL_OK) r = rc(hipStreamSynchronize(e->stream));
+  if (r == KL_OK) r = check_device_error(e);
+  if (r == KL_OK) r = rc(hipMemcpy(ticks, d, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  (void)hipFree(d);
+  return r;
+}
+
+// Measures each workgroup's time on the W1/W3 and W2 phases (the bulk of the
+// streaming) over a few traced steps and re-splits every phase's rows in
+// proportion to the workgroups' speed.  On MI355X some XCDs stream a few
+// percent slower than others, and which ones differs between parts, so the
+// split is measured rather than fixed.  Results do not change (the split-K
+// plan stays the balanced one).  KL_PCALIBRATE=0 keeps the balanced split.
+int calibrate_persistent(kl_engine* e) {
+  if (!e->persistent_ok || e->mode != KL_MODE_PERSISTENT) return KL_OK;
+  if (const char* env = std::getenv("KL_PCALIBRATE"))
+    if (std::atoi(env) == 0) return KL_OK;
+  const int L = e->lay.L, W = e->nwg;
+  if (e->lay.S < 4) return KL_OK;
+  std::vector<unsigned long long> t(static_cast<size_t>(2 * 5 * L + 3) * W);
+  std::vector<double> work(W, 0.0);
+  for (int rep = 0; rep < 4; ++rep) {
+    const int r = trace_once(e, 0, rep, t.data());
+    if (r != KL_OK) return r;
+    if (rep == 0) continue;  // warm-up
+    for (int l = 0; l < L; ++l)
+      for (int p : {5 * l + 3, 5 * l + 4}) {  // W1/W3, W2
+        const unsigned long long* ready = t.data() + static_cast<size_t>(2 * p + 1) * W;
+        const unsigned long long* done = t.data() + static_cast<size_t>(2 * p + 2) * W;
+        for (int b = 0; b < W; ++b)
+          work[b] += done[b] > ready[b] ? static_cast<double>(done[b] - ready[b]) : 0.0;
+      }
+  }
+  double mean = 0.0;
+  for (double w : work) mean += w;
+  mean /= W;
+  if (!(mean > 0.0)) return KL_OK;
+  std::vector<double> wt(W);
+  for (int b = 0; b < W; ++b) {
+    const double sp = work[b] > 0.0 ? mean / work[b] : 1.0;  // relative speed
+    wt[b] = std::min(1.25, std::max(0.8, sp));
+  }
+  e->wg_weight = wt;
+  return setup_persistent(e);
 }
 
 }  // namespace
@@ -1046,6 +1183,7 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   }
   int trc = kl_sincos_table(lay.hd, lay.S, e->theta, e->sin_t, e->cos_t);
   if (trc == KL_OK) trc = setup_persistent(e);
+  if (trc == KL_OK) trc = calibrate_persistent(e);
   if (trc != KL_OK) {
     release(e);
     return trc;
@@ -1171,6 +1309,7 @@ int prefill_scratch(kl_engine* e, int rows) {
   hipError_t err = hipMalloc(&buf, total);
   if (err != hipSuccess) return KL_ENOMEM;
   if (e->pf_buf) (void)hipFree(e->pf_buf);
+  if (e->d_split) (void)hipFree(e->d_split);
   e->pf_buf = buf;
   size_t off = 0;
   auto take = [&](size_t b) {

@@ -34,8 +34,10 @@
 // with the same row split, so each workgroup keeps its own rows of x in LDS
 // and the residual adds read nothing from memory.
 //
-// GEMV phases.  The split dimension (output rows) is cut into balanced
-// contiguous ranges, one per workgroup.  Inside the workgroup, KS waves share
+// GEMV phases.  The split dimension (output rows) is cut into contiguous
+// ranges, one per workgroup: balanced, or weighted by each workgroup's
+// measured streaming speed (the host calibrates once per engine: on a given
+// part some XCDs stream a few percent slower than others).  Inside the workgroup, KS waves share
 // a row (split-K) and RW = 8 / KS row groups take rows round robin; the host
 // planner picks KS per phase.  A wave's work is a list of items = (local row,
 // 1 KiB column chunk): 64 lanes x 16 bytes (4 fp32 or 16 int8 weights per
@@ -93,6 +95,8 @@ struct PGemv {
   float* vcache;          // qkv: V cache layer base (row pos kept for later tokens)
   float* logits;          // classifier output
   const float* bias[3];   // qkv bias (Qwen2) or nullptr
+  const int* split;       // [workgroups + 1] first row of each workgroup, or nullptr:
+                          //   balanced split b * total / n
 };
 
 struct PAttn {
@@ -400,11 +404,18 @@ __device__ __forceinline__ PGeom p_geom(PGp p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   g.ksi = wave % p->ks;
   g.rg = wave / p->ks;
-  // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n).
-  const int total = p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2];
-  const long long b = blockIdx.x, n = gridDim.x;
-  g.base = static_cast<int>(b * total / n);
-  g.cnt = static_cast<int>((b + 1) * total / n) - g.base;
+  if (p->split) {
+    // Measured split: rows in proportion to each workgroup's streaming speed.
+    const KL_CAS int* sp = (const KL_CAS int*)(p->split);
+    g.base = sp[blockIdx.x];
+    g.cnt = sp[blockIdx.x + 1] - g.base;
+  } else {
+    // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n).
+    const int total = p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2];
+    const long long b = blockIdx.x, n = gridDim.x;
+    g.base = static_cast<int>(b * total / n);
+    g.cnt = static_cast<int>((b + 1) * total / n) - g.base;
+  }
   g.nloc = p->paired ? g.cnt * p->nsub : g.cnt;
   const int nrows = g.nloc > g.rg ? (g.nloc - g.rg + p->rw - 1) / p->rw : 0;
   g.n_items = g.ksi < p->nseg ? nrows * p->nsegw : 0;
