@@ -440,6 +440,8 @@ struct kl_engine {
   bool plain_launch = false;
   int nwg = 0;                 // workgroups (co-resident)
   size_t p_lds = 0;
+  size_t p_lds_traced = 0;     // p_lds + the trace slots (traced launches)
+  bool trace_ok = false;       // the traced launch is co-resident too
   const void* p_kernel = nullptr;
   PGemv* d_ph = nullptr;       // [4L + 1] phase descriptors (arena)
   // Row split per workgroup, weighted by measured streaming speed (empty:
@@ -603,12 +605,13 @@ int launch_step(kl_engine* e, Marks* mk = nullptr) {
 // One persistent launch = one token.
 int launch_persistent(kl_engine* e, Marks* mk = nullptr) {
   void* params[] = {&e->pargs};
+  const size_t lds = e->pargs.trace ? e->p_lds_traced : e->p_lds;
   mark(e->stream, mk, kKStep);
   const hipError_t err =
       e->plain_launch
-          ? hipLaunchKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads), params, e->p_lds, e->stream)
-          : hipLaunchCooperativeKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads), params,
-                                       e->p_lds, e->stream);
+          ? hipLaunchKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads), params, lds, e->stream)
+          : hipLaunchCooperativeKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads), params, lds,
+                                       e->stream);
   mark(e->stream, mk, kKEnd);
   return rc(err);
 }
@@ -847,6 +850,9 @@ int setup_persistent(kl_engine* e) {
                                   (attn_lds + 15) & ~size_t(15));
   e->p_lds = xres_at + xres_floats * sizeof(float);
   (void)gemv_lds;
+  const int trace_slots = 2 * 5 * m.L + 3;
+  const size_t trace_at = (e->p_lds + 15) & ~size_t(15);
+  e->p_lds_traced = trace_at + trace_slots * sizeof(unsigned long long);
   hipError_t err = hipMemcpy(e->d_ph, ph.data(), ph.size() * sizeof(PGemv), hipMemcpyHostToDevice);
   if (err == hipSuccess)
     err = hipMemcpy(e->d_at, at.data(), at.size() * sizeof(PAttn), hipMemcpyHostToDevice);
@@ -869,12 +875,14 @@ int setup_persistent(kl_engine* e) {
   a.red_off = red_off;
   a.xres_off = static_cast<int>(xres_at / sizeof(float));
   a.st = e->st; a.prompt = e->prompt; a.out_tokens = e->out_tokens;
+  a.trace_off = static_cast<int>(trace_at / sizeof(unsigned long long));
+  a.trace_slots = trace_slots;
 
   // The grid must be co-resident: one workgroup of 512 threads per CU (or
   // KL_PWG_PER_CU) with this LDS.
-  if (e->p_lds > 64 * 1024) {
+  if (e->p_lds_traced > 64 * 1024) {
     err = hipFuncSetAttribute(e->p_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(e->p_lds));
+                              static_cast<int>(e->p_lds_traced));
     if (err != hipSuccess) {
       (void)hipGetLastError();
       return KL_OK;
@@ -887,6 +895,11 @@ int setup_persistent(kl_engine* e) {
     return KL_OK;
   }
   e->persistent_ok = blocks >= per_cu;
+  int blocks_traced = 0;
+  e->trace_ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks_traced, e->p_kernel, kPThreads,
+                                                             e->p_lds_traced) == hipSuccess &&
+                blocks_traced >= per_cu;
+  (void)hipGetLastError();
   e->mode = e->persistent_ok ? KL_MODE_PERSISTENT : KL_MODE_MULTI;
   e->plain_launch = e->persistent_ok && blocks * e->cus >= e->nwg;
   if (const char* env = std::getenv("KL_PERSISTENT_LAUNCH"))
@@ -918,6 +931,7 @@ namespace {
 
 // One traced persistent step (token, pos): ticks [2 * 5 * L + 3][nwg].
 int trace_once(kl_engine* e, int32_t token, int32_t pos, unsigned long long* ticks) {
+  if (!e->trace_ok) return KL_EUNSUPP;
   const size_t n = static_cast<size_t>(2 * 5 * e->lay.L + 3) * e->nwg;
   unsigned long long* d = nullptr;
   hipError_t err = hipMalloc(&d, n * sizeof(unsigned long long));
@@ -946,7 +960,7 @@ int trace_once(kl_engine* e, int32_t token, int32_t pos, unsigned long long* tic
 // split is measured rather than fixed.  Results do not change (the split-K
 // plan stays the balanced one).  KL_PCALIBRATE=0 keeps the balanced split.
 int calibrate_persistent(kl_engine* e) {
-  if (!e->persistent_ok || e->mode != KL_MODE_PERSISTENT) return KL_OK;
+  if (!e->persistent_ok || !e->trace_ok || e->mode != KL_MODE_PERSISTENT) return KL_OK;
   if (const char* env = std::getenv("KL_PCALIBRATE"))
     if (std::atoi(env) == 0) return KL_OK;
   const int L = e->lay.L, W = e->nwg;
@@ -1562,24 +1576,7 @@ int kl_engine_trace_step(kl_engine* e, int32_t token, int32_t pos, uint64_t* tic
   *n_slots = slots;
   *n_workgroups = e->nwg;
   if (!ticks || static_cast<int64_t>(n) > max_ticks) return KL_EWORKSPACE;
-  unsigned long long* d = nullptr;
-  hipError_t err = hipMalloc(&d, n * sizeof(unsigned long long));
-  if (err != hipSuccess) return rc(err);
-  err = hipMemset(d, 0, n * sizeof(unsigned long long));
-  *e->st_host = StepState{pos, token, 0, 0};
-  if (err == hipSuccess)
-    err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
-  int r = rc(err);
-  if (r == KL_OK) {
-    e->pargs.trace = d;
-    r = launch_persistent(e);
-    e->pargs.trace = nullptr;
-  }
-  if (r == KL_OK) r = rc(hipStreamSynchronize(e->stream));
-  if (r == KL_OK) r = check_device_error(e);
-  if (r == KL_OK) r = rc(hipMemcpy(ticks, d, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
-  (void)hipFree(d);
-  return r;
+  return trace_once(e, token, pos, reinterpret_cast<unsigned long long*>(ticks));
 }
 
 int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, float* avg_ms,

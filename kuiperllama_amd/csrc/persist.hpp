@@ -141,8 +141,14 @@ struct PArgs {
   // Optional device-time trace (nullptr: off).  Slot-major [slot][workgroup]
   // of 100 MHz s_memrealtime ticks: slot 0 = kernel entry; phase p (5 per
   // layer: QKV, attention, WO, W1/W3, W2; then the classifier) has slot 2p+1 =
-  // its input staged and slot 2p+2 = its outputs stored.
+  // its input staged and slot 2p+2 = its outputs stored.  The marks are kept
+  // in LDS (trace_slots 8-byte slots at u64 offset trace_off of the dynamic
+  // LDS) and written out once at the end: a global store per mark would
+  // perturb what it measures, because the vector-memory counter retires loads
+  // and stores in order, so every later load wait would include the store's
+  // acknowledgement.
   unsigned long long* trace;
+  int trace_off, trace_slots;
 };
 
 // ---------------------------------------------------------------------------
@@ -205,9 +211,12 @@ __device__ __forceinline__ float val_of(tagged_t x) {
   return __uint_as_float(static_cast<unsigned int>(x));
 }
 
+__device__ __forceinline__ unsigned long long* trace_lds(const PArgs& a) {
+  extern __shared__ __align__(16) unsigned long long p_dyn_lds_u64[];
+  return p_dyn_lds_u64 + a.trace_off;
+}
 __device__ __forceinline__ void trace_mark(const PArgs& a, int slot) {
-  if (a.trace && threadIdx.x == 0)
-    a.trace[static_cast<size_t>(slot) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
+  if (a.trace && threadIdx.x == 0) trace_lds(a)[slot] = __builtin_amdgcn_s_memrealtime();
 }
 
 // Re-polls, all together, the elements k of `v` (E values already loaded once
@@ -262,13 +271,15 @@ __device__ __forceinline__ float block_sum_p(float v, float* red) {
 __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, unsigned int tag,
                                           const float* emb_row, const float* nw, float eps, int n,
                                           float* xs, float* red) {
+  constexpr int T = kPThreads;
+  const int tid = threadIdx.x;
   float ss = 0.f;
   float wv[8];  // norm weights of the first round
-  for (int b0 = 0; b0 < n; b0 += kPThreads * 8) {
+  for (int b0 = 0; b0 < n; b0 += T * 8) {
     tagged_t v[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int i = b0 + k * kPThreads + threadIdx.x;
+      const int i = b0 + k * T + tid;
       if (src)
         v[k] = i < n ? g_ld64(src + i) : (static_cast<tagged_t>(tag) << 32);
       else
@@ -277,7 +288,7 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
     if (b0 == 0 && nw) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const int i = k * kPThreads + threadIdx.x;
+        const int i = k * T + tid;
         wv[k] = g_rd(nw + (i < n ? i : 0));
       }
     }
@@ -285,12 +296,12 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
       unsigned int valid = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (b0 + k * kPThreads + static_cast<int>(threadIdx.x) < n) valid |= 1u << k;
-      poll_many<8>(a, tag, [&](int k) { return src + b0 + k * kPThreads + threadIdx.x; }, valid, v);
+        if (b0 + k * T + tid < n) valid |= 1u << k;
+      poll_many<8>(a, tag, [&](int k) { return src + b0 + k * T + tid; }, valid, v);
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int i = b0 + k * kPThreads + threadIdx.x;
+      const int i = b0 + k * T + tid;
       if (i < n) {
         const float x = val_of(v[k]);
         xs[i] = x;
@@ -303,10 +314,10 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
     const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int i = k * kPThreads + threadIdx.x;
+      const int i = k * T + tid;
       if (i < n) xs[i] = wv[k] * (r * xs[i]);
     }
-    for (int i = kPThreads * 8 + threadIdx.x; i < n; i += kPThreads) xs[i] = g_rd(nw + i) * (r * xs[i]);
+    for (int i = T * 8 + tid; i < n; i += T) xs[i] = g_rd(nw + i) * (r * xs[i]);
   }
   __syncthreads();
 }
@@ -1029,6 +1040,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     rope_s = g_rd(a.sin_t + static_cast<size_t>(pos) * HD + 2 * j);
   }
   AttnPre<HD> pre;
+  if (a.trace) {
+    for (int s = threadIdx.x; s < a.trace_slots; s += kPThreads) trace_lds(a)[s] = 0;
+    __syncthreads();
+  }
   trace_mark(a, slot++);
 
   PChunk<Q8> A[NB];
@@ -1090,6 +1105,12 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       ++slot;
       trace_mark(a, slot++);
     }
+  }
+
+  if (a.trace) {
+    __syncthreads();
+    for (int s = threadIdx.x; s < a.trace_slots; s += kPThreads)
+      a.trace[static_cast<size_t>(s) * gridDim.x + blockIdx.x] = trace_lds(a)[s];
   }
 
   // End of step: the last workgroup to arrive samples (or takes the next
