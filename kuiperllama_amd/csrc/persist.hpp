@@ -247,30 +247,31 @@ __device__ __forceinline__ void poll_many(const PArgs& a, unsigned int tag, Addr
   }
 }
 
-// Sum over the 512 threads of the workgroup; `red` holds >= kPWaves floats.
-__device__ __forceinline__ float block_sum_p(float v, float* red) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+// The RMSNorm scale of a staged vector: 1 / sqrt(mean(x^2) + eps) from the
+// per-wave sums of squares stage_vec left in ssq (after its barrier).
+__device__ __forceinline__ float norm_scale(const float* ssq, int n, float eps) {
   float t = 0.f;
 #pragma unroll
-  for (int w = 0; w < kPWaves; ++w) t += red[w];
-  return t;
+  for (int w = 0; w < kPWaves; ++w) t += ssq[w];
+  return 1.f / sqrtf(t / static_cast<float>(n) + eps);
 }
 
 // Stages a GEMV input vector into LDS: the tagged vector `src` (all n elements
 // polled until they carry `tag`), or the embedding row `emb_row` when src is
-// null; applies RMSNorm when `nw` is set:
-// y = w * (x * (1 / sqrt(mean(x^2) + eps))) (kernels/cpu/rmsnorm_kernel.cpp:30-32).
+// null.  With RMSNorm (`nw` set), y = w * (x * r), r = 1 / sqrt(mean(x^2) + eps)
+// (kernels/cpu/rmsnorm_kernel.cpp:30-32), the staged vector is w * x and the
+// scalar r is applied to the GEMV's row totals (W y = r (W (w * x))): the
+// per-wave sums of squares go to ssq[kPWaves] and norm_scale() combines them
+// after the closing barrier, so the norm adds no barrier or extra pass over
+// the vector to the hand-off.
 // No weight loads are in flight while the input is polled: the phase's first
 // weight segment is issued after the staging (measured: issuing it before
 // the wait slows the hand-off more than it saves, because every workgroup's
 // burst of prefetches queues ahead of the polls in the memory system).
 // Ends with a workgroup barrier.
 __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, unsigned int tag,
-                                          const float* emb_row, const float* nw, float eps, int n,
-                                          float* xs, float* red) {
+                                          const float* emb_row, const float* nw, int n, float* xs,
+                                          float* ssq) {
   constexpr int T = kPThreads;
   const int tid = threadIdx.x;
   float ss = 0.f;
@@ -304,20 +305,14 @@ __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, u
       const int i = b0 + k * T + tid;
       if (i < n) {
         const float x = val_of(v[k]);
-        xs[i] = x;
         ss += x * x;
+        xs[i] = nw ? (b0 == 0 ? wv[k] : g_rd(nw + i)) * x : x;
       }
     }
   }
   if (nw) {
-    ss = block_sum_p(ss, red);
-    const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int i = k * T + tid;
-      if (i < n) xs[i] = wv[k] * (r * xs[i]);
-    }
-    for (int i = T * 8 + tid; i < n; i += T) xs[i] = g_rd(nw + i) * (r * xs[i]);
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) ssq[tid >> 6] = ss;
   }
   __syncthreads();
 }
@@ -969,17 +964,17 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 // ---------------------------------------------------------------------------
 // Epilogues of the QKV, residual and SwiGLU phases.  `xres` holds this
 // workgroup's rows of the residual stream (the WO and W2 phases split the D
-// rows identically).
+// rows identically); `rn` is the RMSNorm scale of the phase's input.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void p_epilogue(PGp p, const PGeom& g, const float* red, int pos,
-                                           unsigned int tag, float* xres) {
+                                           unsigned int tag, float* xres, float rn) {
   const int ks = p->ks;
   const int epi = p->epi;
   if (epi == kEpiQkv) {
     for (int lr = threadIdx.x; lr < g.nloc; lr += kPThreads) {
       int sub, row;
       p_row(p, g, lr, sub, row);
-      float v = p_row_total(ks, red, lr);
+      float v = rn * p_row_total(ks, red, lr);
       const float* b = p->bias[sub];
       if (b) v = v + g_rd(b + row);
       g_st_tagged(p->out[sub] + row, v, tag);
@@ -995,8 +990,8 @@ __device__ __forceinline__ void p_epilogue(PGp p, const PGeom& g, const float* r
   } else if (epi == kEpiSwiglu) {
     tagged_t* out = p->out[0];
     for (int lr = threadIdx.x; lr < g.cnt; lr += kPThreads) {
-      const float a1 = p_row_total(ks, red, lr);
-      const float a3 = p_row_total(ks, red, lr + g.cnt);
+      const float a1 = rn * p_row_total(ks, red, lr);
+      const float a3 = rn * p_row_total(ks, red, lr + g.cnt);
       // kernels/cpu/swiglu_kernel.cpp:21-22
       const float s = a1 * (1.0f / (1.0f + expf(-a1)));
       g_st_tagged(out + g.base + lr, s * a3, tag);
@@ -1063,20 +1058,22 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     const unsigned int tag_in = epoch * kTagLayers + p->in_layer + 1;
     const unsigned int tag = epoch * kTagLayers + p->layer + 1;
     if ((k & 3) == 0 && !is_cls) attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
-    stage_vec(a, p->in, tag_in, emb_row, p->norm, a.eps, p->cols, xs, sred);
+    stage_vec(a, p->in, tag_in, emb_row, p->norm, p->cols, xs, sred);
     trace_mark(a, slot++);
     {
       PCur c0{0, 0, 0};
       p_seg_issue<Q8, NB>(p, g, c0, A);
     }
     p_stream<Q8, NB>(p, g, A, xs, red);
+    // RMSNorm scale of this phase's input (1 without a norm).
+    const float rn = p->norm ? norm_scale(sred, p->cols, a.eps) : 1.f;
     if (is_cls) {
       // Logits (plain stores, read by the host after the launch) and this
       // workgroup's (max, first index) pair (sampler/argmax_sampler.cpp:5-13).
       float* logits = p->logits;
       const int ks = p->ks;
       for (int lr = threadIdx.x; lr < g.nloc; lr += kPThreads) {
-        const float v = p_row_total(ks, red, lr);
+        const float v = rn * p_row_total(ks, red, lr);
         logits[g.base + lr] = v;
         argmax_merge(bv, bi, v, g.base + lr);
       }
@@ -1094,7 +1091,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       trace_mark(a, slot++);
       break;
     }
-    p_epilogue(p, g, red, pos, tag, xres);
+    p_epilogue(p, g, red, pos, tag, xres, rn);
     __syncthreads();  // red and xres are rewritten by the next phase
     trace_mark(a, slot++);
     if (!pn) break;  // last layer of a prompt position: no classifier
