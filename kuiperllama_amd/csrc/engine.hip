@@ -844,7 +844,7 @@ int setup_persistent(kl_engine* e) {
   const int xres_off = red_off + static_cast<int>((red_floats + 3) & ~size_t(3));
   const int xres_floats = weighted ? share_d : (m.D + e->nwg - 1) / e->nwg;
   const size_t gemv_lds = (static_cast<size_t>(xres_off) + xres_floats) * sizeof(float);
-  const size_t attn_lds = attn_p_lds_floats(m.hd, m.H / m.KVH, e->attn.G) * sizeof(float);
+  const size_t attn_lds = attn_p_lds_floats(m.hd, m.H / m.KVH) * sizeof(float);
   // The residual rows must survive the attention phase, which uses LDS from 0.
   const size_t xres_at = std::max(static_cast<size_t>(xres_off) * sizeof(float),
                                   (attn_lds + 15) & ~size_t(15));

@@ -618,17 +618,19 @@ __device__ __forceinline__ float p_row_total(int ks, const float* red, int lr) {
 // of the kv head merges them.  Rows before pos come from the cache
 // (written by earlier launches); q and the new K/V rows come from the tagged
 // QKV outputs.  The chunk that holds pos writes the transformed K row to the
-// cache for later tokens.  LDS floats needed: attn_p_lds_floats.
+// cache for later tokens.  Inside a chunk: a row's K in registers (HD / 4
+// lanes x float4), scores by 16-lane DPP sums, the heads of the group four at
+// a time so the reductions overlap; V staged to LDS and o = p V summed by
+// groups of 8 adjacent lanes, each group owning one float4 of the output.
+// LDS floats needed: attn_p_lds_floats.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int attn_p_rpp(int hd) { return kPThreads / (hd / 4); }
 
-__host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul, int G) {
+__host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul) {
   const int pt = attn_chunk(hd);
   const size_t head = static_cast<size_t>(kv_mul) * hd + static_cast<size_t>(kv_mul) * pt +
                       2 * static_cast<size_t>(hd) + 2 * kAttnMaxKvMul;
-  const size_t pv = static_cast<size_t>(attn_p_rpp(hd)) * kv_mul * hd;
-  const size_t merge = 2 * static_cast<size_t>(G) * kv_mul;
-  return head + (pv > merge ? pv : merge);
+  return head + static_cast<size_t>(pt) * hd;  // + the chunk's V rows
 }
 
 // What the attention of a layer needs that does not depend on the layer's
@@ -710,7 +712,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
   float* kp = sc + kvm * PT;            // [HD] K[pos] (transformed)
   float* vp = kp + HD;                  // [HD] V[pos]
   float* ml = vp + HD;                  // [2 * kAttnMaxKvMul]
-  float* red = ml + 2 * kAttnMaxKvMul;  // [RPP][kvm][HD]; merge: [nsplit][kvm][2]
+  float* vs = ml + 2 * kAttnMaxKvMul;   // [PT][HD] V rows of the chunk
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int g = it / nsplit;
     const int s = it - g * nsplit;
@@ -825,18 +827,37 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
       }
     }
 
-    // 3. Scores.
+    // The chunk's V rows to LDS for step 5 (row-major [PT][HD]).
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int tt = p * RPP + rr;
+      if (tt < PT) reinterpret_cast<f4*>(vs + static_cast<size_t>(tt) * HD)[sub] = vr[p];
+    }
+
+    // 3. Scores, four heads at a time (the q reads and the 16-lane reductions
+    //    of the four heads and NP rows are independent and overlap).
     {
       const f4* q4 = reinterpret_cast<const f4*>(qs);
+      for (int h0 = 0; h0 < kvm; h0 += 4) {
+        f4 qv[4];
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        const int tt = p * RPP + rr;
+        for (int j = 0; j < 4; ++j) qv[j] = q4[min(h0 + j, kvm - 1) * TPR + sub];
+        float d[NP][4];
 #pragma unroll
-        for (int h = 0; h < kAttnMaxKvMul; ++h) {
-          if (h < kvm) {
-            float d = hsum(kr[p] * q4[h * TPR + sub]);
-            d = group_sum_dpp<TPR>(d);
-            if (sub == TPR - 1 && tt < cnt) sc[h * PT + tt] = d * a.scale;
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[p][j] = hsum(kr[p] * qv[j]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[p][j] = group_sum_dpp<TPR>(d[p][j]);
+        if (sub == TPR - 1) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int tt = p * RPP + rr;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (tt < cnt && h0 + j < kvm) sc[(h0 + j) * PT + tt] = d[p][j] * a.scale;
           }
         }
       }
@@ -861,49 +882,51 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
       }
     }
     __syncthreads();
-    // 5. o_h = sum_t p_h[t] V_t.
-#pragma unroll
-    for (int h = 0; h < kAttnMaxKvMul; ++h) {
-      if (h < kvm) {
+    // 5. o_h = sum_t p_h[t] V_t: each output float4 (head h, dims 4 sub4 ..)
+    //    by PV_T adjacent lanes over PT / PV_T rows each, summed by DPP; the
+    //    chunk's output (one chunk: o / l) or its partial (o, m, l) is stored
+    //    by the first lane of each group.
+    {
+      constexpr int PV_T = 8;
+      constexpr int RPT = PT / PV_T;
+      static_assert(PT % PV_T == 0, "rows per lane");
+      const f4* v4 = reinterpret_cast<const f4*>(vs);
+      tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
+      tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
+      for (int b = tid; b < kvm * TPR * PV_T; b += kPThreads) {
+        const int part = b & (PV_T - 1), o4 = b / PV_T;
+        const int h = o4 / TPR, sub4 = o4 - h * TPR;
+        const float* ph = sc + h * PT;
         f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const int tt = p * RPP + rr;
-          if (tt < cnt) o += sc[h * PT + tt] * vr[p];
+        for (int j = 0; j < RPT; ++j) {
+          const int tt = part * RPT + j;
+          if (tt < cnt) o += ph[tt] * v4[tt * TPR + sub4];
         }
-        reinterpret_cast<f4*>(red + (static_cast<size_t>(rr) * kvm + h) * HD)[sub] = o;
-      }
-    }
-    __syncthreads();
-    tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
-    tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
-    // Row slots summed in two halves (threads idx and idx + 256 of a pair of
-    // outputs), then combined through LDS.
-    {
-      const int half = tid >= kPThreads / 2;
-      for (int idx = tid - half * (kPThreads / 2); idx < kvm * HD; idx += kPThreads / 2) {
-        const int h = idx / HD, d = idx - h * HD;
-        float o = 0.f;
-#pragma unroll 8
-        for (int k = half * (RPP / 2); k < (half + 1) * (RPP / 2); ++k)
-          o += red[(static_cast<size_t>(k) * kvm + h) * HD + d];
-        if (half) red[(static_cast<size_t>(RPP / 2) * kvm + h) * HD + d] = o;  // slot RPP/2: upper sum
-        else red[(static_cast<size_t>(0) * kvm + h) * HD + d] = o;             // slot 0: lower sum
-      }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
-      const int h = idx / HD, d = idx - h * HD;
-      const float o = red[(static_cast<size_t>(0) * kvm + h) * HD + d] +
-                      red[(static_cast<size_t>(RPP / 2) * kvm + h) * HD + d];
-      if (nsplit == 1) {
-        g_st_tagged(outg + h * HD + d, o / ml[2 * h + 1], tag);
-      } else {
-        tagged_t* ps = pg + (static_cast<size_t>(s) * kvm + h) * (HD + 2);
-        g_st_tagged(ps + d, o, tag);
-        if (d == 0) {
-          g_st_tagged(ps + HD, ml[2 * h], tag);
-          g_st_tagged(ps + HD + 1, ml[2 * h + 1], tag);
+        o.x = group_sum_dpp<PV_T>(o.x);
+        o.y = group_sum_dpp<PV_T>(o.y);
+        o.z = group_sum_dpp<PV_T>(o.z);
+        o.w = group_sum_dpp<PV_T>(o.w);
+        if (part == 0) {
+          const int d = 4 * sub4;
+          if (nsplit == 1) {
+            const float l = ml[2 * h + 1];
+            tagged_t* op = outg + h * HD + d;
+            g_st_tagged(op + 0, o.x / l, tag);
+            g_st_tagged(op + 1, o.y / l, tag);
+            g_st_tagged(op + 2, o.z / l, tag);
+            g_st_tagged(op + 3, o.w / l, tag);
+          } else {
+            tagged_t* ps = pg + (static_cast<size_t>(s) * kvm + h) * (HD + 2);
+            g_st_tagged(ps + d + 0, o.x, tag);
+            g_st_tagged(ps + d + 1, o.y, tag);
+            g_st_tagged(ps + d + 2, o.z, tag);
+            g_st_tagged(ps + d + 3, o.w, tag);
+            if (d == 0) {
+              g_st_tagged(ps + HD, ml[2 * h], tag);
+              g_st_tagged(ps + HD + 1, ml[2 * h + 1], tag);
+            }
+          }
         }
       }
     }
@@ -911,53 +934,48 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
   }
   if (nsplit == 1) return;
   // 6. The workgroup that owns chunk 0 of a kv head merges its chunks, once all
-  //    of this workgroup's own chunks are written (so it never waits on itself):
-  //    O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+  //    of this workgroup's own chunks are written (so it never waits on itself).
+  //    Every output element polls the chunks' (o, m, l) together, eight chunks
+  //    per round trip, and merges them online:
+  //    M' = max(M, m_s), L' = L e^(M - M') + l_s e^(m_s - M'),
+  //    O' = O e^(M - M') + o_s e^(m_s - M'); the output is O / L.
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int g = it / nsplit;
     if (it - g * nsplit != 0) continue;
     const tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
-    float* mls = lds;  // [nsplit][kvm][2]
-    for (int i = tid; i < nsplit * kvm; i += kPThreads) {
-      const tagged_t* pk = pg + static_cast<size_t>(i) * (HD + 2);
-      tagged_t v[2] = {g_ld64(pk + HD), g_ld64(pk + HD + 1)};
-      poll_many<2>(a, tag, [&](int k) { return pk + HD + k; }, 3u, v);
-      mls[2 * i] = val_of(v[0]);
-      mls[2 * i + 1] = val_of(v[1]);
-    }
-    __syncthreads();
     tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
     for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
       const int h = idx / HD, d = idx - h * HD;
-      float M = -INFINITY;
-      for (int k = 0; k < nsplit; ++k) M = fmaxf(M, mls[2 * (k * kvm + h)]);
-      float L = 0.f, O = 0.f;
-      // The chunks' partial outputs, 8 at a time, polled together.
+      float M = -INFINITY, L = 0.f, O = 0.f;
       for (int k0 = 0; k0 < nsplit; k0 += 8) {
-        auto addr = [&](int k) {
-          const int kk = k0 + k < nsplit ? k0 + k : 0;
-          return pg + (static_cast<size_t>(kk) * kvm + h) * (HD + 2) + d;
+        // e < 8: o of chunk k0 + e; 8 <= e < 16: its m; 16 <= e < 24: its l.
+        auto addr = [&](int e) {
+          const int k = e & 7, kk = k0 + k < nsplit ? k0 + k : 0;
+          const tagged_t* ps = pg + (static_cast<size_t>(kk) * kvm + h) * (HD + 2);
+          return e < 8 ? ps + d : ps + HD + (e >> 4);
         };
-        tagged_t v[8];
+        tagged_t v[24];
         unsigned int valid = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (k0 + k < nsplit) valid |= 1u << k;
-          v[k] = g_ld64(addr(k));
+        for (int e = 0; e < 24; ++e) {
+          if (k0 + (e & 7) < nsplit) valid |= 1u << e;
+          v[e] = g_ld64(addr(e));
         }
-        poll_many<8>(a, tag, addr, valid, v);
+        poll_many<24>(a, tag, addr, valid, v);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           if (k0 + k < nsplit) {
-            const float w = expf(mls[2 * ((k0 + k) * kvm + h)] - M);
-            L += mls[2 * ((k0 + k) * kvm + h) + 1] * w;
-            O += val_of(v[k]) * w;
+            const float ms = val_of(v[8 + k]);
+            const float Mn = fmaxf(M, ms);
+            const float c = expf(M - Mn), w = expf(ms - Mn);
+            L = L * c + val_of(v[16 + k]) * w;
+            O = O * c + val_of(v[k]) * w;
+            M = Mn;
           }
         }
       }
       g_st_tagged(outg + h * HD + d, O / L, tag);
     }
-    __syncthreads();
   }
 }
 
