@@ -961,35 +961,44 @@ int trace_once(kl_engine* e, int32_t token, int32_t pos, unsigned long long* tic
 // plan stays the balanced one).  KL_PCALIBRATE=0 keeps the balanced split.
 int calibrate_persistent(kl_engine* e) {
   if (!e->persistent_ok || !e->trace_ok || e->mode != KL_MODE_PERSISTENT) return KL_OK;
-  if (const char* env = std::getenv("KL_PCALIBRATE"))
-    if (std::atoi(env) == 0) return KL_OK;
+  // Passes of the fixed-point iteration (KL_PCALIBRATE; 0 disables): each
+  // re-measures the FFN phases with the current split and scales every
+  // workgroup's weight by mean work / its work.  One pass: a second evens out
+  // the per-XCD means further but does not lower the slowest workgroup, whose
+  // identity varies from step to step (measured).
+  int passes = 1;
+  if (const char* env = std::getenv("KL_PCALIBRATE")) passes = std::max(0, std::atoi(env));
   const int L = e->lay.L, W = e->nwg;
-  if (e->lay.S < 4) return KL_OK;
+  if (e->lay.S < 4 || passes == 0) return KL_OK;
   std::vector<unsigned long long> t(static_cast<size_t>(2 * 5 * L + 3) * W);
-  std::vector<double> work(W, 0.0);
-  for (int rep = 0; rep < 4; ++rep) {
-    const int r = trace_once(e, 0, rep, t.data());
+  std::vector<double> wt(W, 1.0);
+  for (int pass = 0; pass < passes; ++pass) {
+    std::vector<double> work(W, 0.0);
+    for (int rep = 0; rep < 4; ++rep) {
+      const int r = trace_once(e, 0, rep, t.data());
+      if (r != KL_OK) return r;
+      if (rep == 0) continue;  // warm-up
+      for (int l = 0; l < L; ++l)
+        for (int p : {5 * l + 3, 5 * l + 4}) {  // W1/W3, W2
+          const unsigned long long* ready = t.data() + static_cast<size_t>(2 * p + 1) * W;
+          const unsigned long long* done = t.data() + static_cast<size_t>(2 * p + 2) * W;
+          for (int b = 0; b < W; ++b)
+            work[b] += done[b] > ready[b] ? static_cast<double>(done[b] - ready[b]) : 0.0;
+        }
+    }
+    double mean = 0.0;
+    for (double w : work) mean += w;
+    mean /= W;
+    if (!(mean > 0.0)) return KL_OK;
+    for (int b = 0; b < W; ++b) {
+      const double sp = work[b] > 0.0 ? mean / work[b] : 1.0;  // relative speed
+      wt[b] = std::min(1.25, std::max(0.8, wt[b] * sp));
+    }
+    e->wg_weight = wt;
+    const int r = setup_persistent(e);
     if (r != KL_OK) return r;
-    if (rep == 0) continue;  // warm-up
-    for (int l = 0; l < L; ++l)
-      for (int p : {5 * l + 3, 5 * l + 4}) {  // W1/W3, W2
-        const unsigned long long* ready = t.data() + static_cast<size_t>(2 * p + 1) * W;
-        const unsigned long long* done = t.data() + static_cast<size_t>(2 * p + 2) * W;
-        for (int b = 0; b < W; ++b)
-          work[b] += done[b] > ready[b] ? static_cast<double>(done[b] - ready[b]) : 0.0;
-      }
   }
-  double mean = 0.0;
-  for (double w : work) mean += w;
-  mean /= W;
-  if (!(mean > 0.0)) return KL_OK;
-  std::vector<double> wt(W);
-  for (int b = 0; b < W; ++b) {
-    const double sp = work[b] > 0.0 ? mean / work[b] : 1.0;  // relative speed
-    wt[b] = std::min(1.25, std::max(0.8, sp));
-  }
-  e->wg_weight = wt;
-  return setup_persistent(e);
+  return KL_OK;
 }
 
 }  // namespace
