@@ -1332,7 +1332,6 @@ int prefill_scratch(kl_engine* e, int rows) {
   hipError_t err = hipMalloc(&buf, total);
   if (err != hipSuccess) return KL_ENOMEM;
   if (e->pf_buf) (void)hipFree(e->pf_buf);
-  if (e->d_split) (void)hipFree(e->d_split);
   e->pf_buf = buf;
   size_t off = 0;
   auto take = [&](size_t b) {
