@@ -9,13 +9,17 @@
 // of C; each wave owns TM x TN blocks of 32 x 32 accumulated with
 // v_mfma_f32_32x32x2f32 (A operand: lane l holds A[l % 32][k], B operand:
 // W[l % 32][k], result register r of lane l is C[8 (r / 4) + 4 (l / 32) +
-// r % 4][l % 32]).  K advances in blocks of 16 staged in LDS (double
+// r % 4][l % 32]).  K advances in blocks of 32 staged in LDS (double
 // buffered, one barrier per block, the next block's global loads in flight
-// during the current block's MFMAs).  Inside a block the 16 k indices are
-// visited in the order that lets each lane fetch its 8 operands of a block
-// with two ds_read_b128: MFMA step s uses, in lane l, column 8 (l / 32) + s.
+// during the current block's 16 MFMAs).  Inside a block the 32 k indices are
+// visited in the order that lets each lane fetch its 16 operands of a block
+// with four ds_read_b128: MFMA step s uses, in lane l, column 16 (l / 32) + s.
 // The same permutation applies to both operands, so every product
-// A[m][k] W[n][k] is formed exactly once.
+// A[m][k] W[n][k] is formed exactly once.  (Measured at the Qwen3-4B prefill
+// shapes, M = 512: blocks of 32 are 3-7% faster than 16; 64 x 64 tiles of four
+// waves beat 128 x 64, 64 x 128 and 128 x 128 tiles, which leave too few
+// workgroups; two accumulators per wave or loads two blocks ahead change
+// nothing.)
 //
 // Grouped launches compute up to three outputs over the same A (the Q, K and V
 // projections) in one grid, and split-K divides the K blocks among
@@ -31,7 +35,7 @@ namespace kl {
 typedef float gf4 __attribute__((ext_vector_type(4)));
 typedef float gf16 __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmBK = 16;
+constexpr int kGemmBK = 32;
 constexpr int kGemmLDK = kGemmBK + 4;  // padded LDS row (floats)
 constexpr int kGemmMaxSeg = 3;
 
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int idx = tid + i * NT;
-      const int r = idx >> 2, c = (idx & 3) * 4;
+      const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
       const int m = m0 + r, k = k0 + c;
       const bool ok = (A4 % NT == 0 || idx < A4) && m < M && k < K;
       oka |= ok ? 1u << i : 0u;
@@ -119,7 +123,7 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
       const int idx = tid + i * NT;
-      const int r = idx >> 2, c = (idx & 3) * 4;
+      const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
       const int n = n0 + r, k = k0 + c;
       const bool ok = (W4 % NT == 0 || idx < W4) && n < N && k < K;
       okw |= ok ? 1u << i : 0u;
@@ -132,13 +136,13 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
     for (int i = 0; i < LA; ++i) {
       const int idx = tid + i * NT;
       if (A4 % NT == 0 || idx < A4)
-        *reinterpret_cast<gf4*>(&As[buf][(idx >> 2) * LDK + (idx & 3) * 4]) = ((oka >> i) & 1u) ? ra[i] : z;
+        *reinterpret_cast<gf4*>(&As[buf][(idx / (BK / 4)) * LDK + (idx % (BK / 4)) * 4]) = ((oka >> i) & 1u) ? ra[i] : z;
     }
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
       const int idx = tid + i * NT;
       if (W4 % NT == 0 || idx < W4)
-        *reinterpret_cast<gf4*>(&Ws[buf][(idx >> 2) * LDK + (idx & 3) * 4]) = ((okw >> i) & 1u) ? rw[i] : z;
+        *reinterpret_cast<gf4*>(&Ws[buf][(idx / (BK / 4)) * LDK + (idx % (BK / 4)) * 4]) = ((okw >> i) & 1u) ? rw[i] : z;
     }
   };
 
@@ -153,25 +157,27 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
     sstore(0);
   }
   __syncthreads();
-  const int kc = 8 * (lane >> 5);  // this lane's 8 columns of a k block
+  constexpr int KH = BK / 2;       // columns of a k block per lane half
+  constexpr int NR = KH / 4;       // float4 reads per operand
+  const int kc = KH * (lane >> 5);  // this lane's KH columns of a k block
   for (int kt = kb0; kt < kb1; ++kt) {
     const int cur = (kt - kb0) & 1;
     if (kt + 1 < kb1) gload((kt + 1) * BK);
-    gf4 af[TM][2], bf[TN][2];
+    gf4 af[TM][NR], bf[TN][NR];
 #pragma unroll
     for (int a = 0; a < TM; ++a) {
       const float* p = &As[cur][(wm * TM * 32 + a * 32 + (lane & 31)) * LDK + kc];
-      af[a][0] = *reinterpret_cast<const gf4*>(p);
-      af[a][1] = *reinterpret_cast<const gf4*>(p + 4);
+#pragma unroll
+      for (int j = 0; j < NR; ++j) af[a][j] = *reinterpret_cast<const gf4*>(p + 4 * j);
     }
 #pragma unroll
     for (int b = 0; b < TN; ++b) {
       const float* p = &Ws[cur][(wn * TN * 32 + b * 32 + (lane & 31)) * LDK + kc];
-      bf[b][0] = *reinterpret_cast<const gf4*>(p);
-      bf[b][1] = *reinterpret_cast<const gf4*>(p + 4);
+#pragma unroll
+      for (int j = 0; j < NR; ++j) bf[b][j] = *reinterpret_cast<const gf4*>(p + 4 * j);
     }
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < KH; ++s)
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
