@@ -620,18 +620,26 @@ namespace {
 template <int HD>
 int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
                         int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st) {
-  const size_t lds = attn_prefill_lds_bytes(HD);
+  // Head sizes 64 and 128 on the matrix cores; 32 on the vector ALUs.
+  constexpr bool kMfma = HD == 64 || HD == 128;
+  const void* fn = kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_mfma<kMfma ? HD : 64>)
+                         : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
+  const size_t lds = kMfma ? attn_prefill_mfma_lds_bytes(HD) : attn_prefill_lds_bytes(HD);
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_prefill<HD>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds));
     if (e != hipSuccess) return rc(e);
     attr_set = true;
   }
   const float scale = 1.f / std::sqrt(static_cast<float>(HD));
-  hipLaunchKernelGGL(k_attn_prefill<HD>, dim3((n + kPrefillQB - 1) / kPrefillQB, heads), dim3(256),
-                     lds, st, q, ldq, kc, vc, kv_dim, kv_mul, out, ldo, pos0, n, scale);
+  const dim3 grid((n + kPrefillQB - 1) / kPrefillQB, heads);
+  if constexpr (kMfma)
+    hipLaunchKernelGGL(k_attn_prefill_mfma<HD>, grid, dim3(256), lds, st, q, ldq, kc, vc, kv_dim,
+                       kv_mul, out, ldo, pos0, n, scale);
+  else
+    hipLaunchKernelGGL(k_attn_prefill<HD>, grid, dim3(256), lds, st, q, ldq, kc, vc, kv_dim, kv_mul,
+                       out, ldo, pos0, n, scale);
   return launch_rc();
 }
 }  // namespace

@@ -144,4 +144,173 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
   }
 }
 
+// The same attention on the matrix cores (head sizes 64 and 128):
+// flash-attention over key blocks of 64 with v_mfma_f32_32x32x2f32 (lane l
+// supplies A[l % 32][k = l / 32] and B[k = l / 32][l % 32]; result register r
+// of lane l is D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  Four waves per
+// 64 query rows of one head: wave (wm, wn) = (w % 2, w / 2) computes the
+// scores of rows 32 wm .. against keys 32 wn .. of the block (S = Q K^T, k
+// running over d), and the output of rows 32 wm .. for columns wn HD / 2 ..
+// (O += P V, k running over the 64 keys).  In both products lane half h takes
+// the k indices of its half of the range in order, so each lane reads its
+// operands as contiguous runs: its Q row slice stays in registers, K is kept
+// row-major and V transposed in LDS.  Only the row maxima cross waves (through
+// LDS); each wave keeps the partial row sums of its key half, combined at the
+// end.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restrict__ q, int ldq,
+                                                           const float* __restrict__ kc,
+                                                           const float* __restrict__ vc,
+                                                           int kv_dim, int kv_mul,
+                                                           float* __restrict__ out, int ldo,
+                                                           int pos0, int n, float scale) {
+  static_assert(HD == 64 || HD == 128, "head size");
+  typedef float f16v __attribute__((ext_vector_type(16)));
+  constexpr int QB = kPrefillQB, KB = kPrefillKB;
+  constexpr int LDK = HD + 4;  // K row (floats)
+  constexpr int LDV = KB + 4;  // V^T row
+  constexpr int LDP = KB + 4;  // P row
+  constexpr int HH = HD / 2;   // d per lane half (scores) and columns per wave (output)
+  constexpr int OT = HH / 32;  // 32 x 32 output tiles per wave
+  extern __shared__ __align__(16) float sm[];
+  float* Ks = sm;                 // [KB][LDK]
+  float* Vt = Ks + KB * LDK;      // [HD][LDV]
+  float* Ps = Vt + HD * LDV;      // [QB][LDP]
+  float* rmax = Ps + QB * LDP;    // [2][QB] per key half
+  float* rsum = rmax + 2 * QB;    // [2][QB]
+  const int h = blockIdx.y, g = h / kv_mul;
+  const int p0 = blockIdx.x * QB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1, hl = lane >> 5, li = lane & 31;
+
+  // This lane's Q slice: row 32 wm + li, d in [HH hl, HH hl + HH).
+  pf4 qr[HH / 4];
+  {
+    const int p = p0 + 32 * wm + li;
+    const float* qp = q + static_cast<size_t>(p < n ? p : 0) * ldq + h * HD + HH * hl;
+#pragma unroll
+    for (int j = 0; j < HH / 4; ++j)
+      qr[j] = p < n ? *reinterpret_cast<const pf4*>(qp + 4 * j) : pf4{0.f, 0.f, 0.f, 0.f};
+  }
+  // Rows of this lane's accumulator registers: 32 wm + 8 (r / 4) + 4 hl + r % 4.
+  float m[16], lsum[16];
+  f16v o[OT];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    m[r] = -INFINITY;
+    lsum[r] = 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < OT; ++t) o[t] = f16v{};
+  const int rows = n - p0 < QB ? n - p0 : QB;
+  const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
+  const int qbase = pos0 + p0 + 32 * wm + 4 * hl;
+  for (int j0 = 0; j0 <= last; j0 += KB) {
+    __syncthreads();  // the previous block's K, V and P are consumed
+    for (int i = tid; i < KB * HD / 4; i += 256) {
+      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+      const int j = j0 + r;
+      const size_t off = static_cast<size_t>(j <= last ? j : 0) * kv_dim + g * HD + c;
+      pf4 kv = *reinterpret_cast<const pf4*>(kc + off);
+      pf4 vv = *reinterpret_cast<const pf4*>(vc + off);
+      if (j > last) kv = vv = pf4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<pf4*>(Ks + r * LDK + c) = kv;
+      Vt[(c + 0) * LDV + r] = vv.x;
+      Vt[(c + 1) * LDV + r] = vv.y;
+      Vt[(c + 2) * LDV + r] = vv.z;
+      Vt[(c + 3) * LDV + r] = vv.w;
+    }
+    __syncthreads();
+    // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
+    f16v sacc = f16v{};
+    {
+      const float* kp = Ks + (32 * wn + li) * LDK + HH * hl;
+#pragma unroll
+      for (int j = 0; j < HH / 4; ++j) {
+        const pf4 kv = *reinterpret_cast<const pf4*>(kp + 4 * j);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].x, kv.x, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].y, kv.y, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].z, kv.z, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].w, kv.w, sacc, 0, 0, 0);
+      }
+    }
+    // Scale, causal mask, and the row maxima over this wave's 32 keys.
+    const int kpos = j0 + 32 * wn + li;
+    float sv[16], mx[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qpos = qbase + 8 * (r >> 2) + (r & 3);
+      sv[r] = kpos <= qpos ? sacc[r] * scale : -INFINITY;
+      float v = sv[r];
+#pragma unroll
+      for (int w = 1; w < 32; w <<= 1) v = fmaxf(v, __shfl_xor(v, w, 32));
+      mx[r] = v;
+    }
+    if (li == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rmax[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = mx[r];
+    }
+    __syncthreads();
+    float alpha[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
+      const float mn = fmaxf(m[r], fmaxf(mx[r], rmax[(1 - wn) * QB + row]));
+      // Key 0 is in the first block for every row, so mn is finite from then on.
+      alpha[r] = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
+      m[r] = mn;
+      const float pv = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mn);
+      Ps[row * LDP + 32 * wn + li] = pv;
+      float s = pv;
+#pragma unroll
+      for (int w = 1; w < 32; w <<= 1) s += __shfl_xor(s, w, 32);
+      lsum[r] = lsum[r] * alpha[r] + s;
+    }
+    __syncthreads();
+    // O = O alpha + P V for rows 32 wm .., columns wn HH + 32 t ...
+#pragma unroll
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha[r];
+    {
+      const float* pp = Ps + (32 * wm + li) * LDP + 32 * hl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const pf4 pv = *reinterpret_cast<const pf4*>(pp + 4 * j);
+#pragma unroll
+        for (int t = 0; t < OT; ++t) {
+          const pf4 vv = *reinterpret_cast<const pf4*>(Vt + (wn * HH + 32 * t + li) * LDV + 32 * hl + 4 * j);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.x, vv.x, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.y, vv.y, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.z, vv.z, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.w, vv.w, o[t], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // Row sums: this wave's key half plus the other's.
+  if (li == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rsum[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = lsum[r];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
+    const int p = p0 + row;
+    if (p < n) {
+      const float l = lsum[r] + rsum[(1 - wn) * QB + row];
+      float* op = out + static_cast<size_t>(p) * ldo + h * HD + wn * HH + li;
+#pragma unroll
+      for (int t = 0; t < OT; ++t) op[32 * t] = o[t][r] / l;
+    }
+  }
+}
+
+__host__ __device__ constexpr size_t attn_prefill_mfma_lds_bytes(int hd) {
+  return (static_cast<size_t>(kPrefillKB) * (hd + 4) + static_cast<size_t>(hd) * (kPrefillKB + 4) +
+          static_cast<size_t>(kPrefillQB) * (kPrefillKB + 4) + 4 * kPrefillQB) *
+         sizeof(float);
+}
+
 }  // namespace kl
