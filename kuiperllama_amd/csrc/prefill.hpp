@@ -157,6 +157,28 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 // row-major and V transposed in LDS.  Only the row maxima cross waves (through
 // LDS); each wave keeps the partial row sums of its key half, combined at the
 // end.
+// Maximum / sum over the 32 lanes of each half wave, in every lane: DPP
+// within each 16-lane row (quad permutes and mirrors), then one exchange
+// between the two rows of the half.
+template <int CTRL>
+__device__ __forceinline__ float pf_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float half_max(float v) {
+  v = fmaxf(v, pf_dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, pf_dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, pf_dpp<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, pf_dpp<0x140>(v));  // row_mirror
+  return fmaxf(v, __shfl_xor(v, 16, 32));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  v += pf_dpp<0xB1>(v);
+  v += pf_dpp<0x4E>(v);
+  v += pf_dpp<0x141>(v);
+  v += pf_dpp<0x140>(v);
+  return v + __shfl_xor(v, 16, 32);
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restrict__ q, int ldq,
                                                            const float* __restrict__ kc,
@@ -241,10 +263,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
     for (int r = 0; r < 16; ++r) {
       const int qpos = qbase + 8 * (r >> 2) + (r & 3);
       sv[r] = kpos <= qpos ? sacc[r] * scale : -INFINITY;
-      float v = sv[r];
-#pragma unroll
-      for (int w = 1; w < 32; w <<= 1) v = fmaxf(v, __shfl_xor(v, w, 32));
-      mx[r] = v;
+      mx[r] = half_max(sv[r]);
     }
     if (li == 0) {
 #pragma unroll
@@ -261,10 +280,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
       m[r] = mn;
       const float pv = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mn);
       Ps[row * LDP + 32 * wn + li] = pv;
-      float s = pv;
-#pragma unroll
-      for (int w = 1; w < 32; w <<= 1) s += __shfl_xor(s, w, 32);
-      lsum[r] = lsum[r] * alpha[r] + s;
+      lsum[r] = lsum[r] * alpha[r] + half_sum(pv);
     }
     __syncthreads();
     // O = O alpha + P V for rows 32 wm .., columns wn HH + 32 t ...
