@@ -152,11 +152,12 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 // scores of rows 32 wm .. against keys 32 wn .. of the block (S = Q K^T, k
 // running over d), and the output of rows 32 wm .. for columns wn HD / 2 ..
 // (O += P V, k running over the 64 keys).  In both products lane half h takes
-// the k indices of its half of the range in order, so each lane reads its
-// operands as contiguous runs: its Q row slice stays in registers, K is kept
-// row-major and V transposed in LDS.  Only the row maxima cross waves (through
-// LDS); each wave keeps the partial row sums of its key half, combined at the
-// end.
+// the k indices of its half of the range in order: a lane's Q row slice stays
+// in registers and its K and P operands are contiguous runs of a row in LDS;
+// the V operand of step s is one float of key row 32 h + s, read by the 32
+// lanes of a half as consecutive floats.  Only the row maxima cross waves
+// (through LDS); each wave keeps the partial row sums of its key half,
+// combined at the end.
 // Maximum / sum over the 32 lanes of each half wave, in every lane: DPP
 // within each 16-lane row (quad permutes and mirrors), then one exchange
 // between the two rows of the half.
@@ -189,15 +190,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
   static_assert(HD == 64 || HD == 128, "head size");
   typedef float f16v __attribute__((ext_vector_type(16)));
   constexpr int QB = kPrefillQB, KB = kPrefillKB;
-  constexpr int LDK = HD + 4;  // K row (floats)
-  constexpr int LDV = KB + 4;  // V^T row
+  constexpr int LDK = HD + 4;  // K and V row (floats)
   constexpr int LDP = KB + 4;  // P row
   constexpr int HH = HD / 2;   // d per lane half (scores) and columns per wave (output)
   constexpr int OT = HH / 32;  // 32 x 32 output tiles per wave
   extern __shared__ __align__(16) float sm[];
   float* Ks = sm;                 // [KB][LDK]
-  float* Vt = Ks + KB * LDK;      // [HD][LDV]
-  float* Ps = Vt + HD * LDV;      // [QB][LDP]
+  float* Vs = Ks + KB * LDK;      // [KB][LDK]
+  float* Ps = Vs + KB * LDK;      // [QB][LDP]
   float* rmax = Ps + QB * LDP;    // [2][QB] per key half
   float* rsum = rmax + 2 * QB;    // [2][QB]
   const int h = blockIdx.y, g = h / kv_mul;
@@ -237,10 +237,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
       pf4 vv = *reinterpret_cast<const pf4*>(vc + off);
       if (j > last) kv = vv = pf4{0.f, 0.f, 0.f, 0.f};
       *reinterpret_cast<pf4*>(Ks + r * LDK + c) = kv;
-      Vt[(c + 0) * LDV + r] = vv.x;
-      Vt[(c + 1) * LDV + r] = vv.y;
-      Vt[(c + 2) * LDV + r] = vv.z;
-      Vt[(c + 3) * LDV + r] = vv.w;
+      *reinterpret_cast<pf4*>(Vs + r * LDK + c) = vv;
     }
     __syncthreads();
     // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
@@ -295,11 +292,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
         const pf4 pv = *reinterpret_cast<const pf4*>(pp + 4 * j);
 #pragma unroll
         for (int t = 0; t < OT; ++t) {
-          const pf4 vv = *reinterpret_cast<const pf4*>(Vt + (wn * HH + 32 * t + li) * LDV + 32 * hl + 4 * j);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.x, vv.x, o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.y, vv.y, o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.z, vv.z, o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.w, vv.w, o[t], 0, 0, 0);
+          const float* vp = Vs + (32 * hl + 4 * j) * LDK + wn * HH + 32 * t + li;
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.x, vp[0], o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.y, vp[LDK], o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.z, vp[2 * LDK], o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.w, vp[3 * LDK], o[t], 0, 0, 0);
         }
       }
     }
@@ -324,7 +321,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
 }
 
 __host__ __device__ constexpr size_t attn_prefill_mfma_lds_bytes(int hd) {
-  return (static_cast<size_t>(kPrefillKB) * (hd + 4) + static_cast<size_t>(hd) * (kPrefillKB + 4) +
+  return (2 * static_cast<size_t>(kPrefillKB) * (hd + 4) +
           static_cast<size_t>(kPrefillQB) * (kPrefillKB + 4) + 4 * kPrefillQB) *
          sizeof(float);
 }
