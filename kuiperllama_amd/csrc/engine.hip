@@ -870,6 +870,11 @@ int setup_persistent(kl_engine* e) {
   a.q = e->t_q; a.knew = e->t_k; a.vnew = e->t_v; a.att = e->t_att;
   a.attn_part = e->t_part;
   a.attn_G = e->attn.G;
+  // Attention merge beyond kAttnMergeChunks chunks per kv head: one merging
+  // workgroup per 2 chunks (measured best of 1, 2, 4, 8 on Qwen2.5-1.5B at
+  // 4000 positions; KL_ATTN_MERGE_CHUNKS overrides).
+  a.merge_chunks = 2;
+  if (const char* env = std::getenv("KL_ATTN_MERGE_CHUNKS")) a.merge_chunks = std::max(1, std::atoi(env));
   a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
   a.epoch = e->epoch; a.err = e->derr;
   a.red_off = red_off;

@@ -128,6 +128,7 @@ struct PArgs {
   tagged_t* att;           // attention output [Dq] (tagged)
   tagged_t* attn_part;     // split partials [KVH][G][kv_mul][HD + 2] (tagged)
   int attn_G;              // chunk slots per kv head
+  int merge_chunks;        // chunks per merging workgroup beyond kAttnMergeChunks chunks
   float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
   unsigned int* am_cnt;    // end-of-step arrival counter
@@ -614,8 +615,8 @@ __device__ __forceinline__ float p_row_total(int ks, const float* red, int lr) {
 // optional Qwen3 per-head q/k RMSNorm (model/qwen3.cpp:485-500) and RoPE
 // (kernels/cpu/rope_kernel.cpp) applied first).  One item = (kv head, chunk
 // of PT positions); items are spread over the workgroups; every chunk writes
-// its partial (o, m, l) as tagged values and the workgroup that owns chunk 0
-// of the kv head merges them.  Rows before pos come from the cache
+// its partial (o, m, l) as tagged values, and the workgroups of a kv head's
+// chunks merge them, each a slice of the head's outputs.  Rows before pos come from the cache
 // (written by earlier launches); q and the new K/V rows come from the tagged
 // QKV outputs.  The chunk that holds pos writes the transformed K row to the
 // cache for later tokens.  Inside a chunk: a row's K in registers (HD / 4
@@ -625,6 +626,7 @@ __device__ __forceinline__ float p_row_total(int ks, const float* red, int lr) {
 // LDS floats needed: attn_p_lds_floats.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int attn_p_rpp(int hd) { return kPThreads / (hd / 4); }
+constexpr int kAttnMergeChunks = 8;  // chunks per merging workgroup
 
 __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul) {
   const int pt = attn_chunk(hd);
@@ -933,24 +935,52 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     __syncthreads();  // LDS is reused by the next item
   }
   if (nsplit == 1) return;
-  // 6. The workgroup that owns chunk 0 of a kv head merges its chunks, once all
-  //    of this workgroup's own chunks are written (so it never waits on itself).
-  //    Every output element polls the chunks' (o, m, l) together, eight chunks
-  //    per round trip, and merges them online:
-  //    M' = max(M, m_s), L' = L e^(M - M') + l_s e^(m_s - M'),
-  //    O' = O e^(M - M') + o_s e^(m_s - M'); the output is O / L.
+  // 6. Merge, once all of this workgroup's own chunks are written (so it never
+  //    waits on itself): the kvm * HD outputs of kv head g are split over
+  //    MW = ceil(nsplit / kAttnMergeChunks) merging workgroups, those of chunks
+  //    0, kAttnMergeChunks, 2 kAttnMergeChunks, ... (one per head up to that
+  //    many chunks, where a single merger is fastest; at long contexts the
+  //    reads a merger makes would otherwise be bound by one CU's read rate).
+  //    Merger m takes outputs [m E / MW, (m + 1) E / MW).  T adjacent lanes
+  //    share an output; each polls the
+  //    (o, m, l) of every T-th chunk, eight per round trip, merges them online,
+  //    and the T partials are combined by lane exchanges:
+  //    M = max(M1, M2), L = L1 e^(M1 - M) + L2 e^(M2 - M), likewise O; the
+  //    output is O / L.
+  auto merge2 = [](float& M, float& L, float& O, float m2, float l2, float o2) {
+    const float Mn = fmaxf(M, m2);
+    if (Mn == -INFINITY) return;  // neither side holds a chunk yet
+    const float c1 = M == -INFINITY ? 0.f : expf(M - Mn);
+    const float c2 = m2 == -INFINITY ? 0.f : expf(m2 - Mn);
+    L = L * c1 + l2 * c2;
+    O = O * c1 + o2 * c2;
+    M = Mn;
+  };
+  const int E = kvm * HD;
+  const int R = nsplit <= kAttnMergeChunks ? kAttnMergeChunks : a.merge_chunks;
+  const int MW = (nsplit + R - 1) / R;
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int g = it / nsplit;
-    if (it - g * nsplit != 0) continue;
+    const int s = it - g * nsplit;
+    if (s % R != 0) continue;
+    const int mi = s / R;
+    const int lo = static_cast<int>(static_cast<long long>(mi) * E / MW);
+    const int cnt = static_cast<int>(static_cast<long long>(mi + 1) * E / MW) - lo;
+    if (cnt <= 0) continue;
+    int T = kWave;  // lanes per output (uniform)
+    while (T > 1 && T * cnt > kPThreads) T >>= 1;
     const tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
     tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
-    for (int idx = tid; idx < kvm * HD; idx += kPThreads) {
+    for (int base = tid; base < ((cnt * T + kWave - 1) / kWave) * kWave; base += kPThreads) {
+      const int j = base / T, c = base - j * T;
+      const bool active = j < cnt;
+      const int idx = lo + (active ? j : 0);
       const int h = idx / HD, d = idx - h * HD;
       float M = -INFINITY, L = 0.f, O = 0.f;
-      for (int k0 = 0; k0 < nsplit; k0 += 8) {
-        // e < 8: o of chunk k0 + e; 8 <= e < 16: its m; 16 <= e < 24: its l.
+      for (int k0 = c; k0 < nsplit && active; k0 += 8 * T) {
+        // e < 8: o of chunk k0 + (e & 7) T; 8 <= e < 16: its m; 16 <= e < 24: its l.
         auto addr = [&](int e) {
-          const int k = e & 7, kk = k0 + k < nsplit ? k0 + k : 0;
+          const int k = k0 + (e & 7) * T, kk = k < nsplit ? k : 0;
           const tagged_t* ps = pg + (static_cast<size_t>(kk) * kvm + h) * (HD + 2);
           return e < 8 ? ps + d : ps + HD + (e >> 4);
         };
@@ -958,23 +988,19 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         unsigned int valid = 0;
 #pragma unroll
         for (int e = 0; e < 24; ++e) {
-          if (k0 + (e & 7) < nsplit) valid |= 1u << e;
-          v[e] = g_ld64(addr(e));
+          const bool ok = k0 + (e & 7) * T < nsplit;
+          if (ok) valid |= 1u << e;
+          v[e] = ok ? g_ld64(addr(e)) : 0;  // only the chunks that exist are read
         }
         poll_many<24>(a, tag, addr, valid, v);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (k0 + k < nsplit) {
-            const float ms = val_of(v[8 + k]);
-            const float Mn = fmaxf(M, ms);
-            const float c = expf(M - Mn), w = expf(ms - Mn);
-            L = L * c + val_of(v[16 + k]) * w;
-            O = O * c + val_of(v[k]) * w;
-            M = Mn;
-          }
-        }
+        for (int k = 0; k < 8; ++k)
+          if (k0 + k * T < nsplit) merge2(M, L, O, val_of(v[8 + k]), val_of(v[16 + k]), val_of(v[k]));
       }
-      g_st_tagged(outg + h * HD + d, O / L, tag);
+      // Combine the T lanes of this output (adjacent lanes, T divides 64).
+      for (int w = 1; w < T; w <<= 1)
+        merge2(M, L, O, __shfl_xor(M, w), __shfl_xor(L, w), __shfl_xor(O, w));
+      if (active && c == 0) g_st_tagged(outg + idx, O / L, tag);
     }
   }
 }
