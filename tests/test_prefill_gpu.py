@@ -157,7 +157,7 @@ def test_rope_rows_bit_exact(K, O, gpu, style, dim, kv, hd, pos0, n):
 # ----------------------------------------------------------- attention ------
 @pytest.mark.parametrize("H,kvm,hd,S,pos0,n", [(12, 1, 64, 160, 0, 143), (32, 4, 128, 256, 0, 200),
                                               (4, 2, 32, 80, 17, 50), (12, 6, 128, 4096, 3900, 100),
-                                              (8, 8, 64, 70, 0, 1)])
+                                              (8, 8, 64, 70, 0, 1), (8, 2, 64, 300, 130, 70)])
 def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
     rng = np.random.default_rng(H * S + pos0 + n)
     kvd = H // kvm * hd
