@@ -137,7 +137,8 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
 /* C[M x N] = A[M x K] . W[N x K]^T (+ bias[N]) (+ C when accumulate != 0): the
  * MatmulKernel product (KI:9-10) for M input rows at once, on the matrix cores
  * (v_mfma_f32_32x32x2f32, 64 x 64 workgroup tiles).  lda, ldw, ldc are row strides in floats.  Needs
- * K, lda, ldw multiples of 4 and A, W 16-byte aligned (else KL_EUNSUPP). */
+ * K, lda, ldw multiples of 4, A, W 16-byte aligned and M x lda, N x ldw under 4 GiB
+ * (else KL_EUNSUPP). */
 int kl_gemm_f32(const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
                 int ldc, const float* bias, int accumulate, void* stream);
 

@@ -104,46 +104,64 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
   const int kb0 = static_cast<int>(blockIdx.y) * nkt / g.splits;
   const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
 
-  // The next block's loads land in ra/rw while the current block's MFMAs run;
-  // out-of-range elements are zeroed when the registers are written to LDS
-  // (after the MFMAs), so no wait is forced at load time.
+  // The next block's loads land in ra/rw while the current block's MFMAs run.
+  // The steady state spends almost no vector instructions on addressing: each
+  // load is a per-thread 32-bit byte offset (fixed for the whole K loop) from a
+  // uniform base that advances by one block, and each LDS store address is
+  // fixed.  Rows past M or N are clamped to the last row instead of masked:
+  // they only feed outputs that are never stored.  Only a partial last block
+  // (K not a multiple of BK) zeroes columns past K, in both operands.
+  static_assert(A4 % NT == 0 && W4 % NT == 0, "whole float4 loads per thread");
   gf4 ra[LA], rw[LW];
-  unsigned int oka = 0, okw = 0;
+  unsigned int offa[LA], offw[LW], colok_a[LA], colok_w[LW];
+  unsigned int lofa[LA], lofw[LW];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int idx = tid + i * NT;
+    const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
+    const int m = min(m0 + r, M - 1);
+    offa[i] = static_cast<unsigned int>((m * lda + c) * 4);
+    colok_a[i] = static_cast<unsigned int>(c);
+    lofa[i] = static_cast<unsigned int>(r * LDK + c);
+  }
+#pragma unroll
+  for (int i = 0; i < LW; ++i) {
+    const int idx = tid + i * NT;
+    const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
+    const int n = min(n0 + r, N - 1);
+    offw[i] = static_cast<unsigned int>((n * ldw + c) * 4);
+    colok_w[i] = static_cast<unsigned int>(c);
+    lofw[i] = static_cast<unsigned int>(r * LDK + c);
+  }
   auto gload = [&](int k0) {
-    oka = okw = 0;
+    const char* ba = reinterpret_cast<const char*>(A) + static_cast<size_t>(k0) * 4;
+    const char* bw = reinterpret_cast<const char*>(W) + static_cast<size_t>(k0) * 4;
+    if (k0 + BK <= K) {
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int idx = tid + i * NT;
-      const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
-      const int m = m0 + r, k = k0 + c;
-      const bool ok = (A4 % NT == 0 || idx < A4) && m < M && k < K;
-      oka |= ok ? 1u << i : 0u;
-      ra[i] = *reinterpret_cast<const gf4*>(A + static_cast<size_t>(ok ? m : 0) * lda + (ok ? k : 0));
-    }
+      for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const gf4*>(ba + offa[i]);
 #pragma unroll
-    for (int i = 0; i < LW; ++i) {
-      const int idx = tid + i * NT;
-      const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
-      const int n = n0 + r, k = k0 + c;
-      const bool ok = (W4 % NT == 0 || idx < W4) && n < N && k < K;
-      okw |= ok ? 1u << i : 0u;
-      rw[i] = *reinterpret_cast<const gf4*>(W + static_cast<size_t>(ok ? n : 0) * ldw + (ok ? k : 0));
+      for (int i = 0; i < LW; ++i) rw[i] = *reinterpret_cast<const gf4*>(bw + offw[i]);
+    } else {  // partial last block: columns past K read column k0 and are zeroed
+      const gf4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < LA; ++i) {
+        const bool ok = k0 + static_cast<int>(colok_a[i]) < K;
+        ra[i] = *reinterpret_cast<const gf4*>(ba + offa[i] - (ok ? 0u : colok_a[i] * 4));
+        if (!ok) ra[i] = z;
+      }
+#pragma unroll
+      for (int i = 0; i < LW; ++i) {
+        const bool ok = k0 + static_cast<int>(colok_w[i]) < K;
+        rw[i] = *reinterpret_cast<const gf4*>(bw + offw[i] - (ok ? 0u : colok_w[i] * 4));
+        if (!ok) rw[i] = z;
+      }
     }
   };
   auto sstore = [&](int buf) {
-    const gf4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int idx = tid + i * NT;
-      if (A4 % NT == 0 || idx < A4)
-        *reinterpret_cast<gf4*>(&As[buf][(idx / (BK / 4)) * LDK + (idx % (BK / 4)) * 4]) = ((oka >> i) & 1u) ? ra[i] : z;
-    }
+    for (int i = 0; i < LA; ++i) *reinterpret_cast<gf4*>(&As[buf][lofa[i]]) = ra[i];
 #pragma unroll
-    for (int i = 0; i < LW; ++i) {
-      const int idx = tid + i * NT;
-      if (W4 % NT == 0 || idx < W4)
-        *reinterpret_cast<gf4*>(&Ws[buf][(idx / (BK / 4)) * LDK + (idx % (BK / 4)) * 4]) = ((okw >> i) & 1u) ? rw[i] : z;
-    }
+    for (int i = 0; i < LW; ++i) *reinterpret_cast<gf4*>(&Ws[buf][lofw[i]]) = rw[i];
   };
 
   gf16 acc[TM][TN];

@@ -547,6 +547,8 @@ bool gemm_shape_ok(const float* A, int M, int K, int lda) {
 int gemm_launch(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs, int accumulate,
                 float* ws, int splits, hipStream_t st) {
   if (K % 4 || lda % 4 || !aligned16(A)) return KL_EUNSUPP;
+  // The kernel addresses each operand with 32-bit byte offsets.
+  if (static_cast<size_t>(M) * lda * sizeof(float) > 0xFFFFFFFFu) return KL_EUNSUPP;
   GemmArgs g{};
   g.A = A;
   g.M = M;
@@ -562,6 +564,7 @@ int gemm_launch(const float* A, int M, int K, int lda, int nseg, const GemmSeg* 
     const GemmSeg& sg = segs[i];
     if (!sg.W || !sg.C || sg.N <= 0 || sg.ldw < K || sg.ldc < sg.N) return KL_EINVAL;
     if (sg.ldw % 4 || !aligned16(sg.W)) return KL_EUNSUPP;
+    if (static_cast<size_t>(sg.N) * sg.ldw * sizeof(float) > 0xFFFFFFFFu) return KL_EUNSUPP;
     g.seg[i] = sg;
     g.seg[i].tile0 = static_cast<int>(tiles);
     tiles += static_cast<long long>(g.tiles_m) * ((sg.N + kGemmTile - 1) / kGemmTile);

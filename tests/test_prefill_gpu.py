@@ -58,7 +58,7 @@ def test_gemm_kat_exact(K, O, gpu):
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 3, 4), (5, 37, 12), (64, 64, 64), (77, 300, 256),
                                     (512, 1024, 2560), (130, 2560, 4096), (512, 9728, 512),
-                                    (1000, 256, 1536)])
+                                    (1000, 256, 1536), (33, 70, 100), (65, 129, 36)])
 def test_gemm_vs_oracle_rows(K, O, gpu, M, N, Kd):
     rng = np.random.default_rng(M * 7 + N + Kd)
     A = rng.standard_normal((M, Kd)).astype(np.float32)
