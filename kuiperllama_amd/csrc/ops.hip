@@ -147,6 +147,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ 
   for (int i = threadIdx.x; i < n; i += 256) yr[i] = (r * xr[i]) * w[i];
 }
 
+// Rows of at most 1024 floats (n % 4 == 0, 16-byte aligned rows): one wave
+// per row, float4 accesses, the sum of squares by lane exchanges only (no LDS,
+// no barrier).  The per-head q/k norms of a prefill are 10^4+ such rows.
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_w(const float* __restrict__ x,
+                                                       const float* __restrict__ w, float* y,
+                                                       int rows, int n, float eps) {
+  const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // whole waves
+  const f4* xr = reinterpret_cast<const f4*>(x + static_cast<size_t>(row) * n);
+  f4* yr = reinterpret_cast<f4*>(y + static_cast<size_t>(row) * n);
+  const f4* w4 = reinterpret_cast<const f4*>(w);
+  const int n4 = n / 4;
+  f4 v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = lane + j * kWave;
+    v[j] = i < n4 ? xr[i] : f4{0.f, 0.f, 0.f, 0.f};
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = lane + j * kWave;
+    if (i < n4) yr[i] = (r * v[j]) * w4[i];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // RoPE: one thread per rotated pair of q (and of k where the index < kv_dim).
 // ---------------------------------------------------------------------------
@@ -436,8 +466,14 @@ int kl_rmsnorm(const float* x, const float* w, float* y, int n, float eps, void*
 int kl_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n, float eps,
                     void* stream) {
   if (!x || !w || !y || rows <= 0 || n <= 0) return KL_EINVAL;
-  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(256), 0, as_stream(stream), x, w, y, rows, n,
-                     eps);
+  if (n <= 4 * kWave * 4 && n % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y)) {
+    const int blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
+    hipLaunchKernelGGL(k_rmsnorm_rows_w, dim3(blocks), dim3(256), 0, as_stream(stream), x, w, y,
+                       rows, n, eps);
+  } else {
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(256), 0, as_stream(stream), x, w, y, rows,
+                       n, eps);
+  }
   return launch_rc();
 }
 
