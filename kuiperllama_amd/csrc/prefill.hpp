@@ -227,18 +227,33 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
   const int rows = n - p0 < QB ? n - p0 : QB;
   const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
   const int qbase = pos0 + p0 + 32 * wm + 4 * hl;
-  for (int j0 = 0; j0 <= last; j0 += KB) {
-    __syncthreads();  // the previous block's K, V and P are consumed
-    for (int i = tid; i < KB * HD / 4; i += 256) {
+  // K and V of the next key block are loaded into registers while the current
+  // block is multiplied.
+  constexpr int NL = KB * HD / 4 / 256;  // float4s of K (and of V) per thread
+  pf4 kpre[NL], vpre[NL];
+  auto kvload = [&](int j0) {
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = tid + 256 * t;
       const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
       const int j = j0 + r;
       const size_t off = static_cast<size_t>(j <= last ? j : 0) * kv_dim + g * HD + c;
-      pf4 kv = *reinterpret_cast<const pf4*>(kc + off);
-      pf4 vv = *reinterpret_cast<const pf4*>(vc + off);
-      if (j > last) kv = vv = pf4{0.f, 0.f, 0.f, 0.f};
-      *reinterpret_cast<pf4*>(Ks + r * LDK + c) = kv;
-      *reinterpret_cast<pf4*>(Vs + r * LDK + c) = vv;
+      kpre[t] = *reinterpret_cast<const pf4*>(kc + off);
+      vpre[t] = *reinterpret_cast<const pf4*>(vc + off);
     }
+  };
+  kvload(0);
+  for (int j0 = 0; j0 <= last; j0 += KB) {
+    __syncthreads();  // the previous block's K, V and P are consumed
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = tid + 256 * t;
+      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+      const bool live = j0 + r <= last;
+      *reinterpret_cast<pf4*>(Ks + r * LDK + c) = live ? kpre[t] : pf4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<pf4*>(Vs + r * LDK + c) = live ? vpre[t] : pf4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (j0 + KB <= last) kvload(j0 + KB);
     __syncthreads();
     // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
     f16v sacc = f16v{};
