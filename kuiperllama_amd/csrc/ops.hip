@@ -177,6 +177,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_w(const float* __restrict_
   }
 }
 
+// Rows of up to 8192 floats (n % 4 == 0, 16-byte aligned): one block per
+// row, each thread's float4s kept in registers between the sum of squares and
+// the scaling, so the row is read once.
+template <int R>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_b(const float* __restrict__ x,
+                                                       const float* __restrict__ w, float* y,
+                                                       int rows, int n, float eps) {
+  __shared__ float red[kWavesPerBlock];
+  const int row = blockIdx.x;
+  const f4* xr = reinterpret_cast<const f4*>(x + static_cast<size_t>(row) * n);
+  f4* yr = reinterpret_cast<f4*>(y + static_cast<size_t>(row) * n);
+  const f4* w4 = reinterpret_cast<const f4*>(w);
+  const int n4 = n / 4;
+  f4 v[R];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int i = threadIdx.x + j * 256;
+    v[j] = i < n4 ? xr[i] : f4{0.f, 0.f, 0.f, 0.f};
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  ss = block_sum(ss, red);
+  const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int i = threadIdx.x + j * 256;
+    if (i < n4) yr[i] = (r * v[j]) * w4[i];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // RoPE: one thread per rotated pair of q (and of k where the index < kv_dim).
 // ---------------------------------------------------------------------------
@@ -470,6 +500,14 @@ int kl_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n, f
     const int blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
     hipLaunchKernelGGL(k_rmsnorm_rows_w, dim3(blocks), dim3(256), 0, as_stream(stream), x, w, y,
                        rows, n, eps);
+  } else if (n <= 8 * 256 * 4 && n % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y)) {
+    const int r4 = (n / 4 + 255) / 256;  // float4s per thread
+    auto launch = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(rows), dim3(256), 0, as_stream(stream), x, w, y, rows, n, eps);
+    };
+    if (r4 <= 2) launch(k_rmsnorm_rows_b<2>);
+    else if (r4 <= 4) launch(k_rmsnorm_rows_b<4>);
+    else launch(k_rmsnorm_rows_b<8>);
   } else {
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(256), 0, as_stream(stream), x, w, y, rows,
                        n, eps);
