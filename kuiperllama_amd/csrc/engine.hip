@@ -869,6 +869,7 @@ int setup_persistent(kl_engine* e) {
   a.sin_t = e->sin_t; a.cos_t = e->cos_t; a.emb = e->emb;
   a.q = e->t_q; a.knew = e->t_k; a.vnew = e->t_v; a.att = e->t_att;
   a.attn_part = e->t_part;
+  a.attn_part_n = static_cast<long long>(e->attn.part_floats);
   a.attn_G = e->attn.G;
   // Attention merge beyond kAttnMergeChunks chunks per kv head: one merging
   // workgroup per 2 chunks (measured best of 1, 2, 4, 8 on Qwen2.5-1.5B at
@@ -1205,6 +1206,11 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void**>(&e->derr_host), sizeof(int), hipHostMallocDefault);
   if (err == hipSuccess) err = hipEventCreate(&e->ev0);
   if (err == hipSuccess) err = hipEventCreate(&e->ev1);
+  if (const char* env = std::getenv("KL_EPOCH_START")) {
+    // Test hook: start the tag epoch just before its wrap.
+    const unsigned int ep = static_cast<unsigned int>(std::strtoul(env, nullptr, 10)) % kEpochWrap;
+    if (err == hipSuccess) err = hipMemcpy(e->epoch, &ep, sizeof(ep), hipMemcpyHostToDevice);
+  }
   if (err != hipSuccess) {
     release(e);
     return rc(err);

@@ -61,6 +61,12 @@ constexpr int kPThreads = 512;
 constexpr int kPWaves = kPThreads / kWave;
 constexpr int kSpinLimit = 1 << 22;
 constexpr int kTagLayers = 128;  // tag = epoch * kTagLayers + layer + 1
+// The epoch wraps to 0 after kEpochWrap launches, so tags stay below 2^31.
+// Every tagged vector except the attention partials is rewritten by every
+// launch, so its old tags never equal a new one; partial slots past a step's
+// chunk count can sit untouched, so the wrapping launch zeroes them (tag 0 is
+// never a valid tag).
+constexpr unsigned int kEpochWrap = 1u << 24;
 
 // Error codes written to PArgs::err by the device.
 constexpr int kDevErrWait = 1;   // a wait for another workgroup exceeded kSpinLimit polls
@@ -127,6 +133,7 @@ struct PArgs {
   const tagged_t* vnew;
   tagged_t* att;           // attention output [Dq] (tagged)
   tagged_t* attn_part;     // split partials [KVH][G][kv_mul][HD + 2] (tagged)
+  long long attn_part_n;   // its elements
   int attn_G;              // chunk slots per kv head
   int merge_chunks;        // chunks per merging workgroup beyond kAttnMergeChunks chunks
   float* am_pv;            // [gridDim] argmax partials
@@ -1181,6 +1188,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   } else {
     next = g_rd(a.prompt + pos + 1);
   }
+  const bool wrap = epoch + 1 >= kEpochWrap;
+  if (wrap) {
+    for (long long i = threadIdx.x; i < a.attn_part_n; i += kPThreads) a.attn_part[i] = 0;
+  }
   if (threadIdx.x == 0) {
     if (next < 0 || next >= a.V) {
       g_st(a.err, kDevErrToken);
@@ -1194,7 +1205,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     ns.token = next;
     ns.pos = pos + 1;
     *a.st = ns;
-    *a.epoch = epoch + 1;
+    *a.epoch = wrap ? 0u : epoch + 1;
     g_st(a.am_cnt, 0u);
   }
 }

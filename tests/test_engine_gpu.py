@@ -130,6 +130,31 @@ def test_persistent_is_deterministic_and_close_to_multi(K, O, gpu):
     assert list(ga) == list(gb)
 
 
+def test_tag_epoch_wrap(K, O, gpu, monkeypatch):
+    """The hand-off tags wrap after 2^24 launches (the wrapping launch clears
+    the attention partials).  An engine whose epoch starts just before the
+    wrap decodes across it, after split attention has begun (positions >= 64),
+    bit for bit like one that starts at 0."""
+    cfg = K.TINY["tiny_llama3"]  # 96 positions, 64-position attention chunks
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    a = K.Engine(img, cfg)
+    # engine creation runs 4 calibration steps; the wrap then falls near position 70
+    monkeypatch.setenv("KL_EPOCH_START", str((1 << 24) - 4 - 70))
+    b = K.Engine(img, cfg)
+    monkeypatch.delenv("KL_EPOCH_START")
+    for e in (a, b):
+        e.set_mode(K.MODE_PERSISTENT)
+    seq = [int(t) for t in prompt]
+    for pos in range(cfg.seq_len - 1):
+        t = seq[pos] if pos < len(seq) else seq[-1]
+        na, la = a.step(t, pos)
+        nb, lb = b.step(t, pos)
+        assert na == nb and np.array_equal(la, lb), pos
+        if pos + 1 >= len(seq):
+            seq.append(int(na))
+
+
 def test_engine_rejects_bad_tokens(K, gpu):
     cfg = K.TINY["tiny_llama2"]
     eng = K.Engine(K.synth_image(cfg), cfg)
