@@ -974,8 +974,11 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     const int lo = static_cast<int>(static_cast<long long>(mi) * E / MW);
     const int cnt = static_cast<int>(static_cast<long long>(mi + 1) * E / MW) - lo;
     if (cnt <= 0) continue;
-    int T = kWave;  // lanes per output (uniform)
+    // Lanes per output (uniform): one while a lane's eight-chunk round trip covers
+    // every chunk, more at long contexts.
+    int T = kWave;
     while (T > 1 && T * cnt > kPThreads) T >>= 1;
+    if (nsplit <= 8) T = 1;
     const tagged_t* pg = a.attn_part + static_cast<size_t>(g) * a.attn_G * kvm * (HD + 2);
     tagged_t* outg = a.att + static_cast<size_t>(g) * kvm * HD;
     for (int base = tid; base < ((cnt * T + kWave - 1) / kWave) * kWave; base += kPThreads) {
@@ -1001,8 +1004,18 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         }
         poll_many<24>(a, tag, addr, valid, v);
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (k0 + k * T < nsplit) merge2(M, L, O, val_of(v[8 + k]), val_of(v[16 + k]), val_of(v[k]));
+        // A lane's first chunk has a finite max, so its own updates need no
+        // guard (e^(-inf) = 0 clears the empty start).
+        for (int k = 0; k < 8; ++k) {
+          if (k0 + k * T < nsplit) {
+            const float ms = val_of(v[8 + k]);
+            const float Mn = fmaxf(M, ms);
+            const float cm = expf(M - Mn), w = expf(ms - Mn);
+            L = L * cm + val_of(v[16 + k]) * w;
+            O = O * cm + val_of(v[k]) * w;
+            M = Mn;
+          }
+        }
       }
       // Combine the T lanes of this output (adjacent lanes, T divides 64).
       for (int w = 1; w < T; w <<= 1)
