@@ -136,6 +136,11 @@ struct PArgs {
   long long attn_part_n;   // its elements
   int attn_G;              // chunk slots per kv head
   int merge_chunks;        // chunks per merging workgroup beyond kAttnMergeChunks chunks
+  // Workgroups without an attention item pull weight rows of the next phases
+  // into L2 while the attention runs, after touch_delay 100 MHz ticks: their
+  // first wo_touch_rows / w13_touch_rows local rows of WO and W1/W3 (0: none,
+  // -1: one per row group of waves), and those of one attention workgroup.
+  int touch_delay, wo_touch_rows, w13_touch_rows;
   float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
   unsigned int* am_cnt;    // end-of-step arrival counter
@@ -410,6 +415,22 @@ struct PGeom {
   int rg, ksi;
 };
 
+// Rows [base, base + cnt) of a phase owned by workgroup b.
+__device__ __forceinline__ void p_share(PGp p, int b, int& base, int& cnt) {
+  if (p->split) {
+    // Measured split: rows in proportion to each workgroup's streaming speed.
+    const KL_CAS int* sp = (const KL_CAS int*)(p->split);
+    base = sp[b];
+    cnt = sp[b + 1] - base;
+  } else {
+    // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n).
+    const int total = p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2];
+    const long long bb = b, n = gridDim.x;
+    base = static_cast<int>(bb * total / n);
+    cnt = static_cast<int>((bb + 1) * total / n) - base;
+  }
+}
+
 __device__ __forceinline__ PGeom p_geom(PGp p) {
   PGeom g;
   // The wave index is uniform across the wave; readfirstlane lets the compiler
@@ -418,22 +439,53 @@ __device__ __forceinline__ PGeom p_geom(PGp p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   g.ksi = wave % p->ks;
   g.rg = wave / p->ks;
-  if (p->split) {
-    // Measured split: rows in proportion to each workgroup's streaming speed.
-    const KL_CAS int* sp = (const KL_CAS int*)(p->split);
-    g.base = sp[blockIdx.x];
-    g.cnt = sp[blockIdx.x + 1] - g.base;
-  } else {
-    // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n).
-    const int total = p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2];
-    const long long b = blockIdx.x, n = gridDim.x;
-    g.base = static_cast<int>(b * total / n);
-    g.cnt = static_cast<int>((b + 1) * total / n) - g.base;
-  }
+  p_share(p, blockIdx.x, g.base, g.cnt);
   g.nloc = p->paired ? g.cnt * p->nsub : g.cnt;
   const int nrows = g.nloc > g.rg ? (g.nloc - g.rg + p->rw - 1) / p->rw : 0;
   g.n_items = g.ksi < p->nseg ? nrows * p->nsegw : 0;
   return g;
+}
+
+// Reads one word of every 128-byte line of workgroup b's first `lim` local
+// rows (all rows: lim >= its share) of phase p, weights and int8 scales, so
+// that they sit in this XCD's L2 when the phase streams them.  Returns an XOR
+// of the words (kept live by the caller).
+template <bool Q8>
+__device__ __forceinline__ unsigned int p_touch(PGp p, int b, int lim) {
+  int base, cnt;
+  p_share(p, b, base, cnt);
+  unsigned int acc = 0;
+  const size_t es = Q8 ? 1 : 4;
+  int off = 0, done = 0;  // done: local rows before this sub-matrix's
+  for (int sub = 0; sub < p->nsub; ++sub) {
+    const int lo = p->paired ? base : max(base - off, 0);
+    int hi = p->paired ? base + cnt : min(base + cnt - off, p->rows[sub]);
+    off += p->rows[sub];
+    const int room = max(lim - done, 0);
+    if (hi - lo > room) hi = lo + room;
+    done += max(hi - lo, 0);
+    if (hi <= lo) continue;
+    const size_t e0 = static_cast<size_t>(lo) * p->cols;
+    const char* w = static_cast<const char*>(p->w[sub]) + e0 * es;
+    const int lines = static_cast<int>((static_cast<size_t>(hi - lo) * p->cols * es + 127) / 128);
+    for (int i0 = threadIdx.x; i0 < lines; i0 += 4 * kPThreads) {
+      unsigned int v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = i0 + k * kPThreads;
+        v[k] = g_rd(reinterpret_cast<const unsigned int*>(w + static_cast<size_t>(i < lines ? i : i0) * 128));
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc ^= v[k];
+    }
+    if constexpr (Q8) {
+      const char* sc = reinterpret_cast<const char*>(p->sc[sub] + (e0 >> p->gshift));
+      const int sl = static_cast<int>(((static_cast<size_t>(hi - lo) * p->cols >> p->gshift) * 4 + 127) / 128);
+      for (int i = threadIdx.x; i < sl; i += kPThreads)
+        acc ^= g_rd(reinterpret_cast<const unsigned int*>(sc + static_cast<size_t>(i) * 128));
+    }
+  }
+  return acc;
 }
 
 // Local row -> (sub-matrix, row).
@@ -1182,8 +1234,32 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     trace_mark(a, slot++);
     if (!pn) break;  // last layer of a prompt position: no classifier
     if ((k & 3) == 0) {  // after QKV: attention of layer k / 4
-      if (static_cast<int>(blockIdx.x) >= a.KVH * ((pos + attn_chunk(HD)) / attn_chunk(HD)))
+      const int items = a.KVH * ((pos + attn_chunk(HD)) / attn_chunk(HD));
+      const int b = static_cast<int>(blockIdx.x);
+      if (b >= items) {
         trace_mark(a, slot);  // no attention item: "inputs arrived" = now
+        // Idle until the attention output arrives: pull this workgroup's WO
+        // rows into L2, and those of the attention workgroup b - 8 ceil(items / 8)
+        // (the same XCD under round-robin dispatch), which has no time to.
+        if (a.wo_touch_rows != 0 || a.w13_touch_rows != 0) {
+          if (a.touch_delay > 0) {
+            const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+            while (__builtin_amdgcn_s_memrealtime() - t0 < static_cast<unsigned long long>(a.touch_delay))
+              __builtin_amdgcn_s_sleep(4);
+          }
+          const int ai = b - 8 * ((items + 7) / 8);
+          unsigned int t = 0;
+          for (int q = 0; q < 2; ++q) {
+            const PGp pt = pn + q;  // WO, then W1/W3
+            int rows = q == 0 ? a.wo_touch_rows : a.w13_touch_rows;
+            if (rows < 0) rows = pt->rw;
+            if (rows == 0) continue;
+            t ^= p_touch<Q8>(pt, b, rows);
+            if (ai >= 0) t ^= p_touch<Q8>(pt, ai, rows);
+          }
+          asm volatile("" ::"v"(t));  // keeps the loads
+        }
+      }
       attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds, slot, pre, rope_c, rope_s);
       ++slot;
       trace_mark(a, slot++);
