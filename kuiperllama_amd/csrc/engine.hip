@@ -877,19 +877,20 @@ int setup_persistent(kl_engine* e) {
   a.merge_chunks = 2;
   if (const char* env = std::getenv("KL_ATTN_MERGE_CHUNKS")) a.merge_chunks = std::max(1, std::atoi(env));
   // While the attention runs, workgroups without an attention item pull the
-  // first 64 KB of their W1/W3 rows (and of one attention workgroup's of the
-  // same XCD) into L2, 0.5 us after the attention starts, so that the W1/W3
-  // stream starts from L2 instead of waiting out the HBM latency.  Measured on
-  // Llama-3.2-1B at position 200 (tok/s against no touch): 64 KB +1.5-1.7%,
-  // 96 KB -0.1%, 128 KB -1.8% (the touch then outlasts the attention); the
-  // whole WO share instead +0.8%, both together -0.2%; delays 0 / 0.5 / 1 /
-  // 2 us: +0.6 / +1.7 / +1.5 / 0%.
+  // first 96 KB of their W1/W3 rows into L2 (those of the XCD's attention
+  // workgroups are shared out among them), 0.5 us after the attention starts,
+  // so that the W1/W3 stream starts from L2 instead of waiting out the HBM
+  // latency.  Measured on Llama-3.2-1B at position 200 (tok/s against no
+  // touch): 64 KB +2.0%, 80 KB +2.4%, 96 KB +2.5-2.8%, 112 KB +2.3%, 128 KB
+  // +2.6%; delays 0 / 0.25 / 0.5 / 1 us within 0.5% of each other.  Pulling
+  // the whole WO share instead gained 0.8%, and less together with W1/W3.
+  // Off when a workgroup's W1/W3 share is under 128 KB (Llama2-110M: 48 KB,
+  // -1%): its stream is too short for the start to matter.
   const int w13_cols_bytes = m.D * (e->quant ? 1 : 4);
-  a.wo_touch_rows = 0;
-  a.w13_touch_rows = std::max(1, 65536 / w13_cols_bytes);
+  const double w13_share = 2.0 * m.F * w13_cols_bytes / e->nwg;
+  a.w13_touch_rows = w13_share >= 131072.0 ? std::max(1, 98304 / w13_cols_bytes) : 0;
   a.touch_delay = 50;
-  if (const char* env = std::getenv("KL_WO_TOUCH_ROWS")) a.wo_touch_rows = std::atoi(env);
-  if (const char* env = std::getenv("KL_W13_TOUCH_ROWS")) a.w13_touch_rows = std::atoi(env);
+  if (const char* env = std::getenv("KL_W13_TOUCH_ROWS")) a.w13_touch_rows = std::max(0, std::atoi(env));
   if (const char* env = std::getenv("KL_TOUCH_DELAY")) a.touch_delay = std::max(0, std::atoi(env));
   a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
   a.epoch = e->epoch; a.err = e->derr;

@@ -136,11 +136,11 @@ struct PArgs {
   long long attn_part_n;   // its elements
   int attn_G;              // chunk slots per kv head
   int merge_chunks;        // chunks per merging workgroup beyond kAttnMergeChunks chunks
-  // Workgroups without an attention item pull weight rows of the next phases
-  // into L2 while the attention runs, after touch_delay 100 MHz ticks: their
-  // first wo_touch_rows / w13_touch_rows local rows of WO and W1/W3 (0: none,
-  // -1: one per row group of waves), and those of one attention workgroup.
-  int touch_delay, wo_touch_rows, w13_touch_rows;
+  // Workgroups without an attention item pull the first w13_touch_rows local
+  // rows of their W1/W3 share (0: none) into L2 while the attention runs,
+  // after touch_delay 100 MHz ticks, and a slice of the attention
+  // workgroups' rows.
+  int touch_delay, w13_touch_rows;
   float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
   unsigned int* am_cnt;    // end-of-step arrival counter
@@ -446,45 +446,63 @@ __device__ __forceinline__ PGeom p_geom(PGp p) {
   return g;
 }
 
-// Reads one word of every 128-byte line of workgroup b's first `lim` local
-// rows (all rows: lim >= its share) of phase p, weights and int8 scales, so
-// that they sit in this XCD's L2 when the phase streams them.  Returns an XOR
-// of the words (kept live by the caller).
+// A byte range of weight rows to pull into L2, in 128-byte lines.
+struct TouchSpan {
+  const char* ptr;
+  int lines;
+};
+
+// Local rows [r0, r1) of workgroup b's share of a paired phase (rows of its
+// first sub-matrix; r1 is clipped to the share): weights in w, int8 scales in
+// sc (empty for fp32).
 template <bool Q8>
-__device__ __forceinline__ unsigned int p_touch(PGp p, int b, int lim) {
+__device__ __forceinline__ void p_touch_rows(PGp p, int b, int r0, int r1, TouchSpan& w,
+                                             TouchSpan& sc) {
   int base, cnt;
   p_share(p, b, base, cnt);
-  unsigned int acc = 0;
-  const size_t es = Q8 ? 1 : 4;
-  int off = 0, done = 0;  // done: local rows before this sub-matrix's
-  for (int sub = 0; sub < p->nsub; ++sub) {
-    const int lo = p->paired ? base : max(base - off, 0);
-    int hi = p->paired ? base + cnt : min(base + cnt - off, p->rows[sub]);
-    off += p->rows[sub];
-    const int room = max(lim - done, 0);
-    if (hi - lo > room) hi = lo + room;
-    done += max(hi - lo, 0);
-    if (hi <= lo) continue;
-    const size_t e0 = static_cast<size_t>(lo) * p->cols;
-    const char* w = static_cast<const char*>(p->w[sub]) + e0 * es;
-    const int lines = static_cast<int>((static_cast<size_t>(hi - lo) * p->cols * es + 127) / 128);
-    for (int i0 = threadIdx.x; i0 < lines; i0 += 4 * kPThreads) {
-      unsigned int v[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = i0 + k * kPThreads;
-        v[k] = g_rd(reinterpret_cast<const unsigned int*>(w + static_cast<size_t>(i < lines ? i : i0) * 128));
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) acc ^= v[k];
-    }
-    if constexpr (Q8) {
-      const char* sc = reinterpret_cast<const char*>(p->sc[sub] + (e0 >> p->gshift));
-      const int sl = static_cast<int>(((static_cast<size_t>(hi - lo) * p->cols >> p->gshift) * 4 + 127) / 128);
-      for (int i = threadIdx.x; i < sl; i += kPThreads)
-        acc ^= g_rd(reinterpret_cast<const unsigned int*>(sc + static_cast<size_t>(i) * 128));
-    }
+  r1 = min(r1, cnt);
+  const size_t e0 = static_cast<size_t>(base + r0) * p->cols;
+  const size_t ne = r1 > r0 ? static_cast<size_t>(r1 - r0) * p->cols : 0;
+  w.ptr = static_cast<const char*>(p->w[0]) + e0 * (Q8 ? 1 : 4);
+  w.lines = static_cast<int>((ne * (Q8 ? 1 : 4) + 127) / 128);
+  sc.ptr = w.ptr;
+  sc.lines = 0;
+  if constexpr (Q8) {
+    sc.ptr = reinterpret_cast<const char*>(p->sc[0] + (e0 >> p->gshift));
+    sc.lines = static_cast<int>(((ne >> p->gshift) * 4 + 127) / 128);
   }
+}
+
+// Reads one word of every 128-byte line of the spans (up to 8 lines per
+// thread, all issued before any is waited for), so that the lines sit in this
+// XCD's L2 when their phase streams them.  Returns an XOR of the words, which
+// the caller keeps live.
+__device__ __forceinline__ unsigned int p_touch_lines(TouchSpan s0, TouchSpan s1, TouchSpan s2,
+                                                      TouchSpan s3, TouchSpan s4, TouchSpan s5) {
+  const int total = s0.lines + s1.lines + s2.lines + s3.lines + s4.lines + s5.lines;
+  if (total == 0) return 0;
+  auto at = [&](int f) {
+    if (f < s0.lines) return s0.ptr + static_cast<size_t>(f) * 128;
+    f -= s0.lines;
+    if (f < s1.lines) return s1.ptr + static_cast<size_t>(f) * 128;
+    f -= s1.lines;
+    if (f < s2.lines) return s2.ptr + static_cast<size_t>(f) * 128;
+    f -= s2.lines;
+    if (f < s3.lines) return s3.ptr + static_cast<size_t>(f) * 128;
+    f -= s3.lines;
+    if (f < s4.lines) return s4.ptr + static_cast<size_t>(f) * 128;
+    f -= s4.lines;
+    return s5.ptr + static_cast<size_t>(f) * 128;
+  };
+  unsigned int v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int f = static_cast<int>(threadIdx.x) + k * kPThreads;
+    v[k] = g_rd(reinterpret_cast<const unsigned int*>(at(f < total ? f : 0)));
+  }
+  unsigned int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc ^= v[k];
   return acc;
 }
 
@@ -1241,22 +1259,30 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
         // Idle until the attention output arrives: pull this workgroup's WO
         // rows into L2, and those of the attention workgroup b - 8 ceil(items / 8)
         // (the same XCD under round-robin dispatch), which has no time to.
-        if (a.wo_touch_rows != 0 || a.w13_touch_rows != 0) {
+        if (a.w13_touch_rows > 0) {
           if (a.touch_delay > 0) {
             const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
             while (__builtin_amdgcn_s_memrealtime() - t0 < static_cast<unsigned long long>(a.touch_delay))
               __builtin_amdgcn_s_sleep(4);
           }
-          const int ai = b - 8 * ((items + 7) / 8);
-          unsigned int t = 0;
-          for (int q = 0; q < 2; ++q) {
-            const PGp pt = pn + q;  // WO, then W1/W3
-            int rows = q == 0 ? a.wo_touch_rows : a.w13_touch_rows;
-            if (rows < 0) rows = pt->rw;
-            if (rows == 0) continue;
-            t ^= p_touch<Q8>(pt, b, rows);
-            if (ai >= 0) t ^= p_touch<Q8>(pt, ai, rows);
-          }
+          // The attention workgroups of this XCD (x, x + 8, ... below items,
+          // under round-robin dispatch) cannot pull their own rows: the other
+          // workgroups of the XCD share that work, an even slice each (at
+          // most two attention workgroups' rows per slice are pulled).
+          const PGp pw = pn + 1;  // W1/W3
+          const int rows = a.w13_touch_rows;
+          const int x = b & 7, nw = static_cast<int>(gridDim.x);
+          const int cx = items > x ? (items - x + 7) / 8 : 0;  // attention workgroups
+          const int h = (b - x) / 8 - cx, nh = (nw - x + 7) / 8 - cx;
+          const long long tot = static_cast<long long>(cx) * rows;
+          const int q0 = static_cast<int>(tot * h / nh), q1 = static_cast<int>(tot * (h + 1) / nh);
+          const int j0 = q0 / rows, j1 = j0 + 1;
+          TouchSpan s[6];
+          p_touch_rows<Q8>(pw, b, 0, rows, s[0], s[1]);
+          p_touch_rows<Q8>(pw, x + 8 * j0, q0 - j0 * rows, min(q1 - j0 * rows, rows), s[2], s[3]);
+          p_touch_rows<Q8>(pw, x + 8 * min(j1, max(cx - 1, 0)), 0,
+                           j1 < cx ? min(q1 - j1 * rows, rows) : 0, s[4], s[5]);
+          const unsigned int t = p_touch_lines(s[0], s[1], s[2], s[3], s[4], s[5]);
           asm volatile("" ::"v"(t));  // keeps the loads
         }
       }
