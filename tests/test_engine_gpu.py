@@ -155,6 +155,29 @@ def test_tag_epoch_wrap(K, O, gpu, monkeypatch):
             seq.append(int(na))
 
 
+def test_l2_pull_changes_no_bits(K, O, gpu, monkeypatch):
+    """Pulling W1/W3 rows into L2 during the attention phase only reads
+    weights: an engine with the pull off decodes bit for bit like one with it
+    on (cfg 2 shape, past the first 64-position chunk so some workgroups have
+    no attention item)."""
+    cfg = K.BASELINE["llama32_1b"]
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg, 70)
+    a = K.Engine(img, cfg)
+    monkeypatch.setenv("KL_W13_TOUCH_ROWS", "0")
+    b = K.Engine(img, cfg)
+    monkeypatch.delenv("KL_W13_TOUCH_ROWS")
+    for e in (a, b):
+        e.set_mode(K.MODE_PERSISTENT)
+    for pos, t in enumerate(list(prompt) + [3, 4, 5]):
+        na, la = a.step(int(t), pos)
+        nb, lb = b.step(int(t), pos)
+        assert na == nb and np.array_equal(la, lb), pos
+    ga, _ = a.generate(prompt, 8)
+    gb, _ = b.generate(prompt, 8)
+    assert list(ga) == list(gb)
+
+
 def test_engine_rejects_bad_tokens(K, gpu):
     cfg = K.TINY["tiny_llama2"]
     eng = K.Engine(K.synth_image(cfg), cfg)
