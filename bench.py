@@ -143,7 +143,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is described in DESIGN.md, not built)", file=sys.stderr)
+              "(multi-GPU sharding is designed but not built)", file=sys.stderr)
         return 2
 
     import kuiperllama_amd as K
