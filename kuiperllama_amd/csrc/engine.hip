@@ -877,7 +877,7 @@ int setup_persistent(kl_engine* e) {
   a.merge_chunks = 2;
   if (const char* env = std::getenv("KL_ATTN_MERGE_CHUNKS")) a.merge_chunks = std::max(1, std::atoi(env));
   // While the attention runs, workgroups without an attention item pull the
-  // first 96 KB of their W1/W3 rows into L2 (those of the XCD's attention
+  // first 96 KB (up to 1.5x with many attention items) of their W1/W3 rows into L2 (those of the XCD's attention
   // workgroups are shared out among them), 0.5 us after the attention starts,
   // so that the W1/W3 stream starts from L2 instead of waiting out the HBM
   // latency.  Measured on Llama-3.2-1B at position 200 (tok/s against no

@@ -1270,8 +1270,11 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
           // workgroups of the XCD share that work, an even slice each (at
           // most two attention workgroups' rows per slice are pulled).
           const PGp pw = pn + 1;  // W1/W3
-          const int rows = a.w13_touch_rows;
-          const int x = b & 7, nw = static_cast<int>(gridDim.x);
+          const int nw = static_cast<int>(gridDim.x);
+          // The attention phase, and so the window for the pull, lengthens with
+          // the number of attention items: pull up to 1.5x as much then.
+          const int rows = a.w13_touch_rows + a.w13_touch_rows * min(items, nw / 2) / nw;
+          const int x = b & 7;
           const int cx = items > x ? (items - x + 7) / 8 : 0;  // attention workgroups
           const int h = (b - x) / 8 - cx, nh = (nw - x + 7) / 8 - cx;
           const long long tot = static_cast<long long>(cx) * rows;
