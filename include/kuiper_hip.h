@@ -122,9 +122,11 @@ int kl_rope(int style, int dim, int kv_dim, int head_size, float* q, float* k, i
 /* MHAKernel (KI:22-28; cpu/mha_kernel.cpp:5-61, cuda/mha_kernel.cu:109-127):
  * per head h (kv head h / kv_mul): softmax_t((q_h . K_t) / sqrt(hd)) . V_t over
  * t in [0, pos], caches [layers][seq_len][kv_dim].  The reference's score
- * buffer [head_num x seq_len] becomes a split-K workspace of
- * kl_mha_workspace_size() bytes (zero it once before first use; the kernel
- * leaves its counters at zero). */
+ * buffer [head_num x seq_len] floats (llama3.cpp:485-487) serves as the
+ * split workspace: kl_mha_workspace_size() bytes, never more than
+ * head_num * seq_len * 4 (0 where one workgroup per kv head covers seq_len),
+ * needing no initialisation.  Two launches on the stream when the context
+ * spans several workgroups (partials, then their merge). */
 int kl_mha_workspace_size(int head_num, int kv_mul, int seq_len, int head_size, size_t* bytes);
 int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
            int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
@@ -195,11 +197,12 @@ int kl_argmax(const float* x, int n, int32_t* out_index, void* workspace, size_t
 /* ---------------------------------------------------------------------------
  * Synthetic model images in the reference's .bin formats (the byte layouts
  * written by tools/export_llama.py:79-131 (fp32 v0), :134-210 (int8 g64),
- * tools/export_qwen2.py:79-134 (bias after each of wq/wk/wv) and
- * tools/export_qwen3.py:55-102 (8-int header)).  Matrices, embeddings and
- * biases are N(0, stddev) from a counter-based generator keyed by (seed,
- * tensor role, layer, element); norm weights are 1.0; the unused freq tables
- * of the v0/Qwen2 layouts are written as zeros.  Host-only, no GPU needed.
+ * tools/export_qwen2.py:79-134 (bias after each of wq/wk/wv), :137-210 (int8,
+ * the Llama int8 layout) and tools/export_qwen3.py:55-102 (8-int header)).
+ * Matrices, embeddings and biases are N(0, stddev) from a counter-based
+ * generator keyed by (seed, tensor role, layer, element); norm weights are 1.0,
+ * or 1 + N(0, norm_stddev) per norm role and layer; the unused freq tables of
+ * the v0/Qwen2 layouts are written as zeros.  Host-only, no GPU needed.
  * ------------------------------------------------------------------------- */
 typedef struct kl_model_spec {
   int32_t family;     /* KL_FAMILY_* */
@@ -212,7 +215,8 @@ typedef struct kl_model_spec {
   int32_t vocab;
   int32_t seq_len;
   int32_t tied;       /* classifier = embedding (not for int8 or Qwen3) */
-  int32_t group_size; /* 0: fp32 image; >0: int8 per-group image (Llama layout) */
+  int32_t group_size; /* 0: fp32 image; >0: int8 per-group image (Llama / Qwen2) */
+  float norm_stddev;  /* 0: every norm weight 1.0; >0: 1 + N(0, norm_stddev) */
 } kl_model_spec;
 
 int kl_synth_image_size(const kl_model_spec* spec, int64_t* bytes);

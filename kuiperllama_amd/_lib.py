@@ -43,6 +43,7 @@ class ModelSpec(C.Structure):
         ("seq_len", C.c_int32),
         ("tied", C.c_int32),
         ("group_size", C.c_int32),
+        ("norm_stddev", C.c_float),
     ]
 
 

@@ -30,6 +30,7 @@ class Config:
     group_size: int = 0  # >0: int8 weights, one fp32 scale per group
     prompt_len: int = 16
     decode_steps: int = 128
+    norm_std: float = 0.0  # 0: norm weights 1.0; >0: 1 + N(0, norm_std) per norm and layer
 
     @property
     def qd(self) -> int:
@@ -60,6 +61,7 @@ class Config:
             seq_len=self.seq_len,
             tied=int(self.tied),
             group_size=self.group_size,
+            norm_stddev=self.norm_std,
         )
 
     def with_(self, **kw) -> "Config":
@@ -126,15 +128,17 @@ BASELINE = {
 }
 
 TINY = {
-    "tiny_llama2": Config("tiny_llama2", L2, 128, 256, 2, 4, 4, 512, 64, False,
+    "tiny_llama2": Config("tiny_llama2", L2, 128, 256, 2, 4, 4, 512, 64, False, norm_std=0.1,
                           prompt_len=5, decode_steps=20),
-    "tiny_llama3": Config("tiny_llama3", L3, 256, 512, 2, 4, 2, 1000, 96, True,
+    "tiny_llama3": Config("tiny_llama3", L3, 256, 512, 2, 4, 2, 1000, 96, True, norm_std=0.1,
                           prompt_len=7, decode_steps=40),
-    "tiny_q8": Config("tiny_q8", L2, 256, 512, 2, 2, 2, 1024, 64, False, group_size=64,
+    "tiny_q8": Config("tiny_q8", L2, 256, 512, 2, 2, 2, 1024, 64, False, group_size=64, norm_std=0.1,
                       prompt_len=4, decode_steps=20),
-    "tiny_qwen2": Config("tiny_qwen2", Q2, 256, 384, 2, 2, 1, 777, 128, True,
+    "tiny_qwen2": Config("tiny_qwen2", Q2, 256, 384, 2, 2, 1, 777, 128, True, norm_std=0.1,
                          prompt_len=9, decode_steps=40),
-    "tiny_qwen3": Config("tiny_qwen3", Q3, 192, 320, 2, 4, 2, 640, 64, False, q_dim=256,
+    "tiny_qwen2_q8": Config("tiny_qwen2_q8", Q2, 256, 384, 2, 4, 2, 768, 64, False, group_size=64,
+                            norm_std=0.1, prompt_len=5, decode_steps=20),
+    "tiny_qwen3": Config("tiny_qwen3", Q3, 192, 320, 2, 4, 2, 640, 64, False, q_dim=256, norm_std=0.1,
                          prompt_len=6, decode_steps=20),
 }
 

@@ -271,7 +271,9 @@ struct ImageLayout {
 int parse_image(const void* image, size_t size, int family, int quant, ImageLayout* out) {
   if (!image || family < KL_FAMILY_LLAMA2 || family > KL_FAMILY_QWEN3) return KL_EINVAL;
   const bool qwen3 = family == KL_FAMILY_QWEN3;
-  if (quant && family != KL_FAMILY_LLAMA2 && family != KL_FAMILY_LLAMA3) return KL_EUNSUPP;
+  // int8 images: the Llama layout (llama3.cpp:183-287), also for Qwen2
+  // (qwen2.cpp:242-346, no biases); Qwen3 has none.
+  if (quant && qwen3) return KL_EUNSUPP;
   const size_t header_ints = (qwen3 || quant) ? 8 : 7;
   if (size < header_ints * 4) return KL_EFORMAT;
   const int32_t* h = static_cast<const int32_t*>(image);
@@ -552,6 +554,7 @@ int launch_step_t(kl_engine* e, Marks* mk) {
     aa.kv_dim = m.Dkv;
     aa.kv_mul = m.H / m.KVH;
     aa.G = e->attn.G;
+    aa.cpw = 1;
     aa.transform = e->transform;
     aa.rope_style = e->rope_style;
     aa.sin_t = e->sin_t;

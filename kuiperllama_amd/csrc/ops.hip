@@ -549,9 +549,10 @@ int kl_rope(int style, int dim, int kv_dim, int head_size, float* q, float* k, i
 
 int kl_mha_workspace_size(int head_num, int kv_mul, int seq_len, int head_size, size_t* bytes) {
   if (!bytes || seq_len <= 0 || !mha_shape_ok(head_num, kv_mul, head_size)) return KL_EINVAL;
-  const MhaPlan p = mha_plan(head_num / kv_mul, kv_mul, seq_len, head_size);
+  size_t need = 0;
+  const MhaPlan p = mha_plan_fit(head_num, kv_mul, seq_len, head_size, &need);
   if (p.G > 512) return KL_EUNSUPP;
-  *bytes = p.ws_bytes;
+  *bytes = need;
   return KL_OK;
 }
 
@@ -563,9 +564,10 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
   if (pos < 0 || pos >= seq_len || layer_index < 0) return KL_EINVAL;
   const int kv_heads = head_num / kv_mul;
   if (kv_dim != kv_heads * head_size) return KL_EINVAL;
-  const MhaPlan p = mha_plan(kv_heads, kv_mul, seq_len, head_size);
+  size_t need = 0;
+  const MhaPlan p = mha_plan_fit(head_num, kv_mul, seq_len, head_size, &need);
   if (p.G > 512) return KL_EUNSUPP;
-  if (workspace_bytes < p.ws_bytes) return KL_EWORKSPACE;
+  if (workspace_bytes < need) return KL_EWORKSPACE;
   AttnArgs a{};
   const size_t layer_off = static_cast<size_t>(layer_index) * seq_len * kv_dim;
   a.q = q;
@@ -573,21 +575,34 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
   a.vcache = value_cache + layer_off;
   a.out = out;
   a.part = static_cast<float*>(workspace);
-  a.counters = reinterpret_cast<unsigned int*>(static_cast<char*>(workspace) +
-                                               ((p.part_floats * sizeof(float) + 255) & ~size_t(255)));
+  a.counters = nullptr;  // the spans are merged by k_attn_merge: no counter to initialise
   a.pos_ptr = nullptr;
   a.pos_val = pos;
   a.kv_dim = kv_dim;
   a.kv_mul = kv_mul;
   a.G = p.G;
+  a.cpw = p.cpw;
   a.transform = 0;
   a.scale = 1.f / std::sqrt(static_cast<float>(head_size));
+  const int span = attn_chunk(head_size) * p.cpw;
+  const int nsplit = (pos + span) / span;
   const dim3 grid(kv_heads * p.G), block(256);
+  const size_t merge_lds = static_cast<size_t>(nsplit) * kv_mul * 2 * sizeof(float);
+  hipStream_t st = as_stream(stream);
   switch (head_size) {
-    case 32: hipLaunchKernelGGL(k_attn_decode<32>, grid, block, p.lds_bytes, as_stream(stream), a); break;
-    case 64: hipLaunchKernelGGL(k_attn_decode<64>, grid, block, p.lds_bytes, as_stream(stream), a); break;
-    case 128: hipLaunchKernelGGL(k_attn_decode<128>, grid, block, p.lds_bytes, as_stream(stream), a); break;
-    default: hipLaunchKernelGGL(k_attn_decode<256>, grid, block, p.lds_bytes, as_stream(stream), a); break;
+    case 32: hipLaunchKernelGGL(k_attn_decode<32>, grid, block, p.lds_bytes, st, a); break;
+    case 64: hipLaunchKernelGGL(k_attn_decode<64>, grid, block, p.lds_bytes, st, a); break;
+    case 128: hipLaunchKernelGGL(k_attn_decode<128>, grid, block, p.lds_bytes, st, a); break;
+    default: hipLaunchKernelGGL(k_attn_decode<256>, grid, block, p.lds_bytes, st, a); break;
+  }
+  if (nsplit > 1) {
+    const dim3 mg(kv_heads);
+    switch (head_size) {
+      case 32: hipLaunchKernelGGL(k_attn_merge<32>, mg, block, merge_lds, st, a); break;
+      case 64: hipLaunchKernelGGL(k_attn_merge<64>, mg, block, merge_lds, st, a); break;
+      case 128: hipLaunchKernelGGL(k_attn_merge<128>, mg, block, merge_lds, st, a); break;
+      default: hipLaunchKernelGGL(k_attn_merge<256>, mg, block, merge_lds, st, a); break;
+    }
   }
   return launch_rc();
 }

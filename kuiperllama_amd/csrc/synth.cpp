@@ -16,11 +16,15 @@
 //    {q_dim, dim, layers, heads, kv_heads, vocab, seq_len, ffn}, norms
 //    (attention [L], ffn [L], final), embedding, wq, q_norm, wk, k_norm, wv,
 //    wo, w1 (gate), w2 (down), w3 (up), lm_head.
+//  * int8 Qwen2     -- tools/export_qwen2.py:137-210: the int8 Llama layout
+//    (no biases: the int8 loader model/qwen2.cpp:242-346 reads none).
 //
-// Values: N(0, stddev) for matrices, embeddings and biases; 1.0 for every norm
-// weight; zeros for the freq tables (the loaders skip them).  The normal
-// stream of a tensor depends only on (seed, role, layer, element index), so a
-// model's fp32 and int8 images hold the same underlying weights.
+// Values: N(0, stddev) for matrices, embeddings and biases; norm weights
+// (attention, ffn, final, Qwen3 q/k) 1.0, or 1 + N(0, norm_stddev) when the
+// spec asks for it, one stream per norm role and layer; zeros for the freq
+// tables (the loaders skip them).  The normal stream of a tensor depends only
+// on (seed, role, layer, element index), so a model's fp32 and int8 images
+// hold the same underlying weights.
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -59,7 +63,8 @@ void parallel_for(int64_t n, int n_threads, Fn fn) {
 
 enum Role : int32_t {
   kEmb = 1, kWq = 2, kWk = 3, kWv = 4, kWo = 5, kW1 = 6, kW2 = 7, kW3 = 8, kCls = 9,
-  kBq = 10, kBk = 11, kBv = 12
+  kBq = 10, kBk = 11, kBv = 12,
+  kRmsAtt = 13, kRmsFfn = 14, kRmsFinal = 15, kQNorm = 16, kKNorm = 17
 };
 
 inline uint64_t mix64(uint64_t z) {
@@ -112,6 +117,7 @@ void quantize_groups(const float* w, int64_t n, int gs, int8_t* q, float* scales
 struct Dims {
   int64_t D, Dq, Dkv, F, L, H, KVH, V, S, hd, gs;
   bool tied, qwen3, qwen2, q8;
+  float norm_std;
 };
 
 int derive(const kl_model_spec* s, Dims* d) {
@@ -125,7 +131,9 @@ int derive(const kl_model_spec* s, Dims* d) {
   d->qwen2 = s->family == KL_FAMILY_QWEN2;
   d->q8 = s->group_size > 0;
   if (!d->qwen3 && s->q_dim != s->dim) return KL_EINVAL;
-  if (d->q8 && (d->qwen3 || d->qwen2 || s->tied)) return KL_EUNSUPP;
+  if (d->q8 && (d->qwen3 || s->tied)) return KL_EUNSUPP;
+  if (!(s->norm_stddev >= 0.f)) return KL_EINVAL;
+  d->norm_std = s->norm_stddev;
   d->D = s->dim;
   d->Dq = s->q_dim;
   d->H = s->heads;
@@ -181,6 +189,18 @@ class Writer {
   void normal(int32_t role, int32_t layer, int64_t n) {
     float* p = reinterpret_cast<float*>(reserve(n * 4));
     if (p) normal_stream(seed_, role, layer, stddev_, p, n, threads_);
+  }
+  // A norm weight vector: 1.0, or 1 + N(0, norm_std) from the (role, layer)
+  // stream.
+  void norm(int32_t role, int32_t layer, int64_t n, float norm_std) {
+    float* p = reinterpret_cast<float*>(reserve(n * 4));
+    if (!p) return;
+    if (norm_std == 0.f) {
+      for (int64_t i = 0; i < n; ++i) p[i] = 1.f;
+      return;
+    }
+    normal_stream(seed_, role, layer, norm_std, p, n, threads_);
+    for (int64_t i = 0; i < n; ++i) p[i] += 1.f;
   }
   void fill(float v, int64_t n) {
     float* p = reinterpret_cast<float*>(reserve(n * 4));
@@ -258,12 +278,14 @@ int kl_synth_image(const kl_model_spec* spec, uint64_t seed, float stddev, void*
     const int32_t h[8] = {int32_t(d.Dq), int32_t(d.D), L, int32_t(d.H), int32_t(d.KVH),
                           int32_t(d.V), int32_t(d.S), int32_t(d.F)};
     w.header(h, 8);
-    w.fill(1.f, (2 * d.L + 1) * d.D);
+    for (int32_t l = 0; l < L; ++l) w.norm(kRmsAtt, l, d.D, d.norm_std);
+    for (int32_t l = 0; l < L; ++l) w.norm(kRmsFfn, l, d.D, d.norm_std);
+    w.norm(kRmsFinal, 0, d.D, d.norm_std);
     w.normal(kEmb, 0, d.V * d.D);
     for (int32_t l = 0; l < L; ++l) w.normal(kWq, l, d.Dq * d.D);
-    w.fill(1.f, d.L * d.hd);
+    for (int32_t l = 0; l < L; ++l) w.norm(kQNorm, l, d.hd, d.norm_std);
     for (int32_t l = 0; l < L; ++l) w.normal(kWk, l, d.Dkv * d.D);
-    w.fill(1.f, d.L * d.hd);
+    for (int32_t l = 0; l < L; ++l) w.norm(kKNorm, l, d.hd, d.norm_std);
     for (int32_t l = 0; l < L; ++l) w.normal(kWv, l, d.Dkv * d.D);
     for (int32_t l = 0; l < L; ++l) w.normal(kWo, l, d.D * d.Dq);
     for (int32_t l = 0; l < L; ++l) w.normal(kW1, l, d.F * d.D);
@@ -284,14 +306,16 @@ int kl_synth_image(const kl_model_spec* spec, uint64_t seed, float stddev, void*
     for (int32_t l = 0; l < L; ++l) w.quantized(kW3, l, d.F * d.D, gs);
     w.quantized(kCls, 0, d.V * d.D, gs);
     w.normal(kEmb, 0, d.V * d.D);
-    w.fill(1.f, (2 * d.L + 1) * d.D);
+    for (int32_t l = 0; l < L; ++l) w.norm(kRmsAtt, l, d.D, d.norm_std);
+    for (int32_t l = 0; l < L; ++l) w.norm(kRmsFfn, l, d.D, d.norm_std);
+    w.norm(kRmsFinal, 0, d.D, d.norm_std);
   } else {
     const int32_t vocab = d.tied ? int32_t(d.V) : -int32_t(d.V);
     const int32_t h[7] = {int32_t(d.D), int32_t(d.F), L, int32_t(d.H), int32_t(d.KVH), vocab,
                           int32_t(d.S)};
     w.header(h, 7);
     w.normal(kEmb, 0, d.V * d.D);
-    w.fill(1.f, d.L * d.D);
+    for (int32_t l = 0; l < L; ++l) w.norm(kRmsAtt, l, d.D, d.norm_std);
     for (int32_t l = 0; l < L; ++l) {
       w.normal(kWq, l, d.Dq * d.D);
       if (d.qwen2) w.normal(kBq, l, d.Dq);
@@ -305,11 +329,11 @@ int kl_synth_image(const kl_model_spec* spec, uint64_t seed, float stddev, void*
       if (d.qwen2) w.normal(kBv, l, d.Dkv);
     }
     for (int32_t l = 0; l < L; ++l) w.normal(kWo, l, d.D * d.Dq);
-    w.fill(1.f, d.L * d.D);
+    for (int32_t l = 0; l < L; ++l) w.norm(kRmsFfn, l, d.D, d.norm_std);
     for (int32_t l = 0; l < L; ++l) w.normal(kW1, l, d.F * d.D);
     for (int32_t l = 0; l < L; ++l) w.normal(kW2, l, d.D * d.F);
     for (int32_t l = 0; l < L; ++l) w.normal(kW3, l, d.F * d.D);
-    w.fill(1.f, d.D);
+    w.norm(kRmsFinal, 0, d.D, d.norm_std);
     w.fill(0.f, d.S * d.hd);
     if (!d.tied) w.normal(kCls, 0, d.V * d.D);
   }

@@ -147,7 +147,9 @@ void swiglu_hip(const tensor::Tensor& in1, const tensor::Tensor& in2, const tens
            "kl_swiglu");
 }
 
-// kernels/cuda/mha_kernel.cu:109-127; the score tensor is the split-K workspace.
+// kernels/cuda/mha_kernel.cu:109-127; the score tensor ([head_num x seq_len]
+// floats, llama3.cpp:485-487) holds the split partials and needs no
+// initialisation.
 void mha_hip(int32_t pos, int32_t head_num, int32_t layer_index, int32_t seq_len, int32_t kv_dim,
              int32_t kv_mul, int32_t head_size, const tensor::Tensor& mha_out,
              const tensor::Tensor& query_tensor, const tensor::Tensor& score_tensor,

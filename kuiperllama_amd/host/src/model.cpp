@@ -75,8 +75,8 @@ base::Status Model::init(base::DeviceType device_type) {
   if (device_type != base::DeviceType::kDeviceHIP)
     return base::error::InvalidArgument(
         "This backend runs on kDeviceHIP only; the CPU and CUDA paths are the reference's.");
-  if (is_quant_model_ && family_ != ModelFamily::kLlama2 && family_ != ModelFamily::kLlama3)
-    return base::error::InvalidArgument("int8 images exist for the Llama layouts only.");
+  if (is_quant_model_ && family_ == ModelFamily::kQwen3)
+    return base::error::InvalidArgument("Qwen3 images have no int8 layout.");
   device_type_ = device_type;
   // The file is parsed and sized before any device work, so a bad path or
   // image is reported without touching the GPU.
@@ -256,8 +256,9 @@ void Model::create_param_layers() {
   ly.rmsnorm_layers_.push_back(final_norm);
 }
 
-// llama3.cpp:183-287: int8 matrices, each followed by its fp32 group scales,
-// then the fp32 embedding and norm weights.
+// llama3.cpp:183-287 (and qwen2.cpp:242-346, the same walk without biases):
+// int8 matrices, each followed by its fp32 group scales, then the fp32
+// embedding and norm weights.
 void Model::create_param_quant_layers() {
   const auto& c = *config_;
   const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
@@ -375,8 +376,8 @@ const tensor::Tensor& Model::get_buffer(ModelBufferType buffer_idx) const {
 
 // llama3.cpp:424-497 (Qwen3: qwen3.cpp:301-380): moves the layers to the
 // device and lays out the step's buffers with the reference's aliases.  The
-// score buffer is also the attention kernel's split-K workspace, so it holds
-// max(head_num x seq_len floats, the kernel's workspace) and starts zeroed.
+// score buffer is the reference's [head_num x seq_len] floats, uninitialised
+// (llama3.cpp:485-487); the attention kernel keeps its split partials in it.
 void Model::init_mem() {
   const auto& c = *config_;
   auto alloc = base::HIPDeviceAllocatorFactory::get_instance();
@@ -427,10 +428,8 @@ void Model::init_mem() {
   STATUS_CHECK(insert_buffer(ModelBufferType::kInputPos, pos_tensor));
 
   const size_t ws = kernel::mha_workspace_bytes(c.head_num_, c.kv_mul_, c.seq_len_, c.head_size_);
-  int32_t score_cols = c.seq_len_;
-  while (static_cast<size_t>(c.head_num_) * score_cols * sizeof(float) < ws) ++score_cols;
-  T attn(DT::kDataTypeFp32, c.head_num_, score_cols, true, alloc);
-  alloc->memset_zero(attn.ptr<void>(), attn.byte_size(), stream);
+  T attn(DT::kDataTypeFp32, c.head_num_, c.seq_len_, true, alloc);
+  KUIPER_CHECK(attn.byte_size() >= ws, "attention partials exceed the score buffer");
   STATUS_CHECK(insert_buffer(ModelBufferType::kScoreStorage, attn));
   if (qwen3) {
     T attn_output(DT::kDataTypeFp32, c.dim_, true, alloc);

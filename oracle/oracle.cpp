@@ -303,7 +303,8 @@ void gemv_any(const or_model* m, const void* W, const float* s, const float* x, 
 extern "C" {
 
 // Parsing follows model/model.cpp:41-141 (header, derived dims, tied iff
-// vocab > 0) and the offset walks of model/llama3.cpp:183-422 (fp32 and int8),
+// vocab > 0) and the offset walks of model/llama3.cpp:183-422 (fp32 and int8;
+// the int8 Qwen2 walk, model/qwen2.cpp:242-346, is the same and has no bias),
 // model/qwen2.cpp:348-485 (bias after each of wq/wk/wv) and
 // model/qwen3.cpp:186-299 (8-int header, norms first, q/k norms, lm_head).
 or_model* or_model_open(const void* image, size_t size, int family, int quant, char* err,
@@ -317,7 +318,6 @@ or_model* or_model_open(const void* image, size_t size, int family, int quant, c
   if (size < header_ints * 4) return fail("truncated header");
   const int32_t* h = static_cast<const int32_t*>(image);
   if (qwen3 && quant) return fail("qwen3 has no int8 layout");
-  if (family == OR_QWEN2 && quant) return fail("qwen2 int8 layout is not supported");
   or_model* m = new or_model();
   m->family = family;
   m->quant = quant;

@@ -183,6 +183,7 @@ kl_model_spec tiny_spec(int family) {
   s.vocab = 100;
   s.seq_len = 32;
   s.tied = 0;
+  s.norm_stddev = 0.1f;
   return s;
 }
 
@@ -203,10 +204,10 @@ void cpu_model_errors() {
     std::remove(p.c_str());
   }
   {
-    kl_model_spec q = tiny_spec(KL_FAMILY_QWEN2);
-    const std::string p = write_image(q, "/tmp/kuiper_host_q2.bin", 0);
-    model::Qwen2Model m(base::TokenizerType::kEncodeBpe, "", p, true);
-    EXPECT(m.init(DeviceType::kDeviceHIP) == base::kInvalidArgument);  // int8 Qwen2 is undefined
+    kl_model_spec q = tiny_spec(KL_FAMILY_QWEN3);
+    const std::string p = write_image(q, "/tmp/kuiper_host_q3.bin", 0);
+    model::Qwen3Model m(base::TokenizerType::kEncodeBpe, "", p, true);
+    EXPECT(m.init(DeviceType::kDeviceHIP) == base::kInvalidArgument);  // Qwen3 has no int8 layout
     std::remove(p.c_str());
   }
 }

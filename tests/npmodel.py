@@ -8,7 +8,11 @@ wrong family constant shows up as a logits mismatch.  Family constants cite
 the reference: RoPE pairing and theta (kernels/cpu/rope_kernel.cpp:3-122),
 eps (kernels/cpu/rmsnorm_kernel.cpp:24-28), q/k norm eps
 (kernels/cuda/rmsnorm_kernel.cu:148), Qwen2 bias (op/matmul.cpp:74-77),
-Qwen3 q/k norm order (model/qwen3.cpp:485-500).
+Qwen3 q/k norm order (model/qwen3.cpp:485-500).  Norm weights are read per
+role and layer: attention norm of layer l, ffn norm of layer l, the final
+norm (the reference's rmsnorm_layers_[l], [L + l], [2L], llama3.cpp:599-608,
+:687, :723) and Qwen3's q/k norms ([2L + 1 + l], [3L + 1 + l],
+qwen3.cpp:485-500).
 """
 from __future__ import annotations
 
@@ -16,6 +20,7 @@ import numpy as np
 
 # synth.cpp roles
 EMB, WQ, WK, WV, WO, W1, W2, W3, CLS, BQ, BK, BV = range(1, 13)
+RMS_ATT, RMS_FFN, RMS_FINAL, Q_NORM, K_NORM = range(13, 18)
 
 FAMILY = {
     0: dict(style="interleaved", theta=1e4, eps=1e-5, bias=False, qknorm=False),
@@ -42,22 +47,31 @@ class NpModel:
         def vec(role, layer, n):
             return K.synth_normal(seed, role, layer, n, stddev).astype(np.float64)
 
+        def norm(role, layer, n):
+            if not cfg.norm_std:
+                return np.ones(n)
+            return 1.0 + K.synth_normal(seed, role, layer, n, cfg.norm_std).astype(np.float64)
+
         self.E = K.synth_normal(seed, EMB, 0, V * D, stddev).astype(np.float64).reshape(V, D)
         self.layers = []
         for l in range(L):
             d = dict(wq=mat(WQ, l, Dq, D), wk=mat(WK, l, Dkv, D), wv=mat(WV, l, Dkv, D),
                      wo=mat(WO, l, D, Dq), w1=mat(W1, l, F, D), w2=mat(W2, l, D, F),
-                     w3=mat(W3, l, F, D))
-            if f["bias"]:
+                     w3=mat(W3, l, F, D), rms_att=norm(RMS_ATT, l, D), rms_ffn=norm(RMS_FFN, l, D))
+            if f["qknorm"]:
+                hd = cfg.head_size
+                d.update(q_norm=norm(Q_NORM, l, hd), k_norm=norm(K_NORM, l, hd))
+            if f["bias"] and not cfg.quant:
                 d.update(bq=vec(BQ, l, Dq), bk=vec(BK, l, Dkv), bv=vec(BV, l, Dkv))
             self.layers.append(d)
+        self.rms_final = norm(RMS_FINAL, 0, D)
         self.cls = self.E if (cfg.tied and cfg.family != 3) else mat(CLS, 0, V, D)
         self.kc = np.zeros((L, cfg.seq_len, Dkv))
         self.vc = np.zeros((L, cfg.seq_len, Dkv))
 
     @staticmethod
-    def _rms(x, eps):
-        return x / np.sqrt(np.mean(x * x) + eps)
+    def _rms(x, eps, w):
+        return w * (x / np.sqrt(np.mean(x * x) + eps))
 
     def _rope(self, v, pos, n_heads):
         hd = self.cfg.head_size
@@ -78,13 +92,13 @@ class NpModel:
         H, KVH, hd = cfg.heads, cfg.kv_heads, cfg.head_size
         x = self.E[token].copy()
         for l, w in enumerate(self.layers):
-            xb = self._rms(x, f["eps"])
+            xb = self._rms(x, f["eps"], w["rms_att"])
             q, k, v = w["wq"] @ xb, w["wk"] @ xb, w["wv"] @ xb
-            if f["bias"]:
+            if "bq" in w:
                 q, k, v = q + w["bq"], k + w["bk"], v + w["bv"]
             if f["qknorm"]:
-                q = np.concatenate([self._rms(h, 1e-6) for h in q.reshape(H, hd)])
-                k = np.concatenate([self._rms(h, 1e-6) for h in k.reshape(KVH, hd)])
+                q = np.concatenate([self._rms(h, 1e-6, w["q_norm"]) for h in q.reshape(H, hd)])
+                k = np.concatenate([self._rms(h, 1e-6, w["k_norm"]) for h in k.reshape(KVH, hd)])
             q, k = self._rope(q, pos, H), self._rope(k, pos, KVH)
             self.kc[l, pos], self.vc[l, pos] = k, v
             o = np.empty(H * hd)
@@ -97,7 +111,7 @@ class NpModel:
                 p /= p.sum()
                 o[h * hd : (h + 1) * hd] = p @ Vt
             x = x + w["wo"] @ o
-            xb = self._rms(x, f["eps"])
+            xb = self._rms(x, f["eps"], w["rms_ffn"])
             a, b = w["w1"] @ xb, w["w3"] @ xb
             x = x + w["w2"] @ (a / (1.0 + np.exp(-a)) * b)
-        return self.cls @ self._rms(x, f["eps"])
+        return self.cls @ self._rms(x, f["eps"], self.rms_final)

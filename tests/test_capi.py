@@ -57,6 +57,17 @@ def _hdr(img, n):
     return list(np.frombuffer(img[: 4 * n].tobytes(), np.int32))
 
 
+# synth.cpp norm roles: attention, ffn, final, Qwen3 q and k norms
+RMS_ATT, RMS_FFN, RMS_FINAL, Q_NORM, K_NORM = 13, 14, 15, 16, 17
+
+
+def _norms(K, cfg, role, layers, n):
+    """The norm vectors the writer emits for `role` over `layers`: 1 + N(0,
+    norm_std) per layer, concatenated."""
+    return np.concatenate([1.0 + K.synth_normal(1234, role, l, n, cfg.norm_std)
+                           for l in layers]).astype(np.float32)
+
+
 def test_llama_v0_layout(K):
     cfg = K.TINY["tiny_llama2"]
     img = K.synth_image(cfg)
@@ -68,13 +79,14 @@ def test_llama_v0_layout(K):
     emb = K.synth_normal(1234, 1, 0, V * D)
     assert np.array_equal(f[: V * D], emb)
     off = V * D
-    assert np.all(f[off: off + L * D] == 1.0)  # attention norms
+    assert np.array_equal(f[off: off + L * D], _norms(K, cfg, RMS_ATT, range(L), D))
+    assert not np.all(f[off: off + L * D] == 1.0)
     off += L * D
     assert np.array_equal(f[off: off + D * D], K.synth_normal(1234, 2, 0, D * D))  # wq[0]
     off += L * D * D + 2 * L * Dkv * D + L * D * D
-    assert np.all(f[off: off + L * D] == 1.0)  # ffn norms
+    assert np.array_equal(f[off: off + L * D], _norms(K, cfg, RMS_FFN, range(L), D))
     off += L * D + 3 * L * F * D
-    assert np.all(f[off: off + D] == 1.0)  # final norm
+    assert np.array_equal(f[off: off + D], _norms(K, cfg, RMS_FINAL, [0], D))
     off += D + S * hd  # freq tables
     assert np.array_equal(f[off:], K.synth_normal(1234, 9, 0, V * D))  # classifier
     assert f.size == off + V * D
@@ -93,8 +105,11 @@ def test_llama_int8_layout(K, O):
     q_ref, s_ref = O.quantize_q8(K.synth_normal(1234, 2, 0, n), gs)
     assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref)
     # fp32 embedding then (2L + 1) norm vectors close the file
-    tail = np.frombuffer(raw[-4 * (2 * cfg.layers + 1) * D:], np.float32)
-    assert np.all(tail == 1.0)
+    L = cfg.layers
+    tail = np.frombuffer(raw[-4 * (2 * L + 1) * D:], np.float32)
+    want = np.concatenate([_norms(K, cfg, RMS_ATT, range(L), D), _norms(K, cfg, RMS_FFN, range(L), D),
+                           _norms(K, cfg, RMS_FINAL, [0], D)])
+    assert np.array_equal(tail, want)
 
 
 def test_qwen2_bias_follows_weight(K):
@@ -118,11 +133,15 @@ def test_qwen3_layout(K):
     # export_qwen3.py:55-78: {q_dim, dim, L, H, KVH, V, seq, ffn}
     assert _hdr(img, 8) == [Dq, D, L, cfg.heads, cfg.kv_heads, V, cfg.seq_len, cfg.hidden_dim]
     f = np.frombuffer(img[32:].tobytes(), np.float32)
-    assert np.all(f[: (2 * L + 1) * D] == 1.0)
+    want = np.concatenate([_norms(K, cfg, RMS_ATT, range(L), D), _norms(K, cfg, RMS_FFN, range(L), D),
+                           _norms(K, cfg, RMS_FINAL, [0], D)])
+    assert np.array_equal(f[: (2 * L + 1) * D], want)
     off = (2 * L + 1) * D
     assert np.array_equal(f[off: off + V * D], K.synth_normal(1234, 1, 0, V * D))
     off += V * D + L * Dq * D
-    assert np.all(f[off: off + L * hd] == 1.0)  # q norms
+    assert np.array_equal(f[off: off + L * hd], _norms(K, cfg, Q_NORM, range(L), hd))  # q norms
+    off += L * hd + L * cfg.kv_dim * D
+    assert np.array_equal(f[off: off + L * hd], _norms(K, cfg, K_NORM, range(L), hd))  # k norms
     assert np.array_equal(f[-V * D:], K.synth_normal(1234, 9, 0, V * D))  # lm_head
 
 
@@ -139,3 +158,22 @@ def test_image_sizes_of_baseline_configs(K):
         assert extra >= -4 * cfg.dim, name
     gb = K.BASELINE["llama32_1b"].weight_bytes_per_token() / 1e9
     assert 4.94 < gb < 4.95  # 4943.3 MB of weights per token
+
+
+def test_mha_workspace_fits_reference_score_buffer(K):
+    """kl_mha's split partials fit the reference's score tensor, head_num x
+    seq_len floats (llama3.cpp:485-487, qwen2.cpp:550, qwen3.cpp:367), at
+    every BASELINE shape and over a sweep of sequence lengths; a context that
+    one workgroup per kv head covers needs none."""
+    for cfg in K.BASELINE.values():
+        sz = C.c_size_t(0)
+        assert K.lib.kl_mha_workspace_size(cfg.heads, cfg.heads // cfg.kv_heads, cfg.seq_len,
+                                           cfg.head_size, C.byref(sz)) == 0
+        assert 0 < sz.value <= cfg.heads * cfg.seq_len * 4, cfg.name
+    for H, kvm, hd in ((12, 6, 128), (32, 4, 64), (4, 2, 32), (2, 2, 256), (32, 1, 128)):
+        for S in (1, 2, 31, 64, 65, 130, 300, 1000, 4096, 8192, 20000):
+            sz = C.c_size_t(0)
+            assert K.lib.kl_mha_workspace_size(H, kvm, S, hd, C.byref(sz)) == 0
+            assert sz.value <= H * S * 4, (H, kvm, hd, S, sz.value)
+    sz = C.c_size_t(0)
+    assert K.lib.kl_mha_workspace_size(8, 2, 64, 64, C.byref(sz)) == 0 and sz.value == 0

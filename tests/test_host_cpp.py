@@ -4,7 +4,7 @@ model::Model) through its C++ test program tests/cpp/_build/test_host.
 
 * ``cpu_*`` units (no GPU): buffers, tensors, status codes, kernel factories,
   layer checks returning a Status, model-file errors (bad path, truncated
-  image, unsupported int8 layout).
+  image, Qwen3 int8 refused).
 * ``hip_*`` units (GPU): the reference's op tests (matmul known answers,
   int8 matmul, rmsnorm, per-row rmsnorm, add, in-place SwiGLU, embedding,
   first-max argmax, allocator reuse, tensor moves).
@@ -52,7 +52,7 @@ def rel(a, b):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2",
-                                  "tiny_qwen3"])
+                                  "tiny_qwen2_q8", "tiny_qwen3"])
 def test_host_model_matches_oracle(K, O, gpu, tmp_path, name):
     cfg = K.TINY[name]
     img = K.synth_image(cfg)

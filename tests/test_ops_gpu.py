@@ -152,10 +152,16 @@ def test_rope_bit_exact(K, O, gpu, style, dim, kv, hd):
 
 # ----------------------------------------------------------------- MHA ------
 @pytest.mark.parametrize("H,kvm,hd,S,pos", [(12, 1, 64, 1024, 0), (12, 1, 64, 1024, 143),
-                                            (32, 4, 64, 1024, 319), (12, 6, 128, 4096, 4095),
-                                            (32, 4, 128, 1024, 639), (32, 1, 128, 160, 77),
-                                            (4, 2, 32, 50, 17), (2, 2, 256, 300, 299)])
+                                            (32, 4, 64, 1024, 319), (32, 4, 64, 1024, 1023),
+                                            (12, 6, 128, 4096, 4095), (12, 6, 128, 4096, 4000),
+                                            (12, 6, 128, 4096, 191), (32, 4, 128, 1024, 639),
+                                            (32, 1, 128, 160, 77), (4, 2, 32, 50, 17),
+                                            (2, 2, 256, 300, 299), (32, 4, 128, 1024, 511)])
 def test_mha_vs_oracle(K, O, gpu, H, kvm, hd, S, pos):
+    """kl_mha with the reference's own score buffer, exactly head_num x
+    seq_len floats (llama3.cpp:485-487), left uninitialised (filled with NaN
+    bit patterns here): cfg 2's shape (32/8 heads of 64, seq 1024) and cfg
+    4's (12/2 heads of 128, seq 4096) among them."""
     rng = np.random.default_rng(H * S + pos)
     L, layer = 2, 1
     kvd = H // kvm * hd
@@ -164,12 +170,14 @@ def test_mha_vs_oracle(K, O, gpu, H, kvm, hd, S, pos):
     q = rng.standard_normal(H * hd).astype(np.float32)
     sz = C.c_size_t(0)
     ok(K.lib.kl_mha_workspace_size(H, kvm, S, hd, C.byref(sz)))
-    ws = K.DeviceArray(sz.value, np.uint8, zero=True)
+    score_bytes = H * S * 4
+    assert sz.value <= score_bytes
+    ws = D(K, np.full(H * S, np.nan, np.float32))
     dk, dv, dq, do = D(K, kc.ravel()), D(K, vc.ravel()), D(K, q), K.DeviceArray(H * hd)
     ref = O.mha(pos, H, layer, S, kvd, kvm, hd, q, kc, vc)
-    for _ in range(2):  # the second call reuses the workspace (counters reset)
-        ok(K.lib.kl_mha(pos, H, layer, S, kvd, kvm, hd, do.ptr, dq.ptr, ws.ptr, sz.value, dk.ptr,
-                        dv.ptr, None))
+    for _ in range(2):  # the second call reuses the workspace as the first left it
+        ok(K.lib.kl_mha(pos, H, layer, S, kvd, kvm, hd, do.ptr, dq.ptr, ws.ptr, score_bytes,
+                        dk.ptr, dv.ptr, None))
         out = do.numpy()
         assert np.max(np.abs(out - ref)) < 2e-5
     if pos == 0:  # softmax of one element: V0 exactly
@@ -180,10 +188,11 @@ def test_mha_vs_oracle(K, O, gpu, H, kvm, hd, S, pos):
 
 def test_mha_workspace_too_small(K, gpu):
     sz = C.c_size_t(0)
-    ok(K.lib.kl_mha_workspace_size(8, 2, 64, 64, C.byref(sz)))
+    ok(K.lib.kl_mha_workspace_size(8, 2, 1024, 64, C.byref(sz)))
+    assert sz.value > 16
     ws = K.DeviceArray(16, np.uint8, zero=True)
-    buf = K.DeviceArray(8 * 64 * 4)
-    assert K.lib.kl_mha(3, 8, 0, 64, 256, 2, 64, buf.ptr, buf.ptr, ws.ptr, 16, buf.ptr, buf.ptr,
+    buf = K.DeviceArray(8 * 1024 * 64)
+    assert K.lib.kl_mha(3, 8, 0, 1024, 256, 2, 64, buf.ptr, buf.ptr, ws.ptr, 16, buf.ptr, buf.ptr,
                         None) == -6
 
 

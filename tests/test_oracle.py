@@ -286,7 +286,10 @@ def test_argmax_first_max(O):
 
 
 # --------------------------------------------------------- whole model -----
-@pytest.mark.parametrize("name", ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2", "tiny_qwen3"])
+TINY_NAMES = ["tiny_llama2", "tiny_llama3", "tiny_q8", "tiny_qwen2", "tiny_qwen2_q8", "tiny_qwen3"]
+
+
+@pytest.mark.parametrize("name", TINY_NAMES)
 def test_model_step_vs_fp64_model(K, O, name):
     from npmodel import NpModel
 
@@ -302,6 +305,85 @@ def test_model_step_vs_fp64_model(K, O, name):
     # the K cache row holds the rotated key
     assert rel_err(om.kv_row(1, 5, False), nm.kc[1, 5]) < 1e-4
     assert rel_err(om.kv_row(0, 3, True), nm.vc[0, 3]) < 1e-4
+
+
+def _norm_offsets(cfg):
+    """Byte offsets of the norm vectors in an image: {(role, layer): (offset,
+    floats)} for the attention ("att"), ffn ("ffn"), final ("fin") and Qwen3
+    q/k ("qn", "kn") norms, in the writers' layouts (export_llama.py:79-210,
+    export_qwen2.py:79-210, export_qwen3.py:55-102)."""
+    D, Dq, Dkv, F, L, V, hd = (cfg.dim, cfg.qd, cfg.kv_dim, cfg.hidden_dim, cfg.layers, cfg.vocab,
+                               cfg.head_size)
+    out = {}
+    if cfg.family == 3:
+        off = 32
+        for l in range(L):
+            out[("att", l)] = (off + 4 * l * D, D)
+            out[("ffn", l)] = (off + 4 * (L + l) * D, D)
+        out[("fin", 0)] = (off + 4 * 2 * L * D, D)
+        off += 4 * ((2 * L + 1) * D + V * D + L * Dq * D)
+        for l in range(L):
+            out[("qn", l)] = (off + 4 * l * hd, hd)
+        off += 4 * (L * hd + L * Dkv * D)
+        for l in range(L):
+            out[("kn", l)] = (off + 4 * l * hd, hd)
+    elif cfg.quant:
+        gs = cfg.group_size
+        q8 = lambda n: n + n // gs * 4
+        off = 32 + L * (q8(Dq * D) + 2 * q8(Dkv * D) + q8(D * Dq) + 3 * q8(F * D)) + q8(V * D)
+        off += 4 * V * D
+        for l in range(L):
+            out[("att", l)] = (off + 4 * l * D, D)
+            out[("ffn", l)] = (off + 4 * (L + l) * D, D)
+        out[("fin", 0)] = (off + 4 * 2 * L * D, D)
+    else:
+        b = (Dq + 2 * Dkv) if cfg.family == 2 else 0
+        off = 28 + 4 * V * D
+        for l in range(L):
+            out[("att", l)] = (off + 4 * l * D, D)
+        off += 4 * (L * D + L * (Dq * D + 2 * Dkv * D + b + D * Dq))
+        for l in range(L):
+            out[("ffn", l)] = (off + 4 * l * D, D)
+        out[("fin", 0)] = (off + 4 * (L * D + 3 * L * F * D), D)
+    return out
+
+
+@pytest.mark.parametrize("name,a,b", [
+    ("tiny_llama3", ("att", 0), ("ffn", 0)),   # layer l's ffn norm used for attention
+    ("tiny_llama2", ("att", 0), ("att", 1)),   # off-by-one layer index
+    ("tiny_qwen2", ("ffn", 1), ("fin", 0)),    # final norm taken from the wrong slot
+    ("tiny_q8", ("att", 1), ("ffn", 1)),
+    ("tiny_qwen3", ("qn", 0), ("kn", 0)),      # q_norm and k_norm swapped
+    ("tiny_qwen3", ("qn", 0), ("qn", 1)),
+])
+def test_fp64_pin_catches_swapped_norms(K, O, name, a, b):
+    """A planted mistake in the oracle's input: two norm vectors of the image
+    swapped (what a wrong offset in a parser would read) make the oracle
+    disagree with the fp64 model, which takes every norm from its own stream.
+    So the pin sees the norm weights, and the same swap in any GPU path fails
+    its comparison with the oracle."""
+    from npmodel import NpModel
+
+    cfg = K.TINY[name]
+    img = K.synth_image(cfg).copy()
+    offs = _norm_offsets(cfg)
+    (oa, na), (ob, nb) = offs[a], offs[b]
+    n = min(na, nb)
+    va = img[oa: oa + 4 * n].copy()
+    vb = img[ob: ob + 4 * n].copy()
+    assert not np.array_equal(va, vb)
+    nm = NpModel(K, cfg)
+    good = O.Model(K.synth_image(cfg), cfg.family, cfg.quant)
+    img[oa: oa + 4 * n], img[ob: ob + 4 * n] = vb, va
+    bad = O.Model(img, cfg.family, cfg.quant)
+    toks = K.prompt_tokens(cfg, 4)
+    worst_bad = worst_good = 0.0
+    for pos, t in enumerate(toks):
+        ln = nm.step(int(t), pos)
+        worst_good = max(worst_good, rel_err(good.step(int(t), pos), ln))
+        worst_bad = max(worst_bad, rel_err(bad.step(int(t), pos), ln))
+    assert worst_good < 2e-5
+    assert worst_bad > 1e-3, (name, a, b, worst_bad)
 
 
 def test_model_generate_follows_demo_loop(K, O):

@@ -8,7 +8,9 @@ oracle's MHA at each position; whole-prompt logits within 1e-4 relative
 (max |gpu - cpu| / max |cpu|) and the greedy tokens identical.  At full size
 (cfg 5: 512-token prompt, cfg 4: 4000-position fill) the oracle is too slow
 for the whole prompt, so the prefill is checked against the engine's own
-step-by-step path, which the decode tests pin to the oracle.
+step-by-step path, which the decode tests pin to the oracle; cfg 5's shape at
+2 layers (narrow FFN and vocabulary) runs its 512-token prefill against the
+oracle directly.
 """
 import ctypes as C
 
@@ -215,6 +217,43 @@ def test_engine_prefill_vs_oracle(K, O, gpu, name):
         ref2 = om.step(tok, pos)
         assert rel(lg2, ref2) < LOGIT_RTOL
         tok = O.argmax(ref2)
+
+
+def test_qwen3_shape_prefill_512_vs_oracle(K, O, gpu):
+    """cfg 5's layer shape (Qwen3: dim 2560, 32 Q / 8 KV heads of 128, q/k
+    norms) at 2 layers with non-unit norm weights: the 512-token prompt as one
+    batched prefill against the oracle's token-by-token run, then 8 greedy
+    decode steps in the persistent mode from the prefilled cache."""
+    cfg = K.BASELINE["qwen3_4b"].with_(name="qwen3_shape_2l", layers=2, hidden_dim=1024,
+                                       vocab=2048, norm_std=0.1)
+    img = K.synth_image(cfg)
+    P = 512
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    eng = K.Engine(img, cfg)
+    eng.set_mode(K.MODE_PERSISTENT)
+    assert eng.mode == K.MODE_PERSISTENT
+    nxt, lg, ms = eng.prefill(prompt)
+    om = O.Model(img, cfg.family, cfg.quant)
+    for pos in range(P - 1):
+        om.step(prompt[pos], pos)
+    ref = om.step(prompt[P - 1], P - 1)
+    r = rel(lg, ref)
+    print(f"qwen3 shape: prefill of {P} tokens in {ms:.2f} ms, logits rel err {r:.2e}", flush=True)
+    assert r < LOGIT_RTOL
+    want = O.argmax(ref)
+    assert nxt == want, float(ref[want]) - float(ref[nxt])
+    for layer in (0, 1):
+        for pos in (0, 255, 511):
+            for which_v in (False, True):
+                a, b = eng.kv_row(layer, pos, which_v), om.kv_row(layer, pos, which_v)
+                assert np.max(np.abs(a - b)) <= 1e-5 * max(np.max(np.abs(b)), 1.0)
+    tok = want
+    for pos in range(P, P + 8):
+        n2, lg2 = eng.step(tok, pos)
+        ref2 = om.step(tok, pos)
+        assert rel(lg2, ref2) < LOGIT_RTOL, pos
+        tok = O.argmax(ref2)
+        assert n2 == tok, pos
 
 
 @pytest.mark.parametrize("name", FP32_TINY)
