@@ -132,6 +132,20 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
            int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
            const float* key_cache, const float* value_cache, void* stream);
 
+/* No reference counterpart: kl_mha for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same kernels, plan and result as kl_mha; the split partials live in a
+ * library-owned device array of kl_mha_noalloc_max_bytes() bytes (1 MiB) per
+ * device, held until the process ends.  A shape whose partials need more
+ * (kl_mha_workspace_size) returns KL_EWORKSPACE before any launch.  Calls
+ * share the device's array: calls that overlap on one device (different
+ * streams, or host threads) race and must be serialised by the caller.
+ * Allocates nothing. */
+size_t kl_mha_noalloc_max_bytes(void);
+int kl_mha_noalloc(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+                   int head_size, float* out, const float* q, const float* key_cache,
+                   const float* value_cache, void* stream);
+
 /* ---- Batched prompt prefill (no reference counterpart: the reference runs
  * the prompt token by token, demo/main.cpp:20-22, and MatmulLayer accepts
  * only a 1-D input, op/matmul.cpp:20).  Row-major, fp32, device pointers. ---- */

@@ -90,6 +90,8 @@ _SIGS = {
     "kl_rope": (_i, [_i, _i, _i, _i, _p, _p, _i, _p, _p, _p]),
     "kl_mha_workspace_size": (_i, [_i, _i, _i, _i, C.POINTER(_sz)]),
     "kl_mha": (_i, [_i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _sz, _p, _p, _p]),
+    "kl_mha_noalloc_max_bytes": (_sz, []),
+    "kl_mha_noalloc": (_i, [_i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p]),
     "kl_gemm_f32": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
     "kl_gemm_f32_grouped": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
     "kl_gemm_f32_splitk": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i, _i, _p, _sz, _p]),

@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "attn.hpp"
@@ -556,25 +557,23 @@ int kl_mha_workspace_size(int head_num, int kv_mul, int seq_len, int head_size, 
   return KL_OK;
 }
 
-int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
-           int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
-           const float* key_cache, const float* value_cache, void* stream) {
-  if (!out || !q || !workspace || !key_cache || !value_cache) return KL_EINVAL;
-  if (!mha_shape_ok(head_num, kv_mul, head_size)) return KL_EUNSUPP;
-  if (pos < 0 || pos >= seq_len || layer_index < 0) return KL_EINVAL;
+}  // extern "C"
+
+namespace {
+
+// kl_mha's launches with the split partials at `part` (need bytes of the
+// mha_plan_fit plan, checked by the caller).
+int mha_launch(const MhaPlan& p, int pos, int head_num, int layer_index, int seq_len, int kv_dim,
+               int kv_mul, int head_size, float* out, const float* q, float* part,
+               const float* key_cache, const float* value_cache, hipStream_t st) {
   const int kv_heads = head_num / kv_mul;
-  if (kv_dim != kv_heads * head_size) return KL_EINVAL;
-  size_t need = 0;
-  const MhaPlan p = mha_plan_fit(head_num, kv_mul, seq_len, head_size, &need);
-  if (p.G > 512) return KL_EUNSUPP;
-  if (workspace_bytes < need) return KL_EWORKSPACE;
   AttnArgs a{};
   const size_t layer_off = static_cast<size_t>(layer_index) * seq_len * kv_dim;
   a.q = q;
   a.kcache = const_cast<float*>(key_cache) + layer_off;
   a.vcache = value_cache + layer_off;
   a.out = out;
-  a.part = static_cast<float*>(workspace);
+  a.part = part;
   a.counters = nullptr;  // the spans are merged by k_attn_merge: no counter to initialise
   a.pos_ptr = nullptr;
   a.pos_val = pos;
@@ -588,7 +587,6 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
   const int nsplit = (pos + span) / span;
   const dim3 grid(kv_heads * p.G), block(256);
   const size_t merge_lds = static_cast<size_t>(nsplit) * kv_mul * 2 * sizeof(float);
-  hipStream_t st = as_stream(stream);
   switch (head_size) {
     case 32: hipLaunchKernelGGL(k_attn_decode<32>, grid, block, p.lds_bytes, st, a); break;
     case 64: hipLaunchKernelGGL(k_attn_decode<64>, grid, block, p.lds_bytes, st, a); break;
@@ -605,6 +603,82 @@ int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int 
     }
   }
   return launch_rc();
+}
+
+// Argument checks shared by kl_mha and kl_mha_noalloc; on success *p is the
+// plan and *need its workspace bytes.
+int mha_check(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+              int head_size, const float* out, const float* q, const float* key_cache,
+              const float* value_cache, MhaPlan* p, size_t* need) {
+  if (!out || !q || !key_cache || !value_cache) return KL_EINVAL;
+  if (!mha_shape_ok(head_num, kv_mul, head_size)) return KL_EUNSUPP;
+  if (pos < 0 || pos >= seq_len || layer_index < 0) return KL_EINVAL;
+  if (kv_dim != head_num / kv_mul * head_size) return KL_EINVAL;
+  *p = mha_plan_fit(head_num, kv_mul, seq_len, head_size, need);
+  if (p->G > 512) return KL_EUNSUPP;
+  return KL_OK;
+}
+
+// The no-allocation variant's partials: one array per device, found with
+// hipGetSymbolAddress on the first call on each device (the array's host-side
+// name is not a device address).
+constexpr size_t kMhaScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) unsigned char scratch[kMhaScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return rc(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return KL_EUNSUPP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return rc(e);
+    if (!p) return KL_EDEVICE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kl_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+           int head_size, float* out, const float* q, void* workspace, size_t workspace_bytes,
+           const float* key_cache, const float* value_cache, void* stream) {
+  if (!workspace) return KL_EINVAL;
+  MhaPlan p;
+  size_t need = 0;
+  const int r = mha_check(pos, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size, out, q,
+                          key_cache, value_cache, &p, &need);
+  if (r != KL_OK) return r;
+  if (workspace_bytes < need) return KL_EWORKSPACE;
+  return mha_launch(p, pos, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size, out, q,
+                    static_cast<float*>(workspace), key_cache, value_cache, as_stream(stream));
+}
+
+size_t kl_mha_noalloc_max_bytes(void) { return kMhaScratchBytes; }
+
+int kl_mha_noalloc(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
+                   int head_size, float* out, const float* q, const float* key_cache,
+                   const float* value_cache, void* stream) {
+  MhaPlan p;
+  size_t need = 0;
+  int r = mha_check(pos, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size, out, q,
+                    key_cache, value_cache, &p, &need);
+  if (r != KL_OK) return r;
+  if (need > kMhaScratchBytes) return KL_EWORKSPACE;
+  void* part = nullptr;
+  r = scratch_for_current_device(&part);
+  if (r != KL_OK) return r;
+  return mha_launch(p, pos, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size, out, q,
+                    static_cast<float*>(part), key_cache, value_cache, as_stream(stream));
 }
 
 int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ldq, float* k,
