@@ -17,8 +17,15 @@ on both sides.  Prints one JSON line.
                  in --mode multi the W1/W3 + SwiGLU GEMV.  Achieved = bytes per
                  launch / average launch duration, measured with HIP events
                  around each launch on the engine's stream
+  prefill        the batched prompt prefill of cfg 5 (Qwen3-4B shape, 512
+                 tokens) on the matrix cores: prompt tok/s, TFLOP/s against the
+                 fp32 MFMA peak, and the MFMA-busy fraction rocprofv3 measured
+                 for the same command (profiles/prefill_qwen3_4b_pmc.txt)
   cpu_baseline   the CPU oracle (a restatement of the reference CPU path,
-                 "port") on a bounded sample of the same workload
+                 "port") on the same workload: the same prompt through the
+                 demo/main.cpp loop, then the timed positions (continued until
+                 a bounded sample of CPU time is reached), on all the
+                 process's host threads, plus a 1-thread figure
 """
 from __future__ import annotations
 
@@ -72,6 +79,26 @@ def measured_traffic(kernel: str, config: str, mode: str):
 MFMA_FP32_PEAK_TFLOPS = 157.3
 
 
+def measured_mfma_busy(config: str):
+    """MFMA-busy fraction of the prefill kernels on `config`, from the
+    committed rocprofv3 PMC summary of this same command
+    (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, per kernel,
+    weighted by kernel time); None when no summary covers it."""
+    pat = re.compile(r"measured: prefill config=(\S+) mfma_busy=([0-9.]+) gemm_mfma_busy=([0-9.]+) "
+                     r"attn_mfma_busy=([0-9.]+)")
+    path = os.path.join(ROOT, "profiles", f"prefill_{config}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            m = pat.search(line)
+            if m and m.group(1) == config:
+                return {"all": float(m.group(2)), "gemm": float(m.group(3)),
+                        "attention": float(m.group(4)),
+                        "source": os.path.relpath(path, ROOT)}
+    return None
+
+
 def measure_prefill(K, cfg, reps: int = 3) -> dict:
     """Batched prefill of the config's prompt (kl_engine_prefill), device time
     from HIP events inside the call; best of `reps` after one warm-up.  The
@@ -89,37 +116,95 @@ def measure_prefill(K, cfg, reps: int = 3) -> dict:
             "tok_s": round(P / (ms / 1e3), 1), "tflops": round(tf, 2),
             "bound": "mfma", "peak_tflops": MFMA_FP32_PEAK_TFLOPS,
             "frac": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "flops": int(fl),
-            "dtype": "f32"}
+            "dtype": "f32", "mfma_busy": measured_mfma_busy(cfg.name)}
 
 
-def cpu_baseline(K, cfg, img, seconds: float) -> dict:
+def host_cpu() -> dict:
+    """Host threads visible to this process and the CPU model name."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": nproc, "model": model}
+
+
+def cpu_baseline(K, cfg, img, first_pos: int, steps: int, gpu_tokens, seconds: float,
+                 seconds_1t: float) -> dict:
+    """The oracle (the reference CPU path restated) on the bench workload:
+    the same prompt through the demo/main.cpp loop (prompt positions, then
+    greedy decode) untimed up to the GPU's first timed position, then the
+    GPU's timed positions, continued greedily until `seconds` of CPU time (at
+    least `steps` steps) on every host thread the process may use; then a few
+    more steps on 1 thread.  Also reports whether its greedy tokens over the
+    GPU's positions equal the GPU's."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
+    hc = host_cpu()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or hc["nproc"]
+    O.set_threads(threads)
     m = O.Model(img, cfg.family, cfg.quant)
-    threads = O.lib.or_get_threads()
-    prompt = K.prompt_tokens(cfg, 4)
-    tok = int(prompt[0])
-    for pos in range(len(prompt) - 1):
-        m.step(int(prompt[pos]), pos)
-    tok = int(prompt[-1])
-    pos = len(prompt) - 1
+    prompt = [int(t) for t in K.prompt_tokens(cfg)]
+    P = len(prompt)
+    seq = list(prompt)
+    pos = 0
+    t_fill = time.perf_counter()
+    while pos < first_pos:  # positions 0 .. first_pos - 1, untimed
+        lg = m.step(seq[pos], pos)
+        if pos >= P - 1:
+            seq.append(O.argmax(lg))
+        pos += 1
+    t_fill = time.perf_counter() - t_fill
+    reserve = 8  # positions kept for the 1-thread leg
     n, t0 = 0, time.perf_counter()
-    while True:
-        lg = m.step(tok, pos)
-        tok = O.argmax(lg)
+    el = 0.0
+    while pos < cfg.seq_len - 1 - reserve or n < steps:
+        lg = m.step(seq[pos], pos)
+        seq.append(O.argmax(lg))
         pos += 1
         n += 1
         el = time.perf_counter() - t0
-        if (el >= seconds and n >= 2) or pos >= cfg.seq_len - 1:
+        if el >= seconds and n >= steps:
             break
+    all_core = n / el
+    last_all = pos - 1
+    O.set_threads(1)
+    n1, t1 = 0, time.perf_counter()
+    el1 = 0.0
+    while pos < cfg.seq_len - 1:
+        lg = m.step(seq[pos], pos)
+        seq.append(O.argmax(lg))
+        pos += 1
+        n1 += 1
+        el1 = time.perf_counter() - t1
+        if el1 >= seconds_1t and n1 >= 2:
+            break
+    O.set_threads(threads)
+    # seq[i + 1] is the token sampled at position i (i >= P - 1); the GPU's
+    # gpu_tokens[j] was sampled at position P - 1 + j.
+    cpu_tok = seq[P:P + len(gpu_tokens)]
     return {
-        "value": round(n / el, 4),
+        "value": round(all_core, 4),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} greedy decode steps after a 4-token prompt (positions 3..{pos - 1}), "
-                  f"{el:.1f} s, {threads} OpenMP threads",
+        "value_1thread": round(n1 / el1, 4) if n1 else None,
+        "host": hc,
+        "tokens_match_gpu": [int(t) for t in gpu_tokens] == cpu_tok,
+        "sample": f"{P}-token prompt and decode to position {first_pos - 1} untimed "
+                  f"({t_fill:.1f} s), then {n} greedy decode steps at positions "
+                  f"{first_pos}..{last_all} in {el:.1f} s on {threads} OpenMP threads "
+                  f"({hc['nproc']} visible, {hc['model']}), then {n1} steps at positions "
+                  f"{last_all + 1}..{pos - 1} in {el1:.1f} s on 1 thread",
     }
 
 
@@ -129,14 +214,19 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=0, help="timed decode steps (default: config)")
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="llama32_1b")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU baseline: timed seconds on all host threads")
+    ap.add_argument("--cpu-seconds-1t", type=float, default=6.0,
+                    help="CPU baseline: timed seconds on 1 thread")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--mode", choices=("persistent", "multi"), default="persistent")
-    ap.add_argument("--prefill-config", default="",
-                    help="also time the batched prefill of this config's prompt (e.g. qwen3_4b: "
-                         "512 tokens) and report it under 'prefill'")
+    ap.add_argument("--prefill-config", default="qwen3_4b",
+                    help="also time the batched prefill of this config's prompt (default "
+                         "qwen3_4b: 512 tokens) and report it under 'prefill'; 'none' skips it")
+    ap.add_argument("--skip-decode", action="store_true",
+                    help="run only the prefill leg (for profiling it); prints no bench line")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy, the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -158,6 +248,13 @@ def main() -> int:
         K.check(K.lib.kl_device_sync(), "kl_device_sync")
         src.free()
         dst.free()
+    if args.skip_decode:
+        if args.prefill_config == "none":
+            print("bench.py: --skip-decode needs a prefill config", file=sys.stderr)
+            return 2
+        pf = measure_prefill(K, K.BASELINE[args.prefill_config])
+        print(f"# prefill {pf}", file=sys.stderr, flush=True)
+        return 0
     cfg = K.BASELINE[args.config]
     steps = args.steps or cfg.decode_steps
     P = cfg.prompt_len
@@ -211,14 +308,16 @@ def main() -> int:
           + f"; step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
 
     prefill = None
-    if args.prefill_config:
+    if args.prefill_config != "none":
         del eng
         prefill = measure_prefill(K, K.BASELINE[args.prefill_config])
         print(f"# prefill {prefill}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(K, cfg, img, args.cpu_seconds)
+        # toks[j] is the token sampled at position P - 1 + j
+        cpu = cpu_baseline(K, cfg, img, first_pos, steps, toks, args.cpu_seconds,
+                           args.cpu_seconds_1t)
         print(f"# cpu baseline {cpu}", file=sys.stderr, flush=True)
 
     out = {
