@@ -741,6 +741,10 @@ int max_share(const std::vector<int>& off) {
 int setup_persistent(kl_engine* e) {
   const ImageLayout& m = e->lay;
   const bool q8 = e->quant != 0;
+  // Hand-off tags are epoch * kTagLayers + layer + 1 for layers -1 .. L-1:
+  // with L >= kTagLayers one launch's last layer would carry the next
+  // launch's first tag, so such models run the multi-kernel step.
+  if (m.L >= kTagLayers) return KL_OK;
   int nb = 4;
   if (const char* env = std::getenv("KL_PNB")) nb = std::atoi(env);
   if (q8)

@@ -71,6 +71,21 @@ std::vector<int32_t> parse_ids(const std::string& text, bool* ok) {
 }
 
 // main_qwen.cpp:198-284 with token ids.
+// Why a prompt cannot run on the model ("" when it can): ids outside
+// [0, vocab) or more positions than the model's sequence length.
+std::string prompt_error(const model::Model& m, const std::vector<int32_t>& prompt) {
+  const auto& c = m.config();
+  for (int32_t t : prompt) {
+    if (t < 0 || t >= c.vocab_size_)
+      return "token id " + std::to_string(t) + " is outside [0, " + std::to_string(c.vocab_size_) +
+             ")";
+  }
+  if (static_cast<int64_t>(prompt.size()) > c.seq_len_)
+    return "the prompt has " + std::to_string(prompt.size()) + " tokens; the model holds " +
+           std::to_string(c.seq_len_) + " positions";
+  return "";
+}
+
 GenerationResult generate(const model::Model& m, const std::vector<int32_t>& prompt, int max_new,
                           bool use_prefill) {
   GenerationResult r;
@@ -258,6 +273,14 @@ int main(int argc, char** argv) {
         std::fflush(stdout);
         continue;
       }
+      // A bad request gets an error line; it must not reach the model, whose
+      // failed checks end the process.
+      const std::string why = prompt_error(*m, prompt);
+      if (!why.empty()) {
+        std::printf("[ERROR] %s\n", why.c_str());
+        std::fflush(stdout);
+        continue;
+      }
       const auto t0 = std::chrono::steady_clock::now();
       const GenerationResult r = generate(*m, prompt, max_steps, o.prefill);
       const double dt =
@@ -276,6 +299,11 @@ int main(int argc, char** argv) {
   const int max_steps = pos_args.size() == 3 ? parse_max(pos_args[2].c_str()) : 128;
   auto m = load(pos_args[0], o);
   if (!m) return 1;
+  const std::string why = prompt_error(*m, prompt);
+  if (!why.empty()) {
+    std::fprintf(stderr, "kuiper_generate: %s\n", why.c_str());
+    return 2;
+  }
   if (o.prefill) STATUS_CHECK(m->set_prefill(true));
   const auto t0 = std::chrono::steady_clock::now();
   const GenerationResult r = generate(*m, prompt, max_steps, o.prefill);

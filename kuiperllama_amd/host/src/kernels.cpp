@@ -116,7 +116,7 @@ void embedding_hip(const tensor::Tensor& input, const tensor::Tensor& weight,
   if (input.device_type() == base::DeviceType::kDeviceCPU) {
     for (int i = 0; i < n; ++i) {
       const int32_t t = input.index<int32_t>(i);
-      KUIPER_CHECK(t >= 0 && t < vocab_size, "Token index is greater than vocab size.");
+      KUIPER_CHECK(t >= 0 && t < vocab_size, "embedding: token id outside [0, vocab)");
     }
     int32_t* staged = stage_ids(n);
     check_rc(kl_memcpy_h2d(staged, input.ptr<int32_t>(), n * sizeof(int32_t), stream),

@@ -32,32 +32,40 @@ base::Status Layer::init() { return base::error::Success(); }
 
 base::Status Layer::forward() { return base::error::FunctionNotImplement(""); }
 
+// Which property of a layer operand does not match what the layer expects
+// ("" when everything matches): presence, device, element type, then shape.
+static std::string operand_mismatch(const tensor::Tensor& t, base::DeviceType device_type,
+                                    base::DataType data_type, const std::vector<int32_t>* dims) {
+  if (t.is_empty()) return "operand holds no data";
+  if (t.device_type() != device_type) return "operand lives on another device";
+  if (t.data_type() != data_type) return "operand element type differs from the layer's";
+  if (!dims) return "";
+  const int32_t rank = static_cast<int32_t>(dims->size());
+  if (t.dims_size() != rank)
+    return "operand rank " + std::to_string(t.dims_size()) + ", expected " + std::to_string(rank);
+  for (int32_t i = 0; i < rank; ++i) {
+    if (t.get_dim(i) != (*dims)[i])
+      return "operand extent " + std::to_string(t.get_dim(i)) + " on axis " + std::to_string(i) +
+             ", expected " + std::to_string((*dims)[i]);
+  }
+  return "";
+}
+
 base::Status Layer::check_tensor(const tensor::Tensor& tensor, base::DeviceType device_type,
                                  base::DataType data_type) const {
-  if (tensor.is_empty()) return base::error::InvalidArgument("The tensor parameter is empty.");
-  if (tensor.device_type() != device_type)
-    return base::error::InvalidArgument("The tensor has a wrong device type.");
-  if (tensor.data_type() != data_type)
-    return base::error::InvalidArgument("The tensor has a wrong data type.");
-  return base::error::Success();
+  const std::string why = operand_mismatch(tensor, device_type, data_type, nullptr);
+  return why.empty() ? base::error::Success() : base::error::InvalidArgument(why);
 }
 
 base::Status Layer::check_tensor_with_dim(const tensor::Tensor& tensor,
                                           base::DeviceType device_type, base::DataType data_type,
                                           const std::vector<int32_t>& dims) const {
-  base::Status s = check_tensor(tensor, device_type, data_type);
-  if (!s) return s;
-  if (tensor.dims_size() != static_cast<int32_t>(dims.size()))
-    return base::error::InvalidArgument("The tensor has a wrong number of dimensions.");
-  for (size_t i = 0; i < dims.size(); ++i)
-    if (tensor.get_dim(static_cast<int32_t>(i)) != dims[i])
-      return base::error::InvalidArgument("The tensor has a wrong dim in dim" +
-                                          std::to_string(i));
-  return base::error::Success();
+  const std::string why = operand_mismatch(tensor, device_type, data_type, &dims);
+  return why.empty() ? base::error::Success() : base::error::InvalidArgument(why);
 }
 
 base::Status Layer::check() const {
-  return base::error::FunctionNotImplement("The check function is not implement yet");
+  return base::error::FunctionNotImplement(layer_name_ + " defines no operand check");
 }
 
 base::Status Layer::forward(const tensor::Tensor& input1, const tensor::Tensor& output1) {
@@ -443,7 +451,7 @@ base::Status EmbeddingLayer::check() const {
   const tensor::Tensor& input = get_input(0);
   const int32_t token_size = static_cast<int32_t>(get_input(1).size());
   if (token_size > static_cast<int32_t>(input.size()))
-    return base::error::InvalidArgument("The number of input tensor is greater than seq len.");
+    return base::error::InvalidArgument("more token ids than the layer's sequence length");
   base::Status s = check_tensor_with_dim(input, base::DeviceType::kDeviceCPU,
                                          base::DataType::kDataTypeInt32, {token_size});
   if (!s) return s;

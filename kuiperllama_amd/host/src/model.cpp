@@ -101,26 +101,24 @@ base::Status Model::init(base::DeviceType device_type) {
 // Qwen3 images carry an eighth header int (the FFN width).
 base::Status Model::read_model_file() {
   if (model_path_.empty())
-    return base::error::PathNotValid("Failed to open the weight file, the model path is empty!");
+    return base::error::PathNotValid("No model file was given (empty path).");
   auto raw = std::make_shared<RawModelData>();
   raw->fd = open(model_path_.c_str(), O_RDONLY);
   if (raw->fd == -1)
-    return base::error::PathNotValid("Failed to open the weight file " + model_path_ +
-                                     " may be the path does not exist!");
+    return base::error::PathNotValid("Cannot open model file " + model_path_ + ".");
   struct stat st;
   if (fstat(raw->fd, &st) == -1)
-    return base::error::ModelParseError("Failed to retrieve the file size of " + model_path_);
+    return base::error::ModelParseError("Cannot stat model file " + model_path_ + ".");
   raw->file_size = static_cast<size_t>(st.st_size);
   const bool qwen3 = family_ == ModelFamily::kQwen3;
   const size_t header_ints = 7 + ((qwen3 || is_quant_model_) ? 1 : 0);
   if (raw->file_size < header_ints * sizeof(int32_t))
     return base::error::ModelParseError(
-        "Failed to retrieve the configuration information from the model file.");
+        "Model file too short for its header.");
   raw->data = mmap(nullptr, raw->file_size, PROT_READ, MAP_PRIVATE, raw->fd, 0);
   if (raw->data == MAP_FAILED || raw->data == nullptr) {
     raw->data = nullptr;
-    return base::error::ModelParseError("Failed to map the weight file " + model_path_ +
-                                        " into memory.");
+    return base::error::ModelParseError("Cannot mmap model file " + model_path_ + ".");
   }
   const int32_t* h = static_cast<const int32_t*>(raw->data);
   ModelConfig config;
@@ -138,7 +136,7 @@ base::Status Model::read_model_file() {
   if (!s) return s;
   if (is_quant_model_ && group_size_ <= 0)
     return base::error::ModelParseError(
-        "Failed to retrieve the group size information from the model file.");
+        "Model file too short for the int8 group size field.");
   raw->weight_data = static_cast<const int8_t*>(raw->data) + header_ints * sizeof(int32_t);
   raw_model_data_ = raw;
   return base::error::Success();
@@ -341,25 +339,26 @@ base::Status Model::create_layers() {
 
   auto& ly = *layers_;
   if (!ly.embedding_layer_)
-    return base::error::InternalError("Create the embedding layer for the llama model failed!");
+    return base::error::InternalError("The model has no embedding layer after loading.");
   const size_t norms = family_ == ModelFamily::kQwen3 ? 4 * L + 1 : 2 * L + 1;
   if (ly.rmsnorm_layers_.size() != norms)
-    return base::error::InternalError("Create the rmsnorm layers for the llama model failed!");
+    return base::error::InternalError("The model has the wrong number of norm layers after loading.");
   if (ly.wq_layers_.size() != L || ly.wk_layers_.size() != L || ly.wv_layers_.size() != L ||
       ly.wo_layers_.size() != L)
-    return base::error::InternalError("Create the attention matmul layers for the llama model failed!");
+    return base::error::InternalError("An attention projection is missing after loading.");
   if (ly.w1_layers_.size() != L || ly.w2_layers_.size() != L || ly.w3_layers_.size() != L)
-    return base::error::InternalError("Create the feedforward matmul layers for the llama model failed!");
+    return base::error::InternalError("A feed-forward projection is missing after loading.");
   if (!ly.cls_layer_ || !ly.rope_layer_ || !ly.mha_layer_ || !ly.add_layer_ || !ly.swiglu_layer_)
-    return base::error::InternalError("Create the llama model layers failed!");
+    return base::error::InternalError("The model layers are incomplete after loading.");
   return base::error::Success();
 }
 
 base::Status Model::insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor) {
   if (buffers_.count(buffer_idx) > 0)
-    return base::error::KeyHasExits(std::to_string(int(buffer_idx)) +
-                                    " has exits in the buffers");
-  if (tensor.is_empty()) return base::error::InvalidArgument("The tensor is empty for inserting buffer.");
+    return base::error::KeyHasExits("model buffer " + std::to_string(int(buffer_idx)) +
+                                    " is registered already");
+  if (tensor.is_empty())
+    return base::error::InvalidArgument("An empty tensor cannot be registered as a model buffer.");
   buffers_.insert({buffer_idx, tensor});
   return base::error::Success();
 }

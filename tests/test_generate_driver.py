@@ -88,19 +88,29 @@ def test_serve_protocol(K, O, gpu, images):
     cfg, path = images["tiny_qwen3"]
     import numpy as np
     img = np.fromfile(path, np.uint8)
-    prompts = [[int(t) for t in K.prompt_tokens(cfg, 5, seed=s)] for s in (11, 12)]
+    prompts = [[int(t) for t in K.prompt_tokens(cfg, 5, seed=s)] for s in (11, 12, 13)]
+
+    def request(ids_text):
+        return "[PROMPT_START]\n" + ids_text + "\n[PROMPT_END]\n"
+
     stdin = ""
-    for pr in prompts:
-        stdin += "[PROMPT_START]\n" + " ".join(map(str, pr[:3])) + "\n" + \
-                 ",".join(map(str, pr[3:])) + "\n[PROMPT_END]\n"
-    stdin += "[PROMPT_START]\nnot ids\n[PROMPT_END]\n[EXIT]\n"
+    for pr in prompts[:2]:
+        stdin += request(" ".join(map(str, pr[:3])) + "\n" + ",".join(map(str, pr[3:])))
+    # bad requests get an [ERROR] line and the server keeps serving
+    stdin += request("not ids")
+    stdin += request(f"1 2 {cfg.vocab}")                      # id outside [0, vocab)
+    stdin += request(" ".join(["5"] * (cfg.seq_len + 1)))     # longer than seq_len
+    stdin += request(" ".join(map(str, prompts[2])))
+    stdin += "[EXIT]\n"
     p = run(["--serve", "--family", "qwen3", "--prefill", path, "7"], stdin=stdin)
     assert p.returncode == 0, p.stderr
     assert p.stdout.splitlines()[0] == "[READY]"
     blocks = p.stdout.split("[RESPONSE_START]")[1:]
-    assert len(blocks) == 2
+    assert len(blocks) == 3
     for pr, blk in zip(prompts, blocks):
         got = [int(t) for t in blk.split("[RESPONSE_END]")[0].split()]
         want = [int(t) for t in O.Model(img, cfg.family, cfg.quant).generate(pr, 8)]
         assert got == want
-    assert "[ERROR]" in p.stdout
+    errors = [l for l in p.stdout.splitlines() if l.startswith("[ERROR]")]
+    assert len(errors) == 3, errors
+    assert "outside [0, " in errors[1] and "positions" in errors[2]
