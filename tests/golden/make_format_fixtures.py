@@ -40,15 +40,18 @@ SEED, STD, NORM_STD = 1234, 0.02, 0.1
 EMB, WQ, WK, WV, WO, W1, W2, W3, CLS, BQ, BK, BV = range(1, 13)
 RMS_ATT, RMS_FFN, RMS_FINAL, Q_NORM, K_NORM = range(13, 18)
 
-# name -> kl_model_spec fields (family 0 Llama2, 2 Qwen2, 3 Qwen3)
+# name -> kl_model_spec fields (family 0 Llama2, 2 Qwen2, 3 Qwen3).  The int8
+# images keep every row a whole number of 64-element groups (the decode
+# engine's requirement; the reference's group index runs over the flattened
+# matrix, the same thing when rows hold whole groups).
 SPECS = {
     "fmt_llama_fp32": dict(family=0, dim=64, q_dim=64, hidden_dim=96, layers=2, heads=2,
                            kv_heads=1, vocab=128, seq_len=32, tied=0, group_size=0),
-    "fmt_llama_q8": dict(family=0, dim=64, q_dim=64, hidden_dim=96, layers=2, heads=2,
+    "fmt_llama_q8": dict(family=0, dim=64, q_dim=64, hidden_dim=128, layers=2, heads=2,
                          kv_heads=1, vocab=128, seq_len=32, tied=0, group_size=64),
     "fmt_qwen2_fp32": dict(family=2, dim=64, q_dim=64, hidden_dim=96, layers=2, heads=2,
                            kv_heads=1, vocab=128, seq_len=32, tied=1, group_size=0),
-    "fmt_qwen2_q8": dict(family=2, dim=64, q_dim=64, hidden_dim=96, layers=2, heads=2,
+    "fmt_qwen2_q8": dict(family=2, dim=64, q_dim=64, hidden_dim=128, layers=2, heads=2,
                          kv_heads=1, vocab=128, seq_len=32, tied=0, group_size=64),
     "fmt_qwen3_fp32": dict(family=3, dim=64, q_dim=128, hidden_dim=96, layers=2, heads=4,
                            kv_heads=2, vocab=128, seq_len=32, tied=0, group_size=0),
