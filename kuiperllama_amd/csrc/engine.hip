@@ -444,13 +444,16 @@ struct kl_engine {
   size_t p_lds = 0;
   size_t p_lds_traced = 0;     // p_lds + the trace slots (traced launches)
   bool trace_ok = false;       // the traced launch is co-resident too
-  const void* p_kernel = nullptr;
+  const void* p_kernel = nullptr;        // long-context attention variant
+  const void* p_kernel_short = nullptr;  // short-context attention variant
+  int host_pos = 0;  // position of the next persistent launch (chooses the variant)
   PGemv* d_ph = nullptr;       // [4L + 1] phase descriptors (arena)
   // Row split per workgroup, weighted by measured streaming speed (empty:
   // balanced).  d_split holds 4 tables of nwg + 1 row offsets: QKV rows, D, F, V.
   std::vector<double> wg_weight;
   int* d_split = nullptr;
   PAttn* d_at = nullptr;       // [L]
+  float* qkn = nullptr;        // [L][2][hd] Qwen3 q and k norm weights (arena)
   tagged_t *t_q = nullptr, *t_k = nullptr, *t_v = nullptr, *t_att = nullptr;  // tagged
   tagged_t *t_xb = nullptr, *t_h = nullptr, *t_x = nullptr;                    //   hand-off
   tagged_t* t_part = nullptr;  // attention split partials (tagged)
@@ -606,15 +609,25 @@ int launch_step(kl_engine* e, Marks* mk = nullptr) {
 }
 
 // One persistent launch = one token.
+// Uploads the device step state (the next launch's position and token).
+hipError_t set_state(kl_engine* e, const StepState& st) {
+  *e->st_host = st;
+  e->host_pos = st.pos;
+  return hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+}
+
 int launch_persistent(kl_engine* e, Marks* mk = nullptr) {
   void* params[] = {&e->pargs};
   const size_t lds = e->pargs.trace ? e->p_lds_traced : e->p_lds;
+  // Every launch advances the device position by one; the host follows it to
+  // pick the attention variant (a mismatch is reported by the kernel).
+  const void* k = e->host_pos + 1 <= e->pargs.attn_short_max ? e->p_kernel_short : e->p_kernel;
+  ++e->host_pos;
   mark(e->stream, mk, kKStep);
   const hipError_t err =
       e->plain_launch
-          ? hipLaunchKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads), params, lds, e->stream)
-          : hipLaunchCooperativeKernel(e->p_kernel, dim3(e->nwg), dim3(kPThreads), params, lds,
-                                       e->stream);
+          ? hipLaunchKernel(k, dim3(e->nwg), dim3(kPThreads), params, lds, e->stream)
+          : hipLaunchCooperativeKernel(k, dim3(e->nwg), dim3(kPThreads), params, lds, e->stream);
   mark(e->stream, mk, kKEnd);
   return rc(err);
 }
@@ -701,13 +714,13 @@ size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb, int max_share) {
   return static_cast<size_t>(p.paired ? rmax * p.nsub : rmax) * p.ks;
 }
 
-template <bool Q8, int NB>
+template <bool Q8, int NB, bool SHORT>
 const void* persistent_kernel(int hd) {
   switch (hd) {
-    case 32: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 32>);
-    case 64: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 64>);
-    case 128: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 128>);
-    default: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 256>);
+    case 32: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 32, SHORT>);
+    case 64: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 64, SHORT>);
+    case 128: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 128, SHORT>);
+    default: return reinterpret_cast<const void*>(&k_decode_persistent<Q8, NB, 256, SHORT>);
   }
 }
 
@@ -747,10 +760,13 @@ int setup_persistent(kl_engine* e) {
   if (m.L >= kTagLayers) return KL_OK;
   int nb = 4;
   if (const char* env = std::getenv("KL_PNB")) nb = std::atoi(env);
-  if (q8)
-    e->p_kernel = nb == 4 ? persistent_kernel<true, 4>(m.hd) : persistent_kernel<true, 8>(m.hd);
-  else
-    e->p_kernel = nb == 4 ? persistent_kernel<false, 4>(m.hd) : persistent_kernel<false, 8>(m.hd);
+  if (q8) {
+    e->p_kernel = nb == 4 ? persistent_kernel<true, 4, false>(m.hd) : persistent_kernel<true, 8, false>(m.hd);
+    e->p_kernel_short = nb == 4 ? persistent_kernel<true, 4, true>(m.hd) : persistent_kernel<true, 8, true>(m.hd);
+  } else {
+    e->p_kernel = nb == 4 ? persistent_kernel<false, 4, false>(m.hd) : persistent_kernel<false, 8, false>(m.hd);
+    e->p_kernel_short = nb == 4 ? persistent_kernel<false, 4, true>(m.hd) : persistent_kernel<false, 8, true>(m.hd);
+  }
   if (nb != 4 && nb != 8) nb = 8;
   int per_cu = 1;
   if (const char* env = std::getenv("KL_PWG_PER_CU"))
@@ -851,7 +867,8 @@ int setup_persistent(kl_engine* e) {
   const int xres_off = red_off + static_cast<int>((red_floats + 3) & ~size_t(3));
   const int xres_floats = weighted ? share_d : (m.D + e->nwg - 1) / e->nwg;
   const size_t gemv_lds = (static_cast<size_t>(xres_off) + xres_floats) * sizeof(float);
-  const size_t attn_lds = attn_p_lds_floats(m.hd, m.H / m.KVH) * sizeof(float);
+  const size_t attn_lds = std::max(attn_p_lds_floats(m.hd, m.H / m.KVH),
+                                   attn_short_lds_floats(m.hd)) * sizeof(float);
   // The residual rows must survive the attention phase, which uses LDS from 0.
   const size_t xres_at = std::max(static_cast<size_t>(xres_off) * sizeof(float),
                                   (attn_lds + 15) & ~size_t(15));
@@ -899,6 +916,18 @@ int setup_persistent(kl_engine* e) {
   a.touch_delay = 50;
   if (const char* env = std::getenv("KL_W13_TOUCH_ROWS")) a.w13_touch_rows = std::max(0, std::atoi(env));
   if (const char* env = std::getenv("KL_TOUCH_DELAY")) a.touch_delay = std::max(0, std::atoi(env));
+  // Short-context attention (one item per query head, no merge) up to the
+  // positions its registers hold; KL_ATTN_SHORT_MAX lowers the limit (0: off).
+  a.attn_short_max = attn_short_rows(m.hd);
+  if (const char* env = std::getenv("KL_ATTN_SHORT_MAX"))
+    a.attn_short_max = std::min(a.attn_short_max, std::max(0, std::atoi(env)));
+  a.short_touch_rows = a.w13_touch_rows;
+  a.kc0 = e->kcache;
+  a.vc0 = e->vcache;
+  a.kv_layer = static_cast<long long>(m.S) * m.Dkv;
+  a.qkn = e->qkn;
+  if (const char* env = std::getenv("KL_W13_TOUCH_ROWS_SHORT"))
+    a.short_touch_rows = std::max(0, std::atoi(env));
   a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
   a.epoch = e->epoch; a.err = e->derr;
   a.red_off = red_off;
@@ -909,25 +938,31 @@ int setup_persistent(kl_engine* e) {
 
   // The grid must be co-resident: one workgroup of 512 threads per CU (or
   // KL_PWG_PER_CU) with this LDS.
-  if (e->p_lds_traced > 64 * 1024) {
-    err = hipFuncSetAttribute(e->p_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(e->p_lds_traced));
+  int blocks = kMaxPwgPerCu;
+  e->trace_ok = true;
+  for (const void* kern : {e->p_kernel, e->p_kernel_short}) {
+    if (e->p_lds_traced > 64 * 1024) {
+      err = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(e->p_lds_traced));
+      if (err != hipSuccess) {
+        (void)hipGetLastError();
+        return KL_OK;
+      }
+    }
+    int b = 0;
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kern, kPThreads, e->p_lds);
     if (err != hipSuccess) {
       (void)hipGetLastError();
       return KL_OK;
     }
-  }
-  int blocks = 0;
-  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, e->p_kernel, kPThreads, e->p_lds);
-  if (err != hipSuccess) {
-    (void)hipGetLastError();
-    return KL_OK;
+    blocks = std::min(blocks, b);
+    int bt = 0;
+    e->trace_ok = e->trace_ok &&
+                  hipOccupancyMaxActiveBlocksPerMultiprocessor(&bt, kern, kPThreads, e->p_lds_traced) ==
+                      hipSuccess &&
+                  bt >= per_cu;
   }
   e->persistent_ok = blocks >= per_cu;
-  int blocks_traced = 0;
-  e->trace_ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks_traced, e->p_kernel, kPThreads,
-                                                             e->p_lds_traced) == hipSuccess &&
-                blocks_traced >= per_cu;
   (void)hipGetLastError();
   e->mode = e->persistent_ok ? KL_MODE_PERSISTENT : KL_MODE_MULTI;
   e->plain_launch = e->persistent_ok && blocks * e->cus >= e->nwg;
@@ -966,9 +1001,7 @@ int trace_once(kl_engine* e, int32_t token, int32_t pos, unsigned long long* tic
   hipError_t err = hipMalloc(&d, n * sizeof(unsigned long long));
   if (err != hipSuccess) return rc(err);
   err = hipMemset(d, 0, n * sizeof(unsigned long long));
-  *e->st_host = StepState{pos, token, 0, 0};
-  if (err == hipSuccess)
-    err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  if (err == hipSuccess) err = set_state(e, StepState{pos, token, 0, 0});
   int r = rc(err);
   if (r == KL_OK) {
     e->pargs.trace = d;
@@ -1158,6 +1191,7 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   const int gmax = std::max(e->grid_cap, e->cus * kMaxPwgPerCu);
   const size_t ph_at = plan((4 * static_cast<size_t>(lay.L) + 1) * sizeof(PGemv));
   const size_t at_at = plan(static_cast<size_t>(lay.L) * sizeof(PAttn));
+  const size_t qkn_at = plan(static_cast<size_t>(lay.L) * 2 * lay.hd * 4);  // [L][q, k][hd]
   const size_t pv_at = plan(gmax * 4), pi_at = plan(gmax * 4);
   const size_t pr_at = plan(S * 4), ot_at = plan(S * 4);
   e->arena_bytes = cursor;
@@ -1222,6 +1256,19 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   e->t_part = PT(tpart_at);
   e->d_ph = reinterpret_cast<PGemv*>(P(ph_at));
   e->d_at = reinterpret_cast<PAttn*>(P(at_at));
+  // The Qwen3 q/k norm weights again, side by side per layer, for the decode
+  // step's short-context attention (addressed by arithmetic).
+  e->qkn = PF(qkn_at);
+  for (int l = 0; l < lay.L && err == hipSuccess; ++l) {
+    const LayerDev& d = e->layers[l];
+    float* dst = e->qkn + static_cast<size_t>(l) * 2 * lay.hd;
+    if (d.qn) err = hipMemcpy(dst, d.qn, lay.hd * 4, hipMemcpyDeviceToDevice);
+    if (err == hipSuccess && d.kn) err = hipMemcpy(dst + lay.hd, d.kn, lay.hd * 4, hipMemcpyDeviceToDevice);
+  }
+  if (err != hipSuccess) {
+    release(e);
+    return rc(err);
+  }
   e->lay.layers.clear();  // host pointers are no longer needed
   err = hipMemset(e->arena + zero_begin, 0, zero_end - zero_begin);
   if (err == hipSuccess) err = hipMemset(e->kcache, 0, 2 * static_cast<size_t>(lay.L) * S * Dkv * 4);
@@ -1308,9 +1355,7 @@ int kl_engine_step(kl_engine* e, int32_t token, int32_t pos, int32_t* next, floa
   if (!e) return KL_EINVAL;
   if (pos < 0 || pos >= e->lay.S) return KL_EINVAL;
   if (token < 0 || token >= e->lay.V) return KL_ETOKEN;
-  *e->st_host = StepState{pos, token, 0, 0};
-  hipError_t err =
-      hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  hipError_t err = set_state(e, StepState{pos, token, 0, 0});
   if (err != hipSuccess) return rc(err);
   const int r = run_step(e);
   if (r != KL_OK) return r;
@@ -1518,9 +1563,7 @@ int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, in
     out_tokens[0] = first;
     if (decode_ms) *decode_ms = 0.f;
     if (n_new == 1) return KL_OK;
-    *e->st_host = StepState{P, first, P, first};
-    hipError_t err =
-        hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+    hipError_t err = set_state(e, StepState{P, first, P, first});
     if (err == hipSuccess) err = hipEventRecord(e->ev0, e->stream);
     if (err != hipSuccess) return rc(err);
     for (int i = 0; i < n_new - 1; ++i) {
@@ -1544,8 +1587,7 @@ int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, in
   hipError_t err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
                                   e->stream);
   if (err != hipSuccess) return rc(err);
-  *e->st_host = StepState{0, prompt[0], P, 0};
-  err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  err = set_state(e, StepState{0, prompt[0], P, 0});
   if (err != hipSuccess) return rc(err);
   // Prompt positions 0 .. P-2, then n_new sampled positions P-1 .. P+n_new-2.
   for (int i = 0; i < P - 1; ++i) {
@@ -1583,8 +1625,7 @@ int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, in
   hipError_t err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
                                   e->stream);
   if (err != hipSuccess) return rc(err);
-  *e->st_host = StepState{0, prompt[0], P, 0};
-  err = hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  err = set_state(e, StepState{0, prompt[0], P, 0});
   if (err != hipSuccess) return rc(err);
   for (int i = 0; i < P - 1 + n_warmup; ++i) {
     const int r = run_step(e);
@@ -1630,9 +1671,7 @@ int kl_engine_profile(kl_engine* e, int32_t token, int32_t pos0, int steps, floa
     avg_ms[k] = 0.f;
     counts[k] = 0;
   }
-  *e->st_host = StepState{pos0, token, 0, 0};
-  hipError_t err =
-      hipMemcpyAsync(e->st, e->st_host, sizeof(StepState), hipMemcpyHostToDevice, e->stream);
+  hipError_t err = set_state(e, StepState{pos0, token, 0, 0});
   if (err != hipSuccess) return rc(err);
   std::vector<hipEvent_t> ev;
   std::vector<int> kinds;

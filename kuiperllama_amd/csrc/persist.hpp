@@ -72,6 +72,7 @@ constexpr unsigned int kEpochWrap = 1u << 24;
 constexpr int kDevErrWait = 1;   // a wait for another workgroup exceeded kSpinLimit polls
 constexpr int kDevErrPos = 2;    // position or token outside the model's range
 constexpr int kDevErrToken = 3;  // the sampler found no finite maximum
+constexpr int kDevErrVariant = 4;  // the launch's attention variant does not fit its position
 
 enum : int { kEpiQkv = 0, kEpiResid = 1, kEpiSwiglu = 2, kEpiCls = 3 };
 
@@ -141,6 +142,17 @@ struct PArgs {
   // after touch_delay 100 MHz ticks, and a slice of the attention
   // workgroups' rows.
   int touch_delay, w13_touch_rows;
+  // Attention over at most attn_short_max positions (pos + 1) takes the
+  // short-context path: one item per query head, no split (0: never).  Its
+  // idle workgroups pull short_touch_rows local rows of W1/W3 into L2.
+  int attn_short_max, short_touch_rows;
+  // Its per-layer operands by arithmetic (no descriptor load on the critical
+  // path): K/V cache layer l at kc0 / vc0 + l * kv_layer, Qwen3 q/k norm
+  // weights at qkn + l * 2 * HD (q) and + HD (k).
+  float* kc0;
+  const float* vc0;
+  long long kv_layer;
+  const float* qkn;
   float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
   unsigned int* am_cnt;    // end-of-step arrival counter
@@ -758,7 +770,15 @@ __device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, 
   const int n = pos + 1;
   const int nsplit = (n + PT - 1) / PT;
   const int it = blockIdx.x;
-  if (it >= a.KVH * nsplit) return;
+  if (it >= a.KVH * nsplit) {
+    // No item: pre is still written, so that it is dead between attention
+    // phases (nothing carries it around the layer loop).
+#pragma unroll
+    for (int p = 0; p < NP; ++p) pre.kr[p] = pre.vr[p] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < AttnPre<HD>::NW; ++k) pre.qn[k] = pre.kn[k] = 0.f;
+    return;
+  }
   const int g = it / nsplit;
   const int s = it - g * nsplit;
   const int t0 = s * PT;
@@ -775,14 +795,12 @@ __device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, 
     pre.kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
     pre.vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
   }
-  if (a.transform == 2) {
-    const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int k = 0; k < AttnPre<HD>::NW; ++k) {
-      const int d = lane + k * kWave;
-      pre.qn[k] = d < HD ? g_rd(at->qn + d) : 0.f;
-      pre.kn[k] = d < HD ? g_rd(at->kn + d) : 0.f;
-    }
+  for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+    const int d = lane + k * kWave;
+    pre.qn[k] = a.transform == 2 && d < HD ? g_rd(at->qn + d) : 0.f;
+    pre.kn[k] = a.transform == 2 && d < HD ? g_rd(at->kn + d) : 0.f;
   }
 }
 
@@ -1118,6 +1136,271 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 }
 
 // ---------------------------------------------------------------------------
+// Short-context attention (pos + 1 <= attn_short_max).  Same semantics as
+// attn_p_phase, but one item per query head covers every position, so no
+// partials cross workgroups and there is no merge hand-off.  A thread owns
+// one float4 (dims 4 sub .. 4 sub + 3) of one K/V row per pass: TPR = HD / 4
+// lanes per row, RPP rows per pass, up to kAttnShortPasses passes, the K and
+// V rows in registers.  q, the new K and V rows are polled straight into the
+// same lanes (every row group holds a copy), so the Qwen3 q/k RMSNorm is a
+// TPR-lane DPP sum and RoPE's rotate-half partner is the lane TPR / 2 away.
+// Each wave reduces its rows to (m, l, o[HD]); one barrier, then HD / 4
+// threads merge the eight waves and store the head's output.
+// ---------------------------------------------------------------------------
+constexpr int kAttnShortPasses = 8;
+__host__ __device__ constexpr int attn_short_rows(int hd) {
+  return kAttnShortPasses * (kPThreads / (hd / 4));
+}
+// LDS floats: per-wave partials [kPWaves][HD + 2], then per-wave inputs
+// [kPWaves][7 HD] (q, new K, new V, cos, sin, qn, kn).
+__host__ __device__ constexpr size_t attn_short_wp_floats(int hd) {
+  return (static_cast<size_t>(kPWaves) * (hd + 2) + 3) & ~size_t(3);
+}
+__host__ __device__ constexpr size_t attn_short_lds_floats(int hd) {
+  return attn_short_wp_floats(hd) + static_cast<size_t>(kPWaves) * 7 * hd;
+}
+
+// Sum over the W aligned lanes of a row group, in every lane of the group
+// (bitwise equal in all of them: each step adds two values that are equal up
+// to the order of the operands).
+template <int W>
+__device__ __forceinline__ float rowgroup_sum(float v) {
+  if constexpr (W <= 16) {
+    return group_sum_dpp<W>(v);
+  } else {
+    v = group_sum_dpp<16>(v);
+    v += __shfl_xor(v, 16);
+    if constexpr (W == 64) v += __shfl_xor(v, 32);
+    return v;
+  }
+}
+// Sum over the row groups of a wave (lanes W apart), in every lane.
+template <int W>
+__device__ __forceinline__ float across_groups_sum(float v) {
+#pragma unroll
+  for (int off = W; off < kWave; off <<= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Raw buffer load of 16 bytes at byte offset `off` of a buffer of `bytes`
+// bytes: offsets past the end return zeros and read no memory.
+__device__ __forceinline__ f4 buf_ld4(__amdgpu_buffer_rsrc_t r, unsigned int off) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float* base, unsigned int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
+}
+
+template <int HD>
+__device__ __forceinline__ void attn_short_phase(const PArgs& a, int layer, int pos,
+                                                 unsigned int tag, float* lds, int trace_slot) {
+  constexpr int TPR = HD / 4;
+  constexpr int RPP = kPThreads / TPR;
+  constexpr int NPM = kAttnShortPasses;
+  constexpr int NE = (3 * HD + kWave - 1) / kWave;  // polled elements per lane
+  constexpr int NT = (HD + kWave - 1) / kWave;      // table entries per lane and vector
+  float* kcache = a.kc0 + layer * a.kv_layer;
+  const float* vcache = a.vc0 + layer * a.kv_layer;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int sub = tid % TPR;
+  const int rg = tid / TPR;
+  const int kvm = a.kv_mul;
+  const int n = pos + 1;
+  const int items = a.KVH * kvm;
+  const int ppos = pos / RPP, rgpos = pos - ppos * RPP;  // pass and row group of row pos
+  float* wp = lds;  // [kPWaves][HD + 2]: per wave o[HD], m, l
+  // Per wave: q, new K, new V [3 HD], then cos, sin, qn, kn [4 HD].
+  float* wv = lds + attn_short_wp_floats(HD) + wave * 7 * HD;
+  // The cached rows, through buffer loads bounded to rows < pos (row pos
+  // comes from the QKV phase): rows past the context return zeros and cost
+  // no memory traffic, so the code stays straight-line (exact wait counts)
+  // and moves only the context's bytes.
+  const unsigned int ctx_bytes = static_cast<unsigned int>(pos) * a.Dkv * 4;
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    // Items of one kv head sit KVH apart in workgroup order, on the same XCD
+    // when KVH is a multiple of 8 (round-robin dispatch), sharing its L2.
+    const int g = it % a.KVH, j = it / a.KVH;
+    const int h = g * kvm + j;
+    const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
+
+    // 1. Each wave polls q (head h) and the new K and V rows of kv head g
+    //    once ([q | k | v], NE elements per lane); the first round is issued
+    //    before the loads below, so that it is in flight while they are.
+    tagged_t v[NE];
+    auto addr = [&](int k) {
+      int e = lane + k * kWave;
+      e = e < 3 * HD ? e : 0;
+      const tagged_t* base = e < HD       ? a.q + static_cast<size_t>(h) * HD
+                             : e < 2 * HD ? a.knew + static_cast<size_t>(g) * HD - HD
+                                          : a.vnew + static_cast<size_t>(g) * HD - 2 * HD;
+      return base + e;
+    };
+    unsigned int valid = 0;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      v[k] = g_ld64(addr(k));
+      if (lane + k * kWave < 3 * HD) valid |= 1u << k;
+    }
+    // 2. The position's RoPE table rows and the Qwen3 norm weights (NT per
+    //    lane each), and the cached K and V rows.
+    float tb[4][NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const int d = lane + k * kWave < HD ? lane + k * kWave : 0;
+      tb[0][k] = a.transform >= 1 ? g_rd(a.cos_t + static_cast<size_t>(pos) * HD + d) : 1.f;
+      tb[1][k] = a.transform >= 1 ? g_rd(a.sin_t + static_cast<size_t>(pos) * HD + d) : 0.f;
+      tb[2][k] = a.transform == 2 ? g_rd(a.qkn + static_cast<size_t>(layer) * 2 * HD + d) : 0.f;
+      tb[3][k] = a.transform == 2 ? g_rd(a.qkn + static_cast<size_t>(layer) * 2 * HD + HD + d) : 0.f;
+    }
+    const __amdgpu_buffer_rsrc_t kb = buf_rsrc(kcache, ctx_bytes);
+    const __amdgpu_buffer_rsrc_t vb = buf_rsrc(vcache, ctx_bytes);
+    f4 kr[NPM], vr[NPM];
+#pragma unroll
+    for (int p = 0; p < NPM; ++p) {
+      const unsigned int off = static_cast<unsigned int>((p * RPP + rg) * a.Dkv + col) * 4;
+      kr[p] = buf_ld4(kb, off);
+      vr[p] = buf_ld4(vb, off);
+    }
+    poll_many<NE>(a, tag, addr, valid, v);
+    if (it == static_cast<int>(blockIdx.x)) trace_mark(a, trace_slot);  // inputs arrived
+    // Through the wave's own LDS slice (in order within a wave: no barrier).
+#pragma unroll
+    for (int k = 0; k < NE; ++k)
+      if (lane + k * kWave < 3 * HD) wv[lane + k * kWave] = val_of(v[k]);
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+      if (lane + k * kWave < HD)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) wv[3 * HD + x * HD + lane + k * kWave] = tb[x][k];
+    f4 q4 = reinterpret_cast<const f4*>(wv)[sub];
+    f4 k4 = reinterpret_cast<const f4*>(wv + HD)[sub];
+    const f4 v4 = reinterpret_cast<const f4*>(wv + 2 * HD)[sub];
+    const float* cs = wv + 3 * HD;
+    const float* sn = wv + 4 * HD;
+
+    // 3. Qwen3 per-head q/k RMSNorm (model/qwen3.cpp:485-500), then RoPE:
+    //    interleaved pairs (2j, 2j + 1) and rotate-half pairs (j, j + HD / 2)
+    //    both take table entry 2j (kernels/cpu/rope_kernel.cpp).
+    if (a.transform == 2) {
+      const f4 qn = reinterpret_cast<const f4*>(wv + 5 * HD)[sub];
+      const f4 kn = reinterpret_cast<const f4*>(wv + 6 * HD)[sub];
+      const float rq = 1.f / sqrtf(rowgroup_sum<TPR>(hsum(q4 * q4)) / static_cast<float>(HD) + a.qk_eps);
+      const float rk = 1.f / sqrtf(rowgroup_sum<TPR>(hsum(k4 * k4)) / static_cast<float>(HD) + a.qk_eps);
+      q4 = (rq * q4) * qn;
+      k4 = (rk * k4) * kn;
+    }
+    if (a.transform >= 1) {
+      if (a.rope_style == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; k += 2) {
+          const float c = cs[4 * sub + k], sv = sn[4 * sub + k];
+          float a0 = q4[k], a1 = q4[k + 1];
+          rope_pair(a0, a1, c, sv);
+          q4[k] = a0;
+          q4[k + 1] = a1;
+          float b0 = k4[k], b1 = k4[k + 1];
+          rope_pair(b0, b1, c, sv);
+          k4[k] = b0;
+          k4[k + 1] = b1;
+        }
+      } else {
+        // Dims d < HD / 2 pair with d + HD / 2, held TPR / 2 lanes away.
+        const bool lo = sub < TPR / 2;
+        f4 qo, ko;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          qo[k] = __shfl_xor(q4[k], TPR / 2);
+          ko[k] = __shfl_xor(k4[k], TPR / 2);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int ti = 2 * ((4 * sub + k) % (HD / 2));
+          const float c = cs[ti], sv = sn[ti];
+          float a0 = lo ? q4[k] : qo[k], a1 = lo ? qo[k] : q4[k];
+          rope_pair(a0, a1, c, sv);
+          q4[k] = lo ? a0 : a1;
+          float b0 = lo ? k4[k] : ko[k], b1 = lo ? ko[k] : k4[k];
+          rope_pair(b0, b1, c, sv);
+          k4[k] = lo ? b0 : b1;
+        }
+      }
+    }
+    // Row pos joins the registers; its K row (transformed) goes to the cache.
+#pragma unroll
+    for (int p = 0; p < NPM; ++p) {
+      const bool own = p == ppos && rg == rgpos;
+      kr[p] = own ? k4 : kr[p];
+      vr[p] = own ? v4 : vr[p];
+    }
+    if (j == 0 && rg == rgpos) *reinterpret_cast<f4*>(kcache + static_cast<size_t>(pos) * a.Dkv + col) = k4;
+
+    // 4. Scores of this thread's rows (-inf past the context), the wave's
+    //    maximum, its softmax sum and o = sum_t e_t V_t over its rows.
+    float sc[NPM];
+    float m = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < NPM; ++p) {
+      const float d = rowgroup_sum<TPR>(hsum(kr[p] * q4));
+      sc[p] = p * RPP + rg < n ? d * a.scale : -INFINITY;
+      m = fmaxf(m, sc[p]);
+    }
+    m = wave_max_dpp(m);
+    float l = 0.f;
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < NPM; ++p) {
+      const float e = p * RPP + rg < n ? expf(sc[p] - m) : 0.f;  // a wave past the context: m = -inf
+      l += e;
+      o += e * vr[p];
+    }
+    l = across_groups_sum<TPR>(l);
+    o.x = across_groups_sum<TPR>(o.x);
+    o.y = across_groups_sum<TPR>(o.y);
+    o.z = across_groups_sum<TPR>(o.z);
+    o.w = across_groups_sum<TPR>(o.w);
+    float* w = wp + wave * (HD + 2);
+    if (lane < TPR) reinterpret_cast<f4*>(w)[sub] = o;
+    if (lane == 0) {
+      w[HD] = m;
+      w[HD + 1] = l;
+    }
+    __syncthreads();
+    // 5. Merge the waves: M = max m_w, L = sum l_w e^(m_w - M), O likewise
+    //    (a wave without rows has m = -inf, weight 0); the output is O / L.
+    if (tid < TPR) {
+      float mw[kPWaves], lw[kPWaves];
+      f4 ow[kPWaves];
+#pragma unroll
+      for (int x = 0; x < kPWaves; ++x) {
+        mw[x] = wp[x * (HD + 2) + HD];
+        lw[x] = wp[x * (HD + 2) + HD + 1];
+        ow[x] = reinterpret_cast<const f4*>(wp + x * (HD + 2))[tid];
+      }
+      float M = mw[0];
+#pragma unroll
+      for (int x = 1; x < kPWaves; ++x) M = fmaxf(M, mw[x]);
+      float L = 0.f;
+      f4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int x = 0; x < kPWaves; ++x) {
+        const float c = expf(mw[x] - M);
+        L += lw[x] * c;
+        O += c * ow[x];
+      }
+      tagged_t* op = a.att + static_cast<size_t>(h) * HD + 4 * tid;
+      g_st_tagged(op + 0, O.x / L, tag);
+      g_st_tagged(op + 1, O.y / L, tag);
+      g_st_tagged(op + 2, O.z / L, tag);
+      g_st_tagged(op + 3, O.w / L, tag);
+    }
+    __syncthreads();  // LDS is reused by the next item
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Epilogues of the QKV, residual and SwiGLU phases.  `xres` holds this
 // workgroup's rows of the residual stream (the WO and W2 phases split the D
 // rows identically); `rn` is the RMSNorm scale of the phase's input.
@@ -1158,7 +1441,10 @@ __device__ __forceinline__ void p_epilogue(PGp p, const PGeom& g, const float* r
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
-template <bool Q8, int NB, int HD>
+// SHORT selects the attention path at compile time (short-context items, or
+// the chunked split with merges): a kernel holding both needs more registers
+// than a wave has.  The host launches the variant that fits the position.
+template <bool Q8, int NB, int HD, bool SHORT>
 __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ float sred[2 * kPWaves];
@@ -1170,6 +1456,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   const int token = st.token;
   if (pos < 0 || pos >= a.S || token < 0 || token >= a.V) {
     if (blockIdx.x == 0 && threadIdx.x == 0) g_st(a.err, kDevErrPos);
+    return;
+  }
+  if ((pos + 1 <= a.attn_short_max) != SHORT) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) g_st(a.err, kDevErrVariant);
     return;
   }
   const bool sample = pos + 1 >= st.prompt_len;
@@ -1191,6 +1481,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     rope_s = g_rd(a.sin_t + static_cast<size_t>(pos) * HD + 2 * j);
   }
   AttnPre<HD> pre;
+  constexpr bool attn_short = SHORT;
   if (a.trace) {
     for (int s = threadIdx.x; s < a.trace_slots; s += kPThreads) trace_lds(a)[s] = 0;
     __syncthreads();
@@ -1213,7 +1504,16 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     const PGeom g = p_geom(p);
     const unsigned int tag_in = epoch * kTagLayers + p->in_layer + 1;
     const unsigned int tag = epoch * kTagLayers + p->layer + 1;
-    if ((k & 3) == 0 && !is_cls) attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
+    if ((k & 3) == 0 && !is_cls) {
+      if (attn_short) {
+#pragma unroll
+        for (int p = 0; p < AttnPre<HD>::NP; ++p) pre.kr[p] = pre.vr[p] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < AttnPre<HD>::NW; ++q) pre.qn[q] = pre.kn[q] = 0.f;
+      } else {
+        attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
+      }
+    }
     stage_vec(a, p->in, tag_in, emb_row, p->norm, p->cols, xs, sred);
     trace_mark(a, slot++);
     {
@@ -1252,14 +1552,20 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     trace_mark(a, slot++);
     if (!pn) break;  // last layer of a prompt position: no classifier
     if ((k & 3) == 0) {  // after QKV: attention of layer k / 4
-      const int items = a.KVH * ((pos + attn_chunk(HD)) / attn_chunk(HD));
+      const int items = attn_short ? a.KVH * a.kv_mul
+                                   : a.KVH * ((pos + attn_chunk(HD)) / attn_chunk(HD));
       const int b = static_cast<int>(blockIdx.x);
       if (b >= items) {
         trace_mark(a, slot);  // no attention item: "inputs arrived" = now
         // Idle until the attention output arrives: pull this workgroup's WO
         // rows into L2, and those of the attention workgroup b - 8 ceil(items / 8)
         // (the same XCD under round-robin dispatch), which has no time to.
-        if (a.w13_touch_rows > 0) {
+        const int nw = static_cast<int>(gridDim.x);
+        // The attention phase, and so the window for the pull, lengthens with
+        // the number of attention items: pull up to 1.5x as much then.
+        const int rows = attn_short ? a.short_touch_rows
+                                    : a.w13_touch_rows + a.w13_touch_rows * min(items, nw / 2) / nw;
+        if (rows > 0) {
           if (a.touch_delay > 0) {
             const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
             while (__builtin_amdgcn_s_memrealtime() - t0 < static_cast<unsigned long long>(a.touch_delay))
@@ -1270,10 +1576,6 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
           // workgroups of the XCD share that work, an even slice each (at
           // most two attention workgroups' rows per slice are pulled).
           const PGp pw = pn + 1;  // W1/W3
-          const int nw = static_cast<int>(gridDim.x);
-          // The attention phase, and so the window for the pull, lengthens with
-          // the number of attention items: pull up to 1.5x as much then.
-          const int rows = a.w13_touch_rows + a.w13_touch_rows * min(items, nw / 2) / nw;
           const int x = b & 7;
           const int cx = items > x ? (items - x + 7) / 8 : 0;  // attention workgroups
           const int h = (b - x) / 8 - cx, nh = (nw - x + 7) / 8 - cx;
@@ -1289,7 +1591,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
           asm volatile("" ::"v"(t));  // keeps the loads
         }
       }
-      attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds, slot, pre, rope_c, rope_s);
+      if constexpr (SHORT)
+        attn_short_phase<HD>(a, k >> 2, pos, tag, lds, slot);
+      else
+        attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds, slot, pre, rope_c, rope_s);
       ++slot;
       trace_mark(a, slot++);
     }
