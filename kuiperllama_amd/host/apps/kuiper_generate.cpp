@@ -2,7 +2,7 @@
 // (demo/main.cpp:5-47, demo/main_qwen.cpp:198-284 and :404-452) on the
 // MI355X backend, through the C++ host API (model::Model on kDeviceHIP).
 //
-// Prompts and responses are token ids (no tokenizer in this backend):
+// Without a tokenizer, prompts and responses are token ids:
 //
 //   kuiper_generate [options] <model.bin> <ids> [max_new_tokens]
 //       ids: comma- or space-separated prompt token ids.  Prints
@@ -13,16 +13,23 @@
 //       and [PROMPT_END] (token ids) prints one response as above; [EXIT] or
 //       end of input stops.
 //
+// With --tokenizer FILE (a SentencePiece .model for llama2, a tokenizer.json
+// for the other families) the prompt is text, as in the reference demos: the
+// single-shot <ids> argument becomes <prompt>, a served prompt is its lines
+// joined by "\n", and the response is decoded text with the end markers cut
+// and short repeated lines collapsed (main_qwen.cpp:92-148).  The prompt and
+// response ids then go to stderr as [PROMPT_IDS] / [RESPONSE_IDS] lines.
+//
 // Options: --family llama2|llama3|qwen2|qwen3 (default llama2), --quant (int8
 // image), --layered (the layer-by-layer path instead of the fused engine),
 // --prefill (the whole prompt in one batched pass; fused only), --eos ID
-// (end-of-sequence id, repeatable).
+// (end-of-sequence id, repeatable), --tokenizer FILE.
 //
 // Generation follows main_qwen.cpp: prompt positions advance without
 // sampling; in the decode phase only, generation stops at an end-of-sequence
-// id, after 24 identical tokens in a row, or when the last 12 tokens repeat
-// the 12 before them.  (The reference's rule on decoded tail text needs a
-// tokenizer and is not applied.)
+// id (the tokenizer's and --eos ones), after 24 identical tokens in a row,
+// when the last 12 tokens repeat the 12 before them, or, with a tokenizer,
+// when the decoded last 6 tokens hold an end marker.
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -43,6 +50,7 @@ struct Options {
   bool layered = false;
   bool prefill = false;
   std::vector<int32_t> eos;
+  std::string tokenizer;
 };
 
 struct GenerationResult {
@@ -70,6 +78,62 @@ std::vector<int32_t> parse_ids(const std::string& text, bool* ok) {
   return ids;
 }
 
+const char* const kEndMarkers[] = {"<|im_end|>", "<|endoftext|>", "</s>", "<|end|>"};
+
+bool has_end_marker(const std::string& text) {
+  for (const char* mk : kEndMarkers)
+    if (text.find(mk) != std::string::npos) return true;
+  return false;
+}
+
+std::string trim(const std::string& text) {
+  const size_t b = text.find_first_not_of(" \t\r\n");
+  if (b == std::string::npos) return "";
+  const size_t e = text.find_last_not_of(" \t\r\n");
+  return text.substr(b, e - b + 1);
+}
+
+// main_qwen.cpp:92-148: the text before the first end marker (each marker in
+// turn), then runs of one short line cut: the second repeat of a line of at
+// most 32 characters ends the text and drops the first repeat; lines of up to
+// 48 characters are kept at most twice in a row.
+std::string response_text(const std::string& decoded) {
+  std::string text = decoded;
+  for (const char* mk : kEndMarkers) {
+    const size_t at = text.find(mk);
+    if (at != std::string::npos) text = text.substr(0, at);
+  }
+  text = trim(text);
+  std::istringstream in(text);
+  std::string line, prev;
+  std::vector<std::string> kept;
+  int run = 0;
+  while (std::getline(in, line)) {
+    const std::string norm = trim(line);
+    if (!norm.empty() && norm == prev && norm.size() <= 48) {
+      ++run;
+      if (run >= 2 && norm.size() <= 32) {
+        if (!kept.empty() && trim(kept.back()) == norm) kept.pop_back();
+        break;
+      }
+      if (run >= 3) continue;
+    } else {
+      prev = norm;
+      run = 1;
+    }
+    kept.push_back(line);
+  }
+  std::string out;
+  for (size_t i = 0; i < kept.size(); ++i) out += (i ? "\n" : "") + kept[i];
+  return trim(out);
+}
+
+std::string join_ids(const std::vector<int32_t>& ids) {
+  std::string out;
+  for (size_t i = 0; i < ids.size(); ++i) out += (i ? " " : "") + std::to_string(ids[i]);
+  return out;
+}
+
 // main_qwen.cpp:198-284 with token ids.
 // Why a prompt cannot run on the model ("" when it can): ids outside
 // [0, vocab) or more positions than the model's sequence length.
@@ -87,7 +151,7 @@ std::string prompt_error(const model::Model& m, const std::vector<int32_t>& prom
 }
 
 GenerationResult generate(const model::Model& m, const std::vector<int32_t>& prompt, int max_new,
-                          bool use_prefill) {
+                          bool use_prefill, bool has_tokenizer) {
   GenerationResult r;
   const int32_t P = static_cast<int32_t>(prompt.size());
   const int32_t total_steps =
@@ -141,6 +205,11 @@ GenerationResult generate(const model::Model& m, const std::vector<int32_t>& pro
       same_run = 1;
     }
     if (same_run >= 24) break;
+    // 2) an end marker in the decoded last 6 tokens (with a tokenizer)
+    if (has_tokenizer && words.size() > static_cast<size_t>(P + 6)) {
+      const std::string tail = m.decode(std::vector<int32_t>(words.end() - 6, words.end()));
+      if (has_end_marker(tail)) break;
+    }
     // 3) the last 12 tokens repeat the 12 before them
     constexpr int kRepeatWindow = 12;
     if (words.size() >= static_cast<size_t>(P + kRepeatWindow * 2)) {
@@ -157,13 +226,19 @@ GenerationResult generate(const model::Model& m, const std::vector<int32_t>& pro
   return r;
 }
 
-// main_qwen.cpp:378-387
-void print_result(const GenerationResult& r, double duration_sec, bool print_stats) {
+// main_qwen.cpp:378-387.  With a tokenizer the response is text and the ids
+// go to stderr.
+void print_result(const model::Model& m, const GenerationResult& r, double duration_sec,
+                  bool print_stats, bool has_tokenizer) {
   const double sps = duration_sec > 0 ? static_cast<double>(r.steps) / duration_sec : 0.0;
-  std::printf("[RESPONSE_START]\n");
-  for (size_t i = 0; i < r.response.size(); ++i)
-    std::printf("%s%d", i ? " " : "", r.response[i]);
-  std::printf("\n[RESPONSE_END]\n");
+  if (has_tokenizer) {
+    const std::string text = r.response.empty() ? "" : response_text(m.decode(r.response));
+    std::printf("[RESPONSE_START]\n%s\n[RESPONSE_END]\n", text.c_str());
+    std::fprintf(stderr, "[RESPONSE_IDS] %s\n", join_ids(r.response).c_str());
+    std::fflush(stderr);
+  } else {
+    std::printf("[RESPONSE_START]\n%s\n[RESPONSE_END]\n", join_ids(r.response).c_str());
+  }
   std::fflush(stdout);
   if (print_stats) {
     std::fprintf(stderr, "[STATS] steps=%d duration=%.6f steps_per_s=%.6f\n", r.steps,
@@ -176,14 +251,20 @@ std::unique_ptr<model::Model> load(const std::string& path, const Options& o) {
   std::unique_ptr<model::Model> m;
   switch (o.family) {
     case model::ModelFamily::kQwen2:
-      m = std::make_unique<model::Qwen2Model>(base::TokenizerType::kEncodeBpe, "", path, o.quant);
+      m = std::make_unique<model::Qwen2Model>(base::TokenizerType::kEncodeBpe, o.tokenizer, path,
+                                              o.quant);
       break;
     case model::ModelFamily::kQwen3:
-      m = std::make_unique<model::Qwen3Model>(base::TokenizerType::kEncodeBpe, "", path, o.quant);
+      m = std::make_unique<model::Qwen3Model>(base::TokenizerType::kEncodeBpe, o.tokenizer, path,
+                                              o.quant);
+      break;
+    case model::ModelFamily::kLlama3:
+      m = std::make_unique<model::LLama2Model>(base::TokenizerType::kEncodeBpe, o.tokenizer, path,
+                                               o.quant, o.family);
       break;
     default:
-      m = std::make_unique<model::LLama2Model>(base::TokenizerType::kEncodeSpe, "", path, o.quant,
-                                               o.family);
+      m = std::make_unique<model::LLama2Model>(base::TokenizerType::kEncodeSpe, o.tokenizer, path,
+                                               o.quant, o.family);
   }
   const base::Status s = m->init(base::DeviceType::kDeviceHIP);
   if (!s) {
@@ -197,10 +278,10 @@ std::unique_ptr<model::Model> load(const std::string& path, const Options& o) {
 
 int usage(const char* prog) {
   std::fprintf(stderr,
-               "Usage:\n  %s [options] <model.bin> <ids> [max_new_tokens]\n"
+               "Usage:\n  %s [options] <model.bin> <ids|prompt> [max_new_tokens]\n"
                "  %s --serve [options] <model.bin> [max_new_tokens]\n"
                "Options: --family llama2|llama3|qwen2|qwen3, --quant, --layered, --prefill, "
-               "--eos ID\n",
+               "--eos ID, --tokenizer FILE (prompts and responses as text)\n",
                prog, prog);
   return 2;
 }
@@ -228,6 +309,9 @@ int main(int argc, char** argv) {
       o.prefill = true;
     } else if (a == "--eos" && i + 1 < argc) {
       o.eos.push_back(std::atoi(argv[++i]));
+    } else if (a == "--tokenizer" && i + 1 < argc) {
+      o.tokenizer = argv[++i];
+      if (o.tokenizer.empty()) return usage(argv[0]);
     } else if (a == "--family" && i + 1 < argc) {
       const std::string f = argv[++i];
       if (f == "llama2") o.family = model::ModelFamily::kLlama2;
@@ -251,27 +335,40 @@ int main(int argc, char** argv) {
     auto m = load(pos_args[0], o);
     if (!m) return 1;
     if (o.prefill) STATUS_CHECK(m->set_prefill(true));
+    const bool tok = !o.tokenizer.empty();
     std::cout << "[READY]" << std::endl;
     std::string line;
     while (std::getline(std::cin, line)) {
       if (line == "[EXIT]") break;
       if (line != "[PROMPT_START]") continue;
       std::string text;
-      bool has_end = false;
+      bool has_end = false, first = true;
       while (std::getline(std::cin, line)) {
         if (line == "[PROMPT_END]") {
           has_end = true;
           break;
         }
-        text += " " + line;
+        // Text prompts keep their line breaks (main_qwen.cpp:430-436).
+        text += (tok ? (first ? "" : "\n") : " ") + line;
+        first = false;
       }
       if (!has_end) break;
-      bool ok = false;
-      const std::vector<int32_t> prompt = parse_ids(text, &ok);
-      if (!ok || prompt.empty()) {
-        std::printf("[ERROR] the prompt must be token ids\n");
-        std::fflush(stdout);
-        continue;
+      std::vector<int32_t> prompt;
+      if (tok) {
+        prompt = m->encode(text);
+        std::fprintf(stderr, "[PROMPT_IDS] %s\n", join_ids(prompt).c_str());
+        if (prompt.empty()) {  // main_qwen.cpp:158-160: an empty response
+          print_result(*m, GenerationResult{}, 0.0, false, tok);
+          continue;
+        }
+      } else {
+        bool ok = false;
+        prompt = parse_ids(text, &ok);
+        if (!ok || prompt.empty()) {
+          std::printf("[ERROR] the prompt must be token ids\n");
+          std::fflush(stdout);
+          continue;
+        }
       }
       // A bad request gets an error line; it must not reach the model, whose
       // failed checks end the process.
@@ -282,23 +379,35 @@ int main(int argc, char** argv) {
         continue;
       }
       const auto t0 = std::chrono::steady_clock::now();
-      const GenerationResult r = generate(*m, prompt, max_steps, o.prefill);
+      const GenerationResult r = generate(*m, prompt, max_steps, o.prefill, tok);
       const double dt =
           std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-      print_result(r, dt, false);
+      print_result(*m, r, dt, false, tok);
     }
     return 0;
   }
   if (pos_args.size() < 2 || pos_args.size() > 3) return usage(argv[0]);
-  bool ok = false;
-  const std::vector<int32_t> prompt = parse_ids(pos_args[1], &ok);
-  if (!ok || prompt.empty()) {
-    std::fprintf(stderr, "kuiper_generate: the prompt must be token ids\n");
-    return 2;
+  const bool tok = !o.tokenizer.empty();
+  std::vector<int32_t> prompt;
+  if (!tok) {
+    bool ok = false;
+    prompt = parse_ids(pos_args[1], &ok);
+    if (!ok || prompt.empty()) {
+      std::fprintf(stderr, "kuiper_generate: the prompt must be token ids\n");
+      return 2;
+    }
   }
   const int max_steps = pos_args.size() == 3 ? parse_max(pos_args[2].c_str()) : 128;
   auto m = load(pos_args[0], o);
   if (!m) return 1;
+  if (tok) {
+    prompt = m->encode(pos_args[1]);
+    std::fprintf(stderr, "[PROMPT_IDS] %s\n", join_ids(prompt).c_str());
+    if (prompt.empty()) {  // main_qwen.cpp:158-160: an empty response
+      print_result(*m, GenerationResult{}, 0.0, true, tok);
+      return 0;
+    }
+  }
   const std::string why = prompt_error(*m, prompt);
   if (!why.empty()) {
     std::fprintf(stderr, "kuiper_generate: %s\n", why.c_str());
@@ -306,8 +415,8 @@ int main(int argc, char** argv) {
   }
   if (o.prefill) STATUS_CHECK(m->set_prefill(true));
   const auto t0 = std::chrono::steady_clock::now();
-  const GenerationResult r = generate(*m, prompt, max_steps, o.prefill);
+  const GenerationResult r = generate(*m, prompt, max_steps, o.prefill, tok);
   const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-  print_result(r, dt, true);
+  print_result(*m, r, dt, true, tok);
   return 0;
 }

@@ -9,8 +9,11 @@
 // Differences from the reference, by design:
 //  * the model family (RoPE pairing and theta, RMSNorm eps, Qwen2 bias, Qwen3
 //    q/k norm, header size) is a constructor argument instead of a build flag;
-//  * the tokenizer is optional: prompts are token ids (encode/decode report
-//    that no tokenizer is loaded);
+//  * the tokenizer is optional: with an empty token_path prompts are token
+//    ids (encode/decode report that no tokenizer is loaded); with one, the
+//    family picks the layer (SentencePiece for kEncodeSpe; byte-level BPE
+//    with the Qwen special tokens for the Qwen families, the Llama-3 ones
+//    otherwise) and the model's vocabulary size stays the image's;
 //  * kDeviceCPU is refused: the CPU kernels are the reference's own.
 #pragma once
 #include <map>
@@ -18,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "kuiper/encode.h"
 #include "kuiper/hip_config.h"
 #include "kuiper/kernels.h"
 #include "kuiper/layer.h"
@@ -137,13 +141,14 @@ class Model {
   // position prompt.size().  generate() uses it when set_prefill(true).
   base::Status prefill(const std::vector<int32_t>& prompt, int& next) const;
   base::Status set_prefill(bool enable);
-  // End-of-sequence ids for is_sentence_ending() (the tokenizer's EOS in the
-  // reference, encode.cpp; here given explicitly since prompts are ids).
+  // More end-of-sequence ids for is_sentence_ending(), besides the
+  // tokenizer's (encode.cpp); the only ones when no tokenizer is loaded.
   void set_eos_tokens(std::vector<int32_t> ids) { eos_tokens_ = std::move(ids); }
   std::shared_ptr<kernel::HipConfig> hip_config() const { return hip_config_; }
 
  protected:
   base::Status insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor);
+  base::Status create_encode_layer();
   base::Status read_model_file();
   base::Status generate_model_infos(const ModelConfig& config, int32_t extra);
   base::Status create_layers();
@@ -175,6 +180,7 @@ class Model {
   bool fused_ = false;
   bool prefill_ = false;
   std::vector<int32_t> eos_tokens_;
+  std::unique_ptr<op::EncodeLayerBase> encode_layer_;
   kl_engine* engine_ = nullptr;
 };
 

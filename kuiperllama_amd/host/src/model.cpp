@@ -70,7 +70,7 @@ Model::~Model() {
 }
 
 // llama3.cpp:111-145 for kDeviceHIP.  The tokenizer is optional (token ids in
-// and out), so an empty token_path is accepted.
+// and out), so an empty token_path is accepted; a given one must load.
 base::Status Model::init(base::DeviceType device_type) {
   if (device_type != base::DeviceType::kDeviceHIP)
     return base::error::InvalidArgument(
@@ -82,6 +82,10 @@ base::Status Model::init(base::DeviceType device_type) {
   // image is reported without touching the GPU.
   base::Status s = read_model_file();
   if (!s) return s;
+  if (!token_path_.empty()) {
+    s = create_encode_layer();
+    if (!s) return s;
+  }
   s = create_layers();
   if (!s) return s;
   if (kl_set_device(0) != KL_OK) return base::error::InternalError("kl_set_device(0) failed.");
@@ -699,14 +703,47 @@ base::Status Model::prefill(const std::vector<int32_t>& prompt, int& next) const
   return base::error::Success();
 }
 
+// model.cpp:143-173, the layer chosen by tokenizer type and model family
+// rather than build flags.  Unlike the reference, the vocabulary size stays
+// the image's (Qwen tokenizers hold fewer ids than the embedding has rows);
+// a tokenizer with more ids than the model is refused.
+base::Status Model::create_encode_layer() {
+  if (tokenizer_type_ == base::TokenizerType::kEncodeSpe) {
+    encode_layer_ = std::make_unique<op::SpeEncodeLayer>(token_path_, true, false);
+  } else if (tokenizer_type_ == base::TokenizerType::kEncodeBpe) {
+    if (family_ == ModelFamily::kQwen2 || family_ == ModelFamily::kQwen3)
+      encode_layer_ = std::make_unique<op::QwenEncodeLayer>(token_path_, false, false);
+    else
+      encode_layer_ = std::make_unique<op::BpeEncodeLayer>(token_path_, true, false);
+  } else {
+    return base::error::InvalidArgument("A tokenizer file was given without a tokenizer type.");
+  }
+  base::Status s = encode_layer_->init();
+  if (!s) {
+    encode_layer_.reset();
+    return s;
+  }
+  if (encode_layer_->vocab_size() <= 0 || encode_layer_->vocab_size() > config_->vocab_size_) {
+    encode_layer_.reset();
+    return base::error::ModelParseError("The tokenizer's vocabulary does not fit the model's.");
+  }
+  return base::error::Success();
+}
+
 bool Model::is_sentence_ending(int32_t token_idx) const {
+  if (encode_layer_ && encode_layer_->is_sentence_ending(token_idx)) return true;
   for (int32_t e : eos_tokens_)
     if (e == token_idx) return true;
   return false;
 }
-std::string Model::decode(int32_t) const { return std::string(); }
-std::string Model::decode(std::vector<int32_t>) const { return std::string(); }
-std::vector<int32_t> Model::encode(const std::string&) const {
+std::string Model::decode(int32_t token_idx) const {
+  return encode_layer_ ? encode_layer_->decode(token_idx) : std::string();
+}
+std::string Model::decode(std::vector<int32_t> token_idxs) const {
+  return encode_layer_ ? encode_layer_->decode(token_idxs) : std::string();
+}
+std::vector<int32_t> Model::encode(const std::string& sentence) const {
+  if (encode_layer_) return encode_layer_->encode(sentence);
   std::fprintf(stderr, "kuiper: no tokenizer is loaded; pass token ids\n");
   return {};
 }

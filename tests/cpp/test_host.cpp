@@ -14,10 +14,13 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
+#include <memory>
 #include <functional>
 #include <string>
 #include <vector>
 
+#include "kuiper/encode.h"
 #include "kuiper/kernels.h"
 #include "kuiper/layer.h"
 #include "kuiper/model.h"
@@ -562,10 +565,51 @@ int run_model(int argc, char** argv) {
 
 }  // namespace
 
+// tok <spe|bpe|qwen> <tokenizer file> <cases file>: the tokenizer layers
+// (op::SpeEncodeLayer / BpeEncodeLayer / QwenEncodeLayer) on the cases, one
+// per line as hex-encoded UTF-8 ("-" = empty).  Prints a "meta" line, then
+// per case "ids <ids...>" and "dec <hex of decode(ids)>".
+static std::string hex_to_bytes(const std::string& h) {
+  std::string out;
+  if (h == "-") return out;
+  for (size_t i = 0; i + 1 < h.size(); i += 2) out += static_cast<char>(std::stoi(h.substr(i, 2), nullptr, 16));
+  return out;
+}
+
+static int run_tok(int argc, char** argv) {
+  if (argc < 5) {
+    std::fprintf(stderr, "usage: test_host tok <spe|bpe|qwen> <tokenizer> <cases>\n");
+    return 2;
+  }
+  const std::string kind = argv[2];
+  std::unique_ptr<op::EncodeLayerBase> layer;
+  if (kind == "spe") layer = std::make_unique<op::SpeEncodeLayer>(argv[3], true, false);
+  else if (kind == "bpe") layer = std::make_unique<op::BpeEncodeLayer>(argv[3], true, false);
+  else layer = std::make_unique<op::QwenEncodeLayer>(argv[3], false, false);
+  const base::Status st = layer->init();
+  std::printf("meta init %d vocab %d\n", static_cast<int>(st), layer->vocab_size());
+  if (!st) {
+    std::printf("error %s\n", st.get_err_msg().c_str());
+    return 1;
+  }
+  std::ifstream f(argv[4]);
+  std::string line;
+  while (std::getline(f, line)) {
+    const std::vector<int32_t> ids = layer->encode(hex_to_bytes(line));
+    std::printf("ids");
+    for (int32_t id : ids) std::printf(" %d", id);
+    std::printf("\ndec ");
+    for (unsigned char ch : layer->decode(ids)) std::printf("%02x", ch);
+    std::printf("\nend %d\n", ids.empty() ? 0 : static_cast<int>(layer->is_sentence_ending(ids.back())));
+  }
+  return 0;
+}
+
 int main(int argc, char** argv) {
   const std::string mode = argc > 1 ? argv[1] : "unit";
   if (mode == "unit") return run_units(argc > 2 ? argv[2] : "");
   if (mode == "model") return run_model(argc, argv);
+  if (mode == "tok") return run_tok(argc, argv);
   std::fprintf(stderr, "unknown mode %s\n", mode.c_str());
   return 2;
 }

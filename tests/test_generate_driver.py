@@ -114,3 +114,145 @@ def test_serve_protocol(K, O, gpu, images):
     errors = [l for l in p.stdout.splitlines() if l.startswith("[ERROR]")]
     assert len(errors) == 3, errors
     assert "outside [0, " in errors[1] and "positions" in errors[2]
+
+
+# ------------------------------------------------------------- text prompts ----
+TOK = os.path.join(ROOT, "tests", "golden", "tok")
+TOKFILE = {"llama2": "sp_bpe.model", "llama3": "bpe_llama3.json", "qwen2": "bpe_qwen.json",
+           "qwen3": "bpe_qwen.json"}
+MARKERS = ["<|im_end|>", "<|endoftext|>", "</s>", "<|end|>"]
+
+
+def response_text(decoded):
+    """main_qwen.cpp:92-148 (remove_end_markers, collapse_repeated_lines)."""
+    strip = lambda t: t.strip(" \t\r\n")  # noqa: E731
+    for mk in MARKERS:
+        if mk in decoded:
+            decoded = decoded[:decoded.index(mk)]
+    kept, prev, run = [], "", 0
+    for line in strip(decoded).split("\n"):
+        norm = strip(line)
+        if norm and norm == prev and len(norm) <= 48:
+            run += 1
+            if run >= 2 and len(norm) <= 32:
+                if kept and strip(kept[-1]) == norm:
+                    kept.pop()
+                break
+            if run >= 3:
+                continue
+        else:
+            prev, run = norm, 1
+        kept.append(line)
+    return strip("\n".join(kept))
+
+
+def test_response_text_rules():
+    """The restated post-processing on hand-made cases."""
+    assert response_text("  hi <|im_end|> junk") == "hi"
+    assert response_text("a</s>b<|endoftext|>c") == "a"
+    assert response_text("x\nab\nab\nab\ny") == "x"                 # short line repeated twice more
+    long = "l" * 40
+    assert response_text(f"{long}\n{long}\n{long}\n{long}\nz") == f"{long}\n{long}\nz"
+    assert response_text("\n\n") == ""
+
+
+def tokenizer_for(family):
+    """(oracle encode, oracle decode, stop ids) for the family's fixture tokenizer."""
+    path = os.path.join(TOK, TOKFILE[family])
+    if family == "llama2":
+        spm = pytest.importorskip("sentencepiece")
+        sp = spm.SentencePieceProcessor(model_file=path)
+        return (lambda s: [sp.bos_id()] + sp.encode(s, out_type=int)), sp.decode, {sp.eos_id()}
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import tokenizer as T
+    bt = T.BpeTokenizer(path, qwen=family.startswith("qwen"))
+    return bt.encode, bt.decode, {bt.eos, bt.stop2}
+
+
+def ids_line(stderr, tag):
+    line = next(l for l in stderr.splitlines() if l.startswith(tag))
+    return [int(t) for t in line[len(tag):].split()]
+
+
+def test_tokenizer_errors_before_the_gpu(K, tmp_path):
+    """A missing tokenizer file, or one with more ids than the model's
+    vocabulary, fails init() before any GPU call."""
+    cfg = K.TINY["tiny_qwen3"]            # vocab 640 < the fixture's 903 ids
+    p = str(tmp_path / "q3.bin")
+    K.synth_image(cfg).tofile(p)
+    r = run(["--family", "qwen3", "--tokenizer", str(tmp_path / "missing.json"), p, "hi"])
+    assert r.returncode == 1 and "init failed" in r.stderr, r.stderr
+    r = run(["--family", "qwen3", "--tokenizer", os.path.join(TOK, TOKFILE["qwen3"]), p, "hi"])
+    assert r.returncode == 1 and "vocabulary" in r.stderr, r.stderr
+
+
+@pytest.fixture(scope="module")
+def text_images(K, tmp_path_factory):
+    """Tiny images whose vocabularies hold the fixture tokenizers' ids."""
+    d = tmp_path_factory.mktemp("gentext")
+    out = {}
+    for fam, name in (("llama2", "tiny_llama2"), ("llama3", "tiny_llama3"), ("qwen2", "tiny_qwen2")):
+        cfg = K.TINY[name].with_(vocab=1000, seq_len=128)
+        p = str(d / f"{name}_v1000.bin")
+        K.synth_image(cfg).tofile(p)
+        out[fam] = (cfg, p)
+    return out
+
+
+def expected(O, cfg, path, prompt, max_new, stops):
+    import numpy as np
+    ids = [int(t) for t in O.Model(np.fromfile(path, np.uint8), cfg.family, cfg.quant)
+           .generate(prompt, max_new + 1)]
+    for i, t in enumerate(ids):
+        if t in stops:
+            return ids[:i]
+    return ids
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("family,flags", [("llama2", []), ("llama3", ["--prefill"]),
+                                          ("qwen2", ["--layered"])])
+def test_text_prompt_single_shot(O, gpu, text_images, family, flags):
+    cfg, path = text_images[family]
+    enc, dec, stops = tokenizer_for(family)
+    text = "The quick brown fox's 42 jumps\tover the lazy dog."
+    max_new = 9
+    p = run(["--family", family, "--tokenizer", os.path.join(TOK, TOKFILE[family])] + flags +
+            [path, text, str(max_new)])
+    assert p.returncode == 0, p.stderr
+    prompt = ids_line(p.stderr, "[PROMPT_IDS]")
+    assert prompt == enc(text)
+    got = ids_line(p.stderr, "[RESPONSE_IDS]")
+    want = expected(O, cfg, path, prompt, max_new, stops)
+    print(family, flags, prompt, got, flush=True)
+    # Within 10 tokens only an end marker in the decoded tail could stop
+    # earlier; the fixture vocabularies decode no token to one.
+    assert got == want
+    body = p.stdout.split("[RESPONSE_START]\n")[1].split("\n[RESPONSE_END]")[0]
+    assert body == response_text(dec(got))
+
+
+@pytest.mark.gpu
+def test_text_serve_protocol(O, gpu, text_images):
+    cfg, path = text_images["qwen2"]
+    enc, dec, stops = tokenizer_for("qwen2")
+    prompts = ["<|im_start|>user\nHello there, how are you?<|im_end|>\n<|im_start|>assistant\n",
+               "",
+               "single line"]
+    stdin = "".join("[PROMPT_START]\n" + t + "\n[PROMPT_END]\n" for t in prompts) + "[EXIT]\n"
+    p = run(["--serve", "--family", "qwen2", "--tokenizer", os.path.join(TOK, TOKFILE["qwen2"]),
+             path, "6"], stdin=stdin)
+    assert p.returncode == 0, p.stderr
+    blocks = [b.split("[RESPONSE_END]")[0] for b in p.stdout.split("[RESPONSE_START]\n")[1:]]
+    assert len(blocks) == 3
+    got_prompts = [[int(t) for t in l.split()[1:]] for l in p.stderr.splitlines()
+                   if l.startswith("[PROMPT_IDS]")]
+    got_resp = [[int(t) for t in l.split()[1:]] for l in p.stderr.splitlines()
+                if l.startswith("[RESPONSE_IDS]")]
+    assert got_prompts == [enc(t) for t in prompts]
+    assert got_prompts[1] == [] and blocks[1] == "\n"   # an empty prompt: an empty response
+    for k in (0, 2):
+        want = expected(O, cfg, path, got_prompts[k], 6, stops)
+        assert got_resp[k] == want
+        assert blocks[k] == response_text(dec(want)) + "\n"
