@@ -19,7 +19,9 @@ namespace {
 
 // ---------------------------------------------------------------- UTF-8 ---
 // Decodes the code point at s[i] and advances i; a byte that does not start a
-// valid sequence decodes as itself (one "character" of one byte).
+// valid sequence (a stray continuation byte, a truncated or overlong form, a
+// surrogate or a value above U+10FFFF) decodes as itself, one "character" of
+// one byte.
 uint32_t utf8_next(const std::string& s, size_t& i) {
   const unsigned char c = static_cast<unsigned char>(s[i]);
   int len = c < 0x80 ? 1 : (c >> 5) == 0x6 ? 2 : (c >> 4) == 0xE ? 3 : (c >> 3) == 0x1E ? 4 : 0;
@@ -35,6 +37,11 @@ uint32_t utf8_next(const std::string& s, size_t& i) {
       return c;
     }
     cp = (cp << 6) | (d & 0x3F);
+  }
+  static const uint32_t kMin[5] = {0, 0, 0x80, 0x800, 0x10000};
+  if (cp < kMin[len] || cp > 0x10FFFF || (cp >= 0xD800 && cp <= 0xDFFF)) {
+    ++i;
+    return c;
   }
   i += len;
   return cp;

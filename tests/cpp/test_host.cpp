@@ -17,6 +17,7 @@
 #include <fstream>
 #include <memory>
 #include <functional>
+#include <sstream>
 #include <string>
 #include <vector>
 
@@ -568,7 +569,8 @@ int run_model(int argc, char** argv) {
 // tok <spe|bpe|qwen> <tokenizer file> <cases file>: the tokenizer layers
 // (op::SpeEncodeLayer / BpeEncodeLayer / QwenEncodeLayer) on the cases, one
 // per line as hex-encoded UTF-8 ("-" = empty).  Prints a "meta" line, then
-// per case "ids <ids...>" and "dec <hex of decode(ids)>".
+// per case "ids <ids...>", "dec <hex of decode(ids)>" and "end <0|1>"; a line
+// "#<ids...>" is decoded only and prints "only <hex of decode(ids)>".
 static std::string hex_to_bytes(const std::string& h) {
   std::string out;
   if (h == "-") return out;
@@ -595,6 +597,15 @@ static int run_tok(int argc, char** argv) {
   std::ifstream f(argv[4]);
   std::string line;
   while (std::getline(f, line)) {
+    if (!line.empty() && line[0] == '#') {  // "#id id ...": decode only
+      std::vector<int32_t> ids;
+      std::istringstream in(line.substr(1));
+      for (int32_t id; in >> id;) ids.push_back(id);
+      std::printf("only ");
+      for (unsigned char ch : layer->decode(ids)) std::printf("%02x", ch);
+      std::printf("\n");
+      continue;
+    }
     const std::vector<int32_t> ids = layer->encode(hex_to_bytes(line));
     std::printf("ids");
     for (int32_t id : ids) std::printf(" %d", id);

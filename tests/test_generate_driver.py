@@ -16,8 +16,10 @@ FAMILY = {0: "llama2", 1: "llama3", 2: "qwen2", 3: "qwen3"}
 def run(args, stdin=None, timeout=120):
     if not os.path.exists(BIN):
         pytest.fail(f"{BIN} is not built (run __graft_entry__.build())")
-    return subprocess.run([BIN] + args, input=stdin, capture_output=True, text=True,
-                          timeout=timeout)
+    # Decoded responses may end inside a UTF-8 sequence: undecodable bytes
+    # read as U+FFFD, as the test oracle's decode() reads them.
+    return subprocess.run([BIN] + args, input=stdin, capture_output=True, encoding="utf-8",
+                          errors="replace", timeout=timeout)
 
 
 def response(stdout):
@@ -189,12 +191,14 @@ def test_tokenizer_errors_before_the_gpu(K, tmp_path):
 
 @pytest.fixture(scope="module")
 def text_images(K, tmp_path_factory):
-    """Tiny images whose vocabularies hold the fixture tokenizers' ids."""
+    """Tiny images with the fixture tokenizers' vocabulary sizes, so that
+    every generated id decodes."""
     d = tmp_path_factory.mktemp("gentext")
     out = {}
-    for fam, name in (("llama2", "tiny_llama2"), ("llama3", "tiny_llama3"), ("qwen2", "tiny_qwen2")):
-        cfg = K.TINY[name].with_(vocab=1000, seq_len=128)
-        p = str(d / f"{name}_v1000.bin")
+    for fam, name, vocab in (("llama2", "tiny_llama2", 700), ("llama3", "tiny_llama3", 903),
+                             ("qwen2", "tiny_qwen2", 903)):
+        cfg = K.TINY[name].with_(vocab=vocab, seq_len=128)
+        p = str(d / f"{name}_v{vocab}.bin")
         K.synth_image(cfg).tofile(p)
         out[fam] = (cfg, p)
     return out

@@ -181,3 +181,32 @@ def test_oracle_matches_hf_bpe_without_spaces():
     # tiktoken merges by the rank of the joined bytes, HF by merge order; on
     # this HF-trained vocabulary they coincide on every word.
     assert agree == len(words), agree
+
+
+def test_spe_decodes_invalid_byte_runs_like_sentencepiece(tmp_path):
+    """Byte pieces that do not form valid UTF-8 (overlong forms, surrogates,
+    values above U+10FFFF, stray continuation bytes, truncated sequences)
+    decode to U+FFFD per byte, as the sentencepiece library does; valid runs
+    decode to their character."""
+    spm = pytest.importorskip("sentencepiece")
+    sp = spm.SentencePieceProcessor(model_file=os.path.join(TOK, FILES["spe"]))
+    byte_id = {sp.id_to_piece(i): i for i in range(sp.get_piece_size()) if sp.is_byte(i)}
+    lead = next(i for i in range(sp.get_piece_size())
+                if sp.id_to_piece(i).startswith("▁") and len(sp.id_to_piece(i)) > 2)
+    runs = [b"\xc1\x80", b"\xc0\xaf", b"\xe0\x80\x80", b"\xed\xa0\x80", b"\xf4\x90\x80\x80",
+            b"\xf5\x80\x80\x80", b"\x80", b"\xe6\x97", b"\xe6\x97\xa5", b"\xf0\x9f\x98\x80",
+            b"\xc3\xa9\x80\xc3", b"\xef\xbf\xbf", b"\xf0\x90\x80\x80"]
+    cases = []
+    for r in runs:
+        ids = [byte_id[f"<0x{b:02X}>"] for b in r]
+        cases.append(ids)
+        cases.append([lead] + ids + [sp.piece_to_id("a")])
+    f = tmp_path / "dec.txt"
+    f.write_text("".join("#" + " ".join(map(str, ids)) + "\n" for ids in cases))
+    p = subprocess.run([BIN, "tok", "spe", os.path.join(TOK, FILES["spe"]), str(f)],
+                       capture_output=True, text=True, timeout=60)
+    assert p.returncode == 0, p.stdout + p.stderr
+    got = [bytes.fromhex(ln[5:]).decode("utf-8") for ln in p.stdout.splitlines() if ln.startswith("only")]
+    assert len(got) == len(cases)
+    for ids, g in zip(cases, got):
+        assert g == sp.decode(ids), (ids, g, sp.decode(ids))
