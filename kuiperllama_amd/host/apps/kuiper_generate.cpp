@@ -17,7 +17,7 @@
 // for the other families) the prompt is text, as in the reference demos: the
 // single-shot <ids> argument becomes <prompt>, a served prompt is its lines
 // joined by "\n", and the response is decoded text with the end markers cut
-// and short repeated lines collapsed (main_qwen.cpp:92-148).  The prompt and
+// and short repeated lines collapsed (main_qwen.cpp:94-148).  The prompt and
 // response ids then go to stderr as [PROMPT_IDS] / [RESPONSE_IDS] lines.
 //
 // Options: --family llama2|llama3|qwen2|qwen3 (default llama2), --quant (int8
@@ -93,7 +93,7 @@ std::string trim(const std::string& text) {
   return text.substr(b, e - b + 1);
 }
 
-// main_qwen.cpp:92-148: the text before the first end marker (each marker in
+// main_qwen.cpp:94-148: the text before the first end marker (each marker in
 // turn), then runs of one short line cut: the second repeat of a line of at
 // most 32 characters ends the text and drops the first repeat; lines of up to
 // 48 characters are kept at most twice in a row.
@@ -348,7 +348,7 @@ int main(int argc, char** argv) {
           has_end = true;
           break;
         }
-        // Text prompts keep their line breaks (main_qwen.cpp:430-436).
+        // Text prompts keep their line breaks (main_qwen.cpp:423-435).
         text += (tok ? (first ? "" : "\n") : " ") + line;
         first = false;
       }
@@ -357,7 +357,7 @@ int main(int argc, char** argv) {
       if (tok) {
         prompt = m->encode(text);
         std::fprintf(stderr, "[PROMPT_IDS] %s\n", join_ids(prompt).c_str());
-        if (prompt.empty()) {  // main_qwen.cpp:158-160: an empty response
+        if (prompt.empty()) {  // main_qwen.cpp:153-155: an empty response
           print_result(*m, GenerationResult{}, 0.0, false, tok);
           continue;
         }
@@ -403,7 +403,7 @@ int main(int argc, char** argv) {
   if (tok) {
     prompt = m->encode(pos_args[1]);
     std::fprintf(stderr, "[PROMPT_IDS] %s\n", join_ids(prompt).c_str());
-    if (prompt.empty()) {  // main_qwen.cpp:158-160: an empty response
+    if (prompt.empty()) {  // main_qwen.cpp:153-155: an empty response
       print_result(*m, GenerationResult{}, 0.0, true, tok);
       return 0;
     }

@@ -13,13 +13,18 @@
 //    "vocab" and "added_tokens") and encode as the reference's tiktoken path:
 //    the byte-level vocabulary mapped back to raw bytes, a token's id is its
 //    merge rank, special tokens matched anywhere, the text between them split
-//    by the reference's pre-tokenizer pattern (encode.cpp:91-92, matched here
+//    by the reference's pre-tokenizer pattern (encode.cpp:61-62, matched here
 //    by hand), each piece looked up whole or byte-pair merged lowest rank
 //    first.  As in the reference, encode() replaces every " " with U+0120
 //    first and decode() maps U+0120 back to " ".
 //
 // A layer that could not load its file reports it from init(); its encode()
-// then returns no ids and decode() an empty string.
+// then returns no ids and decode() an empty string.  Where the reference
+// aborts or throws on bad input, these layers do not: decode() skips ids it
+// does not know, a tokenizer.json whose vocabulary lacks one of the 256 byte
+// tokens is refused at init(), and a special token the layer names (BOS, EOS,
+// second stop token) that the file does not hold gets id -1, where the
+// reference's map lookup would add it with id 0.
 #pragma once
 
 #include <cstdint>
@@ -56,7 +61,7 @@ class EncodeLayerBase : public Layer {
   base::Status status_;
 };
 
-// SentencePiece BPE model (kuiper/source/op/encode.cpp:14-64).
+// SentencePiece BPE model (kuiper/source/op/encode.cpp:14-57).
 class SpeEncodeLayer : public EncodeLayerBase {
  public:
   explicit SpeEncodeLayer(std::string token_model_path, bool has_bos, bool has_eos);
@@ -86,7 +91,7 @@ class SpeEncodeLayer : public EncodeLayerBase {
 };
 
 // Byte-level BPE from a tokenizer.json, Llama-3 special tokens
-// (kuiper/source/op/encode.cpp:96-130).
+// (kuiper/source/op/encode.cpp:64-146).
 class BpeEncodeLayer : public EncodeLayerBase {
  public:
   explicit BpeEncodeLayer(std::string token_model_path, bool has_bos, bool has_eos);
@@ -119,7 +124,7 @@ class BpeEncodeLayer : public EncodeLayerBase {
   std::unordered_map<int32_t, std::string> special_decoder_;
 };
 
-// The same with the Qwen special tokens (kuiper/source/op/encode.cpp:150-182).
+// The same with the Qwen special tokens (kuiper/source/op/encode.cpp:148-182).
 class QwenEncodeLayer : public BpeEncodeLayer {
  public:
   explicit QwenEncodeLayer(std::string token_model_path, bool has_bos, bool has_eos);

@@ -86,7 +86,7 @@ bool is_other(uint32_t cp) { return !is_ws(cp) && !is_letter(cp) && !is_number(c
 
 // ----------------------------------------------------- pre-tokenizer ---
 // End (code point index) of the piece starting at i, for the reference's
-// pattern (encode.cpp:91-92), alternatives in order, leftmost-first:
+// pattern (encode.cpp:61-62), alternatives in order, leftmost-first:
 //   (?i:'s|'t|'re|'ve|'m|'ll|'d) | [^\r\n\p{L}\p{N}]?\p{L}+ | \p{N} |
 //    ?[^\s\p{L}\p{N}]+[\r\n]* | \s*[\r\n]+ | \s+(?:$|[^\S]) | \s+
 // Every code point starts some alternative, so pieces tile the text.
@@ -672,6 +672,17 @@ void BpeEncodeLayer::load(const char* bos, const char* eos, const char* stop2) {
     encoder_[raw] = id;
     decoder_[id] = raw;
   }
+  // Every single byte must have an id: the byte-pair merge falls back to
+  // them (the reference would throw from tiktoken's ranks.at()).
+  for (int b = 0; b < 256; ++b) {
+    if (!encoder_.count(std::string(1, static_cast<char>(b)))) {
+      encoder_.clear();
+      decoder_.clear();
+      status_ = base::error::ModelParseError("the vocabulary of " + token_model_path_ +
+                                             " lacks the byte-level base tokens");
+      return;
+    }
+  }
   std::unordered_map<std::string, int32_t> named;
   if (added && added->kind == JValue::kArray) {
     for (const JValue& t : added->items) {
@@ -759,7 +770,7 @@ std::vector<int32_t> BpeEncodeLayer::encode(const std::string& sentence) const {
   std::vector<int32_t> ids;
   if (!status_) return ids;
   if (has_bos_) ids.push_back(bos_id_);
-  // encode.cpp:136-138: every space becomes U+0120 before the split.
+  // encode.cpp:110-112: every space becomes U+0120 before the split.
   std::string text;
   for (char ch : sentence) {
     if (ch == ' ') text += "\xC4\xA0";
@@ -798,7 +809,7 @@ std::string BpeEncodeLayer::decode(const std::vector<int32_t>& token_ids) const 
     const auto sp = special_decoder_.find(id);
     if (sp != special_decoder_.end()) bytes += sp->second;
   }
-  // encode.cpp:152-156: U+0120 back to a space.
+  // encode.cpp:129-131: U+0120 back to a space.
   std::string out;
   for (size_t i = 0; i < bytes.size(); ++i) {
     if (i + 1 < bytes.size() && bytes[i] == '\xC4' && bytes[i + 1] == '\xA0') {
@@ -811,7 +822,7 @@ std::string BpeEncodeLayer::decode(const std::vector<int32_t>& token_ids) const 
   return out;
 }
 
-// encode.cpp:150: a single id decodes to nothing in the reference's BPE layer.
+// encode.cpp:124: a single id decodes to nothing in the reference's BPE layer.
 std::string BpeEncodeLayer::decode(int32_t token_id) const { return std::string(); }
 
 bool BpeEncodeLayer::is_sentence_ending(int32_t token_id) const {

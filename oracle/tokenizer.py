@@ -1,21 +1,21 @@
 """CPU restatement of the reference's byte-level BPE tokenizers (test
 infrastructure: only tests/ and the fixture script use it).
 
-Follows kuiper/source/op/encode.cpp:96-182 (BpeEncodeLayer, QwenEncodeLayer)
-over kuiper/include/base/tiktoken.h:15-269 (tiktoken's rank-based byte-pair
+Follows kuiper/source/op/encode.cpp:64-182 (BpeEncodeLayer, QwenEncodeLayer)
+over kuiper/include/base/tiktoken.h:17-268 (tiktoken's rank-based byte-pair
 merge) as the reference builds it:
 
 * the vocabulary of a HF tokenizer.json ("model" -> "vocab") is converted
-  from the byte-level alphabet back to raw bytes (encode.cpp:118-128); a
+  from the byte-level alphabet back to raw bytes (encode.cpp:86-98); a
   token's id is its merge rank;
 * "added_tokens" are the special tokens, matched anywhere in the text
   (tiktoken.h:167-187);
 * the text between special tokens is split by the reference's pattern
-  PAT_STR (encode.cpp:91-92), an RE2 pattern: \\s is ASCII whitespace
+  PAT_STR (encode.cpp:61-62), an RE2 pattern: \\s is ASCII whitespace
   [\\t\\n\\f\\r ], \\p{L} / \\p{N} are Unicode letters / numbers; each piece is
-  looked up whole, else byte-pair merged (tiktoken.h:17-106);
+  looked up whole, else byte-pair merged (tiktoken.h:17-108);
 * encode replaces every " " by "\\u0120" first and decode does the reverse
-  (encode.cpp:136-139, :152-156) -- a reference behaviour kept as is;
+  (encode.cpp:110-112, :129-131) -- a reference behaviour kept as is;
 * BOS (Llama-3: <|begin_of_text|>) is prepended when has_bos; Qwen has none.
 
 Parity of the pre-tokenizer: the `regex` module stands in for RE2 (same
@@ -29,7 +29,7 @@ import json
 
 import regex
 
-# encode.cpp:91-92 with RE2's \s spelled out (RE2: \s == [\t\n\f\r ]) and its $ as
+# encode.cpp:61-62 with RE2's \s spelled out (RE2: \s == [\t\n\f\r ]) and its $ as
 # \Z (RE2's $ matches only at the end of the text).
 _WS = r"\t\n\f\r "
 PAT_STR = (r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}|"
@@ -56,12 +56,12 @@ _U2B = {u: b for b, u in bytes_to_unicode().items()}
 
 def _raw(key: str) -> bytes:
     """A vocabulary key in the byte-level alphabet -> its raw bytes
-    (encode.cpp:120-126: unicode_utf8_to_byte per code point)."""
+    (encode.cpp:89-95: unicode_utf8_to_byte per code point)."""
     return bytes(_U2B[c] for c in key)
 
 
 def byte_pair_merge(piece: bytes, ranks: dict[bytes, int]) -> list[int]:
-    """tiktoken.h:17-106: repeatedly merge the adjacent parts whose joined
+    """tiktoken.h:17-108: repeatedly merge the adjacent parts whose joined
     bytes have the lowest rank (the first such pair on ties)."""
     if len(piece) == 1:
         return [ranks[piece]]
@@ -123,7 +123,7 @@ class BpeTokenizer:
         return out
 
     def encode(self, sentence: str) -> list[int]:
-        text = sentence.replace(" ", "Ġ")  # encode.cpp:136-138
+        text = sentence.replace(" ", "Ġ")  # encode.cpp:110-112
         out = []
         pos = 0
         while True:

@@ -4,10 +4,10 @@ container; nothing on the GPU box runs it).
 * sp_bpe.model: a SentencePiece BPE model trained here on a seeded synthetic
   corpus with the options of the Llama-2 tokenizer (identity normalisation,
   dummy prefix, byte fallback, split digits); sentencepiece is the library
-  the reference's SpeEncodeLayer wraps (kuiper/source/op/encode.cpp:14-64).
+  the reference's SpeEncodeLayer wraps (kuiper/source/op/encode.cpp:14-57).
 * bpe_llama3.json / bpe_qwen.json: byte-level BPE tokenizer.json files
   trained here with HF tokenizers, with the Llama-3 and Qwen special tokens
-  (what BpeEncodeLayer / QwenEncodeLayer read, encode.cpp:96-182).
+  (what BpeEncodeLayer / QwenEncodeLayer read, encode.cpp:64-182).
 * tok_cases.json: test sentences and the expected ids / decoded text:
   SentencePiece cases from the sentencepiece library itself (EncodeAsIds
   with BOS, as SpeEncodeLayer::encode; DecodeIds); BPE cases from

@@ -126,7 +126,7 @@ MARKERS = ["<|im_end|>", "<|endoftext|>", "</s>", "<|end|>"]
 
 
 def response_text(decoded):
-    """main_qwen.cpp:92-148 (remove_end_markers, collapse_repeated_lines)."""
+    """main_qwen.cpp:94-148 (remove_end_markers, collapse_repeated_lines)."""
     strip = lambda t: t.strip(" \t\r\n")  # noqa: E731
     for mk in MARKERS:
         if mk in decoded:

@@ -22,6 +22,7 @@ import subprocess
 import sys
 
 import pytest
+import regex
 
 from conftest import ROOT
 
@@ -132,6 +133,12 @@ def test_bad_files_are_reported(tmp_path):
     bad.write_text("{ not json")
     p = subprocess.run([BIN, "tok", "bpe", str(bad), str(cases)], capture_output=True, text=True, timeout=60)
     assert p.returncode == 1 and "meta init 3" in p.stdout, p.stdout
+    # a byte-level vocabulary without all 256 byte tokens
+    nobytes = tmp_path / "nobytes.json"
+    nobytes.write_text(json.dumps({"added_tokens": [], "model": {"vocab": {"a": 0, "b": 1, "ab": 2}}}))
+    p = subprocess.run([BIN, "tok", "qwen", str(nobytes), str(cases)], capture_output=True, text=True,
+                       timeout=60)
+    assert p.returncode == 1 and "meta init 3" in p.stdout and "byte-level" in p.stdout, p.stdout
 
 
 # ----------------------------------------------- pinning the BPE oracle ----
@@ -210,3 +217,24 @@ def test_spe_decodes_invalid_byte_runs_like_sentencepiece(tmp_path):
     assert len(got) == len(cases)
     for ids, g in zip(cases, got):
         assert g == sp.decode(ids), (ids, g, sp.decode(ids))
+
+
+def test_space_replacement_pin(tmp_path):
+    """encode.cpp:110-112 replaces every " " with U+0120 before the split:
+    a text and its replaced twin encode alike (oracle and C++), and since
+    U+0120 is a letter, words joined by spaces form one pre-tokenizer piece.
+    decode() maps U+0120 back to " " (encode.cpp:129-131), so a literal
+    U+0120 in the input also comes back as a space."""
+    bt = T.BpeTokenizer(os.path.join(TOK, FILES["qwen"]), qwen=True)
+    texts = ["hello world", "a b  c", " lead", "tail ", "xĠy z", "it's a 12 test"]
+    twins = [s.replace(" ", "Ġ") for s in texts]
+    for s, t in zip(texts, twins):
+        assert bt.encode(s) == bt.encode(t)
+        assert bt.decode(bt.encode(t)) == s.replace("Ġ", " ")
+    assert regex.findall(T.PAT_STR, "helloĠworld") == ["helloĠworld"]
+    assert regex.findall(T.PAT_STR, "hello world") == ["hello", " world"]
+    _, got = run_cpp("qwen", texts + twins, tmp_path)
+    n = len(texts)
+    for k in range(n):
+        assert got[k][0] == got[n + k][0] == bt.encode(texts[k])
+        assert got[n + k][1] == texts[k].replace("Ġ", " ")
