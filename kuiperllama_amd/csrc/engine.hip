@@ -922,6 +922,11 @@ int setup_persistent(kl_engine* e) {
   if (const char* env = std::getenv("KL_ATTN_SHORT_MAX"))
     a.attn_short_max = std::min(a.attn_short_max, std::max(0, std::atoi(env)));
   a.short_touch_rows = a.w13_touch_rows;
+  // Inputs at least this wide are staged two elements per load (measured:
+  // +1.1-1.3% on Llama-3.2-1B, Llama2-7B int8 and Qwen2.5-1.5B from the
+  // 8192- to 11008-wide W2 inputs; narrower inputs measured slower paired).
+  a.stage_pair_min = 4096;
+  if (const char* env = std::getenv("KL_STAGE_PAIR_MIN")) a.stage_pair_min = std::max(2, std::atoi(env));
   a.kc0 = e->kcache;
   a.vc0 = e->vcache;
   a.kv_layer = static_cast<long long>(m.S) * m.Dkv;

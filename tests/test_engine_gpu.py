@@ -30,21 +30,27 @@ def say(*a):
 # Execution modes: the persistent step with its default attention (one item
 # per query head while the context is short), the persistent step with the
 # chunked attention split at every position, and the multi-kernel step.
-MODES = {"persistent": 0, "persistent_chunked": 0, "multi": 1}
+MODES = {"persistent": 0, "persistent_chunked": 0, "persistent_pairs": 0, "multi": 1}
+# Engine settings per mode: the chunked attention at every position; every
+# input staged two elements per load (by default only inputs >= 4096 wide,
+# which the tiny models do not have).
+MODE_ENV = {"persistent_chunked": {"KL_ATTN_SHORT_MAX": "0"},
+            "persistent_pairs": {"KL_STAGE_PAIR_MIN": "2"}}
 
 
 def new_engine(K, img, cfg, mode=None):
     """An engine in execution mode `mode` (a MODES key; None: default)."""
-    old = os.environ.get("KL_ATTN_SHORT_MAX")
-    if mode == "persistent_chunked":
-        os.environ["KL_ATTN_SHORT_MAX"] = "0"
+    env = MODE_ENV.get(mode, {})
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         eng = K.Engine(img, cfg)
     finally:
-        if old is None:
-            os.environ.pop("KL_ATTN_SHORT_MAX", None)
-        else:
-            os.environ["KL_ATTN_SHORT_MAX"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     if mode is not None:
         eng.set_mode(MODES[mode])
         assert eng.mode == MODES[mode]
