@@ -869,7 +869,6 @@ struct AttnPre {
   static constexpr int NP = attn_chunk(HD) / attn_p_rpp(HD);
   static constexpr int NW = HD >= kWave ? HD / kWave : 1;
   f4 kr[NP], vr[NP];
-  float qn[NW], kn[NW];
 };
 
 template <int HD>
@@ -888,8 +887,6 @@ __device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, 
     // phases (nothing carries it around the layer loop).
 #pragma unroll
     for (int p = 0; p < NP; ++p) pre.kr[p] = pre.vr[p] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < AttnPre<HD>::NW; ++k) pre.qn[k] = pre.kn[k] = 0.f;
     return;
   }
   const int g = it / nsplit;
@@ -907,13 +904,6 @@ __device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, 
     const size_t off = static_cast<size_t>(t) * a.Dkv + col;
     pre.kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
     pre.vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
-  }
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 0; k < AttnPre<HD>::NW; ++k) {
-    const int d = lane + k * kWave;
-    pre.qn[k] = a.transform == 2 && d < HD ? g_rd(at->qn + d) : 0.f;
-    pre.kn[k] = a.transform == 2 && d < HD ? g_rd(at->kn + d) : 0.f;
   }
 }
 
@@ -972,6 +962,15 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
       }
     }
+    // Qwen3 q/k norm weights: requested just before the polls below, so
+    //    they arrive with them and are live only in this phase.
+    float qn[AttnPre<HD>::NW], kn[AttnPre<HD>::NW];
+#pragma unroll
+    for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+      const int d = lane + k * kWave;
+      qn[k] = a.transform == 2 && d < HD ? g_rd(at->qn + d) : 0.f;
+      kn[k] = a.transform == 2 && d < HD ? g_rd(at->kn + d) : 0.f;
+    }
     // 2. q of the group's heads and (chunk of pos) the new K and V rows, polled
     //    together (element e < kvm * HD is q, the next 2 * HD are K then V).
     {
@@ -1014,7 +1013,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 #pragma unroll
         for (int k = 0; k < AttnPre<HD>::NW; ++k) {
           const int d = lane + k * kWave;
-          if (d < HD) qs[h * HD + d] = (r * qs[h * HD + d]) * pre.qn[k];
+          if (d < HD) qs[h * HD + d] = (r * qs[h * HD + d]) * qn[k];
         }
       }
       if (own_pos && wave == kPWaves - 1) {
@@ -1025,7 +1024,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 #pragma unroll
         for (int k = 0; k < AttnPre<HD>::NW; ++k) {
           const int d = lane + k * kWave;
-          if (d < HD) kp[d] = (r * kp[d]) * pre.kn[k];
+          if (d < HD) kp[d] = (r * kp[d]) * kn[k];
         }
       }
       __syncthreads();
@@ -1601,7 +1600,6 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   }
   trace_mark(a, slot++);
 
-  PChunk<Q8> A[NB];
   {
     // This workgroup's rows of the residual stream start as the embedding row.
     const PGeom gr = p_geom(ph + 1);
@@ -1621,14 +1619,13 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       if (attn_short) {
 #pragma unroll
         for (int p = 0; p < AttnPre<HD>::NP; ++p) pre.kr[p] = pre.vr[p] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < AttnPre<HD>::NW; ++q) pre.qn[q] = pre.kn[q] = 0.f;
       } else {
         attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
       }
     }
     // The phase's first weight segment is requested before its input is
     // polled, so that the weights are on their way during the hand-off.
+    PChunk<Q8> A[NB];
     {
       PCur c0{0, 0, 0};
       p_seg_issue<Q8, NB>(p, g, c0, A);
