@@ -413,6 +413,7 @@ struct kl_engine {
   float* am_pv = nullptr;
   int* am_pi = nullptr;
   unsigned int* am_counter = nullptr;
+  unsigned int* cls_next = nullptr;  // dynamic classifier blocks handed out (same 64-byte slot)
   StepState* st = nullptr;
   StepState* st_host = nullptr;  // pinned staging
   int32_t* prompt = nullptr;
@@ -667,6 +668,7 @@ int check_device_error(kl_engine* e) {
   fprintf(stderr, "kuiper_hip: persistent step reported device error %d\n", *e->derr_host);
   err = hipMemset(e->derr, 0, sizeof(int));
   if (err == hipSuccess) err = hipMemset(e->am_counter, 0, sizeof(unsigned int));
+  if (err == hipSuccess) err = hipMemset(e->cls_next, 0, sizeof(unsigned int));
   if (err == hipSuccess) err = hipMemset(e->attn_counters, 0, e->lay.KVH * sizeof(unsigned int));
   if (err == hipSuccess) err = hipDeviceSynchronize();
   return err == hipSuccess ? KL_EDEVICE : rc(err);
@@ -683,7 +685,7 @@ int check_device_error(kl_engine* e) {
 // order (and so every result bit) does not depend on the measured split;
 // `max_share` (the largest weighted share, or 0) only sizes the LDS slots.
 size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb, int max_share) {
-  const int total = p.paired ? p.rows[0] : p.rows[0] + p.rows[1] + p.rows[2];
+  const int total = (p.paired ? p.rows[0] : p.rows[0] + p.rows[1] + p.rows[2]) - p.dyn;
   const int rpw = (total + nwg - 1) / nwg;  // balanced per-workgroup share
   p.cn16 = q8 ? p.cols / 16 : p.cols / 4;
   p.cn = (p.cn16 + kWave - 1) / kWave;
@@ -710,7 +712,7 @@ size_t plan_phase(PGemv& p, int nwg, bool q8, int gs, int nb, int max_share) {
       p.nsegw = nsegw;
     }
   }
-  const int rmax = std::max(rpw, max_share);
+  const int rmax = std::max(std::max(rpw, max_share), p.dyn > 0 ? p.blk : 0);
   return static_cast<size_t>(p.paired ? rmax * p.nsub : rmax) * p.ks;
 }
 
@@ -816,6 +818,17 @@ int setup_persistent(kl_engine* e) {
     w2.in = e->t_h; w2.norm = nullptr; w2.out[0] = e->t_x;
     at[l] = PAttn{e->kcache + l * kv_layer, e->vcache + l * kv_layer, L.qn, L.kn};
   }
+  // The classifier's last rows are handed out at run time in blocks, so that
+  // workgroups that finish their static share early take more: the slowest
+  // workgroup otherwise ends the step ~10 us after the median one.  Measured
+  // on Llama-3.2-1B: 20 % in blocks of 16 rows +0.7% (10 %: +-0, 40 %: -0.2%);
+  // Llama2-7B int8 and Qwen2.5-1.5B +-0.
+  // KL_CLS_DYN: percent of the rows (0: off); KL_CLS_BLOCK: rows per block.
+  int cls_blk = 16, cls_pct = 20;
+  if (const char* env = std::getenv("KL_CLS_BLOCK")) cls_blk = std::max(1, std::atoi(env));
+  if (const char* env = std::getenv("KL_CLS_DYN")) cls_pct = std::min(90, std::max(0, std::atoi(env)));
+  int cls_dyn = static_cast<int>(static_cast<long long>(m.V) * cls_pct / 100);
+  if (m.V - cls_dyn < e->nwg) cls_dyn = 0;  // every workgroup keeps a static row
   // Weighted splits (after calibration) for the four split dimensions.
   const bool weighted = static_cast<int>(e->wg_weight.size()) == e->nwg;
   int share_qkv = 0, share_d = 0, share_f = 0, share_v = 0;
@@ -823,7 +836,7 @@ int setup_persistent(kl_engine* e) {
     const std::vector<int> sq = weighted_split(m.Dq + 2 * m.Dkv, e->wg_weight);
     const std::vector<int> sd = weighted_split(m.D, e->wg_weight);
     const std::vector<int> sf = weighted_split(m.F, e->wg_weight);
-    const std::vector<int> sv = weighted_split(m.V, e->wg_weight);
+    const std::vector<int> sv = weighted_split(m.V - cls_dyn, e->wg_weight);
     share_qkv = max_share(sq);
     share_d = max_share(sd);
     share_f = max_share(sf);
@@ -848,6 +861,7 @@ int setup_persistent(kl_engine* e) {
   cls = PGemv{};
   cls.w[0] = e->wcls.w; cls.sc[0] = e->wcls.s; cls.rows[0] = m.V;
   cls.nsub = 1; cls.cols = m.D; cls.epi = kEpiCls;
+  cls.dyn = cls_dyn; cls.blk = cls_blk;
   cls.layer = m.L - 1; cls.in_layer = m.L - 1;
   cls.in = e->t_x; cls.norm = e->rms_final; cls.logits = e->logits;
   if (weighted) cls.split = e->d_split + 3 * (static_cast<size_t>(e->nwg) + 1);
@@ -934,6 +948,7 @@ int setup_persistent(kl_engine* e) {
   if (const char* env = std::getenv("KL_W13_TOUCH_ROWS_SHORT"))
     a.short_touch_rows = std::max(0, std::atoi(env));
   a.am_pv = e->am_pv; a.am_pi = e->am_pi; a.am_cnt = e->am_counter;
+  a.cls_next = e->cls_next;
   a.epoch = e->epoch; a.err = e->derr;
   a.red_off = red_off;
   a.xres_off = static_cast<int>(xres_at / sizeof(float));
@@ -1248,6 +1263,7 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
   e->attn_part = PF(part_at);
   e->attn_counters = reinterpret_cast<unsigned int*>(P(actr_at));
   e->am_counter = reinterpret_cast<unsigned int*>(P(amc_at));
+  e->cls_next = e->am_counter + 8;
   e->st = reinterpret_cast<StepState*>(P(st_at));
   e->am_pv = PF(pv_at);
   e->am_pi = reinterpret_cast<int*>(P(pi_at));

@@ -101,6 +101,8 @@ struct PGemv {
   float* vcache;          // qkv: V cache layer base (row pos kept for later tokens)
   float* logits;          // classifier output
   const float* bias[3];   // qkv bias (Qwen2) or nullptr
+  int dyn, blk;           // classifier: the last `dyn` rows are handed out at run time in
+                          //   blocks of `blk` rows (0: every row in the static split)
   const int* split;       // [workgroups + 1] first row of each workgroup, or nullptr:
                           //   balanced split b * total / n
 };
@@ -156,6 +158,7 @@ struct PArgs {
   float* am_pv;            // [gridDim] argmax partials
   int* am_pi;
   unsigned int* am_cnt;    // end-of-step arrival counter
+  unsigned int* cls_next;  // next dynamic classifier block (reset by the last workgroup)
   unsigned int* epoch;     // launch counter for tags
   int* err;
   int red_off;             // LDS floats: input vector at 0, row partials at red_off,
@@ -548,8 +551,9 @@ __device__ __forceinline__ void p_share(PGp p, int b, int& base, int& cnt) {
     base = sp[b];
     cnt = sp[b + 1] - base;
   } else {
-    // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n).
-    const int total = p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2];
+    // Balanced split: workgroup b owns rows [b * total / n, (b + 1) * total / n)
+    // of the statically split rows.
+    const int total = (p->paired ? p->rows[0] : p->rows[0] + p->rows[1] + p->rows[2]) - p->dyn;
     const long long bb = b, n = gridDim.x;
     base = static_cast<int>(bb * total / n);
     cnt = static_cast<int>((bb + 1) * total / n) - base;
@@ -566,6 +570,22 @@ __device__ __forceinline__ PGeom p_geom(PGp p) {
   g.rg = wave / p->ks;
   p_share(p, blockIdx.x, g.base, g.cnt);
   g.nloc = p->paired ? g.cnt * p->nsub : g.cnt;
+  const int nrows = g.nloc > g.rg ? (g.nloc - g.rg + p->rw - 1) / p->rw : 0;
+  g.n_items = g.ksi < p->nseg ? nrows * p->nsegw : 0;
+  return g;
+}
+
+// Geometry of dynamic classifier block `blk`: rows [v0 + blk * B, + B) of the
+// rows past the static split (v0 = total - dyn), clipped to the matrix.
+__device__ __forceinline__ PGeom p_geom_block(PGp p, int blk) {
+  PGeom g;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  g.ksi = wave % p->ks;
+  g.rg = wave / p->ks;
+  const int first = p->rows[0] - p->dyn + blk * p->blk;
+  g.base = first;
+  g.cnt = min(p->blk, p->rows[0] - first);
+  g.nloc = g.cnt;
   const int nrows = g.nloc > g.rg ? (g.nloc - g.rg + p->rw - 1) / p->rw : 0;
   g.n_items = g.ksi < p->nseg ? nrows * p->nsegw : 0;
   return g;
@@ -1561,6 +1581,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ float sred[2 * kPWaves];
   __shared__ int s_last;
+  __shared__ int s_claim;
   __shared__ float s_bv[kPWaves];
   __shared__ int s_bi[kPWaves];
   const PStepState st = *a.st;  // written by the previous launch
@@ -1632,6 +1653,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     }
     stage_vec(a, p->in, tag_in, emb_row, p->norm, p->cols, xs, sred);
     trace_mark(a, slot++);
+    // Classifier: claim the first dynamic block now; the answer is needed
+    // only after the static rows.
+    unsigned int cls_claim = 0;
+    if (is_cls && p->dyn > 0 && threadIdx.x == 0) cls_claim = g_arrive(a.cls_next);
     p_stream<Q8, NB>(p, g, A, xs, red);
     // RMSNorm scale of this phase's input (1 without a norm).
     const float rn = p->norm ? norm_scale(sred, p->cols, a.eps) : 1.f;
@@ -1640,10 +1665,48 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       // workgroup's (max, first index) pair (sampler/argmax_sampler.cpp:5-13).
       float* logits = p->logits;
       const int ks = p->ks;
+      // The dynamic rows: blocks claimed one ahead (the claim is in flight
+      // while a block streams), each block's first segment requested before
+      // the previous block's rows are read out of LDS.
+      const int nblk = p->dyn > 0 ? (p->dyn + p->blk - 1) / p->blk : 0;
+      int blk = nblk;
+      PGeom gd = g;
+      PChunk<Q8> D[NB];
+      if (nblk > 0) {
+        if (threadIdx.x == 0) s_claim = static_cast<int>(cls_claim);
+        __syncthreads();
+        blk = s_claim;
+        if (blk < nblk) {
+          gd = p_geom_block(p, blk);
+          PCur c0{0, 0, 0};
+          p_seg_issue<Q8, NB>(p, gd, c0, D);
+        }
+      }
       for (int lr = threadIdx.x; lr < g.nloc; lr += kPThreads) {
         const float v = rn * p_row_total(ks, red, lr);
         logits[g.base + lr] = v;
         argmax_merge(bv, bi, v, g.base + lr);
+      }
+      while (blk < nblk) {
+        unsigned int claim = 0;
+        if (threadIdx.x == 0) claim = g_arrive(a.cls_next);
+        __syncthreads();  // the previous rows are read out of red
+        p_stream<Q8, NB>(p, gd, D, xs, red);
+        if (threadIdx.x == 0) s_claim = static_cast<int>(claim);
+        __syncthreads();
+        const int nxt = s_claim;
+        const PGeom gc = gd;
+        if (nxt < nblk) {
+          gd = p_geom_block(p, nxt);
+          PCur c0{0, 0, 0};
+          p_seg_issue<Q8, NB>(p, gd, c0, D);
+        }
+        for (int lr = threadIdx.x; lr < gc.nloc; lr += kPThreads) {
+          const float v = rn * p_row_total(ks, red, lr);
+          logits[gc.base + lr] = v;
+          argmax_merge(bv, bi, v, gc.base + lr);
+        }
+        blk = nxt;
       }
       wave_argmax(bv, bi);
       if (lane == 0) {
@@ -1763,6 +1826,9 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     ns.pos = pos + 1;
     *a.st = ns;
     *a.epoch = wrap ? 0u : epoch + 1;
+    // Every workgroup has arrived, so every claim is made (each workgroup's
+    // last claim was past the blocks).
+    g_st(a.cls_next, 0u);
     g_st(a.am_cnt, 0u);
   }
 }

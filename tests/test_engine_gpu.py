@@ -203,6 +203,36 @@ def test_l2_pull_changes_no_bits(K, O, gpu, monkeypatch):
     assert list(ga) == list(gb)
 
 
+@pytest.mark.parametrize("name", ["llama32_1b", "tiny_q8", "tiny_qwen2"])
+def test_dynamic_classifier_rows_change_no_bits(K, O, gpu, monkeypatch, name):
+    """The classifier's last rows handed out to workgroups at run time (the
+    default: 20 % of the rows in blocks of 16), none of them (every row in the
+    static split), or half of them in blocks of one row (every workgroup
+    claims several): each row is computed the same way whichever workgroup
+    takes it, so the logits agree bit for bit, step after step (the claim
+    counter starts every launch at zero)."""
+    cfg = K.ALL[name]
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg, 6)
+    engines = []
+    for env in ({}, {"KL_CLS_DYN": "0"}, {"KL_CLS_DYN": "50", "KL_CLS_BLOCK": "1"}):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        engines.append(K.Engine(img, cfg))
+        for k in env:
+            monkeypatch.delenv(k)
+    for e in engines:
+        e.set_mode(K.MODE_PERSISTENT)
+    for pos, t in enumerate(list(prompt) + [3, 4, 5, 6]):
+        outs = [e.step(int(t), pos) for e in engines]
+        for n, lg in outs[1:]:
+            assert n == outs[0][0] and np.array_equal(lg, outs[0][1]), pos
+    gens = [list(e.generate(prompt, 8)[0]) for e in engines]
+    assert gens[1] == gens[0] and gens[2] == gens[0]
+    om = O.Model(img, cfg.family, cfg.quant)
+    assert gens[0] == [int(x) for x in om.generate(prompt, 8)]
+
+
 def test_engine_rejects_bad_tokens(K, gpu):
     cfg = K.TINY["tiny_llama2"]
     eng = K.Engine(K.synth_image(cfg), cfg)
