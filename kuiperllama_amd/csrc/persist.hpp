@@ -879,16 +879,17 @@ __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul) {
   return head + static_cast<size_t>(pt) * hd;  // + the chunk's V rows
 }
 
-// What the attention of a layer needs that does not depend on the layer's
-// QKV output: this workgroup's first chunk of cached K and V rows, and the
-// Qwen3 q/k norm weights it applies.  Loaded at the start of the QKV phase, so
-// the loads complete while the QKV weights stream instead of adding a round
-// trip when attention starts.
+// What the attention of a layer needs first that does not depend on the
+// layer's QKV output: this workgroup's first chunk of cached K rows, loaded at
+// the start of the QKV phase so that the scores need no round trip when
+// attention starts.  (The V rows are requested at the start of the attention
+// item: held across the QKV phase they doubled the bytes in flight ahead of
+// its polls and the registers that made the head-size-128 variant spill.)
 template <int HD>
 struct AttnPre {
   static constexpr int NP = attn_chunk(HD) / attn_p_rpp(HD);
   static constexpr int NW = HD >= kWave ? HD / kWave : 1;
-  f4 kr[NP], vr[NP];
+  f4 kr[NP];
 };
 
 template <int HD>
@@ -906,7 +907,7 @@ __device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, 
     // No item: pre is still written, so that it is dead between attention
     // phases (nothing carries it around the layer loop).
 #pragma unroll
-    for (int p = 0; p < NP; ++p) pre.kr[p] = pre.vr[p] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < NP; ++p) pre.kr[p] = f4{0.f, 0.f, 0.f, 0.f};
     return;
   }
   const int g = it / nsplit;
@@ -916,14 +917,12 @@ __device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, 
   const int sub = threadIdx.x % TPR, rr = threadIdx.x / TPR;
   const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
   const float* kcache = at->kcache;
-  const float* vcache = at->vcache;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int tt = p * RPP + rr;
     const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);  // row pos comes from QKV
     const size_t off = static_cast<size_t>(t) * a.Dkv + col;
     pre.kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
-    pre.vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
   }
 }
 
@@ -963,22 +962,19 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     const bool own_pos = pos >= t0 && pos < t0 + cnt;
 
     // 1. The chunk's cached K and V rows into registers (row pos is replaced
-    //    below by the new row).
+    //    below by the new row).  The first item's K rows were loaded by
+    //    attn_prefetch during the QKV phase; V rows are requested here, before
+    //    the polls below, and are first needed after the scores.
     f4 kr[NP], vr[NP];
-    if (it == static_cast<int>(blockIdx.x)) {  // loaded by attn_prefetch
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        kr[p] = pre.kr[p];
-        vr[p] = pre.vr[p];
-      }
-    } else {
+    {
+      const bool first = it == static_cast<int>(blockIdx.x);
       const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         const int tt = p * RPP + rr;
         const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);
         const size_t off = static_cast<size_t>(t) * a.Dkv + col;
-        kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
+        kr[p] = first ? pre.kr[p] : g_rd(reinterpret_cast<const f4*>(kcache + off));
         vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
       }
     }
@@ -1639,7 +1635,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     if ((k & 3) == 0 && !is_cls) {
       if (attn_short) {
 #pragma unroll
-        for (int p = 0; p < AttnPre<HD>::NP; ++p) pre.kr[p] = pre.vr[p] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < AttnPre<HD>::NP; ++p) pre.kr[p] = f4{0.f, 0.f, 0.f, 0.f};
       } else {
         attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
       }
