@@ -879,57 +879,14 @@ __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul) {
   return head + static_cast<size_t>(pt) * hd;  // + the chunk's V rows
 }
 
-// What the attention of a layer needs first that does not depend on the
-// layer's QKV output: this workgroup's first chunk of cached K rows, loaded at
-// the start of the QKV phase so that the scores need no round trip when
-// attention starts.  (The V rows are requested at the start of the attention
-// item: held across the QKV phase they doubled the bytes in flight ahead of
-// its polls and the registers that made the head-size-128 variant spill.)
+// Per-lane elements of the Qwen3 q/k norm weights (HD values over 64 lanes).
 template <int HD>
-struct AttnPre {
-  static constexpr int NP = attn_chunk(HD) / attn_p_rpp(HD);
-  static constexpr int NW = HD >= kWave ? HD / kWave : 1;
-  f4 kr[NP];
-};
-
-template <int HD>
-__device__ __forceinline__ void attn_prefetch(const PArgs& a, const PAttn* atp, int pos,
-                                              AttnPre<HD>& pre) {
-  constexpr int PT = attn_chunk(HD);
-  constexpr int TPR = HD / 4;
-  constexpr int RPP = attn_p_rpp(HD);
-  constexpr int NP = AttnPre<HD>::NP;
-  const KL_CAS PAttn* at = (const KL_CAS PAttn*)(atp);
-  const int n = pos + 1;
-  const int nsplit = (n + PT - 1) / PT;
-  const int it = blockIdx.x;
-  if (it >= a.KVH * nsplit) {
-    // No item: pre is still written, so that it is dead between attention
-    // phases (nothing carries it around the layer loop).
-#pragma unroll
-    for (int p = 0; p < NP; ++p) pre.kr[p] = f4{0.f, 0.f, 0.f, 0.f};
-    return;
-  }
-  const int g = it / nsplit;
-  const int s = it - g * nsplit;
-  const int t0 = s * PT;
-  const int cnt = min(n - t0, PT);
-  const int sub = threadIdx.x % TPR, rr = threadIdx.x / TPR;
-  const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
-  const float* kcache = at->kcache;
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int tt = p * RPP + rr;
-    const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);  // row pos comes from QKV
-    const size_t off = static_cast<size_t>(t) * a.Dkv + col;
-    pre.kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
-  }
-}
+constexpr int kNormPerLane = HD >= kWave ? HD / kWave : 1;
 
 template <int HD>
 __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, int pos,
                                              unsigned int tag, float* lds, int trace_slot,
-                                             const AttnPre<HD>& pre, float rope_c, float rope_s) {
+                                             float rope_c, float rope_s) {
   constexpr int PT = attn_chunk(HD);
   constexpr int TPR = HD / 4;
   constexpr int RPP = attn_p_rpp(HD);
@@ -962,27 +919,27 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     const bool own_pos = pos >= t0 && pos < t0 + cnt;
 
     // 1. The chunk's cached K and V rows into registers (row pos is replaced
-    //    below by the new row).  The first item's K rows were loaded by
-    //    attn_prefetch during the QKV phase; V rows are requested here, before
-    //    the polls below, and are first needed after the scores.
+    //    below by the new row), requested before the polls below so that they
+    //    arrive with them.  (Prefetching them during the QKV phase put their
+    //    bytes ahead of that phase's polls in each wave's in-order return
+    //    queue, and its registers made the head-size-128 variant spill.)
     f4 kr[NP], vr[NP];
     {
-      const bool first = it == static_cast<int>(blockIdx.x);
       const size_t col = static_cast<size_t>(g) * HD + 4 * sub;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         const int tt = p * RPP + rr;
-        const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);
+        const int t = t0 + (tt < cnt && t0 + tt != pos ? tt : 0);  // row pos comes from QKV
         const size_t off = static_cast<size_t>(t) * a.Dkv + col;
-        kr[p] = first ? pre.kr[p] : g_rd(reinterpret_cast<const f4*>(kcache + off));
+        kr[p] = g_rd(reinterpret_cast<const f4*>(kcache + off));
         vr[p] = g_rd(reinterpret_cast<const f4*>(vcache + off));
       }
     }
     // Qwen3 q/k norm weights: requested just before the polls below, so
     //    they arrive with them and are live only in this phase.
-    float qn[AttnPre<HD>::NW], kn[AttnPre<HD>::NW];
+    float qn[kNormPerLane<HD>], kn[kNormPerLane<HD>];
 #pragma unroll
-    for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+    for (int k = 0; k < kNormPerLane<HD>; ++k) {
       const int d = lane + k * kWave;
       qn[k] = a.transform == 2 && d < HD ? g_rd(at->qn + d) : 0.f;
       kn[k] = a.transform == 2 && d < HD ? g_rd(at->kn + d) : 0.f;
@@ -1027,7 +984,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         ss = wave_sum(ss);
         const float r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
 #pragma unroll
-        for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+        for (int k = 0; k < kNormPerLane<HD>; ++k) {
           const int d = lane + k * kWave;
           if (d < HD) qs[h * HD + d] = (r * qs[h * HD + d]) * qn[k];
         }
@@ -1038,7 +995,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         ss = wave_sum(ss);
         const float r = 1.f / sqrtf(ss / static_cast<float>(HD) + a.qk_eps);
 #pragma unroll
-        for (int k = 0; k < AttnPre<HD>::NW; ++k) {
+        for (int k = 0; k < kNormPerLane<HD>; ++k) {
           const int d = lane + k * kWave;
           if (d < HD) kp[d] = (r * kp[d]) * kn[k];
         }
@@ -1609,7 +1566,6 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     rope_c = g_rd(a.cos_t + static_cast<size_t>(pos) * HD + 2 * j);
     rope_s = g_rd(a.sin_t + static_cast<size_t>(pos) * HD + 2 * j);
   }
-  AttnPre<HD> pre;
   constexpr bool attn_short = SHORT;
   if (a.trace) {
     for (int s = threadIdx.x; s < a.trace_slots; s += kPThreads) trace_lds(a)[s] = 0;
@@ -1632,14 +1588,6 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
     const PGeom g = p_geom(p);
     const unsigned int tag_in = epoch * kTagLayers + p->in_layer + 1;
     const unsigned int tag = epoch * kTagLayers + p->layer + 1;
-    if ((k & 3) == 0 && !is_cls) {
-      if (attn_short) {
-#pragma unroll
-        for (int p = 0; p < AttnPre<HD>::NP; ++p) pre.kr[p] = f4{0.f, 0.f, 0.f, 0.f};
-      } else {
-        attn_prefetch<HD>(a, a.at + (k >> 2), pos, pre);
-      }
-    }
     // The phase's first weight segment is requested before its input is
     // polled, so that the weights are on their way during the hand-off.
     PChunk<Q8> A[NB];
@@ -1765,7 +1713,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       if constexpr (SHORT)
         attn_short_phase<HD>(a, k >> 2, pos, tag, lds, slot);
       else
-        attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds, slot, pre, rope_c, rope_s);
+        attn_p_phase<HD>(a, a.at + (k >> 2), pos, tag, lds, slot, rope_c, rope_s);
       ++slot;
       trace_mark(a, slot++);
     }
