@@ -820,11 +820,14 @@ int setup_persistent(kl_engine* e) {
   }
   // The classifier's last rows are handed out at run time in blocks, so that
   // workgroups that finish their static share early take more: the slowest
-  // workgroup otherwise ends the step ~10 us after the median one.  Measured
-  // on Llama-3.2-1B: 20 % in blocks of 16 rows +0.7% (10 %: +-0, 40 %: -0.2%);
-  // Llama2-7B int8 and Qwen2.5-1.5B +-0.
+  // workgroup otherwise ends the step ~10 us after the median one.  Measured:
+  // 20 % in blocks of 16 rows +0.7% on Llama-3.2-1B (4 MB of classifier per
+  // workgroup; 10 %: +-0, 40 %: -0.2%), +-0 on Qwen2.5-1.5B and Qwen3-4B,
+  // -1% on Llama2-110M (0.4 MB per workgroup, whose tail is short anyway), so
+  // it is on from 2 MB of classifier weights per workgroup.
   // KL_CLS_DYN: percent of the rows (0: off); KL_CLS_BLOCK: rows per block.
-  int cls_blk = 16, cls_pct = 20;
+  const double cls_bytes_wg = static_cast<double>(m.V) * m.D * (q8 ? 1.0 + 4.0 / m.gs : 4.0) / e->nwg;
+  int cls_blk = 16, cls_pct = cls_bytes_wg >= 2.0 * (1 << 20) ? 20 : 0;
   if (const char* env = std::getenv("KL_CLS_BLOCK")) cls_blk = std::max(1, std::atoi(env));
   if (const char* env = std::getenv("KL_CLS_DYN")) cls_pct = std::min(90, std::max(0, std::atoi(env)));
   int cls_dyn = static_cast<int>(static_cast<long long>(m.V) * cls_pct / 100);

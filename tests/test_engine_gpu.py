@@ -206,11 +206,12 @@ def test_l2_pull_changes_no_bits(K, O, gpu, monkeypatch):
 @pytest.mark.parametrize("name", ["llama32_1b", "tiny_q8", "tiny_qwen2"])
 def test_dynamic_classifier_rows_change_no_bits(K, O, gpu, monkeypatch, name):
     """The classifier's last rows handed out to workgroups at run time (the
-    default: 20 % of the rows in blocks of 16), none of them (every row in the
-    static split), or half of them in blocks of one row (every workgroup
-    claims several): each row is computed the same way whichever workgroup
-    takes it, so the logits agree bit for bit, step after step (the claim
-    counter starts every launch at zero)."""
+    default from 2 MB of classifier per workgroup, as on Llama-3.2-1B: 20 % of
+    the rows in blocks of 16), none of them (every row in the static split),
+    or half of them in blocks of one row (every workgroup claims several):
+    each row is computed the same way whichever workgroup takes it, so the
+    logits agree bit for bit, step after step (the claim counter starts every
+    launch at zero)."""
     cfg = K.ALL[name]
     img = K.synth_image(cfg)
     prompt = K.prompt_tokens(cfg, 6)
