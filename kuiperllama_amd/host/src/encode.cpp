@@ -560,14 +560,21 @@ std::vector<int32_t> SpeEncodeLayer::encode(const std::string& sentence) const {
       add_pair(l.prev, top.left);
       add_pair(top.left, l.next);
     }
+    // A run of unknown pieces becomes one unknown id, as the library merges
+    // them (its decoder then renders one " \u2047 " per run).
+    const size_t first = ids.size();
+    auto push = [&](int32_t id) {
+      if (id == unk_id_ && ids.size() > first && ids.back() == unk_id_) return;
+      ids.push_back(id);
+    };
     for (int i = sym.empty() ? -1 : 0; i >= 0; i = sym[i].next) {
       const auto it = index_.find(sym[i].piece);
       if (it != index_.end()) {
-        ids.push_back(it->second);
+        push(it->second);
       } else if (byte_fallback_) {
-        for (unsigned char b : sym[i].piece) ids.push_back(byte_ids_[b] >= 0 ? byte_ids_[b] : unk_id_);
+        for (unsigned char b : sym[i].piece) push(byte_ids_[b] >= 0 ? byte_ids_[b] : unk_id_);
       } else {
-        ids.push_back(unk_id_);
+        push(unk_id_);
       }
     }
   }

@@ -238,3 +238,42 @@ def test_space_replacement_pin(tmp_path):
     for k in range(n):
         assert got[k][0] == got[n + k][0] == bt.encode(texts[k])
         assert got[n + k][1] == texts[k].replace("Ġ", " ")
+
+
+@pytest.mark.parametrize("opts", [
+    dict(remove_extra_whitespaces=True, byte_fallback=False, add_dummy_prefix=True),
+    dict(remove_extra_whitespaces=False, byte_fallback=False, add_dummy_prefix=False),
+])
+def test_spe_other_model_options_match_sentencepiece(tmp_path, opts):
+    """SentencePiece BPE models trained here with the options the fixture model
+    does not use: extra-whitespace removal, no byte fallback (pieces outside
+    the vocabulary become the unknown id, decoded as " \\u2047 "), no dummy
+    prefix.  The C++ layer must give the library's ids and decodings."""
+    spm = pytest.importorskip("sentencepiece")
+    import io
+    rng = random.Random(21)
+    words = ["the", "quick", "brown", "fox", "jumps", "over", "lazy", "dog", "and", "runs", "far",
+             "away", "from", "home", "while", "singing", "songs", "of", "old", "days", "42", "7"]
+    corpus = [" ".join(rng.choice(words) for _ in range(rng.randint(3, 12))) for _ in range(2000)]
+    buf = io.BytesIO()
+    spm.SentencePieceTrainer.train(
+        sentence_iterator=iter(corpus), model_writer=buf, vocab_size=120, model_type="bpe",
+        normalization_rule_name="identity", split_digits=True, character_coverage=1.0,
+        unk_id=0, bos_id=1, eos_id=2, pad_id=-1, num_threads=1, minloglevel=2, **opts)
+    path = tmp_path / "m.model"
+    path.write_bytes(buf.getvalue())
+    sp = spm.SentencePieceProcessor(model_file=str(path))
+    texts = random_texts(31, 200) + ["  the  quick   fox  ", "\tlazy dog\n", "", " ", "over home"]
+    cases = tmp_path / "cases.txt"
+    cases.write_text("".join((t.encode("utf-8").hex() or "-") + "\n" for t in texts))
+    p = subprocess.run([BIN, "tok", "spe", str(path), str(cases)], capture_output=True, text=True,
+                       timeout=120)
+    assert p.returncode == 0, p.stdout + p.stderr
+    lines = p.stdout.splitlines()
+    ids = [list(map(int, ln.split()[1:])) for ln in lines if ln.startswith("ids")]
+    dec = [bytes.fromhex(ln[4:]).decode("utf-8") for ln in lines if ln.startswith("dec")]
+    assert len(ids) == len(texts)
+    for s, i, d in zip(texts, ids, dec):
+        want = [sp.bos_id()] + sp.encode(s, out_type=int)
+        assert i == want, (s, i, want)
+        assert d == sp.decode(want), (s, d, sp.decode(want))
