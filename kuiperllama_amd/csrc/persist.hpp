@@ -872,11 +872,17 @@ __device__ __forceinline__ float p_row_total(int ks, const float* red, int lr) {
 __host__ __device__ constexpr int attn_p_rpp(int hd) { return kPThreads / (hd / 4); }
 constexpr int kAttnMergeChunks = 8;  // chunks per merging workgroup
 
+// The chunk's V rows sit in LDS with a row stride of hd + 4 floats: the PV
+// step's eight lanes per output read eight different rows of the same
+// columns, which at a stride of hd floats (a multiple of the bank period) all
+// hit the same banks.
+__host__ __device__ constexpr int attn_vs_stride(int hd) { return hd + 4; }
+
 __host__ __device__ inline size_t attn_p_lds_floats(int hd, int kv_mul) {
   const int pt = attn_chunk(hd);
   const size_t head = static_cast<size_t>(kv_mul) * hd + static_cast<size_t>(kv_mul) * pt +
                       2 * static_cast<size_t>(hd) + 2 * kAttnMaxKvMul;
-  return head + static_cast<size_t>(pt) * hd;  // + the chunk's V rows
+  return head + static_cast<size_t>(pt) * attn_vs_stride(hd);  // + the chunk's V rows
 }
 
 // Per-lane elements of the Qwen3 q/k norm weights (HD values over 64 lanes).
@@ -910,7 +916,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
   float* kp = sc + kvm * PT;            // [HD] K[pos] (transformed)
   float* vp = kp + HD;                  // [HD] V[pos]
   float* ml = vp + HD;                  // [2 * kAttnMaxKvMul]
-  float* vs = ml + 2 * kAttnMaxKvMul;   // [PT][HD] V rows of the chunk
+  float* vs = ml + 2 * kAttnMaxKvMul;   // [PT][HD + 4] V rows of the chunk
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int g = it / nsplit;
     const int s = it - g * nsplit;
@@ -1035,7 +1041,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int tt = p * RPP + rr;
-      if (tt < PT) reinterpret_cast<f4*>(vs + static_cast<size_t>(tt) * HD)[sub] = vr[p];
+      if (tt < PT) reinterpret_cast<f4*>(vs + static_cast<size_t>(tt) * attn_vs_stride(HD))[sub] = vr[p];
     }
 
     // 3. Scores, four heads at a time (the q reads and the 16-lane reductions
@@ -1105,7 +1111,7 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
           const int tt = part * RPT + j;
-          if (tt < cnt) o += ph[tt] * v4[tt * TPR + sub4];
+          if (tt < cnt) o += ph[tt] * v4[tt * (attn_vs_stride(HD) / 4) + sub4];
         }
         o.x = group_sum_dpp<PV_T>(o.x);
         o.y = group_sum_dpp<PV_T>(o.y);
