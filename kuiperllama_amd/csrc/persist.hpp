@@ -1107,11 +1107,15 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
         const int part = b & (PV_T - 1), o4 = b / PV_T;
         const int h = o4 / TPR, sub4 = o4 - h * TPR;
         const float* ph = sc + h * PT;
+        // Straight-line over the lane's rows: every row of vs holds finite
+        // values (rows past the chunk were loaded from its first row), and
+        // their weight is 0.
         f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
           const int tt = part * RPT + j;
-          if (tt < cnt) o += ph[tt] * v4[tt * (attn_vs_stride(HD) / 4) + sub4];
+          const float w = ph[tt];
+          o += (tt < cnt ? w : 0.f) * v4[tt * (attn_vs_stride(HD) / 4) + sub4];
         }
         o.x = group_sum_dpp<PV_T>(o.x);
         o.y = group_sum_dpp<PV_T>(o.y);
