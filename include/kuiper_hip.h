@@ -173,6 +173,15 @@ int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, i
                        int ldw, int ldc, const float* bias, int accumulate, int splits,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* MatmulKernelQuant (KI:12-14; cuda/matmul_kernel.cu:111-134) on M rows at
+ * once: C[M x N] (+)= A[M x K] . dequant(q)^T (+ bias), q int8 [N x K] (dense
+ * rows) with scales[(n*K + k) / group_size] (group_size a power of two >= 4),
+ * K a multiple of 32.  Split-K and its workspace as kl_gemm_f32_splitk
+ * (splits = 1 needs none).  Used by the batched prefill of int8 images. */
+int kl_gemm_q8(const float* A, const int8_t* q, const float* scales, int group_size, float* C,
+               int M, int N, int K, int lda, int ldc, const float* bias, int accumulate, int splits,
+               void* workspace, size_t workspace_bytes, void* stream);
+
 /* RoPEKernel (KI:36-39) on n_pos rows: row r of q (stride ldq) and of k
  * (stride ldk) rotated at position pos0 + r. */
 int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ldq, float* k,

@@ -29,6 +29,7 @@
 
 #include "attn.hpp"
 #include "device.hpp"
+#include "gemm_run.hpp"
 #include "gemv.hpp"
 #include "kuiper_hip.h"
 #include "persist.hpp"
@@ -1414,8 +1415,32 @@ int prefill_splits(int rows, int n, int k) {
 }
 
 bool prefill_supported(const kl_engine* e) {
-  const int hd = e->lay.hd;
-  return !e->quant && (hd == 32 || hd == 64 || hd == 128);
+  const ImageLayout& m = e->lay;
+  const int hd = m.hd;
+  if (hd != 32 && hd != 64 && hd != 128) return false;
+  // int8 GEMMs take whole 32-column blocks and groups of at least 4.
+  if (e->quant && (m.D % kGemmBK || m.Dq % kGemmBK || m.F % kGemmBK || m.gs < 4 ||
+                   (m.gs & (m.gs - 1))))
+    return false;
+  return true;
+}
+
+// One projection of a layer as a GEMM segment (fp32 or int8 weights, dense
+// rows of K columns).
+GemmSeg proj_seg(const kl_engine* e, const WView& w, float* C, const float* bias, int N, int K,
+                 int ldc) {
+  GemmSeg sg{};
+  sg.W = w.w;
+  sg.C = C;
+  sg.bias = bias;
+  sg.N = N;
+  sg.ldw = K;
+  sg.ldc = ldc;
+  if (e->quant) {
+    sg.S = w.s;
+    while ((1 << sg.gshift) < e->lay.gs) ++sg.gshift;
+  }
+  return sg;
 }
 
 // Allocates the prefill scratch for `rows` rows (once; grows if needed).
@@ -1477,21 +1502,14 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     float* vc = e->vcache + l * kv_layer;
     float* krow = kc + static_cast<size_t>(pos0) * Dkv;
     float* vrow = vc + static_cast<size_t>(pos0) * Dkv;
-    const float* wq = static_cast<const float*>(Ld.wq.w);
-    const float* wk = static_cast<const float*>(Ld.wk.w);
-    const float* wv = static_cast<const float*>(Ld.wv.w);
-    const float* wo = static_cast<const float*>(Ld.wo.w);
-    const float* w1 = static_cast<const float*>(Ld.w1.w);
-    const float* w2 = static_cast<const float*>(Ld.w2.w);
-    const float* w3 = static_cast<const float*>(Ld.w3.w);
+    hipStream_t hs = static_cast<hipStream_t>(st);
     // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
     {  // q, k and v in one grouped launch; k and v straight into the cache rows
-      const float* W[3] = {wq, wk, wv};
-      float* Cs[3] = {e->pf_q, krow, vrow};
-      const float* B[3] = {Ld.bq, Ld.bk, Ld.bv};
-      const int N[3] = {Dq, Dkv, Dkv}, LW[3] = {D, D, D}, LC[3] = {Dq, Dkv, Dkv};
-      PF(kl_gemm_f32_grouped(e->pf_xn, n, D, D, 3, W, Cs, B, N, LW, LC, 0, st));
+      const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
+                             proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
+                             proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
+      PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, nullptr, 1, hs));
     }
     if (e->transform == 2) {  // Qwen3 per-head q/k RMSNorm, eps 1e-6
       PF(kl_rmsnorm_rows(e->pf_q, Ld.qn, e->pf_q, n * H, hd, 1e-6f, st));
@@ -1502,19 +1520,26 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     PF(kl_attn_prefill(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, st));
     const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
-    PF(kl_gemm_f32_splitk(e->pf_att, wo, e->pf_x, n, D, Dq, Dq, Dq, D, nullptr, 1,
-                          prefill_splits(n, D, Dq), e->pf_ws, ws_bytes, st));
+    {
+      const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
+      const int sp = prefill_splits(n, D, Dq);
+      if (static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
+      PF(gemm_run(e->pf_att, n, Dq, Dq, 1, &sg, 1, e->pf_ws, sp, hs));
+    }
     // feed_forward (llama3.cpp:671-719)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
     {
-      const float* W[2] = {w1, w3};
-      float* Cs[2] = {e->pf_h1, e->pf_h3};
-      const int N[2] = {F, F}, LW[2] = {D, D}, LC[2] = {F, F};
-      PF(kl_gemm_f32_grouped(e->pf_xn, n, D, D, 2, W, Cs, nullptr, N, LW, LC, 0, st));
+      const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
+                             proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
+      PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, nullptr, 1, hs));
     }
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
-    PF(kl_gemm_f32_splitk(e->pf_h1, w2, e->pf_x, n, D, F, F, F, D, nullptr, 1,
-                          prefill_splits(n, D, F), e->pf_ws, ws_bytes, st));
+    {
+      const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
+      const int sp = prefill_splits(n, D, F);
+      if (static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
+      PF(gemm_run(e->pf_h1, n, F, F, 1, &sg, 1, e->pf_ws, sp, hs));
+    }
   }
 #undef PF
   return r;
@@ -1555,8 +1580,10 @@ int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next,
     r = kl_rmsnorm(e->pf_x + static_cast<size_t>(last_n - 1) * m.D, e->rms_final, e->pf_xlast, m.D,
                    e->eps, e->stream);
   if (r == KL_OK)
-    r = kl_gemv_f32(e->pf_xlast, static_cast<const float*>(e->wcls.w), e->logits, m.V, m.D, 1.f,
-                    e->stream);
+    r = e->quant ? kl_gemv_q8(e->pf_xlast, static_cast<const int8_t*>(e->wcls.w), e->wcls.s,
+                              e->logits, m.V, m.D, m.gs, e->stream)
+                 : kl_gemv_f32(e->pf_xlast, static_cast<const float*>(e->wcls.w), e->logits, m.V,
+                               m.D, 1.f, e->stream);
   if (r == KL_OK) r = kl_argmax(e->logits, m.V, e->pf_next, e->pf_am, e->pf_am_bytes, e->stream);
   if (r != KL_OK) return r;
   err = hipEventRecord(e->ev1, e->stream);

@@ -25,43 +25,27 @@
 // projections) in one grid, and split-K divides the K blocks among
 // blockIdx.y with a fixed-order reduction, so that narrow outputs (few tiles)
 // still fill the chip.
+//
+// int8 weights (Q8): W holds int8 [N x ldw] with one fp32 scale per 2^gshift
+// consecutive elements of the flattened matrix (the image's group-wise
+// layout, export_llama.py:49-73).  Each thread loads the 4 bytes that stand in
+// for one float4 of the fp32 path and its group's scale, and stores
+// float(q) * scale to LDS (the dequantised weight of the reference's int8
+// GEMV, cuda/matmul_kernel.cu:73); the MFMA loop is the same.  K must be a
+// whole number of blocks.
 #pragma once
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+
+#include "gemm_run.hpp"
 
 namespace kl {
 
 typedef float gf4 __attribute__((ext_vector_type(4)));
 typedef float gf16 __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmBK = 32;
-constexpr int kGemmLDK = kGemmBK + 4;  // padded LDS row (floats)
-constexpr int kGemmMaxSeg = 3;
-
-// One output of a grouped GEMM: C_s = A . W_s^T (+ bias_s) over the same A.
-struct GemmSeg {
-  const float* W;
-  float* C;
-  const float* bias;
-  int N, ldw, ldc;
-  int tile0;  // first workgroup tile of this segment
-};
-
-struct GemmArgs {
-  const float* A;
-  int M, K, lda;
-  int accumulate;  // C += product (else C = product)
-  int tiles_m;
-  int nseg;
-  GemmSeg seg[kGemmMaxSeg];
-  // Split-K (one segment only): blockIdx.y = split; the partial products go
-  // to ws[split][M][N] and k_gemm_reduce applies bias and accumulate.
-  float* ws;
-  int splits;
-};
-
-template <int WM, int WN, int TM, int TN>
+template <int WM, int WN, int TM, int TN, bool Q8 = false>
 __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm_f32(
     GemmArgs g) {
   constexpr int BM = WM * TM * 32, BN = WN * TN * 32, BK = kGemmBK, LDK = kGemmLDK;
@@ -78,20 +62,23 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
   for (int i = 1; i < kGemmMaxSeg; ++i)
     if (i < g.nseg && static_cast<int>(blockIdx.x) >= g.seg[i].tile0) sidx = i;
   const float* __restrict__ A = g.A;
-  const float* __restrict__ W = g.seg[0].W;
+  const void* W = g.seg[0].W;
   float* C = g.seg[0].C;
   const float* bias = g.seg[0].bias;
-  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0;
+  const float* S = g.seg[0].S;
+  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0, gshift = g.seg[0].gshift;
 #pragma unroll
   for (int i = 1; i < kGemmMaxSeg; ++i)
     if (i == sidx) {
       W = g.seg[i].W;
       C = g.seg[i].C;
       bias = g.seg[i].bias;
+      S = g.seg[i].S;
       N = g.seg[i].N;
       ldw = g.seg[i].ldw;
       ldc = g.seg[i].ldc;
       tile0 = g.seg[i].tile0;
+      gshift = g.seg[i].gshift;
     }
   const int M = g.M, K = g.K, lda = g.lda;
   // Tiles along M are adjacent in launch order, so the workgroups that share
@@ -113,6 +100,8 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
   // (K not a multiple of BK) zeroes columns past K, in both operands.
   static_assert(A4 % NT == 0 && W4 % NT == 0, "whole float4 loads per thread");
   gf4 ra[LA], rw[LW];
+  int rq[LW];     // int8: four weights per thread and load
+  float rs[LW];   // int8: their group's scale
   unsigned int offa[LA], offw[LW], colok_a[LA], colok_w[LW];
   unsigned int lofa[LA], lofw[LW];
 #pragma unroll
@@ -129,14 +118,23 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
     const int idx = tid + i * NT;
     const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
     const int n = min(n0 + r, N - 1);
-    offw[i] = static_cast<unsigned int>((n * ldw + c) * 4);
+    // fp32: byte offset; int8: element (= byte) offset.
+    offw[i] = static_cast<unsigned int>((n * ldw + c) * (Q8 ? 1 : 4));
     colok_w[i] = static_cast<unsigned int>(c);
     lofw[i] = static_cast<unsigned int>(r * LDK + c);
   }
   auto gload = [&](int k0) {
     const char* ba = reinterpret_cast<const char*>(A) + static_cast<size_t>(k0) * 4;
-    const char* bw = reinterpret_cast<const char*>(W) + static_cast<size_t>(k0) * 4;
-    if (k0 + BK <= K) {
+    const char* bw = reinterpret_cast<const char*>(W) + static_cast<size_t>(k0) * (Q8 ? 1 : 4);
+    if constexpr (Q8) {  // whole blocks only
+#pragma unroll
+      for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const gf4*>(ba + offa[i]);
+#pragma unroll
+      for (int i = 0; i < LW; ++i) {
+        rq[i] = *reinterpret_cast<const int*>(bw + offw[i]);
+        rs[i] = S[(offw[i] + static_cast<unsigned int>(k0)) >> gshift];
+      }
+    } else if (k0 + BK <= K) {
 #pragma unroll
       for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const gf4*>(ba + offa[i]);
 #pragma unroll
@@ -160,8 +158,18 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < LA; ++i) *reinterpret_cast<gf4*>(&As[buf][lofa[i]]) = ra[i];
+    if constexpr (Q8) {
 #pragma unroll
-    for (int i = 0; i < LW; ++i) *reinterpret_cast<gf4*>(&Ws[buf][lofw[i]]) = rw[i];
+      for (int i = 0; i < LW; ++i) {
+        const int q = rq[i];
+        const gf4 w = {static_cast<float>((q << 24) >> 24) * rs[i], static_cast<float>((q << 16) >> 24) * rs[i],
+                       static_cast<float>((q << 8) >> 24) * rs[i], static_cast<float>(q >> 24) * rs[i]};
+        *reinterpret_cast<gf4*>(&Ws[buf][lofw[i]]) = w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < LW; ++i) *reinterpret_cast<gf4*>(&Ws[buf][lofw[i]]) = rw[i];
+    }
   };
 
   gf16 acc[TM][TN];

@@ -1,0 +1,43 @@
+// The prefill GEMM's launch interface (kernel in gemm.hpp, launcher in
+// ops.hip): what a caller outside ops.hip needs to run it with fp32 or int8
+// weight segments.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace kl {
+
+constexpr int kGemmBK = 32;
+constexpr int kGemmLDK = kGemmBK + 4;  // padded LDS row (floats)
+constexpr int kGemmMaxSeg = 3;
+
+// One output of a grouped GEMM: C_s = A . W_s^T (+ bias_s) over the same A.
+struct GemmSeg {
+  const void* W;     // fp32, or int8 with scales S
+  float* C;
+  const float* bias;
+  int N, ldw, ldc;
+  int tile0;         // first workgroup tile of this segment
+  const float* S;    // int8 group scales (nullptr: fp32 weights)
+  int gshift;        // int8 group size = 1 << gshift
+};
+
+struct GemmArgs {
+  const float* A;
+  int M, K, lda;
+  int accumulate;  // C += product (else C = product)
+  int tiles_m;
+  int nseg;
+  GemmSeg seg[kGemmMaxSeg];
+  // Split-K (one segment only): blockIdx.y = split; the partial products go
+  // to ws[split][M][N] and k_gemm_reduce applies bias and accumulate.
+  float* ws;
+  int splits;
+};
+
+// Host launcher (ops.hip): C_s (+)= A . W_s^T (+ bias_s) for nseg outputs in
+// one grid; splits > 1 (nseg == 1) divides K among blockIdx.y into
+// ws[splits][M][N] and reduces.  Every segment is fp32 or every one int8.
+int gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs, int accumulate,
+             float* ws, int splits, hipStream_t st);
+
+}  // namespace kl

@@ -705,13 +705,31 @@ bool gemm_shape_ok(const float* A, int M, int K, int lda) {
   return A && M > 0 && K > 0 && lda >= K;
 }
 
+}  // namespace
+
 // C_s (+)= A . W_s^T (+ bias_s) for nseg outputs in one grid; splits > 1
 // (nseg == 1) divides K among blockIdx.y into ws[splits][M][N] and reduces.
-int gemm_launch(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs, int accumulate,
-                float* ws, int splits, hipStream_t st) {
+int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs,
+                 int accumulate, float* ws, int splits, hipStream_t st) {
+  if (!gemm_shape_ok(A, M, K, lda) || nseg < 1 || nseg > kGemmMaxSeg || splits < 1 ||
+      (splits > 1 && (nseg != 1 || !ws)))
+    return KL_EINVAL;
   if (K % 4 || lda % 4 || !aligned16(A)) return KL_EUNSUPP;
   // The kernel addresses each operand with 32-bit byte offsets.
   if (static_cast<size_t>(M) * lda * sizeof(float) > 0xFFFFFFFFu) return KL_EUNSUPP;
+  const bool q8 = segs[0].S != nullptr;
+  if (q8) {
+    // int8: whole K blocks, the image's dense rows (ldw == K), 4-byte loads.
+    if (K % kGemmBK) return KL_EUNSUPP;
+    for (int i = 0; i < nseg; ++i) {
+      const GemmSeg& sg = segs[i];
+      if (!sg.S || sg.ldw != K || (reinterpret_cast<uintptr_t>(sg.W) & 3u) || sg.gshift < 2 ||
+          sg.gshift > 20)
+        return KL_EUNSUPP;
+      if (!sg.W || !sg.C || sg.N <= 0 || sg.ldc < sg.N) return KL_EINVAL;
+      if (static_cast<size_t>(sg.N) * sg.ldw > 0xFFFFFFFFu) return KL_EUNSUPP;
+    }
+  }
   GemmArgs g{};
   g.A = A;
   g.M = M;
@@ -725,16 +743,22 @@ int gemm_launch(const float* A, int M, int K, int lda, int nseg, const GemmSeg* 
   long long tiles = 0;
   for (int i = 0; i < nseg; ++i) {
     const GemmSeg& sg = segs[i];
-    if (!sg.W || !sg.C || sg.N <= 0 || sg.ldw < K || sg.ldc < sg.N) return KL_EINVAL;
-    if (sg.ldw % 4 || !aligned16(sg.W)) return KL_EUNSUPP;
-    if (static_cast<size_t>(sg.N) * sg.ldw * sizeof(float) > 0xFFFFFFFFu) return KL_EUNSUPP;
+    if (!q8) {
+      if (sg.S || !sg.W || !sg.C || sg.N <= 0 || sg.ldw < K || sg.ldc < sg.N) return KL_EINVAL;
+      if (sg.ldw % 4 || !aligned16(sg.W)) return KL_EUNSUPP;
+      if (static_cast<size_t>(sg.N) * sg.ldw * sizeof(float) > 0xFFFFFFFFu) return KL_EUNSUPP;
+    }
     g.seg[i] = sg;
     g.seg[i].tile0 = static_cast<int>(tiles);
     tiles += static_cast<long long>(g.tiles_m) * ((sg.N + kGemmTile - 1) / kGemmTile);
   }
   if (tiles > INT_MAX) return KL_EUNSUPP;
-  hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(static_cast<unsigned>(tiles), splits), dim3(256),
-                     0, st, g);
+  if (q8)
+    hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1, true>), dim3(static_cast<unsigned>(tiles), splits),
+                       dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(static_cast<unsigned>(tiles), splits), dim3(256),
+                       0, st, g);
   int r = launch_rc();
   if (r != KL_OK || splits == 1) return r;
   const GemmSeg& sg = segs[0];
@@ -744,7 +768,6 @@ int gemm_launch(const float* A, int M, int K, int lda, int nseg, const GemmSeg* 
                      sg.bias, accumulate);
   return launch_rc();
 }
-}  // namespace
 
 extern "C" {
 
@@ -752,7 +775,7 @@ int kl_gemm_f32(const float* A, const float* W, float* C, int M, int N, int K, i
                 int ldc, const float* bias, int accumulate, void* stream) {
   if (!gemm_shape_ok(A, M, K, lda) || !W || !C || N <= 0 || ldw < K || ldc < N) return KL_EINVAL;
   const GemmSeg sg{W, C, bias, N, ldw, ldc, 0};
-  return gemm_launch(A, M, K, lda, 1, &sg, accumulate, nullptr, 1, as_stream(stream));
+  return gemm_run(A, M, K, lda, 1, &sg, accumulate, nullptr, 1, as_stream(stream));
 }
 
 int kl_gemm_f32_grouped(const float* A, int M, int K, int lda, int n_seg, const float* const* W,
@@ -764,7 +787,22 @@ int kl_gemm_f32_grouped(const float* A, int M, int K, int lda, int n_seg, const 
   GemmSeg segs[kGemmMaxSeg];
   for (int i = 0; i < n_seg; ++i)
     segs[i] = GemmSeg{W[i], C[i], bias ? bias[i] : nullptr, N[i], ldw[i], ldc[i], 0};
-  return gemm_launch(A, M, K, lda, n_seg, segs, accumulate, nullptr, 1, as_stream(stream));
+  return gemm_run(A, M, K, lda, n_seg, segs, accumulate, nullptr, 1, as_stream(stream));
+}
+
+int kl_gemm_q8(const float* A, const int8_t* q, const float* scales, int group_size, float* C,
+               int M, int N, int K, int lda, int ldc, const float* bias, int accumulate, int splits,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  if (!gemm_shape_ok(A, M, K, lda) || !q || !scales || !C || N <= 0 || ldc < N || splits < 1 ||
+      splits > 16 || group_size < 4 || (group_size & (group_size - 1)))
+    return KL_EINVAL;
+  if (splits > 1 && (!workspace || workspace_bytes < static_cast<size_t>(splits) * M * N * sizeof(float)))
+    return KL_EWORKSPACE;
+  int gshift = 0;
+  while ((1 << gshift) < group_size) ++gshift;
+  GemmSeg sg{q, C, bias, N, K, ldc, 0, scales, gshift};
+  return gemm_run(A, M, K, lda, 1, &sg, accumulate, static_cast<float*>(workspace), splits,
+                  as_stream(stream));
 }
 
 int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, int K, int lda,
@@ -776,7 +814,7 @@ int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, i
   if (splits > 1 && (!workspace || workspace_bytes < static_cast<size_t>(splits) * M * N * sizeof(float)))
     return KL_EWORKSPACE;
   const GemmSeg sg{W, C, bias, N, ldw, ldc, 0};
-  return gemm_launch(A, M, K, lda, 1, &sg, accumulate, static_cast<float*>(workspace), splits,
+  return gemm_run(A, M, K, lda, 1, &sg, accumulate, static_cast<float*>(workspace), splits,
                      as_stream(stream));
 }
 

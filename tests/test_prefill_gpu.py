@@ -182,10 +182,10 @@ def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
 
 
 # ------------------------------------------------------- whole prompt -------
-FP32_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3"]
+PREFILL_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"]
 
 
-@pytest.mark.parametrize("name", FP32_TINY)
+@pytest.mark.parametrize("name", PREFILL_TINY)
 def test_engine_prefill_vs_oracle(K, O, gpu, name):
     cfg = K.TINY[name]
     img = K.synth_image(cfg)
@@ -256,7 +256,7 @@ def test_qwen3_shape_prefill_512_vs_oracle(K, O, gpu):
         assert n2 == tok, pos
 
 
-@pytest.mark.parametrize("name", FP32_TINY)
+@pytest.mark.parametrize("name", PREFILL_TINY)
 def test_generate_with_prefill_matches_oracle(K, O, gpu, name):
     cfg = K.TINY[name]
     img = K.synth_image(cfg)
@@ -268,15 +268,45 @@ def test_generate_with_prefill_matches_oracle(K, O, gpu, name):
     assert list(got) == list(want)
 
 
-def test_prefill_unsupported_for_int8(K, gpu):
-    cfg = K.TINY["tiny_q8"]
-    eng = K.Engine(K.synth_image(cfg), cfg)
-    assert K.lib.kl_engine_set_prefill(eng.handle, 1) == -4
-    p = np.ascontiguousarray(K.prompt_tokens(cfg, 4), np.int32)
-    assert K.lib.kl_engine_prefill(eng.handle, p.ctypes.data, 4, None, None, None) == -4
+@pytest.mark.parametrize("M,N,Kd,gs,splits", [(1, 5, 64, 64, 1), (37, 200, 256, 64, 1),
+                                              (100, 192, 1024, 64, 4), (64, 96, 128, 32, 2),
+                                              (7, 33, 4096, 128, 3)])
+def test_gemm_q8_vs_oracle(K, O, gpu, M, N, Kd, gs, splits):
+    """int8 weights (group-wise scales over the flattened matrix): every row of
+    C within the fp32 GEMV bound of the oracle's int8 MatmulKernel on that
+    row, with bias and accumulate, with and without split-K."""
+    rng = np.random.default_rng(M * 7 + N)
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    Wf = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
+    q, s = O.quantize_q8(Wf.reshape(-1), gs)
+    bias = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    dA, dq, ds, db, dC = D(K, A), D(K, q), D(K, s), D(K, bias), D(K, C0)
+    ws = K.DeviceArray(max(1, splits * M * N))
+    ok(K.lib.kl_gemm_q8(dA.ptr, dq.ptr, ds.ptr, gs, dC.ptr, M, N, Kd, Kd, N, db.ptr, 1, splits,
+                        ws.ptr, ws.nbytes, None), "kl_gemm_q8")
+    y = dC.numpy().reshape(M, N)
+    wd = O.dequant_q8(q, s, gs).reshape(N, Kd).astype(np.float64)
+    for m in range(M):
+        g = O.gemv_q8(A[m], q, s, N, Kd, gs)
+        want = C0[m].astype(np.float64) + g + bias
+        tol = 4e-7 * np.sqrt(Kd) * (np.abs(wd) @ np.abs(A[m])).max() + 1e-6
+        assert np.max(np.abs(y[m] - want)) <= tol, m
 
 
-@pytest.mark.parametrize("name,P", [("qwen3_4b", 512), ("qwen25_15b", 4000)])
+def test_gemm_q8_rejects_bad_shapes(K, gpu):
+    buf = K.DeviceArray(4096)
+    # K not a whole number of 32-column blocks; group size not a power of two
+    assert K.lib.kl_gemm_q8(buf.ptr, buf.ptr, buf.ptr, 64, buf.ptr, 2, 2, 48, 48, 2, None, 0, 1,
+                            None, 0, None) == -4
+    assert K.lib.kl_gemm_q8(buf.ptr, buf.ptr, buf.ptr, 48, buf.ptr, 2, 2, 64, 64, 2, None, 0, 1,
+                            None, 0, None) == -1
+    # split-K without a large enough workspace
+    assert K.lib.kl_gemm_q8(buf.ptr, buf.ptr, buf.ptr, 64, buf.ptr, 2, 2, 64, 64, 2, None, 0, 2,
+                            buf.ptr, 4, None) == -6
+
+
+@pytest.mark.parametrize("name,P", [("qwen3_4b", 512), ("qwen25_15b", 4000), ("llama2_7b_q8", 300)])
 def test_full_size_prefill_vs_steps(K, gpu, name, P):
     cfg = K.BASELINE[name]
     img = K.synth_image(cfg)
