@@ -1523,7 +1523,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
       const int sp = prefill_splits(n, D, Dq);
-      if (static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
+      if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
       PF(gemm_run(e->pf_att, n, Dq, Dq, 1, &sg, 1, e->pf_ws, sp, hs));
     }
     // feed_forward (llama3.cpp:671-719)
@@ -1537,7 +1537,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     {
       const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
       const int sp = prefill_splits(n, D, F);
-      if (static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
+      if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
       PF(gemm_run(e->pf_h1, n, F, F, 1, &sg, 1, e->pf_ws, sp, hs));
     }
   }

@@ -313,17 +313,16 @@ __device__ __forceinline__ tagged2 g_ld_pair(__amdgpu_buffer_rsrc_t r, int pair)
 // scalar r is applied to the GEMV's row totals (W y = r (W (w * x))): the
 // per-wave sums of squares go to ssq[kPWaves] and norm_scale() combines them
 // after the closing barrier, so the norm adds no barrier or extra pass over
-// the vector to the hand-off.  n is even; each thread takes pairs of
-// elements, 8 pairs per round.
+// the vector to the hand-off.  Each thread takes 8 elements per round.
 // The phase's first weight segment is already in flight when the polling
 // starts (the polls' answers wait for it: loads return in order).  Measured on
 // Llama-3.2-1B with the short-context attention: +1.6% against issuing it
 // after the staging (with the chunked attention and its merge hand-off the
 // same change had measured -1.5%).
 // Ends with a workgroup barrier.
-__device__ __forceinline__ void stage_vec_single(const PArgs& a, const tagged_t* src, unsigned int tag,
-                                          const float* emb_row, const float* nw, int n, float* xs,
-                                          float* ssq) {
+__device__ __forceinline__ void stage_vec_single(const PArgs& a, const tagged_t* src,
+                                                 unsigned int tag, const float* emb_row,
+                                                 const float* nw, int n, float* xs, float* ssq) {
   constexpr int T = kPThreads;
   const int tid = threadIdx.x;
   float ss = 0.f;
@@ -369,10 +368,11 @@ __device__ __forceinline__ void stage_vec_single(const PArgs& a, const tagged_t*
   __syncthreads();
 }
 
-
-__device__ __forceinline__ void stage_vec_pairs(const PArgs& a, const tagged_t* src, unsigned int tag,
-                                          const float* emb_row, const float* nw, int n, float* xs,
-                                          float* ssq) {
+// stage_vec_single with two adjacent elements per load (n even): each thread
+// takes 8 pairs per round, and a pair with a stale element is polled again.
+__device__ __forceinline__ void stage_vec_pairs(const PArgs& a, const tagged_t* src,
+                                                unsigned int tag, const float* emb_row,
+                                                const float* nw, int n, float* xs, float* ssq) {
   constexpr int T = kPThreads;
   constexpr int E = 8;  // pairs per thread per round
   const int tid = threadIdx.x;
