@@ -42,7 +42,7 @@ def test_usage_and_errors():
 def images(K, tmp_path_factory):
     d = tmp_path_factory.mktemp("gen")
     out = {}
-    for name in ("tiny_llama3", "tiny_qwen2", "tiny_qwen3"):
+    for name in ("tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"):
         cfg = K.TINY[name]
         p = str(d / f"{name}.bin")
         K.synth_image(cfg).tofile(p)
@@ -52,7 +52,9 @@ def images(K, tmp_path_factory):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,flags", [("tiny_llama3", []), ("tiny_qwen2", ["--layered"]),
-                                        ("tiny_qwen3", ["--prefill"])])
+                                        ("tiny_qwen3", ["--prefill"]),
+                                        ("tiny_q8", ["--quant", "--prefill"]),
+                                        ("tiny_qwen2_q8", ["--quant", "--prefill"])])
 def test_single_shot_matches_oracle(K, O, gpu, images, name, flags):
     cfg, path = images[name]
     prompt = [int(t) for t in K.prompt_tokens(cfg, 6)]
