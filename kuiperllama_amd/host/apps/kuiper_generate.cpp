@@ -23,7 +23,9 @@
 // Options: --family llama2|llama3|qwen2|qwen3 (default llama2), --quant (int8
 // image), --layered (the layer-by-layer path instead of the fused engine),
 // --prefill (the whole prompt in one batched pass; fused only), --eos ID
-// (end-of-sequence id, repeatable), --tokenizer FILE.
+// (end-of-sequence id, repeatable), --tokenizer FILE, --profile (per-operation
+// device times of the generation on stderr, one [PROFILE] line per operation:
+// the reference's op profile, main_qwen.cpp:287-310, timed on the device).
 //
 // Generation follows main_qwen.cpp: prompt positions advance without
 // sampling; in the decode phase only, generation stops at an end-of-sequence
@@ -51,6 +53,7 @@ struct Options {
   bool prefill = false;
   std::vector<int32_t> eos;
   std::string tokenizer;
+  bool profile = false;
 };
 
 struct GenerationResult {
@@ -126,6 +129,13 @@ std::string response_text(const std::string& decoded) {
   std::string out;
   for (size_t i = 0; i < kept.size(); ++i) out += (i ? "\n" : "") + kept[i];
   return trim(out);
+}
+
+void print_profile(const model::Model& m) {
+  for (const model::OpProfileStat& st : m.get_profile_stats())
+    std::fprintf(stderr, "[PROFILE] op=%s calls=%lld total_ms=%.4f avg_ms=%.5f\n", st.op_name.c_str(),
+                 static_cast<long long>(st.calls), st.total_ms, st.avg_ms);
+  std::fflush(stderr);
 }
 
 std::string join_ids(const std::vector<int32_t>& ids) {
@@ -281,7 +291,7 @@ int usage(const char* prog) {
                "Usage:\n  %s [options] <model.bin> <ids|prompt> [max_new_tokens]\n"
                "  %s --serve [options] <model.bin> [max_new_tokens]\n"
                "Options: --family llama2|llama3|qwen2|qwen3, --quant, --layered, --prefill, "
-               "--eos ID, --tokenizer FILE (prompts and responses as text)\n",
+               "--eos ID, --tokenizer FILE (prompts and responses as text), --profile\n",
                prog, prog);
   return 2;
 }
@@ -309,6 +319,8 @@ int main(int argc, char** argv) {
       o.prefill = true;
     } else if (a == "--eos" && i + 1 < argc) {
       o.eos.push_back(std::atoi(argv[++i]));
+    } else if (a == "--profile") {
+      o.profile = true;
     } else if (a == "--tokenizer" && i + 1 < argc) {
       o.tokenizer = argv[++i];
       if (o.tokenizer.empty()) return usage(argv[0]);
@@ -378,11 +390,13 @@ int main(int argc, char** argv) {
         std::fflush(stdout);
         continue;
       }
+      if (o.profile) m->reset_profile_stats();
       const auto t0 = std::chrono::steady_clock::now();
       const GenerationResult r = generate(*m, prompt, max_steps, o.prefill, tok);
       const double dt =
           std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
       print_result(*m, r, dt, false, tok);
+      if (o.profile) print_profile(*m);
     }
     return 0;
   }
@@ -414,9 +428,11 @@ int main(int argc, char** argv) {
     return 2;
   }
   if (o.prefill) STATUS_CHECK(m->set_prefill(true));
+  if (o.profile) m->reset_profile_stats();
   const auto t0 = std::chrono::steady_clock::now();
   const GenerationResult r = generate(*m, prompt, max_steps, o.prefill, tok);
   const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   print_result(*m, r, dt, true, tok);
+  if (o.profile) print_profile(*m);
   return 0;
 }

@@ -89,6 +89,15 @@ struct DecoderLayers {
   void to_hip(const std::shared_ptr<kernel::HipConfig>& config);
 };
 
+// One operation's device time over the profiled predict() calls
+// (model/qwen2.h:13-18).
+struct OpProfileStat {
+  std::string op_name;
+  double total_ms = 0.0;
+  int64_t calls = 0;
+  double avg_ms = 0.0;
+};
+
 class Model {
  public:
   explicit Model(base::TokenizerType tokenizer_type, base::ModelType model_type,
@@ -145,6 +154,15 @@ class Model {
   // tokenizer's (encode.cpp); the only ones when no tokenizer is loaded.
   void set_eos_tokens(std::vector<int32_t> ids) { eos_tokens_ = std::move(ids); }
   std::shared_ptr<kernel::HipConfig> hip_config() const { return hip_config_; }
+  // Per-operation profile of predict() (qwen2.cpp:20-57, :820-822), timed on
+  // the device: HIP events on the model's stream bracket each operation (the
+  // reference times the host-side launch).  Names as the reference's
+  // ("attn.rmsnorm", "attn.wq", ..., "ffn.w2", "output.cls", "sampler.argmax",
+  // plus "input.embedding" for embedding()); the fused step is one
+  // "fused.step" per token and prefill() one "prefill.batched".  Off until
+  // reset_profile_stats() is called; each profiled call waits for the device.
+  void reset_profile_stats() const;
+  std::vector<OpProfileStat> get_profile_stats() const;
 
  protected:
   base::Status insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor);
@@ -162,6 +180,11 @@ class Model {
   void feed_forward(int32_t layer_idx, const tensor::Tensor& input) const;
   void cls_logits(const tensor::Tensor& input) const;
   int32_t post_processing(const tensor::Tensor& pos, bool is_prompt) const;
+  // Runs fn, bracketed by profile events on `stream` (default: the model's)
+  // when profiling is on.
+  template <class Fn>
+  void profiled(const char* name, Fn&& fn, void* stream = nullptr) const;
+  void resolve_profile() const;
 
   int32_t group_size_ = 1;
   bool is_quant_model_ = false;
@@ -182,6 +205,16 @@ class Model {
   std::vector<int32_t> eos_tokens_;
   std::unique_ptr<op::EncodeLayerBase> encode_layer_;
   kl_engine* engine_ = nullptr;
+  struct ProfileRecord {
+    const char* name;
+    void* start;
+    void* stop;
+  };
+  mutable bool profiling_ = false;
+  mutable std::map<std::string, std::pair<double, int64_t>> profile_;
+  mutable std::vector<ProfileRecord> profile_pending_;
+  mutable std::vector<void*> profile_events_;  // free events for reuse
+  mutable std::vector<void*> profile_all_events_;
 };
 
 // Llama2 (default) and Llama3 (family kLlama3) checkpoints.

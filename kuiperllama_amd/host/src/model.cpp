@@ -63,10 +63,73 @@ Model::Model(base::TokenizerType tokenizer_type, base::ModelType model_type,
 Model::~Model() {
   if (engine_) kl_engine_destroy(engine_);
   engine_ = nullptr;
+  for (void* ev : profile_all_events_) kl_event_destroy(ev);
   // Layers and buffers release their device memory before the stream goes.
   layers_.reset();
   buffers_.clear();
   sampler_.reset();
+}
+
+template <class Fn>
+void Model::profiled(const char* name, Fn&& fn, void* stream) const {
+  if (!profiling_) {
+    fn();
+    return;
+  }
+  auto take = [&]() {
+    void* ev = nullptr;
+    if (!profile_events_.empty()) {
+      ev = profile_events_.back();
+      profile_events_.pop_back();
+    } else {
+      KUIPER_CHECK(kl_event_create(&ev) == KL_OK, "kl_event_create failed");
+      profile_all_events_.push_back(ev);
+    }
+    return ev;
+  };
+  void* start = take();
+  void* stop = take();
+  void* st = stream ? stream : hip_config_->stream;
+  KUIPER_CHECK(kl_event_record(start, st) == KL_OK, "kl_event_record failed");
+  fn();
+  KUIPER_CHECK(kl_event_record(stop, st) == KL_OK, "kl_event_record failed");
+  profile_pending_.push_back({name, start, stop});
+}
+
+// Waits for the streams and adds the pending operations' device times.
+void Model::resolve_profile() const {
+  if (profile_pending_.empty()) return;
+  KUIPER_CHECK(kl_device_sync() == KL_OK, "kl_device_sync failed");
+  for (const ProfileRecord& r : profile_pending_) {
+    float ms = 0.f;
+    KUIPER_CHECK(kl_event_elapsed_ms(r.start, r.stop, &ms) == KL_OK, "kl_event_elapsed_ms failed");
+    auto& acc = profile_[r.name];
+    acc.first += ms;
+    acc.second += 1;
+    profile_events_.push_back(r.start);
+    profile_events_.push_back(r.stop);
+  }
+  profile_pending_.clear();
+}
+
+void Model::reset_profile_stats() const {
+  resolve_profile();
+  profile_.clear();
+  profiling_ = true;
+}
+
+std::vector<OpProfileStat> Model::get_profile_stats() const {
+  resolve_profile();
+  std::vector<OpProfileStat> out;
+  for (const auto& [name, acc] : profile_) {
+    OpProfileStat st;
+    st.op_name = name;
+    st.total_ms = acc.first;
+    st.calls = acc.second;
+    st.avg_ms = acc.second ? acc.first / static_cast<double>(acc.second) : 0.0;
+    out.push_back(st);
+  }
+  return out;
 }
 
 // llama3.cpp:111-145 for kDeviceHIP.  The tokenizer is optional (token ids in
@@ -477,7 +540,10 @@ op::EmbeddingOutput Model::embedding(const std::vector<int>& tokens) const {
   }
   for (int32_t i = 0; i < n; ++i) input_tokens.index<int32_t>(i) = tokens[i];
   tensor::Tensor input_token_num(base::DataType::kDataTypeInt32, n);
-  STATUS_CHECK(layers_->embedding_layer_->forward(input_tokens, input_token_num, input_embeddings));
+  profiled("input.embedding", [&] {
+    STATUS_CHECK(layers_->embedding_layer_->forward(input_tokens, input_token_num, input_embeddings));
+  });
+  resolve_profile();
   return op::EmbeddingOutput(input_tokens, input_embeddings, input_token_num);
 }
 
@@ -499,10 +565,13 @@ tensor::Tensor Model::fill_input(const tensor::Tensor& pos_tensor,
   return input;
 }
 
-// The layer-by-layer step (llama3.cpp:146-166, :599-744; qwen2/qwen3 alike).
+// The layer-by-layer step (llama3.cpp:146-166, :599-744; qwen2/qwen3 alike),
+// with the reference's profile names (qwen2.cpp:648-800).
 void Model::attention_rms(int32_t layer_idx, const tensor::Tensor& input) const {
-  STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx)->forward(
-      input, get_buffer(ModelBufferType::kOutputRMSNorm)));
+  profiled("attn.rmsnorm", [&] {
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx)->forward(
+        input, get_buffer(ModelBufferType::kOutputRMSNorm)));
+  });
 }
 
 void Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
@@ -511,24 +580,30 @@ void Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) c
   const int32_t pos = pos_tensor.index<int32_t>(0);
   auto [key, val] = slice_kv_cache(layer_idx, pos);
   const tensor::Tensor& rms = get_buffer(ModelBufferType::kOutputRMSNorm);
-  STATUS_CHECK(layers_->wq_layers_.at(layer_idx)->forward(rms, query));
+  profiled("attn.wq", [&] { STATUS_CHECK(layers_->wq_layers_.at(layer_idx)->forward(rms, query)); });
   if (family_ == ModelFamily::kQwen3) {
     // Per-head q/k RMSNorm (qwen3.cpp:485-500).
     query.reshape({c.q_dim_ / c.head_size_, c.head_size_});
-    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 2 * c.layer_num_ + 1)->forward(query, query));
+    profiled("attn.q_norm", [&] {
+      STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 2 * c.layer_num_ + 1)->forward(query, query));
+    });
     query.reshape({c.q_dim_});
-    STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key));
+    profiled("attn.wk", [&] { STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key)); });
     key.reshape({c.kv_dim_ / c.head_size_, c.head_size_});
-    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 3 * c.layer_num_ + 1)->forward(key, key));
+    profiled("attn.k_norm", [&] {
+      STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 3 * c.layer_num_ + 1)->forward(key, key));
+    });
     key.reshape({c.kv_dim_});
   } else {
-    STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key));
+    profiled("attn.wk", [&] { STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key)); });
   }
-  STATUS_CHECK(layers_->wv_layers_.at(layer_idx)->forward(rms, val));
-  STATUS_CHECK(layers_->rope_layer_->forward(query, key, pos_tensor,
-                                             get_buffer(ModelBufferType::kSinCache),
-                                             get_buffer(ModelBufferType::kCosCache),
-                                             tensor::Tensor{}));
+  profiled("attn.wv", [&] { STATUS_CHECK(layers_->wv_layers_.at(layer_idx)->forward(rms, val)); });
+  profiled("attn.rope", [&] {
+    STATUS_CHECK(layers_->rope_layer_->forward(query, key, pos_tensor,
+                                               get_buffer(ModelBufferType::kSinCache),
+                                               get_buffer(ModelBufferType::kCosCache),
+                                               tensor::Tensor{}));
+  });
 }
 
 void Model::attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
@@ -536,38 +611,54 @@ void Model::attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) c
   auto mha = std::static_pointer_cast<op::MultiHeadAttention>(layers_->mha_layer_);
   mha->set_pos(pos_tensor.index<int32_t>(0));
   mha->set_layer_idx(layer_idx);
-  STATUS_CHECK(mha->forward(get_buffer(ModelBufferType::kQuery),
-                            get_buffer(ModelBufferType::kScoreStorage),
-                            get_buffer(ModelBufferType::kKeyCache),
-                            get_buffer(ModelBufferType::kValueCache), mha_output));
-  STATUS_CHECK(layers_->wo_layers_.at(layer_idx)->forward(
-      mha_output, get_buffer(ModelBufferType::kAttnOutput)));
+  profiled("attn.mha", [&] {
+    STATUS_CHECK(mha->forward(get_buffer(ModelBufferType::kQuery),
+                              get_buffer(ModelBufferType::kScoreStorage),
+                              get_buffer(ModelBufferType::kKeyCache),
+                              get_buffer(ModelBufferType::kValueCache), mha_output));
+  });
+  profiled("attn.wo", [&] {
+    STATUS_CHECK(layers_->wo_layers_.at(layer_idx)->forward(
+        mha_output, get_buffer(ModelBufferType::kAttnOutput)));
+  });
 }
 
 void Model::feed_forward(int32_t layer_idx, const tensor::Tensor& input) const {
   const auto& c = *config_;
-  STATUS_CHECK(layers_->add_layer_->forward(input, get_buffer(ModelBufferType::kAttnOutput), input));
+  profiled("ffn.residual_add1", [&] {
+    STATUS_CHECK(layers_->add_layer_->forward(input, get_buffer(ModelBufferType::kAttnOutput), input));
+  });
   const tensor::Tensor& ffn_norm = get_buffer(ModelBufferType::kFFNRMSNorm);
-  STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + c.layer_num_)->forward(input, ffn_norm));
+  profiled("ffn.rmsnorm", [&] {
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + c.layer_num_)->forward(input, ffn_norm));
+  });
   const tensor::Tensor& w1 = get_buffer(ModelBufferType::kW1Output);
   const tensor::Tensor& w3 = get_buffer(ModelBufferType::kW3Output);
-  STATUS_CHECK(layers_->w1_layers_.at(layer_idx)->forward(ffn_norm, w1));
-  STATUS_CHECK(layers_->w3_layers_.at(layer_idx)->forward(ffn_norm, w3));
-  STATUS_CHECK(layers_->swiglu_layer_->forward(w1, w3, w1));
+  profiled("ffn.w1", [&] { STATUS_CHECK(layers_->w1_layers_.at(layer_idx)->forward(ffn_norm, w1)); });
+  profiled("ffn.w3", [&] { STATUS_CHECK(layers_->w3_layers_.at(layer_idx)->forward(ffn_norm, w3)); });
+  profiled("ffn.swiglu", [&] { STATUS_CHECK(layers_->swiglu_layer_->forward(w1, w3, w1)); });
   const tensor::Tensor& w2 = get_buffer(ModelBufferType::kW2Output);
-  STATUS_CHECK(layers_->w2_layers_.at(layer_idx)->forward(w1, w2));
-  STATUS_CHECK(layers_->add_layer_->forward(input, w2, input));
+  profiled("ffn.w2", [&] { STATUS_CHECK(layers_->w2_layers_.at(layer_idx)->forward(w1, w2)); });
+  profiled("ffn.residual_add2", [&] { STATUS_CHECK(layers_->add_layer_->forward(input, w2, input)); });
 }
 
 void Model::cls_logits(const tensor::Tensor& input) const {
-  STATUS_CHECK(layers_->rmsnorm_layers_.at(2 * config_->layer_num_)->forward(input, input));
-  STATUS_CHECK(layers_->cls_layer_->forward(input, get_buffer(ModelBufferType::kForwardOutput)));
+  profiled("output.rmsnorm", [&] {
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(2 * config_->layer_num_)->forward(input, input));
+  });
+  profiled("output.cls", [&] {
+    STATUS_CHECK(layers_->cls_layer_->forward(input, get_buffer(ModelBufferType::kForwardOutput)));
+  });
 }
 
 int32_t Model::post_processing(const tensor::Tensor&, bool is_prompt) const {
   const tensor::Tensor& out = get_buffer(ModelBufferType::kForwardOutput);
   if (is_prompt) return -1;
-  return static_cast<int32_t>(sampler_->sample(out.ptr<float>(), out.size(), hip_config_->stream));
+  int32_t next = -1;
+  profiled("sampler.argmax", [&] {
+    next = static_cast<int32_t>(sampler_->sample(out.ptr<float>(), out.size(), hip_config_->stream));
+  });
+  return next;
 }
 
 base::Status Model::forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
@@ -595,6 +686,7 @@ base::Status Model::predict(const tensor::Tensor& input, const tensor::Tensor& p
     base::Status s = forward(input, pos_tensor, next);
     if (!s) return s;
     next = post_processing(pos_tensor, is_prompt);
+    resolve_profile();
     return base::error::Success();
   }
   const int32_t pos = pos_tensor.index<int32_t>(0);
@@ -608,7 +700,11 @@ base::Status Model::predict(const tensor::Tensor& input, const tensor::Tensor& p
     return base::error::InvalidArgument(
         "The fused step takes the input row that fill_input() returned for embedding().");
   int32_t sampled = -1;
-  int rc = kl_engine_step(engine_, tokens.index<int32_t>(row), pos, &sampled, nullptr);
+  int rc = KL_OK;
+  void* est = nullptr;
+  kl_engine_stream(engine_, &est);
+  profiled("fused.step", [&] { rc = kl_engine_step(engine_, tokens.index<int32_t>(row), pos, &sampled, nullptr); },
+           est);
   if (rc != KL_OK) return base::error::InternalError(std::string("kl_engine_step: ") + kl_error_string(rc));
   const float* d_logits = nullptr;
   kl_engine_buffers(engine_, &d_logits, nullptr, nullptr);
@@ -617,6 +713,7 @@ base::Status Model::predict(const tensor::Tensor& input, const tensor::Tensor& p
                      hip_config_->stream);
   if (rc == KL_OK) rc = kl_stream_sync(hip_config_->stream);
   if (rc != KL_OK) return base::error::InternalError("logits copy failed");
+  resolve_profile();
   next = is_prompt ? -1 : sampled;
   return base::error::Success();
 }
@@ -688,10 +785,16 @@ base::Status Model::prefill(const std::vector<int32_t>& prompt, int& next) const
   if (prompt.empty() || static_cast<int32_t>(prompt.size()) > config_->seq_len_)
     return base::error::InvalidArgument("The prompt does not fit the sequence length.");
   int32_t nx = -1;
+  float ms = 0.f;
   int rc = kl_engine_prefill(engine_, prompt.data(), static_cast<int>(prompt.size()), &nx, nullptr,
-                             nullptr);
+                             &ms);
   if (rc != KL_OK)
     return base::error::InternalError(std::string("kl_engine_prefill: ") + kl_error_string(rc));
+  if (profiling_) {  // the engine times the batched pass on its stream
+    auto& acc = profile_["prefill.batched"];
+    acc.first += ms;
+    acc.second += 1;
+  }
   const float* d_logits = nullptr;
   kl_engine_buffers(engine_, &d_logits, nullptr, nullptr);
   const tensor::Tensor& out = get_buffer(ModelBufferType::kForwardOutput);

@@ -262,3 +262,46 @@ def test_text_serve_protocol(O, gpu, text_images):
         want = expected(O, cfg, path, got_prompts[k], 6, stops)
         assert got_resp[k] == want
         assert blocks[k] == response_text(dec(want)) + "\n"
+
+
+def profile_lines(stderr):
+    out = {}
+    for line in stderr.splitlines():
+        if line.startswith("[PROFILE] "):
+            kv = dict(f.split("=", 1) for f in line[len("[PROFILE] "):].split())
+            out[kv["op"]] = (int(kv["calls"]), float(kv["total_ms"]), float(kv["avg_ms"]))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("flags", [["--layered"], [], ["--prefill"]])
+def test_profile_counts_operations(K, gpu, images, flags):
+    """--profile (the reference's per-operation profile, timed on the device):
+    the layer-by-layer step reports every operation once per layer and
+    position, the sampler once per decode step; the fused step one
+    "fused.step" per position (the batched prefill one "prefill.batched")."""
+    cfg, path = images["tiny_llama3"]
+    P, max_new = 6, 9
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    p = run(["--family", "llama3", "--profile"] + flags + [path, ",".join(map(str, prompt)), str(max_new)])
+    assert p.returncode == 0, p.stderr
+    steps = int(p.stderr.split("[STATS] steps=")[1].split()[0])
+    prof = profile_lines(p.stderr)
+    print(flags, steps, prof, flush=True)
+    assert prof and all(t >= 0 and n > 0 for n, t, _ in prof.values())
+    decode = len(response(p.stdout))  # sampled positions that produced a response token
+    if flags == ["--layered"]:
+        L = cfg.layers
+        for op in ("attn.rmsnorm", "attn.wq", "attn.wk", "attn.wv", "attn.rope", "attn.mha", "attn.wo",
+                   "ffn.rmsnorm", "ffn.w1", "ffn.w3", "ffn.swiglu", "ffn.w2", "ffn.residual_add1",
+                   "ffn.residual_add2"):
+            assert prof[op][0] == steps * L, op
+        assert prof["output.cls"][0] == steps
+        assert prof["sampler.argmax"][0] == steps - (P - 1)
+        assert prof["attn.wq"][1] > 0
+    elif flags == ["--prefill"]:
+        assert prof["prefill.batched"][0] == 1 and prof["prefill.batched"][1] > 0
+        assert prof["fused.step"][0] == steps - P
+    else:
+        assert prof["fused.step"][0] == steps and prof["fused.step"][1] > 0
+    assert decode >= 1
