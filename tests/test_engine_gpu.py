@@ -351,6 +351,46 @@ def test_other_baseline_shapes_full(K, O, gpu, name, steps):
         del eng, om
 
 
+# ------------------------------------------------------- medium widths ----
+# Shapes between the tiny models and the BASELINE configs, where a weight row
+# spans several 4 KiB segments with a partial last one (fp32 D = 1536, F =
+# 4608; int8 D = 5120, F = 5632: rows of 5 and 5.5 KiB), against the oracle.
+MID = {
+    "mid_llama3": lambda K: K.BASELINE["llama32_1b"].with_(
+        name="mid_llama3", dim=2048, hidden_dim=4096, layers=2, heads=16, kv_heads=4,
+        vocab=1000, seq_len=128, norm_std=NORMS, prompt_len=8, decode_steps=24),
+    "mid_qwen2": lambda K: K.BASELINE["qwen25_15b"].with_(
+        name="mid_qwen2", hidden_dim=4608, layers=2, vocab=1000, seq_len=128, norm_std=NORMS,
+        prompt_len=8, decode_steps=24),
+    "mid_q8": lambda K: K.BASELINE["llama2_7b_q8"].with_(
+        name="mid_q8", dim=5120, hidden_dim=5632, layers=2, heads=40, kv_heads=40, vocab=1000,
+        seq_len=64, norm_std=NORMS, prompt_len=6, decode_steps=12),
+}
+
+
+@pytest.mark.parametrize("name", list(MID))
+def test_medium_width_parity(K, O, gpu, name):
+    """Every step's logits within 1e-4 of the oracle and no argmax
+    disagreement, teacher forced, in every mode; then free-running greedy
+    tokens identical to the oracle's."""
+    cfg = MID[name](K)
+    img = K.synth_image(cfg)
+    prompt = K.prompt_tokens(cfg)
+    for mode in MODES:
+        say("case", name, mode)
+        eng, om, worst, mm = teacher_forced(K, O, cfg, img, prompt, cfg.decode_steps, mode=mode)
+        say(name, mode, "worst logits rel err", worst, "near-ties", mm)
+        assert not mm
+        for layer in (0, cfg.layers - 1):
+            for pos in (0, cfg.prompt_len):
+                for v in (False, True):
+                    assert rel(eng.kv_row(layer, pos, v), om.kv_row(layer, pos, v)) < 1e-4
+        del eng, om
+    want = O.Model(img, cfg.family, cfg.quant).generate(prompt, cfg.decode_steps)
+    got, _ = K.Engine(img, cfg).generate(prompt, cfg.decode_steps)
+    assert list(got) == list(want)
+
+
 # ----------------------------- long contexts on the benchmarked attention ----
 def long_context(K, O, cfg, n_pos, check, n_greedy):
     """Teacher-forces `n_pos` seeded prompt positions through a persistent and
