@@ -312,9 +312,9 @@ int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, in
  * greedy token, logits (host, may be NULL) the vocab logits of position P-1.
  * Same result as P kl_engine_step calls up to float rounding; a following
  * kl_engine_step(e, *next, P, ...) continues the sequence.  Chunks of at most
- * 1024 positions.  KL_EUNSUPP for int8 images and head sizes other than 32,
- * 64, 128.  Blocks until done; *prefill_ms (may be NULL) receives its device
- * time. */
+ * 1024 positions.  KL_EUNSUPP for head sizes other than 32, 64, 128 (and for
+ * int8 images whose dimensions are not whole 32-column blocks).  Blocks until
+ * done; *prefill_ms (may be NULL) receives its device time. */
 int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next, float* logits,
                       float* prefill_ms);
 /* When enabled (default off), kl_engine_generate runs prompts of 2 or more
@@ -322,6 +322,18 @@ int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next,
  * and *decode_ms covers the n_new - 1 decode steps that follow.  Returns
  * KL_EUNSUPP (and stays off) where the prefill does not support the model. */
 int kl_engine_set_prefill(kl_engine* e, int enable);
+/* Which GEMM runs the prefill's projections of an fp32 image:
+ * KL_PREFILL_GEMM_LIBRARY (the default; hipBLASLt, for every shape it has a
+ * plan for) or KL_PREFILL_GEMM_OWN (the MFMA GEMM of kl_gemm_f32 /
+ * kl_gemm_f32_grouped for all of them; also the default where the environment
+ * sets KL_PREFILL_GEMM=own).  int8 images always run the own GEMM, so
+ * KL_PREFILL_GEMM_LIBRARY returns KL_EUNSUPP for them, as it does where the
+ * library handle cannot be created.  kl_engine_prefill_gemm_calls counts the
+ * projections each one has run since the engine was created. */
+#define KL_PREFILL_GEMM_LIBRARY 0
+#define KL_PREFILL_GEMM_OWN 1
+int kl_engine_set_prefill_gemm(kl_engine* e, int backend);
+int kl_engine_prefill_gemm_calls(const kl_engine* e, int64_t* library_calls, int64_t* own_calls);
 
 /* Per-kernel timing: runs `steps` decode steps from (token, pos0) without the
  * graph, with a HIP event recorded between consecutive launches on the

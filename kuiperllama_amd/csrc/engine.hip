@@ -32,6 +32,7 @@
 #include "gemm_run.hpp"
 #include "gemv.hpp"
 #include "kuiper_hip.h"
+#include "lt_gemm.hpp"
 #include "persist.hpp"
 
 using namespace kl;
@@ -475,6 +476,12 @@ struct kl_engine {
   int32_t* pf_next = nullptr;
   void* pf_am = nullptr;        // argmax workspace (zeroed once)
   size_t pf_am_bytes = 0;
+  // fp32 projections through hipBLASLt (created with the prefill scratch;
+  // null for int8 images or with KL_PREFILL_GEMM=own: then every projection
+  // runs the hand-written MFMA GEMM of gemm.hpp).
+  kl::LtGemm* lt = nullptr;
+  bool pf_own = false;               // KL_PREFILL_GEMM_OWN chosen
+  int64_t pf_lib_calls = 0, pf_own_calls = 0;
 };
 
 namespace {
@@ -992,6 +999,7 @@ int setup_persistent(kl_engine* e) {
   e->plain_launch = e->persistent_ok && blocks * e->cus >= e->nwg;
   if (const char* env = std::getenv("KL_PERSISTENT_LAUNCH"))
     if (std::strcmp(env, "cooperative") == 0) e->plain_launch = false;
+  if (const char* env = std::getenv("KL_PREFILL_GEMM")) e->pf_own = std::strcmp(env, "own") == 0;
   if (const char* env = std::getenv("KL_ENGINE_MODE")) {
     if (std::atoi(env) == KL_MODE_MULTI) e->mode = KL_MODE_MULTI;
   }
@@ -1006,6 +1014,7 @@ void release(kl_engine* e) {
   if (e->ev1) (void)hipEventDestroy(e->ev1);
   if (e->arena) (void)hipFree(e->arena);
   if (e->pf_buf) (void)hipFree(e->pf_buf);
+  delete e->lt;
   if (e->d_split) (void)hipFree(e->d_split);
   if (e->st_host) (void)hipHostFree(e->st_host);
   if (e->derr_host) (void)hipHostFree(e->derr_host);
@@ -1443,6 +1452,16 @@ GemmSeg proj_seg(const kl_engine* e, const WView& w, float* C, const float* bias
   return sg;
 }
 
+// Creates the hipBLASLt handle of an fp32 engine once; false if it cannot be.
+bool lt_handle(kl_engine* e) {
+  if (e->lt) return true;
+  e->lt = new kl::LtGemm();
+  if (e->lt->init()) return true;
+  delete e->lt;
+  e->lt = nullptr;
+  return false;
+}
+
 // Allocates the prefill scratch for `rows` rows (once; grows if needed).
 int prefill_scratch(kl_engine* e, int rows) {
   if (rows <= e->pf_rows) return KL_OK;
@@ -1481,7 +1500,9 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_am_bytes = am;
   e->pf_rows = rows;
   err = hipMemsetAsync(e->pf_am, 0, am, e->stream);
-  return err == hipSuccess ? KL_OK : rc(err);
+  if (err != hipSuccess) return rc(err);
+  if (!e->quant && !e->pf_own) (void)lt_handle(e);  // without one, gemm.hpp runs every projection
+  return KL_OK;
 }
 
 // Positions pos0 .. pos0+n-1 through every layer; leaves the residual rows in
@@ -1492,6 +1513,21 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
   void* st = e->stream;
   const size_t kv_layer = static_cast<size_t>(m.S) * Dkv;
   int r = kl_embedding(e->pf_tok + pos0, n, e->emb, m.V, D, e->pf_x, nullptr, st);
+  hipStream_t hs0 = static_cast<hipStream_t>(st);
+  // C[n x N] (+)= A[n x K] . W^T (+ bias) through hipBLASLt (fp32 images with
+  // a library plan for the shape; lib_ok tells which).
+  auto lib_ok = [&](const float* A, int K, const WView& w, int N, int ldc, const float* bias) {
+    const bool yes = !e->pf_own && e->lt != nullptr && e->lt->ready(n, N, K, K, K, ldc, bias != nullptr);
+    if (!yes) ++e->pf_own_calls;  // counted once per projection (or grouped launch)
+    return yes;
+  };
+  auto lib = [&](const float* A, int K, const WView& w, float* C, int N, int ldc, const float* bias,
+                 bool acc) {
+    ++e->pf_lib_calls;
+    return e->lt->gemm(A, n, K, K, static_cast<const float*>(w.w), N, K, C, ldc, bias, acc, hs0)
+               ? KL_OK
+               : KL_EDEVICE;
+  };
 #define PF(call)          \
   do {                    \
     if (r == KL_OK) r = (call); \
@@ -1505,7 +1541,14 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     hipStream_t hs = static_cast<hipStream_t>(st);
     // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
-    {  // q, k and v in one grouped launch; k and v straight into the cache rows
+    // q, k and v (k and v straight into the cache rows): three library
+    // GEMMs, or one grouped launch of gemm.hpp
+    if (lib_ok(e->pf_xn, D, Ld.wq, Dq, Dq, Ld.bq) && lib_ok(e->pf_xn, D, Ld.wk, Dkv, Dkv, Ld.bk) &&
+        lib_ok(e->pf_xn, D, Ld.wv, Dkv, Dkv, Ld.bv)) {
+      PF(lib(e->pf_xn, D, Ld.wq, e->pf_q, Dq, Dq, Ld.bq, false));
+      PF(lib(e->pf_xn, D, Ld.wk, krow, Dkv, Dkv, Ld.bk, false));
+      PF(lib(e->pf_xn, D, Ld.wv, vrow, Dkv, Dkv, Ld.bv, false));
+    } else {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
@@ -1520,7 +1563,9 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     PF(kl_attn_prefill(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, st));
     const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
-    {
+    if (lib_ok(e->pf_att, Dq, Ld.wo, D, D, nullptr)) {
+      PF(lib(e->pf_att, Dq, Ld.wo, e->pf_x, D, D, nullptr, true));
+    } else {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
       const int sp = prefill_splits(n, D, Dq);
       if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
@@ -1528,13 +1573,18 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     }
     // feed_forward (llama3.cpp:671-719)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
-    {
+    if (lib_ok(e->pf_xn, D, Ld.w1, F, F, nullptr)) {
+      PF(lib(e->pf_xn, D, Ld.w1, e->pf_h1, F, F, nullptr, false));
+      PF(lib(e->pf_xn, D, Ld.w3, e->pf_h3, F, F, nullptr, false));
+    } else {
       const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
       PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, nullptr, 1, hs));
     }
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
-    {
+    if (lib_ok(e->pf_h1, F, Ld.w2, D, D, nullptr)) {
+      PF(lib(e->pf_h1, F, Ld.w2, e->pf_x, D, D, nullptr, true));
+    } else {
       const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
       const int sp = prefill_splits(n, D, F);
       if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
@@ -1553,6 +1603,26 @@ int kl_engine_set_prefill(kl_engine* e, int enable) {
   if (!e) return KL_EINVAL;
   if (enable && !prefill_supported(e)) return KL_EUNSUPP;
   e->use_prefill = enable != 0;
+  return KL_OK;
+}
+
+int kl_engine_set_prefill_gemm(kl_engine* e, int backend) {
+  if (!e) return KL_EINVAL;
+  if (backend == KL_PREFILL_GEMM_OWN) {
+    e->pf_own = true;
+    return KL_OK;
+  }
+  if (backend != KL_PREFILL_GEMM_LIBRARY) return KL_EINVAL;
+  if (e->quant) return KL_EUNSUPP;
+  if (!lt_handle(e)) return KL_EUNSUPP;
+  e->pf_own = false;
+  return KL_OK;
+}
+
+int kl_engine_prefill_gemm_calls(const kl_engine* e, int64_t* library_calls, int64_t* own_calls) {
+  if (!e || !library_calls || !own_calls) return KL_EINVAL;
+  *library_calls = e->pf_lib_calls;
+  *own_calls = e->pf_own_calls;
   return KL_OK;
 }
 

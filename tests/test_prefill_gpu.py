@@ -185,14 +185,40 @@ def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
 PREFILL_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"]
 
 
+def set_gemm(K, eng, cfg, backend):
+    """Selects the prefill's projection GEMM; int8 images only have the own one."""
+    if cfg.quant and backend == K.PREFILL_GEMM_LIBRARY:
+        with pytest.raises(K.KlError):
+            eng.set_prefill_gemm(backend)
+        return K.PREFILL_GEMM_OWN
+    eng.set_prefill_gemm(backend)
+    return backend
+
+
+def check_gemm_calls(eng, backend, before=(0, 0)):
+    """The projections ran on the chosen GEMM, none on the other."""
+    lib_n, own_n = eng.prefill_gemm_calls()
+    lib_n, own_n = lib_n - before[0], own_n - before[1]
+    if backend == 0:
+        assert lib_n > 0 and own_n == 0, (lib_n, own_n)
+    else:
+        assert own_n > 0 and lib_n == 0, (lib_n, own_n)
+
+
+GEMMS = [pytest.param(0, id="library"), pytest.param(1, id="own")]
+
+
+@pytest.mark.parametrize("backend", GEMMS)
 @pytest.mark.parametrize("name", PREFILL_TINY)
-def test_engine_prefill_vs_oracle(K, O, gpu, name):
+def test_engine_prefill_vs_oracle(K, O, gpu, name, backend):
     cfg = K.TINY[name]
     img = K.synth_image(cfg)
     P = min(40, cfg.seq_len - 10)
     prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
     eng = K.Engine(img, cfg)
+    backend = set_gemm(K, eng, cfg, backend)
     nxt, lg, ms = eng.prefill(prompt)
+    check_gemm_calls(eng, backend)
     om = O.Model(img, cfg.family, cfg.quant)
     for pos in range(P - 1):
         om.step(prompt[pos], pos)
@@ -219,7 +245,8 @@ def test_engine_prefill_vs_oracle(K, O, gpu, name):
         tok = O.argmax(ref2)
 
 
-def test_qwen3_shape_prefill_512_vs_oracle(K, O, gpu):
+@pytest.mark.parametrize("backend", GEMMS)
+def test_qwen3_shape_prefill_512_vs_oracle(K, O, gpu, backend):
     """cfg 5's layer shape (Qwen3: dim 2560, 32 Q / 8 KV heads of 128, q/k
     norms) at 2 layers with non-unit norm weights: the 512-token prompt as one
     batched prefill against the oracle's token-by-token run, then 8 greedy
@@ -232,7 +259,9 @@ def test_qwen3_shape_prefill_512_vs_oracle(K, O, gpu):
     eng = K.Engine(img, cfg)
     eng.set_mode(K.MODE_PERSISTENT)
     assert eng.mode == K.MODE_PERSISTENT
+    eng.set_prefill_gemm(backend)
     nxt, lg, ms = eng.prefill(prompt)
+    check_gemm_calls(eng, backend)
     om = O.Model(img, cfg.family, cfg.quant)
     for pos in range(P - 1):
         om.step(prompt[pos], pos)
@@ -308,12 +337,22 @@ def test_gemm_q8_rejects_bad_shapes(K, gpu):
 
 @pytest.mark.parametrize("name,P", [("qwen3_4b", 512), ("qwen25_15b", 4000), ("llama2_7b_q8", 300)])
 def test_full_size_prefill_vs_steps(K, gpu, name, P):
+    """The default GEMM (the library for fp32 images), and for cfg 5 the own
+    GEMM on the same engine as well."""
     cfg = K.BASELINE[name]
     img = K.synth_image(cfg)
     prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
     eng = K.Engine(img, cfg)
     nxt, lg, ms = eng.prefill(prompt)
     print(f"{name}: prefill of {P} tokens in {ms:.1f} ms", flush=True)
+    check_gemm_calls(eng, K.PREFILL_GEMM_OWN if cfg.quant else K.PREFILL_GEMM_LIBRARY)
+    if name == "qwen3_4b":
+        before = eng.prefill_gemm_calls()
+        eng.set_prefill_gemm(K.PREFILL_GEMM_OWN)
+        n_own, lg_own, ms_own = eng.prefill(prompt)
+        check_gemm_calls(eng, K.PREFILL_GEMM_OWN, before)
+        print(f"{name}: own GEMM {ms_own:.1f} ms, library vs own rel {rel(lg, lg_own):.2e}", flush=True)
+        assert rel(lg_own, lg) < LOGIT_RTOL
     ref_eng = K.Engine(img, cfg)
     for pos in range(P - 1):
         ref_eng.step(prompt[pos], pos, want_logits=False)
