@@ -824,11 +824,16 @@ namespace {
 template <int HD>
 int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
                         int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st) {
-  // Head sizes 64 and 128 on the matrix cores; 32 on the vector ALUs.
+  // Head sizes 64 and 128 on the matrix cores (128: eight waves per
+  // workgroup); 32 on the vector ALUs.
   constexpr bool kMfma = HD == 64 || HD == 128;
-  const void* fn = kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_mfma<kMfma ? HD : 64>)
-                         : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
-  const size_t lds = kMfma ? attn_prefill_mfma_lds_bytes(HD) : attn_prefill_lds_bytes(HD);
+  constexpr bool kMfma8 = HD == 128;
+  const void* fn = kMfma8 ? reinterpret_cast<const void*>(&k_attn_prefill_mfma8<128>)
+                   : kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_mfma<kMfma ? HD : 64>)
+                           : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
+  const size_t lds = kMfma8 ? attn_prefill_mfma8_lds_bytes(HD)
+                     : kMfma ? attn_prefill_mfma_lds_bytes(HD)
+                             : attn_prefill_lds_bytes(HD);
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -838,7 +843,10 @@ int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* v
   }
   const float scale = 1.f / std::sqrt(static_cast<float>(HD));
   const dim3 grid((n + kPrefillQB - 1) / kPrefillQB, heads);
-  if constexpr (kMfma)
+  if constexpr (kMfma8)
+    hipLaunchKernelGGL(k_attn_prefill_mfma8<128>, grid, dim3(512), lds, st, q, ldq, kc, vc, kv_dim,
+                       kv_mul, out, ldo, pos0, n, scale);
+  else if constexpr (kMfma)
     hipLaunchKernelGGL(k_attn_prefill_mfma<HD>, grid, dim3(256), lds, st, q, ldq, kc, vc, kv_dim,
                        kv_mul, out, ldo, pos0, n, scale);
   else

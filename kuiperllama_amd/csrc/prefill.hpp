@@ -335,6 +335,169 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
   }
 }
 
+// Head size 128 with eight waves per workgroup, two per SIMD, so that one
+// wave's LDS reads, softmax and barriers overlap the other's matrix-core work
+// (the four-wave kernel above leaves one wave per SIMD: 311 VGPRs + AGPRs).
+// Key blocks of 128; wave (wm, wn) = (w % 2, w / 2) computes the scores of
+// rows 32 wm .. against keys 32 wn .. of the block (k over d; its Q row slice
+// in registers as above) and the output of rows 32 wm .. for columns 32 wn ..
+// (k over the block's 128 keys: lane half h takes keys 64 h .. 64 h + 63).
+// K and V of a block share one LDS buffer: K while the scores are computed,
+// then V, loaded into registers during the scores.  The next block's K is
+// loaded into registers during the current block.  Row maxima and sums cross
+// the four key quarters through LDS and are combined in a fixed order.
+constexpr int kPrefillKB8 = 128;
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restrict__ q, int ldq,
+                                                            const float* __restrict__ kc,
+                                                            const float* __restrict__ vc,
+                                                            int kv_dim, int kv_mul,
+                                                            float* __restrict__ out, int ldo,
+                                                            int pos0, int n, float scale) {
+  static_assert(HD == 128, "head size");
+  typedef float f16v __attribute__((ext_vector_type(16)));
+  constexpr int QB = kPrefillQB, KB = kPrefillKB8;
+  constexpr int LDK = HD + 4;  // K / V row (floats)
+  constexpr int LDP = KB + 4;  // P row
+  constexpr int HH = HD / 2;   // d per lane half (scores)
+  constexpr int KH = KB / 2;   // keys per lane half (output)
+  constexpr int NT = 512;
+  extern __shared__ __align__(16) float sm[];
+  float* KVs = sm;              // [KB][LDK]: the block's K, then its V
+  float* Ps = KVs + KB * LDK;   // [QB][LDP]
+  float* rmax = Ps + QB * LDP;  // [4][QB] per key quarter
+  float* rsum = rmax + 4 * QB;  // [4][QB]
+  const int h = blockIdx.y, g = h / kv_mul;
+  const int p0 = blockIdx.x * QB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1, hl = lane >> 5, li = lane & 31;
+
+  pf4 qr[HH / 4];  // Q row 32 wm + li, d in [HH hl, HH hl + HH)
+  {
+    const int p = p0 + 32 * wm + li;
+    const float* qp = q + static_cast<size_t>(p < n ? p : 0) * ldq + h * HD + HH * hl;
+#pragma unroll
+    for (int j = 0; j < HH / 4; ++j)
+      qr[j] = p < n ? *reinterpret_cast<const pf4*>(qp + 4 * j) : pf4{0.f, 0.f, 0.f, 0.f};
+  }
+  // Rows of this lane's accumulator registers: 32 wm + 8 (r / 4) + 4 hl + r % 4.
+  float m[16], lsum[16];
+  f16v o = f16v{};
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    m[r] = -INFINITY;
+    lsum[r] = 0.f;
+  }
+  const int rows = n - p0 < QB ? n - p0 : QB;
+  const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
+  const int qbase = pos0 + p0 + 32 * wm + 4 * hl;
+  constexpr int NL = KB * HD / 4 / NT;  // float4s of K (and of V) per thread
+  pf4 kpre[NL], vcur[NL];
+  auto load = [&](const float* base, int j0, pf4* dst) {
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = tid + NT * t;
+      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+      const int j = j0 + r;
+      dst[t] = *reinterpret_cast<const pf4*>(base + static_cast<size_t>(j <= last ? j : 0) * kv_dim +
+                                             g * HD + c);
+    }
+  };
+  auto stage = [&](int j0, const pf4* src) {  // rows past `last` as zeros
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = tid + NT * t;
+      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+      *reinterpret_cast<pf4*>(KVs + r * LDK + c) = j0 + r <= last ? src[t] : pf4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  load(kc, 0, kpre);
+  for (int j0 = 0; j0 <= last; j0 += KB) {
+    __syncthreads();  // the previous block's V and P are consumed
+    stage(j0, kpre);
+    load(vc, j0, vcur);                          // this block's V, used after the scores
+    if (j0 + KB <= last) load(kc, j0 + KB, kpre);  // the next block's K
+    __syncthreads();
+    // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
+    f16v sacc = f16v{};
+    {
+      const float* kp = KVs + (32 * wn + li) * LDK + HH * hl;
+#pragma unroll
+      for (int j = 0; j < HH / 4; ++j) {
+        const pf4 kv = *reinterpret_cast<const pf4*>(kp + 4 * j);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].x, kv.x, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].y, kv.y, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].z, kv.z, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].w, kv.w, sacc, 0, 0, 0);
+      }
+    }
+    // Scale, causal mask, and the row maxima over this wave's 32 keys.
+    const int kpos = j0 + 32 * wn + li;
+    float sv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qpos = qbase + 8 * (r >> 2) + (r & 3);
+      sv[r] = kpos <= qpos ? sacc[r] * scale : -INFINITY;
+      const float mx = half_max(sv[r]);
+      if (li == 0) rmax[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = mx;
+    }
+    __syncthreads();  // every wave's scores are done (K is dead) and its maxima visible
+    stage(j0, vcur);
+    float alpha[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
+      const float mn = fmaxf(fmaxf(m[r], fmaxf(rmax[row], rmax[QB + row])),
+                             fmaxf(rmax[2 * QB + row], rmax[3 * QB + row]));
+      // Key 0 is in the first block for every row, so mn is finite from then on.
+      alpha[r] = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
+      m[r] = mn;
+      const float pv = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mn);
+      Ps[row * LDP + 32 * wn + li] = pv;
+      lsum[r] = lsum[r] * alpha[r] + half_sum(pv);
+    }
+    __syncthreads();  // P and V are in LDS
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] *= alpha[r];
+    // O = O alpha + P V for rows 32 wm .., columns 32 wn ...
+    {
+      const float* pp = Ps + (32 * wm + li) * LDP + KH * hl;
+      const float* vb = KVs + KH * hl * LDK + 32 * wn + li;
+#pragma unroll
+      for (int j = 0; j < KH / 4; ++j) {
+        const pf4 pv = *reinterpret_cast<const pf4*>(pp + 4 * j);
+        const float* vp = vb + 4 * j * LDK;
+        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.x, vp[0], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.y, vp[LDK], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.z, vp[2 * LDK], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.w, vp[3 * LDK], o, 0, 0, 0);
+      }
+    }
+  }
+  // Row sums: the four key quarters, in a fixed order.
+  if (li == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rsum[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = lsum[r];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
+    const int p = p0 + row;
+    if (p < n) {
+      const float l = ((rsum[row] + rsum[QB + row]) + rsum[2 * QB + row]) + rsum[3 * QB + row];
+      out[static_cast<size_t>(p) * ldo + h * HD + 32 * wn + li] = o[r] / l;
+    }
+  }
+}
+
+__host__ __device__ constexpr size_t attn_prefill_mfma8_lds_bytes(int hd) {
+  return (static_cast<size_t>(kPrefillKB8) * (hd + 4) +
+          static_cast<size_t>(kPrefillQB) * (kPrefillKB8 + 4) + 8 * kPrefillQB) *
+         sizeof(float);
+}
+
 __host__ __device__ constexpr size_t attn_prefill_mfma_lds_bytes(int hd) {
   return (2 * static_cast<size_t>(kPrefillKB) * (hd + 4) +
           static_cast<size_t>(kPrefillQB) * (kPrefillKB + 4) + 4 * kPrefillQB) *
