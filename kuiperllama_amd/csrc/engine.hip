@@ -1546,8 +1546,19 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     if (lib_ok(e->pf_xn, D, Ld.wq, Dq, Dq, Ld.bq) && lib_ok(e->pf_xn, D, Ld.wk, Dkv, Dkv, Ld.bk) &&
         lib_ok(e->pf_xn, D, Ld.wv, Dkv, Dkv, Ld.bv)) {
       PF(lib(e->pf_xn, D, Ld.wq, e->pf_q, Dq, Dq, Ld.bq, false));
-      PF(lib(e->pf_xn, D, Ld.wk, krow, Dkv, Dkv, Ld.bk, false));
-      PF(lib(e->pf_xn, D, Ld.wv, vrow, Dkv, Dkv, Ld.bv, false));
+      // K and V as one batch of two where there is no bias (their weights
+      // and cache rows lie at fixed distances); else two products.
+      const float* wk = static_cast<const float*>(Ld.wk.w);
+      const float* wv = static_cast<const float*>(Ld.wv.w);
+      const bool pair = !Ld.bk && !Ld.bv && r == KL_OK &&
+                        e->lt->gemm_pair(e->pf_xn, n, D, D, wk, wv - wk, Dkv, D, krow, vrow - krow,
+                                         Dkv, hs0);
+      if (pair) {
+        ++e->pf_lib_calls;
+      } else {
+        PF(lib(e->pf_xn, D, Ld.wk, krow, Dkv, Dkv, Ld.bk, false));
+        PF(lib(e->pf_xn, D, Ld.wv, vrow, Dkv, Dkv, Ld.bv, false));
+      }
     } else {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),

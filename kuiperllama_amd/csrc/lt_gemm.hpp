@@ -56,6 +56,22 @@ class LtGemm {
     return plan(M, N, K, lda, ldw, ldc, has_bias) != nullptr;
   }
 
+  // Two products over the same A as one strided batch, C_i = A . W_i^T for
+  // i = 0, 1, where W1 and C1 lie w_stride and c_stride elements after W0
+  // and C0 (both positive; no bias: the library has no per-batch bias
+  // stride).  The batch fills the chip where one narrow product does not
+  // (the K and V projections of a prefill).  False if there is no plan or
+  // the call fails.
+  bool gemm_pair(const float* A, int M, int K, int lda, const float* W0, long long w_stride, int N,
+                 int ldw, float* C0, long long c_stride, int ldc, hipStream_t st) {
+    if (w_stride <= 0 || c_stride <= 0) return false;
+    Plan* p = plan(M, N, K, lda, ldw, ldc, false, w_stride, c_stride);
+    if (!p) return false;
+    const float alpha = 1.f, beta = 0.f;
+    return hipblasLtMatmul(handle_, p->op, &alpha, W0, p->lw, A, p->la, &beta, C0, p->lc, C0,
+                           p->lc, &p->algo, ws_, kWorkspaceBytes, st) == HIPBLAS_STATUS_SUCCESS;
+  }
+
   // C (+)= A . W^T (+ bias) on stream st; false if the shape has no plan or
   // the call fails.
   bool gemm(const float* A, int M, int K, int lda, const float* W, int N, int ldw, float* C,
@@ -77,10 +93,12 @@ class LtGemm {
     hipblasLtMatmulAlgo_t algo{};
     bool ok = false;
   };
-  typedef std::tuple<int, int, int, int, int, int, bool> Key;
+  typedef std::tuple<int, int, int, int, int, int, bool, long long, long long> Key;
 
-  Plan* plan(int M, int N, int K, int lda, int ldw, int ldc, bool has_bias) {
-    const Key key{M, N, K, lda, ldw, ldc, has_bias};
+  // One plan per shape; w_stride > 0 makes it a batch of two (A shared).
+  Plan* plan(int M, int N, int K, int lda, int ldw, int ldc, bool has_bias,
+             long long w_stride = 0, long long c_stride = 0) {
+    const Key key{M, N, K, lda, ldw, ldc, has_bias, w_stride, c_stride};
     auto it = plans_.find(key);
     if (it != plans_.end()) return it->second.ok ? &it->second : nullptr;
     Plan& p = plans_[key];
@@ -103,6 +121,17 @@ class LtGemm {
            hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_32F, K, N, ldw) == HIPBLAS_STATUS_SUCCESS &&
            hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, K, M, lda) == HIPBLAS_STATUS_SUCCESS &&
            hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS;
+    if (good && w_stride > 0) {
+      const int32_t two = 2;
+      const int64_t sw = w_stride, sa = 0, sc = c_stride;
+      auto batch = [&](hipblasLtMatrixLayout_t l, int64_t stride) {
+        return hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &two,
+                                                 sizeof(two)) == HIPBLAS_STATUS_SUCCESS &&
+               hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET,
+                                                 &stride, sizeof(stride)) == HIPBLAS_STATUS_SUCCESS;
+      };
+      good = batch(p.lw, sw) && batch(p.la, sa) && batch(p.lc, sc);
+    }
     if (good) {
       hipblasLtMatmulPreference_t pref = nullptr;
       good = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
