@@ -1585,8 +1585,19 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // feed_forward (llama3.cpp:671-719)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
     if (lib_ok(e->pf_xn, D, Ld.w1, F, F, nullptr)) {
-      PF(lib(e->pf_xn, D, Ld.w1, e->pf_h1, F, F, nullptr, false));
-      PF(lib(e->pf_xn, D, Ld.w3, e->pf_h3, F, F, nullptr, false));
+      const float* w1 = static_cast<const float*>(Ld.w1.w);
+      const float* w3 = static_cast<const float*>(Ld.w3.w);
+      // W1 and W3 as one batch of two as well (at 512 rows each alone is 244
+      // library tiles, under one per CU; together they pack better).
+      const bool pair = r == KL_OK &&
+                        e->lt->gemm_pair(e->pf_xn, n, D, D, w1, w3 - w1, F, D, e->pf_h1,
+                                         e->pf_h3 - e->pf_h1, F, hs0);
+      if (pair) {
+        ++e->pf_lib_calls;
+      } else {
+        PF(lib(e->pf_xn, D, Ld.w1, e->pf_h1, F, F, nullptr, false));
+        PF(lib(e->pf_xn, D, Ld.w3, e->pf_h3, F, F, nullptr, false));
+      }
     } else {
       const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
