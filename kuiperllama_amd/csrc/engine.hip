@@ -925,6 +925,13 @@ int setup_persistent(kl_engine* e) {
   // 4000 positions; KL_ATTN_MERGE_CHUNKS overrides).
   a.merge_chunks = 2;
   if (const char* env = std::getenv("KL_ATTN_MERGE_CHUNKS")) a.merge_chunks = std::max(1, std::atoi(env));
+  // 9-16 chunks: a merger per 4 chunks (3-4 per kv head) measured +1.4%
+  // on Qwen3-4B at 520-640 positions and +0.6% on Llama-3.2-1B at 600-700
+  // against one per 2; beyond 16 chunks one per 2 stays best (Qwen2.5-1.5B
+  // at 4000 positions: one per 4 -1.1%).
+  a.merge_chunks_mid = 4;
+  if (const char* env = std::getenv("KL_ATTN_MERGE_CHUNKS_MID"))
+    a.merge_chunks_mid = std::max(1, std::atoi(env));
   // While the attention runs, workgroups without an attention item pull the
   // first 96 KB (up to 1.5x with many attention items) of their W1/W3 rows into L2 (those of the XCD's attention
   // workgroups are shared out among them), 0.5 us after the attention starts,

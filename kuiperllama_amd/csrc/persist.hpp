@@ -137,7 +137,8 @@ struct PArgs {
   tagged_t* attn_part;     // split partials [KVH][G][kv_mul][HD + 2] (tagged)
   long long attn_part_n;   // its elements
   int attn_G;              // chunk slots per kv head
-  int merge_chunks;        // chunks per merging workgroup beyond kAttnMergeChunks chunks
+  int merge_chunks;        // chunks per merging workgroup beyond 2 kAttnMergeChunks chunks
+  int merge_chunks_mid;    //   and from kAttnMergeChunks + 1 to 2 kAttnMergeChunks chunks
   // Workgroups without an attention item pull the first w13_touch_rows local
   // rows of their W1/W3 share (0: none) into L2 while the attention runs,
   // after touch_delay 100 MHz ticks, and a slice of the attention
@@ -1169,7 +1170,9 @@ __device__ __forceinline__ void attn_p_phase(const PArgs& a, const PAttn* atp, i
     M = Mn;
   };
   const int E = kvm * HD;
-  const int R = nsplit <= kAttnMergeChunks ? kAttnMergeChunks : a.merge_chunks;
+  const int R = nsplit <= kAttnMergeChunks       ? kAttnMergeChunks
+                : nsplit <= 2 * kAttnMergeChunks ? a.merge_chunks_mid
+                                                 : a.merge_chunks;
   const int MW = (nsplit + R - 1) / R;
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int g = it / nsplit;

@@ -432,11 +432,12 @@ def test_long_context_qwen25_attention_shape(K, O, gpu):
     """cfg 4's attention (Qwen2: 12 Q / 2 KV heads of 128, QKV bias, 4096
     positions) at 2 layers with a narrow FFN and vocabulary: positions past
     512 and 1024 (9 and 17 chunks of 64 per kv head, where the persistent
-    merge switches to several lanes and mergers per output) and a cache
+    merge switches to several lanes and mergers per output, with a merger
+    per 4 chunks up to 16 chunks and per 2 beyond) and a cache
     filled to 4000 positions followed by 8 greedy steps."""
     cfg = K.BASELINE["qwen25_15b"].with_(name="qwen25_attn_2l", layers=2, hidden_dim=512,
                                          vocab=1024, norm_std=NORMS)
-    check = set(range(0, 4)) | set(range(188, 196)) | set(range(508, 520)) \
+    check = set(range(0, 4)) | set(range(188, 196)) | set(range(508, 520)) | set(range(700, 704)) \
         | set(range(1020, 1032)) | set(range(2040, 2052)) | set(range(3000, 3004))
     long_context(K, O, cfg, 4000, check, 8)
 
@@ -446,6 +447,6 @@ def test_long_context_llama32_attention_shape(K, O, gpu):
     layers: past 512 and 1024 positions, to 1200."""
     cfg = K.BASELINE["llama32_1b"].with_(name="llama32_attn_2l", layers=2, hidden_dim=512,
                                          vocab=1024, seq_len=1216, norm_std=NORMS)
-    check = set(range(0, 4)) | set(range(380, 390)) | set(range(508, 520)) \
+    check = set(range(0, 4)) | set(range(380, 390)) | set(range(508, 520)) | set(range(700, 704)) \
         | set(range(1020, 1032))
     long_context(K, O, cfg, 1190, check, 8)
