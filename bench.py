@@ -264,8 +264,13 @@ def main() -> int:
     steps = args.steps or cfg.decode_steps
     P = cfg.prompt_len
     if P + args.warmup + steps - 1 > cfg.seq_len:
-        print("bench.py: prompt + warmup + steps exceed the model's seq_len", file=sys.stderr)
-        return 1
+        # cfg 4 (4000-token prompt, 96 steps, seq_len 4096): fewer warmup steps
+        warm = max(0, cfg.seq_len - P - steps + 1)
+        if P + warm + steps - 1 > cfg.seq_len:
+            print("bench.py: prompt + steps exceed the model's seq_len", file=sys.stderr)
+            return 1
+        print(f"# warmup {args.warmup} -> {warm} steps (seq_len {cfg.seq_len})", file=sys.stderr)
+        args.warmup = warm
     t0 = time.time()
     img = K.synth_image(cfg)
     t_img = time.time() - t0
