@@ -195,6 +195,19 @@ int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ld
 int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
                     int ldq, const float* key_cache, const float* value_cache, int kv_dim,
                     float* out, int ldo, void* stream);
+/* kl_attn_prefill with a workspace (no reference counterpart for the split
+ * itself; same MHAKernel semantics): where the (64-row block, head) pairs of
+ * a launch are fewer than the device's CUs — rows far into a long context —
+ * head size 128 cuts each row block's keys into up to 4 contiguous parts, one
+ * workgroup each, and a merge pass combines their partial (max, sum, output)
+ * rows in a fixed order.  workspace: kl_attn_prefill_workspace_size bytes,
+ * 16-byte aligned (0 bytes for head sizes 32 and 64, which run
+ * kl_attn_prefill; so does a launch that fills the CUs); KL_EWORKSPACE if
+ * smaller. */
+int kl_attn_prefill_workspace_size(int n_pos, int head_num, int head_size, size_t* bytes);
+int kl_attn_prefill_ws(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
+                       int ldq, const float* key_cache, const float* value_cache, int kv_dim,
+                       float* out, int ldo, void* workspace, size_t workspace_bytes, void* stream);
 
 /* SwigluKernel (KI:19-20; cpu/swiglu_kernel.cpp:3-23): out = a*sigmoid(a)*b. */
 int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream);

@@ -471,7 +471,8 @@ struct kl_engine {
   char* pf_buf = nullptr;       // one allocation for everything below
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
   float *pf_h1 = nullptr, *pf_h3 = nullptr, *pf_xlast = nullptr;
-  float* pf_ws = nullptr;       // split-K partials [kPrefillMaxSplits][rows][dim]
+  float* pf_ws = nullptr;       // split-K partials [kPrefillMaxSplits][rows][dim], or the
+  size_t pf_ws_bytes = 0;       //   attention's key-range parts (whichever is larger)
   int32_t* pf_tok = nullptr;    // [seq_len] prompt ids
   int32_t* pf_next = nullptr;
   void* pf_am = nullptr;        // argmax workspace (zeroed once)
@@ -1479,7 +1480,10 @@ int prefill_scratch(kl_engine* e, int rows) {
   auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t R = rows;
   const size_t sz_x = al(R * m.D * 4), sz_q = al(R * m.Dq * 4), sz_h = al(R * m.F * 4);
-  const size_t sz_ws = al(static_cast<size_t>(kPrefillMaxSplits) * R * m.D * 4);
+  size_t attn_ws = 0;
+  r = kl_attn_prefill_workspace_size(rows, m.H, m.hd, &attn_ws);
+  if (r != KL_OK) return r;
+  const size_t sz_ws = al(std::max(static_cast<size_t>(kPrefillMaxSplits) * R * m.D * 4, attn_ws));
   const size_t total =
       2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(m.D * 4) + al(m.S * 4) + al(256) + al(am);
   char* buf = nullptr;
@@ -1500,6 +1504,7 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_h1 = reinterpret_cast<float*>(take(sz_h));
   e->pf_h3 = reinterpret_cast<float*>(take(sz_h));
   e->pf_ws = reinterpret_cast<float*>(take(sz_ws));
+  e->pf_ws_bytes = sz_ws;
   e->pf_xlast = reinterpret_cast<float*>(take(al(m.D * 4)));
   e->pf_tok = reinterpret_cast<int32_t*>(take(al(m.S * 4)));
   e->pf_next = reinterpret_cast<int32_t*>(take(al(256)));
@@ -1579,7 +1584,10 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     PF(kl_rope_rows(e->rope_style, Dq, Dkv, hd, e->pf_q, Dq, krow, Dkv, pos0, n, e->sin_t,
                     e->cos_t, st));
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
-    PF(kl_attn_prefill(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, st));
+    // pf_ws (the own GEMM's split-K partials) is free between the GEMMs; it
+    // holds the key-range parts of the attention where the rows are few.
+    PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, e->pf_ws,
+                          e->pf_ws_bytes, st));
     const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
     if (lib_ok(e->pf_att, Dq, Ld.wo, D, D, nullptr)) {
       PF(lib(e->pf_att, Dq, Ld.wo, e->pf_x, D, D, nullptr, true));

@@ -846,9 +846,39 @@ int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, i
 }  // extern "C"
 
 namespace {
+constexpr int kPrefillMaxParts = 4;  // key-range parts of the split causal attention
+
+// Key-range parts for a prefill attention launch (head size 128): 1 where the
+// (row block, head) workgroups fill the CUs, else the count of at most
+// kPrefillMaxParts that minimises rounds of workgroups per part length
+// (ceil(g parts / cus) / parts), each part keeping at least 2 key blocks.
+int attn_prefill_parts(int pos0, int n, int heads) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+  }
+  const long long g = static_cast<long long>((n + kPrefillQB - 1) / kPrefillQB) * heads;
+  const int max_kb = (pos0 + n - 1) / kPrefillKB8 + 1;
+  int best = 1;
+  double best_cost = 1.0;
+  for (int s = 2; s <= kPrefillMaxParts && 2 * s <= max_kb && g < cus; ++s) {
+    const double cost = static_cast<double>((g * s + cus - 1) / cus) / s;
+    if (cost < best_cost - 1e-9) {
+      best = s;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <int HD>
 int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
-                        int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st) {
+                        int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st,
+                        float* part = nullptr) {
   // Head sizes 64 and 128 on the matrix cores (128: eight waves per
   // workgroup); 32 on the vector ALUs.
   constexpr bool kMfma = HD == 64 || HD == 128;
@@ -868,10 +898,17 @@ int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* v
   }
   const float scale = 1.f / std::sqrt(static_cast<float>(HD));
   const dim3 grid((n + kPrefillQB - 1) / kPrefillQB, heads);
-  if constexpr (kMfma8)
-    hipLaunchKernelGGL(k_attn_prefill_mfma8<128>, grid, dim3(512), lds, st, q, ldq, kc, vc, kv_dim,
-                       kv_mul, out, ldo, pos0, n, scale);
-  else if constexpr (kMfma)
+  if constexpr (kMfma8) {
+    const int parts = part ? attn_prefill_parts(pos0, n, heads) : 1;
+    hipLaunchKernelGGL(k_attn_prefill_mfma8<128>, dim3(grid.x, grid.y, parts), dim3(512), lds, st, q,
+                       ldq, kc, vc, kv_dim, kv_mul, out, ldo, pos0, n, scale, parts, part);
+    if (parts > 1) {
+      const int r = launch_rc();
+      if (r != KL_OK) return r;
+      hipLaunchKernelGGL(k_attn_prefill_merge8<128>, grid, dim3(256), 0, st, part, out, ldo, n,
+                         parts);
+    }
+  } else if constexpr (kMfma)
     hipLaunchKernelGGL(k_attn_prefill_mfma<HD>, grid, dim3(256), lds, st, q, ldq, kc, vc, kv_dim,
                        kv_mul, out, ldo, pos0, n, scale);
   else
@@ -900,6 +937,38 @@ int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size
     case 128: return attn_prefill_launch<128>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
     default: return KL_EUNSUPP;
   }
+}
+
+int kl_attn_prefill_workspace_size(int n_pos, int head_num, int head_size, size_t* bytes) {
+  if (!bytes || n_pos <= 0 || head_num <= 0 || head_size <= 0) return KL_EINVAL;
+  *bytes = head_size == 128 ? static_cast<size_t>(kPrefillMaxParts) * head_num *
+                                  ((n_pos + kPrefillQB - 1) / kPrefillQB) * kPrefillQB *
+                                  attn_prefill_part_floats(head_size) * sizeof(float)
+                            : 0;
+  return KL_OK;
+}
+
+int kl_attn_prefill_ws(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
+                       int ldq, const float* key_cache, const float* value_cache, int kv_dim,
+                       float* out, int ldo, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  size_t need = 0;
+  if (kl_attn_prefill_workspace_size(n_pos, head_num, head_size, &need) != KL_OK) return KL_EINVAL;
+  if (need == 0 || attn_prefill_parts(pos0, n_pos, head_num) == 1)
+    return kl_attn_prefill(pos0, n_pos, head_num, kv_mul, head_size, q, ldq, key_cache,
+                           value_cache, kv_dim, out, ldo, stream);
+  if (!workspace || workspace_bytes < need) return KL_EWORKSPACE;
+  if (!aligned16(workspace)) return KL_EUNSUPP;
+  if (!q || !key_cache || !value_cache || !out || pos0 < 0 || n_pos > 65535 * 64 || kv_mul <= 0 ||
+      head_num % kv_mul != 0 || kv_dim != head_num / kv_mul * head_size ||
+      ldq < head_num * head_size || ldo < head_num * head_size)
+    return KL_EINVAL;
+  if (ldq % 4 || ldo % 4 || kv_dim % 4 || !aligned16(q) || !aligned16(out) ||
+      !aligned16(key_cache) || !aligned16(value_cache))
+    return KL_EUNSUPP;
+  return attn_prefill_launch<128>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out,
+                                  ldo, pos0, n_pos, as_stream(stream),
+                                  static_cast<float*>(workspace));
 }
 
 int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream) {

@@ -287,7 +287,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
     for (int r = 0; r < 16; ++r) {
       const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
       const float mn = fmaxf(m[r], fmaxf(mx[r], rmax[(1 - wn) * QB + row]));
-      // Key 0 is in the first block for every row, so mn is finite from then on.
+      // A row whose keys so far are all masked (only in a part after the
+      // first) keeps m = -inf, p = 0 and o = 0.
       alpha[r] = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
       m[r] = mn;
       const float pv = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mn);
@@ -346,7 +347,17 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
 // then V, loaded into registers during the scores.  The next block's K is
 // loaded into registers during the current block.  Row maxima and sums cross
 // the four key quarters through LDS and are combined in a fixed order.
+//
+// Key-range split (nparts > 1, blockIdx.z = part): where a chunk of rows far
+// into the context gives fewer (row block, head) workgroups than the device
+// has CUs, each one's key blocks are cut into nparts contiguous ranges, one
+// workgroup each; a workgroup then writes its rows' unnormalised output with
+// their running maximum and sum to `part` (an empty range writes max -inf,
+// sum 0), and k_attn_prefill_merge8 combines the parts in order.
 constexpr int kPrefillKB8 = 128;
+
+// One partial record per query row: HD output floats, then max and sum.
+__host__ __device__ constexpr size_t attn_prefill_part_floats(int hd) { return hd + 2; }
 
 template <int HD>
 __global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restrict__ q, int ldq,
@@ -354,7 +365,8 @@ __global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restr
                                                             const float* __restrict__ vc,
                                                             int kv_dim, int kv_mul,
                                                             float* __restrict__ out, int ldo,
-                                                            int pos0, int n, float scale) {
+                                                            int pos0, int n, float scale,
+                                                            int nparts, float* __restrict__ part) {
   static_assert(HD == 128, "head size");
   typedef float f16v __attribute__((ext_vector_type(16)));
   constexpr int QB = kPrefillQB, KB = kPrefillKB8;
@@ -392,6 +404,10 @@ __global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restr
   const int rows = n - p0 < QB ? n - p0 : QB;
   const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
   const int qbase = pos0 + p0 + 32 * wm + 4 * hl;
+  // This workgroup's key blocks [kb0, kb1): all of them, or part blockIdx.z.
+  const int nkb = last / KB + 1;
+  const int kb0 = static_cast<int>(blockIdx.z) * nkb / nparts;
+  const int kb1 = (static_cast<int>(blockIdx.z) + 1) * nkb / nparts;
   constexpr int NL = KB * HD / 4 / NT;  // float4s of K (and of V) per thread
   pf4 kpre[NL], vcur[NL];
   auto load = [&](const float* base, int j0, pf4* dst) {
@@ -412,12 +428,13 @@ __global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restr
       *reinterpret_cast<pf4*>(KVs + r * LDK + c) = j0 + r <= last ? src[t] : pf4{0.f, 0.f, 0.f, 0.f};
     }
   };
-  load(kc, 0, kpre);
-  for (int j0 = 0; j0 <= last; j0 += KB) {
+  const int jend = kb1 * KB;  // one past the last key of this workgroup's range
+  if (kb0 < kb1) load(kc, kb0 * KB, kpre);
+  for (int j0 = kb0 * KB; j0 < jend; j0 += KB) {
     __syncthreads();  // the previous block's V and P are consumed
     stage(j0, kpre);
     load(vc, j0, vcur);                          // this block's V, used after the scores
-    if (j0 + KB <= last) load(kc, j0 + KB, kpre);  // the next block's K
+    if (j0 + KB < jend) load(kc, j0 + KB, kpre);  // the next block's K
     __syncthreads();
     // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
     f16v sacc = f16v{};
@@ -481,14 +498,61 @@ __global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restr
     for (int r = 0; r < 16; ++r) rsum[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = lsum[r];
   }
   __syncthreads();
+  float* rec = nparts > 1 ? part + ((static_cast<size_t>(blockIdx.z) * gridDim.y + h) * gridDim.x +
+                                    blockIdx.x) * QB * attn_prefill_part_floats(HD)
+                          : nullptr;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
     const int p = p0 + row;
     if (p < n) {
       const float l = ((rsum[row] + rsum[QB + row]) + rsum[2 * QB + row]) + rsum[3 * QB + row];
-      out[static_cast<size_t>(p) * ldo + h * HD + 32 * wn + li] = o[r] / l;
+      if (rec) {
+        float* rp = rec + static_cast<size_t>(row) * attn_prefill_part_floats(HD);
+        rp[32 * wn + li] = o[r];
+        if (wn == 0 && li == 0) {
+          rp[HD] = m[r];
+          rp[HD + 1] = l;
+        }
+      } else {
+        out[static_cast<size_t>(p) * ldo + h * HD + 32 * wn + li] = o[r] / l;
+      }
     }
+  }
+}
+
+// Combines the nparts partial records of every row (grid: row blocks x
+// heads, 256 threads): o = sum_i w_i o_i / sum_i w_i l_i with
+// w_i = exp(m_i - max_j m_j), parts in order.  The part holding key 0 has a
+// finite maximum for every row, so the overall one is finite; a part whose
+// keys are all masked for a row (or that has no keys) has m_i = -inf and
+// w_i = 0.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill_merge8(const float* __restrict__ part,
+                                                             float* __restrict__ out, int ldo,
+                                                             int n, int nparts) {
+  const int p0 = blockIdx.x * kPrefillQB, h = blockIdx.y;
+  constexpr size_t RF = attn_prefill_part_floats(HD);
+  const size_t stride = static_cast<size_t>(gridDim.y) * gridDim.x * kPrefillQB * RF;
+  const float* r0 = part + (static_cast<size_t>(h) * gridDim.x + blockIdx.x) * kPrefillQB * RF;
+  constexpr int C4 = HD / 4;  // float4 columns per row
+  for (int i = threadIdx.x; i < kPrefillQB * C4; i += 256) {
+    const int row = i / C4, c = 4 * (i % C4);
+    const int p = p0 + row;
+    if (p >= n) continue;
+    const float* a = r0 + row * RF;
+    float mm = -INFINITY;
+    for (int k = 0; k < nparts; ++k) mm = fmaxf(mm, a[k * stride + HD]);
+    float l = 0.f;
+    pf4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nparts; ++k) {
+      const float* b = a + k * stride;
+      const float mk = b[HD];
+      const float w = mk == -INFINITY ? 0.f : expf(mk - mm);
+      l += w * b[HD + 1];
+      o += w * *reinterpret_cast<const pf4*>(b + c);
+    }
+    *reinterpret_cast<pf4*>(out + static_cast<size_t>(p) * ldo + h * HD + c) = o * (1.f / l);
   }
 }
 

@@ -181,6 +181,42 @@ def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
                                atol=1e-7)
 
 
+@pytest.mark.parametrize("H,kvm,hd,S,pos0,n", [(4, 2, 128, 3200, 3000, 64), (12, 6, 128, 600, 0, 512),
+                                              (12, 6, 128, 1100, 1000, 70), (8, 8, 128, 4096, 3968, 128),
+                                              (32, 4, 128, 520, 0, 512), (8, 2, 64, 300, 130, 70)])
+def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
+    """kl_attn_prefill_ws: with few (row block, head) pairs far into the
+    context (the first four cases) each row block's keys run in up to 4
+    parts merged afterwards; every row against the oracle's MHA and within
+    2e-5 of kl_attn_prefill.  32 heads x 8 row blocks fill the CUs (one part)
+    and head size 64 has no split: both the same as kl_attn_prefill."""
+    rng = np.random.default_rng(H * S + pos0 + n + 7)
+    kvd = H // kvm * hd
+    kc = rng.standard_normal((1, S, kvd)).astype(np.float32)
+    vc = rng.standard_normal((1, S, kvd)).astype(np.float32)
+    q = rng.standard_normal((n, H * hd)).astype(np.float32)
+    dk, dv, dq = D(K, kc.ravel()), D(K, vc.ravel()), D(K, q)
+    do, du = K.DeviceArray(n * H * hd), K.DeviceArray(n * H * hd)
+    need = C.c_size_t(0)
+    ok(K.lib.kl_attn_prefill_workspace_size(n, H, hd, C.byref(need)), "workspace size")
+    assert (need.value > 0) == (hd == 128)
+    ws = K.DeviceArray(max(1, need.value // 4))
+    ok(K.lib.kl_attn_prefill_ws(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd, do.ptr,
+                                H * hd, ws.ptr, need.value, None), "kl_attn_prefill_ws")
+    ok(K.lib.kl_attn_prefill(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd, du.ptr,
+                             H * hd, None), "kl_attn_prefill")
+    out = do.numpy().reshape(n, H * hd)
+    whole = du.numpy().reshape(n, H * hd)
+    assert np.max(np.abs(out - whole)) < 2e-5
+    if H * ((n + 63) // 64) < 256 and hd == 128 and pos0 > 0:
+        # split: a workspace short of one float is refused
+        assert K.lib.kl_attn_prefill_ws(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd,
+                                        do.ptr, H * hd, ws.ptr, need.value - 4, None) == -6
+    for r in range(n):
+        ref = O.mha(pos0 + r, H, 0, S, kvd, kvm, hd, q[r], kc, vc)
+        assert np.max(np.abs(out[r] - ref)) < 2e-5, r
+
+
 # ------------------------------------------------------- whole prompt -------
 PREFILL_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"]
 
