@@ -13,10 +13,12 @@ on both sides.  Prints one JSON line.
   achieved_GBps  algorithmic HBM bytes of the timed steps / time
   roofline       the dominant kernel: in the default persistent mode the
                  whole-token kernel k_decode_persistent (one launch = one
-                 decode step, so its bytes are the step's algorithmic bytes);
-                 in --mode multi the W1/W3 + SwiGLU GEMV.  Achieved = bytes per
-                 launch / average launch duration, measured with HIP events
-                 around each launch on the engine's stream
+                 decode step, so its bytes are the step's algorithmic bytes
+                 and its average launch duration over the timed region is the
+                 region's HIP-event time per step; the per-launch events of
+                 --profile-steps more steps are reported beside it); in --mode
+                 multi the W1/W3 + SwiGLU GEMV, timed with HIP events around
+                 each of its launches in the profile steps
   prefill        the batched prompt prefill of cfg 5 (Qwen3-4B shape, 512
                  tokens) on the matrix cores: prompt tok/s, TFLOP/s against the
                  fp32 MFMA peak, and the MFMA-busy fraction rocprofv3 measured
@@ -304,9 +306,16 @@ def main() -> int:
     prof = eng.profile(int(toks[-1]), prof_pos, args.profile_steps)
     per_step_eager = sum(v[0] * v[1] for v in prof.values()) / args.profile_steps
     if persistent:
+        # One launch is one decode step and the timed steps run back to back
+        # on the engine's stream, so the kernel's average launch duration over
+        # the timed region is the HIP-event time of that region per step (it
+        # includes the few-microsecond gaps between launches); the algorithmic
+        # bytes per launch are the timed positions' average.  The profile
+        # steps' per-launch events are reported beside it.
         dom_name = "k_decode_persistent (whole decode step: every layer, classifier, argmax)"
-        dom_ms = prof["step"][0]
-        dom_bytes = cfg.decode_bytes(prof_pos, args.profile_steps) / args.profile_steps
+        dom_ms = ms / steps
+        dom_bytes = step_bytes / steps
+        prof_bytes = cfg.decode_bytes(prof_pos, args.profile_steps) / args.profile_steps
     else:
         dom_name = "k_w13_swiglu (RMSNorm + W1/W3 GEMV + SwiGLU)"
         dom_ms = prof["w13"][0]
@@ -383,10 +392,18 @@ def main() -> int:
             "traffic_source": traffic_src,
             "bytes_per_launch": int(dom_bytes),
             "avg_launch_ms": round(dom_ms, 5),
+            "over": ("the timed region (HIP events around its back-to-back launches)" if persistent
+                     else f"{args.profile_steps} profile steps (HIP events around each launch)"),
         },
         "launch_ms": {k: round(v[0], 5) for k, v in prof.items() if v[1]},
         "cpu_baseline": cpu,
     }
+    if persistent:
+        out["roofline"]["profile_steps"] = {
+            "positions": f"{prof_pos}..{prof_pos + args.profile_steps - 1}",
+            "avg_launch_ms": round(prof["step"][0], 5),
+            "achieved": round(prof_bytes / (prof["step"][0] / 1e3) / 1e9, 1),
+            "frac": round(prof_bytes / (prof["step"][0] / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
     if hbm is not None:
         hbm["decode_frac_of_read"] = round(gbps / hbm["read_GBps"], 4)
         hbm["kernel_frac_of_read"] = round(dom_gbps / hbm["read_GBps"], 4)
