@@ -16,6 +16,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <map>
 #include <tuple>
 
@@ -47,6 +48,7 @@ class LtGemm {
       if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
     }
     if (ws_) (void)hipFree(ws_);
+    if (scratch_) (void)hipFree(scratch_);
     if (handle_) hipblasLtDestroy(handle_);
   }
 
@@ -68,8 +70,12 @@ class LtGemm {
     Plan* p = plan(M, N, K, lda, ldw, ldc, false, w_stride, c_stride);
     if (!p) return false;
     const float alpha = 1.f, beta = 0.f;
-    return hipblasLtMatmul(handle_, p->op, &alpha, W0, p->lw, A, p->la, &beta, C0, p->lc, C0,
-                           p->lc, &p->algo, ws_, kWorkspaceBytes, st) == HIPBLAS_STATUS_SUCCESS;
+    auto run = [&](const hipblasLtMatmulAlgo_t& algo) {
+      return hipblasLtMatmul(handle_, p->op, &alpha, W0, p->lw, A, p->la, &beta, C0, p->lc, C0,
+                             p->lc, &algo, ws_, kWorkspaceBytes, st) == HIPBLAS_STATUS_SUCCESS;
+    };
+    tune(p, st, run);  // C = product: the trial runs write the same result
+    return run(p->algo);
   }
 
   // C (+)= A . W^T (+ bias) on stream st; false if the shape has no plan or
@@ -82,17 +88,83 @@ class LtGemm {
                                                 sizeof(bias)) != HIPBLAS_STATUS_SUCCESS)
       return false;
     const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
+    if (!p->tuned) {
+      // Trial runs of an accumulating product go to a scratch output (C = product
+      // there), so C is accumulated into exactly once.
+      float* out = accumulate ? tune_scratch(static_cast<size_t>(M) * ldc) : C;
+      const float b0 = 0.f;
+      if (out)
+        tune(p, st, [&](const hipblasLtMatmulAlgo_t& algo) {
+          return hipblasLtMatmul(handle_, p->op, &alpha, W, p->lw, A, p->la, &b0, out, p->lc, out,
+                                 p->lc, &algo, ws_, kWorkspaceBytes, st) == HIPBLAS_STATUS_SUCCESS;
+        });
+      p->tuned = true;
+    }
     return hipblasLtMatmul(handle_, p->op, &alpha, W, p->lw, A, p->la, &beta, C, p->lc, C, p->lc,
                            &p->algo, ws_, kWorkspaceBytes, st) == HIPBLAS_STATUS_SUCCESS;
   }
 
  private:
+  static constexpr int kCandidates = 8;  // heuristic algorithms timed per shape
+
   struct Plan {
     hipblasLtMatmulDesc_t op = nullptr;
     hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
     hipblasLtMatmulAlgo_t algo{};
+    hipblasLtMatmulAlgo_t cand[kCandidates]{};
+    int ncand = 0;
     bool ok = false;
+    bool tuned = false;
   };
+
+  // Times each heuristic candidate of a plan once (one warm-up and three
+  // timed runs of `run` on stream st, on the real operands) and keeps the
+  // fastest; the library's first choice stays where timing fails.
+  // KL_LT_TUNE=0 keeps the first choice without timing.
+  template <class Run>
+  void tune(Plan* p, hipStream_t st, Run run) {
+    if (p->tuned) return;
+    p->tuned = true;
+    const char* env = std::getenv("KL_LT_TUNE");
+    if (p->ncand < 2 || (env && std::atoi(env) == 0)) return;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+      if (e0) (void)hipEventDestroy(e0);
+      return;
+    }
+    float best = 0.f;
+    int bi = -1;
+    for (int i = 0; i < p->ncand; ++i) {
+      if (!run(p->cand[i])) continue;
+      bool good = hipEventRecord(e0, st) == hipSuccess;
+      for (int r = 0; r < 3 && good; ++r) good = run(p->cand[i]);
+      float ms = 0.f;
+      good = good && hipEventRecord(e1, st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+             hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+      if (good && (bi < 0 || ms < best)) {
+        best = ms;
+        bi = i;
+      }
+    }
+    if (bi >= 0) p->algo = p->cand[bi];
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+
+  // Scratch output of at least n floats for the trial runs (grown on demand).
+  float* tune_scratch(size_t n) {
+    if (n > scratch_n_) {
+      if (scratch_) (void)hipFree(scratch_);
+      scratch_ = nullptr;
+      scratch_n_ = 0;
+      if (hipMalloc(&scratch_, n * sizeof(float)) != hipSuccess) {
+        scratch_ = nullptr;
+        return nullptr;
+      }
+      scratch_n_ = n;
+    }
+    return scratch_;
+  }
   typedef std::tuple<int, int, int, int, int, int, bool, long long, long long> Key;
 
   // One plan per shape; w_stride > 0 makes it a batch of two (A shared).
@@ -138,13 +210,15 @@ class LtGemm {
       const uint64_t wsb = kWorkspaceBytes;
       good = good && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                            &wsb, sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS;
-      hipblasLtMatmulHeuristicResult_t res[1];
+      hipblasLtMatmulHeuristicResult_t res[kCandidates];
       int n = 0;
-      good = good &&
-             hipblasLtMatmulAlgoGetHeuristic(handle_, p.op, p.lw, p.la, p.lc, p.lc, pref, 1, res, &n) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-             n > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= kWorkspaceBytes;
-      if (good) p.algo = res[0].algo;
+      good = good && hipblasLtMatmulAlgoGetHeuristic(handle_, p.op, p.lw, p.la, p.lc, p.lc, pref,
+                                                     kCandidates, res, &n) == HIPBLAS_STATUS_SUCCESS;
+      for (int i = 0; good && i < n; ++i)
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kWorkspaceBytes)
+          p.cand[p.ncand++] = res[i].algo;
+      good = good && p.ncand > 0;
+      if (good) p.algo = p.cand[0];
       if (pref) hipblasLtMatmulPreferenceDestroy(pref);
     }
     p.ok = good;
@@ -153,6 +227,8 @@ class LtGemm {
 
   hipblasLtHandle_t handle_ = nullptr;
   void* ws_ = nullptr;
+  float* scratch_ = nullptr;  // trial outputs of accumulating products
+  size_t scratch_n_ = 0;
   std::map<Key, Plan> plans_;
 };
 
