@@ -188,6 +188,18 @@ int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ld
                  int ldk, int pos0, int n_pos, const float* sin_cache, const float* cos_cache,
                  void* stream);
 
+/* Qwen3's per-head q/k RMSNorm (model/qwen3.cpp:485-500; RMSNormKernelDim
+ * semantics, y = w * (x / sqrt(mean(x^2) + eps))) followed by RoPEKernel on
+ * n_pos prefill rows in one pass (no reference counterpart for the fusion:
+ * the reference applies the two per token).  Row r of q (q_heads heads,
+ * stride ldq) and of k (kv_heads heads, stride ldk) at position pos0 + r;
+ * every k head is rotated.  head_size 64 or 128 (else KL_EUNSUPP); the same
+ * values as kl_rmsnorm_rows then kl_rope_rows up to float rounding. */
+int kl_qk_norm_rope_rows(int style, int head_size, int q_heads, int kv_heads, float* q, int ldq,
+                         float* k, int ldk, const float* q_norm, const float* k_norm, float eps,
+                         int pos0, int n_pos, const float* sin_cache, const float* cos_cache,
+                         void* stream);
+
 /* MHAKernel (KI:22-28) for query positions pos0 .. pos0+n_pos-1 at once:
  * row r of q (stride ldq, head_num*head_size floats) attends key/value rows
  * 0 .. pos0+r of one layer's caches ([seq_len][kv_dim]), causal; out row r

@@ -100,6 +100,8 @@ _SIGS = {
     "kl_rope_rows": (_i, [_i, _i, _i, _i, _p, _i, _p, _i, _i, _i, _p, _p, _p]),
     "kl_attn_prefill": (_i, [_i, _i, _i, _i, _i, _p, _i, _p, _p, _i, _p, _i, _p]),
     "kl_hbm_probe": (_i, [C.c_size_t, _i, _fp, _fp]),
+    "kl_qk_norm_rope_rows": (_i, [_i, _i, _i, _i, _p, _i, _p, _i, _p, _p, C.c_float, _i, _i, _p, _p,
+                                  _p]),
     "kl_attn_prefill_workspace_size": (_i, [_i, _i, _i, C.POINTER(C.c_size_t)]),
     "kl_attn_prefill_ws": (_i, [_i, _i, _i, _i, _i, _p, _i, _p, _p, _i, _p, _i, _p, C.c_size_t,
                                 _p]),

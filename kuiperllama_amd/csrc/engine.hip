@@ -1577,12 +1577,17 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
       PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, nullptr, 1, hs));
     }
-    if (e->transform == 2) {  // Qwen3 per-head q/k RMSNorm, eps 1e-6
-      PF(kl_rmsnorm_rows(e->pf_q, Ld.qn, e->pf_q, n * H, hd, 1e-6f, st));
-      PF(kl_rmsnorm_rows(krow, Ld.kn, krow, n * KVH, hd, 1e-6f, st));
+    if (e->transform == 2 && (hd == 64 || hd == 128)) {  // Qwen3 q/k RMSNorm (eps 1e-6) + RoPE
+      PF(kl_qk_norm_rope_rows(e->rope_style, hd, H, KVH, e->pf_q, Dq, krow, Dkv, Ld.qn, Ld.kn, 1e-6f,
+                              pos0, n, e->sin_t, e->cos_t, st));
+    } else {
+      if (e->transform == 2) {
+        PF(kl_rmsnorm_rows(e->pf_q, Ld.qn, e->pf_q, n * H, hd, 1e-6f, st));
+        PF(kl_rmsnorm_rows(krow, Ld.kn, krow, n * KVH, hd, 1e-6f, st));
+      }
+      PF(kl_rope_rows(e->rope_style, Dq, Dkv, hd, e->pf_q, Dq, krow, Dkv, pos0, n, e->sin_t,
+                      e->cos_t, st));
     }
-    PF(kl_rope_rows(e->rope_style, Dq, Dkv, hd, e->pf_q, Dq, krow, Dkv, pos0, n, e->sin_t,
-                    e->cos_t, st));
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     // pf_ws (the own GEMM's split-K partials) is free between the GEMMs; it
     // holds the key-range parts of the attention where the rows are few.

@@ -217,6 +217,34 @@ def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
         assert np.max(np.abs(out[r] - ref)) < 2e-5, r
 
 
+@pytest.mark.parametrize("style,hd,H,KVH,pos0,n", [(1, 128, 32, 8, 0, 40), (1, 128, 16, 8, 300, 17),
+                                                  (0, 128, 8, 2, 5, 9), (1, 64, 8, 4, 7, 33),
+                                                  (0, 64, 4, 4, 0, 5)])
+def test_qk_norm_rope_rows_matches_two_step(K, O, gpu, style, hd, H, KVH, pos0, n):
+    """The fused Qwen3 q/k RMSNorm + RoPE of the prefill against the two-step
+    path it replaces (kl_rmsnorm_rows per head, then kl_rope_rows, both pinned
+    to the oracle): every element within a few float roundings."""
+    rng = np.random.default_rng(hd * H + pos0 + n + style)
+    S = pos0 + n + 4
+    q = rng.standard_normal((n, H * hd)).astype(np.float32)
+    k = rng.standard_normal((n, KVH * hd)).astype(np.float32)
+    qn = (1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    sin_t, cos_t = K.DeviceArray(S * hd), K.DeviceArray(S * hd)
+    ok(K.lib.kl_sincos_table(hd, S, 1e6, sin_t.ptr, cos_t.ptr), "kl_sincos_table")
+    dq, dk, dqn, dkn = D(K, q), D(K, k), D(K, qn), D(K, kn)
+    dq2, dk2 = D(K, q), D(K, k)
+    ok(K.lib.kl_qk_norm_rope_rows(style, hd, H, KVH, dq.ptr, H * hd, dk.ptr, KVH * hd, dqn.ptr, dkn.ptr,
+                                  1e-6, pos0, n, sin_t.ptr, cos_t.ptr, None), "kl_qk_norm_rope_rows")
+    ok(K.lib.kl_rmsnorm_rows(dq2.ptr, dqn.ptr, dq2.ptr, n * H, hd, C.c_float(1e-6), None), "norm q")
+    ok(K.lib.kl_rmsnorm_rows(dk2.ptr, dkn.ptr, dk2.ptr, n * KVH, hd, C.c_float(1e-6), None), "norm k")
+    ok(K.lib.kl_rope_rows(style, H * hd, KVH * hd, hd, dq2.ptr, H * hd, dk2.ptr, KVH * hd, pos0, n,
+                          sin_t.ptr, cos_t.ptr, None), "kl_rope_rows")
+    for a, b in ((dq, dq2), (dk, dk2)):
+        x, y = a.numpy(), b.numpy()
+        assert np.max(np.abs(x - y)) <= 4e-7 * np.max(np.abs(y)), np.max(np.abs(x - y))
+
+
 # ------------------------------------------------------- whole prompt -------
 PREFILL_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"]
 
