@@ -410,6 +410,9 @@ def test_full_size_prefill_vs_steps(K, gpu, name, P):
     nxt, lg, ms = eng.prefill(prompt)
     print(f"{name}: prefill of {P} tokens in {ms:.1f} ms", flush=True)
     check_gemm_calls(eng, K.PREFILL_GEMM_OWN if cfg.quant else K.PREFILL_GEMM_LIBRARY)
+    # The kernels chosen on the first call stay: a second prefill is bitwise the same.
+    nxt2, lg2, _ = eng.prefill(prompt)
+    assert nxt2 == nxt and np.array_equal(lg2, lg)
     if name == "qwen3_4b":
         before = eng.prefill_gemm_calls()
         eng.set_prefill_gemm(K.PREFILL_GEMM_OWN)
