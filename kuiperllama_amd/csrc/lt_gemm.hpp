@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <map>
@@ -105,7 +106,7 @@ class LtGemm {
   }
 
  private:
-  static constexpr int kCandidates = 8;  // heuristic algorithms timed per shape
+  static constexpr int kCandidates = 16;  // at most this many heuristic algorithms per shape
 
   struct Plan {
     hipblasLtMatmulDesc_t op = nullptr;
@@ -211,9 +212,11 @@ class LtGemm {
       good = good && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                            &wsb, sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS;
       hipblasLtMatmulHeuristicResult_t res[kCandidates];
-      int n = 0;
+      int n = 0, want = kCandidates;  // KL_LT_CANDIDATES: how many to time (1 .. kCandidates)
+      if (const char* env = std::getenv("KL_LT_CANDIDATES"))
+        want = std::max(1, std::min(kCandidates, std::atoi(env)));
       good = good && hipblasLtMatmulAlgoGetHeuristic(handle_, p.op, p.lw, p.la, p.lc, p.lc, pref,
-                                                     kCandidates, res, &n) == HIPBLAS_STATUS_SUCCESS;
+                                                     want, res, &n) == HIPBLAS_STATUS_SUCCESS;
       for (int i = 0; good && i < n; ++i)
         if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kWorkspaceBytes)
           p.cand[p.ncand++] = res[i].algo;
