@@ -337,7 +337,10 @@ int kl_engine_generate(kl_engine* e, const int32_t* prompt, int P, int n_new, in
                        float* decode_ms);
 /* Benchmark run: like kl_engine_generate with n_warmup + n_timed sampled
  * tokens, where *timed_ms is the device time (HIP events on the engine's
- * stream) of the last n_timed steps only.  out_tokens[n_warmup + n_timed]. */
+ * stream) of the last n_timed steps only.  out_tokens[n_warmup + n_timed].
+ * With kl_engine_set_prefill on (and n_warmup >= 1, P >= 2) the prompt runs
+ * as one batched prefill, which also samples the first warm-up token; the
+ * timed steps are at the same positions either way. */
 int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, int n_timed,
                     int32_t* out_tokens, float* timed_ms);
 /* Batched prompt prefill: positions 0 .. P-1 of `prompt` through every layer
@@ -357,18 +360,6 @@ int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next,
  * and *decode_ms covers the n_new - 1 decode steps that follow.  Returns
  * KL_EUNSUPP (and stays off) where the prefill does not support the model. */
 int kl_engine_set_prefill(kl_engine* e, int enable);
-/* Which GEMM runs the prefill's projections of an fp32 image:
- * KL_PREFILL_GEMM_LIBRARY (the default; hipBLASLt, for every shape it has a
- * plan for) or KL_PREFILL_GEMM_OWN (the MFMA GEMM of kl_gemm_f32 /
- * kl_gemm_f32_grouped for all of them; also the default where the environment
- * sets KL_PREFILL_GEMM=own).  int8 images always run the own GEMM, so
- * KL_PREFILL_GEMM_LIBRARY returns KL_EUNSUPP for them, as it does where the
- * library handle cannot be created.  kl_engine_prefill_gemm_calls counts the
- * projections each one has run since the engine was created. */
-#define KL_PREFILL_GEMM_LIBRARY 0
-#define KL_PREFILL_GEMM_OWN 1
-int kl_engine_set_prefill_gemm(kl_engine* e, int backend);
-int kl_engine_prefill_gemm_calls(const kl_engine* e, int64_t* library_calls, int64_t* own_calls);
 
 /* Per-kernel timing: runs `steps` decode steps from (token, pos0) without the
  * graph, with a HIP event recorded between consecutive launches on the

@@ -16,13 +16,12 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import (MODE_MULTI, MODE_PERSISTENT, PREFILL_GEMM_LIBRARY, PREFILL_GEMM_OWN, KlError,
-                   check, lib)
+from ._lib import MODE_MULTI, MODE_PERSISTENT, KlError, check, lib
 from .configs import ALL, BASELINE, TINY, Config
 
 __all__ = [
     "ALL", "BASELINE", "TINY", "Config", "DeviceArray", "Engine", "KlError", "Stream",
-    "MODE_MULTI", "MODE_PERSISTENT", "PREFILL_GEMM_LIBRARY", "PREFILL_GEMM_OWN",
+    "MODE_MULTI", "MODE_PERSISTENT",
     "synth_image", "synth_normal", "quantize_q8", "device_count",
 ]
 
@@ -212,18 +211,6 @@ class Engine:
     def set_prefill(self, enable: bool):
         """Whether generate() runs the prompt through the batched prefill."""
         check(lib.kl_engine_set_prefill(self.handle, int(enable)), "kl_engine_set_prefill")
-
-    def set_prefill_gemm(self, backend: int):
-        """PREFILL_GEMM_LIBRARY (hipBLASLt, fp32 images) or PREFILL_GEMM_OWN
-        (the MFMA GEMM of gemm.hpp) for the prefill's projections."""
-        check(lib.kl_engine_set_prefill_gemm(self.handle, int(backend)), "kl_engine_set_prefill_gemm")
-
-    def prefill_gemm_calls(self):
-        """(projections run by the library, by the own GEMM) since create."""
-        a, b = C.c_int64(0), C.c_int64(0)
-        check(lib.kl_engine_prefill_gemm_calls(self.handle, C.byref(a), C.byref(b)),
-              "kl_engine_prefill_gemm_calls")
-        return a.value, b.value
 
     def bench(self, prompt, n_warmup: int, n_timed: int):
         """Prompt + n_warmup untimed decode steps, then n_timed decode steps

@@ -19,7 +19,6 @@ KL_ETOKEN = -5
 KL_EWORKSPACE = -6
 KL_EDEVICE = -7
 MODE_PERSISTENT, MODE_MULTI = 0, 1
-PREFILL_GEMM_LIBRARY, PREFILL_GEMM_OWN = 0, 1
 
 FAMILY_LLAMA2, FAMILY_LLAMA3, FAMILY_QWEN2, FAMILY_QWEN3 = 0, 1, 2, 3
 ROPE_INTERLEAVED, ROPE_HALF = 0, 1
@@ -127,8 +126,6 @@ _SIGS = {
     "kl_engine_bench": (_i, [_p, _p, _i, _i, _i, _p, _fp]),
     "kl_engine_prefill": (_i, [_p, _p, _i, _i32p, _p, _fp]),
     "kl_engine_set_prefill": (_i, [_p, _i]),
-    "kl_engine_set_prefill_gemm": (_i, [_p, _i]),
-    "kl_engine_prefill_gemm_calls": (_i, [_p, _i64p, _i64p]),
     "kl_engine_profile": (_i, [_p, C.c_int32, C.c_int32, _i, _fp, _i32p]),
     "kl_engine_trace_step": (_i, [_p, C.c_int32, C.c_int32, _p, C.c_int64, _i32p, _i32p]),
     "kl_engine_buffers": (_i, [_p, C.POINTER(_p), C.POINTER(_p), C.POINTER(_p)]),

@@ -32,7 +32,6 @@
 #include "gemm_run.hpp"
 #include "gemv.hpp"
 #include "kuiper_hip.h"
-#include "lt_gemm.hpp"
 #include "persist.hpp"
 
 using namespace kl;
@@ -432,8 +431,10 @@ struct kl_engine {
   hipGraphExec_t graph_exec = nullptr;
   hipGraph_t graph = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  // Persistent step (persist.hpp): one cooperative launch per token.
-  int mode = KL_MODE_PERSISTENT;
+  // Persistent step (persist.hpp): one launch per token.  The multi-kernel
+  // step until setup_persistent() has shown that the persistent grid fits
+  // (every early return there leaves this mode).
+  int mode = KL_MODE_MULTI;
   bool persistent_ok = false;  // the persistent kernel fits this device and model
   // The persistent grid is launched with hipLaunchKernel where the occupancy
   // query shows every workgroup resident at once (one per CU), else with
@@ -477,12 +478,6 @@ struct kl_engine {
   int32_t* pf_next = nullptr;
   void* pf_am = nullptr;        // argmax workspace (zeroed once)
   size_t pf_am_bytes = 0;
-  // fp32 projections through hipBLASLt (created with the prefill scratch;
-  // null for int8 images or with KL_PREFILL_GEMM=own: then every projection
-  // runs the hand-written MFMA GEMM of gemm.hpp).
-  kl::LtGemm* lt = nullptr;
-  bool pf_own = false;               // KL_PREFILL_GEMM_OWN chosen
-  int64_t pf_lib_calls = 0, pf_own_calls = 0;
 };
 
 namespace {
@@ -1007,7 +1002,6 @@ int setup_persistent(kl_engine* e) {
   e->plain_launch = e->persistent_ok && blocks * e->cus >= e->nwg;
   if (const char* env = std::getenv("KL_PERSISTENT_LAUNCH"))
     if (std::strcmp(env, "cooperative") == 0) e->plain_launch = false;
-  if (const char* env = std::getenv("KL_PREFILL_GEMM")) e->pf_own = std::strcmp(env, "own") == 0;
   if (const char* env = std::getenv("KL_ENGINE_MODE")) {
     if (std::atoi(env) == KL_MODE_MULTI) e->mode = KL_MODE_MULTI;
   }
@@ -1022,7 +1016,6 @@ void release(kl_engine* e) {
   if (e->ev1) (void)hipEventDestroy(e->ev1);
   if (e->arena) (void)hipFree(e->arena);
   if (e->pf_buf) (void)hipFree(e->pf_buf);
-  delete e->lt;
   if (e->d_split) (void)hipFree(e->d_split);
   if (e->st_host) (void)hipHostFree(e->st_host);
   if (e->derr_host) (void)hipHostFree(e->derr_host);
@@ -1460,16 +1453,6 @@ GemmSeg proj_seg(const kl_engine* e, const WView& w, float* C, const float* bias
   return sg;
 }
 
-// Creates the hipBLASLt handle of an fp32 engine once; false if it cannot be.
-bool lt_handle(kl_engine* e) {
-  if (e->lt) return true;
-  e->lt = new kl::LtGemm();
-  if (e->lt->init()) return true;
-  delete e->lt;
-  e->lt = nullptr;
-  return false;
-}
-
 // Allocates the prefill scratch for `rows` rows (once; grows if needed).
 int prefill_scratch(kl_engine* e, int rows) {
   if (rows <= e->pf_rows) return KL_OK;
@@ -1513,7 +1496,6 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_rows = rows;
   err = hipMemsetAsync(e->pf_am, 0, am, e->stream);
   if (err != hipSuccess) return rc(err);
-  if (!e->quant && !e->pf_own) (void)lt_handle(e);  // without one, gemm.hpp runs every projection
   return KL_OK;
 }
 
@@ -1525,21 +1507,6 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
   void* st = e->stream;
   const size_t kv_layer = static_cast<size_t>(m.S) * Dkv;
   int r = kl_embedding(e->pf_tok + pos0, n, e->emb, m.V, D, e->pf_x, nullptr, st);
-  hipStream_t hs0 = static_cast<hipStream_t>(st);
-  // C[n x N] (+)= A[n x K] . W^T (+ bias) through hipBLASLt (fp32 images with
-  // a library plan for the shape; lib_ok tells which).
-  auto lib_ok = [&](const float* A, int K, const WView& w, int N, int ldc, const float* bias) {
-    const bool yes = !e->pf_own && e->lt != nullptr && e->lt->ready(n, N, K, K, K, ldc, bias != nullptr);
-    if (!yes) ++e->pf_own_calls;  // counted once per projection (or grouped launch)
-    return yes;
-  };
-  auto lib = [&](const float* A, int K, const WView& w, float* C, int N, int ldc, const float* bias,
-                 bool acc) {
-    ++e->pf_lib_calls;
-    return e->lt->gemm(A, n, K, K, static_cast<const float*>(w.w), N, K, C, ldc, bias, acc, hs0)
-               ? KL_OK
-               : KL_EDEVICE;
-  };
 #define PF(call)          \
   do {                    \
     if (r == KL_OK) r = (call); \
@@ -1553,25 +1520,8 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     hipStream_t hs = static_cast<hipStream_t>(st);
     // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
-    // q, k and v (k and v straight into the cache rows): three library
-    // GEMMs, or one grouped launch of gemm.hpp
-    if (lib_ok(e->pf_xn, D, Ld.wq, Dq, Dq, Ld.bq) && lib_ok(e->pf_xn, D, Ld.wk, Dkv, Dkv, Ld.bk) &&
-        lib_ok(e->pf_xn, D, Ld.wv, Dkv, Dkv, Ld.bv)) {
-      PF(lib(e->pf_xn, D, Ld.wq, e->pf_q, Dq, Dq, Ld.bq, false));
-      // K and V as one batch of two where there is no bias (their weights
-      // and cache rows lie at fixed distances); else two products.
-      const float* wk = static_cast<const float*>(Ld.wk.w);
-      const float* wv = static_cast<const float*>(Ld.wv.w);
-      const bool pair = !Ld.bk && !Ld.bv && r == KL_OK &&
-                        e->lt->gemm_pair(e->pf_xn, n, D, D, wk, wv - wk, Dkv, D, krow, vrow - krow,
-                                         Dkv, hs0);
-      if (pair) {
-        ++e->pf_lib_calls;
-      } else {
-        PF(lib(e->pf_xn, D, Ld.wk, krow, Dkv, Dkv, Ld.bk, false));
-        PF(lib(e->pf_xn, D, Ld.wv, vrow, Dkv, Dkv, Ld.bv, false));
-      }
-    } else {
+    // q, k and v in one grouped launch (k and v straight into the cache rows)
+    {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
@@ -1594,9 +1544,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, e->pf_ws,
                           e->pf_ws_bytes, st));
     const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
-    if (lib_ok(e->pf_att, Dq, Ld.wo, D, D, nullptr)) {
-      PF(lib(e->pf_att, Dq, Ld.wo, e->pf_x, D, D, nullptr, true));
-    } else {
+    {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
       const int sp = prefill_splits(n, D, Dq);
       if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
@@ -1604,29 +1552,13 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     }
     // feed_forward (llama3.cpp:671-719)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
-    if (lib_ok(e->pf_xn, D, Ld.w1, F, F, nullptr)) {
-      const float* w1 = static_cast<const float*>(Ld.w1.w);
-      const float* w3 = static_cast<const float*>(Ld.w3.w);
-      // W1 and W3 as one batch of two as well (at 512 rows each alone is 244
-      // library tiles, under one per CU; together they pack better).
-      const bool pair = r == KL_OK &&
-                        e->lt->gemm_pair(e->pf_xn, n, D, D, w1, w3 - w1, F, D, e->pf_h1,
-                                         e->pf_h3 - e->pf_h1, F, hs0);
-      if (pair) {
-        ++e->pf_lib_calls;
-      } else {
-        PF(lib(e->pf_xn, D, Ld.w1, e->pf_h1, F, F, nullptr, false));
-        PF(lib(e->pf_xn, D, Ld.w3, e->pf_h3, F, F, nullptr, false));
-      }
-    } else {
+    {
       const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
       PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, nullptr, 1, hs));
     }
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
-    if (lib_ok(e->pf_h1, F, Ld.w2, D, D, nullptr)) {
-      PF(lib(e->pf_h1, F, Ld.w2, e->pf_x, D, D, nullptr, true));
-    } else {
+    {
       const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
       const int sp = prefill_splits(n, D, F);
       if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
@@ -1645,26 +1577,6 @@ int kl_engine_set_prefill(kl_engine* e, int enable) {
   if (!e) return KL_EINVAL;
   if (enable && !prefill_supported(e)) return KL_EUNSUPP;
   e->use_prefill = enable != 0;
-  return KL_OK;
-}
-
-int kl_engine_set_prefill_gemm(kl_engine* e, int backend) {
-  if (!e) return KL_EINVAL;
-  if (backend == KL_PREFILL_GEMM_OWN) {
-    e->pf_own = true;
-    return KL_OK;
-  }
-  if (backend != KL_PREFILL_GEMM_LIBRARY) return KL_EINVAL;
-  if (e->quant) return KL_EUNSUPP;
-  if (!lt_handle(e)) return KL_EUNSUPP;
-  e->pf_own = false;
-  return KL_OK;
-}
-
-int kl_engine_prefill_gemm_calls(const kl_engine* e, int64_t* library_calls, int64_t* own_calls) {
-  if (!e || !library_calls || !own_calls) return KL_EINVAL;
-  *library_calls = e->pf_lib_calls;
-  *own_calls = e->pf_own_calls;
   return KL_OK;
 }
 
@@ -1785,14 +1697,30 @@ int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, in
   if (P + n_warmup + n_timed - 1 > e->lay.S) return KL_EINVAL;
   for (int i = 0; i < P; ++i)
     if (prompt[i] < 0 || prompt[i] >= e->lay.V) return KL_ETOKEN;
-  hipError_t err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
-                                  e->stream);
-  if (err != hipSuccess) return rc(err);
-  err = set_state(e, StepState{0, prompt[0], P, 0});
-  if (err != hipSuccess) return rc(err);
-  for (int i = 0; i < P - 1 + n_warmup; ++i) {
-    const int r = run_step(e);
+  // With the batched prefill on, the prompt (positions 0 .. P-1, the first
+  // warm-up step included) is one kl_engine_prefill call; the timed steps
+  // run at the same positions either way.
+  const bool batched = e->use_prefill && P >= 2 && n_warmup >= 1;
+  int32_t first = -1;
+  hipError_t err = hipSuccess;
+  if (batched) {
+    int r = kl_engine_prefill(e, prompt, P, &first, nullptr, nullptr);
     if (r != KL_OK) return r;
+    err = set_state(e, StepState{P, first, P, first});
+    if (err != hipSuccess) return rc(err);
+    for (int i = 0; i < n_warmup - 1; ++i) {
+      r = run_step(e);
+      if (r != KL_OK) return r;
+    }
+  } else {
+    err = hipMemcpyAsync(e->prompt, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice, e->stream);
+    if (err != hipSuccess) return rc(err);
+    err = set_state(e, StepState{0, prompt[0], P, 0});
+    if (err != hipSuccess) return rc(err);
+    for (int i = 0; i < P - 1 + n_warmup; ++i) {
+      const int r = run_step(e);
+      if (r != KL_OK) return r;
+    }
   }
   err = hipStreamSynchronize(e->stream);
   if (err == hipSuccess) err = hipEventRecord(e->ev0, e->stream);
@@ -1804,9 +1732,14 @@ int kl_engine_bench(kl_engine* e, const int32_t* prompt, int P, int n_warmup, in
   err = hipEventRecord(e->ev1, e->stream);
   if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
   if (err == hipSuccess) err = hipEventElapsedTime(timed_ms, e->ev0, e->ev1);
-  if (err == hipSuccess)
+  if (err == hipSuccess && batched) {
+    out_tokens[0] = first;  // sampled by the prefill at position P-1
+    err = hipMemcpy(out_tokens + 1, e->out_tokens + P, sizeof(int32_t) * (n_warmup + n_timed - 1),
+                    hipMemcpyDeviceToHost);
+  } else if (err == hipSuccess) {
     err = hipMemcpy(out_tokens, e->out_tokens + (P - 1), sizeof(int32_t) * (n_warmup + n_timed),
                     hipMemcpyDeviceToHost);
+  }
   if (err != hipSuccess) return rc(err);
   return check_device_error(e);
 }

@@ -356,8 +356,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
 // sum 0), and k_attn_prefill_merge8 combines the parts in order.
 constexpr int kPrefillKB8 = 128;
 
-// One partial record per query row: HD output floats, then max and sum.
-__host__ __device__ constexpr size_t attn_prefill_part_floats(int hd) { return hd + 2; }
+// One partial record per query row: HD output floats, then max and sum,
+// padded to a multiple of 4 floats so that every record (and every float4
+// column group the merge reads) starts 16-byte aligned.
+__host__ __device__ constexpr size_t attn_prefill_part_floats(int hd) { return hd + 4; }
 
 template <int HD>
 __global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restrict__ q, int ldq,

@@ -696,6 +696,17 @@ void BpeEncodeLayer::load(const char* bos, const char* eos, const char* stop2) {
       const JValue* id = t.get("id");
       const JValue* content = t.get("content");
       if (!id || !content) continue;
+      // An empty special token would match at every position and never
+      // advance the encoder, so such a file is refused.
+      if (content->str.empty()) {
+        encoder_.clear();
+        decoder_.clear();
+        special_.clear();
+        special_decoder_.clear();
+        status_ = base::error::ModelParseError("an added token of " + token_model_path_ +
+                                               " has empty content");
+        return;
+      }
       special_.emplace_back(content->str, static_cast<int32_t>(id->number));
       special_decoder_[static_cast<int32_t>(id->number)] = content->str;
       named[content->str] = static_cast<int32_t>(id->number);

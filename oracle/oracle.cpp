@@ -48,6 +48,64 @@ inline float arma_accumulate(const float* x, int n) {
   return acc1 + acc2;
 }
 
+typedef float ov8 __attribute__((vector_size(32)));
+typedef int8_t oq8 __attribute__((vector_size(8)));
+
+inline ov8 ld8(const float* p) {
+  ov8 v;
+  std::memcpy(&v, p, sizeof(v));
+  return v;
+}
+
+inline float fold8(const ov8 a) {
+  return ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+}
+
+// The int8 counterpart of q8_row_dot for RB rows x TB positions.  Needs
+// group_size % 8 == 0 and cols % 8 == 0, so that the 8 columns of a step
+// share one scale: each lane still forms (x * scale) * float(q).
+template <int RB, int TB>
+void tile_q8(const int8_t* Q, const float* S, int64_t row0, int cols, int gs, const float* X,
+             int64_t ldx, float* Y, int64_t ldy) {
+  ov8 acc[RB][TB];
+  for (int j = 0; j < RB; ++j)
+    for (int i = 0; i < TB; ++i) acc[j][i] = ov8{0, 0, 0, 0, 0, 0, 0, 0};
+  for (int c = 0; c < cols; c += 8) {
+    ov8 x[TB];
+    for (int i = 0; i < TB; ++i) x[i] = ld8(X + i * ldx + c);
+    for (int j = 0; j < RB; ++j) {
+      const int64_t base = (row0 + j) * cols + c;
+      oq8 qv;
+      std::memcpy(&qv, Q + base, sizeof(qv));
+      const ov8 qf = __builtin_convertvector(qv, ov8);
+      const float sc = S[base / gs];
+      for (int i = 0; i < TB; ++i) acc[j][i] += (x[i] * sc) * qf;
+    }
+  }
+  for (int j = 0; j < RB; ++j)
+    for (int i = 0; i < TB; ++i) Y[i * ldy + j] = fold8(acc[j][i]);
+}
+
+// One row of the int8 GEMV below: 8 interleaved accumulators of
+// (x[c] * scale) * float(q), folded as in dot8, then the scalar tail.
+inline float q8_row_dot(const float* x, const int8_t* q, const float* scales, int64_t base,
+                        int cols, int group_size) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int c = 0;
+  for (; c + 8 <= cols; c += 8) {
+    for (int k = 0; k < 8; ++k) {
+      const int64_t idx = base + c + k;
+      acc[k] += (x[c + k] * scales[idx / group_size]) * static_cast<float>(q[idx]);
+    }
+  }
+  float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+  for (; c < cols; ++c) {
+    const int64_t idx = base + c;
+    s += (x[c] * scales[idx / group_size]) * static_cast<float>(q[idx]);
+  }
+  return s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -69,26 +127,24 @@ void or_gemv_f32(const float* x, const float* W, float* y, int rows, int cols, f
 // no CPU int8 kernel, kernels_interfaces.cpp:54-61):
 //   y[r] = sum_c (x[c] * scales[(r*cols + c) / group_size]) * float(q[r*cols + c])
 // The group index is taken over the flattened matrix, as in the reference.
+// Where group_size and cols are multiples of 8, the 8 columns of a step share
+// one scale and tile_q8 evaluates the same lanes with vector instructions
+// (bitwise equal to q8_row_dot, which or_gemv_q8_scalar keeps for the test
+// that pins the two together).
 void or_gemv_q8(const float* x, const int8_t* q, const float* scales, float* y, int rows, int cols,
                 int group_size) {
+  if (group_size % 8 == 0 && cols % 8 == 0) {
 #pragma omp parallel for schedule(static)
-  for (int r = 0; r < rows; ++r) {
-    const int64_t base = (int64_t)r * cols;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int c = 0;
-    for (; c + 8 <= cols; c += 8) {
-      for (int k = 0; k < 8; ++k) {
-        const int64_t idx = base + c + k;
-        acc[k] += (x[c + k] * scales[idx / group_size]) * static_cast<float>(q[idx]);
-      }
-    }
-    float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
-    for (; c < cols; ++c) {
-      const int64_t idx = base + c;
-      s += (x[c] * scales[idx / group_size]) * static_cast<float>(q[idx]);
-    }
-    y[r] = s;
+    for (int r = 0; r < rows; ++r) tile_q8<1, 1>(q, scales, r, cols, group_size, x, 0, y + r, 0);
+    return;
   }
+  or_gemv_q8_scalar(x, q, scales, y, rows, cols, group_size);
+}
+
+void or_gemv_q8_scalar(const float* x, const int8_t* q, const float* scales, float* y, int rows,
+                       int cols, int group_size) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) y[r] = q8_row_dot(x, q, scales, (int64_t)r * cols, cols, group_size);
 }
 
 // tools/export_llama.py:49-73 (quantize_q80): per contiguous group of
@@ -199,6 +255,33 @@ void or_softmax(float* x, int n) {
   for (int i = 0; i < n; ++i) x[i] = x[i] / sum;
 }
 
+}  // extern "C"
+
+namespace {
+
+// One head of or_mha: scores of head h against positions 0..pos of one
+// layer's caches, softmax, then the weighted sum of V in increasing t.
+inline void mha_head(int pos, int h, int kv_dim, int kv_mul, int head_size, float* oh,
+                     const float* qh, float* sh, const float* kcache, const float* vcache) {
+  const float scale = 1.f / std::sqrt(static_cast<float>(head_size));
+  const int64_t head_off = (int64_t)(h / kv_mul) * head_size;
+  for (int t = 0; t <= pos; ++t) {
+    const float* kt = kcache + (int64_t)t * kv_dim + head_off;
+    sh[t] = dot8(qh, kt, head_size) * scale;
+  }
+  or_softmax(sh, pos + 1);
+  for (int d = 0; d < head_size; ++d) oh[d] = 0.f;
+  for (int t = 0; t <= pos; ++t) {
+    const float* vt = vcache + (int64_t)t * kv_dim + head_off;
+    const float p = sh[t];
+    for (int d = 0; d < head_size; ++d) oh[d] += p * vt[d];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
 // kernels/cpu/mha_kernel.cpp:5-61 with softmax_kernel.cpp:4-15 and
 // scale_sum_kernel.cpp:5-22.  Per head h (kv head h / kv_mul):
 //   s_t = (q_h . K_t) * (1/sqrt(hd)), t in [0, pos]; softmax; out_h = sum_t p_t V_t
@@ -207,25 +290,11 @@ void or_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int
             int head_size, float* out, const float* q, float* score, const float* key_cache,
             const float* value_cache) {
   const int64_t layer_offset = (int64_t)layer_index * seq_len * kv_dim;
-  const float scale = 1.f / std::sqrt(static_cast<float>(head_size));
 #pragma omp parallel for schedule(static)
-  for (int h = 0; h < head_num; ++h) {
-    float* sh = score + (int64_t)h * seq_len;
-    const float* qh = q + (int64_t)h * head_size;
-    const int64_t head_off = (int64_t)(h / kv_mul) * head_size;
-    for (int t = 0; t <= pos; ++t) {
-      const float* kt = key_cache + layer_offset + (int64_t)t * kv_dim + head_off;
-      sh[t] = dot8(qh, kt, head_size) * scale;
-    }
-    or_softmax(sh, pos + 1);
-    float* oh = out + (int64_t)h * head_size;
-    for (int d = 0; d < head_size; ++d) oh[d] = 0.f;
-    for (int t = 0; t <= pos; ++t) {
-      const float* vt = value_cache + layer_offset + (int64_t)t * kv_dim + head_off;
-      const float p = sh[t];
-      for (int d = 0; d < head_size; ++d) oh[d] += p * vt[d];
-    }
-  }
+  for (int h = 0; h < head_num; ++h)
+    mha_head(pos, h, kv_dim, kv_mul, head_size, out + (int64_t)h * head_size,
+             q + (int64_t)h * head_size, score + (int64_t)h * seq_len, key_cache + layer_offset,
+             value_cache + layer_offset);
 }
 
 // kernels/cpu/swiglu_kernel.cpp:3-23: a = a * (1 / (1 + exp(-a))); out = a * b.
@@ -517,24 +586,195 @@ int or_model_step(or_model* m, int32_t token, int32_t pos, float* logits) {
   return 0;
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Batched prompt: the same arithmetic as or_model_step run position after
+// position, reorganised so that each weight row is applied to many positions
+// while it is in cache.  Every output element is still one dot8 /
+// q8_row_dot-ordered sum (8 interleaved accumulators over increasing columns,
+// the same fold, the same tail), every per-row operation is the one the step
+// calls, and attention of a position reads only the cache rows at or before it,
+// which the layer's projections of all earlier positions have written first.
+// So the logits and cache rows are bitwise those of the sequential steps
+// (pinned by tests/test_oracle.py); only the time differs.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Y[i][j] = dot8(W_j, X_i) for RB rows of W and TB positions: one ov8
+// accumulator per pair holds dot8's 8 interleaved partial sums.
+template <int RB, int TB>
+void tile_f32(const float* W, int64_t ldw, const float* X, int64_t ldx, int n, float* Y,
+              int64_t ldy) {
+  ov8 acc[RB][TB];
+  for (int j = 0; j < RB; ++j)
+    for (int i = 0; i < TB; ++i) acc[j][i] = ov8{0, 0, 0, 0, 0, 0, 0, 0};
+  int c = 0;
+  for (; c + 8 <= n; c += 8) {
+    ov8 w[RB], x[TB];
+    for (int j = 0; j < RB; ++j) w[j] = ld8(W + j * ldw + c);
+    for (int i = 0; i < TB; ++i) x[i] = ld8(X + i * ldx + c);
+    for (int j = 0; j < RB; ++j)
+      for (int i = 0; i < TB; ++i) acc[j][i] += w[j] * x[i];
+  }
+  for (int j = 0; j < RB; ++j)
+    for (int i = 0; i < TB; ++i) {
+      float s = fold8(acc[j][i]);
+      for (int cc = c; cc < n; ++cc) s += W[j * ldw + cc] * X[i * ldx + cc];
+      Y[i * ldy + j] = s;
+    }
+}
+
+template <int RB>
+void tile_any(const or_model* m, const void* W, const float* S, int r, int cols, const float* X,
+              int64_t ldx, int tb, float* Y, int64_t ldy) {
+  if (m->quant) {
+    const int gs = m->group_size;
+    if (gs % 8 == 0 && cols % 8 == 0) {
+      const int8_t* Q = static_cast<const int8_t*>(W);
+      switch (tb) {
+        case 1: tile_q8<RB, 1>(Q, S, r, cols, gs, X, ldx, Y, ldy); break;
+        case 2: tile_q8<RB, 2>(Q, S, r, cols, gs, X, ldx, Y, ldy); break;
+        case 3: tile_q8<RB, 3>(Q, S, r, cols, gs, X, ldx, Y, ldy); break;
+        default: tile_q8<RB, 4>(Q, S, r, cols, gs, X, ldx, Y, ldy); break;
+      }
+    } else {
+      for (int j = 0; j < RB; ++j)
+        for (int i = 0; i < tb; ++i)
+          Y[i * ldy + j] = q8_row_dot(X + i * ldx, static_cast<const int8_t*>(W), S,
+                                      (int64_t)(r + j) * cols, cols, gs);
+    }
+    return;
+  }
+  const float* Wr = static_cast<const float*>(W) + (int64_t)r * cols;
+  switch (tb) {
+    case 1: tile_f32<RB, 1>(Wr, cols, X, ldx, cols, Y, ldy); break;
+    case 2: tile_f32<RB, 2>(Wr, cols, X, ldx, cols, Y, ldy); break;
+    case 3: tile_f32<RB, 3>(Wr, cols, X, ldx, cols, Y, ldy); break;
+    default: tile_f32<RB, 4>(Wr, cols, X, ldx, cols, Y, ldy); break;
+  }
+}
+
+// Y[i][r] (row stride ldy) = row r of W applied to X[i] (row stride ldx), for
+// i < n and r < rows: the GEMV of gemv_any for each position.  Positions go
+// in blocks of 64 (their inputs stay in each core's cache); threads take
+// pairs of weight rows, which stay in L1 across a block.
+void gemm_rows(const or_model* m, const void* W, const float* S, const float* X, int64_t ldx,
+               int n, float* Y, int64_t ldy, int rows, int cols) {
+  constexpr int kTB = 64;
+  for (int t0 = 0; t0 < n; t0 += kTB) {
+    const int tn = std::min(kTB, n - t0);
+#pragma omp parallel for schedule(static)
+    for (int rp = 0; rp < (rows + 1) / 2; ++rp) {
+      const int r = 2 * rp;
+      for (int t = t0; t < t0 + tn; t += 4) {
+        const int tb = std::min(4, t0 + tn - t);
+        const float* Xt = X + (int64_t)t * ldx;
+        float* Yt = Y + (int64_t)t * ldy + r;
+        if (r + 1 < rows) tile_any<2>(m, W, S, r, cols, Xt, ldx, tb, Yt, ldy);
+        else tile_any<1>(m, W, S, r, cols, Xt, ldx, tb, Yt, ldy);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int or_model_prompt(or_model* m, const int32_t* tokens, int n_tokens, int32_t pos0, float* logits) {
+  if (n_tokens <= 0 || pos0 < 0 || (int64_t)pos0 + n_tokens > m->S) return -2;
+  for (int i = 0; i < n_tokens; ++i)
+    if (tokens[i] < 0 || tokens[i] >= m->V) return -1;
+  const int D = m->D, Dq = m->Dq, Dkv = m->Dkv, F = m->F, S = m->S, hd = m->hd, H = m->H;
+  const int kv_mul = m->H / m->KVH;
+  const bool q8 = m->quant != 0;
+  constexpr int kChunk = 512;  // positions per pass (bounds the scratch)
+  const int R = std::min(kChunk, n_tokens);
+  const int DX = std::max(D, Dq);
+  std::vector<float> X((size_t)R * D), XB((size_t)R * DX), Q((size_t)R * Dq), A((size_t)R * D),
+      HB((size_t)R * F), HB2((size_t)R * F);
+  for (int c0 = 0; c0 < n_tokens; c0 += kChunk) {
+    const int n = std::min(kChunk, n_tokens - c0);
+    const int p0 = pos0 + c0;
+    or_embedding(tokens + c0, n, m->emb, m->V, D, X.data());
+    for (int l = 0; l < m->L; ++l) {
+      float* kslot = m->kcache.data() + ((size_t)l * S + p0) * Dkv;
+      float* vslot = m->vcache.data() + ((size_t)l * S + p0) * Dkv;
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < n; ++i)
+        or_rmsnorm(&X[(size_t)i * D], m->rms_att[l], &XB[(size_t)i * DX], D, m->eps);
+      gemm_rows(m, m->wq[l], q8 ? m->sq[l] : nullptr, XB.data(), DX, n, Q.data(), Dq, Dq, D);
+      gemm_rows(m, m->wk[l], q8 ? m->sk[l] : nullptr, XB.data(), DX, n, kslot, Dkv, Dkv, D);
+      gemm_rows(m, m->wv[l], q8 ? m->sv[l] : nullptr, XB.data(), DX, n, vslot, Dkv, Dkv, D);
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < n; ++i) {
+        float* qi = &Q[(size_t)i * Dq];
+        float* ki = kslot + (size_t)i * Dkv;
+        float* vi = vslot + (size_t)i * Dkv;
+        if (!m->bq.empty()) or_add(qi, m->bq[l], qi, Dq);
+        if (m->family == OR_QWEN3) or_rmsnorm_rows(qi, m->q_norm[l], qi, Dq / hd, hd, 1e-6f);
+        if (!m->bk.empty()) or_add(ki, m->bk[l], ki, Dkv);
+        if (m->family == OR_QWEN3) or_rmsnorm_rows(ki, m->k_norm[l], ki, Dkv / hd, hd, 1e-6f);
+        if (!m->bv.empty()) or_add(vi, m->bv[l], vi, Dkv);
+        or_rope(m->rope_style, Dq, Dkv, hd, qi, ki, p0 + i, m->sin_t.data(), m->cos_t.data());
+      }
+      const float* kl = m->kcache.data() + (size_t)l * S * Dkv;
+      const float* vl = m->vcache.data() + (size_t)l * S * Dkv;
+#pragma omp parallel
+      {
+        std::vector<float> sc(S);
+#pragma omp for schedule(dynamic, 1)
+        for (int ih = 0; ih < n * H; ++ih) {
+          const int i = n - 1 - ih / H, h = ih % H;  // the longest rows first
+          mha_head(p0 + i, h, Dkv, kv_mul, hd, &XB[(size_t)i * DX + (size_t)h * hd],
+                   &Q[(size_t)i * Dq + (size_t)h * hd], sc.data(), kl, vl);
+        }
+      }
+      gemm_rows(m, m->wo[l], q8 ? m->so[l] : nullptr, XB.data(), DX, n, A.data(), D, D, Dq);
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < n; ++i) {
+        float* xi = &X[(size_t)i * D];
+        or_add(xi, &A[(size_t)i * D], xi, D);
+        or_rmsnorm(xi, m->rms_ffn[l], &XB[(size_t)i * DX], D, m->eps);
+      }
+      gemm_rows(m, m->w1[l], q8 ? m->s1[l] : nullptr, XB.data(), DX, n, HB.data(), F, F, D);
+      gemm_rows(m, m->w3[l], q8 ? m->s3[l] : nullptr, XB.data(), DX, n, HB2.data(), F, F, D);
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < n; ++i)
+        or_swiglu(&HB[(size_t)i * F], &HB2[(size_t)i * F], &HB[(size_t)i * F], F);
+      gemm_rows(m, m->w2[l], q8 ? m->s2[l] : nullptr, HB.data(), F, n, A.data(), D, D, F);
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < n; ++i) or_add(&X[(size_t)i * D], &A[(size_t)i * D], &X[(size_t)i * D], D);
+    }
+    if (c0 + n == n_tokens) {
+      float* x = m->x.data();
+      std::memcpy(x, &X[(size_t)(n - 1) * D], sizeof(float) * D);
+      or_rmsnorm(x, m->rms_final, x, D, m->eps);
+      gemv_any(m, m->wcls, m->scls, x, m->logits.data(), m->V, D);
+    }
+  }
+  if (logits) std::memcpy(logits, m->logits.data(), sizeof(float) * m->V);
+  return 0;
+}
+
 // demo/main.cpp:5-47: prompt positions 0..P-2 run without sampling; from
 // position P-1 on, the current token is embedded, the step runs and the
 // argmax becomes the next token.  `next` starts at prompt[0]
 // (demo/main_qwen3.cpp:93), which keeps a 1-token prompt well defined.
 int or_model_generate(or_model* m, const int32_t* prompt, int P, int n_new, int32_t* out_tokens) {
   if (P <= 0 || n_new <= 0) return 0;
-  int32_t next = prompt[0];
+  // Positions 0..P-1 all take prompt tokens (at P-1 through the decode
+  // branch, whose `next` is prompt[P-1]); they run as one batched prompt,
+  // bitwise equal to stepping them one by one.
+  if (or_model_prompt(m, prompt, P, 0, nullptr) != 0) return -1;
+  int32_t next = static_cast<int32_t>(or_argmax(m->logits.data(), m->V));
   int n_out = 0;
-  const int total = P + n_new - 1;
-  for (int pos = 0; pos < total; ++pos) {
-    if (pos < P - 1) {
-      if (or_model_step(m, prompt[pos], pos, nullptr) != 0) return -1;
-      next = prompt[pos + 1];
-    } else {
-      if (or_model_step(m, next, pos, nullptr) != 0) return -1;
-      next = static_cast<int32_t>(or_argmax(m->logits.data(), m->V));
-      out_tokens[n_out++] = next;
-    }
+  out_tokens[n_out++] = next;
+  for (int pos = P; pos < P + n_new - 1; ++pos) {
+    if (or_model_step(m, next, pos, nullptr) != 0) return -1;
+    next = static_cast<int32_t>(or_argmax(m->logits.data(), m->V));
+    out_tokens[n_out++] = next;
   }
   return n_out;
 }

@@ -35,6 +35,11 @@ int or_get_threads(void);
 void or_gemv_f32(const float* x, const float* W, float* y, int rows, int cols, float scale);
 void or_gemv_q8(const float* x, const int8_t* q, const float* scales, float* y, int rows, int cols,
                 int group_size);
+/* The element-by-element loop of or_gemv_q8 (test hook: or_gemv_q8 takes a
+ * vector path where group_size and cols are multiples of 8; tests check the
+ * two are bitwise equal). */
+void or_gemv_q8_scalar(const float* x, const int8_t* q, const float* scales, float* y, int rows,
+                       int cols, int group_size);
 void or_quantize_q8(const float* w, int64_t n, int group_size, int8_t* q, float* scales);
 void or_dequant_q8(const int8_t* q, const float* scales, int64_t n, int group_size, float* out);
 void or_rmsnorm(const float* x, const float* w, float* y, int n, float eps);
@@ -64,6 +69,12 @@ void or_model_dims(const or_model* m, int32_t* out10);
 /* One reference forward step (embedding of `token` at `pos` + all layers +
  * final norm + classifier).  logits may be NULL. */
 int or_model_step(or_model* m, int32_t token, int32_t pos, float* logits);
+/* n_tokens prompt tokens at positions pos0 .. pos0+n_tokens-1, equal bit
+ * for bit (logits of the last position, cache rows) to or_model_step on each
+ * position in turn, but with each weight row applied to many positions while
+ * it is cached.  logits (of the last position) may be NULL.  Returns 0, -1 for
+ * a token outside the vocabulary, -2 for positions outside the cache. */
+int or_model_prompt(or_model* m, const int32_t* tokens, int n_tokens, int32_t pos0, float* logits);
 /* demo/main.cpp:5-47 greedy loop: P prompt tokens, then n_new sampled tokens
  * written to out_tokens.  Returns the number of tokens written. */
 int or_model_generate(or_model* m, const int32_t* prompt, int P, int n_new, int32_t* out_tokens);

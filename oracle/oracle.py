@@ -35,6 +35,7 @@ _sigs = {
     "or_get_threads": (_i, []),
     "or_gemv_f32": (None, [_p, _p, _p, _i, _i, _f]),
     "or_gemv_q8": (None, [_p, _p, _p, _p, _i, _i, _i]),
+    "or_gemv_q8_scalar": (None, [_p, _p, _p, _p, _i, _i, _i]),
     "or_quantize_q8": (None, [_p, C.c_int64, _i, _p, _p]),
     "or_dequant_q8": (None, [_p, _p, C.c_int64, _i, _p]),
     "or_rmsnorm": (None, [_p, _p, _p, _i, _f]),
@@ -51,6 +52,7 @@ _sigs = {
     "or_model_close": (None, [_p]),
     "or_model_dims": (None, [_p, _p]),
     "or_model_step": (_i, [_p, C.c_int32, C.c_int32, _p]),
+    "or_model_prompt": (_i, [_p, _p, _i, C.c_int32, _p]),
     "or_model_generate": (_i, [_p, _p, _i, _i, _p]),
     "or_model_kv_row": (None, [_p, _i, _i, _i, _p]),
 }
@@ -76,12 +78,13 @@ def gemv_f32(x, W, scale=1.0):
     return y
 
 
-def gemv_q8(x, q, s, rows, cols, gs):
+def gemv_q8(x, q, s, rows, cols, gs, scalar=False):
     x = _f32(x)
     q = np.ascontiguousarray(q, np.int8)
     s = _f32(s)
     y = np.empty(rows, np.float32)
-    lib.or_gemv_q8(x.ctypes.data, q.ctypes.data, s.ctypes.data, y.ctypes.data, rows, cols, gs)
+    fn = lib.or_gemv_q8_scalar if scalar else lib.or_gemv_q8
+    fn(x.ctypes.data, q.ctypes.data, s.ctypes.data, y.ctypes.data, rows, cols, gs)
     return y
 
 
@@ -198,6 +201,16 @@ class Model:
         rc = lib.or_model_step(self.handle, int(token), int(pos), logits.ctypes.data)
         if rc != 0:
             raise ValueError(f"or_model_step rc={rc}")
+        return logits
+
+    def prompt(self, tokens, pos0: int = 0) -> np.ndarray:
+        """Prompt tokens at positions pos0.. in one batched pass, bitwise equal
+        to step() on each position in turn; the last position's logits."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.vocab, np.float32)
+        rc = lib.or_model_prompt(self.handle, t.ctypes.data, t.size, int(pos0), logits.ctypes.data)
+        if rc != 0:
+            raise ValueError(f"or_model_prompt rc={rc}")
         return logits
 
     def generate(self, prompt, n_new: int) -> np.ndarray:

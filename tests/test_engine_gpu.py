@@ -450,3 +450,20 @@ def test_long_context_llama32_attention_shape(K, O, gpu):
     check = set(range(0, 4)) | set(range(380, 390)) | set(range(508, 520)) | set(range(700, 704)) \
         | set(range(1020, 1032))
     long_context(K, O, cfg, 1190, check, 8)
+
+
+def test_128_layer_image_runs_multi_kernel(K, O, gpu):
+    """Hand-off tags hold the layer in 7 bits, so an image of 128 or more
+    layers cannot run the persistent step: the engine must come up in the
+    multi-kernel mode (refusing the persistent one) and match the oracle."""
+    cfg = K.TINY["tiny_llama3"].with_(name="tiny_llama3_128l", layers=128, dim=64, hidden_dim=128,
+                                      heads=2, kv_heads=1, vocab=300)
+    img = K.synth_image(cfg)
+    eng = K.Engine(img, cfg)
+    assert eng.mode == K.MODE_MULTI
+    with pytest.raises(K.KlError):
+        eng.set_mode(K.MODE_PERSISTENT)
+    om = O.Model(img, cfg.family, cfg.quant)
+    for pos, t in enumerate(K.prompt_tokens(cfg, 6)):
+        nxt, lg = eng.step(int(t), pos)
+        assert rel(lg, om.step(int(t), pos)) < LOGIT_RTOL, pos

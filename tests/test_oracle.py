@@ -90,7 +90,8 @@ def test_dequant_exact_for_grid_values(O):
     assert np.array_equal(O.dequant_q8(q, s2, 64), w)
 
 
-@pytest.mark.parametrize("rows,cols,gs", [(8, 256, 64), (33, 4096, 64), (4, 96, 32)])
+@pytest.mark.parametrize("rows,cols,gs", [(8, 256, 64), (33, 4096, 64), (4, 96, 32), (5, 100, 20),
+                                           (7, 120, 40)])
 def test_gemv_q8_brute_force(O, rows, cols, gs):
     rng = np.random.default_rng(cols)
     q = rng.integers(-127, 128, rows * cols).astype(np.int8)
@@ -100,6 +101,8 @@ def test_gemv_q8_brute_force(O, rows, cols, gs):
     Wd = (np.repeat(s.astype(np.float64), gs) * q).reshape(rows, cols)
     ref = Wd @ x.astype(np.float64)
     assert rel_err(y, ref) < 1e-5
+    # the vector path (gs and cols multiples of 8) and the element loop agree bit for bit
+    assert np.array_equal(y, O.gemv_q8(x, q, s, rows, cols, gs, scalar=True))
 
 
 # ------------------------------------------------------------- RMSNorm ------
@@ -409,3 +412,71 @@ def test_model_rejects_truncated_image(K, O):
         O.Model(img[:-4], cfg.family, cfg.quant)
     with pytest.raises(ValueError):
         O.Model(img[:20], cfg.family, cfg.quant)
+
+
+# Shapes beyond the tiny set for the batched prompt: widths that are not a
+# multiple of 8 (dot8's scalar tail), int8 groups of 40 (vector path) and of
+# 20 (a group boundary inside an 8-column step: the scalar int8 path), and a
+# prompt longer than one 512-position pass.
+PROMPT_EXTRA = {
+    "odd_llama2": dict(base="tiny_llama2", dim=108, hidden_dim=230, heads=6, kv_heads=3, vocab=301),
+    "q8_g40": dict(base="tiny_q8", dim=120, hidden_dim=200, heads=4, kv_heads=2, vocab=500,
+                   group_size=40),
+    "q8_g20": dict(base="tiny_qwen2_q8", dim=120, hidden_dim=200, heads=4, kv_heads=2, vocab=500,
+                   group_size=20),
+    "long_llama3": dict(base="tiny_llama3", seq_len=700),
+}
+
+
+def _prompt_cfg(K, name):
+    if name in K.TINY:
+        return K.TINY[name]
+    kw = dict(PROMPT_EXTRA[name])
+    return K.TINY[kw.pop("base")].with_(name=name, **kw)
+
+
+@pytest.mark.parametrize("name", TINY_NAMES + list(PROMPT_EXTRA))
+def test_model_prompt_bitwise_equals_steps(K, O, name):
+    """or_model_prompt (each weight row applied to many positions while
+    cached) against or_model_step position by position: the last logits and
+    every cache row bit for bit, for a prompt from position 0 and for one
+    continuing a cache that steps filled; and generate() (which runs its
+    prompt batched) against the demo loop made of steps."""
+    cfg = _prompt_cfg(K, name)
+    img = K.synth_image(cfg)
+    P = 600 if name == "long_llama3" else min(37, cfg.seq_len - 12)
+    toks = [int(t) for t in K.prompt_tokens(cfg, P)]
+    a = O.Model(img, cfg.family, cfg.quant)
+    b = O.Model(img, cfg.family, cfg.quant)
+    for pos, t in enumerate(toks):
+        ref = a.step(t, pos)
+    got = b.prompt(toks)
+    assert np.array_equal(got, ref), name
+    # a continuation from a filled cache: 5 more positions as one batch
+    more = [int(t) for t in K.prompt_tokens(cfg, P + 5)[P:]]
+    for i, t in enumerate(more):
+        ref = a.step(t, P + i)
+    assert np.array_equal(b.prompt(more, P), ref), name
+    for layer in range(cfg.layers):
+        for pos in range(P + 5):
+            for v in (False, True):
+                assert np.array_equal(a.kv_row(layer, pos, v), b.kv_row(layer, pos, v)), (layer, pos, v)
+    if name != "long_llama3":
+        prompt = toks[:9]
+        gen = O.Model(img, cfg.family, cfg.quant).generate(prompt, 6)
+        m = O.Model(img, cfg.family, cfg.quant)
+        seq = list(prompt)
+        for pos in range(len(prompt) + 6 - 1):
+            lg = m.step(seq[pos], pos)
+            if pos >= len(prompt) - 1:
+                seq.append(O.argmax(lg))
+        assert list(gen) == seq[len(prompt):]
+
+
+def test_model_prompt_rejects_bad_input(K, O):
+    cfg = K.TINY["tiny_llama2"]
+    m = O.Model(K.synth_image(cfg), cfg.family, cfg.quant)
+    with pytest.raises(ValueError):
+        m.prompt([1, cfg.vocab])
+    with pytest.raises(ValueError):
+        m.prompt([1, 2], cfg.seq_len - 1)

@@ -139,6 +139,19 @@ def test_bad_files_are_reported(tmp_path):
     p = subprocess.run([BIN, "tok", "qwen", str(nobytes), str(cases)], capture_output=True, text=True,
                        timeout=60)
     assert p.returncode == 1 and "meta init 3" in p.stdout and "byte-level" in p.stdout, p.stdout
+    # an added token with empty content (it would match at every position, and
+    # an encoder that took it would never advance): refused at init, no hang
+    with open(os.path.join(TOK, FILES["qwen"]), encoding="utf-8") as f:
+        src = json.load(f)
+    src["added_tokens"].append({"id": len(src["model"]["vocab"]) + len(src["added_tokens"]),
+                                "content": "", "special": True})
+    empty = tmp_path / "empty_added.json"
+    empty.write_text(json.dumps(src))
+    cases.write_text("hello world\n")
+    for kind in ("bpe", "qwen"):
+        p = subprocess.run([BIN, "tok", kind, str(empty), str(cases)], capture_output=True, text=True,
+                           timeout=60)
+        assert p.returncode == 1 and "meta init 3" in p.stdout and "empty content" in p.stdout, p.stdout
 
 
 # ----------------------------------------------- pinning the BPE oracle ----
