@@ -5,29 +5,47 @@
 // K-contiguous.  The reference has no batched path (MatmulLayer takes a 1-D
 // input, op/matmul.cpp:20; the prompt runs token by token, demo/main.cpp:20-22).
 //
-// Tiling: a workgroup of WM x WN waves computes a (WM*TM*32) x (WN*TN*32) tile
-// of C; each wave owns TM x TN blocks of 32 x 32 accumulated with
-// v_mfma_f32_32x32x2f32 (A operand: lane l holds A[l % 32][k], B operand:
-// W[l % 32][k], result register r of lane l is C[8 (r / 4) + 4 (l / 32) +
-// r % 4][l % 32]).  K advances in blocks of 32 staged in LDS (double
-// buffered, one barrier per block, the next block's global loads in flight
-// during the current block's 16 MFMAs).  Inside a block the 32 k indices are
-// visited in the order that lets each lane fetch its 16 operands of a block
-// with four ds_read_b128: MFMA step s uses, in lane l, column 16 (l / 32) + s.
-// The same permutation applies to both operands, so every product
-// A[m][k] W[n][k] is formed exactly once.  (Measured at the Qwen3-4B prefill
-// shapes, M = 512: blocks of 32 are 3-7% faster than 16; 64 x 64 tiles of four
-// waves beat 128 x 64, 64 x 128 and 128 x 128 tiles, which leave too few
-// workgroups; two accumulators per wave or loads two blocks ahead change
-// nothing.)
+// Two kernels share the launch arguments (GemmArgs, gemm_run.hpp) and the
+// 64 x 64 workgroup tile of four waves:
+//
+// k_gemm_f32_dma (fp32 weights, K a multiple of 32; every model projection):
+// each wave owns 2 x 2 blocks of 16 x 16 accumulated with
+// v_mfma_f32_16x16x4f32 (A operand: lane l holds A[l % 16][k], B operand
+// W[l % 16][k], k = l / 16; result register r of lane l is
+// C[4 (l / 16) + r][l % 16]).  K advances in blocks of 32 columns staged in
+// LDS by direct-to-LDS loads (global_load_lds_dwordx4: no VGPR staging, no LDS
+// store instructions) through a 3-stage ring, block k + 2 requested while
+// block k is computed, one barrier per block.  A 1 KB load instruction of a
+// wave fills 8 rows of 128 B; chunk q (16 B) of row r sits in slot
+// q ^ (r & 7), which each lane gets by loading the chunk that belongs in its
+// slot, so the operand reads are conflict-free without padding.  Lane group
+// g = l / 16 takes k columns 8 g .. 8 g + 7 of a block (two contiguous 16 B
+// reads per row; A and W use the same permutation, so every product
+// A[m][k] W[n][k] is formed exactly once).  The next block's operands are read
+// into the other register buffer right after the barrier, while the current
+// block's last two k steps run; the loop is unrolled by two so the buffers
+// alternate without copies.  Measured on the Qwen3-4B prefill shapes (M = 512,
+// one box): 107-121 TFLOP/s against 87-107 for k_gemm_f32 below; 2 x 2 waves of
+// 32 x 32 with 16 x 16 blocks beat 32 x 32 blocks (v_mfma_f32_32x32x2f32),
+// larger tiles (fewer workgroups at M = 512), a K depth of 64 (one workgroup
+// per CU) and a hand-pinned schedule.
+//
+// k_gemm_f32 (int8 weights, and K not a multiple of 32): each wave owns one
+// 32 x 32 block of v_mfma_f32_32x32x2f32 (A operand: lane l holds A[l % 32][k],
+// B operand W[l % 32][k], result register r of lane l is C[8 (r / 4) +
+// 4 (l / 32) + r % 4][l % 32]); K in blocks of 32 through double-buffered,
+// padded LDS stored from registers (the next block's global loads in flight
+// during the current block's 16 MFMAs); MFMA step s uses, in lane l, column
+// 16 (l / 32) + s, so each lane fetches its 16 operands of a block with four
+// ds_read_b128.
 //
 // Grouped launches compute up to three outputs over the same A (the Q, K and V
 // projections) in one grid, and split-K divides the K blocks among
 // blockIdx.y with a fixed-order reduction, so that narrow outputs (few tiles)
-// still fill the chip.
+// still fill the chip.  Tiles along M are adjacent in launch order.
 //
-// int8 weights (Q8): W holds int8 [N x ldw] with one fp32 scale per 2^gshift
-// consecutive elements of the flattened matrix (the image's group-wise
+// int8 weights (Q8, k_gemm_f32): W holds int8 [N x ldw] with one fp32 scale per
+// 2^gshift consecutive elements of the flattened matrix (the image's group-wise
 // layout, export_llama.py:49-73).  Each thread loads the 4 bytes that stand in
 // for one float4 of the fp32 path and its group's scale, and stores
 // float(q) * scale to LDS (the dequantised weight of the reference's int8
@@ -223,6 +241,168 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * TM * 32 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int n = n0 + wn * TN * 32 + b * 32 + (lane & 31);
+        if (m < M && n < N) {
+          float v = acc[a][b][r];
+          if (wsp) {
+            wsp[static_cast<size_t>(m) * N + n] = v;
+          } else {
+            if (bias) v += bias[n];
+            float* cp = C + static_cast<size_t>(m) * ldc + n;
+            if (g.accumulate) v = *cp + v;
+            *cp = v;
+          }
+        }
+      }
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+constexpr int kDmaStages = 3;
+
+__global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
+  constexpr int BM = 64, BN = 64, BK = 32;
+  constexpr int SA = BM * BK, SW = BN * BK;   // floats per stage and operand
+  constexpr int LI = BM / 8 / 4;              // 1 KB load instructions per wave and operand
+  __shared__ __align__(1024) float L[kDmaStages * (SA + SW)];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  int sidx = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i < g.nseg && static_cast<int>(blockIdx.x) >= g.seg[i].tile0) sidx = i;
+  const float* __restrict__ A = g.A;
+  const void* W = g.seg[0].W;
+  float* C = g.seg[0].C;
+  const float* bias = g.seg[0].bias;
+  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i == sidx) {
+      W = g.seg[i].W;
+      C = g.seg[i].C;
+      bias = g.seg[i].bias;
+      N = g.seg[i].N;
+      ldw = g.seg[i].ldw;
+      ldc = g.seg[i].ldc;
+      tile0 = g.seg[i].tile0;
+    }
+  const int M = g.M, K = g.K, lda = g.lda;
+  const int local = static_cast<int>(blockIdx.x) - tile0;
+  const int tm = local % g.tiles_m, tn = local / g.tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nkt = K / BK;
+  const int kb0 = static_cast<int>(blockIdx.y) * nkt / g.splits;
+  const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
+
+  // Load instruction i of this wave fills tile rows 8 j .. 8 j + 7
+  // (j = LI * wave + i); lane l writes slot l % 8 of row 8 j + l / 8, which
+  // holds chunk (l % 8) ^ (l / 8).  Rows past M or N read the last row (they
+  // only feed outputs that are never stored).
+  const int rsub = lane >> 3, chunk = (lane & 7) ^ rsub;
+  unsigned int ga[LI], gw[LI];
+#pragma unroll
+  for (int i = 0; i < LI; ++i) {
+    const int r = 8 * (LI * wave + i) + rsub;
+    ga[i] = static_cast<unsigned int>((min(m0 + r, M - 1) * lda + 4 * chunk) * 4);
+    gw[i] = static_cast<unsigned int>((min(n0 + r, N - 1) * ldw + 4 * chunk) * 4);
+  }
+  auto request = [&](int kb, int st) {
+    const char* ba = reinterpret_cast<const char*>(A) + static_cast<size_t>(kb) * BK * 4;
+    const char* bw = reinterpret_cast<const char*>(W) + static_cast<size_t>(kb) * BK * 4;
+    float* la = L + st * (SA + SW);
+    float* lw = la + SA;
+#pragma unroll
+    for (int i = 0; i < LI; ++i)
+      __builtin_amdgcn_global_load_lds((global_void_t*)(ba + ga[i]),
+                                       (lds_void_t*)(la + 256 * (LI * wave + i)), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LI; ++i)
+      __builtin_amdgcn_global_load_lds((global_void_t*)(bw + gw[i]),
+                                       (lds_void_t*)(lw + 256 * (LI * wave + i)), 16, 0, 0);
+  };
+  // Operands: lane group g4 = l / 16 reads chunks 2 g4 and 2 g4 + 1 of rows
+  // 32 wm + 16 a + l % 16 (A) and 32 wn + 16 b + l % 16 (W).
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int rowa = 32 * wm + r16, rowb = 32 * wn + r16;
+  int oa[2], ob[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    oa[j] = rowa * BK + 4 * ((2 * g4 + j) ^ (rowa & 7));
+    ob[j] = rowb * BK + 4 * ((2 * g4 + j) ^ (rowb & 7));
+  }
+  gf4 af[2][2][2], bf[2][2][2];  // [register buffer][block][16-byte read]
+  auto operands = [&](int st, int p) {
+    const float* la = L + st * (SA + SW);
+    const float* lw = la + SA;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) af[p][a][j] = *reinterpret_cast<const gf4*>(la + a * 16 * BK + oa[j]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[p][b][j] = *reinterpret_cast<const gf4*>(lw + b * 16 * BK + ob[j]);
+  };
+  gf4 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = gf4{0.f, 0.f, 0.f, 0.f};
+  auto steps = [&](int p, int s0, int s1) {
+#pragma unroll
+    for (int s = s0; s < s1; ++s)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[p][a][s >> 2][s & 3], bf[p][b][s >> 2][s & 3],
+                                                           acc[a][b], 0, 0, 0);
+  };
+  constexpr int kLoads = 2 * LI;  // load instructions per block and wave
+  if (kb0 < kb1) {
+    // Blocks kb0 and kb0 + 1 in flight, block kb0 landed in every wave.
+    request(kb0, 0);
+    request(min(kb0 + 1, kb1 - 1), 1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+    __builtin_amdgcn_s_barrier();
+    operands(0, 0);
+    int st = 0;
+    // Block kt with its operands in register buffer p: request block kt + 2
+    // into the stage block kt - 1 used, run 6 of the 8 k steps, wait until
+    // block kt + 1 has landed (only the newest request may be outstanding)
+    // and every wave is done reading, then read block kt + 1's operands into
+    // buffer p ^ 1 while the last 2 steps run.  The last blocks request
+    // themselves again (a stage nobody reads afterwards).
+    auto block = [&](int kt, int p) {
+      const int sn = st == 0 ? 2 : st - 1;
+      const int st1 = st == 2 ? 0 : st + 1;
+      request(min(kt + 2, kb1 - 1), sn);
+      steps(p, 0, 6);
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(kLoads) : "memory");
+      __builtin_amdgcn_s_barrier();
+      operands(st1, p ^ 1);
+      steps(p, 6, 8);
+      st = st1;
+    };
+    int kt = kb0;
+    for (; kt + 1 < kb1; kt += 2) {
+      block(kt, 0);
+      block(kt + 1, 1);
+    }
+    if (kt < kb1) block(kt, 0);
+  }
+
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * M * N : nullptr;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 32 * wm + 16 * a + 4 * g4 + r;
+        const int n = n0 + 32 * wn + 16 * b + r16;
         if (m < M && n < N) {
           float v = acc[a][b][r];
           if (wsp) {

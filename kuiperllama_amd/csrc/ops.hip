@@ -806,7 +806,7 @@ int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ld
 }  // extern "C"
 
 namespace {
-constexpr int kGemmTile = 64;  // workgroup tile (2 x 2 waves of 32 x 32)
+constexpr int kGemmTile = 64;  // workgroup tile of both GEMM kernels (2 x 2 waves of 32 x 32)
 
 bool gemm_shape_ok(const float* A, int M, int K, int lda) {
   return A && M > 0 && K > 0 && lda >= K;
@@ -860,9 +860,14 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
     tiles += static_cast<long long>(g.tiles_m) * ((sg.N + kGemmTile - 1) / kGemmTile);
   }
   if (tiles > INT_MAX) return KL_EUNSUPP;
+  // fp32 weights with K a whole number of 32-column blocks (every model
+  // projection) stream through the direct-to-LDS kernel; int8 weights and
+  // other K through the register-staged one.
   if (q8)
     hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1, true>), dim3(static_cast<unsigned>(tiles), splits),
                        dim3(256), 0, st, g);
+  else if (K % kGemmBK == 0)
+    hipLaunchKernelGGL(k_gemm_f32_dma, dim3(static_cast<unsigned>(tiles), splits), dim3(256), 0, st, g);
   else
     hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(static_cast<unsigned>(tiles), splits), dim3(256),
                        0, st, g);

@@ -129,6 +129,30 @@ def test_gemm_splitk_vs_oracle(K, O, gpu, splits):
                                         splits, ws.ptr, ws.nbytes - 4, None) == -6
 
 
+@pytest.mark.parametrize("M,N,Kd,splits", [(1, 1, 32, 1), (3, 65, 64, 1), (65, 1, 96, 1), (64, 64, 32, 1),
+                                            (70, 130, 160, 1), (5, 200, 32, 4), (129, 96, 96, 2),
+                                            (200, 70, 2560, 3)])
+def test_gemm_k32_blocks_vs_oracle(K, O, gpu, M, N, Kd, splits):
+    """K a whole number of 32-column blocks (the direct-to-LDS kernel): one
+    block, odd and even block counts (the loop runs blocks in pairs), single
+    rows and columns (edge tiles clamp their loads), and more splits than
+    blocks (empty splits contribute zeros); accumulate into C with a bias."""
+    rng = np.random.default_rng(M * 131 + N * 7 + Kd + splits)
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    W = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    dA, dW, dC, db = D(K, A), D(K, W), D(K, C0), D(K, b)
+    ws = K.DeviceArray(max(1, splits * M * N))
+    ok(K.lib.kl_gemm_f32_splitk(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, Kd, Kd, N, db.ptr, 1, splits,
+                                ws.ptr, ws.nbytes, None), "splitk")
+    y = dC.numpy().reshape(M, N)
+    for m in range(M):
+        want = C0[m].astype(np.float64) + O.gemv_f32(A[m], W) + b
+        tol = 4e-7 * np.sqrt(Kd) * (np.abs(W) @ np.abs(A[m])).max() + 1e-6
+        assert np.max(np.abs(y[m] - want)) <= tol, (m, np.max(np.abs(y[m] - want)))
+
+
 def test_gemm_rejects_unaligned_k(K, gpu):
     buf = K.DeviceArray(64)
     assert K.lib.kl_gemm_f32(buf.ptr, buf.ptr, buf.ptr, 2, 2, 3, 3, 3, 2, None, 0, None) == -4
