@@ -23,6 +23,10 @@ on both sides.  Prints one JSON line.
                  tokens) on the matrix cores: prompt tok/s, TFLOP/s against the
                  fp32 MFMA peak, and the MFMA-busy fraction rocprofv3 measured
                  for the same command (profiles/prefill_qwen3_4b_pmc.txt)
+  configs        the other four BASELINE configs, each a short decode leg of
+                 its own workload (prompt via the batched prefill, then
+                 --config-steps timed steps): tok/s, ms per step, GB/s and the
+                 fraction of 8 TB/s, plus the prompt's prefill time
   hbm_measured   this box's HBM read and copy rates (kl_hbm_probe, outside the
                  timed region) and the decode rate as a fraction of the read rate
   cpu_baseline   the CPU oracle (a restatement of the reference CPU path,
@@ -104,12 +108,12 @@ def measured_mfma_busy(config: str):
     return None
 
 
-def measure_prefill(K, cfg, reps: int = 3) -> dict:
+def measure_prefill(K, cfg, eng=None, reps: int = 3) -> dict:
     """Batched prefill of the config's prompt (kl_engine_prefill), device time
     from HIP events inside the call; best of `reps` after one warm-up.  The
     roofline is the fp32 matrix-core peak."""
-    img = K.synth_image(cfg)
-    eng = K.Engine(img, cfg)
+    if eng is None:
+        eng = K.Engine(K.synth_image(cfg), cfg)
     prompt = K.prompt_tokens(cfg)
     P = len(prompt)
     eng.prefill(prompt, want_logits=False)
@@ -121,7 +125,44 @@ def measure_prefill(K, cfg, reps: int = 3) -> dict:
             "tok_s": round(P / (ms / 1e3), 1), "tflops": round(tf, 2),
             "bound": "mfma", "peak_tflops": MFMA_FP32_PEAK_TFLOPS,
             "frac": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "flops": int(fl),
-            "dtype": "f32", "mfma_busy": measured_mfma_busy(cfg.name)}
+            "dtype": "int8w-f32" if cfg.quant else "f32", "mfma_busy": measured_mfma_busy(cfg.name)}
+
+
+# The other BASELINE configs, each timed as a short decode leg of its own
+# workload (bench lines are cfg 2's; these ride along in "configs").
+OTHER_CONFIGS = ("llama2_110m", "llama2_7b_q8", "qwen25_15b", "qwen3_4b")
+
+
+def decode_leg(K, cfg, steps: int, warmup: int, prefill_reps: int) -> dict:
+    """One config's workload: its prompt through the batched prefill (cfg 4:
+    the 4000-position cache fill), `warmup` untimed decode steps (the first
+    sampled by the prefill), then `steps` decode steps timed with HIP events
+    on the engine's stream; then the prefill alone, best of `prefill_reps`."""
+    t0 = time.time()
+    img = K.synth_image(cfg)
+    eng = K.Engine(img, cfg)
+    t_setup = time.time() - t0
+    eng.set_prefill(True)
+    prompt = K.prompt_tokens(cfg)
+    P = len(prompt)
+    warmup = max(1, min(warmup, cfg.seq_len - P - steps + 1))
+    toks, ms = eng.bench(prompt, warmup, steps)
+    first_pos = P - 1 + warmup
+    b = cfg.decode_bytes(first_pos, steps)
+    gbps = b / (ms / 1e3) / 1e9
+    out = {"config": cfg.name,
+           "workload": f"{P}-token prompt (batched prefill), then {steps} timed greedy decode steps "
+                       f"at positions {first_pos}..{first_pos + steps - 1}",
+           "dtype": "int8w-f32" if cfg.quant else "f32",
+           "tok_s": round(steps / (ms / 1e3), 2), "ms_per_step": round(ms / steps, 5),
+           "achieved_GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+           "bytes_per_token": int(b / steps), "mode": "persistent" if eng.mode == K.MODE_PERSISTENT
+           else "multi"}
+    if prefill_reps > 0:
+        out["prefill"] = measure_prefill(K, cfg, eng, prefill_reps)
+    print(f"# leg {cfg.name}: setup {t_setup:.1f} s; {out}", file=sys.stderr, flush=True)
+    del eng, img
+    return out
 
 
 def host_cpu() -> dict:
@@ -232,6 +273,11 @@ def main() -> int:
     ap.add_argument("--prefill-config", default="qwen3_4b",
                     help="also time the batched prefill of this config's prompt (default "
                          "qwen3_4b: 512 tokens) and report it under 'prefill'; 'none' skips it")
+    ap.add_argument("--configs", default=",".join(OTHER_CONFIGS),
+                    help="comma-separated configs timed as short decode legs of their own "
+                         "workloads under 'configs' (prompt via the batched prefill); 'none' skips")
+    ap.add_argument("--config-steps", type=int, default=32, help="timed decode steps per config leg")
+    ap.add_argument("--config-warmup", type=int, default=8, help="untimed decode steps per config leg")
     ap.add_argument("--skip-decode", action="store_true",
                     help="run only the prefill leg (for profiling it); prints no bench line")
     ap.add_argument("--pmc-calibration", action="store_true",
@@ -339,10 +385,20 @@ def main() -> int:
                         "device-to-device copy (read + written bytes)"}
         print(f"# hbm probe {hbm}", file=sys.stderr, flush=True)
 
+    del eng
+    legs = {}
     prefill = None
-    if args.prefill_config != "none":
-        del eng
+    names = [] if args.configs == "none" else [c for c in args.configs.split(",") if c]
+    for name in names:
+        if name == cfg.name:
+            continue
+        reps = 3 if name == args.prefill_config else 1
+        legs[name] = decode_leg(K, K.BASELINE[name], args.config_steps, args.config_warmup, reps)
+        if name == args.prefill_config:
+            prefill = legs[name]["prefill"]
+    if args.prefill_config != "none" and prefill is None:
         prefill = measure_prefill(K, K.BASELINE[args.prefill_config])
+    if prefill is not None:
         print(f"# prefill {prefill}", file=sys.stderr, flush=True)
 
     cpu = None
@@ -410,6 +466,8 @@ def main() -> int:
         out["hbm_measured"] = hbm
     if prefill is not None:
         out["prefill"] = prefill
+    if legs:
+        out["configs"] = legs
     print(json.dumps(out), flush=True)
     return 0
 
