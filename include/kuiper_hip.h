@@ -227,6 +227,20 @@ int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream);
 /* AddKernel (KI:6-7; cpu/add_kernel.cpp:5-19): out = a + b. */
 int kl_add(const float* a, const float* b, float* out, int n, void* stream);
 
+/* ScaleKernel (KI:41; cpu/scale_kernel.cpp:3-9): x = x * scale in place. */
+int kl_scale(float scale, float* x, int n, void* stream);
+
+/* SoftmaxInplaceKernel (KI:43; cpu/softmax_kernel.cpp:4-16): x = exp(x - max x)
+ * / sum, in place over one vector of n floats (one workgroup). */
+int kl_softmax(float* x, int n, void* stream);
+
+/* ScaleSumKernel (KI:45-47; cpu/scale_sum_kernel.cpp:5-22): for d < size,
+ * out[d] += scale[i] * value[i * stride + d] for i = 0 .. pos, in increasing i,
+ * each product and each sum rounded to fp32 (bit-exact with the CPU path).
+ * The rows of value may not overlap (stride >= size when pos > 0). */
+int kl_scale_sum(const float* value, const float* scale, float* out, int pos, int size, int stride,
+                 void* stream);
+
 /* EmbeddingKernel (KI:16-17; cpu/emb_kernel.cpp:4-29, cuda/emb_kernel.cu:23-48):
  * out[i, :] = table[tokens[i], :] for i < n_tokens (no 512-token cap).
  * tokens is a DEVICE int32 array; ids outside [0, vocab) leave their row

@@ -106,6 +106,9 @@ _SIGS = {
                                 _p]),
     "kl_swiglu": (_i, [_p, _p, _p, _i, _p]),
     "kl_add": (_i, [_p, _p, _p, _i, _p]),
+    "kl_scale": (_i, [C.c_float, _p, _i, _p]),
+    "kl_softmax": (_i, [_p, _i, _p]),
+    "kl_scale_sum": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "kl_embedding": (_i, [_p, _i, _p, _i, _i, _p, _p, _p]),
     "kl_argmax_workspace_size": (_i, [_i, C.POINTER(_sz)]),
     "kl_argmax": (_i, [_p, _i, _p, _p, _sz, _p]),

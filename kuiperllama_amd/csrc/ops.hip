@@ -333,6 +333,57 @@ __global__ void k_add(const float* __restrict__ a, const float* __restrict__ b, 
     out[i] = a[i] + b[i];
 }
 
+// ScaleKernel (cpu/scale_kernel.cpp:3-9): x = x * scale, one rounding.
+__global__ void k_scale(float scale, float* x, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    x[i] = x[i] * scale;
+}
+
+// SoftmaxInplaceKernel (cpu/softmax_kernel.cpp:4-16) over one vector, one
+// workgroup: the maximum (exact in any order), x = exp(x - max), their sum
+// (in this workgroup's fixed tree order), x = x / sum.
+__global__ __launch_bounds__(1024) void k_softmax_1(float* x, int n) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  float m = -INFINITY;
+  for (int i = tid; i < n; i += blockDim.x) m = fmaxf(m, x[i]);
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = red[0];
+  for (int w = 1; w < nw; ++w) m = fmaxf(m, red[w]);
+  __syncthreads();
+  float s = 0.f;
+  for (int i = tid; i < n; i += blockDim.x) {
+    const float e = expf(x[i] - m);
+    x[i] = e;
+    s += e;
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  s = red[0];
+  for (int w = 1; w < nw; ++w) s += red[w];
+  for (int i = tid; i < n; i += blockDim.x) x[i] = x[i] / s;
+}
+
+// ScaleSumKernel (cpu/scale_sum_kernel.cpp:5-22): out[d] += scale[i] * value[i
+// * stride + d] for i = 0 .. pos in increasing i, the product and the sum each
+// rounded (contraction into a fused multiply-add is off here), as the
+// reference's vector expression does.
+__global__ void k_scale_sum(const float* __restrict__ value, const float* __restrict__ scale,
+                            float* out, int pos, int size, int stride) {
+#pragma clang fp contract(off)
+  for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < size; d += gridDim.x * blockDim.x) {
+    float acc = out[d];
+    for (int i = 0; i <= pos; ++i) {
+      const float p = scale[i] * value[static_cast<size_t>(i) * stride + d];
+      acc = acc + p;
+    }
+    out[d] = acc;
+  }
+}
+
 // One workgroup per token row.
 __global__ __launch_bounds__(256) void k_embedding(const int32_t* __restrict__ tokens,
                                                   const float* __restrict__ table, int vocab,
@@ -1069,6 +1120,28 @@ int kl_add(const float* a, const float* b, float* out, int n, void* stream) {
   if (!a || !b || !out || n <= 0) return KL_EINVAL;
   hipLaunchKernelGGL(k_add, dim3(std::min((n + 255) / 256, 4096)), dim3(256), 0, as_stream(stream),
                      a, b, out, n);
+  return launch_rc();
+}
+
+int kl_scale(float scale, float* x, int n, void* stream) {
+  if (!x || n <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_scale, dim3(std::min((n + 255) / 256, 4096)), dim3(256), 0, as_stream(stream),
+                     scale, x, n);
+  return launch_rc();
+}
+
+int kl_softmax(float* x, int n, void* stream) {
+  if (!x || n <= 0) return KL_EINVAL;
+  hipLaunchKernelGGL(k_softmax_1, dim3(1), dim3(1024), 0, as_stream(stream), x, n);
+  return launch_rc();
+}
+
+int kl_scale_sum(const float* value, const float* scale, float* out, int pos, int size, int stride,
+                 void* stream) {
+  if (!value || !scale || !out || pos < 0 || size <= 0 || stride < 0) return KL_EINVAL;
+  if (pos > 0 && stride < size) return KL_EINVAL;  // rows may not overlap
+  hipLaunchKernelGGL(k_scale_sum, dim3(std::min((size + 255) / 256, 4096)), dim3(256), 0,
+                     as_stream(stream), value, scale, out, pos, size, stride);
   return launch_rc();
 }
 

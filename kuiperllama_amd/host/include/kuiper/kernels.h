@@ -1,9 +1,9 @@
 // Kernel dispatch of the host API: the reference's function-pointer typedefs
-// (source/op/kernels/kernels_interface.h:6-47) and get_*_kernel(DeviceType)
-// factories (kernels_interfaces.cpp:21-141).  For kDeviceHIP each factory
-// returns an adapter that unpacks the Tensors into a call of the C ABI
-// (include/kuiper_hip.h); the reference's own CPU/CUDA kernels are not part of
-// this backend, so other device types return nullptr.
+// (source/op/kernels/kernels_interface.h:6-49) and get_*_kernel(DeviceType)
+// factories (kernels_interface.h:51-75, kernels_interfaces.cpp:21-141).  For
+// kDeviceHIP each factory returns an adapter that unpacks the Tensors into a
+// call of the C ABI (include/kuiper_hip.h); the reference's own CPU/CUDA
+// kernels are not part of this backend, so other device types return nullptr.
 #pragma once
 #include "kuiper/hip_config.h"
 #include "kuiper/tensor.h"
@@ -36,6 +36,17 @@ typedef void (*RoPEKernel)(int32_t dim, int32_t kv_dim, int32_t head_size,
                            const tensor::Tensor& input_q, const tensor::Tensor& input_k,
                            const tensor::Tensor& input_pos, const tensor::Tensor& sin_cache,
                            const tensor::Tensor& cos_cache, void* stream);
+// The CPU MHA's building blocks (kernels_interface.h:41-49): in-place scale,
+// in-place softmax of a whole tensor, and output += sum_i scale[i] * value_i
+// over rows i = 0 .. t of `size` floats at a stride.
+typedef void (*ScaleKernel)(float scale, const tensor::Tensor& input, void* stream);
+typedef void (*SoftmaxInplaceKernel)(const tensor::Tensor& input, void* stream);
+typedef void (*ScaleSumKernel)(const tensor::Tensor& value, const tensor::Tensor& scale,
+                               const tensor::Tensor& output, int t, int size, int stride,
+                               void* stream);
+
+// Softmax in place over `size` floats in host memory (kernels_interface.h:49).
+void softmax_inplace_cpu(const float* input_ptr, size_t size);
 
 // What the reference fixes with -DLLAMA3_SUPPORT / -DQWEN2_SUPPORT /
 // -DQWEN3_SUPPORT (RoPE pairing and theta, RMSNorm eps; see
@@ -59,6 +70,9 @@ RMSNormKernel get_rmsnorm_kernel(base::DeviceType device_type);
 RMSNormKernelDim get_rmsnorm_dim_kernel(base::DeviceType device_type);
 RoPEKernel get_rope_kernel(base::DeviceType device_type);
 SwigluKernel get_swiglu_kernel(base::DeviceType device_type, void* stream = nullptr);
+ScaleKernel get_scale_kernel(base::DeviceType device_type);
+SoftmaxInplaceKernel get_softmax_kernel(base::DeviceType device_type);
+ScaleSumKernel get_scale_sum_kernel(base::DeviceType device_type);
 
 // sin_cos_cache_calc (kernels/cpu/rope_kernel.cpp:4-16): fills the device
 // tables [seq_len x head_size] with the reference's float formula.

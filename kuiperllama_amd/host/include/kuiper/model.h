@@ -98,6 +98,10 @@ struct OpProfileStat {
   double avg_ms = 0.0;
 };
 
+// The model interface (include/model/model.h:14-94): init, predict, forward,
+// embedding, post_processing and the layer/buffer factories are pure virtual,
+// implemented by each family's class; the file reading, buffers, tokenizer
+// and the fused engine are shared.
 class Model {
  public:
   explicit Model(base::TokenizerType tokenizer_type, base::ModelType model_type,
@@ -105,43 +109,45 @@ class Model {
                  ModelFamily family);
   virtual ~Model();
 
-  base::Status init(base::DeviceType device_type);
+  virtual base::Status init(base::DeviceType device_type) = 0;
   // One token: forward() then, unless is_prompt, greedy sampling into next
   // (-1 for prompt positions), as llama3.cpp:641-649.
-  base::Status predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
-                       bool is_prompt, int& next) const;
-  base::Status forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
-                       int& next) const;
+  virtual base::Status predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                               bool is_prompt, int& next) const = 0;
+  virtual base::Status forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                               int& next) const = 0;
 
   base::ModelType model_type() const { return model_type_; }
   ModelFamily family() const { return family_; }
   const std::string& token_path() const { return token_path_; }
   const std::string& model_path() const { return model_path_; }
   const TransformerConfig& config() const { return *config_; }
-  tensor::Tensor& get_buffer(ModelBufferType buffer_idx);
-  const tensor::Tensor& get_buffer(ModelBufferType buffer_idx) const;
+  virtual tensor::Tensor& get_buffer(ModelBufferType buffer_idx);
+  virtual const tensor::Tensor& get_buffer(ModelBufferType buffer_idx) const;
 
-  bool is_sentence_ending(int32_t token_idx) const;
-  std::string decode(int32_t token_idx) const;
-  std::string decode(std::vector<int32_t> token_idxs) const;
-  std::vector<int32_t> encode(const std::string& sentence) const;
+  virtual bool is_sentence_ending(int32_t token_idx) const;
+  virtual std::string decode(int32_t token_idx) const;
+  virtual std::string decode(std::vector<int32_t> token_idxs) const;
+  virtual std::vector<int32_t> encode(const std::string& sentence) const;
 
   // K and V cache rows of (layer, position) as device tensors [kv_dim].
-  std::pair<tensor::Tensor, tensor::Tensor> slice_kv_cache(int32_t layer_idx,
-                                                           int32_t token_pos) const;
+  virtual std::pair<tensor::Tensor, tensor::Tensor> slice_kv_cache(int32_t layer_idx,
+                                                                   int32_t token_pos) const;
   // Embeds tokens (all at once) into kInputEmbeddings.
-  op::EmbeddingOutput embedding(const std::vector<int>& tokens) const;
+  virtual op::EmbeddingOutput embedding(const std::vector<int>& tokens) const = 0;
   // The residual-stream input of a step: row pos of the prompt embeddings
   // (is_prompt) or row 0 (the single decoded token), as model.cpp:240-265.
-  tensor::Tensor fill_input(const tensor::Tensor& pos_tensor,
-                            const op::EmbeddingOutput& embedding_output, bool is_prompt) const;
+  virtual tensor::Tensor fill_input(const tensor::Tensor& pos_tensor,
+                                    const op::EmbeddingOutput& embedding_output,
+                                    bool is_prompt) const;
 
   // Fused decode engine (one persistent launch per token); predict() uses it
   // when enabled.  The engine is created on first use from the mapped file.
   base::Status set_fused(bool enable);
   bool is_fused() const { return fused_; }
   // The greedy loop of demo/main.cpp:5-47: P prompt tokens, then n_new
-  // sampled tokens written to out (fused: entirely on the device).
+  // sampled tokens written to out (fused: entirely on the device; layered:
+  // through the virtual embedding(), fill_input() and predict()).
   base::Status generate(const std::vector<int32_t>& prompt, int32_t n_new,
                         std::vector<int32_t>& out) const;
   // Fused only: the whole prompt in one batched pass (kl_engine_prefill);
@@ -165,21 +171,19 @@ class Model {
   std::vector<OpProfileStat> get_profile_stats() const;
 
  protected:
-  base::Status insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor);
-  base::Status create_encode_layer();
-  base::Status read_model_file();
-  base::Status generate_model_infos(const ModelConfig& config, int32_t extra);
-  base::Status create_layers();
-  void create_param_layers();
-  void create_param_quant_layers();
-  void create_nonparam_layers();
-  void init_mem();
-  void attention_rms(int32_t layer_idx, const tensor::Tensor& input) const;
-  void attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const;
-  void attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const;
-  void feed_forward(int32_t layer_idx, const tensor::Tensor& input) const;
-  void cls_logits(const tensor::Tensor& input) const;
-  int32_t post_processing(const tensor::Tensor& pos, bool is_prompt) const;
+  virtual base::Status insert_buffer(ModelBufferType buffer_idx, const tensor::Tensor& tensor);
+  virtual base::Status read_model_file();
+  virtual base::Status create_encode_layer();
+  // model.cpp:113-141: the header's sizes into config_; `extra` is the
+  // eighth header int of layouts that have one (int8: the group size, read
+  // before this call; Qwen3: the FFN width).
+  virtual base::Status generate_model_infos(const ModelConfig& config, int32_t extra);
+  virtual int32_t post_processing(const tensor::Tensor& pos, bool is_prompt) const = 0;
+  virtual void init_mem() = 0;
+  virtual base::Status create_layers() = 0;
+  virtual void create_param_layers() = 0;
+  virtual void create_nonparam_layers() = 0;
+  virtual void create_param_quant_layers() = 0;
   // Runs fn, bracketed by profile events on `stream` (default: the model's)
   // when profiling is on.
   template <class Fn>
@@ -217,30 +221,68 @@ class Model {
   mutable std::vector<void*> profile_all_events_;
 };
 
-// Llama2 (default) and Llama3 (family kLlama3) checkpoints.
+// Llama2 (default) and Llama3 (family kLlama3) checkpoints: the decoder of
+// include/model/llama3.h:33-74 (llama3.cpp), layer by layer on the HIP
+// kernels.  Its step stages are virtual so a family can change one.
 class LLama2Model : public Model {
  public:
   explicit LLama2Model(base::TokenizerType tokenizer_type, std::string token_path,
                        std::string model_path, bool is_quant_model,
-                       ModelFamily family = ModelFamily::kLlama2)
-      : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
-              std::move(model_path), is_quant_model, family) {}
+                       ModelFamily family = ModelFamily::kLlama2);
+
+  base::Status init(base::DeviceType device_type) override;
+  base::Status predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                       bool is_prompt, int& next) const override;
+  base::Status forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                       int& next) const override;
+  op::EmbeddingOutput embedding(const std::vector<int>& tokens) const override;
+
+ protected:
+  int32_t post_processing(const tensor::Tensor& pos, bool is_prompt) const override;
+  void init_mem() override;
+  base::Status create_layers() override;
+  void create_param_layers() override;
+  void create_nonparam_layers() override;
+  void create_param_quant_layers() override;
+  // The fp32 walk of llama3.cpp:289-422 (with_bias: qwen2.cpp:348-485, a
+  // bias vector after each of wq, wk, wv).
+  void create_param_layers_fp32(bool with_bias);
+  // Bytes the fp32 layout needs after the header (create_layers checks the file).
+  virtual size_t fp32_weight_bytes() const;
+
+  virtual void attention_rms(int32_t layer_idx, const tensor::Tensor& input) const;
+  virtual void attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const;
+  virtual void attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const;
+  virtual void feed_forward(int32_t layer_idx, const tensor::Tensor& input) const;
+  virtual void cls_logits(const tensor::Tensor& input) const;
 };
 
-class Qwen2Model : public Model {
+// Qwen2 / Qwen2.5 (include/model/qwen2.h:42-87): the Llama decoder with
+// q/k/v biases in the fp32 layout (the int8 layout has none, qwen2.cpp:242-346).
+class Qwen2Model : public LLama2Model {
  public:
   explicit Qwen2Model(base::TokenizerType tokenizer_type, std::string token_path,
-                      std::string model_path, bool is_quant_model)
-      : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
-              std::move(model_path), is_quant_model, ModelFamily::kQwen2) {}
+                      std::string model_path, bool is_quant_model);
+
+ protected:
+  void create_param_layers() override;
+  size_t fp32_weight_bytes() const override;
 };
 
-class Qwen3Model : public Model {
+// Qwen3 (include/model/qwen3.h:48-89): an 8-int header {q_dim, dim, ...,
+// ffn_dim}, norms first and a separate lm_head in the file, q_dim != dim, and
+// a per-head q/k RMSNorm before RoPE.  fp32 only.
+class Qwen3Model : public LLama2Model {
  public:
   explicit Qwen3Model(base::TokenizerType tokenizer_type, std::string token_path,
-                      std::string model_path, bool is_quant_model)
-      : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
-              std::move(model_path), is_quant_model, ModelFamily::kQwen3) {}
+                      std::string model_path, bool is_quant_model);
+  base::Status init(base::DeviceType device_type) override;
+
+ protected:
+  base::Status generate_model_infos(const ModelConfig& config, int32_t extra) override;
+  void create_param_layers() override;
+  size_t fp32_weight_bytes() const override;
+  void attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const override;
 };
 
 }  // namespace model

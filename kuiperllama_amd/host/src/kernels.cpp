@@ -2,6 +2,7 @@
 // (source/op/kernels/kernels_interface.h:6-47) into one call of the C ABI.  A
 // failed call is fatal, as a failed CHECK inside the reference's kernels is.
 #include <algorithm>
+#include <cmath>
 #include <string>
 
 #include "kuiper/alloc.h"
@@ -224,7 +225,58 @@ void rope_hip(int32_t dim, int32_t kv_dim, int32_t head_size, const tensor::Tens
                    cos_cache.ptr<float>(), stream),
            "kl_rope");
 }
+
+// kernels/cpu/scale_kernel.cpp:3-9: input = input * scale in place.
+void scale_hip(float scale, const tensor::Tensor& input, void* stream) {
+  require_hip(input, "scale input");
+  check_rc(kl_scale(scale, const_cast<float*>(input.ptr<float>()), as_int(input.size()), stream),
+           "kl_scale");
+}
+
+// kernels/cpu/softmax_kernel.cpp:4-16: softmax of the whole tensor in place.
+void softmax_hip(const tensor::Tensor& input, void* stream) {
+  require_hip(input, "softmax input");
+  check_rc(kl_softmax(const_cast<float*>(input.ptr<float>()), as_int(input.size()), stream),
+           "kl_softmax");
+}
+
+// kernels/cpu/scale_sum_kernel.cpp:5-22: output += scale[i] * value_i for
+// i = 0 .. t, value_i the `size` floats at value + i * stride (the tensor
+// `value` is a view of its first row, as mha_kernel.cpp:53-59 builds it).
+void scale_sum_hip(const tensor::Tensor& value, const tensor::Tensor& scale,
+                   const tensor::Tensor& output, int t, int size, int stride, void* stream) {
+  require_hip(value, "scale_sum value");
+  require_hip(scale, "scale_sum scale");
+  require_hip(output, "scale_sum output");
+  KUIPER_CHECK(static_cast<size_t>(size) == value.size() &&
+                   static_cast<size_t>(size) == output.size(),
+               "scale_sum size mismatch");
+  KUIPER_CHECK(t >= 0 && scale.size() > static_cast<size_t>(t), "scale_sum: too few scales");
+  check_rc(kl_scale_sum(value.ptr<float>(), scale.ptr<float>(),
+                        const_cast<float*>(output.ptr<float>()), t, size, stride, stream),
+           "kl_scale_sum");
+}
 }  // namespace
+
+// kernels/cpu/softmax_kernel.cpp:18-25 (a host function of the interface):
+// subtract the maximum, exp, divide by the sum, in place in host memory.  The
+// sum adds even and odd elements in two running sums, the order of
+// Armadillo's accumulate that the reference's arma::sum uses.
+void softmax_inplace_cpu(const float* input_ptr, size_t size) {
+  if (!input_ptr || size == 0) return;
+  float* x = const_cast<float*>(input_ptr);
+  const float mx = *std::max_element(x, x + size);
+  for (size_t i = 0; i < size; ++i) x[i] = std::exp(x[i] - mx);
+  float even = 0.f, odd = 0.f;
+  size_t i = 0;
+  for (; i + 1 < size; i += 2) {
+    even += x[i];
+    odd += x[i + 1];
+  }
+  if (i < size) even += x[i];
+  const float sum = even + odd;
+  for (size_t j = 0; j < size; ++j) x[j] = x[j] / sum;
+}
 
 void set_kernel_traits(const KernelTraits& traits) { g_traits = traits; }
 const KernelTraits& kernel_traits() { return g_traits; }
@@ -255,6 +307,15 @@ RoPEKernel get_rope_kernel(base::DeviceType t) {
 }
 SwigluKernel get_swiglu_kernel(base::DeviceType t, void*) {
   return t == base::DeviceType::kDeviceHIP ? swiglu_hip : nullptr;
+}
+ScaleKernel get_scale_kernel(base::DeviceType t) {
+  return t == base::DeviceType::kDeviceHIP ? scale_hip : nullptr;
+}
+SoftmaxInplaceKernel get_softmax_kernel(base::DeviceType t) {
+  return t == base::DeviceType::kDeviceHIP ? softmax_hip : nullptr;
+}
+ScaleSumKernel get_scale_sum_kernel(base::DeviceType t) {
+  return t == base::DeviceType::kDeviceHIP ? scale_sum_hip : nullptr;
 }
 
 void sin_cos_cache_calc_hip(int head_size, int max_seq_len, const tensor::Tensor& sin_cache,

@@ -60,6 +60,21 @@ Model::Model(base::TokenizerType tokenizer_type, base::ModelType model_type,
       model_type_(model_type),
       tokenizer_type_(tokenizer_type) {}
 
+LLama2Model::LLama2Model(base::TokenizerType tokenizer_type, std::string token_path,
+                         std::string model_path, bool is_quant_model, ModelFamily family)
+    : Model(tokenizer_type, base::ModelType::kModelTypeLLama2, std::move(token_path),
+            std::move(model_path), is_quant_model, family) {}
+
+Qwen2Model::Qwen2Model(base::TokenizerType tokenizer_type, std::string token_path,
+                       std::string model_path, bool is_quant_model)
+    : LLama2Model(tokenizer_type, std::move(token_path), std::move(model_path), is_quant_model,
+                  ModelFamily::kQwen2) {}
+
+Qwen3Model::Qwen3Model(base::TokenizerType tokenizer_type, std::string token_path,
+                       std::string model_path, bool is_quant_model)
+    : LLama2Model(tokenizer_type, std::move(token_path), std::move(model_path), is_quant_model,
+                  ModelFamily::kQwen3) {}
+
 Model::~Model() {
   if (engine_) kl_engine_destroy(engine_);
   engine_ = nullptr;
@@ -134,12 +149,10 @@ std::vector<OpProfileStat> Model::get_profile_stats() const {
 
 // llama3.cpp:111-145 for kDeviceHIP.  The tokenizer is optional (token ids in
 // and out), so an empty token_path is accepted; a given one must load.
-base::Status Model::init(base::DeviceType device_type) {
+base::Status LLama2Model::init(base::DeviceType device_type) {
   if (device_type != base::DeviceType::kDeviceHIP)
     return base::error::InvalidArgument(
         "This backend runs on kDeviceHIP only; the CPU and CUDA paths are the reference's.");
-  if (is_quant_model_ && family_ == ModelFamily::kQwen3)
-    return base::error::InvalidArgument("Qwen3 images have no int8 layout.");
   device_type_ = device_type;
   // The file is parsed and sized before any device work, so a bad path or
   // image is reported without touching the GPU.
@@ -162,6 +175,12 @@ base::Status Model::init(base::DeviceType device_type) {
                                  get_buffer(ModelBufferType::kCosCache));
   sampler_ = std::make_unique<sampler::ArgmaxSampler>(device_type_);
   return base::error::Success();
+}
+
+// Qwen3 images are fp32 only (qwen3.cpp has no int8 loader).
+base::Status Qwen3Model::init(base::DeviceType device_type) {
+  if (is_quant_model_) return base::error::InvalidArgument("Qwen3 images have no int8 layout.");
+  return LLama2Model::init(device_type);
 }
 
 // model.cpp:41-111: header, optional group size, then mmap of the whole file.
@@ -224,32 +243,35 @@ base::Status Model::generate_model_infos(const ModelConfig& c, int32_t extra) {
   cfg->kv_dim_ = c.dim * c.kv_head_num / c.head_num;
   cfg->kv_mul_ = c.head_num / c.kv_head_num;
   cfg->q_dim_ = c.dim;
-  if (family_ == ModelFamily::kQwen3) {
-    if (extra <= 0) return base::error::ModelParseError("The Qwen3 FFN width is not valid.");
-    cfg->dim_ = c.hidden_dim;  // the model width
-    cfg->hidden_dim_ = extra;  // the FFN width
-    cfg->is_shared_weight_ = false;
-  } else {
-    cfg->dim_ = c.dim;
-    cfg->hidden_dim_ = c.hidden_dim;
-    cfg->is_shared_weight_ = c.vocab_size > 0;
-  }
+  cfg->dim_ = c.dim;
+  cfg->hidden_dim_ = c.hidden_dim;
+  cfg->is_shared_weight_ = c.vocab_size > 0;
   cfg->vocab_size_ = std::abs(c.vocab_size);
   config_ = std::move(cfg);
   return base::error::Success();
 }
 
-// Walks the weight region in file order (llama3.cpp:183-422, qwen2.cpp:348-485,
-// qwen3.cpp:186-299), wrapping each tensor as an external CPU weight.
-void Model::create_param_layers() {
-  const auto& c = *config_;
-  const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
-                V = c.vocab_size_, hd = c.head_size_;
-  const auto cpu = base::DeviceType::kDeviceCPU;
-  const auto dev = device_type_;
-  const float* p = reinterpret_cast<const float*>(raw_model_data_->weight_data);
-  auto& ly = *layers_;
-  auto matmul = [&](int32_t rows, int32_t cols, bool bias = false) {
+// qwen3.cpp's header {q_dim, dim, layers, heads, kv_heads, vocab, seq_len,
+// ffn_dim}: the first int sizes the heads, the second is the model width,
+// the eighth the FFN width; the classifier is always a separate lm_head.
+base::Status Qwen3Model::generate_model_infos(const ModelConfig& c, int32_t extra) {
+  if (extra <= 0) return base::error::ModelParseError("The Qwen3 FFN width is not valid.");
+  base::Status s = Model::generate_model_infos(c, extra);
+  if (!s) return s;
+  config_->dim_ = c.hidden_dim;
+  config_->hidden_dim_ = extra;
+  config_->is_shared_weight_ = false;
+  return base::error::Success();
+}
+
+namespace {
+// Wraps consecutive tensors of the weight region as external CPU weights of
+// new layers, advancing through the file.
+struct WeightWalk {
+  const float* p;
+  base::DeviceType dev;
+  std::shared_ptr<op::Layer> matmul(int32_t rows, int32_t cols, bool bias = false) {
+    const auto cpu = base::DeviceType::kDeviceCPU;
     auto m = std::make_shared<op::MatmulLayer>(dev, rows, cols, false, bias);
     m->set_weight(0, {rows, cols}, p, cpu);
     p += static_cast<size_t>(rows) * cols;
@@ -259,72 +281,93 @@ void Model::create_param_layers() {
       p += rows;
     }
     return m;
-  };
-  auto norm = [&](int32_t n) {
+  }
+  std::shared_ptr<op::Layer> norm(int32_t n) {
     auto r = std::make_shared<op::RmsNormLayer>(dev, n);
-    r->set_weight(0, {n}, p, cpu);
+    r->set_weight(0, {n}, p, base::DeviceType::kDeviceCPU);
     p += n;
     return r;
-  };
-  auto embedding = [&]() {
-    auto e = std::make_shared<op::EmbeddingLayer>(dev, D, c.seq_len_, V);
-    e->set_weight(0, {V, D}, p, cpu);
+  }
+  std::shared_ptr<op::Layer> embedding(int32_t V, int32_t D, int32_t seq_len) {
+    auto e = std::make_shared<op::EmbeddingLayer>(dev, D, seq_len, V);
+    e->set_weight(0, {V, D}, p, base::DeviceType::kDeviceCPU);
     p += static_cast<size_t>(V) * D;
     return e;
-  };
-
-  if (family_ == ModelFamily::kQwen3) {
-    for (int32_t i = 0; i < 2 * L + 1; ++i) ly.rmsnorm_layers_.push_back(norm(D));
-    ly.embedding_layer_ = embedding();
-    std::vector<std::shared_ptr<op::Layer>> qn, kn;
-    for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(matmul(Dq, D));
-    for (int32_t l = 0; l < L; ++l) qn.push_back(norm(hd));
-    for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(matmul(Dkv, D));
-    for (int32_t l = 0; l < L; ++l) kn.push_back(norm(hd));
-    for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(matmul(Dkv, D));
-    for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(matmul(D, Dq));
-    for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(matmul(F, D));
-    for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(matmul(D, F));
-    for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(matmul(F, D));
-    ly.cls_layer_ = matmul(V, D);
-    for (auto& x : qn) ly.rmsnorm_layers_.push_back(x);
-    for (auto& x : kn) ly.rmsnorm_layers_.push_back(x);
-    return;
   }
-  const bool bias = family_ == ModelFamily::kQwen2;
-  ly.embedding_layer_ = embedding();
+};
+}  // namespace
+
+void LLama2Model::create_param_layers() { create_param_layers_fp32(false); }
+
+void Qwen2Model::create_param_layers() { create_param_layers_fp32(true); }
+
+// Walks the fp32 weight region in file order (llama3.cpp:289-422; with
+// biases, qwen2.cpp:348-485), wrapping each tensor as an external CPU weight.
+void LLama2Model::create_param_layers_fp32(bool bias) {
+  const auto& c = *config_;
+  const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+                V = c.vocab_size_, hd = c.head_size_;
+  WeightWalk w{reinterpret_cast<const float*>(raw_model_data_->weight_data), device_type_};
+  auto& ly = *layers_;
+  ly.embedding_layer_ = w.embedding(V, D, c.seq_len_);
   std::vector<std::shared_ptr<op::Layer>> att, ffn;
-  for (int32_t l = 0; l < L; ++l) att.push_back(norm(D));
-  for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(matmul(Dq, D, bias));
-  for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(matmul(Dkv, D, bias));
-  for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(matmul(Dkv, D, bias));
-  for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(matmul(D, Dq));
-  for (int32_t l = 0; l < L; ++l) ffn.push_back(norm(D));
-  for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(matmul(F, D));
-  for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(matmul(D, F));
-  for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(matmul(F, D));
-  auto final_norm = norm(D);
-  p += static_cast<size_t>(c.seq_len_) * hd;  // freq_cis_real + freq_cis_imag, unused
+  for (int32_t l = 0; l < L; ++l) att.push_back(w.norm(D));
+  for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(w.matmul(Dq, D, bias));
+  for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(w.matmul(Dkv, D, bias));
+  for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(w.matmul(Dkv, D, bias));
+  for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(w.matmul(D, Dq));
+  for (int32_t l = 0; l < L; ++l) ffn.push_back(w.norm(D));
+  for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(w.matmul(F, D));
+  for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(w.matmul(D, F));
+  for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(w.matmul(F, D));
+  auto final_norm = w.norm(D);
+  w.p += static_cast<size_t>(c.seq_len_) * hd;  // freq_cis_real + freq_cis_imag, unused
   if (c.is_shared_weight_) {
-    auto cls = std::make_shared<op::MatmulLayer>(dev, V, D);
+    auto cls = std::make_shared<op::MatmulLayer>(device_type_, V, D);
     cls->set_weight(0, {V, D},
                     std::static_pointer_cast<op::LayerParam>(ly.embedding_layer_)
                         ->get_weight(0)
                         .ptr<float>(),
-                    cpu);
+                    base::DeviceType::kDeviceCPU);
     ly.cls_layer_ = cls;
   } else {
-    ly.cls_layer_ = matmul(V, D);
+    ly.cls_layer_ = w.matmul(V, D);
   }
   for (auto& x : att) ly.rmsnorm_layers_.push_back(x);
   for (auto& x : ffn) ly.rmsnorm_layers_.push_back(x);
   ly.rmsnorm_layers_.push_back(final_norm);
 }
 
+// qwen3.cpp:186-299: the norms first, the embedding, then per kind of matrix
+// all layers (q norms after wq, k norms after wk) and the lm_head; the q/k
+// norms go to rmsnorm slots 2L+1 .. 4L.
+void Qwen3Model::create_param_layers() {
+  const auto& c = *config_;
+  const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+                V = c.vocab_size_, hd = c.head_size_;
+  WeightWalk w{reinterpret_cast<const float*>(raw_model_data_->weight_data), device_type_};
+  auto& ly = *layers_;
+  for (int32_t i = 0; i < 2 * L + 1; ++i) ly.rmsnorm_layers_.push_back(w.norm(D));
+  ly.embedding_layer_ = w.embedding(V, D, c.seq_len_);
+  std::vector<std::shared_ptr<op::Layer>> qn, kn;
+  for (int32_t l = 0; l < L; ++l) ly.wq_layers_.push_back(w.matmul(Dq, D));
+  for (int32_t l = 0; l < L; ++l) qn.push_back(w.norm(hd));
+  for (int32_t l = 0; l < L; ++l) ly.wk_layers_.push_back(w.matmul(Dkv, D));
+  for (int32_t l = 0; l < L; ++l) kn.push_back(w.norm(hd));
+  for (int32_t l = 0; l < L; ++l) ly.wv_layers_.push_back(w.matmul(Dkv, D));
+  for (int32_t l = 0; l < L; ++l) ly.wo_layers_.push_back(w.matmul(D, Dq));
+  for (int32_t l = 0; l < L; ++l) ly.w1_layers_.push_back(w.matmul(F, D));
+  for (int32_t l = 0; l < L; ++l) ly.w2_layers_.push_back(w.matmul(D, F));
+  for (int32_t l = 0; l < L; ++l) ly.w3_layers_.push_back(w.matmul(F, D));
+  ly.cls_layer_ = w.matmul(V, D);
+  for (auto& x : qn) ly.rmsnorm_layers_.push_back(x);
+  for (auto& x : kn) ly.rmsnorm_layers_.push_back(x);
+}
+
 // llama3.cpp:183-287 (and qwen2.cpp:242-346, the same walk without biases):
 // int8 matrices, each followed by its fp32 group scales, then the fp32
 // embedding and norm weights.
-void Model::create_param_quant_layers() {
+void LLama2Model::create_param_quant_layers() {
   const auto& c = *config_;
   const int32_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
                 V = c.vocab_size_;
@@ -360,7 +403,7 @@ void Model::create_param_quant_layers() {
   }
 }
 
-void Model::create_nonparam_layers() {
+void LLama2Model::create_nonparam_layers() {
   const auto& c = *config_;
   auto& ly = *layers_;
   ly.rope_layer_ = std::make_shared<op::RoPELayer>(device_type_, c.q_dim_, c.kv_dim_, c.head_size_);
@@ -370,11 +413,35 @@ void Model::create_nonparam_layers() {
   ly.swiglu_layer_ = std::make_shared<op::SwiGLULayer>(device_type_, c.hidden_dim_);
 }
 
-// llama3.cpp:499-575: sizes the image, creates every layer and checks them.
-base::Status Model::create_layers() {
+// Bytes of the fp32 layouts after the header (export_llama.py:79-210 with
+// biases for Qwen2, export_qwen3.py:55-102).
+size_t LLama2Model::fp32_weight_bytes() const {
   const auto& c = *config_;
   const size_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
                V = c.vocab_size_, hd = c.head_size_;
+  return 4 * (V * D + L * (2 * D + Dq * D + 2 * Dkv * D + D * Dq + 3 * F * D) + D +
+              static_cast<size_t>(c.seq_len_) * hd + (c.is_shared_weight_ ? 0 : V * D));
+}
+
+size_t Qwen2Model::fp32_weight_bytes() const {
+  const auto& c = *config_;
+  return LLama2Model::fp32_weight_bytes() +
+         4 * static_cast<size_t>(c.layer_num_) * (c.q_dim_ + 2 * static_cast<size_t>(c.kv_dim_));
+}
+
+size_t Qwen3Model::fp32_weight_bytes() const {
+  const auto& c = *config_;
+  const size_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+               V = c.vocab_size_, hd = c.head_size_;
+  return 4 * ((2 * L + 1) * D + V * D + L * (Dq * D + 2 * hd + 2 * Dkv * D + D * Dq + 3 * F * D) +
+              V * D);
+}
+
+// llama3.cpp:499-575: sizes the image, creates every layer and checks them.
+base::Status LLama2Model::create_layers() {
+  const auto& c = *config_;
+  const size_t L = c.layer_num_, D = c.dim_, Dq = c.q_dim_, Dkv = c.kv_dim_, F = c.hidden_dim_,
+               V = c.vocab_size_;
   size_t need = 0;  // bytes after the header
   if (is_quant_model_) {
     if (c.is_shared_weight_)
@@ -386,13 +453,8 @@ base::Status Model::create_layers() {
       if (n % gs) return base::error::ModelParseError("A matrix is not a multiple of the group size.");
     need = L * (q8(Dq * D) + 2 * q8(Dkv * D) + q8(D * Dq) + 2 * q8(F * D) + q8(D * F)) +
            q8(V * D) + 4 * (V * D + (2 * L + 1) * D);
-  } else if (family_ == ModelFamily::kQwen3) {
-    need = 4 * ((2 * L + 1) * D + V * D + L * (Dq * D + 2 * hd + 2 * Dkv * D + D * Dq +
-                                               3 * F * D) + V * D);
   } else {
-    const size_t b = family_ == ModelFamily::kQwen2 ? (Dq + 2 * Dkv) : 0;
-    need = 4 * (V * D + L * (2 * D + Dq * D + 2 * Dkv * D + D * Dq + 3 * F * D + b) + D +
-                static_cast<size_t>(c.seq_len_) * hd + (c.is_shared_weight_ ? 0 : V * D));
+    need = fp32_weight_bytes();
   }
   const size_t have = raw_model_data_->file_size -
                       (raw_model_data_->weight_data - static_cast<const int8_t*>(raw_model_data_->data));
@@ -444,7 +506,7 @@ const tensor::Tensor& Model::get_buffer(ModelBufferType buffer_idx) const {
 // device and lays out the step's buffers with the reference's aliases.  The
 // score buffer is the reference's [head_num x seq_len] floats, uninitialised
 // (llama3.cpp:485-487); the attention kernel keeps its split partials in it.
-void Model::init_mem() {
+void LLama2Model::init_mem() {
   const auto& c = *config_;
   auto alloc = base::HIPDeviceAllocatorFactory::get_instance();
   auto alloc_cpu = base::CPUDeviceAllocatorFactory::get_instance();
@@ -462,10 +524,13 @@ void Model::init_mem() {
   STATUS_CHECK(insert_buffer(ModelBufferType::kInputTokens, input_tokens));
   STATUS_CHECK(insert_buffer(ModelBufferType::kInputEmbeddings, input_embeddings));
 
-  const bool qwen3 = family_ == ModelFamily::kQwen3;
+  // The reference's aliases (llama3.cpp:455-459, :486-488) where the widths
+  // agree; separate buffers where the heads' width differs from the model's
+  // (Qwen3, qwen3.cpp:301-380).
+  const bool separate = c.q_dim_ != c.dim_;
   T rms_output(DT::kDataTypeFp32, c.dim_, true, alloc);
   STATUS_CHECK(insert_buffer(ModelBufferType::kOutputRMSNorm, rms_output));
-  if (qwen3) {
+  if (separate) {
     T out_mha(DT::kDataTypeFp32, c.q_dim_, true, alloc);
     STATUS_CHECK(insert_buffer(ModelBufferType::kOutputMHA, out_mha));
   } else {
@@ -497,7 +562,7 @@ void Model::init_mem() {
   T attn(DT::kDataTypeFp32, c.head_num_, c.seq_len_, true, alloc);
   KUIPER_CHECK(attn.byte_size() >= ws, "attention partials exceed the score buffer");
   STATUS_CHECK(insert_buffer(ModelBufferType::kScoreStorage, attn));
-  if (qwen3) {
+  if (separate) {
     T attn_output(DT::kDataTypeFp32, c.dim_, true, alloc);
     STATUS_CHECK(insert_buffer(ModelBufferType::kAttnOutput, attn_output));
   } else {
@@ -528,9 +593,9 @@ std::pair<tensor::Tensor, tensor::Tensor> Model::slice_kv_cache(int32_t layer_id
 }
 
 // llama3.cpp:577-597
-op::EmbeddingOutput Model::embedding(const std::vector<int>& tokens) const {
+op::EmbeddingOutput LLama2Model::embedding(const std::vector<int>& tokens) const {
   KUIPER_CHECK(!tokens.empty(), "no tokens to embed");
-  auto* self = const_cast<Model*>(this);
+  auto* self = const_cast<LLama2Model*>(this);
   tensor::Tensor& input_tokens = self->get_buffer(ModelBufferType::kInputTokens);
   tensor::Tensor& input_embeddings = self->get_buffer(ModelBufferType::kInputEmbeddings);
   const int32_t n = static_cast<int32_t>(tokens.size());
@@ -567,36 +632,20 @@ tensor::Tensor Model::fill_input(const tensor::Tensor& pos_tensor,
 
 // The layer-by-layer step (llama3.cpp:146-166, :599-744; qwen2/qwen3 alike),
 // with the reference's profile names (qwen2.cpp:648-800).
-void Model::attention_rms(int32_t layer_idx, const tensor::Tensor& input) const {
+void LLama2Model::attention_rms(int32_t layer_idx, const tensor::Tensor& input) const {
   profiled("attn.rmsnorm", [&] {
     STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx)->forward(
         input, get_buffer(ModelBufferType::kOutputRMSNorm)));
   });
 }
 
-void Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
-  const auto& c = *config_;
+void LLama2Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
   tensor::Tensor query = get_buffer(ModelBufferType::kQuery);
   const int32_t pos = pos_tensor.index<int32_t>(0);
   auto [key, val] = slice_kv_cache(layer_idx, pos);
   const tensor::Tensor& rms = get_buffer(ModelBufferType::kOutputRMSNorm);
   profiled("attn.wq", [&] { STATUS_CHECK(layers_->wq_layers_.at(layer_idx)->forward(rms, query)); });
-  if (family_ == ModelFamily::kQwen3) {
-    // Per-head q/k RMSNorm (qwen3.cpp:485-500).
-    query.reshape({c.q_dim_ / c.head_size_, c.head_size_});
-    profiled("attn.q_norm", [&] {
-      STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 2 * c.layer_num_ + 1)->forward(query, query));
-    });
-    query.reshape({c.q_dim_});
-    profiled("attn.wk", [&] { STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key)); });
-    key.reshape({c.kv_dim_ / c.head_size_, c.head_size_});
-    profiled("attn.k_norm", [&] {
-      STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 3 * c.layer_num_ + 1)->forward(key, key));
-    });
-    key.reshape({c.kv_dim_});
-  } else {
-    profiled("attn.wk", [&] { STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key)); });
-  }
+  profiled("attn.wk", [&] { STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key)); });
   profiled("attn.wv", [&] { STATUS_CHECK(layers_->wv_layers_.at(layer_idx)->forward(rms, val)); });
   profiled("attn.rope", [&] {
     STATUS_CHECK(layers_->rope_layer_->forward(query, key, pos_tensor,
@@ -606,7 +655,36 @@ void Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) c
   });
 }
 
-void Model::attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
+// qwen3.cpp:459-513: the per-head q/k RMSNorm (rows of head_size, norm
+// layers 2L+1+l and 3L+1+l) between the projections and RoPE.
+void Qwen3Model::attention_qkv(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
+  const auto& c = *config_;
+  tensor::Tensor query = get_buffer(ModelBufferType::kQuery);
+  const int32_t pos = pos_tensor.index<int32_t>(0);
+  auto [key, val] = slice_kv_cache(layer_idx, pos);
+  const tensor::Tensor& rms = get_buffer(ModelBufferType::kOutputRMSNorm);
+  profiled("attn.wq", [&] { STATUS_CHECK(layers_->wq_layers_.at(layer_idx)->forward(rms, query)); });
+  query.reshape({c.q_dim_ / c.head_size_, c.head_size_});
+  profiled("attn.q_norm", [&] {
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 2 * c.layer_num_ + 1)->forward(query, query));
+  });
+  query.reshape({c.q_dim_});
+  profiled("attn.wk", [&] { STATUS_CHECK(layers_->wk_layers_.at(layer_idx)->forward(rms, key)); });
+  key.reshape({c.kv_dim_ / c.head_size_, c.head_size_});
+  profiled("attn.k_norm", [&] {
+    STATUS_CHECK(layers_->rmsnorm_layers_.at(layer_idx + 3 * c.layer_num_ + 1)->forward(key, key));
+  });
+  key.reshape({c.kv_dim_});
+  profiled("attn.wv", [&] { STATUS_CHECK(layers_->wv_layers_.at(layer_idx)->forward(rms, val)); });
+  profiled("attn.rope", [&] {
+    STATUS_CHECK(layers_->rope_layer_->forward(query, key, pos_tensor,
+                                               get_buffer(ModelBufferType::kSinCache),
+                                               get_buffer(ModelBufferType::kCosCache),
+                                               tensor::Tensor{}));
+  });
+}
+
+void LLama2Model::attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) const {
   const tensor::Tensor& mha_output = get_buffer(ModelBufferType::kOutputMHA);
   auto mha = std::static_pointer_cast<op::MultiHeadAttention>(layers_->mha_layer_);
   mha->set_pos(pos_tensor.index<int32_t>(0));
@@ -623,7 +701,7 @@ void Model::attention_mha(int32_t layer_idx, const tensor::Tensor& pos_tensor) c
   });
 }
 
-void Model::feed_forward(int32_t layer_idx, const tensor::Tensor& input) const {
+void LLama2Model::feed_forward(int32_t layer_idx, const tensor::Tensor& input) const {
   const auto& c = *config_;
   profiled("ffn.residual_add1", [&] {
     STATUS_CHECK(layers_->add_layer_->forward(input, get_buffer(ModelBufferType::kAttnOutput), input));
@@ -642,7 +720,7 @@ void Model::feed_forward(int32_t layer_idx, const tensor::Tensor& input) const {
   profiled("ffn.residual_add2", [&] { STATUS_CHECK(layers_->add_layer_->forward(input, w2, input)); });
 }
 
-void Model::cls_logits(const tensor::Tensor& input) const {
+void LLama2Model::cls_logits(const tensor::Tensor& input) const {
   profiled("output.rmsnorm", [&] {
     STATUS_CHECK(layers_->rmsnorm_layers_.at(2 * config_->layer_num_)->forward(input, input));
   });
@@ -651,7 +729,7 @@ void Model::cls_logits(const tensor::Tensor& input) const {
   });
 }
 
-int32_t Model::post_processing(const tensor::Tensor&, bool is_prompt) const {
+int32_t LLama2Model::post_processing(const tensor::Tensor&, bool is_prompt) const {
   const tensor::Tensor& out = get_buffer(ModelBufferType::kForwardOutput);
   if (is_prompt) return -1;
   int32_t next = -1;
@@ -661,7 +739,7 @@ int32_t Model::post_processing(const tensor::Tensor&, bool is_prompt) const {
   return next;
 }
 
-base::Status Model::forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+base::Status LLama2Model::forward(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
                             int&) const {
   if (input.is_empty()) return base::error::InvalidArgument("The input tensor is empty.");
   const int32_t pos = pos_tensor.index<int32_t>(0);
@@ -680,7 +758,7 @@ base::Status Model::forward(const tensor::Tensor& input, const tensor::Tensor& p
 // llama3.cpp:641-649.  Fused: the token is the one embedding() stored for
 // this input row (fill_input's row of kInputEmbeddings), and the engine runs
 // the whole step in one launch; its logits are copied into kForwardOutput.
-base::Status Model::predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+base::Status LLama2Model::predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
                             bool is_prompt, int& next) const {
   if (!fused_) {
     base::Status s = forward(input, pos_tensor, next);

@@ -297,6 +297,25 @@ void or_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int
              value_cache + layer_offset);
 }
 
+// kernels/cpu/scale_kernel.cpp:3-9: x = x * scale (Armadillo's vector times
+// scalar: one rounding per element).
+void or_scale(float scale, float* x, int n) {
+  for (int i = 0; i < n; ++i) x[i] = x[i] * scale;
+}
+
+// kernels/cpu/scale_sum_kernel.cpp:5-22: output += scale[i] * value_i for
+// i = 0 .. pos in increasing i, value_i the `size` floats at value + i * stride
+// (Armadillo evaluates the product vector, then adds it: two roundings).
+void or_scale_sum(const float* value, const float* scale, float* out, int pos, int size, int stride) {
+  for (int i = 0; i <= pos; ++i) {
+    const float* v = value + (int64_t)i * stride;
+    for (int d = 0; d < size; ++d) {
+      const float p = scale[i] * v[d];
+      out[d] = out[d] + p;
+    }
+  }
+}
+
 // kernels/cpu/swiglu_kernel.cpp:3-23: a = a * (1 / (1 + exp(-a))); out = a * b.
 void or_swiglu(const float* a, const float* b, float* out, int n) {
   for (int i = 0; i < n; ++i) {

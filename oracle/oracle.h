@@ -51,6 +51,8 @@ void or_softmax(float* x, int n);
 void or_mha(int pos, int head_num, int layer_index, int seq_len, int kv_dim, int kv_mul,
             int head_size, float* out, const float* q, float* score, const float* key_cache,
             const float* value_cache);
+void or_scale(float scale, float* x, int n);
+void or_scale_sum(const float* value, const float* scale, float* out, int pos, int size, int stride);
 void or_swiglu(const float* a, const float* b, float* out, int n);
 void or_add(const float* a, const float* b, float* out, int n);
 int or_embedding(const int32_t* tokens, int n_tokens, const float* table, int vocab, int dim,

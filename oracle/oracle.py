@@ -44,6 +44,8 @@ _sigs = {
     "or_rope": (None, [_i, _i, _i, _i, _p, _p, _i, _p, _p]),
     "or_softmax": (None, [_p, _i]),
     "or_mha": (None, [_i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p]),
+    "or_scale": (None, [_f, _p, _i]),
+    "or_scale_sum": (None, [_p, _p, _p, _i, _i, _i]),
     "or_swiglu": (None, [_p, _p, _p, _i]),
     "or_add": (None, [_p, _p, _p, _i]),
     "or_embedding": (_i, [_p, _i, _p, _i, _i, _p]),
@@ -147,6 +149,21 @@ def mha(pos, head_num, layer, seq_len, kv_dim, kv_mul, hd, q, kcache, vcache):
     lib.or_mha(pos, head_num, layer, seq_len, kv_dim, kv_mul, hd, out.ctypes.data, q.ctypes.data,
                score.ctypes.data, kcache.ctypes.data, vcache.ctypes.data)
     return out
+
+
+def scale(s, x):
+    y = _f32(x).copy()
+    lib.or_scale(s, y.ctypes.data, y.size)
+    return y
+
+
+def scale_sum(value, sc, out, pos, size, stride):
+    """out[d] += sc[i] * value[i * stride + d] for i <= pos (value flat)."""
+    v = _f32(value)
+    s = _f32(sc)
+    o = _f32(out).copy()
+    lib.or_scale_sum(v.ctypes.data, s.ctypes.data, o.ctypes.data, pos, size, stride)
+    return o
 
 
 def swiglu(a, b):

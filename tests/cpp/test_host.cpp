@@ -143,12 +143,36 @@ void cpu_status_codes() {
 
 TEST_CASE(cpu_kernel_factories)
 void cpu_kernel_factories() {
-  // The reference's CPU kernels are not part of this backend.
-  EXPECT(kernel::get_matmul_kernel(DeviceType::kDeviceCPU) == nullptr);
-  EXPECT(kernel::get_add_kernel(DeviceType::kDeviceCUDA) == nullptr);
-  EXPECT(kernel::get_matmul_kernel(DeviceType::kDeviceHIP) != nullptr);
-  EXPECT(kernel::get_mha_kernel(DeviceType::kDeviceHIP) != nullptr);
-  EXPECT(kernel::get_rmsnorm_dim_kernel(DeviceType::kDeviceHIP) != nullptr);
+  // Every factory of kernels_interface.h:51-75 has a kDeviceHIP adapter; the
+  // reference's CPU and CUDA kernels are not part of this backend.
+  const DeviceType H = DeviceType::kDeviceHIP;
+  EXPECT(kernel::get_add_kernel(H) && kernel::get_emb_kernel(H) && kernel::get_matmul_kernel(H) &&
+         kernel::get_matmul_kernel_quant8(H) && kernel::get_mha_kernel(H) &&
+         kernel::get_rmsnorm_kernel(H) && kernel::get_rmsnorm_dim_kernel(H) &&
+         kernel::get_rope_kernel(H) && kernel::get_swiglu_kernel(H) && kernel::get_scale_kernel(H) &&
+         kernel::get_softmax_kernel(H) && kernel::get_scale_sum_kernel(H));
+  for (DeviceType t : {DeviceType::kDeviceCPU, DeviceType::kDeviceCUDA}) {
+    EXPECT(kernel::get_matmul_kernel(t) == nullptr && kernel::get_add_kernel(t) == nullptr);
+    EXPECT(kernel::get_scale_kernel(t) == nullptr && kernel::get_softmax_kernel(t) == nullptr &&
+           kernel::get_scale_sum_kernel(t) == nullptr);
+  }
+}
+
+TEST_CASE(cpu_softmax_inplace)
+void cpu_softmax_inplace() {
+  // softmax_kernel.cpp:18-25 on host memory: exp(x - max) / sum.
+  std::vector<float> x = {1.f, 2.f, 3.f};
+  kernel::softmax_inplace_cpu(x.data(), x.size());
+  const double e1 = std::exp(-2.0), e2 = std::exp(-1.0), s = e1 + e2 + 1.0;
+  EXPECT_NEAR(x[0], e1 / s, 1e-7);
+  EXPECT_NEAR(x[1], e2 / s, 1e-7);
+  EXPECT_NEAR(x[2], 1.0 / s, 1e-7);
+  std::vector<float> one = {-7.5f};
+  kernel::softmax_inplace_cpu(one.data(), 1);
+  EXPECT(one[0] == 1.f);  // one element: exp(0) / exp(0)
+  std::vector<float> same(9, 3.25f);
+  kernel::softmax_inplace_cpu(same.data(), same.size());
+  for (float v : same) EXPECT(v == 1.f / 9.f);
 }
 
 TEST_CASE(cpu_layer_check_reports_status)
@@ -422,6 +446,69 @@ void hip_add_swiglu() {
   }
 }
 
+TEST_CASE(hip_mha_from_building_blocks)
+void hip_mha_from_building_blocks() {
+  // The reference's CPU MHA (kernels/cpu/mha_kernel.cpp:5-61) written the
+  // reference's way, from factory kernels on kDeviceHIP tensors: per head, a
+  // 1-row matmul per position (score = q . K_t / sqrt(hd)), the in-place
+  // softmax, a zeroed output and the scale-sum over V rows.  It must agree
+  // with the fused MHA kernel on the same caches.
+  const int head_num = 8, kv_mul = 4, head_size = 64, seq_len = 96, layer = 1, pos = 70;
+  const int kv_dim = head_num / kv_mul * head_size;
+  auto alloc = hip_alloc();
+  Tensor q(DataType::kDataTypeFp32, head_num * head_size, true, cpu_alloc());
+  Tensor kc(DataType::kDataTypeFp32, 2 * seq_len * kv_dim, true, cpu_alloc());
+  Tensor vc(DataType::kDataTypeFp32, 2 * seq_len * kv_dim, true, cpu_alloc());
+  fill(q, 31);
+  fill(kc, 32);
+  fill(vc, 33);
+  q.to_hip();
+  kc.to_hip();
+  vc.to_hip();
+  Tensor score(DataType::kDataTypeFp32, head_num * seq_len, true, alloc);
+  Tensor out(DataType::kDataTypeFp32, head_num * head_size, true, alloc);
+  const DeviceType H = DeviceType::kDeviceHIP;
+  auto view = [&](const float* p, std::vector<int32_t> dims) {
+    Tensor t(DataType::kDataTypeFp32, dims, false, nullptr, const_cast<float*>(p));
+    t.set_device_type(H);
+    return t;
+  };
+  const float scale = 1.f / std::sqrt(static_cast<float>(head_size));
+  const size_t layer_off = static_cast<size_t>(layer) * seq_len * kv_dim;
+  for (int h = 0; h < head_num; ++h) {
+    float* sh = score.ptr<float>() + h * seq_len;
+    Tensor qh = view(q.ptr<float>() + h * head_size, {head_size});
+    for (int t = 0; t <= pos; ++t) {
+      const float* kt = kc.ptr<float>() + layer_off + t * kv_dim + (h / kv_mul) * head_size;
+      kernel::get_matmul_kernel(H)(qh, view(kt, {1, head_size}), view(sh + t, {1}), scale, nullptr);
+    }
+    Tensor sc = view(sh, {pos + 1});
+    kernel::get_softmax_kernel(H)(sc, nullptr);
+    float* oh = out.ptr<float>() + h * head_size;
+    alloc->memset_zero(oh, sizeof(float) * head_size, nullptr, false);
+    const float* vh = vc.ptr<float>() + layer_off + (h / kv_mul) * head_size;
+    kernel::get_scale_sum_kernel(H)(view(vh, {head_size}), sc, view(oh, {head_size}), pos,
+                                    head_size, kv_dim, nullptr);
+  }
+  Tensor ws(DataType::kDataTypeFp32,
+            static_cast<int32_t>(kernel::mha_workspace_bytes(head_num, kv_mul, seq_len, head_size) / 4) + 1,
+            true, alloc);
+  alloc->memset_zero(ws.ptr<float>(), ws.byte_size(), nullptr, true);
+  Tensor fused(DataType::kDataTypeFp32, head_num * head_size, true, alloc);
+  kernel::get_mha_kernel(H)(pos, head_num, layer, seq_len, kv_dim, kv_mul, head_size, fused, q, ws, kc,
+                            vc, H, nullptr);
+  Tensor a = to_host(out), b = to_host(fused);
+  for (int i = 0; i < head_num * head_size; ++i) EXPECT_NEAR(a.index<float>(i), b.index<float>(i), 2e-6);
+  // The scale kernel: x * scale in place, one rounding.
+  Tensor x(DataType::kDataTypeFp32, 1000, true, cpu_alloc());
+  fill(x, 34);
+  Tensor xh = x.clone();
+  x.to_hip();
+  kernel::get_scale_kernel(H)(0.375f, x, nullptr);
+  Tensor y = to_host(x);
+  for (int i = 0; i < 1000; ++i) EXPECT(y.index<float>(i) == xh.index<float>(i) * 0.375f);
+}
+
 TEST_CASE(hip_embedding)
 void hip_embedding() {
   // test_cu_emb.cpp:emb1_nostream: row 1 of a [vocab x 512] table of i.
@@ -494,6 +581,30 @@ std::string join(const std::vector<int32_t>& v) {
   return s + "]";
 }
 
+// A reference-style subclass (include/model/llama3.h:33-53 overrides
+// predict): counts its predict() calls and forwards them.  Model::generate
+// must reach it through the virtual interface.
+template <class Base>
+class CountingModel : public Base {
+ public:
+  using Base::Base;
+  base::Status predict(const tensor::Tensor& input, const tensor::Tensor& pos_tensor,
+                       bool is_prompt, int& next) const override {
+    ++calls;
+    return Base::predict(input, pos_tensor, is_prompt, next);
+  }
+  mutable int calls = 0;
+};
+
+template <class M>
+std::pair<std::vector<int32_t>, int> counted_generate(M* m, const std::vector<int32_t>& prompt,
+                                                      int n_new) {
+  STATUS_CHECK(m->init(DeviceType::kDeviceHIP));
+  std::vector<int32_t> out;
+  STATUS_CHECK(static_cast<const model::Model*>(m)->generate(prompt, n_new, out));
+  return {out, m->calls};
+}
+
 int run_model(int argc, char** argv) {
   if (argc < 7) {
     std::fprintf(stderr, "usage: model <image> <family> <quant> <n_new> <tok0> [tok...]\n");
@@ -554,12 +665,25 @@ int run_model(int argc, char** argv) {
       tok = next;
     }
   }
+  // The same loop through a subclass that overrides predict().
+  std::pair<std::vector<int32_t>, int> sub;
+  if (family == model::ModelFamily::kQwen2) {
+    CountingModel<model::Qwen2Model> cm(base::TokenizerType::kEncodeBpe, "", path, quant);
+    sub = counted_generate(&cm, prompt, n_new);
+  } else if (family == model::ModelFamily::kQwen3) {
+    CountingModel<model::Qwen3Model> cm(base::TokenizerType::kEncodeBpe, "", path, quant);
+    sub = counted_generate(&cm, prompt, n_new);
+  } else {
+    CountingModel<model::LLama2Model> cm(base::TokenizerType::kEncodeSpe, "", path, quant, family);
+    sub = counted_generate(&cm, prompt, n_new);
+  }
   const auto& c = m->config();
   std::printf("{\"dims\": [%d, %d, %d, %d, %d, %d, %d, %d], \"layered\": %s, \"fused\": %s, "
-              "\"fused_steps\": %s, \"pooled_bytes\": %zu}\n",
+              "\"fused_steps\": %s, \"subclass\": %s, \"subclass_predict_calls\": %d, "
+              "\"pooled_bytes\": %zu}\n",
               c.dim_, c.q_dim_, c.kv_dim_, c.hidden_dim_, c.layer_num_, c.head_num_,
               c.kv_head_num_, c.vocab_size_, join(layered).c_str(), join(fused).c_str(),
-              join(fused_steps).c_str(),
+              join(fused_steps).c_str(), join(sub.first).c_str(), sub.second,
               base::HIPDeviceAllocatorFactory::get_instance()->pooled_bytes());
   return 0;
 }

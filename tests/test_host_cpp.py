@@ -10,7 +10,8 @@ model::Model) through its C++ test program tests/cpp/_build/test_host.
   first-max argmax, allocator reuse, tensor moves).
 * whole model (GPU): a synthetic image loaded by model::Model, driven the way
   demo/main.cpp drives it, layer by layer and fused; first-step logits within
-  1e-4 relative of the CPU oracle and greedy tokens identical to it.
+  1e-4 relative of the CPU oracle and greedy tokens identical to it; the same
+  loop through a subclass that overrides the virtual predict().
 """
 import json
 import os
@@ -81,3 +82,7 @@ def test_host_model_matches_oracle(K, O, gpu, tmp_path, name):
     assert out["layered"] == want, (out["layered"], want)
     assert out["fused"] == want, (out["fused"], want)
     assert out["fused_steps"] == want, (out["fused_steps"], want)
+    # a subclass overriding predict() (llama3.h:33-53): generate() reaches it
+    # once per position, and its tokens are the oracle's
+    assert out["subclass"] == want, (out["subclass"], want)
+    assert out["subclass_predict_calls"] == len(prompt) + n_new - 1

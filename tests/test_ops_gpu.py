@@ -218,6 +218,52 @@ def test_add_exact(K, O, gpu):
     assert np.array_equal(da.numpy(), O.add(a, b))
 
 
+def test_scale_bit_exact(K, O, gpu):
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal(10001).astype(np.float32)
+    for sc in (0.125, 1.0 / np.sqrt(128.0), -3.7):
+        d = D(K, x)
+        ok(K.lib.kl_scale(C.c_float(sc), d.ptr, x.size, None), "kl_scale")
+        assert np.array_equal(d.numpy(), O.scale(np.float32(sc), x))
+
+
+@pytest.mark.parametrize("n", [1, 7, 1000, 4096, 70001])
+def test_softmax_vs_oracle(K, O, gpu, n):
+    """One vector in place: max-subtract, exp, sum, divide.  The sum runs in
+    another order than the CPU's (which adds in two running sums), so every
+    element differs by about the same factor, bounded by the sums' rounding
+    (~4e-7 sqrt(n) relative), plus the device expf; both sides are also held
+    to an fp64 softmax.  A single element is exactly 1."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 4).astype(np.float32)
+    d = D(K, x)
+    ok(K.lib.kl_softmax(d.ptr, n, None), "kl_softmax")
+    got, want = d.numpy(), O.softmax(x)
+    bound = 4e-7 * np.sqrt(n) + 1e-6
+    assert np.max(np.abs(got / want - 1)) <= bound, np.max(np.abs(got / want - 1))
+    e = np.exp(x.astype(np.float64) - x.max())
+    exact = e / e.sum()
+    for y in (got, want):
+        assert np.max(np.abs(y / exact - 1)) <= bound
+    if n == 1:
+        assert got[0] == 1.0
+
+
+@pytest.mark.parametrize("pos,size,stride", [(0, 64, 512), (17, 64, 512), (300, 128, 256), (5, 1000, 1000)])
+def test_scale_sum_bit_exact(K, O, gpu, pos, size, stride):
+    """The MHA's weighted sum of V rows (value rows at a stride, as in the
+    cache): bit-exact, the products and sums rounded in the reference's order."""
+    rng = np.random.default_rng(pos + size)
+    value = rng.standard_normal(pos * stride + size).astype(np.float32)
+    sc = rng.random(pos + 1).astype(np.float32)
+    out0 = rng.standard_normal(size).astype(np.float32)
+    dv, ds, do = D(K, value), D(K, sc), D(K, out0)
+    ok(K.lib.kl_scale_sum(dv.ptr, ds.ptr, do.ptr, pos, size, stride, None), "kl_scale_sum")
+    assert np.array_equal(do.numpy(), O.scale_sum(value, sc, out0, pos, size, stride))
+    # overlapping rows are refused
+    assert K.lib.kl_scale_sum(dv.ptr, ds.ptr, do.ptr, 1, size, size - 1, None) == -1
+
+
 def test_embedding_kat_and_bounds(K, O, gpu):
     W = np.arange(2048, dtype=np.float32).reshape(4, 512)
     toks = np.array([1, 2], np.int32)

@@ -249,6 +249,43 @@ def test_mha_brute_force(O, H, kvm, hd):
 
 
 # ------------------------------------------- SwiGLU / add / emb / argmax ----
+def test_scale_closed_form(O):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(513).astype(np.float32)
+    # a power of two scales exactly; otherwise one fp32 rounding per element
+    assert np.array_equal(O.scale(0.25, x), x / np.float32(4))
+    assert np.array_equal(O.scale(np.float32(0.3), x), x * np.float32(0.3))
+
+
+def test_scale_sum_pins(O):
+    """One-hot weights pick one value row exactly (catches a wrong stride or
+    row index); integer data sums exactly; fp64 brute force otherwise; and
+    rows past pos are never read."""
+    rng = np.random.default_rng(5)
+    pos, size, stride = 9, 24, 40
+    value = rng.standard_normal(pos * stride + size).astype(np.float32)
+    out0 = rng.standard_normal(size).astype(np.float32)
+    for i in (0, 4, pos):
+        sc = np.zeros(pos + 1, np.float32)
+        sc[i] = 1.0
+        got = O.scale_sum(value, sc, np.zeros(size, np.float32), pos, size, stride)
+        assert np.array_equal(got, value[i * stride:i * stride + size])
+    vi = rng.integers(-50, 50, value.size).astype(np.float32)
+    si = rng.integers(-3, 4, pos + 1).astype(np.float32)
+    oi = rng.integers(-50, 50, size).astype(np.float32)
+    want = oi.astype(np.int64) + sum(int(si[i]) * vi[i * stride:i * stride + size].astype(np.int64)
+                                     for i in range(pos + 1))
+    assert np.array_equal(O.scale_sum(vi, si, oi, pos, size, stride), want.astype(np.float32))
+    sc = rng.random(pos + 1).astype(np.float32)
+    ref = out0.astype(np.float64) + sum(float(sc[i]) * value[i * stride:i * stride + size].astype(np.float64)
+                                        for i in range(pos + 1))
+    assert rel_err(O.scale_sum(value, sc, out0, pos, size, stride), ref) < 1e-6
+    # a NaN past pos would poison the sum if it were read
+    bad = value.copy()
+    bad = np.concatenate([bad, np.full(stride, np.nan, np.float32)])
+    assert np.all(np.isfinite(O.scale_sum(bad, sc, out0, pos, size, stride)))
+
+
 def test_swiglu(O):
     a = np.array([0.0, 30.0, -30.0, 1.0], np.float32)
     b = np.array([5.0, 2.0, 2.0, 3.0], np.float32)
