@@ -208,14 +208,15 @@ int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size
                     int ldq, const float* key_cache, const float* value_cache, int kv_dim,
                     float* out, int ldo, void* stream);
 /* kl_attn_prefill with a workspace (no reference counterpart for the split
- * itself; same MHAKernel semantics): where the (64-row block, head) pairs of
- * a launch are fewer than the device's CUs — rows far into a long context —
- * head size 128 cuts each row block's keys into up to 4 contiguous parts, one
- * workgroup each, and a merge pass combines their partial (max, sum, output)
- * rows in a fixed order.  workspace: kl_attn_prefill_workspace_size bytes,
- * 16-byte aligned (0 bytes for head sizes 32 and 64, which run
- * kl_attn_prefill; so does a launch that fills the CUs); KL_EWORKSPACE if
- * smaller. */
+ * itself; same MHAKernel semantics).  Head sizes 64 and 128: where the causal
+ * (64-row block, head) segments are unequal or fewer than the CUs, one
+ * workgroup per CU takes an equal share of the (row block, 64-key block)
+ * units; a segment cut between workgroups leaves partial (max, sum, output)
+ * rows in the workspace, and a merge pass combines them in key order.
+ * workspace: kl_attn_prefill_workspace_size bytes, 16-byte aligned, no
+ * initialisation needed (launches sharing one workspace must not overlap);
+ * KL_EWORKSPACE if smaller.  0 bytes for head size 32, which runs
+ * kl_attn_prefill, as does a launch that the split would not shorten. */
 int kl_attn_prefill_workspace_size(int n_pos, int head_num, int head_size, size_t* bytes);
 int kl_attn_prefill_ws(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
                        int ldq, const float* key_cache, const float* value_cache, int kv_dim,

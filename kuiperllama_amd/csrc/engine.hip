@@ -472,8 +472,9 @@ struct kl_engine {
   char* pf_buf = nullptr;       // one allocation for everything below
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
   float *pf_h1 = nullptr, *pf_h3 = nullptr, *pf_xlast = nullptr;
-  float* pf_ws = nullptr;       // split-K partials [kPrefillMaxSplits][rows][dim], or the
-  size_t pf_ws_bytes = 0;       //   attention's key-range parts (whichever is larger)
+  float* pf_ws = nullptr;       // split-K partials [kPrefillMaxSplits][rows][dim]
+  void* pf_aws = nullptr;       // the attention's stream-K records
+  size_t pf_aws_bytes = 0;
   int32_t* pf_tok = nullptr;    // [seq_len] prompt ids
   int32_t* pf_next = nullptr;
   void* pf_am = nullptr;        // argmax workspace (zeroed once)
@@ -1466,9 +1467,9 @@ int prefill_scratch(kl_engine* e, int rows) {
   size_t attn_ws = 0;
   r = kl_attn_prefill_workspace_size(rows, m.H, m.hd, &attn_ws);
   if (r != KL_OK) return r;
-  const size_t sz_ws = al(std::max(static_cast<size_t>(kPrefillMaxSplits) * R * m.D * 4, attn_ws));
-  const size_t total =
-      2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(m.D * 4) + al(m.S * 4) + al(256) + al(am);
+  const size_t sz_ws = al(static_cast<size_t>(kPrefillMaxSplits) * R * m.D * 4);
+  const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(attn_ws) + al(m.D * 4) +
+                       al(m.S * 4) + al(256) + al(am);
   char* buf = nullptr;
   hipError_t err = hipMalloc(&buf, total);
   if (err != hipSuccess) return KL_ENOMEM;
@@ -1487,7 +1488,8 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_h1 = reinterpret_cast<float*>(take(sz_h));
   e->pf_h3 = reinterpret_cast<float*>(take(sz_h));
   e->pf_ws = reinterpret_cast<float*>(take(sz_ws));
-  e->pf_ws_bytes = sz_ws;
+  e->pf_aws = take(al(attn_ws));
+  e->pf_aws_bytes = attn_ws;
   e->pf_xlast = reinterpret_cast<float*>(take(al(m.D * 4)));
   e->pf_tok = reinterpret_cast<int32_t*>(take(al(m.S * 4)));
   e->pf_next = reinterpret_cast<int32_t*>(take(al(256)));
@@ -1539,10 +1541,8 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
                       e->cos_t, st));
     }
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
-    // pf_ws (the own GEMM's split-K partials) is free between the GEMMs; it
-    // holds the key-range parts of the attention where the rows are few.
-    PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq, e->pf_ws,
-                          e->pf_ws_bytes, st));
+    PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq,
+                          e->pf_aws, e->pf_aws_bytes, st));
     const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
     {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);

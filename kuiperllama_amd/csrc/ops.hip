@@ -984,49 +984,41 @@ int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, i
 }  // extern "C"
 
 namespace {
-constexpr int kPrefillMaxParts = 4;  // key-range parts of the split causal attention
-
-// Key-range parts for a prefill attention launch (head size 128): 1 where the
-// (row block, head) workgroups fill the CUs, else the count of at most
-// kPrefillMaxParts that minimises rounds of workgroups per part length
-// (ceil(g parts / cus) / parts), each part keeping at least 2 key blocks.
-int attn_prefill_parts(int pos0, int n, int heads) {
+int device_cus() {
   static int cus = 0;
   if (cus == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
-      cus = 256;
+      cus = kFaMaxWorkers;
   }
-  const long long g = static_cast<long long>((n + kPrefillQB - 1) / kPrefillQB) * heads;
-  const int max_kb = (pos0 + n - 1) / kPrefillKB8 + 1;
-  int best = 1;
-  double best_cost = 1.0;
-  for (int s = 2; s <= kPrefillMaxParts && 2 * s <= max_kb && g < cus; ++s) {
-    const double cost = static_cast<double>((g * s + cus - 1) / cus) / s;
-    if (cost < best_cost - 1e-9) {
-      best = s;
-      best_cost = cost;
-    }
-  }
-  return best;
+  return cus;
+}
+
+// Stream-K workgroups for a head size 64 / 128 prefill attention launch with
+// a workspace: one per CU (at most kFaMaxWorkers, at most one per unit), or 0
+// (one workgroup per segment) where equal ranges would not shorten the
+// longest walk: the last row block's key blocks when the segments fit the
+// CUs at once.
+int attn_prefill_workers(int pos0, int n, int heads) {
+  const FaGeom geo = fa_geom(pos0, n);
+  const long long W = geo.wh * heads, segs = static_cast<long long>(geo.nqb) * heads;
+  const long long G = std::min<long long>(std::min(device_cus(), kFaMaxWorkers), W);
+  const long long per = (W + G - 1) / G;
+  const long long plain = segs <= device_cus() ? geo.nk_last : (W + device_cus() - 1) / device_cus() + geo.nk_last;
+  return per < plain ? static_cast<int>(G) : 0;
 }
 
 template <int HD>
 int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
                         int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st,
                         float* part = nullptr) {
-  // Head sizes 64 and 128 on the matrix cores (128: eight waves per
-  // workgroup); 32 on the vector ALUs.
+  // Head sizes 64 and 128 on the matrix cores; 32 on the vector ALUs.
   constexpr bool kMfma = HD == 64 || HD == 128;
-  constexpr bool kMfma8 = HD == 128;
-  const void* fn = kMfma8 ? reinterpret_cast<const void*>(&k_attn_prefill_mfma8<128>)
-                   : kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_mfma<kMfma ? HD : 64>)
-                           : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
-  const size_t lds = kMfma8 ? attn_prefill_mfma8_lds_bytes(HD)
-                     : kMfma ? attn_prefill_mfma_lds_bytes(HD)
-                             : attn_prefill_lds_bytes(HD);
+  const void* fn = kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_fa<kMfma ? HD : 64>)
+                         : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
+  const size_t lds = kMfma ? attn_prefill_fa_lds_bytes(HD) : attn_prefill_lds_bytes(HD);
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1036,22 +1028,22 @@ int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* v
   }
   const float scale = 1.f / std::sqrt(static_cast<float>(HD));
   const dim3 grid((n + kPrefillQB - 1) / kPrefillQB, heads);
-  if constexpr (kMfma8) {
-    const int parts = part ? attn_prefill_parts(pos0, n, heads) : 1;
-    hipLaunchKernelGGL(k_attn_prefill_mfma8<128>, dim3(grid.x, grid.y, parts), dim3(512), lds, st, q,
-                       ldq, kc, vc, kv_dim, kv_mul, out, ldo, pos0, n, scale, parts, part);
-    if (parts > 1) {
+  if constexpr (kMfma) {
+    const int workers = part ? attn_prefill_workers(pos0, n, heads) : 0;
+    const unsigned blocks = workers ? workers : grid.x * grid.y;
+    hipLaunchKernelGGL(k_attn_prefill_fa<HD>, dim3(blocks), dim3(512), lds, st, q, ldq, kc, vc,
+                       kv_dim, kv_mul, out, ldo, pos0, n, scale, heads, workers ? part : nullptr);
+    if (workers) {
       const int r = launch_rc();
       if (r != KL_OK) return r;
-      hipLaunchKernelGGL(k_attn_prefill_merge8<128>, grid, dim3(256), 0, st, part, out, ldo, n,
-                         parts);
+      constexpr int kGroups = kPrefillQB / (256 / (HD / 4));  // merge workgroups per row block
+      hipLaunchKernelGGL(k_attn_prefill_merge<HD>, dim3(grid.x * kGroups, heads), dim3(256), 0, st,
+                         part, out, ldo, pos0, n, heads, workers);
     }
-  } else if constexpr (kMfma)
-    hipLaunchKernelGGL(k_attn_prefill_mfma<HD>, grid, dim3(256), lds, st, q, ldq, kc, vc, kv_dim,
-                       kv_mul, out, ldo, pos0, n, scale);
-  else
+  } else {
     hipLaunchKernelGGL(k_attn_prefill<HD>, grid, dim3(256), lds, st, q, ldq, kc, vc, kv_dim, kv_mul,
                        out, ldo, pos0, n, scale);
+  }
   return launch_rc();
 }
 }  // namespace
@@ -1079,10 +1071,7 @@ int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size
 
 int kl_attn_prefill_workspace_size(int n_pos, int head_num, int head_size, size_t* bytes) {
   if (!bytes || n_pos <= 0 || head_num <= 0 || head_size <= 0) return KL_EINVAL;
-  *bytes = head_size == 128 ? static_cast<size_t>(kPrefillMaxParts) * head_num *
-                                  ((n_pos + kPrefillQB - 1) / kPrefillQB) * kPrefillQB *
-                                  attn_prefill_part_floats(head_size) * sizeof(float)
-                            : 0;
+  *bytes = head_size == 64 || head_size == 128 ? attn_prefill_fa_ws_bytes(head_size) : 0;
   return KL_OK;
 }
 
@@ -1092,21 +1081,25 @@ int kl_attn_prefill_ws(int pos0, int n_pos, int head_num, int kv_mul, int head_s
                        void* stream) {
   size_t need = 0;
   if (kl_attn_prefill_workspace_size(n_pos, head_num, head_size, &need) != KL_OK) return KL_EINVAL;
-  if (need == 0 || attn_prefill_parts(pos0, n_pos, head_num) == 1)
+  if (need == 0 || pos0 < 0 || attn_prefill_workers(pos0, n_pos, head_num) == 0)
     return kl_attn_prefill(pos0, n_pos, head_num, kv_mul, head_size, q, ldq, key_cache,
                            value_cache, kv_dim, out, ldo, stream);
   if (!workspace || workspace_bytes < need) return KL_EWORKSPACE;
   if (!aligned16(workspace)) return KL_EUNSUPP;
-  if (!q || !key_cache || !value_cache || !out || pos0 < 0 || n_pos > 65535 * 64 || kv_mul <= 0 ||
+  if (!q || !key_cache || !value_cache || !out || n_pos > 65535 * 64 || kv_mul <= 0 ||
       head_num % kv_mul != 0 || kv_dim != head_num / kv_mul * head_size ||
       ldq < head_num * head_size || ldo < head_num * head_size)
     return KL_EINVAL;
   if (ldq % 4 || ldo % 4 || kv_dim % 4 || !aligned16(q) || !aligned16(out) ||
       !aligned16(key_cache) || !aligned16(value_cache))
     return KL_EUNSUPP;
-  return attn_prefill_launch<128>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out,
-                                  ldo, pos0, n_pos, as_stream(stream),
-                                  static_cast<float*>(workspace));
+  const hipStream_t st = as_stream(stream);
+  float* ws = static_cast<float*>(workspace);
+  return head_size == 64
+             ? attn_prefill_launch<64>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out,
+                                       ldo, pos0, n_pos, st, ws)
+             : attn_prefill_launch<128>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num,
+                                        out, ldo, pos0, n_pos, st, ws);
 }
 
 int kl_swiglu(const float* a, const float* b, float* out, int n, void* stream) {

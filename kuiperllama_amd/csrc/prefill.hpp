@@ -144,430 +144,369 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
   }
 }
 
-// The same attention on the matrix cores (head sizes 64 and 128):
-// flash-attention over key blocks of 64 with v_mfma_f32_32x32x2f32 (lane l
-// supplies A[l % 32][k = l / 32] and B[k = l / 32][l % 32]; result register r
-// of lane l is D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  Four waves per
-// 64 query rows of one head: wave (wm, wn) = (w % 2, w / 2) computes the
-// scores of rows 32 wm .. against keys 32 wn .. of the block (S = Q K^T, k
-// running over d), and the output of rows 32 wm .. for columns wn HD / 2 ..
-// (O += P V, k running over the 64 keys).  In both products lane half h takes
-// the k indices of its half of the range in order: a lane's Q row slice stays
-// in registers and its K and P operands are contiguous runs of a row in LDS;
-// the V operand of step s is one float of key row 32 h + s, read by the 32
-// lanes of a half as consecutive floats.  Only the row maxima cross waves
-// (through LDS); each wave keeps the partial row sums of its key half,
-// combined at the end.
-// Maximum / sum over the 32 lanes of each half wave, in every lane: DPP
-// within each 16-lane row (quad permutes and mirrors), then one exchange
-// between the two rows of the half.
-template <int CTRL>
-__device__ __forceinline__ float pf_dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float half_max(float v) {
-  v = fmaxf(v, pf_dpp<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, pf_dpp<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, pf_dpp<0x141>(v));  // row_half_mirror
-  v = fmaxf(v, pf_dpp<0x140>(v));  // row_mirror
-  return fmaxf(v, __shfl_xor(v, 16, 32));
-}
-__device__ __forceinline__ float half_sum(float v) {
-  v += pf_dpp<0xB1>(v);
-  v += pf_dpp<0x4E>(v);
-  v += pf_dpp<0x141>(v);
-  v += pf_dpp<0x140>(v);
-  return v + __shfl_xor(v, 16, 32);
-}
-
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restrict__ q, int ldq,
-                                                           const float* __restrict__ kc,
-                                                           const float* __restrict__ vc,
-                                                           int kv_dim, int kv_mul,
-                                                           float* __restrict__ out, int ldo,
-                                                           int pos0, int n, float scale) {
-  static_assert(HD == 64 || HD == 128, "head size");
-  typedef float f16v __attribute__((ext_vector_type(16)));
-  constexpr int QB = kPrefillQB, KB = kPrefillKB;
-  constexpr int LDK = HD + 4;  // K and V row (floats)
-  constexpr int LDP = KB + 4;  // P row
-  constexpr int HH = HD / 2;   // d per lane half (scores) and columns per wave (output)
-  constexpr int OT = HH / 32;  // 32 x 32 output tiles per wave
-  extern __shared__ __align__(16) float sm[];
-  float* Ks = sm;                 // [KB][LDK]
-  float* Vs = Ks + KB * LDK;      // [KB][LDK]
-  float* Ps = Vs + KB * LDK;      // [QB][LDP]
-  float* rmax = Ps + QB * LDP;    // [2][QB] per key half
-  float* rsum = rmax + 2 * QB;    // [2][QB]
-  const int h = blockIdx.y, g = h / kv_mul;
-  const int p0 = blockIdx.x * QB;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1, hl = lane >> 5, li = lane & 31;
-
-  // This lane's Q slice: row 32 wm + li, d in [HH hl, HH hl + HH).
-  pf4 qr[HH / 4];
-  {
-    const int p = p0 + 32 * wm + li;
-    const float* qp = q + static_cast<size_t>(p < n ? p : 0) * ldq + h * HD + HH * hl;
-#pragma unroll
-    for (int j = 0; j < HH / 4; ++j)
-      qr[j] = p < n ? *reinterpret_cast<const pf4*>(qp + 4 * j) : pf4{0.f, 0.f, 0.f, 0.f};
-  }
-  // Rows of this lane's accumulator registers: 32 wm + 8 (r / 4) + 4 hl + r % 4.
-  float m[16], lsum[16];
-  f16v o[OT];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    m[r] = -INFINITY;
-    lsum[r] = 0.f;
-  }
-#pragma unroll
-  for (int t = 0; t < OT; ++t) o[t] = f16v{};
-  const int rows = n - p0 < QB ? n - p0 : QB;
-  const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
-  const int qbase = pos0 + p0 + 32 * wm + 4 * hl;
-  // K and V of the next key block are loaded into registers while the current
-  // block is multiplied.
-  constexpr int NL = KB * HD / 4 / 256;  // float4s of K (and of V) per thread
-  pf4 kpre[NL], vpre[NL];
-  auto kvload = [&](int j0) {
-#pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const int i = tid + 256 * t;
-      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-      const int j = j0 + r;
-      const size_t off = static_cast<size_t>(j <= last ? j : 0) * kv_dim + g * HD + c;
-      kpre[t] = *reinterpret_cast<const pf4*>(kc + off);
-      vpre[t] = *reinterpret_cast<const pf4*>(vc + off);
-    }
-  };
-  kvload(0);
-  for (int j0 = 0; j0 <= last; j0 += KB) {
-    __syncthreads();  // the previous block's K, V and P are consumed
-#pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const int i = tid + 256 * t;
-      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-      const bool live = j0 + r <= last;
-      *reinterpret_cast<pf4*>(Ks + r * LDK + c) = live ? kpre[t] : pf4{0.f, 0.f, 0.f, 0.f};
-      *reinterpret_cast<pf4*>(Vs + r * LDK + c) = live ? vpre[t] : pf4{0.f, 0.f, 0.f, 0.f};
-    }
-    if (j0 + KB <= last) kvload(j0 + KB);
-    __syncthreads();
-    // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
-    f16v sacc = f16v{};
-    {
-      const float* kp = Ks + (32 * wn + li) * LDK + HH * hl;
-#pragma unroll
-      for (int j = 0; j < HH / 4; ++j) {
-        const pf4 kv = *reinterpret_cast<const pf4*>(kp + 4 * j);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].x, kv.x, sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].y, kv.y, sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].z, kv.z, sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].w, kv.w, sacc, 0, 0, 0);
-      }
-    }
-    // Scale, causal mask, and the row maxima over this wave's 32 keys.
-    const int kpos = j0 + 32 * wn + li;
-    float sv[16], mx[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qpos = qbase + 8 * (r >> 2) + (r & 3);
-      sv[r] = kpos <= qpos ? sacc[r] * scale : -INFINITY;
-      mx[r] = half_max(sv[r]);
-    }
-    if (li == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) rmax[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = mx[r];
-    }
-    __syncthreads();
-    float alpha[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
-      const float mn = fmaxf(m[r], fmaxf(mx[r], rmax[(1 - wn) * QB + row]));
-      // A row whose keys so far are all masked (only in a part after the
-      // first) keeps m = -inf, p = 0 and o = 0.
-      alpha[r] = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
-      m[r] = mn;
-      const float pv = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mn);
-      Ps[row * LDP + 32 * wn + li] = pv;
-      lsum[r] = lsum[r] * alpha[r] + half_sum(pv);
-    }
-    __syncthreads();
-    // O = O alpha + P V for rows 32 wm .., columns wn HH + 32 t ...
-#pragma unroll
-    for (int t = 0; t < OT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= alpha[r];
-    {
-      const float* pp = Ps + (32 * wm + li) * LDP + 32 * hl;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const pf4 pv = *reinterpret_cast<const pf4*>(pp + 4 * j);
-#pragma unroll
-        for (int t = 0; t < OT; ++t) {
-          const float* vp = Vs + (32 * hl + 4 * j) * LDK + wn * HH + 32 * t + li;
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.x, vp[0], o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.y, vp[LDK], o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.z, vp[2 * LDK], o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.w, vp[3 * LDK], o[t], 0, 0, 0);
-        }
-      }
-    }
-  }
-  // Row sums: this wave's key half plus the other's.
-  if (li == 0) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) rsum[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = lsum[r];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
-    const int p = p0 + row;
-    if (p < n) {
-      const float l = lsum[r] + rsum[(1 - wn) * QB + row];
-      float* op = out + static_cast<size_t>(p) * ldo + h * HD + wn * HH + li;
-#pragma unroll
-      for (int t = 0; t < OT; ++t) op[32 * t] = o[t][r] / l;
-    }
-  }
-}
-
-// Head size 128 with eight waves per workgroup, two per SIMD, so that one
-// wave's LDS reads, softmax and barriers overlap the other's matrix-core work
-// (the four-wave kernel above leaves one wave per SIMD: 311 VGPRs + AGPRs).
-// Key blocks of 128; wave (wm, wn) = (w % 2, w / 2) computes the scores of
-// rows 32 wm .. against keys 32 wn .. of the block (k over d; its Q row slice
-// in registers as above) and the output of rows 32 wm .. for columns 32 wn ..
-// (k over the block's 128 keys: lane half h takes keys 64 h .. 64 h + 63).
-// K and V of a block share one LDS buffer: K while the scores are computed,
-// then V, loaded into registers during the scores.  The next block's K is
-// loaded into registers during the current block.  Row maxima and sums cross
-// the four key quarters through LDS and are combined in a fixed order.
+// Head sizes 64 and 128 on the matrix cores: FlashAttention-2 style on
+// v_mfma_f32_16x16x4f32 with no exchange between waves inside a key block.
+// A workgroup of eight waves takes 64 query rows of one head and walks key
+// blocks of 64: wave w computes for query rows 16 (w % 4) .. + 15 and the
+// keys of half w / 4 of every block, two waves per SIMD; the two halves'
+// running (max, sum, output) merge once at the end.  Each wave computes
+// S^T = K Q^T and O^T += V^T P^T, so that in the 16 x 16 accumulator layout
+// (register r of lane l holds row 4 (l / 16) + r, column l % 16) every score
+// and every output value a lane holds belongs to query l % 16: the row
+// maximum and sum need only the lane's 8 scores of a block and two lane
+// exchanges (xor 16, 32), and the rescaling of O and the P operand of O^T stay
+// in registers (P^T's accumulator register r of a 16-key sub-block is the B
+// operand of step r, key 4 (l / 16) + r of the sub-block).  Lane group
+// g = l / 16 takes d columns HD/4 g .. of the scores' k dimension (its Q row
+// slice in registers), in two halves with their own accumulators so that
+// consecutive MFMAs are independent.  Row i of O^T block b is
+// d = 64 (b / 4) + 4 i + b % 4: the A operand of step r for blocks
+// 4 hb .. 4 hb + 3 is then one 16-byte read of V row (key) 4 (l / 16) + r at
+// d = 64 hb + 4 (l % 16), and a lane ends holding 16 consecutive output
+// columns 64 hb + 16 (l / 16) .. of its query.
 //
-// Key-range split (nparts > 1, blockIdx.z = part): where a chunk of rows far
-// into the context gives fewer (row block, head) workgroups than the device
-// has CUs, each one's key blocks are cut into nparts contiguous ranges, one
-// workgroup each; a workgroup then writes its rows' unnormalised output with
-// their running maximum and sum to `part` (an empty range writes max -inf,
-// sum 0), and k_attn_prefill_merge8 combines the parts in order.
-constexpr int kPrefillKB8 = 128;
+// K and V are both staged row-major [key][d] by direct-to-LDS loads (no
+// register staging), unpadded, 16-byte chunk c of row r at slot c ^ (r & 15):
+// the 16 lanes of a K read (16 rows, one chunk) and of a V read (one row, 16
+// chunks) hit distinct banks.  K of the next block is requested as soon as
+// every wave has its scores, V of a block once every wave is done with the
+// previous one; two barriers per key block.  Scores are kept in base 2
+// (scale log2 e) for the native exponential.
+//
+// Work decomposition.  A unit is one (head h, 64-row block i, 64-key block
+// kb) triple; the units of row block i of head h form segment h nqb + i (key
+// blocks 0 .. (last position of the row block) / 64).  Without a workspace,
+// workgroup s takes segment s whole.  With one (stream-K), G workgroups take
+// equal contiguous ranges [w W / G, (w + 1) W / G) of the W units in segment
+// order, so every CU walks the same number of key blocks however unequal the
+// causal segments are.  A segment cut by a range boundary leaves one partial
+// record per piece (unnormalised output row, natural-log max, sum; slot 0 for
+// the piece that starts the workgroup's range, slot 1 for the one that ends
+// it), combined in key order by k_attn_prefill_merge; a piece whose keys all
+// come after a row's position leaves that row max -inf, sum 0.
+constexpr int kFaKB = 64;          // keys per block
+constexpr int kFaMaxWorkers = 256; // stream-K workgroups (one per CU of an MI355X)
+static_assert(kFaKB == kPrefillQB, "row blocks and key blocks share the 64 grid");
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
 
 // One partial record per query row: HD output floats, then max and sum,
 // padded to a multiple of 4 floats so that every record (and every float4
 // column group the merge reads) starts 16-byte aligned.
 __host__ __device__ constexpr size_t attn_prefill_part_floats(int hd) { return hd + 4; }
 
-template <int HD>
-__global__ __launch_bounds__(512) void k_attn_prefill_mfma8(const float* __restrict__ q, int ldq,
-                                                            const float* __restrict__ kc,
-                                                            const float* __restrict__ vc,
-                                                            int kv_dim, int kv_mul,
-                                                            float* __restrict__ out, int ldo,
-                                                            int pos0, int n, float scale,
-                                                            int nparts, float* __restrict__ part) {
-  static_assert(HD == 128, "head size");
-  typedef float f16v __attribute__((ext_vector_type(16)));
-  constexpr int QB = kPrefillQB, KB = kPrefillKB8;
-  constexpr int LDK = HD + 4;  // K / V row (floats)
-  constexpr int LDP = KB + 4;  // P row
-  constexpr int HH = HD / 2;   // d per lane half (scores)
-  constexpr int KH = KB / 2;   // keys per lane half (output)
-  constexpr int NT = 512;
-  extern __shared__ __align__(16) float sm[];
-  float* KVs = sm;              // [KB][LDK]: the block's K, then its V
-  float* Ps = KVs + KB * LDK;   // [QB][LDP]
-  float* rmax = Ps + QB * LDP;  // [4][QB] per key quarter
-  float* rsum = rmax + 4 * QB;  // [4][QB]
-  const int h = blockIdx.y, g = h / kv_mul;
-  const int p0 = blockIdx.x * QB;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1, hl = lane >> 5, li = lane & 31;
-
-  pf4 qr[HH / 4];  // Q row 32 wm + li, d in [HH hl, HH hl + HH)
-  {
-    const int p = p0 + 32 * wm + li;
-    const float* qp = q + static_cast<size_t>(p < n ? p : 0) * ldq + h * HD + HH * hl;
-#pragma unroll
-    for (int j = 0; j < HH / 4; ++j)
-      qr[j] = p < n ? *reinterpret_cast<const pf4*>(qp + 4 * j) : pf4{0.f, 0.f, 0.f, 0.f};
-  }
-  // Rows of this lane's accumulator registers: 32 wm + 8 (r / 4) + 4 hl + r % 4.
-  float m[16], lsum[16];
-  f16v o = f16v{};
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    m[r] = -INFINITY;
-    lsum[r] = 0.f;
-  }
-  const int rows = n - p0 < QB ? n - p0 : QB;
-  const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
-  const int qbase = pos0 + p0 + 32 * wm + 4 * hl;
-  // This workgroup's key blocks [kb0, kb1): all of them, or part blockIdx.z.
-  const int nkb = last / KB + 1;
-  const int kb0 = static_cast<int>(blockIdx.z) * nkb / nparts;
-  const int kb1 = (static_cast<int>(blockIdx.z) + 1) * nkb / nparts;
-  constexpr int NL = KB * HD / 4 / NT;  // float4s of K (and of V) per thread
-  pf4 kpre[NL], vcur[NL];
-  auto load = [&](const float* base, int j0, pf4* dst) {
-#pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const int i = tid + NT * t;
-      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-      const int j = j0 + r;
-      dst[t] = *reinterpret_cast<const pf4*>(base + static_cast<size_t>(j <= last ? j : 0) * kv_dim +
-                                             g * HD + c);
-    }
-  };
-  auto stage = [&](int j0, const pf4* src) {  // rows past `last` as zeros
-#pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const int i = tid + NT * t;
-      const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-      *reinterpret_cast<pf4*>(KVs + r * LDK + c) = j0 + r <= last ? src[t] : pf4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  const int jend = kb1 * KB;  // one past the last key of this workgroup's range
-  if (kb0 < kb1) load(kc, kb0 * KB, kpre);
-  for (int j0 = kb0 * KB; j0 < jend; j0 += KB) {
-    __syncthreads();  // the previous block's V and P are consumed
-    stage(j0, kpre);
-    load(vc, j0, vcur);                          // this block's V, used after the scores
-    if (j0 + KB < jend) load(kc, j0 + KB, kpre);  // the next block's K
-    __syncthreads();
-    // S = Q K^T for rows 32 wm .., keys 32 wn .. of the block.
-    f16v sacc = f16v{};
-    {
-      const float* kp = KVs + (32 * wn + li) * LDK + HH * hl;
-#pragma unroll
-      for (int j = 0; j < HH / 4; ++j) {
-        const pf4 kv = *reinterpret_cast<const pf4*>(kp + 4 * j);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].x, kv.x, sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].y, kv.y, sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].z, kv.z, sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qr[j].w, kv.w, sacc, 0, 0, 0);
-      }
-    }
-    // Scale, causal mask, and the row maxima over this wave's 32 keys.
-    const int kpos = j0 + 32 * wn + li;
-    float sv[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qpos = qbase + 8 * (r >> 2) + (r & 3);
-      sv[r] = kpos <= qpos ? sacc[r] * scale : -INFINITY;
-      const float mx = half_max(sv[r]);
-      if (li == 0) rmax[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = mx;
-    }
-    __syncthreads();  // every wave's scores are done (K is dead) and its maxima visible
-    stage(j0, vcur);
-    float alpha[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
-      const float mn = fmaxf(fmaxf(m[r], fmaxf(rmax[row], rmax[QB + row])),
-                             fmaxf(rmax[2 * QB + row], rmax[3 * QB + row]));
-      // Key 0 is in the first block for every row, so mn is finite from then on.
-      alpha[r] = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
-      m[r] = mn;
-      const float pv = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mn);
-      Ps[row * LDP + 32 * wn + li] = pv;
-      lsum[r] = lsum[r] * alpha[r] + half_sum(pv);
-    }
-    __syncthreads();  // P and V are in LDS
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[r] *= alpha[r];
-    // O = O alpha + P V for rows 32 wm .., columns 32 wn ...
-    {
-      const float* pp = Ps + (32 * wm + li) * LDP + KH * hl;
-      const float* vb = KVs + KH * hl * LDK + 32 * wn + li;
-#pragma unroll
-      for (int j = 0; j < KH / 4; ++j) {
-        const pf4 pv = *reinterpret_cast<const pf4*>(pp + 4 * j);
-        const float* vp = vb + 4 * j * LDK;
-        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.x, vp[0], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.y, vp[LDK], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.z, vp[2 * LDK], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_32x32x2f32(pv.w, vp[3 * LDK], o, 0, 0, 0);
-      }
-    }
-  }
-  // Row sums: the four key quarters, in a fixed order.
-  if (li == 0) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) rsum[wn * QB + 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3)] = lsum[r];
-  }
-  __syncthreads();
-  float* rec = nparts > 1 ? part + ((static_cast<size_t>(blockIdx.z) * gridDim.y + h) * gridDim.x +
-                                    blockIdx.x) * QB * attn_prefill_part_floats(HD)
-                          : nullptr;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = 32 * wm + 8 * (r >> 2) + 4 * hl + (r & 3);
-    const int p = p0 + row;
-    if (p < n) {
-      const float l = ((rsum[row] + rsum[QB + row]) + rsum[2 * QB + row]) + rsum[3 * QB + row];
-      if (rec) {
-        float* rp = rec + static_cast<size_t>(row) * attn_prefill_part_floats(HD);
-        rp[32 * wn + li] = o[r];
-        if (wn == 0 && li == 0) {
-          rp[HD] = m[r];
-          rp[HD + 1] = l;
-        }
-      } else {
-        out[static_cast<size_t>(p) * ldo + h * HD + 32 * wn + li] = o[r] / l;
-      }
-    }
-  }
+__host__ __device__ constexpr size_t attn_prefill_fa_lds_bytes(int hd) {
+  return 2 * static_cast<size_t>(kFaKB) * hd * sizeof(float);
 }
 
-// Combines the nparts partial records of every row (grid: row blocks x
-// heads, 256 threads): o = sum_i w_i o_i / sum_i w_i l_i with
-// w_i = exp(m_i - max_j m_j), parts in order.  The part holding key 0 has a
-// finite maximum for every row, so the overall one is finite; a part whose
-// keys are all masked for a row (or that has no keys) has m_i = -inf and
-// w_i = 0.
+// Stream-K workspace: two record slots of 64 rows per workgroup.
+__host__ __device__ constexpr size_t attn_prefill_fa_ws_bytes(int hd) {
+  return 2 * static_cast<size_t>(kFaMaxWorkers) * kPrefillQB * attn_prefill_part_floats(hd) *
+         sizeof(float);
+}
+
+// Unit geometry of a launch over query positions pos0 .. pos0 + n - 1.
+struct FaGeom {
+  int nqb;        // 64-row blocks
+  int a;          // key blocks of row block 0; row block i < nqb - 1 has a + i
+  int nk_last;    // key blocks of the last row block
+  long long wh;   // units per head
+};
+__host__ __device__ inline long long fa_seg_start(const FaGeom& g, long long i) {
+  return i * g.a + i * (i - 1) / 2;
+}
+__host__ __device__ inline int fa_seg_len(const FaGeom& g, int i) {
+  return i < g.nqb - 1 ? g.a + i : g.nk_last;
+}
+__host__ __device__ inline FaGeom fa_geom(int pos0, int n) {
+  FaGeom g;
+  g.nqb = (n + kPrefillQB - 1) / kPrefillQB;
+  g.a = (pos0 + kPrefillQB - 1) / kFaKB + 1;
+  g.nk_last = (pos0 + n - 1) / kFaKB + 1;
+  g.wh = fa_seg_start(g, g.nqb - 1) + g.nk_last;
+  return g;
+}
+// Row block of the segment holding unit r (0 <= r < wh) of a head: the
+// largest i < nqb with fa_seg_start(i) <= r (a root estimate, then exact).
+__device__ inline int fa_locate(const FaGeom& g, long long r) {
+  const double b = g.a - 0.5;
+  long long i = static_cast<long long>(sqrt(b * b + 2.0 * static_cast<double>(r)) - b);
+  i = i < 0 ? 0 : (i > g.nqb - 1 ? g.nqb - 1 : i);
+  while (i > 0 && fa_seg_start(g, i) > r) --i;
+  while (i < g.nqb - 1 && fa_seg_start(g, i + 1) <= r) ++i;
+  return static_cast<int>(i);
+}
+// Workgroup whose range holds unit u (W units over G workgroups).
+__host__ __device__ inline long long fa_worker(long long u, long long W, long long G) {
+  return ((u + 1) * G - 1) / W;
+}
+
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prefill_merge8(const float* __restrict__ part,
-                                                             float* __restrict__ out, int ldo,
-                                                             int n, int nparts) {
-  const int p0 = blockIdx.x * kPrefillQB, h = blockIdx.y;
+__global__ __launch_bounds__(512) void k_attn_prefill_fa(const float* __restrict__ q, int ldq,
+                                                         const float* __restrict__ kc,
+                                                         const float* __restrict__ vc, int kv_dim,
+                                                         int kv_mul, float* __restrict__ out,
+                                                         int ldo, int pos0, int n, float scale,
+                                                         int heads, float* __restrict__ part) {
+  static_assert(HD == 64 || HD == 128, "head size");
+  constexpr int QB = kPrefillQB, KB = kFaKB, NT = 512;
+  constexpr int DG = HD / 4;       // d columns per lane group (scores)
+  constexpr int DC = DG / 4;       // their float4 chunks
+  constexpr int NB = HD / 16;      // 16-row blocks of O^T
+  constexpr int NH = HD / 64;      // 64-column groups of a V row
+  constexpr int C4 = HD / 4;       // 16-byte chunks per K / V row
+  constexpr int LI = KB * C4 / NT; // 1 KB direct-to-LDS loads per wave and operand
+  constexpr int LDO = HD + 4;      // merge record row: o[HD], m, l
   constexpr size_t RF = attn_prefill_part_floats(HD);
-  const size_t stride = static_cast<size_t>(gridDim.y) * gridDim.x * kPrefillQB * RF;
-  const float* r0 = part + (static_cast<size_t>(h) * gridDim.x + blockIdx.x) * kPrefillQB * RF;
-  constexpr int C4 = HD / 4;  // float4 columns per row
-  for (int i = threadIdx.x; i < kPrefillQB * C4; i += 256) {
-    const int row = i / C4, c = 4 * (i % C4);
-    const int p = p0 + row;
-    if (p >= n) continue;
-    const float* a = r0 + row * RF;
-    float mm = -INFINITY;
-    for (int k = 0; k < nparts; ++k) mm = fmaxf(mm, a[k * stride + HD]);
-    float l = 0.f;
-    pf4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < nparts; ++k) {
-      const float* b = a + k * stride;
-      const float mk = b[HD];
-      const float w = mk == -INFINITY ? 0.f : expf(mk - mm);
-      l += w * b[HD + 1];
-      o += w * *reinterpret_cast<const pf4*>(b + c);
+  static_assert(QB == 64 && KB == 64 && DC % 2 == 0 && KB * C4 % NT == 0, "tile");
+  static_assert(static_cast<size_t>(QB) * LDO <= 2 * static_cast<size_t>(KB) * HD,
+                "merge records fit the K/V buffers");
+  extern __shared__ __align__(1024) float sm[];
+  float* Ks = sm;            // [KB][HD], chunk c of row r at slot c ^ (r & 15)
+  float* Vs = sm + KB * HD;  // same layout
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = wave & 3, kh = wave >> 2;  // query group, key half
+  const int lg = lane >> 4, l16 = lane & 15;
+  const FaGeom geo = fa_geom(pos0, n);
+  // This workgroup's unit range [u0, u1) and the segment (h, i) holding u0.
+  long long u0, u1;
+  int h, i;
+  if (part) {
+    const long long W = geo.wh * heads, G = gridDim.x;
+    u0 = blockIdx.x * W / G;
+    u1 = (blockIdx.x + 1) * W / G;
+    h = static_cast<int>(u0 / geo.wh);
+    i = fa_locate(geo, u0 - h * geo.wh);
+  } else {
+    h = static_cast<int>(blockIdx.x) / geo.nqb;
+    i = static_cast<int>(blockIdx.x) % geo.nqb;
+    u0 = h * geo.wh + fa_seg_start(geo, i);
+    u1 = u0 + fa_seg_len(geo, i);
+  }
+  long long seg = h * geo.wh + fa_seg_start(geo, i);  // first unit of segment (h, i)
+  // Direct-to-LDS load u of this wave fills tile chunks 64 (LI wave + u) + lane:
+  // row r = that / C4, slot s = that % C4, which holds chunk s ^ (r & 15).
+  int drow[LI], dofs[LI];
+#pragma unroll
+  for (int u = 0; u < LI; ++u) {
+    const int P = 64 * (LI * wave + u) + lane;
+    const int r = P / C4, s = P % C4;
+    drow[u] = r;
+    dofs[u] = 4 * (s ^ (r & 15));
+  }
+  const float scale2 = scale * 1.44269504088896340736f;
+  for (long long u = u0; u < u1;) {
+    const int len = fa_seg_len(geo, i);
+    const long long e = u1 < seg + len ? u1 : seg + len;
+    const int kbA = static_cast<int>(u - seg), kbB = static_cast<int>(e - seg);
+    const int p0 = QB * i;
+    const int rows = n - p0 < QB ? n - p0 : QB;
+    const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
+    const float* kg = kc + (h / kv_mul) * HD;
+    const float* vg = vc + (h / kv_mul) * HD;
+    // Rows past `last` read row `last` (their scores are masked, p = 0).
+    auto request = [&](const float* src, float* dst, int j0) {
+#pragma unroll
+      for (int t = 0; t < LI; ++t) {
+        const int row = j0 + drow[t] <= last ? j0 + drow[t] : last;
+        __builtin_amdgcn_global_load_lds(
+            (global_void_t*)(src + static_cast<size_t>(row) * kv_dim + dofs[t]),
+            (lds_void_t*)(dst + 256 * (LI * wave + t)), 16, 0, 0);
+      }
+    };
+    __syncthreads();  // the previous piece's merge records are read
+    request(kg, Ks, kbA * KB);
+    const int qrow = p0 + 16 * qg + l16;  // this lane's query (rows past n: not stored)
+    const int qpos = pos0 + (qrow < n ? qrow : n - 1);
+    pf4 qr[DC];
+    {
+      const float* qp = q + static_cast<size_t>(qrow < n ? qrow : 0) * ldq + h * HD + DG * lg;
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+        qr[c] = qrow < n ? *reinterpret_cast<const pf4*>(qp + 4 * c) : pf4{0.f, 0.f, 0.f, 0.f};
     }
-    *reinterpret_cast<pf4*>(out + static_cast<size_t>(p) * ldo + h * HD + c) = o * (1.f / l);
+    float m = -INFINITY, l = 0.f;  // running maximum (base 2) and sum of this key half
+    pf4 oacc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) oacc[b] = pf4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = kbA; kb < kbB; ++kb) {
+      const int j0 = kb * KB;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // K of this block landed; V of the previous one consumed
+      request(vg, Vs, j0);
+      // S^T[key][query] for keys 16 (2 kh + k) + 4 lg + r of the block, the d
+      // range in two halves with their own accumulators.
+      pf4 sacc[2][2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) sacc[k][0] = sacc[k][1] = pf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c2 = 0; c2 < DC / 2; ++c2) {
+        pf4 kf[2][2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int dh = 0; dh < 2; ++dh) {
+            const int r = 16 * (2 * kh + k) + l16;
+            const int c = DC * lg + c2 + dh * DC / 2;
+            kf[k][dh] = *reinterpret_cast<const pf4*>(Ks + r * HD + 4 * (c ^ l16));
+          }
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4)
+#pragma unroll
+          for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+              sacc[k][dh] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                  kf[k][dh][e4], qr[c2 + dh * DC / 2][e4], sacc[k][dh], 0, 0, 0);
+      }
+      pf4 sc[2];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = j0 + 16 * (2 * kh + k) + 4 * lg + r;
+          const float v = sacc[k][0][r] + sacc[k][1][r];
+          sc[k][r] = key <= qpos ? v * scale2 : -INFINITY;
+          mx = fmaxf(mx, sc[k][r]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m, mx);
+      // A key half with no key at or before the row yet keeps max -inf, sum 0.
+      const float alpha = m == -INFINITY ? 0.f : exp2f(m - mn);
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = sc[k][r];
+          const float pv = v == -INFINITY ? 0.f : exp2f(v - mn);
+          sc[k][r] = pv;
+          sum += pv;
+        }
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      l = l * alpha + sum;
+      m = mn;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) oacc[b] *= alpha;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // V landed; every wave's K reads of this block done
+      if (kb + 1 < kbB) request(kg, Ks, j0 + KB);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int r = 16 * (2 * kh + k) + 4 * lg + r4;
+          pf4 vf[NH];
+#pragma unroll
+          for (int hb = 0; hb < NH; ++hb)
+            vf[hb] = *reinterpret_cast<const pf4*>(Vs + r * HD + 4 * ((16 * hb + l16) ^ (r & 15)));
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+            oacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[b / 4][b % 4], sc[k][r4], oacc[b], 0,
+                                                           0, 0);
+        }
+    }
+    // Output columns 64 hb + 16 lg + 4 r .. + 3 of this lane's query.
+    auto cols = [&](int hb, int r) {
+      return pf4{oacc[4 * hb][r], oacc[4 * hb + 1][r], oacc[4 * hb + 2][r], oacc[4 * hb + 3][r]};
+    };
+    // Merge the key halves: half 1 leaves (o, m, l) in LDS, half 0 combines.
+    __syncthreads();  // the last block's K and V are consumed
+    float* rec = sm + (16 * qg + l16) * LDO;
+    if (kh == 1) {
+#pragma unroll
+      for (int hb = 0; hb < NH; ++hb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<pf4*>(rec + 64 * hb + 16 * lg + 4 * r) = cols(hb, r);
+      if (lg == 0) {
+        rec[HD] = m;
+        rec[HD + 1] = l;
+      }
+    }
+    __syncthreads();
+    if (kh == 0 && qrow < n) {
+      const float m1 = rec[HD], l1 = rec[HD + 1];
+      const float mm = fmaxf(m, m1);
+      const float w0 = m == -INFINITY ? 0.f : exp2f(m - mm);
+      const float w1 = m1 == -INFINITY ? 0.f : exp2f(m1 - mm);
+      l = l * w0 + l1 * w1;
+      const bool whole = kbA == 0 && kbB == len;
+      float* dst;
+      if (whole) {
+        dst = out + static_cast<size_t>(qrow) * ldo + h * HD;
+      } else {
+        dst = part + ((2 * static_cast<size_t>(blockIdx.x) + (u == u0 ? 0 : 1)) * QB + (qrow - p0)) * RF;
+        if (lg == 0) {
+          dst[HD] = mm * 0.69314718055994530942f;  // natural units for the merge
+          dst[HD + 1] = l;
+        }
+      }
+#pragma unroll
+      for (int hb = 0; hb < NH; ++hb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 64 * hb + 16 * lg + 4 * r;
+          pf4 o = cols(hb, r) * w0 + *reinterpret_cast<const pf4*>(rec + d) * w1;
+          if (whole) o = o / l;
+          *reinterpret_cast<pf4*>(dst + d) = o;
+        }
+    }
+    u = e;
+    seg += len;
+    if (++i == geo.nqb) {
+      i = 0;
+      ++h;
+    }
   }
 }
 
-__host__ __device__ constexpr size_t attn_prefill_mfma8_lds_bytes(int hd) {
-  return (static_cast<size_t>(kPrefillKB8) * (hd + 4) +
-          static_cast<size_t>(kPrefillQB) * (kPrefillKB8 + 4) + 8 * kPrefillQB) *
-         sizeof(float);
-}
-
-__host__ __device__ constexpr size_t attn_prefill_mfma_lds_bytes(int hd) {
-  return (2 * static_cast<size_t>(kPrefillKB) * (hd + 4) +
-          static_cast<size_t>(kPrefillQB) * (kPrefillKB + 4) + 4 * kPrefillQB) *
-         sizeof(float);
+// Combines the pieces of every segment that stream-K cut: thread t of a
+// 256-thread workgroup takes float4 column t % (HD / 4) of one row (grid:
+// row groups x heads); o = sum_k w_k o_k / sum_k w_k l_k with
+// w_k = exp(m_k - max_j m_j) over the pieces in key order.  The piece holding
+// key 0 has a finite maximum for every row, so the overall one is finite; a
+// piece whose keys are all masked for a row has m_k = -inf and w_k = 0.
+// Segments left whole were written by the attention kernel.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ part,
+                                                            float* __restrict__ out, int ldo,
+                                                            int pos0, int n, int heads,
+                                                            int workers) {
+  constexpr int TPR = HD / 4, RPB = 256 / TPR, GPB = kPrefillQB / RPB;  // threads per row, rows per workgroup
+  constexpr size_t RF = attn_prefill_part_floats(HD);
+  const int i = blockIdx.x / GPB, h = blockIdx.y;
+  const int row = RPB * (blockIdx.x % GPB) + threadIdx.x / TPR, c = 4 * (threadIdx.x % TPR);
+  const FaGeom geo = fa_geom(pos0, n);
+  const long long W = geo.wh * heads, G = workers;
+  const long long s0 = h * geo.wh + fa_seg_start(geo, i), s1 = s0 + fa_seg_len(geo, i);
+  const long long wa = fa_worker(s0, W, G), wb = fa_worker(s1 - 1, W, G);
+  const int p = kPrefillQB * i + row;
+  if (wa == wb || p >= n) return;
+  // The first piece is slot 1 of its workgroup unless the segment starts that
+  // workgroup's range; every later piece starts its workgroup's range.
+  const int slot_a = s0 > wa * W / G ? 1 : 0;
+  const float* r0 = part + ((2 * static_cast<size_t>(wa) + slot_a) * kPrefillQB + row) * RF;
+  const float* r1 = part + (2 * static_cast<size_t>(wa + 1) * kPrefillQB + row) * RF;
+  const size_t step = 2 * kPrefillQB * RF;  // one workgroup's records
+  auto rec = [&](long long w) { return w == wa ? r0 : r1 + (w - wa - 1) * step; };
+  float mm = -INFINITY;
+  for (long long w = wa; w <= wb; ++w) mm = fmaxf(mm, rec(w)[HD]);
+  float l = 0.f;
+  pf4 o = {0.f, 0.f, 0.f, 0.f};
+  for (long long w = wa; w <= wb; ++w) {
+    const float* b = rec(w);
+    const float mk = b[HD];
+    const float wk = mk == -INFINITY ? 0.f : expf(mk - mm);
+    l += wk * b[HD + 1];
+    o += wk * *reinterpret_cast<const pf4*>(b + c);
+  }
+  *reinterpret_cast<pf4*>(out + static_cast<size_t>(p) * ldo + h * HD + c) = o * (1.f / l);
 }
 
 }  // namespace kl

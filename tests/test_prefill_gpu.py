@@ -202,15 +202,34 @@ def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
                                atol=1e-7)
 
 
+def _fa_workers(pos0, n, H, cus=256):
+    """Stream-K workgroups the launcher picks (0: one workgroup per segment):
+    a unit is one (head, 64-row block, 64-key block); row block i < nqb - 1
+    walks a + i key blocks, the last one (pos0 + n - 1) // 64 + 1."""
+    nqb, a, nk_last = (n + 63) // 64, (pos0 + 63) // 64 + 1, (pos0 + n - 1) // 64 + 1
+    m = nqb - 1
+    W = (m * a + m * (m - 1) // 2 + nk_last) * H
+    G = min(cus, 256, W)
+    plain = nk_last if nqb * H <= cus else -(-W // cus) + nk_last
+    return G if -(-W // G) < plain else 0
+
+
 @pytest.mark.parametrize("H,kvm,hd,S,pos0,n", [(4, 2, 128, 3200, 3000, 64), (12, 6, 128, 600, 0, 512),
                                               (12, 6, 128, 1100, 1000, 70), (8, 8, 128, 4096, 3968, 128),
-                                              (32, 4, 128, 520, 0, 512), (8, 2, 64, 300, 130, 70)])
+                                              (32, 4, 128, 520, 0, 512), (8, 2, 64, 300, 130, 70),
+                                              (6, 3, 128, 400, 30, 300), (2, 1, 128, 2100, 0, 2048),
+                                              (16, 4, 64, 700, 0, 640), (64, 8, 128, 64, 0, 16)])
 def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
-    """kl_attn_prefill_ws: with few (row block, head) pairs far into the
-    context (the first four cases) each row block's keys run in up to 4
-    parts merged afterwards; every row against the oracle's MHA and within
-    2e-5 of kl_attn_prefill.  32 heads x 8 row blocks fill the CUs (one part)
-    and head size 64 has no split: both the same as kl_attn_prefill."""
+    """kl_attn_prefill_ws: where the causal segments (64-row block, head) are
+    unequal or fewer than the CUs, equal ranges of (row block, key block)
+    units per workgroup, cut segments merged afterwards; a second launch on
+    the same workspace gives the same bits; rows against the
+    oracle's MHA and within 2e-5 of kl_attn_prefill (one workgroup per
+    segment).  Cases: one row block far into the context (48 pieces per
+    segment), ranges crossing segment boundaries (512 rows from position 0),
+    head size 64, a start off the 64 grid (pieces where a row's keys are all
+    masked), 2048 rows (long segments over many workgroups), and 16 rows x
+    64 heads (one unit per segment: no split)."""
     rng = np.random.default_rng(H * S + pos0 + n + 7)
     kvd = H // kvm * hd
     kc = rng.standard_normal((1, S, kvd)).astype(np.float32)
@@ -220,20 +239,27 @@ def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
     do, du = K.DeviceArray(n * H * hd), K.DeviceArray(n * H * hd)
     need = C.c_size_t(0)
     ok(K.lib.kl_attn_prefill_workspace_size(n, H, hd, C.byref(need)), "workspace size")
-    assert (need.value > 0) == (hd == 128)
-    ws = K.DeviceArray(max(1, need.value // 4))
+    assert need.value == 2 * 256 * 64 * (hd + 4) * 4
+    ws = K.DeviceArray(need.value // 4)
+    split = _fa_workers(pos0, n, H) > 0
+    assert split == ((H, n) != (64, 16))
     ok(K.lib.kl_attn_prefill_ws(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd, do.ptr,
                                 H * hd, ws.ptr, need.value, None), "kl_attn_prefill_ws")
     ok(K.lib.kl_attn_prefill(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd, du.ptr,
                              H * hd, None), "kl_attn_prefill")
     out = do.numpy().reshape(n, H * hd)
     whole = du.numpy().reshape(n, H * hd)
+    assert np.all(np.isfinite(out))
     assert np.max(np.abs(out - whole)) < 2e-5
-    if H * ((n + 63) // 64) < 256 and hd == 128 and pos0 > 0:
-        # split: a workspace short of one float is refused
+    # a second launch on the same (now dirty) workspace gives the same bits
+    ok(K.lib.kl_attn_prefill_ws(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd, du.ptr,
+                                H * hd, ws.ptr, need.value, None), "kl_attn_prefill_ws again")
+    assert np.array_equal(du.numpy().reshape(n, H * hd), out)
+    if split:  # a workspace short of one float is refused before any launch
         assert K.lib.kl_attn_prefill_ws(pos0, n, H, kvm, hd, dq.ptr, H * hd, dk.ptr, dv.ptr, kvd,
                                         do.ptr, H * hd, ws.ptr, need.value - 4, None) == -6
-    for r in range(n):
+    rows = range(n) if n <= 512 else sorted(set(np.linspace(0, n - 1, 96).astype(int)))
+    for r in rows:
         ref = O.mha(pos0 + r, H, 0, S, kvd, kvm, hd, q[r], kc, vc)
         assert np.max(np.abs(out[r] - ref)) < 2e-5, r
 
