@@ -472,7 +472,8 @@ struct kl_engine {
   char* pf_buf = nullptr;       // one allocation for everything below
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
   float *pf_h1 = nullptr, *pf_h3 = nullptr, *pf_xlast = nullptr;
-  float* pf_ws = nullptr;       // split-K partials [kPrefillMaxSplits][rows][dim]
+  float* pf_ws = nullptr;       // split-K partials (prefill_scratch sizes them)
+  size_t pf_ws_bytes = 0;
   void* pf_aws = nullptr;       // the attention's stream-K records
   size_t pf_aws_bytes = 0;
   int32_t* pf_tok = nullptr;    // [seq_len] prompt ids
@@ -885,7 +886,7 @@ int setup_persistent(kl_engine* e) {
     red_floats = std::max(red_floats, plan_phase(p, e->nwg, q8, m.gs, nb, share));
     max_cols = std::max(max_cols, p.cols);
   }
-  const int red_off = (max_cols + 3) & ~3;
+  const int red_off = ((q8 ? xpad(max_cols) : max_cols) + 3) & ~3;  // int8: padded input layout
   const int xres_off = red_off + static_cast<int>((red_floats + 3) & ~size_t(3));
   const int xres_floats = weighted ? share_d : (m.D + e->nwg - 1) / e->nwg;
   const size_t gemv_lds = (static_cast<size_t>(xres_off) + xres_floats) * sizeof(float);
@@ -1416,11 +1417,21 @@ namespace {
 constexpr int kPrefillChunk = 1024;  // rows per prefill pass
 constexpr int kPrefillMaxSplits = 4;
 
-// Split-K factor for a GEMM of rows x n outputs over k: enough workgroup
-// tiles (64 x 64) to fill the chip, each split keeping >= 32 k blocks.
-int prefill_splits(int rows, int n, int k) {
-  const long long tiles = static_cast<long long>((rows + 63) / 64) * ((n + 63) / 64);
+constexpr int kPrefillMaxSplitsQ8 = 16;  // int8 weights, at most 32 rows
+
+// Split-K factor for a GEMM launch of rows x n outputs (all of its outputs
+// together) over k.  fp32 weights / int8 over 32 rows: enough 64 x 64
+// workgroup tiles to fill the chip, each split keeping >= 32 k blocks.
+// int8 with at most 32 rows (32 x 128 tiles, one per 128 outputs): about
+// three tiles per CU, each split keeping >= 8 blocks of 32.
+int prefill_splits(int rows, int n, int k, bool q8) {
   int s = 1;
+  if (q8 && rows <= 32) {
+    const long long tiles = (n + 127) / 128;
+    while (s < kPrefillMaxSplitsQ8 && tiles * s < 768 && k / 32 / (2 * s) >= 8) s *= 2;
+    return s;
+  }
+  const long long tiles = static_cast<long long>((rows + 63) / 64) * ((n + 63) / 64);
   while (s < kPrefillMaxSplits && tiles * s < 1024 && k / 16 / (2 * s) >= 32) s *= 2;
   return s;
 }
@@ -1467,7 +1478,16 @@ int prefill_scratch(kl_engine* e, int rows) {
   size_t attn_ws = 0;
   r = kl_attn_prefill_workspace_size(rows, m.H, m.hd, &attn_ws);
   if (r != KL_OK) return r;
-  const size_t sz_ws = al(static_cast<size_t>(kPrefillMaxSplits) * R * m.D * 4);
+  // Split-K partials: up to kPrefillMaxSplits x rows x D (the WO and W2
+  // outputs), and for int8 prompts of at most 32 rows also the grouped QKV
+  // and W1/W3 outputs at up to kPrefillMaxSplitsQ8 splits.
+  size_t ws_floats = static_cast<size_t>(kPrefillMaxSplits) * R * m.D;
+  if (e->quant)
+    ws_floats = std::max(ws_floats, static_cast<size_t>(kPrefillMaxSplitsQ8) * std::min<size_t>(R, 32) *
+                                        std::max<size_t>({static_cast<size_t>(m.Dq) + 2 * m.Dkv,
+                                                          2 * static_cast<size_t>(m.F),
+                                                          static_cast<size_t>(m.D)}));
+  const size_t sz_ws = al(ws_floats * 4);
   const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(attn_ws) + al(m.D * 4) +
                        al(m.S * 4) + al(256) + al(am);
   char* buf = nullptr;
@@ -1488,6 +1508,7 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_h1 = reinterpret_cast<float*>(take(sz_h));
   e->pf_h3 = reinterpret_cast<float*>(take(sz_h));
   e->pf_ws = reinterpret_cast<float*>(take(sz_ws));
+  e->pf_ws_bytes = sz_ws;
   e->pf_aws = take(al(attn_ws));
   e->pf_aws_bytes = attn_ws;
   e->pf_xlast = reinterpret_cast<float*>(take(al(m.D * 4)));
@@ -1506,6 +1527,7 @@ int prefill_scratch(kl_engine* e, int rows) {
 int prefill_chunk(kl_engine* e, int pos0, int n) {
   const ImageLayout& m = e->lay;
   const int D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F, H = m.H, KVH = m.KVH, hd = m.hd;
+  const bool q8 = e->quant != 0;
   void* st = e->stream;
   const size_t kv_layer = static_cast<size_t>(m.S) * Dkv;
   int r = kl_embedding(e->pf_tok + pos0, n, e->emb, m.V, D, e->pf_x, nullptr, st);
@@ -1523,11 +1545,20 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
     // q, k and v in one grouped launch (k and v straight into the cache rows)
+    // Split-K where the launch would leave CUs idle (int8, at most 32 rows);
+    // every split's partials fit pf_ws (prefill_scratch).
+    auto splits_for = [&](int ntot, int k, bool grouped) {
+      const int sp = grouped && !(q8 && n <= 32) ? 1 : prefill_splits(n, ntot, k, q8);
+      if (r == KL_OK && static_cast<size_t>(sp) * n * ntot * sizeof(float) > e->pf_ws_bytes)
+        r = KL_EWORKSPACE;
+      return sp;
+    };
     {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
-      PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, nullptr, 1, hs));
+      const int sp = splits_for(Dq + 2 * Dkv, D, true);
+      PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, e->pf_ws, sp, hs));
     }
     if (e->transform == 2 && (hd == 64 || hd == 128)) {  // Qwen3 q/k RMSNorm (eps 1e-6) + RoPE
       PF(kl_qk_norm_rope_rows(e->rope_style, hd, H, KVH, e->pf_q, Dq, krow, Dkv, Ld.qn, Ld.kn, 1e-6f,
@@ -1543,11 +1574,9 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq,
                           e->pf_aws, e->pf_aws_bytes, st));
-    const size_t ws_bytes = static_cast<size_t>(kPrefillMaxSplits) * e->pf_rows * D * sizeof(float);
     {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
-      const int sp = prefill_splits(n, D, Dq);
-      if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
+      const int sp = splits_for(D, Dq, false);
       PF(gemm_run(e->pf_att, n, Dq, Dq, 1, &sg, 1, e->pf_ws, sp, hs));
     }
     // feed_forward (llama3.cpp:671-719)
@@ -1555,13 +1584,13 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     {
       const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
-      PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, nullptr, 1, hs));
+      const int sp = splits_for(2 * F, D, true);
+      PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, e->pf_ws, sp, hs));
     }
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
     {
       const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
-      const int sp = prefill_splits(n, D, F);
-      if (r == KL_OK && static_cast<size_t>(sp) * n * D * sizeof(float) > ws_bytes) r = KL_EWORKSPACE;
+      const int sp = splits_for(D, F, false);
       PF(gemm_run(e->pf_h1, n, F, F, 1, &sg, 1, e->pf_ws, sp, hs));
     }
   }

@@ -85,6 +85,7 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
   const float* bias = g.seg[0].bias;
   const float* S = g.seg[0].S;
   int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0, gshift = g.seg[0].gshift;
+  size_t wsoff = 0;
 #pragma unroll
   for (int i = 1; i < kGemmMaxSeg; ++i)
     if (i == sidx) {
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
       ldc = g.seg[i].ldc;
       tile0 = g.seg[i].tile0;
       gshift = g.seg[i].gshift;
+      wsoff = g.seg[i].wsoff;
     }
   const int M = g.M, K = g.K, lda = g.lda;
   // Tiles along M are adjacent in launch order, so the workgroups that share
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
   }
 
-  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * M * N : nullptr;
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -277,6 +279,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
   float* C = g.seg[0].C;
   const float* bias = g.seg[0].bias;
   int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0;
+  size_t wsoff = 0;
 #pragma unroll
   for (int i = 1; i < kGemmMaxSeg; ++i)
     if (i == sidx) {
@@ -287,6 +290,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
       ldw = g.seg[i].ldw;
       ldc = g.seg[i].ldc;
       tile0 = g.seg[i].tile0;
+      wsoff = g.seg[i].wsoff;
     }
   const int M = g.M, K = g.K, lda = g.lda;
   const int local = static_cast<int>(blockIdx.x) - tile0;
@@ -394,7 +398,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
     if (kt < kb1) block(kt, 0);
   }
 
-  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * M * N : nullptr;
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -417,19 +421,33 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
       }
 }
 
-// C = sum of the split partials in split order (+ bias) (+ C).
-__global__ void k_gemm_reduce(const float* __restrict__ ws, int splits, int M, int N,
-                              float* __restrict__ C, int ldc, const float* __restrict__ bias,
-                              int accumulate) {
-  const size_t total = static_cast<size_t>(M) * N;
+// C_s = sum of the split partials in split order (+ bias_s) (+ C_s), over
+// every output s of the launch: element i of a split's slab belongs to the
+// output whose [M][N_s] block (at seg[s].wsoff) holds it.
+__global__ void k_gemm_reduce(GemmArgs g) {
+  const size_t total = g.ws_split;
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
        i += static_cast<size_t>(gridDim.x) * blockDim.x) {
-    float v = ws[i];
-    for (int s = 1; s < splits; ++s) v += ws[static_cast<size_t>(s) * total + i];
-    const int m = static_cast<int>(i / N), n = static_cast<int>(i - static_cast<size_t>(m) * N);
+    float* C = g.seg[0].C;
+    const float* bias = g.seg[0].bias;
+    int N = g.seg[0].N, ldc = g.seg[0].ldc;
+    size_t off = 0;
+#pragma unroll
+    for (int k = 1; k < kGemmMaxSeg; ++k)
+      if (k < g.nseg && i >= g.seg[k].wsoff) {
+        C = g.seg[k].C;
+        bias = g.seg[k].bias;
+        N = g.seg[k].N;
+        ldc = g.seg[k].ldc;
+        off = g.seg[k].wsoff;
+      }
+    float v = g.ws[i];
+    for (int z = 1; z < g.splits; ++z) v += g.ws[static_cast<size_t>(z) * total + i];
+    const size_t local = i - off;
+    const int m = static_cast<int>(local / N), n = static_cast<int>(local - static_cast<size_t>(m) * N);
     if (bias) v += bias[n];
     float* cp = C + static_cast<size_t>(m) * ldc + n;
-    if (accumulate) v = *cp + v;
+    if (g.accumulate) v = *cp + v;
     *cp = v;
   }
 }

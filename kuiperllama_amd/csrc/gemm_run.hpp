@@ -19,6 +19,7 @@ struct GemmSeg {
   int tile0;         // first workgroup tile of this segment
   const float* S;    // int8 group scales (nullptr: fp32 weights)
   int gshift;        // int8 group size = 1 << gshift
+  size_t wsoff;      // split-K: this output's [M][N] partials within a split's slab
 };
 
 struct GemmArgs {
@@ -28,15 +29,18 @@ struct GemmArgs {
   int tiles_m;
   int nseg;
   GemmSeg seg[kGemmMaxSeg];
-  // Split-K (one segment only): blockIdx.y = split; the partial products go
-  // to ws[split][M][N] and k_gemm_reduce applies bias and accumulate.
+  // Split-K: blockIdx.y = split; the partial products of output s go to
+  // ws + split * ws_split + seg[s].wsoff ([M][N_s]) and k_gemm_reduce applies
+  // bias and accumulate.
   float* ws;
+  size_t ws_split;  // floats per split: M * (N_0 + N_1 + ...)
   int splits;
 };
 
 // Host launcher (ops.hip): C_s (+)= A . W_s^T (+ bias_s) for nseg outputs in
-// one grid; splits > 1 (nseg == 1) divides K among blockIdx.y into
-// ws[splits][M][N] and reduces.  Every segment is fp32 or every one int8.
+// one grid; splits > 1 divides K among blockIdx.y into ws (splits * M *
+// (N_0 + ...) floats) and reduces in split order.  Every segment is fp32 or
+// every one int8.
 int gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs, int accumulate,
              float* ws, int splits, hipStream_t st);
 

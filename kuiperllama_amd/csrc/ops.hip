@@ -870,7 +870,7 @@ bool gemm_shape_ok(const float* A, int M, int K, int lda) {
 int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs,
                  int accumulate, float* ws, int splits, hipStream_t st) {
   if (!gemm_shape_ok(A, M, K, lda) || nseg < 1 || nseg > kGemmMaxSeg || splits < 1 ||
-      (splits > 1 && (nseg != 1 || !ws)))
+      (splits > 1 && !ws))
     return KL_EINVAL;
   if (K % 4 || lda % 4 || !aligned16(A)) return KL_EUNSUPP;
   // The kernel addresses each operand with 32-bit byte offsets.
@@ -897,8 +897,12 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
   g.nseg = nseg;
   g.ws = ws;
   g.splits = splits;
-  g.tiles_m = (M + kGemmTile - 1) / kGemmTile;
+  // int8 weights with at most 32 rows: 32 x 128 tiles (no padded rows).
+  const bool small = q8 && M <= 32;
+  const int bm = small ? 32 : kGemmTile, bn = small ? 128 : kGemmTile;
+  g.tiles_m = (M + bm - 1) / bm;
   long long tiles = 0;
+  size_t wsoff = 0;
   for (int i = 0; i < nseg; ++i) {
     const GemmSeg& sg = segs[i];
     if (!q8) {
@@ -908,13 +912,19 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
     }
     g.seg[i] = sg;
     g.seg[i].tile0 = static_cast<int>(tiles);
-    tiles += static_cast<long long>(g.tiles_m) * ((sg.N + kGemmTile - 1) / kGemmTile);
+    g.seg[i].wsoff = wsoff;
+    tiles += static_cast<long long>(g.tiles_m) * ((sg.N + bn - 1) / bn);
+    wsoff += static_cast<size_t>(M) * sg.N;
   }
+  g.ws_split = wsoff;
   if (tiles > INT_MAX) return KL_EUNSUPP;
   // fp32 weights with K a whole number of 32-column blocks (every model
   // projection) stream through the direct-to-LDS kernel; int8 weights and
   // other K through the register-staged one.
-  if (q8)
+  if (small)
+    hipLaunchKernelGGL((k_gemm_f32<1, 4, 1, 1, true>), dim3(static_cast<unsigned>(tiles), splits),
+                       dim3(256), 0, st, g);
+  else if (q8)
     hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1, true>), dim3(static_cast<unsigned>(tiles), splits),
                        dim3(256), 0, st, g);
   else if (K % kGemmBK == 0)
@@ -924,11 +934,8 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
                        0, st, g);
   int r = launch_rc();
   if (r != KL_OK || splits == 1) return r;
-  const GemmSeg& sg = segs[0];
-  const size_t total = static_cast<size_t>(M) * sg.N;
-  const int grid = static_cast<int>(std::min<size_t>((total + 255) / 256, 4096));
-  hipLaunchKernelGGL(k_gemm_reduce, dim3(grid), dim3(256), 0, st, ws, splits, M, sg.N, sg.C, sg.ldc,
-                     sg.bias, accumulate);
+  const int grid = static_cast<int>(std::min<size_t>((g.ws_split + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_gemm_reduce, dim3(grid), dim3(256), 0, st, g);
   return launch_rc();
 }
 

@@ -321,6 +321,14 @@ __device__ __forceinline__ tagged2 g_ld_pair(__amdgpu_buffer_rsrc_t r, int pair)
 // after the staging (with the chunked attention and its merge hand-off the
 // same change had measured -1.5%).
 // Ends with a workgroup barrier.
+//
+// Layout in LDS: element i at i (fp32 weights: a lane reads 4 consecutive
+// elements, lanes 16 bytes apart) or, PAD (int8 weights: a lane reads the 16
+// elements of its 16 weights, lanes 64 bytes apart), at xpad(i) = i + 4 (i / 16):
+// the 16 lanes of a quarter-wave 16-byte read then start 80 bytes apart and
+// hit distinct banks.
+__host__ __device__ constexpr int xpad(int i) { return i + ((i >> 4) << 2); }
+template <bool PAD>
 __device__ __forceinline__ void stage_vec_single(const PArgs& a, const tagged_t* src,
                                                  unsigned int tag, const float* emb_row,
                                                  const float* nw, int n, float* xs, float* ssq) {
@@ -358,7 +366,7 @@ __device__ __forceinline__ void stage_vec_single(const PArgs& a, const tagged_t*
       if (i < n) {
         const float x = val_of(v[k]);
         ss += x * x;
-        xs[i] = nw ? (b0 == 0 ? wv[k] : g_rd(nw + i)) * x : x;
+        xs[PAD ? xpad(i) : i] = nw ? (b0 == 0 ? wv[k] : g_rd(nw + i)) * x : x;
       }
     }
   }
@@ -371,6 +379,7 @@ __device__ __forceinline__ void stage_vec_single(const PArgs& a, const tagged_t*
 
 // stage_vec_single with two adjacent elements per load (n even): each thread
 // takes 8 pairs per round, and a pair with a stale element is polled again.
+template <bool PAD>
 __device__ __forceinline__ void stage_vec_pairs(const PArgs& a, const tagged_t* src,
                                                 unsigned int tag, const float* emb_row,
                                                 const float* nw, int n, float* xs, float* ssq) {
@@ -435,7 +444,7 @@ __device__ __forceinline__ void stage_vec_pairs(const PArgs& a, const tagged_t* 
           const f2 w = b0 == 0 ? wv[k] : g_rd(reinterpret_cast<const f2*>(nw) + i);
           y = f2{w.x * x0, w.y * x1};
         }
-        reinterpret_cast<f2*>(xs)[i] = y;
+        *reinterpret_cast<f2*>(xs + (PAD ? xpad(2 * i) : 2 * i)) = y;  // one 16-group
       }
     }
   }
@@ -450,13 +459,14 @@ __device__ __forceinline__ void stage_vec_pairs(const PArgs& a, const tagged_t* 
 // round trips); narrower ones one element per load, which measured faster
 // for the 2048-wide inputs of Llama-3.2-1B and the 768-wide ones of
 // Llama2-110M (where each thread holds only a few elements).
+template <bool PAD>
 __device__ __forceinline__ void stage_vec(const PArgs& a, const tagged_t* src, unsigned int tag,
                                           const float* emb_row, const float* nw, int n, float* xs,
                                           float* ssq) {
   if (n >= a.stage_pair_min)
-    stage_vec_pairs(a, src, tag, emb_row, nw, n, xs, ssq);
+    stage_vec_pairs<PAD>(a, src, tag, emb_row, nw, n, xs, ssq);
   else
-    stage_vec_single(a, src, tag, emb_row, nw, n, xs, ssq);
+    stage_vec_single<PAD>(a, src, tag, emb_row, nw, n, xs, ssq);
 }
 
 // Lane-shifted copy of x through DPP (lanes without a source read 0).
@@ -737,7 +747,7 @@ __device__ __forceinline__ void p_seg_issue(PGp p, const PGeom& g, PCur& c,
 template <bool Q8>
 __device__ __forceinline__ float p_dot(const PChunk<Q8>& it, const float* xs, int u) {
   if constexpr (Q8) {
-    const f4* xc = reinterpret_cast<const f4*>(xs) + 4 * u;
+    const f4* xc = reinterpret_cast<const f4*>(xs + xpad(16 * u));  // the padded layout
     float q[16];
     unpack_i8x4(it.w.x, q);
     unpack_i8x4(it.w.y, q + 4);
@@ -1608,7 +1618,7 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       PCur c0{0, 0, 0};
       p_seg_issue<Q8, NB>(p, g, c0, A);
     }
-    stage_vec(a, p->in, tag_in, emb_row, p->norm, p->cols, xs, sred);
+    stage_vec<Q8>(a, p->in, tag_in, emb_row, p->norm, p->cols, xs, sred);
     trace_mark(a, slot++);
     // Classifier: claim the first dynamic block now; the answer is needed
     // only after the static rows.

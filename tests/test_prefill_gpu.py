@@ -379,11 +379,13 @@ def test_generate_with_prefill_matches_oracle(K, O, gpu, name):
 
 @pytest.mark.parametrize("M,N,Kd,gs,splits", [(1, 5, 64, 64, 1), (37, 200, 256, 64, 1),
                                               (100, 192, 1024, 64, 4), (64, 96, 128, 32, 2),
-                                              (7, 33, 4096, 128, 3)])
+                                              (7, 33, 4096, 128, 3), (32, 300, 512, 64, 8),
+                                              (32, 1024, 2048, 64, 16)])
 def test_gemm_q8_vs_oracle(K, O, gpu, M, N, Kd, gs, splits):
     """int8 weights (group-wise scales over the flattened matrix): every row of
     C within the fp32 GEMV bound of the oracle's int8 MatmulKernel on that
-    row, with bias and accumulate, with and without split-K."""
+    row, with bias and accumulate, with and without split-K; M <= 32 runs the
+    32 x 128 tiles (N = 300: a partial last tile)."""
     rng = np.random.default_rng(M * 7 + N)
     A = rng.standard_normal((M, Kd)).astype(np.float32)
     Wf = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
