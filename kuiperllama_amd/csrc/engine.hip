@@ -1549,7 +1549,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // every split's partials fit pf_ws (prefill_scratch).
     auto splits_for = [&](int ntot, int k, bool grouped) {
       const int sp = grouped && !(q8 && n <= 32) ? 1 : prefill_splits(n, ntot, k, q8);
-      if (r == KL_OK && static_cast<size_t>(sp) * n * ntot * sizeof(float) > e->pf_ws_bytes)
+      if (r == KL_OK && sp > 1 && static_cast<size_t>(sp) * n * ntot * sizeof(float) > e->pf_ws_bytes)
         r = KL_EWORKSPACE;
       return sp;
     };
