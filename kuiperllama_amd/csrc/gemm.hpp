@@ -8,8 +8,12 @@
 // Two kernels share the launch arguments (GemmArgs, gemm_run.hpp) and the
 // 64 x 64 workgroup tile of four waves:
 //
-// k_gemm_f32_dma (fp32 weights, K a multiple of 32; every model projection):
-// each wave owns 2 x 2 blocks of 16 x 16 accumulated with
+// k_gemm_f32_dma<TA> (fp32 weights, K a multiple of 32; every model
+// projection): a workgroup tile of 32 TA x 64 (TA = 2: 64 x 64, three
+// workgroups per CU; TA = 4: 128 x 64, two per CU, for launches with at least
+// 1024 such tiles, where halving the operand reads and barriers per MFMA pays
+// for the fewer resident waves: +6% on the cfg 5 W1/W3 shape, -5 to -13% on
+// the narrower ones); each wave owns TA x 2 blocks of 16 x 16 accumulated with
 // v_mfma_f32_16x16x4f32 (A operand: lane l holds A[l % 16][k], B operand
 // W[l % 16][k], k = l / 16; result register r of lane l is
 // C[4 (l / 16) + r][l % 16]).  K advances in blocks of 32 columns staged in
@@ -17,8 +21,8 @@
 // store instructions) through a 3-stage ring, block k + 2 requested while
 // block k is computed, one barrier per block.  A 1 KB load instruction of a
 // wave fills 8 rows of 128 B; chunk q (16 B) of row r sits in slot
-// q ^ (r & 7), which each lane gets by loading the chunk that belongs in its
-// slot, so the operand reads are conflict-free without padding.  Lane group
+// q ^ dma_swz(r), which each lane gets by loading the chunk that belongs in
+// its slot, so the operand reads are conflict-free without padding.  Lane group
 // g = l / 16 takes k columns 8 g .. 8 g + 7 of a block (two contiguous 16 B
 // reads per row; A and W use the same permutation, so every product
 // A[m][k] W[n][k] is formed exactly once).  The next block's operands are read
@@ -262,10 +266,24 @@ typedef __attribute__((address_space(1))) void global_void_t;
 
 constexpr int kDmaStages = 3;
 
+// Chunk swizzle of the direct-to-LDS tiles (rows of 128 B = 8 chunks of
+// 16 B; chunk q of row r sits in slot q ^ dma_swz(r)).  A 16-byte LDS read
+// is served half a wave at a time over 512 B of banks, i.e. the 32 lanes of
+// a half wave (16 consecutive rows, two chunks c and c ^ 2 each) must land in
+// 32 distinct 16-byte slots modulo 512 B: rows r, r + 4, r + 8, r + 12 share
+// their position within 512 B, so bits 0 and 2 of the swizzle must follow
+// r / 4 (bits 2 and 3 of r) and bit 1 may follow bit 1 of r.  r & 7 (the
+// plain XOR) leaves rows r and r + 8 on the same slots: 2-way conflicts on
+// every operand read (SQ_LDS_BANK_CONFLICT 1.05e9 -> 0 on the cfg 5 shapes).
+__device__ __forceinline__ int dma_swz(int r) { return ((r >> 2) & 1) | (r & 2) | ((r >> 1) & 4); }
+
+template <int TA>
 __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
-  constexpr int BM = 64, BN = 64, BK = 32;
+  static_assert(TA == 2 || TA == 4, "wave tile rows: 32 or 64");
+  constexpr int BM = 32 * TA, BN = 64, BK = 32;
   constexpr int SA = BM * BK, SW = BN * BK;   // floats per stage and operand
-  constexpr int LI = BM / 8 / 4;              // 1 KB load instructions per wave and operand
+  constexpr int LI = BM / 8 / 4;              // 1 KB load instructions per wave: A
+  constexpr int LW = BN / 8 / 4;              //   and W
   __shared__ __align__(1024) float L[kDmaStages * (SA + SW)];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -301,16 +319,19 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
   const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
 
   // Load instruction i of this wave fills tile rows 8 j .. 8 j + 7
-  // (j = LI * wave + i); lane l writes slot l % 8 of row 8 j + l / 8, which
-  // holds chunk (l % 8) ^ (l / 8).  Rows past M or N read the last row (they
-  // only feed outputs that are never stored).
-  const int rsub = lane >> 3, chunk = (lane & 7) ^ rsub;
-  unsigned int ga[LI], gw[LI];
+  // (j = LI * wave + i); lane l writes slot l % 8 of row r = 8 j + l / 8,
+  // which holds chunk (l % 8) ^ dma_swz(r).  Rows past M or N read the last
+  // row (they only feed outputs that are never stored).
+  unsigned int ga[LI], gw[LW];
 #pragma unroll
   for (int i = 0; i < LI; ++i) {
-    const int r = 8 * (LI * wave + i) + rsub;
-    ga[i] = static_cast<unsigned int>((min(m0 + r, M - 1) * lda + 4 * chunk) * 4);
-    gw[i] = static_cast<unsigned int>((min(n0 + r, N - 1) * ldw + 4 * chunk) * 4);
+    const int r = 8 * (LI * wave + i) + (lane >> 3);
+    ga[i] = static_cast<unsigned int>((min(m0 + r, M - 1) * lda + 4 * ((lane & 7) ^ dma_swz(r))) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < LW; ++i) {
+    const int r = 8 * (LW * wave + i) + (lane >> 3);
+    gw[i] = static_cast<unsigned int>((min(n0 + r, N - 1) * ldw + 4 * ((lane & 7) ^ dma_swz(r))) * 4);
   }
   auto request = [&](int kb, int st) {
     const char* ba = reinterpret_cast<const char*>(A) + static_cast<size_t>(kb) * BK * 4;
@@ -322,26 +343,26 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
       __builtin_amdgcn_global_load_lds((global_void_t*)(ba + ga[i]),
                                        (lds_void_t*)(la + 256 * (LI * wave + i)), 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < LI; ++i)
+    for (int i = 0; i < LW; ++i)
       __builtin_amdgcn_global_load_lds((global_void_t*)(bw + gw[i]),
-                                       (lds_void_t*)(lw + 256 * (LI * wave + i)), 16, 0, 0);
+                                       (lds_void_t*)(lw + 256 * (LW * wave + i)), 16, 0, 0);
   };
   // Operands: lane group g4 = l / 16 reads chunks 2 g4 and 2 g4 + 1 of rows
-  // 32 wm + 16 a + l % 16 (A) and 32 wn + 16 b + l % 16 (W).
+  // 16 TA wm + 16 a + l % 16 (A) and 32 wn + 16 b + l % 16 (W).
   const int g4 = lane >> 4, r16 = lane & 15;
-  const int rowa = 32 * wm + r16, rowb = 32 * wn + r16;
+  const int rowa = 16 * TA * wm + r16, rowb = 32 * wn + r16;
   int oa[2], ob[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    oa[j] = rowa * BK + 4 * ((2 * g4 + j) ^ (rowa & 7));
-    ob[j] = rowb * BK + 4 * ((2 * g4 + j) ^ (rowb & 7));
+    oa[j] = rowa * BK + 4 * ((2 * g4 + j) ^ dma_swz(rowa));
+    ob[j] = rowb * BK + 4 * ((2 * g4 + j) ^ dma_swz(rowb));
   }
-  gf4 af[2][2][2], bf[2][2][2];  // [register buffer][block][16-byte read]
+  gf4 af[2][TA][2], bf[2][2][2];  // [register buffer][block][16-byte read]
   auto operands = [&](int st, int p) {
     const float* la = L + st * (SA + SW);
     const float* lw = la + SA;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < TA; ++a)
 #pragma unroll
       for (int j = 0; j < 2; ++j) af[p][a][j] = *reinterpret_cast<const gf4*>(la + a * 16 * BK + oa[j]);
 #pragma unroll
@@ -349,22 +370,22 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) bf[p][b][j] = *reinterpret_cast<const gf4*>(lw + b * 16 * BK + ob[j]);
   };
-  gf4 acc[2][2];
+  gf4 acc[TA][2];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < TA; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = gf4{0.f, 0.f, 0.f, 0.f};
   auto steps = [&](int p, int s0, int s1) {
 #pragma unroll
     for (int s = s0; s < s1; ++s)
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < TA; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[p][a][s >> 2][s & 3], bf[p][b][s >> 2][s & 3],
                                                            acc[a][b], 0, 0, 0);
   };
-  constexpr int kLoads = 2 * LI;  // load instructions per block and wave
+  constexpr int kLoads = LI + LW;  // load instructions per block and wave
   if (kb0 < kb1) {
     // Blocks kb0 and kb0 + 1 in flight, block kb0 landed in every wave.
     request(kb0, 0);
@@ -400,12 +421,12 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
 
   float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < TA; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 32 * wm + 16 * a + 4 * g4 + r;
+        const int m = m0 + 16 * TA * wm + 16 * a + 4 * g4 + r;
         const int n = n0 + 32 * wn + 16 * b + r16;
         if (m < M && n < N) {
           float v = acc[a][b][r];

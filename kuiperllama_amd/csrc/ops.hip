@@ -898,8 +898,18 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
   g.ws = ws;
   g.splits = splits;
   // int8 weights with at most 32 rows: 32 x 128 tiles (no padded rows).
+  // fp32 through the direct-to-LDS kernel: 128 x 64 tiles where the launch
+  // has at least 1024 of them (two rounds of two workgroups per CU), else
+  // 64 x 64.
   const bool small = q8 && M <= 32;
-  const int bm = small ? 32 : kGemmTile, bn = small ? 128 : kGemmTile;
+  const bool dma = !q8 && K % kGemmBK == 0;
+  bool tall = false;
+  if (dma && M >= 128) {
+    long long t = 0;
+    for (int i = 0; i < nseg; ++i) t += static_cast<long long>((M + 127) / 128) * ((segs[i].N + 63) / 64);
+    tall = t >= 1024;
+  }
+  const int bm = small ? 32 : tall ? 128 : kGemmTile, bn = small ? 128 : kGemmTile;
   g.tiles_m = (M + bm - 1) / bm;
   long long tiles = 0;
   size_t wsoff = 0;
@@ -927,8 +937,10 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
   else if (q8)
     hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1, true>), dim3(static_cast<unsigned>(tiles), splits),
                        dim3(256), 0, st, g);
-  else if (K % kGemmBK == 0)
-    hipLaunchKernelGGL(k_gemm_f32_dma, dim3(static_cast<unsigned>(tiles), splits), dim3(256), 0, st, g);
+  else if (tall)
+    hipLaunchKernelGGL(k_gemm_f32_dma<4>, dim3(static_cast<unsigned>(tiles), splits), dim3(256), 0, st, g);
+  else if (dma)
+    hipLaunchKernelGGL(k_gemm_f32_dma<2>, dim3(static_cast<unsigned>(tiles), splits), dim3(256), 0, st, g);
   else
     hipLaunchKernelGGL((k_gemm_f32<2, 2, 1, 1>), dim3(static_cast<unsigned>(tiles), splits), dim3(256),
                        0, st, g);

@@ -166,9 +166,13 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 // columns 64 hb + 16 (l / 16) .. of its query.
 //
 // K and V are both staged row-major [key][d] by direct-to-LDS loads (no
-// register staging), unpadded, 16-byte chunk c of row r at slot c ^ (r & 15):
-// the 16 lanes of a K read (16 rows, one chunk) and of a V read (one row, 16
-// chunks) hit distinct banks.  K of the next block is requested as soon as
+// register staging), unpadded, 16-byte chunk c of row r at slot
+// c ^ fa_swz<HD>(r).  A 16-byte LDS read is served half a wave (32 lanes) at a
+// time over 512 B of banks; the swizzle puts the 32 lanes of a K read (16
+// consecutive rows, chunks c and c + HD/16) and of a V read (rows R and R + 4,
+// 16 consecutive chunks each) on distinct slots (head size 64: the K reads;
+// its V rows R and R + 4 share a 512-byte window whatever the swizzle).  K of
+// the next block is requested as soon as
 // every wave has its scores, V of a block once every wave is done with the
 // previous one; two barriers per key block.  Scores are kept in base 2
 // (scale log2 e) for the native exponential.
@@ -190,6 +194,16 @@ static_assert(kFaKB == kPrefillQB, "row blocks and key blocks share the 64 grid"
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
+
+// Chunk swizzle of the K/V tiles (see above).  Head size 128 (512-byte rows,
+// 32 chunks): bits 0, 1, 2, 4 = bits 0, 1, 3, 2 of r.  Head size 64 (256-byte
+// rows, 16 chunks): bits 0, 1, 2, 3 = bits 1, 2, 0, 3 of r.  Both depend on
+// r mod 16 only and are a bijection of the row's chunks.
+template <int HD>
+__host__ __device__ constexpr int fa_swz(int r) {
+  return HD == 128 ? (r & 3) | ((r >> 1) & 4) | ((r & 4) << 2)
+                   : ((r >> 1) & 3) | ((r & 1) << 2) | (r & 8);
+}
 
 // One partial record per query row: HD output floats, then max and sum,
 // padded to a multiple of 4 floats so that every record (and every float4
@@ -263,7 +277,7 @@ __global__ __launch_bounds__(512) void k_attn_prefill_fa(const float* __restrict
   static_assert(static_cast<size_t>(QB) * LDO <= 2 * static_cast<size_t>(KB) * HD,
                 "merge records fit the K/V buffers");
   extern __shared__ __align__(1024) float sm[];
-  float* Ks = sm;            // [KB][HD], chunk c of row r at slot c ^ (r & 15)
+  float* Ks = sm;            // [KB][HD], chunk c of row r at slot c ^ fa_swz<HD>(r)
   float* Vs = sm + KB * HD;  // same layout
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -287,15 +301,16 @@ __global__ __launch_bounds__(512) void k_attn_prefill_fa(const float* __restrict
   }
   long long seg = h * geo.wh + fa_seg_start(geo, i);  // first unit of segment (h, i)
   // Direct-to-LDS load u of this wave fills tile chunks 64 (LI wave + u) + lane:
-  // row r = that / C4, slot s = that % C4, which holds chunk s ^ (r & 15).
+  // row r = that / C4, slot s = that % C4, which holds chunk s ^ fa_swz(r).
   int drow[LI], dofs[LI];
 #pragma unroll
   for (int u = 0; u < LI; ++u) {
     const int P = 64 * (LI * wave + u) + lane;
     const int r = P / C4, s = P % C4;
     drow[u] = r;
-    dofs[u] = 4 * (s ^ (r & 15));
+    dofs[u] = 4 * (s ^ fa_swz<HD>(r));
   }
+  const int kswz = fa_swz<HD>(l16);  // the swizzle of every K row this lane reads
   const float scale2 = scale * 1.44269504088896340736f;
   for (long long u = u0; u < u1;) {
     const int len = fa_seg_len(geo, i);
@@ -350,7 +365,7 @@ __global__ __launch_bounds__(512) void k_attn_prefill_fa(const float* __restrict
           for (int dh = 0; dh < 2; ++dh) {
             const int r = 16 * (2 * kh + k) + l16;
             const int c = DC * lg + c2 + dh * DC / 2;
-            kf[k][dh] = *reinterpret_cast<const pf4*>(Ks + r * HD + 4 * (c ^ l16));
+            kf[k][dh] = *reinterpret_cast<const pf4*>(Ks + r * HD + 4 * (c ^ kswz));
           }
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4)
@@ -404,7 +419,7 @@ __global__ __launch_bounds__(512) void k_attn_prefill_fa(const float* __restrict
           pf4 vf[NH];
 #pragma unroll
           for (int hb = 0; hb < NH; ++hb)
-            vf[hb] = *reinterpret_cast<const pf4*>(Vs + r * HD + 4 * ((16 * hb + l16) ^ (r & 15)));
+            vf[hb] = *reinterpret_cast<const pf4*>(Vs + r * HD + 4 * ((16 * hb + l16) ^ fa_swz<HD>(r)));
 #pragma unroll
           for (int b = 0; b < NB; ++b)
             oacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[b / 4][b % 4], sc[k][r4], oacc[b], 0,

@@ -57,8 +57,12 @@ def test_gemm_kat_exact(K, O, gpu):
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 3, 4), (5, 37, 12), (64, 64, 64), (77, 300, 256),
                                     (512, 1024, 2560), (130, 2560, 4096), (512, 9728, 512),
-                                    (1000, 256, 1536), (33, 70, 100), (65, 129, 36)])
+                                    (1000, 256, 1536), (33, 70, 100), (65, 129, 36),
+                                    (512, 16384, 96), (300, 33000, 64)])
 def test_gemm_vs_oracle_rows(K, O, gpu, M, N, Kd):
+    """fp32 GEMM rows against the oracle's GEMV within the fp32 rounding bound.
+    (512, 16384) and (300, 33000) have at least 1024 tiles of 128 x 64 and
+    run the tall-tile kernel (the latter with partial tiles in both dims)."""
     rng = np.random.default_rng(M * 7 + N + Kd)
     A = rng.standard_normal((M, Kd)).astype(np.float32)
     W = (rng.standard_normal((N, Kd)) * 0.02).astype(np.float32)
