@@ -1439,7 +1439,7 @@ int prefill_splits(int rows, int n, int k, bool q8) {
 bool prefill_supported(const kl_engine* e) {
   const ImageLayout& m = e->lay;
   const int hd = m.hd;
-  if (hd != 32 && hd != 64 && hd != 128) return false;
+  if (hd != 32 && hd != 64 && hd != 128 && hd != 256) return false;
   // int8 GEMMs take whole 32-column blocks and groups of at least 4.
   if (e->quant && (m.D % kGemmBK || m.Dq % kGemmBK || m.F % kGemmBK || m.gs < 4 ||
                    (m.gs & (m.gs - 1))))

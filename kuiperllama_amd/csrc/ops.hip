@@ -1033,7 +1033,7 @@ template <int HD>
 int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
                         int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st,
                         float* part = nullptr) {
-  // Head sizes 64 and 128 on the matrix cores; 32 on the vector ALUs.
+  // Head sizes 64 and 128 on the matrix cores; 32 and 256 on the vector ALUs.
   constexpr bool kMfma = HD == 64 || HD == 128;
   const void* fn = kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_fa<kMfma ? HD : 64>)
                          : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
@@ -1084,6 +1084,7 @@ int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size
     case 32: return attn_prefill_launch<32>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
     case 64: return attn_prefill_launch<64>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
     case 128: return attn_prefill_launch<128>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
+    case 256: return attn_prefill_launch<256>(q, ldq, key_cache, value_cache, kv_dim, kv_mul, head_num, out, ldo, pos0, n_pos, st);
     default: return KL_EUNSUPP;
   }
 }

@@ -4,12 +4,13 @@
 // query positions pos0 .. pos0 + n - 1 at once, reading K and V rows 0 ..
 // pos0 + n - 1 of one layer's caches ([seq_len][kv_dim]).
 //
-// One workgroup (256 threads) owns 64 query rows of one head and walks the
-// key positions in blocks of 64 through LDS with an online softmax: thread
-// (rg, cg) = (tid / 16, tid % 16) scores rows 4 rg .. 4 rg + 3 against keys
-// 4 cg .. 4 cg + 3 of the block, the 16 threads of a row group combine the
-// row maxima and sums with lane shuffles, and the same thread accumulates
-// output columns cg * HD / 16 .. of its 4 rows.
+// VALU kernel (head sizes 32 and 256): one workgroup (256 threads) owns 64
+// query rows of one head and walks the key positions in blocks of KB (64; 32
+// for head size 256) through LDS with an online softmax: thread (rg, cg) =
+// (tid / 16, tid % 16) scores rows 4 rg .. 4 rg + 3 against keys
+// KB/16 cg .. of the block, the 16 threads of a row group combine the row
+// maxima and sums with lane shuffles, and the same thread accumulates output
+// columns cg * HD / 16 .. of its 4 rows.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -22,9 +23,13 @@ typedef float pf4 __attribute__((ext_vector_type(4)));
 constexpr int kPrefillQB = 64;  // query rows per workgroup
 constexpr int kPrefillKB = 64;  // key positions per block
 
+// Keys per block of the VALU kernel: 64, or 32 for head size 256 so that the
+// Q, K and V tiles fit the 160 KB of LDS (142 KB).
+__host__ __device__ constexpr int attn_prefill_kb(int hd) { return hd > 128 ? 32 : kPrefillKB; }
+
 __host__ __device__ constexpr size_t attn_prefill_lds_bytes(int hd) {
-  return (static_cast<size_t>(kPrefillQB + 2 * kPrefillKB) * (hd + 4) +
-          static_cast<size_t>(kPrefillQB) * (kPrefillKB + 4)) * sizeof(float);
+  return (static_cast<size_t>(kPrefillQB + 2 * attn_prefill_kb(hd)) * (hd + 4) +
+          static_cast<size_t>(kPrefillQB) * (attn_prefill_kb(hd) + 4)) * sizeof(float);
 }
 
 template <int HD>
@@ -33,7 +38,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                                                       const float* __restrict__ vc, int kv_dim,
                                                       int kv_mul, float* __restrict__ out, int ldo,
                                                       int pos0, int n, float scale) {
-  constexpr int QB = kPrefillQB, KB = kPrefillKB, LD = HD + 4, LP = KB + 4, DPT = HD / 16;
+  constexpr int QB = kPrefillQB, KB = attn_prefill_kb(HD), LD = HD + 4, LP = KB + 4, DPT = HD / 16;
+  constexpr int KPT = KB / 16;  // keys per thread and block
   extern __shared__ __align__(16) float sm[];
   float* Qs = sm;
   float* Ks = Qs + QB * LD;
@@ -72,21 +78,21 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
       *reinterpret_cast<pf4*>(Vs + r * LD + c) = j <= last ? vv : pf4{0.f, 0.f, 0.f, 0.f};
     }
     __syncthreads();
-    float s[4][4];
+    float s[4][KPT];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) s[a][b] = 0.f;
+      for (int b = 0; b < KPT; ++b) s[a][b] = 0.f;
     for (int d = 0; d < HD; d += 4) {
-      pf4 qv[4], kv[4];
+      pf4 qv[4], kv[KPT];
 #pragma unroll
       for (int a = 0; a < 4; ++a) qv[a] = *reinterpret_cast<const pf4*>(Qs + (4 * rg + a) * LD + d);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) kv[b] = *reinterpret_cast<const pf4*>(Ks + (4 * cg + b) * LD + d);
+      for (int b = 0; b < KPT; ++b) kv[b] = *reinterpret_cast<const pf4*>(Ks + (KPT * cg + b) * LD + d);
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < KPT; ++b)
           s[a][b] += qv[a].x * kv[b].x + qv[a].y * kv[b].y + qv[a].z * kv[b].z + qv[a].w * kv[b].w;
     }
 #pragma unroll
@@ -94,8 +100,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
       const int qpos = pos0 + p0 + 4 * rg + a;
       float mx = -INFINITY;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int kpos = j0 + 4 * cg + b;
+      for (int b = 0; b < KPT; ++b) {
+        const int kpos = j0 + KPT * cg + b;
         s[a][b] = kpos <= qpos ? s[a][b] * scale : -INFINITY;
         mx = fmaxf(mx, s[a][b]);
       }
@@ -106,9 +112,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
       const float alpha = m[a] == -INFINITY ? 0.f : expf(m[a] - mn);
       float rs = 0.f;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < KPT; ++b) {
         const float pv = s[a][b] == -INFINITY ? 0.f : expf(s[a][b] - mn);
-        Ps[(4 * rg + a) * LP + 4 * cg + b] = pv;
+        Ps[(4 * rg + a) * LP + KPT * cg + b] = pv;
         rs += pv;
       }
 #pragma unroll

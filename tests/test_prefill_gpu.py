@@ -184,7 +184,8 @@ def test_rope_rows_bit_exact(K, O, gpu, style, dim, kv, hd, pos0, n):
 # ----------------------------------------------------------- attention ------
 @pytest.mark.parametrize("H,kvm,hd,S,pos0,n", [(12, 1, 64, 160, 0, 143), (32, 4, 128, 256, 0, 200),
                                               (4, 2, 32, 80, 17, 50), (12, 6, 128, 4096, 3900, 100),
-                                              (8, 8, 64, 70, 0, 1), (8, 2, 64, 300, 130, 70)])
+                                              (8, 8, 64, 70, 0, 1), (8, 2, 64, 300, 130, 70),
+                                              (4, 2, 256, 200, 0, 150), (2, 2, 256, 160, 37, 100)])
 def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
     rng = np.random.default_rng(H * S + pos0 + n)
     kvd = H // kvm * hd
@@ -300,9 +301,17 @@ def test_qk_norm_rope_rows_matches_two_step(K, O, gpu, style, hd, H, KVH, pos0, 
 PREFILL_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"]
 
 
-@pytest.mark.parametrize("name", PREFILL_TINY)
+def _prefill_cfg(K, name):
+    if name == "tiny_hd256":  # head size 256 (the VALU attention with 32-key blocks)
+        return K.TINY["tiny_llama2"].with_(name="tiny_hd256", dim=512, hidden_dim=768, heads=2,
+                                          kv_heads=1, vocab=600, seq_len=96)
+    return K.TINY[name]
+
+
+@pytest.mark.parametrize("name", PREFILL_TINY + ["tiny_hd256"])
 def test_engine_prefill_vs_oracle(K, O, gpu, name):
-    cfg = K.TINY[name]
+    cfg = _prefill_cfg(K, name)
+    assert name != "tiny_hd256" or cfg.head_size == 256
     img = K.synth_image(cfg)
     P = min(40, cfg.seq_len - 10)
     prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
