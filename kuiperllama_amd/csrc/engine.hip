@@ -1422,13 +1422,22 @@ constexpr int kPrefillMaxSplitsQ8 = 16;  // int8 weights, at most 32 rows
 // Split-K factor for a GEMM launch of rows x n outputs (all of its outputs
 // together) over k.  fp32 weights / int8 over 32 rows: enough 64 x 64
 // workgroup tiles to fill the chip, each split keeping >= 32 k blocks.
-// int8 with at most 32 rows (32 x 128 tiles, one per 128 outputs): about
-// three tiles per CU, each split keeping >= 8 blocks of 32.
-int prefill_splits(int rows, int n, int k, bool q8) {
+// int8 with at most 32 rows (32 x 128 tiles, one per 128 outputs): the split
+// (up to kPrefillMaxSplitsQ8) that minimises rounds of resident workgroups x
+// k blocks per split, `slots` workgroups resident at once (5 per CU for the
+// direct-to-LDS int8 kernel, 3 for the register-staged one).
+int prefill_splits(int rows, int n, int k, bool q8, int slots = 768) {
   int s = 1;
   if (q8 && rows <= 32) {
-    const long long tiles = (n + 127) / 128;
-    while (s < kPrefillMaxSplitsQ8 && tiles * s < 768 && k / 32 / (2 * s) >= 8) s *= 2;
+    const long long tiles = (n + 127) / 128, nkb = k / 32;
+    long long best = -1;
+    for (int t = 1; t <= kPrefillMaxSplitsQ8 && t <= nkb; ++t) {
+      const long long cost = (tiles * t + slots - 1) / slots * ((nkb + t - 1) / t);
+      if (best < 0 || cost < best) {
+        best = cost;
+        s = t;
+      }
+    }
     return s;
   }
   const long long tiles = static_cast<long long>((rows + 63) / 64) * ((n + 63) / 64);
@@ -1546,9 +1555,11 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
     // q, k and v in one grouped launch (k and v straight into the cache rows)
     // Split-K where the launch would leave CUs idle (int8, at most 32 rows);
-    // every split's partials fit pf_ws (prefill_scratch).
+    // every split's partials fit pf_ws (prefill_scratch).  Groups of at least
+    // 32 run the direct-to-LDS int8 kernel (5 workgroups per CU).
+    const int slots = (m.gs >= 32 ? 5 : 3) * 256;
     auto splits_for = [&](int ntot, int k, bool grouped) {
-      const int sp = grouped && !(q8 && n <= 32) ? 1 : prefill_splits(n, ntot, k, q8);
+      const int sp = grouped && !(q8 && n <= 32) ? 1 : prefill_splits(n, ntot, k, q8, slots);
       if (r == KL_OK && sp > 1 && static_cast<size_t>(sp) * n * ntot * sizeof(float) > e->pf_ws_bytes)
         r = KL_EWORKSPACE;
       return sp;

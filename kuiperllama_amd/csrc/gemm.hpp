@@ -442,6 +442,173 @@ __global__ __launch_bounds__(256) void k_gemm_f32_dma(GemmArgs g) {
       }
 }
 
+// k_gemm_q8_dma (int8 weights, at most 32 rows, group size >= 32): the
+// direct-to-LDS pipeline of k_gemm_f32_dma for a 32 x 128 tile, with the
+// weights staged as int8.  Per 32-column block a 3-stage ring holds the A tile
+// (32 rows of 128 B, chunks swizzled by dma_swz), the W tile (128 rows of
+// 32 B) and each W row's group scale (one per row and block: the block lies in
+// one group); every wave issues one direct-to-LDS load of each per block (its
+// 8 A rows, its 32 W rows, its 32 scales), so the wait counts are uniform.
+// Wave w owns columns 32 w .. 32 w + 31 as 2 x 2 blocks of 16 x 16
+// (v_mfma_f32_16x16x4f32); lane group g4 = l / 16 takes k = 8 g4 .. 8 g4 + 7
+// of a block: two 16-byte A reads per row block and one 8-byte read of its
+// weights per column block, dequantised in registers as float(q) * scale (the
+// reference int8 GEMV's weight, cuda/matmul_kernel.cu:73).  A quarter of the
+// LDS traffic of staging dequantised floats, and no register staging.
+__global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
+  constexpr int BM = 32, BN = 128, BK = 32;
+  constexpr int SA = BM * BK;        // A floats per stage
+  constexpr int SW = BN * BK / 4;    // W int8 bytes per stage, in floats
+  constexpr int SS = 4 * 64;         // scale slots per stage (64 per wave, 32 used)
+  constexpr int ST = SA + SW + SS;
+  __shared__ __align__(1024) float L[kDmaStages * ST];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int sidx = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i < g.nseg && static_cast<int>(blockIdx.x) >= g.seg[i].tile0) sidx = i;
+  const float* __restrict__ A = g.A;
+  const void* W = g.seg[0].W;
+  float* C = g.seg[0].C;
+  const float* bias = g.seg[0].bias;
+  const float* S = g.seg[0].S;
+  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0, gshift = g.seg[0].gshift;
+  size_t wsoff = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i == sidx) {
+      W = g.seg[i].W;
+      C = g.seg[i].C;
+      bias = g.seg[i].bias;
+      S = g.seg[i].S;
+      N = g.seg[i].N;
+      ldw = g.seg[i].ldw;
+      ldc = g.seg[i].ldc;
+      tile0 = g.seg[i].tile0;
+      gshift = g.seg[i].gshift;
+      wsoff = g.seg[i].wsoff;
+    }
+  const int M = g.M, K = g.K, lda = g.lda;
+  const int n0 = (static_cast<int>(blockIdx.x) - tile0) * BN;  // one row tile (M <= 32)
+  const int nkt = K / BK;
+  const int kb0 = static_cast<int>(blockIdx.y) * nkt / g.splits;
+  const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
+
+  // Per-lane source offsets (block 0): A row 8 wave + l / 8, its chunk
+  // (l % 8) ^ dma_swz(row); W row 32 wave + l / 2, its half l % 2; the scale
+  // of W row 32 wave + l % 32 (lanes 32..63 repeat lanes 0..31's).
+  const int ra = 8 * wave + (lane >> 3);
+  const unsigned int ga = static_cast<unsigned int>(
+      (min(ra, M - 1) * lda + 4 * ((lane & 7) ^ dma_swz(ra))) * 4);
+  const int rw = 32 * wave + (lane >> 1);
+  const size_t gw = static_cast<size_t>(min(n0 + rw, N - 1)) * ldw + 16 * (lane & 1);
+  const size_t gs = static_cast<size_t>(min(n0 + 32 * wave + (lane & 31), N - 1)) * ldw;
+  auto request = [&](int kb, int st) {
+    float* la = L + st * ST;
+    __builtin_amdgcn_global_load_lds(
+        (global_void_t*)(reinterpret_cast<const char*>(A) + static_cast<size_t>(kb) * BK * 4 + ga),
+        (lds_void_t*)(la + 256 * wave), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        (global_void_t*)(static_cast<const char*>(W) + gw + static_cast<size_t>(kb) * BK),
+        (lds_void_t*)(la + SA + 256 * wave), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        (global_void_t*)(S + ((gs + static_cast<size_t>(kb) * BK) >> gshift)),
+        (lds_void_t*)(la + SA + SW + 64 * wave), 4, 0, 0);
+  };
+  const int g4 = lane >> 4, r16 = lane & 15;
+  int oa[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) oa[j] = r16 * BK + 4 * ((2 * g4 + j) ^ dma_swz(r16));
+  gf4 af[2][2][2], bf[2][2][2];  // [register buffer][block][16-byte group of k]
+  auto operands = [&](int st, int p) {
+    const float* la = L + st * ST;
+    const unsigned char* lw = reinterpret_cast<const unsigned char*>(la + SA);
+    const float* ls = la + SA + SW + 64 * wave;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) af[p][a][j] = *reinterpret_cast<const gf4*>(la + a * 16 * BK + oa[j]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int row = 32 * wave + 16 * b + r16;
+      const uint2 q = *reinterpret_cast<const uint2*>(lw + row * BK + 8 * g4);
+      const float sc = ls[16 * b + r16];
+      const int lo = static_cast<int>(q.x), hi = static_cast<int>(q.y);
+      bf[p][b][0] = gf4{static_cast<float>((lo << 24) >> 24) * sc, static_cast<float>((lo << 16) >> 24) * sc,
+                        static_cast<float>((lo << 8) >> 24) * sc, static_cast<float>(lo >> 24) * sc};
+      bf[p][b][1] = gf4{static_cast<float>((hi << 24) >> 24) * sc, static_cast<float>((hi << 16) >> 24) * sc,
+                        static_cast<float>((hi << 8) >> 24) * sc, static_cast<float>(hi >> 24) * sc};
+    }
+  };
+  gf4 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = gf4{0.f, 0.f, 0.f, 0.f};
+  auto steps = [&](int p, int s0, int s1) {
+#pragma unroll
+    for (int s = s0; s < s1; ++s)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[p][a][s >> 2][s & 3], bf[p][b][s >> 2][s & 3],
+                                                           acc[a][b], 0, 0, 0);
+  };
+  constexpr int kLoads = 3;  // load instructions per block and wave
+  if (kb0 < kb1) {
+    request(kb0, 0);
+    request(min(kb0 + 1, kb1 - 1), 1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+    __builtin_amdgcn_s_barrier();
+    operands(0, 0);
+    int st = 0;
+    // As k_gemm_f32_dma: request block kt + 2, run 6 of the 8 k steps, wait
+    // for block kt + 1 and every wave's reads, read its operands into the
+    // other register buffer while the last 2 steps run.
+    auto block = [&](int kt, int p) {
+      const int sn = st == 0 ? 2 : st - 1;
+      const int st1 = st == 2 ? 0 : st + 1;
+      request(min(kt + 2, kb1 - 1), sn);
+      steps(p, 0, 6);
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(kLoads) : "memory");
+      __builtin_amdgcn_s_barrier();
+      operands(st1, p ^ 1);
+      steps(p, 6, 8);
+      st = st1;
+    };
+    int kt = kb0;
+    for (; kt + 1 < kb1; kt += 2) {
+      block(kt, 0);
+      block(kt + 1, 1);
+    }
+    if (kt < kb1) block(kt, 0);
+  }
+
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * a + 4 * g4 + r;
+        const int n = n0 + 32 * wave + 16 * b + r16;
+        if (m < M && n < N) {
+          float v = acc[a][b][r];
+          if (wsp) {
+            wsp[static_cast<size_t>(m) * N + n] = v;
+          } else {
+            if (bias) v += bias[n];
+            float* cp = C + static_cast<size_t>(m) * ldc + n;
+            if (g.accumulate) v = *cp + v;
+            *cp = v;
+          }
+        }
+      }
+}
+
 // C_s = sum of the split partials in split order (+ bias_s) (+ C_s), over
 // every output s of the launch: element i of a split's slab belongs to the
 // output whose [M][N_s] block (at seg[s].wsoff) holds it.

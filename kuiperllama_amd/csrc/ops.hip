@@ -931,7 +931,15 @@ int kl::gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg*
   // fp32 weights with K a whole number of 32-column blocks (every model
   // projection) stream through the direct-to-LDS kernel; int8 weights and
   // other K through the register-staged one.
-  if (small)
+  // Short int8 prompts with groups of at least 32 (one scale per row and
+  // 32-column block) and 16-byte aligned weights stage the int8 tiles
+  // directly into LDS.
+  bool small_dma = small;
+  for (int i = 0; i < nseg && small_dma; ++i)
+    small_dma = segs[i].gshift >= 5 && (reinterpret_cast<uintptr_t>(segs[i].W) & 15u) == 0;
+  if (small_dma)
+    hipLaunchKernelGGL(k_gemm_q8_dma, dim3(static_cast<unsigned>(tiles), splits), dim3(256), 0, st, g);
+  else if (small)
     hipLaunchKernelGGL((k_gemm_f32<1, 4, 1, 1, true>), dim3(static_cast<unsigned>(tiles), splits),
                        dim3(256), 0, st, g);
   else if (q8)
