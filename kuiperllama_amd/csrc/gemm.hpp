@@ -5,8 +5,9 @@
 // K-contiguous.  The reference has no batched path (MatmulLayer takes a 1-D
 // input, op/matmul.cpp:20; the prompt runs token by token, demo/main.cpp:20-22).
 //
-// Two kernels share the launch arguments (GemmArgs, gemm_run.hpp) and the
-// 64 x 64 workgroup tile of four waves:
+// Three kernels share the launch arguments (GemmArgs, gemm_run.hpp), four
+// waves per workgroup: k_gemm_f32_dma (fp32), k_gemm_f32 (int8 and other K)
+// and k_gemm_q8_dma (int8, at most 32 rows; described at its definition).
 //
 // k_gemm_f32_dma<TA> (fp32 weights, K a multiple of 32; every model
 // projection): a workgroup tile of 32 TA x 64 (TA = 2: 64 x 64, three
