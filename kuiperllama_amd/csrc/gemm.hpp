@@ -13,7 +13,7 @@
 // projection): a workgroup tile of 32 TA x 64 (TA = 2: 64 x 64, three
 // workgroups per CU; TA = 4: 128 x 64, two per CU, for launches with at least
 // 1024 such tiles, where halving the operand reads and barriers per MFMA pays
-// for the fewer resident waves: +6% on the cfg 5 W1/W3 shape, -5 to -13% on
+// for the fewer resident waves: +6% on the Qwen3-4B W1/W3 shape at 512 rows, -5 to -13% on
 // the narrower ones); each wave owns TA x 2 blocks of 16 x 16 accumulated with
 // v_mfma_f32_16x16x4f32 (A operand: lane l holds A[l % 16][k], B operand
 // W[l % 16][k], k = l / 16; result register r of lane l is
@@ -275,7 +275,7 @@ constexpr int kDmaStages = 3;
 // their position within 512 B, so bits 0 and 2 of the swizzle must follow
 // r / 4 (bits 2 and 3 of r) and bit 1 may follow bit 1 of r.  r & 7 (the
 // plain XOR) leaves rows r and r + 8 on the same slots: 2-way conflicts on
-// every operand read (SQ_LDS_BANK_CONFLICT 1.05e9 -> 0 on the cfg 5 shapes).
+// every operand read (SQ_LDS_BANK_CONFLICT 1.05e9 -> 0 on the Qwen3-4B 512-row shapes).
 __device__ __forceinline__ int dma_swz(int r) { return ((r >> 2) & 1) | (r & 2) | ((r >> 1) & 4); }
 
 template <int TA>
