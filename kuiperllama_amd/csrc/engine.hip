@@ -389,9 +389,16 @@ int parse_image(const void* image, size_t size, int family, int quant, ImageLayo
 // ---------------------------------------------------------------------------
 // Engine.
 // ---------------------------------------------------------------------------
+// bf16 planes (k_split3) of one layer's fp32 projections for the
+// split-product prefill GEMM: 3 planes of N x K each.
+struct XPlanes {
+  const void *q, *k, *v, *o, *w1, *w2, *w3;
+};
+
 struct LayerDev {
   const float *rms_att, *rms_ffn, *bq, *bk, *bv, *qn, *kn;
   WView wq, wk, wv, wo, w1, w2, w3;
+  XPlanes xp;
 };
 
 struct kl_engine {
@@ -468,6 +475,13 @@ struct kl_engine {
   // Batched prompt prefill (kl_engine_prefill): scratch for one chunk of
   // rows, allocated on first use.
   bool use_prefill = false;
+  // fp32 images: the projections run as split-product GEMMs (k_gemm_x6) on
+  // bf16 planes of the weights (xw_buf, built on the first prefill, 1.5x the
+  // fp32 projection bytes) and of each GEMM input (pf_ax).
+  bool pf_x6 = false;
+  char* xw_buf = nullptr;
+  void* pf_ax = nullptr;        // 3 planes of pf_rows x max(D, Dq, F) bf16
+  size_t pf_ax_plane = 0;       // elements per plane
   int pf_rows = 0;              // rows the scratch holds
   char* pf_buf = nullptr;       // one allocation for everything below
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
@@ -1018,6 +1032,7 @@ void release(kl_engine* e) {
   if (e->ev1) (void)hipEventDestroy(e->ev1);
   if (e->arena) (void)hipFree(e->arena);
   if (e->pf_buf) (void)hipFree(e->pf_buf);
+  if (e->xw_buf) (void)hipFree(e->xw_buf);
   if (e->d_split) (void)hipFree(e->d_split);
   if (e->st_host) (void)hipHostFree(e->st_host);
   if (e->derr_host) (void)hipHostFree(e->derr_host);
@@ -1133,6 +1148,13 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
     default: e->eps = 1e-6f; e->theta = 1000000.f; e->rope_style = KL_ROPE_HALF; break;
   }
   e->transform = family == KL_FAMILY_QWEN3 ? 2 : 1;
+  {
+    // Batched prefill of fp32 images with every GEMM depth a multiple of 32:
+    // split-product GEMMs; KL_PREFILL_GEMM=f32 keeps the fp32 matrix-core kernels.
+    const char* env = std::getenv("KL_PREFILL_GEMM");
+    e->pf_x6 = !quant && lay.D % 32 == 0 && lay.Dq % 32 == 0 && lay.F % 32 == 0 &&
+               !(env && std::strcmp(env, "f32") == 0);
+  }
   int dev = 0;
   hipDeviceProp_t prop;
   if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
@@ -1491,14 +1513,21 @@ int prefill_scratch(kl_engine* e, int rows) {
   // outputs), and for int8 prompts of at most 32 rows also the grouped QKV
   // and W1/W3 outputs at up to kPrefillMaxSplitsQ8 splits.
   size_t ws_floats = static_cast<size_t>(kPrefillMaxSplits) * R * m.D;
+  // The split-product GEMMs choose up to 8 splits for WO and W2, 4 for the
+  // grouped q/k/v and 2 for W1/W3 within this workspace.
+  if (e->pf_x6)
+    ws_floats = std::max({ws_floats, 8 * R * m.D, 4 * R * (static_cast<size_t>(m.Dq) + 2 * m.Dkv),
+                          2 * R * 2 * static_cast<size_t>(m.F)});
   if (e->quant)
     ws_floats = std::max(ws_floats, static_cast<size_t>(kPrefillMaxSplitsQ8) * std::min<size_t>(R, 32) *
                                         std::max<size_t>({static_cast<size_t>(m.Dq) + 2 * m.Dkv,
                                                           2 * static_cast<size_t>(m.F),
                                                           static_cast<size_t>(m.D)}));
   const size_t sz_ws = al(ws_floats * 4);
+  const size_t ax_plane = e->pf_x6 ? R * std::max({m.D, m.Dq, m.F}) : 0;
+  const size_t sz_ax = al(3 * ax_plane * 2);
   const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(attn_ws) + al(m.D * 4) +
-                       al(m.S * 4) + al(256) + al(am);
+                       al(m.S * 4) + al(256) + al(am) + sz_ax;
   char* buf = nullptr;
   hipError_t err = hipMalloc(&buf, total);
   if (err != hipSuccess) return KL_ENOMEM;
@@ -1525,10 +1554,46 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_next = reinterpret_cast<int32_t*>(take(al(256)));
   e->pf_am = take(al(am));
   e->pf_am_bytes = am;
+  e->pf_ax = sz_ax ? take(sz_ax) : nullptr;
+  e->pf_ax_plane = ax_plane;
   e->pf_rows = rows;
   err = hipMemsetAsync(e->pf_am, 0, am, e->stream);
   if (err != hipSuccess) return rc(err);
   return KL_OK;
+}
+
+// Builds the bf16 planes of every layer's fp32 projections (once).
+int prefill_planes(kl_engine* e) {
+  if (!e->pf_x6 || e->xw_buf) return KL_OK;
+  const ImageLayout& m = e->lay;
+  const size_t D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F;
+  const size_t per_layer = (Dq + 2 * Dkv) * D + D * Dq + 2 * F * D + D * F;  // elements
+  char* buf = nullptr;
+  hipError_t err = hipMalloc(&buf, 3 * per_layer * 2 * m.L);
+  if (err != hipSuccess) return KL_ENOMEM;
+  e->xw_buf = buf;
+  hipStream_t hs = static_cast<hipStream_t>(e->stream);
+  size_t off = 0;
+  int r = KL_OK;
+  auto planes = [&](const WView& w, size_t N, size_t K) -> const void* {
+    char* dst = buf + off;
+    off += 3 * N * K * 2;
+    if (r == KL_OK)
+      r = split3_run(static_cast<const float*>(w.w), static_cast<int>(N), static_cast<int>(K),
+                     static_cast<int>(K), dst, N * K, hs);
+    return dst;
+  };
+  for (int l = 0; l < m.L; ++l) {
+    LayerDev& Ld = e->layers[l];
+    Ld.xp.q = planes(Ld.wq, Dq, D);
+    Ld.xp.k = planes(Ld.wk, Dkv, D);
+    Ld.xp.v = planes(Ld.wv, Dkv, D);
+    Ld.xp.o = planes(Ld.wo, D, Dq);
+    Ld.xp.w1 = planes(Ld.w1, F, D);
+    Ld.xp.w2 = planes(Ld.w2, D, F);
+    Ld.xp.w3 = planes(Ld.w3, F, D);
+  }
+  return r;
 }
 
 // Positions pos0 .. pos0+n-1 through every layer; leaves the residual rows in
@@ -1564,12 +1629,31 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
         r = KL_EWORKSPACE;
       return sp;
     };
+    // fp32 weights: the split-product GEMM over bf16 planes of the input
+    // (split here) and of the weights (prefill_planes).
+    auto x6 = [&](const float* in, int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc) {
+      PF(split3_run(in, n, k, k, e->pf_ax, e->pf_ax_plane, hs));
+      GemmX6Planes p{};
+      p.A = e->pf_ax;
+      p.a_plane = e->pf_ax_plane;
+      p.lda = k;
+      for (int i = 0; i < nseg; ++i) {
+        p.W[i] = wx[i];
+        p.w_plane[i] = static_cast<size_t>(sg[i].N) * k;
+      }
+      PF(gemm_run_x6(p, n, k, nseg, sg, acc, e->pf_ws, e->pf_ws_bytes, hs));
+    };
     {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
-      const int sp = splits_for(Dq + 2 * Dkv, D, true);
-      PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, e->pf_ws, sp, hs));
+      if (e->pf_x6) {
+        const void* wx[3] = {Ld.xp.q, Ld.xp.k, Ld.xp.v};
+        x6(e->pf_xn, D, 3, sg, wx, 0);
+      } else {
+        const int sp = splits_for(Dq + 2 * Dkv, D, true);
+        PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, e->pf_ws, sp, hs));
+      }
     }
     if (e->transform == 2 && (hd == 64 || hd == 128)) {  // Qwen3 q/k RMSNorm (eps 1e-6) + RoPE
       PF(kl_qk_norm_rope_rows(e->rope_style, hd, H, KVH, e->pf_q, Dq, krow, Dkv, Ld.qn, Ld.kn, 1e-6f,
@@ -1587,22 +1671,35 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
                           e->pf_aws, e->pf_aws_bytes, st));
     {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
-      const int sp = splits_for(D, Dq, false);
-      PF(gemm_run(e->pf_att, n, Dq, Dq, 1, &sg, 1, e->pf_ws, sp, hs));
+      if (e->pf_x6) {
+        x6(e->pf_att, Dq, 1, &sg, &Ld.xp.o, 1);
+      } else {
+        const int sp = splits_for(D, Dq, false);
+        PF(gemm_run(e->pf_att, n, Dq, Dq, 1, &sg, 1, e->pf_ws, sp, hs));
+      }
     }
     // feed_forward (llama3.cpp:671-719)
     PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
     {
       const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
-      const int sp = splits_for(2 * F, D, true);
-      PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, e->pf_ws, sp, hs));
+      if (e->pf_x6) {
+        const void* wx[2] = {Ld.xp.w1, Ld.xp.w3};
+        x6(e->pf_xn, D, 2, sg, wx, 0);
+      } else {
+        const int sp = splits_for(2 * F, D, true);
+        PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, e->pf_ws, sp, hs));
+      }
     }
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
     {
       const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
-      const int sp = splits_for(D, F, false);
-      PF(gemm_run(e->pf_h1, n, F, F, 1, &sg, 1, e->pf_ws, sp, hs));
+      if (e->pf_x6) {
+        x6(e->pf_h1, F, 1, &sg, &Ld.xp.w2, 1);
+      } else {
+        const int sp = splits_for(D, F, false);
+        PF(gemm_run(e->pf_h1, n, F, F, 1, &sg, 1, e->pf_ws, sp, hs));
+      }
     }
   }
 #undef PF
@@ -1629,6 +1726,7 @@ int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next,
     if (prompt[i] < 0 || prompt[i] >= m.V) return KL_ETOKEN;
   if (!prefill_supported(e)) return KL_EUNSUPP;
   int r = prefill_scratch(e, std::min(P, kPrefillChunk));
+  if (r == KL_OK) r = prefill_planes(e);
   if (r != KL_OK) return r;
   hipError_t err = hipMemcpyAsync(e->pf_tok, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
                                   e->stream);

@@ -5,9 +5,11 @@
 // K-contiguous.  The reference has no batched path (MatmulLayer takes a 1-D
 // input, op/matmul.cpp:20; the prompt runs token by token, demo/main.cpp:20-22).
 //
-// Three kernels share the launch arguments (GemmArgs, gemm_run.hpp), four
-// waves per workgroup: k_gemm_f32_dma (fp32), k_gemm_f32 (int8 and other K)
-// and k_gemm_q8_dma (int8, at most 32 rows; described at its definition).
+// Four kernels share the launch arguments (GemmArgs, gemm_run.hpp), four
+// waves per workgroup: k_gemm_f32_dma (fp32), k_gemm_f32 (int8 and other K),
+// k_gemm_q8_dma (int8, at most 32 rows) and k_gemm_x6 (fp32 operands as bf16
+// planes on the bf16 matrix cores); the last two are described at their
+// definitions.
 //
 // k_gemm_f32_dma<TA> (fp32 weights, K a multiple of 32; every model
 // projection): a workgroup tile of 32 TA x 64 (TA = 2: 64 x 64, three
@@ -608,6 +610,248 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
           }
         }
       }
+}
+
+// ---------------------------------------------------------------------------
+// Split-product GEMM (fp32 accuracy on the bf16 matrix cores).  Each fp32
+// operand x is held as three bf16 planes x = x0 + x1 + x2 (x0 = bf16(x),
+// x1 = bf16(x - x0), x2 = bf16(x - x0 - x1), round to nearest even;
+// k_split3): 8 + 8 + 8 significand bits carry all 24 of x.  The product
+// A W^T = sum over i, j of Ai Wj^T; the kernel forms the six terms with
+// i + j <= 2, each a bf16 x bf16 product that fp32 holds exactly, accumulated
+// in fp32 by v_mfma_f32_32x32x16_bf16.  The three terms left out (i + j >= 3)
+// are each at most 2^-24 |a w| (|x1| <= 2^-8 |x|, |x2| <= 2^-16 |x|), the
+// size of one fp32 rounding, so the result is as accurate as an fp32 GEMM
+// (measured on the prefill shapes: max |error| / sum |a w| 3e-8 (split K) to
+// 1.1e-7 (one K pass) against 1.3e-7 to 2.2e-7 for k_gemm_f32_dma).  bf16 MFMA
+// runs at 16x the fp32 MFMA rate, six products at 2.7x.
+//
+// Workgroup tile 128 x 128, four waves of 64 x 64 (2 x 2 blocks of 32 x 32;
+// A operand: lane l holds A[l % 32][8 k-values], B operand W[l % 32][the
+// same 8 k-values], k-values 8 (l / 32) .. + 7 of a 16-column step; result
+// register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  K
+// advances in blocks of 32 columns: the six plane tiles of a block (A0 A1 A2
+// W0 W1 W2, 128 rows x 64 B each, 48 KB) land in LDS by direct-to-LDS loads
+// through a 3-stage ring (144 KB: one workgroup per CU), block k + 2
+// requested while block k is computed.  A row holds four 16-byte chunks;
+// chunk c of row r sits in slot c ^ x6_swz(r), so the 32 lanes of a half
+// wave (32 consecutive rows, one chunk each) read 32 distinct 16-byte slots
+// of the 512 B bank period.  Each block runs as two 16-column steps of 24
+// MFMAs (six products x four blocks); the second step's operands are read
+// from LDS during the first step, the next block's first-step operands
+// during the second (the reads are interleaved one per MFMA).
+//
+// Launch order is XCD-aware: workgroup b runs on XCD b % 8 (round-robin
+// dispatch), so tile t = (b % 8) ceil(T / 8) + b / 8 gives each XCD a
+// contiguous run of tiles whose M tiles share their W tile in its L2.
+// Split-K as k_gemm_f32_dma (blockIdx.y = split, partials to ws, then
+// k_gemm_reduce).
+__device__ __forceinline__ int x6_swz(int r) { return (r >> 3) & 3; }
+
+typedef __bf16 xbf8 __attribute__((ext_vector_type(8)));
+
+__global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
+  constexpr int BM = 128, BN = 128, BK = 32, ST = 3;
+  constexpr int PT = BM * BK;  // bf16 per plane tile
+  constexpr int SS = 6 * PT;   // per stage
+  constexpr int LPW = 12;      // 1 KB load instructions per wave and block
+  __shared__ __align__(1024) __bf16 L[ST * SS];
+  const GemmArgs& g = x.g;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int per = static_cast<int>(gridDim.x) >> 3;
+  const int b = static_cast<int>(blockIdx.x);
+  const int t = (b & 7) * per + (b >> 3);
+  if (t >= x.tiles) return;
+  int sidx = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i < g.nseg && t >= g.seg[i].tile0) sidx = i;
+  const char* W = static_cast<const char*>(x.p.W[0]);
+  size_t wplane = x.p.w_plane[0];
+  float* C = g.seg[0].C;
+  const float* bias = g.seg[0].bias;
+  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0;
+  size_t wsoff = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i == sidx) {
+      W = static_cast<const char*>(x.p.W[i]);
+      wplane = x.p.w_plane[i];
+      C = g.seg[i].C;
+      bias = g.seg[i].bias;
+      N = g.seg[i].N;
+      ldw = g.seg[i].ldw;
+      ldc = g.seg[i].ldc;
+      tile0 = g.seg[i].tile0;
+      wsoff = g.seg[i].wsoff;
+    }
+  const int M = g.M, K = g.K, lda = x.p.lda;
+  const int local = t - tile0;
+  const int tm = local % g.tiles_m, tn = local / g.tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nkt = K / BK;
+  const int kb0 = static_cast<int>(blockIdx.y) * nkt / g.splits;
+  const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
+  const char* A = static_cast<const char*>(x.p.A);
+  const size_t aplane = x.p.a_plane;
+
+  // Load instruction i of this wave fills 1 KB j = 12 wave + i of a stage:
+  // plane tile j / 8, rows 16 (j % 8) .. + 15; lane l fills slot l % 4 of row
+  // r = 16 (j % 8) + l / 4 with chunk (l % 4) ^ x6_swz(r).  Rows past M or N
+  // read the last row (they only feed outputs that are never stored).
+  const char* src[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int j = LPW * wave + i;
+    const int pt = j >> 3;
+    const int r = 16 * (j & 7) + (lane >> 2);
+    const int c = (lane & 3) ^ x6_swz(r);
+    src[i] = pt < 3 ? A + (pt * aplane + static_cast<size_t>(min(m0 + r, M - 1)) * lda) * 2 + 16 * c
+                    : W + ((pt - 3) * wplane + static_cast<size_t>(min(n0 + r, N - 1)) * ldw) * 2 + 16 * c;
+  }
+  auto request = [&](int kb, int st) {
+    __bf16* base = L + st * SS;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i)
+      __builtin_amdgcn_global_load_lds((global_void_t*)(src[i] + static_cast<size_t>(kb) * BK * 2),
+                                       (lds_void_t*)(base + 512 * (LPW * wave + i)), 16, 0, 0);
+  };
+  // Step s of a block: lane half h = l / 32 reads chunk 2 s + h of rows
+  // 64 wm + 32 q + l % 32 (A planes) and 64 wn + 32 q + l % 32 (W planes).
+  const int h = lane >> 5, r32 = lane & 31;
+  int oa[2][2], ow[2][2];  // [block q][step s], bf16 offsets within a plane tile
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int ra = 64 * wm + 32 * q + r32, rw = 64 * wn + 32 * q + r32;
+      oa[q][s] = ra * BK + 8 * ((2 * s + h) ^ x6_swz(ra));
+      ow[q][s] = rw * BK + 8 * ((2 * s + h) ^ x6_swz(rw));
+    }
+  xbf8 fa[2][3][2], fw[2][3][2];  // [register buffer][plane][block]
+  auto operands = [&](int st, int s, int p) {
+    const __bf16* base = L + st * SS;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        fa[p][pl][q] = *reinterpret_cast<const xbf8*>(base + pl * PT + oa[q][s]);
+        fw[p][pl][q] = *reinterpret_cast<const xbf8*>(base + (3 + pl) * PT + ow[q][s]);
+      }
+  };
+  gf16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][c][r] = 0.f;
+  // The six products of one step, smallest terms first.
+  auto step = [&](int p) {
+    constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PW[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          acc[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][PA[k]][a], fw[p][PW[k]][c], acc[a][c], 0,
+                                                              0, 0);
+  };
+  // One LDS operand read (and, with loads, one direct-to-LDS request) after
+  // each of the first 12 MFMAs of a step.
+#define KL_X6_INTERLEAVE(loads)                                           \
+  do {                                                                    \
+    _Pragma("unroll") for (int i_ = 0; i_ < 12; ++i_) {                   \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  \
+      if (loads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);       \
+    }                                                                     \
+    __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);                   \
+  } while (0)
+  if (kb0 < kb1) {
+    request(kb0, 0);
+    request(min(kb0 + 1, kb1 - 1), 1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    __builtin_amdgcn_s_barrier();
+    operands(0, 0, 0);
+    int st = 0;
+    // Block kt in stage st, its first-step operands in buffer 0: request
+    // block kt + 2 into the stage block kt - 1 used, read the second step's
+    // operands and run the first step, wait until block kt + 1 has landed and
+    // every wave is done reading stage st, then read block kt + 1's first
+    // step while the second step runs.  The last blocks request themselves
+    // again (a stage nobody reads afterwards).
+    for (int kt = kb0; kt < kb1; ++kt) {
+      const int sn = st == 0 ? ST - 1 : st - 1;
+      const int st1 = st == ST - 1 ? 0 : st + 1;
+      __builtin_amdgcn_sched_barrier(0);
+      request(min(kt + 2, kb1 - 1), sn);
+      operands(st, 1, 1);
+      step(0);
+      KL_X6_INTERLEAVE(true);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(LPW) : "memory");
+      __builtin_amdgcn_s_barrier();
+      operands(st1, 0, 0);
+      step(1);
+      KL_X6_INTERLEAVE(false);
+      __builtin_amdgcn_sched_barrier(0);
+      st = st1;
+    }
+  }
+#undef KL_X6_INTERLEAVE
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 64 * wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int n = n0 + 64 * wn + 32 * c + r32;
+        if (m < M && n < N) {
+          float v = acc[a][c][r];
+          if (wsp) {
+            wsp[static_cast<size_t>(m) * N + n] = v;
+          } else {
+            if (bias) v += bias[n];
+            float* cp = C + static_cast<size_t>(m) * ldc + n;
+            if (g.accumulate) v = *cp + v;
+            *cp = v;
+          }
+        }
+      }
+}
+
+// fp32 rows -> three bf16 planes x0, x1, x2 (k_gemm_x6): row r of plane p at
+// out + p * plane + r * cols; eight values per thread.
+__global__ void k_split3(const float* __restrict__ x, int rows, int cols, int ldx,
+                         __bf16* __restrict__ out, size_t plane) {
+  const int c8 = cols / 8;
+  const size_t total = static_cast<size_t>(rows) * c8;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int r = static_cast<int>(i / c8);
+    const int c = static_cast<int>(i - static_cast<size_t>(r) * c8) * 8;
+    const gf4* p = reinterpret_cast<const gf4*>(x + static_cast<size_t>(r) * ldx + c);
+    const gf4 v0 = p[0], v1 = p[1];
+    xbf8 x0, x1, x2;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = j < 4 ? v0[j] : v1[j - 4];
+      x0[j] = static_cast<__bf16>(v);
+      const float r1 = v - static_cast<float>(x0[j]);
+      x1[j] = static_cast<__bf16>(r1);
+      x2[j] = static_cast<__bf16>(r1 - static_cast<float>(x1[j]));
+    }
+    const size_t o = static_cast<size_t>(r) * cols + c;
+    *reinterpret_cast<xbf8*>(out + o) = x0;
+    *reinterpret_cast<xbf8*>(out + plane + o) = x1;
+    *reinterpret_cast<xbf8*>(out + 2 * plane + o) = x2;
+  }
 }
 
 // C_s = sum of the split partials in split order (+ bias_s) (+ C_s), over

@@ -37,11 +37,39 @@ struct GemmArgs {
   int splits;
 };
 
+// Operands of the split-product GEMM (k_gemm_x6): A and every W_s as three
+// bf16 planes (k_split3), plane p at base + p * plane elements, rows of lda
+// (A) and seg[s].ldw (W_s) elements.
+struct GemmX6Planes {
+  const void* A;
+  size_t a_plane;
+  int lda;
+  const void* W[kGemmMaxSeg];
+  size_t w_plane[kGemmMaxSeg];
+};
+
+struct GemmX6Args {
+  GemmArgs g;
+  GemmX6Planes p;
+  int tiles;  // 128 x 128 tiles over every output (the grid is padded to a multiple of 8)
+};
+
 // Host launcher (ops.hip): C_s (+)= A . W_s^T (+ bias_s) for nseg outputs in
 // one grid; splits > 1 divides K among blockIdx.y into ws (splits * M *
 // (N_0 + ...) floats) and reduces in split order.  Every segment is fp32 or
 // every one int8.
 int gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* segs, int accumulate,
              float* ws, int splits, hipStream_t st);
+
+// Host launcher (ops.hip) of k_gemm_x6: the same products from bf16 planes
+// (segs[s].W unused).  K a multiple of 32.  Chooses the split count itself
+// (up to 8, where ws_bytes holds splits * M * (N_0 + ...) floats).
+int gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSeg* segs,
+                int accumulate, float* ws, size_t ws_bytes, hipStream_t st);
+
+// Host launcher (ops.hip) of k_split3: rows x cols fp32 (stride ldx) into
+// three bf16 planes of rows x cols (plane stride `plane` elements).
+int split3_run(const float* x, int rows, int cols, int ldx, void* planes, size_t plane,
+               hipStream_t st);
 
 }  // namespace kl

@@ -1011,6 +1011,115 @@ int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, i
 }  // extern "C"
 
 namespace {
+int device_cus();
+
+// Split count of a k_gemm_x6 launch of `tiles` tiles over nkt 32-column
+// blocks and mn output floats, one workgroup per CU: the time model is the
+// grid's rounds x blocks per split x 1.45 us, plus (splits > 1) the partials
+// written and read once and the outputs written ((2 splits + 1) x mn floats)
+// at 4 TB/s; a split count must win by 3% over the next smaller one.  On the
+// Qwen3-4B (512 rows) and Qwen2.5-1.5B (1024 rows) projections it picks the
+// best measured split of 1, 2, 3, 4, 6, 8 on every shape.
+int x6_splits(long long tiles, int nkt, size_t mn, size_t ws_floats) {
+  const long long cus = device_cus();
+  int best = 1;
+  double tbest = 1e300;
+  for (int s = 1; s <= 8 && nkt / s >= 4; ++s) {
+    if (s > 1 && static_cast<size_t>(s) * mn > ws_floats) break;
+    const long long rounds = (tiles * s + cus - 1) / cus;
+    const double t = static_cast<double>(rounds) * ((nkt + s - 1) / s) * 1.45 +
+                     (s > 1 ? static_cast<double>(mn) * 4.0 * (2 * s + 1) / 4e6 : 0.0);
+    if (t < tbest * 0.97) {
+      tbest = t;
+      best = s;
+    }
+  }
+  return best;
+}
+}  // namespace
+
+int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSeg* segs,
+                    int accumulate, float* ws, size_t ws_bytes, hipStream_t st) {
+  if (!planes.A || M <= 0 || K <= 0 || nseg < 1 || nseg > kGemmMaxSeg || planes.lda < K)
+    return KL_EINVAL;
+  if (K % 32 || planes.lda % 8 || planes.a_plane % 8 || !aligned16(planes.A)) return KL_EUNSUPP;
+  // Every plane must hold its rows (the kernel reads three planes of each).
+  if (planes.a_plane < static_cast<size_t>(M - 1) * planes.lda + K) return KL_EINVAL;
+  GemmArgs g{};
+  g.M = M;
+  g.K = K;
+  g.accumulate = accumulate;
+  g.nseg = nseg;
+  g.ws = ws;
+  g.tiles_m = (M + 127) / 128;
+  GemmX6Args x{};
+  x.p = planes;
+  long long tiles = 0;
+  size_t wsoff = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const GemmSeg& sg = segs[i];
+    if (!planes.W[i] || !sg.C || sg.N <= 0 || sg.ldw < K || sg.ldc < sg.N || sg.S) return KL_EINVAL;
+    if (sg.ldw % 8 || planes.w_plane[i] % 8 || !aligned16(planes.W[i])) return KL_EUNSUPP;
+    if (planes.w_plane[i] < static_cast<size_t>(sg.N - 1) * sg.ldw + K) return KL_EINVAL;
+    g.seg[i] = sg;
+    g.seg[i].tile0 = static_cast<int>(tiles);
+    g.seg[i].wsoff = wsoff;
+    tiles += static_cast<long long>(g.tiles_m) * ((sg.N + 127) / 128);
+    wsoff += static_cast<size_t>(M) * sg.N;
+  }
+  if (tiles > INT_MAX / 2) return KL_EUNSUPP;
+  g.ws_split = wsoff;
+  g.splits = ws ? x6_splits(tiles, K / 32, wsoff, ws_bytes / sizeof(float)) : 1;
+  x.g = g;
+  x.tiles = static_cast<int>(tiles);
+  const unsigned grid = static_cast<unsigned>(8 * ((tiles + 7) / 8));
+  hipLaunchKernelGGL(k_gemm_x6, dim3(grid, g.splits), dim3(256), 0, st, x);
+  int r = launch_rc();
+  if (r != KL_OK || g.splits == 1) return r;
+  const int rgrid = static_cast<int>(std::min<size_t>((g.ws_split + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, g);
+  return launch_rc();
+}
+
+int kl::split3_run(const float* x, int rows, int cols, int ldx, void* planes, size_t plane,
+                   hipStream_t st) {
+  if (!x || !planes || rows <= 0 || cols <= 0 || ldx < cols) return KL_EINVAL;
+  if (cols % 8 || ldx % 4 || plane % 8 || plane < static_cast<size_t>(rows) * cols || !aligned16(x) ||
+      !aligned16(planes))
+    return KL_EUNSUPP;
+  const size_t work = static_cast<size_t>(rows) * (cols / 8);
+  const int grid = static_cast<int>(std::min<size_t>((work + 255) / 256, 8192));
+  hipLaunchKernelGGL(k_split3, dim3(grid), dim3(256), 0, st, x, rows, cols, ldx,
+                     static_cast<__bf16*>(planes), plane);
+  return launch_rc();
+}
+
+extern "C" {
+
+int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, size_t plane_stride,
+                    void* stream) {
+  return split3_run(x, rows, cols, ldx, planes, plane_stride, as_stream(stream));
+}
+
+int kl_gemm_x6(const void* a_planes, size_t a_plane_stride, int lda, const void* w_planes,
+               size_t w_plane_stride, int ldw, float* C, int M, int N, int K, int ldc,
+               const float* bias, int accumulate, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  if (!C || N <= 0 || ldw < K || ldc < N) return KL_EINVAL;
+  GemmX6Planes p{};
+  p.A = a_planes;
+  p.a_plane = a_plane_stride;
+  p.lda = lda;
+  p.W[0] = w_planes;
+  p.w_plane[0] = w_plane_stride;
+  const GemmSeg sg{nullptr, C, bias, N, ldw, ldc, 0};
+  return gemm_run_x6(p, M, K, 1, &sg, accumulate, static_cast<float*>(workspace), workspace_bytes,
+                     as_stream(stream));
+}
+
+}  // extern "C"
+
+namespace {
 int device_cus() {
   static int cus = 0;
   if (cus == 0) {

@@ -112,6 +112,142 @@ def test_gemm_grouped_matches_single(K, O, gpu):
         assert np.array_equal(y, gemm(K, A, w, bias=b))  # same kernel, same order
 
 
+# --------------------------------------------- split-product GEMM (x6) ------
+def _bf16_rne(x):
+    """fp32 -> the nearest bf16 (ties to even), as fp32 (finite inputs)."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    return (r & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+
+
+def _split3_ref(x):
+    """x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 - x1); the fp32
+    differences are exact (x0 holds x's leading bits)."""
+    x = np.asarray(x, np.float32)
+    x0 = _bf16_rne(x)
+    r1 = (x - x0).astype(np.float32)
+    x1 = _bf16_rne(r1)
+    x2 = _bf16_rne((r1 - x1).astype(np.float32))
+    return x0, x1, x2
+
+
+def _as_f32(u16):
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+def _split_dev(K, X, pad_rows=0):
+    """kl_split_bf16x3 of X (rows x cols, row stride cols + 4) into planes of
+    (rows + pad_rows) x cols; returns the plane array and its stride."""
+    rows, cols = X.shape
+    Xp = np.zeros((rows, cols + 4), np.float32)
+    Xp[:, :cols] = X
+    dX = D(K, Xp)
+    plane = (rows + pad_rows) * cols
+    dP = K.DeviceArray(3 * plane, np.uint16)
+    ok(K.lib.kl_split_bf16x3(dX.ptr, rows, cols, cols + 4, dP.ptr, plane, None), "split")
+    return dP, plane
+
+
+def test_split_bf16x3_bit_exact(K, gpu):
+    rng = np.random.default_rng(11)
+    rows, cols = 37, 264
+    X = (rng.standard_normal((rows, cols)) * 10.0 ** rng.integers(-20, 20, (rows, cols))).astype(np.float32)
+    X[0, :8] = [0.0, -0.0, 1.0, -1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -9, 3.0e38, -1.5e-30]
+    dP, plane = _split_dev(K, X)
+    got = dP.numpy()
+    refs = _split3_ref(X)
+    for p in range(3):
+        g = _as_f32(got[p * plane:(p + 1) * plane].reshape(rows, cols))
+        assert np.array_equal(g.view(np.uint32), refs[p].view(np.uint32)), f"plane {p}"
+    # the planes hold x exactly (24 significand bits in 8 + 8 + 8)
+    x0, x1, x2 = (r.astype(np.float64) for r in refs)
+    finite = np.abs(X) < 1e37
+    assert np.array_equal((x0 + x1 + x2)[finite], X.astype(np.float64)[finite])
+
+
+def gemm_x6(K, A, W, bias=None, C0=None, ws=True):
+    M, Kd = A.shape
+    N = W.shape[0]
+    dA, ap = _split_dev(K, A, pad_rows=3)
+    dW, wp = _split_dev(K, W)
+    dC = D(K, C0) if C0 is not None else K.DeviceArray(M * N)
+    db = D(K, bias) if bias is not None else None
+    wsa = K.DeviceArray(8 * M * N) if ws else None
+    ok(K.lib.kl_gemm_x6(dA.ptr, ap, Kd, dW.ptr, wp, Kd, dC.ptr, M, N, Kd, N,
+                        db.ptr if db else None, int(C0 is not None), wsa.ptr if wsa else None,
+                        wsa.nbytes if wsa else 0, None), "kl_gemm_x6")
+    return dC.numpy().reshape(M, N)
+
+
+def test_gemm_x6_kat_six_terms_exact(K, gpu):
+    """a = s_m sigma_k c, w = t_n sigma_k c with c = 1 + 2^-9 + 2^-17 (planes
+    exactly 1, 2^-9, 2^-17), K = 32: every partial sum is exact in fp32, so
+    the product is exactly 32 s_m t_n (1 + 2^-8 + 2^-16 + 2^-18), the six
+    terms Ai Wj with i + j <= 2 (x0 w0; x0 w1 + x1 w0 = 2^-8; x0 w2 + x2 w0 =
+    2^-16; x1 w1 = 2^-18).  A missing or mis-paired term moves it by at least
+    32 |s t| 2^-18, a whole number of fp32 ulps."""
+    c = np.float32(1 + 2 ** -9 + 2 ** -17)
+    M, N, Kd = 130, 200, 32
+    s = np.array([(-1) ** (m % 3) * 2.0 ** (m % 5 - 2) for m in range(M)], np.float32)
+    t = np.array([(-1) ** (n % 2) * 2.0 ** (n % 7 - 3) for n in range(N)], np.float32)
+    sig = np.array([(-1) ** (k % 3 == 1) for k in range(Kd)], np.float32)
+    A = (s[:, None] * sig[None, :] * c).astype(np.float32)
+    W = (t[:, None] * sig[None, :] * c).astype(np.float32)
+    assert [float(v[0, 0]) for v in _split3_ref(np.array([[c]]))] == [1.0, 2 ** -9, 2 ** -17]
+    want = (32 * (1 + 2 ** -8 + 2 ** -16 + 2 ** -18) * np.outer(s.astype(np.float64), t)).astype(np.float32)
+    for ws in (False, True):
+        y = gemm_x6(K, A, W, ws=ws)
+        assert np.array_equal(y, want), np.max(np.abs(y - want))
+    # each of the six terms is visible in fp32: dropping any one changes every output
+    st = np.outer(s.astype(np.float64), t)
+    for term in (1.0, 2 ** -9, 2 ** -17, 2 ** -18):
+        less = (32 * (1 + 2 ** -8 + 2 ** -16 + 2 ** -18 - term) * st).astype(np.float32)
+        assert not np.any(less == want)
+
+
+X6_TOL = 1e-6  # |C - A W^T| <= X6_TOL * (|A| |W|^T), elementwise (fp32 GEMMs here: <= 2.2e-7)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 64, 32), (37, 200, 96), (300, 1000, 256), (513, 130, 1024),
+                                    (512, 2560, 4096), (1024, 1536, 1536), (129, 257, 64)])
+def test_gemm_x6_vs_fp64(K, gpu, M, N, Kd):
+    """Within an fp32 GEMM's error of the exact product, with and without the
+    split-K workspace (the launcher picks the split count; the narrow, deep
+    shapes split)."""
+    rng = np.random.default_rng(M + 3 * N + Kd)
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    W = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
+    exact = A.astype(np.float64) @ W.astype(np.float64).T
+    mag = np.abs(A).astype(np.float64) @ np.abs(W).astype(np.float64).T
+    for ws in (False, True):
+        y = gemm_x6(K, A, W, ws=ws)
+        err = np.max(np.abs(y - exact) / mag)
+        print(f"x6 {M}x{N}x{Kd} ws={ws}: max err / sum|aw| {err:.2e}", flush=True)
+        assert err <= X6_TOL
+
+
+def test_gemm_x6_bias_accumulate_and_refusals(K, O, gpu):
+    rng = np.random.default_rng(21)
+    M, N, Kd = 70, 200, 96
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    W = rng.standard_normal((N, Kd)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    exact = A.astype(np.float64) @ W.astype(np.float64).T
+    mag = np.abs(A).astype(np.float64) @ np.abs(W).astype(np.float64).T
+    yb = gemm_x6(K, A, W, bias=b)
+    ya = gemm_x6(K, A, W, C0=C0)
+    assert np.max(np.abs(yb - (exact + b)) / (mag + np.abs(b))) <= X6_TOL
+    assert np.max(np.abs(ya - (exact + C0)) / (mag + np.abs(C0))) <= X6_TOL
+    dP, plane = _split_dev(K, A)
+    dC = K.DeviceArray(M * N)
+    # K not a multiple of 32, a plane too short for its rows
+    assert K.lib.kl_gemm_x6(dP.ptr, plane, 80, dP.ptr, plane, 80, dC.ptr, M, N, 80, N, None, 0,
+                            None, 0, None) == -4
+    assert K.lib.kl_gemm_x6(dP.ptr, plane - 8, Kd, dP.ptr, plane, Kd, dC.ptr, M, M, Kd, N, None, 0,
+                            None, 0, None) == -1
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
 def test_gemm_splitk_vs_oracle(K, O, gpu, splits):
     rng = np.random.default_rng(splits)
@@ -299,6 +435,25 @@ def test_qk_norm_rope_rows_matches_two_step(K, O, gpu, style, hd, H, KVH, pos0, 
 
 # ------------------------------------------------------- whole prompt -------
 PREFILL_TINY = ["tiny_llama2", "tiny_llama3", "tiny_qwen2", "tiny_qwen3", "tiny_q8", "tiny_qwen2_q8"]
+
+
+def test_engine_prefill_f32_gemm_path(K, O, gpu, monkeypatch):
+    """KL_PREFILL_GEMM=f32 keeps the fp32 matrix-core GEMMs: same bars, and
+    logits close to the default (split-product) engine's."""
+    cfg = K.TINY["tiny_llama3"]
+    img = K.synth_image(cfg)
+    P = 40
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    _, lg6, _ = K.Engine(img, cfg).prefill(prompt)
+    monkeypatch.setenv("KL_PREFILL_GEMM", "f32")
+    nxt, lg, _ = K.Engine(img, cfg).prefill(prompt)
+    om = O.Model(img, cfg.family, cfg.quant)
+    for pos in range(P - 1):
+        om.step(prompt[pos], pos)
+    ref = om.step(prompt[P - 1], P - 1)
+    assert rel(lg, ref) < LOGIT_RTOL and rel(lg6, ref) < LOGIT_RTOL
+    assert not np.array_equal(lg, lg6)  # the two paths did run
+    assert nxt == int(np.argmax(lg))
 
 
 def _prefill_cfg(K, name):
