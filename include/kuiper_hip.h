@@ -185,25 +185,26 @@ int kl_gemm_q8(const float* A, const int8_t* q, const float* scales, int group_s
 /* fp32 -> three bf16 planes for kl_gemm_x6: x = x0 + x1 + x2 with
  * x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 - x1) (round to nearest
  * even), which hold all 24 significand bits of x.  rows x cols floats (row
- * stride ldx) -> plane p at planes + p * plane_stride bf16 elements, rows of
- * cols.  cols a multiple of 8, ldx of 4, plane_stride of 8 and >= rows *
- * cols; x and planes 16-byte aligned.  No counterpart in the reference: the
- * operand format of the split-product prefill GEMM below. */
-int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, size_t plane_stride,
-                    void* stream);
+ * stride ldx) -> `planes` in the tiled plane format: tiles of 16 rows x 32
+ * columns in row-tile-major order, each tile the three planes' 16 x 32
+ * elements one after another (element (r, k) of plane p at
+ * ((r/16)*(cols/32) + k/32)*1536 + 512*p + 32*(r%16) + k%32).  cols a
+ * multiple of 32, ldx of 4, x and planes 16-byte aligned; planes holds
+ * kl_split_bf16x3_bytes(rows, cols) bytes.  No counterpart in the reference:
+ * the operand format of the split-product prefill GEMM below. */
+size_t kl_split_bf16x3_bytes(int rows, int cols);
+int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, void* stream);
 
-/* C[M x N] (+)= A . W^T (+ bias) from the bf16 planes of A (M rows of lda)
- * and W (N rows of ldw) as kl_split_bf16x3 writes them: the six products
- * Ai Wj^T with i + j <= 2 on the bf16 matrix cores, accumulated in fp32, as
- * accurate as an fp32 GEMM (the terms left out are each below one fp32
- * rounding of |a w|).  The batched form of MatmulLayer (op/matmul.cpp:20)
- * that the prefill runs for fp32 weights.  K a multiple of 32, lda and ldw of
- * 8, plane strides multiples of 8 holding their rows, planes 16-byte aligned.
- * With a workspace the launch divides K among up to 8 slices where that
- * fills the device (it uses at most workspace_bytes; splits * M * N floats
- * per split count); NULL runs one slice. */
-int kl_gemm_x6(const void* a_planes, size_t a_plane_stride, int lda, const void* w_planes,
-               size_t w_plane_stride, int ldw, float* C, int M, int N, int K, int ldc,
+/* C[M x N] (+)= A . W^T (+ bias) from the planes of A (M x K) and W (N x K)
+ * as kl_split_bf16x3 writes them: the six products Ai Wj^T with i + j <= 2 on
+ * the bf16 matrix cores, accumulated in fp32, as accurate as an fp32 GEMM
+ * (the terms left out are each below one fp32 rounding of |a w|).  The
+ * batched form of MatmulLayer (op/matmul.cpp:20) that the prefill runs for
+ * fp32 weights.  K a multiple of 32, planes 16-byte aligned.  With a
+ * workspace the launch divides K among up to 8 slices where that fills the
+ * device (splits * M * N floats, within workspace_bytes); NULL runs one
+ * slice. */
+int kl_gemm_x6(const void* a_planes, const void* w_planes, float* C, int M, int N, int K, int ldc,
                const float* bias, int accumulate, void* workspace, size_t workspace_bytes,
                void* stream);
 

@@ -480,8 +480,7 @@ struct kl_engine {
   // fp32 projection bytes) and of each GEMM input (pf_ax).
   bool pf_x6 = false;
   char* xw_buf = nullptr;
-  void* pf_ax = nullptr;        // 3 planes of pf_rows x max(D, Dq, F) bf16
-  size_t pf_ax_plane = 0;       // elements per plane
+  void* pf_ax = nullptr;        // planes of pf_rows x max(D, Dq, F) (x6_plane_bytes)
   int pf_rows = 0;              // rows the scratch holds
   char* pf_buf = nullptr;       // one allocation for everything below
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr;
@@ -1524,8 +1523,7 @@ int prefill_scratch(kl_engine* e, int rows) {
                                                           2 * static_cast<size_t>(m.F),
                                                           static_cast<size_t>(m.D)}));
   const size_t sz_ws = al(ws_floats * 4);
-  const size_t ax_plane = e->pf_x6 ? R * std::max({m.D, m.Dq, m.F}) : 0;
-  const size_t sz_ax = al(3 * ax_plane * 2);
+  const size_t sz_ax = e->pf_x6 ? al(x6_plane_bytes(rows, std::max({m.D, m.Dq, m.F}))) : 0;
   const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(attn_ws) + al(m.D * 4) +
                        al(m.S * 4) + al(256) + al(am) + sz_ax;
   char* buf = nullptr;
@@ -1555,7 +1553,6 @@ int prefill_scratch(kl_engine* e, int rows) {
   e->pf_am = take(al(am));
   e->pf_am_bytes = am;
   e->pf_ax = sz_ax ? take(sz_ax) : nullptr;
-  e->pf_ax_plane = ax_plane;
   e->pf_rows = rows;
   err = hipMemsetAsync(e->pf_am, 0, am, e->stream);
   if (err != hipSuccess) return rc(err);
@@ -1566,21 +1563,20 @@ int prefill_scratch(kl_engine* e, int rows) {
 int prefill_planes(kl_engine* e) {
   if (!e->pf_x6 || e->xw_buf) return KL_OK;
   const ImageLayout& m = e->lay;
-  const size_t D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F;
-  const size_t per_layer = (Dq + 2 * Dkv) * D + D * Dq + 2 * F * D + D * F;  // elements
+  const int D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F;
+  const size_t per_layer = x6_plane_bytes(Dq, D) + 2 * x6_plane_bytes(Dkv, D) + x6_plane_bytes(D, Dq) +
+                           2 * x6_plane_bytes(F, D) + x6_plane_bytes(D, F);
   char* buf = nullptr;
-  hipError_t err = hipMalloc(&buf, 3 * per_layer * 2 * m.L);
+  hipError_t err = hipMalloc(&buf, per_layer * m.L);
   if (err != hipSuccess) return KL_ENOMEM;
   e->xw_buf = buf;
   hipStream_t hs = static_cast<hipStream_t>(e->stream);
   size_t off = 0;
   int r = KL_OK;
-  auto planes = [&](const WView& w, size_t N, size_t K) -> const void* {
+  auto planes = [&](const WView& w, int N, int K) -> const void* {
     char* dst = buf + off;
-    off += 3 * N * K * 2;
-    if (r == KL_OK)
-      r = split3_run(static_cast<const float*>(w.w), static_cast<int>(N), static_cast<int>(K),
-                     static_cast<int>(K), dst, N * K, hs);
+    off += x6_plane_bytes(N, K);
+    if (r == KL_OK) r = split3_run(static_cast<const float*>(w.w), N, K, K, dst, hs);
     return dst;
   };
   for (int l = 0; l < m.L; ++l) {
@@ -1632,15 +1628,10 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // fp32 weights: the split-product GEMM over bf16 planes of the input
     // (split here) and of the weights (prefill_planes).
     auto x6 = [&](const float* in, int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc) {
-      PF(split3_run(in, n, k, k, e->pf_ax, e->pf_ax_plane, hs));
+      PF(split3_run(in, n, k, k, e->pf_ax, hs));
       GemmX6Planes p{};
       p.A = e->pf_ax;
-      p.a_plane = e->pf_ax_plane;
-      p.lda = k;
-      for (int i = 0; i < nseg; ++i) {
-        p.W[i] = wx[i];
-        p.w_plane[i] = static_cast<size_t>(sg[i].N) * k;
-      }
+      for (int i = 0; i < nseg; ++i) p.W[i] = wx[i];
       PF(gemm_run_x6(p, n, k, nseg, sg, acc, e->pf_ws, e->pf_ws_bytes, hs));
     };
     {

@@ -629,14 +629,18 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
 // Workgroup tile 128 x 128, four waves of 64 x 64 (2 x 2 blocks of 32 x 32;
 // A operand: lane l holds A[l % 32][8 k-values], B operand W[l % 32][the
 // same 8 k-values], k-values 8 (l / 32) .. + 7 of a 16-column step; result
-// register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  K
-// advances in blocks of 32 columns: the six plane tiles of a block (A0 A1 A2
-// W0 W1 W2, 128 rows x 64 B each, 48 KB) land in LDS by direct-to-LDS loads
-// through a 3-stage ring (144 KB: one workgroup per CU), block k + 2
-// requested while block k is computed.  A row holds four 16-byte chunks;
-// chunk c of row r sits in slot c ^ x6_swz(r), so the 32 lanes of a half
-// wave (32 consecutive rows, one chunk each) read 32 distinct 16-byte slots
-// of the 512 B bank period.  Each block runs as two 16-column steps of 24
+// register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  The
+// planes are stored in tiles of 16 rows x 32 columns, the three planes of a
+// tile in 3 KB of consecutive memory (x6_tile_offset), so each 1 KB
+// direct-to-LDS load instruction reads 1 KB of consecutive bytes (rows of 64
+// B in row-major planes touch half of sixteen 128 B lines each: 7-11% slower
+// on the Qwen3-4B and Qwen2.5-1.5B shapes).  K advances in blocks of 32
+// columns: the six plane tiles of a block (A0 A1 A2 W0 W1 W2, 128 rows x 64 B
+// each, 48 KB) land in LDS through a 3-stage ring (144 KB: one workgroup per
+// CU), block k + 2 requested while block k is computed.  A row holds four
+// 16-byte chunks; chunk c of row r sits in slot c ^ x6_swz(r), so the 32
+// lanes of a half wave (32 consecutive rows, one chunk each) read 32 distinct
+// 16-byte slots of the 512 B bank period.  Each block runs as two 16-column steps of 24
 // MFMAs (six products x four blocks); the second step's operands are read
 // from LDS during the first step, the next block's first-step operands
 // during the second (the reads are interleaved one per MFMA).
@@ -647,6 +651,15 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
 // Split-K as k_gemm_f32_dma (blockIdx.y = split, partials to ws, then
 // k_gemm_reduce).
 __device__ __forceinline__ int x6_swz(int r) { return (r >> 3) & 3; }
+
+// Element (r, k) of plane p of an R x K matrix (K a multiple of 32) in the
+// tiled plane format: tiles of 16 rows x 32 columns in row-tile-major order,
+// each holding plane 0, 1, 2 (512 elements each, rows of 32).  A buffer holds
+// ceil(R / 16) * 16 * K * 3 elements; rows past R in the last tile only feed
+// outputs that are never stored.
+__host__ __device__ __forceinline__ size_t x6_tile_offset(int r, int k, int p, int K) {
+  return (static_cast<size_t>(r >> 4) * (K >> 5) + (k >> 5)) * 1536 + 512 * p + 32 * (r & 15) + (k & 31);
+}
 
 typedef __bf16 xbf8 __attribute__((ext_vector_type(8)));
 
@@ -669,25 +682,22 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
   for (int i = 1; i < kGemmMaxSeg; ++i)
     if (i < g.nseg && t >= g.seg[i].tile0) sidx = i;
   const char* W = static_cast<const char*>(x.p.W[0]);
-  size_t wplane = x.p.w_plane[0];
   float* C = g.seg[0].C;
   const float* bias = g.seg[0].bias;
-  int N = g.seg[0].N, ldw = g.seg[0].ldw, ldc = g.seg[0].ldc, tile0 = 0;
+  int N = g.seg[0].N, ldc = g.seg[0].ldc, tile0 = 0;
   size_t wsoff = 0;
 #pragma unroll
   for (int i = 1; i < kGemmMaxSeg; ++i)
     if (i == sidx) {
       W = static_cast<const char*>(x.p.W[i]);
-      wplane = x.p.w_plane[i];
       C = g.seg[i].C;
       bias = g.seg[i].bias;
       N = g.seg[i].N;
-      ldw = g.seg[i].ldw;
       ldc = g.seg[i].ldc;
       tile0 = g.seg[i].tile0;
       wsoff = g.seg[i].wsoff;
     }
-  const int M = g.M, K = g.K, lda = x.p.lda;
+  const int M = g.M, K = g.K;
   const int local = t - tile0;
   const int tm = local % g.tiles_m, tn = local / g.tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
@@ -695,27 +705,31 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
   const int kb0 = static_cast<int>(blockIdx.y) * nkt / g.splits;
   const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
   const char* A = static_cast<const char*>(x.p.A);
-  const size_t aplane = x.p.a_plane;
 
   // Load instruction i of this wave fills 1 KB j = 12 wave + i of a stage:
-  // plane tile j / 8, rows 16 (j % 8) .. + 15; lane l fills slot l % 4 of row
-  // r = 16 (j % 8) + l / 4 with chunk (l % 4) ^ x6_swz(r).  Rows past M or N
-  // read the last row (they only feed outputs that are never stored).
+  // plane (j / 8) % 3 of operand j < 24 ? A : W, rows 16 (j % 8) .. + 15 of
+  // the workgroup tile (one 16-row tile of the plane format: 1 KB of
+  // consecutive bytes per k block, the next k block 3 KB further on); lane l
+  // fills slot l % 4 of row r = 16 (j % 8) + l / 4 with chunk
+  // (l % 4) ^ x6_swz(r).  Row tiles past M or N read the last one (they only
+  // feed outputs that are never stored).
   const char* src[LPW];
+  const int kbs = K / BK;
+  const int lra = (M - 1) >> 4, lrw = (N - 1) >> 4;
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
     const int j = LPW * wave + i;
     const int pt = j >> 3;
-    const int r = 16 * (j & 7) + (lane >> 2);
-    const int c = (lane & 3) ^ x6_swz(r);
-    src[i] = pt < 3 ? A + (pt * aplane + static_cast<size_t>(min(m0 + r, M - 1)) * lda) * 2 + 16 * c
-                    : W + ((pt - 3) * wplane + static_cast<size_t>(min(n0 + r, N - 1)) * ldw) * 2 + 16 * c;
+    const int c = (lane & 3) ^ x6_swz(16 * (j & 7) + (lane >> 2));
+    const int rt = pt < 3 ? min((m0 >> 4) + (j & 7), lra) : min((n0 >> 4) + (j & 7), lrw);
+    src[i] = (pt < 3 ? A : W) + (static_cast<size_t>(rt) * kbs * 1536 + 512 * (pt % 3)) * 2 +
+             64 * (lane >> 2) + 16 * c;
   }
   auto request = [&](int kb, int st) {
     __bf16* base = L + st * SS;
 #pragma unroll
     for (int i = 0; i < LPW; ++i)
-      __builtin_amdgcn_global_load_lds((global_void_t*)(src[i] + static_cast<size_t>(kb) * BK * 2),
+      __builtin_amdgcn_global_load_lds((global_void_t*)(src[i] + static_cast<size_t>(kb) * 3072),
                                        (lds_void_t*)(base + 512 * (LPW * wave + i)), 16, 0, 0);
   };
   // Step s of a block: lane half h = l / 32 reads chunk 2 s + h of rows
@@ -826,10 +840,10 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
       }
 }
 
-// fp32 rows -> three bf16 planes x0, x1, x2 (k_gemm_x6): row r of plane p at
-// out + p * plane + r * cols; eight values per thread.
+// fp32 rows -> the three bf16 planes x0, x1, x2 of k_gemm_x6 in the tiled
+// plane format (x6_tile_offset); eight values per thread.
 __global__ void k_split3(const float* __restrict__ x, int rows, int cols, int ldx,
-                         __bf16* __restrict__ out, size_t plane) {
+                         __bf16* __restrict__ out) {
   const int c8 = cols / 8;
   const size_t total = static_cast<size_t>(rows) * c8;
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
@@ -847,10 +861,10 @@ __global__ void k_split3(const float* __restrict__ x, int rows, int cols, int ld
       x1[j] = static_cast<__bf16>(r1);
       x2[j] = static_cast<__bf16>(r1 - static_cast<float>(x1[j]));
     }
-    const size_t o = static_cast<size_t>(r) * cols + c;
+    const size_t o = x6_tile_offset(r, c, 0, cols);
     *reinterpret_cast<xbf8*>(out + o) = x0;
-    *reinterpret_cast<xbf8*>(out + plane + o) = x1;
-    *reinterpret_cast<xbf8*>(out + 2 * plane + o) = x2;
+    *reinterpret_cast<xbf8*>(out + o + 512) = x1;
+    *reinterpret_cast<xbf8*>(out + o + 1024) = x2;
   }
 }
 

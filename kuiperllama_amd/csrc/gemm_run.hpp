@@ -37,15 +37,12 @@ struct GemmArgs {
   int splits;
 };
 
-// Operands of the split-product GEMM (k_gemm_x6): A and every W_s as three
-// bf16 planes (k_split3), plane p at base + p * plane elements, rows of lda
-// (A) and seg[s].ldw (W_s) elements.
+// Operands of the split-product GEMM (k_gemm_x6): A (M x K) and every W_s
+// (N_s x K) as three bf16 planes in the tiled plane format of k_split3
+// (x6_tile_offset, gemm.hpp).
 struct GemmX6Planes {
   const void* A;
-  size_t a_plane;
-  int lda;
   const void* W[kGemmMaxSeg];
-  size_t w_plane[kGemmMaxSeg];
 };
 
 struct GemmX6Args {
@@ -62,14 +59,17 @@ int gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* seg
              float* ws, int splits, hipStream_t st);
 
 // Host launcher (ops.hip) of k_gemm_x6: the same products from bf16 planes
-// (segs[s].W unused).  K a multiple of 32.  Chooses the split count itself
-// (up to 8, where ws_bytes holds splits * M * (N_0 + ...) floats).
+// (segs[s].W and ldw unused).  K a multiple of 32.  Chooses the split count
+// itself (up to 8, where ws_bytes holds splits * M * (N_0 + ...) floats).
 int gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSeg* segs,
                 int accumulate, float* ws, size_t ws_bytes, hipStream_t st);
 
-// Host launcher (ops.hip) of k_split3: rows x cols fp32 (stride ldx) into
-// three bf16 planes of rows x cols (plane stride `plane` elements).
-int split3_run(const float* x, int rows, int cols, int ldx, void* planes, size_t plane,
-               hipStream_t st);
+// Host launcher (ops.hip) of k_split3: rows x cols fp32 (stride ldx, cols a
+// multiple of 32) into the tiled planes (x6_plane_bytes(rows, cols) bytes).
+int split3_run(const float* x, int rows, int cols, int ldx, void* planes, hipStream_t st);
+
+inline size_t x6_plane_bytes(int rows, int cols) {
+  return static_cast<size_t>((rows + 15) / 16) * 16 * cols * 3 * 2;
+}
 
 }  // namespace kl

@@ -1040,11 +1040,8 @@ int x6_splits(long long tiles, int nkt, size_t mn, size_t ws_floats) {
 
 int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSeg* segs,
                     int accumulate, float* ws, size_t ws_bytes, hipStream_t st) {
-  if (!planes.A || M <= 0 || K <= 0 || nseg < 1 || nseg > kGemmMaxSeg || planes.lda < K)
-    return KL_EINVAL;
-  if (K % 32 || planes.lda % 8 || planes.a_plane % 8 || !aligned16(planes.A)) return KL_EUNSUPP;
-  // Every plane must hold its rows (the kernel reads three planes of each).
-  if (planes.a_plane < static_cast<size_t>(M - 1) * planes.lda + K) return KL_EINVAL;
+  if (!planes.A || M <= 0 || K <= 0 || nseg < 1 || nseg > kGemmMaxSeg) return KL_EINVAL;
+  if (K % 32 || !aligned16(planes.A)) return KL_EUNSUPP;
   GemmArgs g{};
   g.M = M;
   g.K = K;
@@ -1058,9 +1055,8 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
   size_t wsoff = 0;
   for (int i = 0; i < nseg; ++i) {
     const GemmSeg& sg = segs[i];
-    if (!planes.W[i] || !sg.C || sg.N <= 0 || sg.ldw < K || sg.ldc < sg.N || sg.S) return KL_EINVAL;
-    if (sg.ldw % 8 || planes.w_plane[i] % 8 || !aligned16(planes.W[i])) return KL_EUNSUPP;
-    if (planes.w_plane[i] < static_cast<size_t>(sg.N - 1) * sg.ldw + K) return KL_EINVAL;
+    if (!planes.W[i] || !sg.C || sg.N <= 0 || sg.ldc < sg.N || sg.S) return KL_EINVAL;
+    if (!aligned16(planes.W[i])) return KL_EUNSUPP;
     g.seg[i] = sg;
     g.seg[i].tile0 = static_cast<int>(tiles);
     g.seg[i].wsoff = wsoff;
@@ -1081,38 +1077,34 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
   return launch_rc();
 }
 
-int kl::split3_run(const float* x, int rows, int cols, int ldx, void* planes, size_t plane,
-                   hipStream_t st) {
+int kl::split3_run(const float* x, int rows, int cols, int ldx, void* planes, hipStream_t st) {
   if (!x || !planes || rows <= 0 || cols <= 0 || ldx < cols) return KL_EINVAL;
-  if (cols % 8 || ldx % 4 || plane % 8 || plane < static_cast<size_t>(rows) * cols || !aligned16(x) ||
-      !aligned16(planes))
-    return KL_EUNSUPP;
+  if (cols % 32 || ldx % 4 || !aligned16(x) || !aligned16(planes)) return KL_EUNSUPP;
   const size_t work = static_cast<size_t>(rows) * (cols / 8);
   const int grid = static_cast<int>(std::min<size_t>((work + 255) / 256, 8192));
   hipLaunchKernelGGL(k_split3, dim3(grid), dim3(256), 0, st, x, rows, cols, ldx,
-                     static_cast<__bf16*>(planes), plane);
+                     static_cast<__bf16*>(planes));
   return launch_rc();
 }
 
 extern "C" {
 
-int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, size_t plane_stride,
-                    void* stream) {
-  return split3_run(x, rows, cols, ldx, planes, plane_stride, as_stream(stream));
+size_t kl_split_bf16x3_bytes(int rows, int cols) {
+  return rows > 0 && cols > 0 ? x6_plane_bytes(rows, cols) : 0;
 }
 
-int kl_gemm_x6(const void* a_planes, size_t a_plane_stride, int lda, const void* w_planes,
-               size_t w_plane_stride, int ldw, float* C, int M, int N, int K, int ldc,
+int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, void* stream) {
+  return split3_run(x, rows, cols, ldx, planes, as_stream(stream));
+}
+
+int kl_gemm_x6(const void* a_planes, const void* w_planes, float* C, int M, int N, int K, int ldc,
                const float* bias, int accumulate, void* workspace, size_t workspace_bytes,
                void* stream) {
-  if (!C || N <= 0 || ldw < K || ldc < N) return KL_EINVAL;
+  if (!C || N <= 0 || ldc < N) return KL_EINVAL;
   GemmX6Planes p{};
   p.A = a_planes;
-  p.a_plane = a_plane_stride;
-  p.lda = lda;
   p.W[0] = w_planes;
-  p.w_plane[0] = w_plane_stride;
-  const GemmSeg sg{nullptr, C, bias, N, ldw, ldc, 0};
+  const GemmSeg sg{nullptr, C, bias, N, K, ldc, 0};
   return gemm_run_x6(p, M, K, 1, &sg, accumulate, static_cast<float*>(workspace), workspace_bytes,
                      as_stream(stream));
 }

@@ -50,8 +50,9 @@ def test_host_side_argument_checks(K):
     bad = np.zeros(64, np.uint8)
     h = C.c_void_p()
     assert lib.kl_engine_create(bad.ctypes.data, 8, 0, 0, C.byref(h)) == -3
-    assert lib.kl_split_bf16x3(None, 4, 8, 8, None, 32, None) == -1
-    assert lib.kl_gemm_x6(None, 0, 32, None, 0, 32, None, 4, 4, 32, 4, None, 0, None, 0, None) == -1
+    assert lib.kl_split_bf16x3(None, 4, 32, 32, None, None) == -1
+    assert lib.kl_split_bf16x3_bytes(17, 64) == 32 * 64 * 6 and lib.kl_split_bf16x3_bytes(0, 64) == 0
+    assert lib.kl_gemm_x6(None, None, None, 4, 4, 32, 4, None, 0, None, 0, None) == -1
     rd, cp = C.c_float(0), C.c_float(0)
     assert lib.kl_hbm_probe(1 << 19, 1, C.byref(rd), C.byref(cp)) == -1  # under 1 MiB
     assert lib.kl_hbm_probe(1 << 20, 0, C.byref(rd), C.byref(cp)) == -1  # no passes

@@ -135,30 +135,36 @@ def _as_f32(u16):
     return (u16.astype(np.uint32) << 16).view(np.float32)
 
 
-def _split_dev(K, X, pad_rows=0):
-    """kl_split_bf16x3 of X (rows x cols, row stride cols + 4) into planes of
-    (rows + pad_rows) x cols; returns the plane array and its stride."""
+def _untile(buf, rows, cols):
+    """Planes [3][rows][cols] from the tiled plane format: tiles of 16 rows x
+    32 columns, row-tile-major, each tile plane 0, 1, 2 of 16 x 32 in turn."""
+    rt, kt = (rows + 15) // 16, cols // 32
+    t = buf[: rt * kt * 1536].reshape(rt, kt, 3, 16, 32)
+    return t.transpose(2, 0, 3, 1, 4).reshape(3, rt * 16, cols)[:, :rows]
+
+
+def _split_dev(K, X):
+    """kl_split_bf16x3 of X (rows x cols, row stride cols + 4)."""
     rows, cols = X.shape
     Xp = np.zeros((rows, cols + 4), np.float32)
     Xp[:, :cols] = X
     dX = D(K, Xp)
-    plane = (rows + pad_rows) * cols
-    dP = K.DeviceArray(3 * plane, np.uint16)
-    ok(K.lib.kl_split_bf16x3(dX.ptr, rows, cols, cols + 4, dP.ptr, plane, None), "split")
-    return dP, plane
+    nbytes = K.lib.kl_split_bf16x3_bytes(rows, cols)
+    assert nbytes == ((rows + 15) // 16) * 16 * cols * 6
+    dP = K.DeviceArray(nbytes // 2, np.uint16)
+    ok(K.lib.kl_split_bf16x3(dX.ptr, rows, cols, cols + 4, dP.ptr, None), "split")
+    return dP
 
 
 def test_split_bf16x3_bit_exact(K, gpu):
     rng = np.random.default_rng(11)
-    rows, cols = 37, 264
+    rows, cols = 37, 256
     X = (rng.standard_normal((rows, cols)) * 10.0 ** rng.integers(-20, 20, (rows, cols))).astype(np.float32)
     X[0, :8] = [0.0, -0.0, 1.0, -1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -9, 3.0e38, -1.5e-30]
-    dP, plane = _split_dev(K, X)
-    got = dP.numpy()
+    got = _untile(_split_dev(K, X).numpy(), rows, cols)
     refs = _split3_ref(X)
     for p in range(3):
-        g = _as_f32(got[p * plane:(p + 1) * plane].reshape(rows, cols))
-        assert np.array_equal(g.view(np.uint32), refs[p].view(np.uint32)), f"plane {p}"
+        assert np.array_equal(_as_f32(got[p]).view(np.uint32), refs[p].view(np.uint32)), f"plane {p}"
     # the planes hold x exactly (24 significand bits in 8 + 8 + 8)
     x0, x1, x2 = (r.astype(np.float64) for r in refs)
     finite = np.abs(X) < 1e37
@@ -168,14 +174,13 @@ def test_split_bf16x3_bit_exact(K, gpu):
 def gemm_x6(K, A, W, bias=None, C0=None, ws=True):
     M, Kd = A.shape
     N = W.shape[0]
-    dA, ap = _split_dev(K, A, pad_rows=3)
-    dW, wp = _split_dev(K, W)
+    dA, dW = _split_dev(K, A), _split_dev(K, W)
     dC = D(K, C0) if C0 is not None else K.DeviceArray(M * N)
     db = D(K, bias) if bias is not None else None
     wsa = K.DeviceArray(8 * M * N) if ws else None
-    ok(K.lib.kl_gemm_x6(dA.ptr, ap, Kd, dW.ptr, wp, Kd, dC.ptr, M, N, Kd, N,
-                        db.ptr if db else None, int(C0 is not None), wsa.ptr if wsa else None,
-                        wsa.nbytes if wsa else 0, None), "kl_gemm_x6")
+    ok(K.lib.kl_gemm_x6(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, N, db.ptr if db else None,
+                        int(C0 is not None), wsa.ptr if wsa else None, wsa.nbytes if wsa else 0,
+                        None), "kl_gemm_x6")
     return dC.numpy().reshape(M, N)
 
 
@@ -239,13 +244,13 @@ def test_gemm_x6_bias_accumulate_and_refusals(K, O, gpu):
     ya = gemm_x6(K, A, W, C0=C0)
     assert np.max(np.abs(yb - (exact + b)) / (mag + np.abs(b))) <= X6_TOL
     assert np.max(np.abs(ya - (exact + C0)) / (mag + np.abs(C0))) <= X6_TOL
-    dP, plane = _split_dev(K, A)
+    dP = _split_dev(K, A)
     dC = K.DeviceArray(M * N)
-    # K not a multiple of 32, a plane too short for its rows
-    assert K.lib.kl_gemm_x6(dP.ptr, plane, 80, dP.ptr, plane, 80, dC.ptr, M, N, 80, N, None, 0,
-                            None, 0, None) == -4
-    assert K.lib.kl_gemm_x6(dP.ptr, plane - 8, Kd, dP.ptr, plane, Kd, dC.ptr, M, M, Kd, N, None, 0,
-                            None, 0, None) == -1
+    # K not a multiple of 32; ldc < N; a missing operand (all refused before any launch)
+    assert K.lib.kl_gemm_x6(dP.ptr, dP.ptr, dC.ptr, M, N, 80, N, None, 0, None, 0, None) == -4
+    assert K.lib.kl_gemm_x6(dP.ptr, dP.ptr, dC.ptr, M, N, Kd, N - 1, None, 0, None, 0, None) == -1
+    assert K.lib.kl_gemm_x6(dP.ptr, None, dC.ptr, M, N, Kd, N, None, 0, None, 0, None) == -1
+    assert K.lib.kl_split_bf16x3(dC.ptr, M, 80, 80, dP.ptr, None) == -4  # cols % 32
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
