@@ -20,9 +20,12 @@ on both sides.  Prints one JSON line.
                  multi the W1/W3 + SwiGLU GEMV, timed with HIP events around
                  each of its launches in the profile steps
   prefill        the batched prompt prefill of cfg 5 (Qwen3-4B shape, 512
-                 tokens) on the matrix cores: prompt tok/s, TFLOP/s against the
-                 fp32 MFMA peak, and the MFMA-busy fraction rocprofv3 measured
-                 for the same command (profiles/prefill_qwen3_4b_pmc.txt)
+                 tokens) on the matrix cores: prompt tok/s, algorithmic
+                 TFLOP/s, the fraction of its matrix-core roofline (fp32
+                 projections as six bf16 products each at the bf16 peak,
+                 attention at the fp32 peak), and the MFMA-busy fraction
+                 rocprofv3 measured for the same command
+                 (profiles/prefill_qwen3_4b_pmc.txt)
   configs        the other four BASELINE configs, each a short decode leg of
                  its own workload (prompt via the batched prefill, then
                  --config-steps timed steps): tok/s, ms per step, GB/s and the
@@ -86,6 +89,7 @@ def measured_traffic(kernel: str, config: str, mode: str):
 
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def measured_mfma_busy(config: str):
@@ -110,8 +114,12 @@ def measured_mfma_busy(config: str):
 
 def measure_prefill(K, cfg, eng=None, reps: int = 3) -> dict:
     """Batched prefill of the config's prompt (kl_engine_prefill), device time
-    from HIP events inside the call; best of `reps` after one warm-up.  The
-    roofline is the fp32 matrix-core peak."""
+    from HIP events inside the call; best of `reps` after one warm-up.
+    `tflops` counts the algorithmic fp32 flops.  The roofline is the time the
+    matrix cores would need at their peaks: fp32 projections run as six bf16
+    products per multiply-add (kl_gemm_x6) at the bf16 peak, int8 ones and
+    the attention and classifier at the fp32 peak; `frac` = that time over
+    the measured one."""
     if eng is None:
         eng = K.Engine(K.synth_image(cfg), cfg)
     prompt = K.prompt_tokens(cfg)
@@ -119,12 +127,17 @@ def measure_prefill(K, cfg, eng=None, reps: int = 3) -> dict:
     eng.prefill(prompt, want_logits=False)
     times = [eng.prefill(prompt, want_logits=False)[2] for _ in range(reps)]
     ms = min(times)
-    fl = cfg.prefill_flops(P)
+    proj, attn, cls = cfg.prefill_flops_parts(P)
+    fl = proj + attn + cls
     tf = fl / (ms / 1e3) / 1e12
+    x6 = not cfg.quant and os.environ.get("KL_PREFILL_GEMM") != "f32"
+    roof_ms = ((6 * proj / MFMA_BF16_PEAK_TFLOPS if x6 else proj / MFMA_FP32_PEAK_TFLOPS) +
+               (attn + cls) / MFMA_FP32_PEAK_TFLOPS) / 1e9
     return {"config": cfg.name, "tokens": P, "ms": round(ms, 3),
-            "tok_s": round(P / (ms / 1e3), 1), "tflops": round(tf, 2),
-            "bound": "mfma", "peak_tflops": MFMA_FP32_PEAK_TFLOPS,
-            "frac": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "flops": int(fl),
+            "tok_s": round(P / (ms / 1e3), 1), "tflops": round(tf, 2), "flops": int(fl),
+            "gemm": "bf16x6 split products, fp32 accumulate" if x6 else "fp32 MFMA",
+            "bound": "mfma", "roofline_ms": round(roof_ms, 3), "frac": round(roof_ms / ms, 4),
+            "peak_tflops": {"bf16": MFMA_BF16_PEAK_TFLOPS, "fp32": MFMA_FP32_PEAK_TFLOPS},
             "dtype": "int8w-f32" if cfg.quant else "f32", "mfma_busy": measured_mfma_busy(cfg.name)}
 
 

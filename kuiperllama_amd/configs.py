@@ -100,10 +100,14 @@ class Config:
         row), causal attention (q.k and p.v over t <= position: 4 * heads *
         head_size * (pos + 1) per position and layer) and the classifier of
         the last position."""
+        return sum(self.prefill_flops_parts(n))
+
+    def prefill_flops_parts(self, n: int):
+        """prefill_flops as (projections, attention, classifier)."""
         D, Dq, Dkv, F, L = self.dim, self.qd, self.kv_dim, self.hidden_dim, self.layers
         proj = L * (Dq * D + 2 * Dkv * D + D * Dq + 3 * F * D)
         attn = L * 4 * self.heads * self.head_size * (n * (n + 1) // 2)
-        return 2 * proj * n + attn + 2 * self.vocab * D
+        return 2 * proj * n, attn, 2 * self.vocab * D
 
     def decode_bytes(self, first_pos: int, steps: int) -> int:
         """Algorithmic HBM bytes of `steps` decode steps at positions
