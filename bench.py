@@ -117,8 +117,10 @@ def measure_prefill(K, cfg, eng=None, reps: int = 3) -> dict:
     from HIP events inside the call; best of `reps` after one warm-up.
     `tflops` counts the algorithmic fp32 flops.  The roofline is the time the
     matrix cores would need at their peaks: fp32 projections run as six bf16
-    products per multiply-add (kl_gemm_x6) at the bf16 peak, int8 ones and
-    the attention and classifier at the fp32 peak; `frac` = that time over
+    products per multiply-add (kl_gemm_x6) at the bf16 peak; int8 ones on
+    prompts of at most 32 rows (kl_gemm_q8s) as three bf16 products, or the
+    int8 weight bytes at 8 TB/s where that is longer; other int8 ones, the
+    attention and the classifier at the fp32 peak; `frac` = that time over
     the measured one."""
     if eng is None:
         eng = K.Engine(K.synth_image(cfg), cfg)
@@ -130,12 +132,24 @@ def measure_prefill(K, cfg, eng=None, reps: int = 3) -> dict:
     proj, attn, cls = cfg.prefill_flops_parts(P)
     fl = proj + attn + cls
     tf = fl / (ms / 1e3) / 1e12
-    x6 = not cfg.quant and os.environ.get("KL_PREFILL_GEMM") != "f32"
-    roof_ms = ((6 * proj / MFMA_BF16_PEAK_TFLOPS if x6 else proj / MFMA_FP32_PEAK_TFLOPS) +
-               (attn + cls) / MFMA_FP32_PEAK_TFLOPS) / 1e9
+    fp32_gemm = os.environ.get("KL_PREFILL_GEMM") == "f32"
+    x6 = not cfg.quant and not fp32_gemm
+    q8s = cfg.quant and not fp32_gemm and P <= 32 and cfg.group_size in (32, 64)
+    if x6:
+        gemm, proj_ms = "bf16x6 split products, fp32 accumulate", 6 * proj / MFMA_BF16_PEAK_TFLOPS / 1e9
+    elif q8s:
+        # three bf16 products per multiply-add, or the int8 weight bytes at 8 TB/s
+        D, Dq, Dkv, F, L = cfg.dim, cfg.qd, cfg.kv_dim, cfg.hidden_dim, cfg.layers
+        mats = L * (Dq * D + 2 * Dkv * D + D * Dq + 3 * F * D)
+        wbytes = mats + mats // cfg.group_size * 4
+        gemm = "int8 weights x bf16x3 activations (k_gemm_q8s), fp32 accumulate"
+        proj_ms = max(3 * proj / MFMA_BF16_PEAK_TFLOPS / 1e9, wbytes / HBM_PEAK_GBPS / 1e6)
+    else:
+        gemm, proj_ms = "fp32 MFMA" + (" (int8 dequantised)" if cfg.quant else ""), proj / MFMA_FP32_PEAK_TFLOPS / 1e9
+    roof_ms = proj_ms + (attn + cls) / MFMA_FP32_PEAK_TFLOPS / 1e9
     return {"config": cfg.name, "tokens": P, "ms": round(ms, 3),
             "tok_s": round(P / (ms / 1e3), 1), "tflops": round(tf, 2), "flops": int(fl),
-            "gemm": "bf16x6 split products, fp32 accumulate" if x6 else "fp32 MFMA",
+            "gemm": gemm,
             "bound": "mfma", "roofline_ms": round(roof_ms, 3), "frac": round(roof_ms / ms, 4),
             "peak_tflops": {"bf16": MFMA_BF16_PEAK_TFLOPS, "fp32": MFMA_FP32_PEAK_TFLOPS},
             "dtype": "int8w-f32" if cfg.quant else "f32", "mfma_busy": measured_mfma_busy(cfg.name)}

@@ -208,6 +208,26 @@ int kl_gemm_x6(const void* a_planes, const void* w_planes, float* C, int M, int 
                const float* bias, int accumulate, void* workspace, size_t workspace_bytes,
                void* stream);
 
+/* MatmulKernelQuant (KI:12-14; cuda/matmul_kernel.cu:111-134) for prompts of
+ * at most 32 rows, bound by the int8 weight bytes: the weights prepacked once
+ * (kl_q8s_pack: q int8 [N x K] dense rows, scales[(n*K + k) / group_size],
+ * group_size 32 or 64 dividing K, into kl_q8s_packed_bytes bytes,
+ * 16-byte aligned), then C[M x N] (+)= A . dequant(q)^T (+ bias) as sum over
+ * groups of scale * (sum of a*q over the group): A as three bf16 planes and q
+ * exactly in bf16, three products per multiply-add on the bf16 matrix cores,
+ * fp32 accumulation (as accurate as the fp32 GEMM).  The workspace holds A's
+ * planes (K * 192 bytes, else KL_EWORKSPACE) and, beyond them (at the next
+ * 256-byte boundary), split-K partials where they fit (splits * M * N
+ * floats); a split holds at most 832 columns of K, so K > 832 needs room for
+ * ceil(K / 832) splits or more (else KL_EWORKSPACE).  M <= 32.  No
+ * counterpart of the packed format in the reference. */
+size_t kl_q8s_packed_bytes(int N, int K, int group_size);
+int kl_q8s_pack(const int8_t* q, const float* scales, int N, int K, int group_size, void* packed,
+                void* stream);
+int kl_gemm_q8s(const float* A, int M, int K, int lda, const void* packed, int N, int group_size,
+                float* C, int ldc, const float* bias, int accumulate, void* workspace,
+                size_t workspace_bytes, void* stream);
+
 /* RoPEKernel (KI:36-39) on n_pos rows: row r of q (stride ldq) and of k
  * (stride ldk) rotated at position pos0 + r. */
 int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ldq, float* k,

@@ -99,6 +99,9 @@ _SIGS = {
     "kl_split_bf16x3_bytes": (_sz, [_i, _i]),
     "kl_split_bf16x3": (_i, [_p, _i, _i, _i, _p, _p]),
     "kl_gemm_x6": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _i, _p, _sz, _p]),
+    "kl_q8s_packed_bytes": (_sz, [_i, _i, _i]),
+    "kl_q8s_pack": (_i, [_p, _p, _i, _i, _i, _p, _p]),
+    "kl_gemm_q8s": (_i, [_p, _i, _i, _i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),
     "kl_rope_rows": (_i, [_i, _i, _i, _i, _p, _i, _p, _i, _i, _i, _p, _p, _p]),
     "kl_attn_prefill": (_i, [_i, _i, _i, _i, _i, _p, _i, _p, _p, _i, _p, _i, _p]),
     "kl_hbm_probe": (_i, [C.c_size_t, _i, _fp, _fp]),

@@ -479,6 +479,10 @@ struct kl_engine {
   // bf16 planes of the weights (xw_buf, built on the first prefill, 1.5x the
   // fp32 projection bytes) and of each GEMM input (pf_ax).
   bool pf_x6 = false;
+  // int8 images: chunks of at most 32 rows run k_gemm_q8s over the
+  // projections prepacked into xw_buf (built on the first such prefill; the
+  // int8 bytes plus the scales again), the GEMM inputs split into pf_ax.
+  bool pf_q8s = false;
   char* xw_buf = nullptr;
   void* pf_ax = nullptr;        // planes of pf_rows x max(D, Dq, F) (x6_plane_bytes)
   int pf_rows = 0;              // rows the scratch holds
@@ -1153,6 +1157,9 @@ int kl_engine_create(const void* image, size_t bytes, int family, int quant, kl_
     const char* env = std::getenv("KL_PREFILL_GEMM");
     e->pf_x6 = !quant && lay.D % 32 == 0 && lay.Dq % 32 == 0 && lay.F % 32 == 0 &&
                !(env && std::strcmp(env, "f32") == 0);
+    const int gs = lay.gs;
+    e->pf_q8s = quant && (gs == 32 || gs == 64) && lay.D % gs == 0 && lay.Dq % gs == 0 &&
+                lay.F % gs == 0 && !(env && std::strcmp(env, "f32") == 0);
   }
   int dev = 0;
   hipDeviceProp_t prop;
@@ -1523,7 +1530,8 @@ int prefill_scratch(kl_engine* e, int rows) {
                                                           2 * static_cast<size_t>(m.F),
                                                           static_cast<size_t>(m.D)}));
   const size_t sz_ws = al(ws_floats * 4);
-  const size_t sz_ax = e->pf_x6 ? al(x6_plane_bytes(rows, std::max({m.D, m.Dq, m.F}))) : 0;
+  const int kmax = std::max({m.D, m.Dq, m.F});
+  const size_t sz_ax = e->pf_x6 ? al(x6_plane_bytes(rows, kmax)) : e->pf_q8s ? al(q8s_aplane_bytes(kmax)) : 0;
   const size_t total = 2 * sz_x + 2 * sz_q + 2 * sz_h + sz_ws + al(attn_ws) + al(m.D * 4) +
                        al(m.S * 4) + al(256) + al(am) + sz_ax;
   char* buf = nullptr;
@@ -1559,10 +1567,41 @@ int prefill_scratch(kl_engine* e, int rows) {
   return KL_OK;
 }
 
-// Builds the bf16 planes of every layer's fp32 projections (once).
-int prefill_planes(kl_engine* e) {
-  if (!e->pf_x6 || e->xw_buf) return KL_OK;
+// Builds the bf16 planes of every layer's fp32 projections, or the packed
+// int8 projections where a chunk of `last_rows` (<= 32) rows will use them
+// (once).
+int prefill_planes(kl_engine* e, int last_rows) {
+  if (e->xw_buf) return KL_OK;
   const ImageLayout& m = e->lay;
+  if (e->pf_q8s && last_rows <= 32) {
+    const int D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F, gs = m.gs;
+    auto pb = [&](int N, int K) { return (q8s_packed_bytes(N, K, gs) + 255) & ~size_t(255); };
+    const size_t per_layer = pb(Dq, D) + 2 * pb(Dkv, D) + pb(D, Dq) + 2 * pb(F, D) + pb(D, F);
+    char* buf = nullptr;
+    if (hipMalloc(&buf, per_layer * m.L) != hipSuccess) return KL_ENOMEM;
+    e->xw_buf = buf;
+    hipStream_t hs = static_cast<hipStream_t>(e->stream);
+    size_t off = 0;
+    int r = KL_OK;
+    auto pack = [&](const WView& w, int N, int K) -> const void* {
+      char* dst = buf + off;
+      off += (q8s_packed_bytes(N, K, gs) + 255) & ~size_t(255);
+      if (r == KL_OK) r = q8s_pack_run(static_cast<const int8_t*>(w.w), w.s, N, K, gs, dst, hs);
+      return dst;
+    };
+    for (int l = 0; l < m.L; ++l) {
+      LayerDev& Ld = e->layers[l];
+      Ld.xp.q = pack(Ld.wq, Dq, D);
+      Ld.xp.k = pack(Ld.wk, Dkv, D);
+      Ld.xp.v = pack(Ld.wv, Dkv, D);
+      Ld.xp.o = pack(Ld.wo, D, Dq);
+      Ld.xp.w1 = pack(Ld.w1, F, D);
+      Ld.xp.w2 = pack(Ld.w2, D, F);
+      Ld.xp.w3 = pack(Ld.w3, F, D);
+    }
+    return r;
+  }
+  if (!e->pf_x6) return KL_OK;
   const int D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F;
   const size_t per_layer = x6_plane_bytes(Dq, D) + 2 * x6_plane_bytes(Dkv, D) + x6_plane_bytes(D, Dq) +
                            2 * x6_plane_bytes(F, D) + x6_plane_bytes(D, F);
@@ -1627,18 +1666,31 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     };
     // fp32 weights: the split-product GEMM over bf16 planes of the input
     // (split here) and of the weights (prefill_planes).
+    // int8 weights, at most 32 rows: k_gemm_q8s over the packed weights.
+    const bool q8s = e->pf_q8s && n <= 32 && e->xw_buf;
     auto x6 = [&](const float* in, int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc) {
+      if (q8s) {
+        PF(q8s_split_run(in, n, k, k, e->pf_ax, hs));
+        GemmSeg s2[kGemmMaxSeg];
+        for (int i = 0; i < nseg; ++i) {
+          s2[i] = sg[i];
+          s2[i].W = wx[i];
+        }
+        PF(gemm_run_q8s(e->pf_ax, n, k, m.gs, nseg, s2, acc, e->pf_ws, e->pf_ws_bytes, hs));
+        return;
+      }
       PF(split3_run(in, n, k, k, e->pf_ax, hs));
       GemmX6Planes p{};
       p.A = e->pf_ax;
       for (int i = 0; i < nseg; ++i) p.W[i] = wx[i];
       PF(gemm_run_x6(p, n, k, nseg, sg, acc, e->pf_ws, e->pf_ws_bytes, hs));
     };
+    const bool fast = e->pf_x6 || q8s;
     {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
-      if (e->pf_x6) {
+      if (fast) {
         const void* wx[3] = {Ld.xp.q, Ld.xp.k, Ld.xp.v};
         x6(e->pf_xn, D, 3, sg, wx, 0);
       } else {
@@ -1662,7 +1714,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
                           e->pf_aws, e->pf_aws_bytes, st));
     {
       const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
-      if (e->pf_x6) {
+      if (fast) {
         x6(e->pf_att, Dq, 1, &sg, &Ld.xp.o, 1);
       } else {
         const int sp = splits_for(D, Dq, false);
@@ -1674,7 +1726,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     {
       const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
-      if (e->pf_x6) {
+      if (fast) {
         const void* wx[2] = {Ld.xp.w1, Ld.xp.w3};
         x6(e->pf_xn, D, 2, sg, wx, 0);
       } else {
@@ -1685,7 +1737,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
     {
       const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
-      if (e->pf_x6) {
+      if (fast) {
         x6(e->pf_h1, F, 1, &sg, &Ld.xp.w2, 1);
       } else {
         const int sp = splits_for(D, F, false);
@@ -1717,7 +1769,7 @@ int kl_engine_prefill(kl_engine* e, const int32_t* prompt, int P, int32_t* next,
     if (prompt[i] < 0 || prompt[i] >= m.V) return KL_ETOKEN;
   if (!prefill_supported(e)) return KL_EUNSUPP;
   int r = prefill_scratch(e, std::min(P, kPrefillChunk));
-  if (r == KL_OK) r = prefill_planes(e);
+  if (r == KL_OK) r = prefill_planes(e, (P - 1) % kPrefillChunk + 1);
   if (r != KL_OK) return r;
   hipError_t err = hipMemcpyAsync(e->pf_tok, prompt, sizeof(int32_t) * P, hipMemcpyHostToDevice,
                                   e->stream);

@@ -868,6 +868,289 @@ __global__ void k_split3(const float* __restrict__ x, int rows, int cols, int ld
   }
 }
 
+// ---------------------------------------------------------------------------
+// Short int8 prompts (at most 32 rows, group size 32 or 64): k_gemm_q8s.  The batched form of the reference int8 GEMV (float(q) * scale
+// per weight, cuda/matmul_kernel.cu:73) computed as sum over groups g of
+// scale[n][g] * sum_{k in g} a[k] q[n][k]: the activations as three bf16
+// planes (k_split3's split, rows padded to 32), each int8 weight exactly a
+// bf16, so the three products a_i q per multiply-add are exact in fp32 and
+// accumulate in fp32 on v_mfma_f32_32x32x16_bf16, one group at a time, then
+// scale into the output registers.  At 32 rows the launch is bound by the int8
+// weight bytes (cfg 3: 6.9 GB for 32 tokens), so the weights are prepacked
+// once (k_q8s_pack) in the order the lanes consume them: a 1 KB block per 32
+// columns x 32 k holding, for lane l, the 16 bytes W[32 b + l % 32][32 j +
+// 16 (l / 32) .. + 15], and the group scales as 128 B per (32 columns,
+// group); every weight load is a whole 1 KB of consecutive bytes straight
+// into registers, prefetched four groups ahead.  The
+// activation planes use the same k order: plane p, k step s (8 values) of
+// chunk j at element (((j * 3 + p) * 2 + s) * 64 + l) * 8 of the plane buffer,
+// lane l holding A[l % 32][32 j + 16 (l / 32) + 8 s .. + 7] (k_q8s_split).  A
+// workgroup of eight waves copies its split's activation planes (6 KB per
+// chunk, at most kQ8sLdsChunks) into LDS once, behind one barrier, and each
+// wave then streams the weights of its two 32-column blocks (32 x 64 of C):
+// with the activations read from L2 by every wave instead, they were three
+// times the weight bytes through each CU's load path and the kernel ran at
+// 1.6-2.8 TB/s.  Split-K over whole groups (blockIdx.y) as k_gemm_f32_dma.
+constexpr int kQ8sLdsChunks = 26;  // activation chunks a split may hold in LDS (156 KB)
+
+__host__ __device__ inline size_t q8s_tile_bytes(int N, int K) {
+  return static_cast<size_t>((N + 31) / 32) * (K / 32) * 1024;
+}
+
+typedef int gi4 __attribute__((ext_vector_type(4)));
+
+// Byte e (sign-extended) of w -> float: one SDWA conversion (the compiler
+// shifts the odd bytes first otherwise).
+template <int E>
+__device__ __forceinline__ float q8s_byte(int w) {
+  float f;
+  if constexpr (E == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(f) : "v"(w));
+  else if constexpr (E == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(f) : "v"(w));
+  else if constexpr (E == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(f) : "v"(w));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(f) : "v"(w));
+  return f;
+}
+
+// Eight int8 (two 32-bit words) -> eight bf16 (exact).
+__device__ __forceinline__ xbf8 q8s_bf16(int lo, int hi) {
+  xbf8 r;
+  r[0] = static_cast<__bf16>(q8s_byte<0>(lo));
+  r[1] = static_cast<__bf16>(q8s_byte<1>(lo));
+  r[2] = static_cast<__bf16>(q8s_byte<2>(lo));
+  r[3] = static_cast<__bf16>(q8s_byte<3>(lo));
+  r[4] = static_cast<__bf16>(q8s_byte<0>(hi));
+  r[5] = static_cast<__bf16>(q8s_byte<1>(hi));
+  r[6] = static_cast<__bf16>(q8s_byte<2>(hi));
+  r[7] = static_cast<__bf16>(q8s_byte<3>(hi));
+  return r;
+}
+
+template <int CPG>  // 32-column chunks per scale group (group size 32 CPG)
+__global__ __launch_bounds__(512, 1) void k_gemm_q8s(GemmQ8sArgs g) {
+  static_assert(CPG == 1 || CPG == 2, "group size 32 or 64");
+  constexpr int GD = 4;  // groups in flight
+  __shared__ __align__(1024) char Al[kQ8sLdsChunks * 6144];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bx = static_cast<int>(blockIdx.x);
+  int sidx = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i < g.nseg && bx >= g.seg[i].wg0) sidx = i;
+  const char* P = static_cast<const char*>(g.seg[0].P);
+  float* C = g.seg[0].C;
+  const float* bias = g.seg[0].bias;
+  int N = g.seg[0].N, ldc = g.seg[0].ldc, wg0 = 0;
+  size_t wsoff = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i == sidx) {
+      P = static_cast<const char*>(g.seg[i].P);
+      C = g.seg[i].C;
+      bias = g.seg[i].bias;
+      N = g.seg[i].N;
+      ldc = g.seg[i].ldc;
+      wg0 = g.seg[i].wg0;
+      wsoff = g.seg[i].wsoff;
+    }
+  const int K = g.K, nc = K / 32, ng = K / (32 * CPG);
+  const int gb = static_cast<int>(blockIdx.y) * ng / g.splits;
+  const int ge = (static_cast<int>(blockIdx.y) + 1) * ng / g.splits;
+  // The split's activation planes (6 KB per chunk, consecutive) into LDS,
+  // spread over the waves; every wave then streams only its own weights.
+  {
+    const char* src = static_cast<const char*>(g.A) + static_cast<size_t>(gb) * CPG * 6144 + 16 * lane;
+    const int n1k = (ge - gb) * CPG * 6;
+    for (int i = wave; i < n1k; i += 8)
+      __builtin_amdgcn_global_load_lds((global_void_t*)(src + static_cast<size_t>(i) * 1024),
+                                       (lds_void_t*)(Al + 1024 * i), 16, 0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  const int nb = (N + 31) / 32;
+  const int b0 = 16 * (bx - wg0) + 2 * wave;
+  if (b0 >= nb || gb >= ge) return;  // past the last barrier: waves leave on their own
+  const int b1 = min(b0 + 1, nb - 1);
+  const char* w0 = P + static_cast<size_t>(b0) * nc * 1024 + 16 * lane;
+  const char* w1 = P + static_cast<size_t>(b1) * nc * 1024 + 16 * lane;
+  const float* S = reinterpret_cast<const float*>(P + q8s_tile_bytes(N, K));
+  const float* s0p = S + static_cast<size_t>(b0) * ng * 32 + (lane & 31);
+  const float* s1p = S + static_cast<size_t>(b1) * ng * 32 + (lane & 31);
+  const char* Ap = Al + 16 * lane;
+  gf16 acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+  gi4 wq[GD][CPG][2];  // raw int8 fragments of the groups in flight
+  float sc[GD][2];
+  xbf8 qb[2][CPG][2][2];  // bf16 weights: [buffer][chunk][block][k step]
+  // Group grp (clamped to the split's last) into ring slot u: its chunks'
+  // weight fragments (1 KB per block and chunk) and scales.
+  auto load = [&](int grp, int u) {
+    const int gg = min(grp, ge - 1);
+#pragma unroll
+    for (int c = 0; c < CPG; ++c) {
+      const size_t j = static_cast<size_t>(gg) * CPG + c;
+      wq[u][c][0] = __builtin_nontemporal_load(reinterpret_cast<const gi4*>(w0 + j * 1024));
+      wq[u][c][1] = __builtin_nontemporal_load(reinterpret_cast<const gi4*>(w1 + j * 1024));
+    }
+    sc[u][0] = s0p[static_cast<size_t>(gg) * 32];
+    sc[u][1] = s1p[static_cast<size_t>(gg) * 32];
+  };
+  auto convert = [&](int u, int v) {
+#pragma unroll
+    for (int c = 0; c < CPG; ++c)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) qb[v][c][b][st] = q8s_bf16(wq[u][c][b][2 * st], wq[u][c][b][2 * st + 1]);
+  };
+  // Group grp (ring slot u, bf16 weights in buffer v): its activation
+  // fragments from LDS, then the MFMAs, with the next group (slot un) converted
+  // into buffer v ^ 1 in their shadow (a few VALU instructions after each
+  // MFMA: converting first and multiplying after left the VALU and the matrix
+  // core taking turns), then the group's sums scaled into acc.
+  auto group = [&](int grp, int u, int v, int un) {
+    xbf8 a[CPG][3][2];
+#pragma unroll
+    for (int c = 0; c < CPG; ++c) {
+      const int jl = (grp - gb) * CPG + c;
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+          a[c][p][st] = *reinterpret_cast<const xbf8*>(Ap + ((jl * 3 + p) * 2 + st) * 1024);
+    }
+    gf16 t[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t[0][r] = t[1][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPG; ++c)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int p = 2; p >= 0; --p)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            t[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][p][st], qb[v][c][b][st], t[b], 0, 0, 0);
+    convert(un, v ^ 1);
+    // 12 CPG MFMAs; 12 CPG conversions of 4 values (2 VALU each) and 2 CPG LDS reads per MFMA slot
+#pragma unroll
+    for (int i = 0; i < 12 * CPG; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc0[r] += sc[u][0] * t[0][r];
+      acc1[r] += sc[u][1] * t[1][r];
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < GD; ++u) load(gb + u, u);
+  convert(0, 0);
+  int grp = gb;
+  // Ring slot of group gb + i is i % GD and its bf16 buffer i % 2 (GD even):
+  // an unroll of GD keeps both compile-time.
+  for (; grp + GD <= ge; grp += GD) {
+#pragma unroll
+    for (int i = 0; i < GD; ++i) {
+      group(grp + i, i, i & 1, (i + 1) % GD);
+      load(grp + i + GD, i);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GD; ++i)
+    if (grp + i < ge) group(grp + i, i, i & 1, (i + 1) % GD);
+  const int h = lane >> 5;
+  float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int n = 32 * (q ? b0 + 1 : b0) + (lane & 31);
+    if (n >= N) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+      if (m < g.M) {
+        float v = q ? acc1[r] : acc0[r];
+        if (wsp) {
+          wsp[static_cast<size_t>(m) * N + n] = v;
+        } else {
+          if (bias) v += bias[n];
+          float* cp = C + static_cast<size_t>(m) * ldc + n;
+          if (g.accumulate) v = *cp + v;
+          *cp = v;
+        }
+      }
+    }
+  }
+}
+
+// int8 weights [N x K] (row-major, scales[(n K + k) >> gshift]) -> the packed
+// order of k_gemm_q8s: one thread per 16-byte lane fragment, then the scales.
+// Rows past N are zero.
+__global__ void k_q8s_pack(const int8_t* __restrict__ q, const float* __restrict__ sc, int N, int K,
+                           int gshift, char* __restrict__ out) {
+  const int nb = (N + 31) / 32, nc = K / 32, ng = K >> gshift;
+  const size_t frags = static_cast<size_t>(nb) * nc * 64;
+  const size_t scales = static_cast<size_t>(nb) * ng * 32;
+  float* so = reinterpret_cast<float*>(out + q8s_tile_bytes(N, K));
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < frags + scales;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    if (i < frags) {
+      const int l = static_cast<int>(i & 63);
+      const size_t bj = i >> 6;
+      const int b = static_cast<int>(bj / nc), j = static_cast<int>(bj % nc);
+      const int n = 32 * b + (l & 31), k = 32 * j + 16 * (l >> 5);
+      gi4 v = {0, 0, 0, 0};
+      if (n < N) v = *reinterpret_cast<const gi4*>(q + static_cast<size_t>(n) * K + k);
+      *reinterpret_cast<gi4*>(out + 16 * i) = v;
+    } else {
+      const size_t t = i - frags;
+      const int nn = static_cast<int>(t & 31);
+      const size_t bg = t >> 5;
+      const int b = static_cast<int>(bg / ng), grp = static_cast<int>(bg % ng);
+      const int n = 32 * b + nn;
+      so[t] = n < N ? sc[(static_cast<size_t>(n) * K >> gshift) + grp] : 0.f;
+    }
+  }
+}
+
+// Activation rows (at most 32, row stride ldx) -> the three bf16 planes of
+// k_gemm_q8s in its lane order (rows past M are zero).
+__global__ void k_q8s_split(const float* __restrict__ x, int M, int K, int ldx, __bf16* __restrict__ out) {
+  const size_t total = static_cast<size_t>(K / 32) * 2 * 64;  // (chunk, step, lane)
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int l = static_cast<int>(i & 63);
+    const int st = static_cast<int>((i >> 6) & 1);
+    const int j = static_cast<int>(i >> 7);
+    const int m = l & 31, k = 32 * j + 16 * (l >> 5) + 8 * st;
+    gf4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+    if (m < M) {
+      const gf4* src = reinterpret_cast<const gf4*>(x + static_cast<size_t>(m) * ldx + k);
+      v0 = src[0];
+      v1 = src[1];
+    }
+    xbf8 x0, x1, x2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = e < 4 ? v0[e] : v1[e - 4];
+      x0[e] = static_cast<__bf16>(v);
+      const float r1 = v - static_cast<float>(x0[e]);
+      x1[e] = static_cast<__bf16>(r1);
+      x2[e] = static_cast<__bf16>(r1 - static_cast<float>(x1[e]));
+    }
+    const size_t base = ((static_cast<size_t>(j) * 3) * 2 + st) * 512 + 8 * l;
+    *reinterpret_cast<xbf8*>(out + base) = x0;
+    *reinterpret_cast<xbf8*>(out + base + 1024) = x1;
+    *reinterpret_cast<xbf8*>(out + base + 2048) = x2;
+  }
+}
+
 // C_s = sum of the split partials in split order (+ bias_s) (+ C_s), over
 // every output s of the launch: element i of a split's slab belongs to the
 // output whose [M][N_s] block (at seg[s].wsoff) holds it.

@@ -51,6 +51,24 @@ struct GemmX6Args {
   int tiles;  // 128 x 128 tiles over every output (the grid is padded to a multiple of 8)
 };
 
+// Short int8 prompts (k_gemm_q8s): one output over prepacked weights P
+// (k_q8s_pack); wg0 = first workgroup of the output.
+struct GemmQ8sSeg {
+  const void* P;
+  float* C;
+  const float* bias;
+  int N, ldc, wg0;
+  size_t wsoff;
+};
+
+struct GemmQ8sArgs {
+  const void* A;  // activation planes (k_q8s_split)
+  int M, K, gshift, accumulate, nseg, splits;
+  GemmQ8sSeg seg[kGemmMaxSeg];
+  float* ws;
+  size_t ws_split;
+};
+
 // Host launcher (ops.hip): C_s (+)= A . W_s^T (+ bias_s) for nseg outputs in
 // one grid; splits > 1 divides K among blockIdx.y into ws (splits * M *
 // (N_0 + ...) floats) and reduces in split order.  Every segment is fp32 or
@@ -67,6 +85,18 @@ int gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSe
 // Host launcher (ops.hip) of k_split3: rows x cols fp32 (stride ldx, cols a
 // multiple of 32) into the tiled planes (x6_plane_bytes(rows, cols) bytes).
 int split3_run(const float* x, int rows, int cols, int ldx, void* planes, hipStream_t st);
+
+// Short int8 prompts: bytes of a prepacked int8 matrix (q8s_pack_run) and of
+// the activation planes (q8s_split_run, 32 rows); the launcher over nseg
+// outputs of the same A (segs[s].W: the packed matrix), splits chosen within
+// ws_bytes; M <= 32, group size 32 or 64 dividing K.
+size_t q8s_packed_bytes(int N, int K, int group_size);
+inline size_t q8s_aplane_bytes(int K) { return static_cast<size_t>(K) * 32 * 3 * 2; }
+int q8s_pack_run(const int8_t* q, const float* scales, int N, int K, int group_size, void* packed,
+                 hipStream_t st);
+int q8s_split_run(const float* A, int M, int K, int lda, void* planes, hipStream_t st);
+int gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg, const GemmSeg* segs,
+                 int accumulate, float* ws, size_t ws_bytes, hipStream_t st);
 
 inline size_t x6_plane_bytes(int rows, int cols) {
   return static_cast<size_t>((rows + 15) / 16) * 16 * cols * 3 * 2;

@@ -1077,6 +1077,117 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
   return launch_rc();
 }
 
+namespace {
+// Split count of a k_gemm_q8s launch of `wgs` workgroups over ng groups of
+// cpg chunks and mn output floats, one workgroup per CU: rounds x (3 us +
+// 1.2 us per group of a split) plus the partials written and read once
+// ((2 splits + 1) mn floats at 4 TB/s); a split's activations must fit the
+// kernel's LDS (kQ8sLdsChunks chunks), and a split count must win by 3% over
+// the next smaller one.  0 when no split count up to 64 fits.
+int q8s_splits(long long wgs, int ng, int cpg, size_t mn, size_t ws_floats) {
+  const long long slots = device_cus();
+  int best = 0;
+  double tbest = 1e300;
+  for (int s = 1; s <= 64 && s <= ng; ++s) {
+    if ((ng + s - 1) / s * cpg > kQ8sLdsChunks) continue;
+    if (s > 1 && static_cast<size_t>(s) * mn > ws_floats) break;
+    const long long rounds = (wgs * s + slots - 1) / slots;
+    const double t = static_cast<double>(rounds) * (3.0 + ((ng + s - 1) / s) * 1.2) +
+                     (s > 1 ? static_cast<double>(mn) * 4.0 * (2 * s + 1) / 4e6 : 0.0);
+    if (t < tbest * 0.97) {
+      tbest = t;
+      best = s;
+    }
+  }
+  return best;
+}
+
+bool q8s_group_ok(int K, int group_size) {
+  return (group_size == 32 || group_size == 64) && K > 0 && K % group_size == 0;
+}
+}  // namespace
+
+size_t kl::q8s_packed_bytes(int N, int K, int group_size) {
+  if (N <= 0 || !q8s_group_ok(K, group_size)) return 0;
+  return q8s_tile_bytes(N, K) + static_cast<size_t>((N + 31) / 32) * (K / group_size) * 32 * sizeof(float);
+}
+
+int kl::q8s_pack_run(const int8_t* q, const float* scales, int N, int K, int group_size, void* packed,
+                     hipStream_t st) {
+  if (!q || !scales || !packed || N <= 0) return KL_EINVAL;
+  if (!q8s_group_ok(K, group_size) || !aligned16(q) || !aligned16(packed)) return KL_EUNSUPP;
+  int gshift = 0;
+  while ((1 << gshift) < group_size) ++gshift;
+  const size_t work = static_cast<size_t>((N + 31) / 32) * (K / 32) * 64 +
+                      static_cast<size_t>((N + 31) / 32) * (K / group_size) * 32;
+  const int grid = static_cast<int>(std::min<size_t>((work + 255) / 256, 16384));
+  hipLaunchKernelGGL(k_q8s_pack, dim3(grid), dim3(256), 0, st, q, scales, N, K, gshift,
+                     static_cast<char*>(packed));
+  return launch_rc();
+}
+
+int kl::q8s_split_run(const float* A, int M, int K, int lda, void* planes, hipStream_t st) {
+  if (!A || !planes || M <= 0 || M > 32 || K <= 0 || lda < K) return KL_EINVAL;
+  if (K % 32 || lda % 4 || !aligned16(A) || !aligned16(planes)) return KL_EUNSUPP;
+  const size_t work = static_cast<size_t>(K / 32) * 128;
+  const int grid = static_cast<int>(std::min<size_t>((work + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_q8s_split, dim3(grid), dim3(256), 0, st, A, M, K, lda, static_cast<__bf16*>(planes));
+  return launch_rc();
+}
+
+int kl::gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg, const GemmSeg* segs,
+                     int accumulate, float* ws, size_t ws_bytes, hipStream_t st) {
+  if (!planes || M <= 0 || M > 32 || nseg < 1 || nseg > kGemmMaxSeg) return KL_EINVAL;
+  if (!q8s_group_ok(K, group_size) || !aligned16(planes)) return KL_EUNSUPP;
+  GemmQ8sArgs g{};
+  g.A = planes;
+  g.M = M;
+  g.K = K;
+  while ((1 << g.gshift) < group_size) ++g.gshift;
+  g.accumulate = accumulate;
+  g.nseg = nseg;
+  g.ws = ws;
+  long long wgs = 0;
+  size_t wsoff = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const GemmSeg& sg = segs[i];
+    if (!sg.W || !sg.C || sg.N <= 0 || sg.ldc < sg.N) return KL_EINVAL;
+    if (!aligned16(sg.W)) return KL_EUNSUPP;
+    g.seg[i] = GemmQ8sSeg{sg.W, sg.C, sg.bias, sg.N, sg.ldc, static_cast<int>(wgs), wsoff};
+    wgs += (sg.N + 511) / 512;
+    wsoff += static_cast<size_t>(M) * sg.N;
+  }
+  if (wgs > INT_MAX / 2) return KL_EUNSUPP;
+  g.ws_split = wsoff;
+  g.splits = q8s_splits(wgs, K / group_size, group_size / 32, wsoff, ws ? ws_bytes / sizeof(float) : 0);
+  if (g.splits == 0) return KL_EWORKSPACE;  // K too deep for one split's LDS: room for partials needed
+  const dim3 grid(static_cast<unsigned>(wgs), g.splits);
+  if (group_size == 32)
+    hipLaunchKernelGGL(k_gemm_q8s<1>, grid, dim3(512), 0, st, g);
+  else
+    hipLaunchKernelGGL(k_gemm_q8s<2>, grid, dim3(512), 0, st, g);
+  int r = launch_rc();
+  if (r != KL_OK || g.splits == 1) return r;
+  // k_gemm_reduce reads the output list of a GemmArgs.
+  GemmArgs ra{};
+  ra.M = M;
+  ra.accumulate = accumulate;
+  ra.nseg = nseg;
+  ra.ws = ws;
+  ra.ws_split = wsoff;
+  ra.splits = g.splits;
+  for (int i = 0; i < nseg; ++i) {
+    ra.seg[i].C = segs[i].C;
+    ra.seg[i].bias = segs[i].bias;
+    ra.seg[i].N = segs[i].N;
+    ra.seg[i].ldc = segs[i].ldc;
+    ra.seg[i].wsoff = g.seg[i].wsoff;
+  }
+  const int rgrid = static_cast<int>(std::min<size_t>((wsoff + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, ra);
+  return launch_rc();
+}
+
 int kl::split3_run(const float* x, int rows, int cols, int ldx, void* planes, hipStream_t st) {
   if (!x || !planes || rows <= 0 || cols <= 0 || ldx < cols) return KL_EINVAL;
   if (cols % 32 || ldx % 4 || !aligned16(x) || !aligned16(planes)) return KL_EUNSUPP;
@@ -1095,6 +1206,27 @@ size_t kl_split_bf16x3_bytes(int rows, int cols) {
 
 int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, void* stream) {
   return split3_run(x, rows, cols, ldx, planes, as_stream(stream));
+}
+
+size_t kl_q8s_packed_bytes(int N, int K, int group_size) { return q8s_packed_bytes(N, K, group_size); }
+
+int kl_q8s_pack(const int8_t* q, const float* scales, int N, int K, int group_size, void* packed,
+                void* stream) {
+  return q8s_pack_run(q, scales, N, K, group_size, packed, as_stream(stream));
+}
+
+int kl_gemm_q8s(const float* A, int M, int K, int lda, const void* packed, int N, int group_size,
+                float* C, int ldc, const float* bias, int accumulate, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (!C || N <= 0 || ldc < N || M <= 0 || M > 32) return KL_EINVAL;
+  if (!workspace || workspace_bytes < q8s_aplane_bytes(K)) return KL_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  int r = q8s_split_run(A, M, K, lda, workspace, st);
+  if (r != KL_OK) return r;
+  const size_t pb = (q8s_aplane_bytes(K) + 255) & ~size_t(255);
+  float* ws = workspace_bytes > pb ? reinterpret_cast<float*>(static_cast<char*>(workspace) + pb) : nullptr;
+  const GemmSeg sg{packed, C, bias, N, K, ldc, 0};
+  return gemm_run_q8s(workspace, M, K, group_size, 1, &sg, accumulate, ws, ws ? workspace_bytes - pb : 0, st);
 }
 
 int kl_gemm_x6(const void* a_planes, const void* w_planes, float* C, int M, int N, int K, int ldc,

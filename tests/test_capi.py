@@ -53,6 +53,8 @@ def test_host_side_argument_checks(K):
     assert lib.kl_split_bf16x3(None, 4, 32, 32, None, None) == -1
     assert lib.kl_split_bf16x3_bytes(17, 64) == 32 * 64 * 6 and lib.kl_split_bf16x3_bytes(0, 64) == 0
     assert lib.kl_gemm_x6(None, None, None, 4, 4, 32, 4, None, 0, None, 0, None) == -1
+    assert lib.kl_q8s_packed_bytes(40, 128, 64) == 64 * 128 + 2 * 2 * 128
+    assert lib.kl_q8s_pack(None, None, 32, 64, 64, None, None) == -1
     rd, cp = C.c_float(0), C.c_float(0)
     assert lib.kl_hbm_probe(1 << 19, 1, C.byref(rd), C.byref(cp)) == -1  # under 1 MiB
     assert lib.kl_hbm_probe(1 << 20, 0, C.byref(rd), C.byref(cp)) == -1  # no passes

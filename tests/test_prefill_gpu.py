@@ -578,6 +578,86 @@ def test_gemm_q8_vs_oracle(K, O, gpu, M, N, Kd, gs, splits):
         assert np.max(np.abs(y[m] - want)) <= tol, m
 
 
+def gemm_q8s(K, A, q, s, gs, N, bias=None, C0=None, ws=True):
+    M, Kd = A.shape
+    pb = K.lib.kl_q8s_packed_bytes(N, Kd, gs)
+    assert pb == ((N + 31) // 32) * (Kd * 32 + (Kd // gs) * 128)
+    dq, ds, dP = D(K, q), D(K, s), K.DeviceArray(pb, np.uint8)
+    ok(K.lib.kl_q8s_pack(dq.ptr, ds.ptr, N, Kd, gs, dP.ptr, None), "kl_q8s_pack")
+    dA = D(K, A)
+    dC = D(K, C0) if C0 is not None else K.DeviceArray(M * N)
+    db = D(K, bias) if bias is not None else None
+    wsb = Kd * 192 + (64 * 32 * N * 4 + 256 if ws else 0)
+    w = K.DeviceArray(wsb, np.uint8)
+    rc = K.lib.kl_gemm_q8s(dA.ptr, M, Kd, Kd, dP.ptr, N, gs, dC.ptr, N, db.ptr if db else None,
+                           int(C0 is not None), w.ptr, wsb, None)
+    if not ws and Kd > 832:  # one split holds at most 832 columns of K
+        assert rc == -6
+        return None
+    ok(rc, "kl_gemm_q8s")
+    return dC.numpy().reshape(M, N)
+
+
+def test_gemm_q8s_kat_exact(K, gpu):
+    """a = s_m sigma_k c (c = 1 + 2^-9 + 2^-17: three exact bf16 planes),
+    q = t_n sigma_k, group scales powers of two: every partial sum is exact, so
+    C = s_m t_n c 32 (sc_0 + sc_1) exactly; without the third plane it would
+    miss 32 |s t| 2^-17 per group."""
+    c = np.float32(1 + 2 ** -9 + 2 ** -17)
+    M, N, Kd, gs = 19, 100, 64, 32
+    sm = np.array([(-1) ** (m % 3) * 2.0 ** (m % 5 - 2) for m in range(M)], np.float32)
+    tn = np.array([(-1) ** (n % 2) * (1 << (n % 4)) for n in range(N)], np.int64)
+    sig = np.array([(-1) ** (k % 3 == 1) for k in range(Kd)], np.int64)
+    A = (sm[:, None] * sig[None, :].astype(np.float32) * c).astype(np.float32)
+    q = (tn[:, None] * sig[None, :]).astype(np.int8)
+    sc = np.array([[1.0, 2.0] if n % 2 else [0.5, 4.0] for n in range(N)], np.float32).reshape(-1)
+    want = np.array([[float(sm[m]) * float(tn[n]) * float(c) * 32 * (sc[2 * n] + sc[2 * n + 1])
+                      for n in range(N)] for m in range(M)]).astype(np.float32)
+    for ws in (False, True):
+        y = gemm_q8s(K, A, q.reshape(-1), sc, gs, N, ws=ws)
+        assert np.array_equal(y, want), np.max(np.abs(y - want))
+
+
+@pytest.mark.parametrize("M,N,Kd,gs", [(1, 64, 64, 64), (5, 300, 256, 32), (32, 1000, 512, 64),
+                                       (17, 4096, 4096, 64), (32, 4096, 11008, 64), (3, 100, 1024, 32),
+                                       (32, 12288, 4096, 64)])
+def test_gemm_q8s_vs_oracle(K, O, gpu, M, N, Kd, gs):
+    """The short-prompt int8 GEMM against the oracle's int8 MatmulKernel row by
+    row within the fp32 GEMV bound, with bias and accumulate, with and without
+    the split-K workspace."""
+    rng = np.random.default_rng(M * 13 + N + gs)
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    Wf = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
+    q, s = O.quantize_q8(Wf.reshape(-1), gs)
+    bias = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    wd = O.dequant_q8(q, s, gs).reshape(N, Kd).astype(np.float64)
+    for ws in (False, True):
+        y = gemm_q8s(K, A, q, s, gs, N, bias=bias, C0=C0, ws=ws)
+        if y is None:
+            continue
+        for m in range(M):
+            g = O.gemv_q8(A[m], q, s, N, Kd, gs)
+            want = C0[m].astype(np.float64) + g + bias
+            tol = 4e-7 * np.sqrt(Kd) * (np.abs(wd) @ np.abs(A[m])).max() + 1e-6
+            assert np.max(np.abs(y[m] - want)) <= tol, (ws, m)
+
+
+def test_gemm_q8s_refusals(K, gpu):
+    buf = K.DeviceArray(1 << 16, np.uint8)
+    # 33 rows; group size 16; K not a multiple of the group; a workspace short of A's planes
+    assert K.lib.kl_gemm_q8s(buf.ptr, 33, 64, 64, buf.ptr, 32, 64, buf.ptr, 32, None, 0, buf.ptr,
+                             buf.nbytes, None) == -1
+    assert K.lib.kl_gemm_q8s(buf.ptr, 4, 64, 64, buf.ptr, 32, 16, buf.ptr, 32, None, 0, buf.ptr,
+                             buf.nbytes, None) == -4
+    assert K.lib.kl_gemm_q8s(buf.ptr, 4, 96, 96, buf.ptr, 32, 64, buf.ptr, 32, None, 0, buf.ptr,
+                             buf.nbytes, None) == -4
+    assert K.lib.kl_gemm_q8s(buf.ptr, 4, 64, 64, buf.ptr, 32, 64, buf.ptr, 32, None, 0, buf.ptr,
+                             64 * 192 - 1, None) == -6
+    assert K.lib.kl_q8s_packed_bytes(32, 96, 64) == 0
+    assert K.lib.kl_q8s_packed_bytes(32, 256, 128) == 0  # groups of 128 take kl_gemm_q8
+
+
 def test_gemm_q8_rejects_bad_shapes(K, gpu):
     buf = K.DeviceArray(4096)
     # K not a whole number of 32-column blocks; group size not a power of two
