@@ -1638,22 +1638,45 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
   const int D = m.D, Dq = m.Dq, Dkv = m.Dkv, F = m.F, H = m.H, KVH = m.KVH, hd = m.hd;
   const bool q8 = e->quant != 0;
   void* st = e->stream;
+  hipStream_t hs = static_cast<hipStream_t>(st);
   const size_t kv_layer = static_cast<size_t>(m.S) * Dkv;
   int r = kl_embedding(e->pf_tok + pos0, n, e->emb, m.V, D, e->pf_x, nullptr, st);
 #define PF(call)          \
   do {                    \
     if (r == KL_OK) r = (call); \
   } while (0)
+  // fp32 weights: split-product GEMMs over bf16 planes of the weights
+  // (prefill_planes) and of each GEMM input; int8 weights with at most 32
+  // rows: k_gemm_q8s over the packed weights.  On these paths every GEMM
+  // input is written as planes by its producer (the row norms, SwiGLU, or a
+  // split of the attention output), and the split-K partials of Wo, W1/W3
+  // and W2 are summed by the next producer instead of a reduction pass
+  // (pend: W2's partials of the previous layer, not yet added to pf_x).
+  const bool q8s = e->pf_q8s && n <= 32 && e->xw_buf;
+  const bool fast = e->pf_x6 || q8s;
+  const size_t nD = static_cast<size_t>(n) * D, nF = static_cast<size_t>(n) * F;
+  int pend = 0;
+  auto gemm_fast = [&](int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc, int* deferred) {
+    if (q8s) {
+      GemmSeg s2[kGemmMaxSeg];
+      for (int i = 0; i < nseg; ++i) {
+        s2[i] = sg[i];
+        s2[i].W = wx[i];
+      }
+      PF(gemm_run_q8s(e->pf_ax, n, k, m.gs, nseg, s2, acc, e->pf_ws, e->pf_ws_bytes, hs, deferred));
+      return;
+    }
+    GemmX6Planes p{};
+    p.A = e->pf_ax;
+    for (int i = 0; i < nseg; ++i) p.W[i] = wx[i];
+    PF(gemm_run_x6(p, n, k, nseg, sg, acc, e->pf_ws, e->pf_ws_bytes, hs, deferred));
+  };
   for (int l = 0; l < m.L && r == KL_OK; ++l) {
     const LayerDev& Ld = e->layers[l];
     float* kc = e->kcache + l * kv_layer;
     float* vc = e->vcache + l * kv_layer;
     float* krow = kc + static_cast<size_t>(pos0) * Dkv;
     float* vrow = vc + static_cast<size_t>(pos0) * Dkv;
-    hipStream_t hs = static_cast<hipStream_t>(st);
-    // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513)
-    PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
-    // q, k and v in one grouped launch (k and v straight into the cache rows)
     // Split-K where the launch would leave CUs idle (int8, at most 32 rows);
     // every split's partials fit pf_ws (prefill_scratch).  Groups of at least
     // 32 run the direct-to-LDS int8 kernel (5 workgroups per CU).
@@ -1664,36 +1687,19 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
         r = KL_EWORKSPACE;
       return sp;
     };
-    // fp32 weights: the split-product GEMM over bf16 planes of the input
-    // (split here) and of the weights (prefill_planes).
-    // int8 weights, at most 32 rows: k_gemm_q8s over the packed weights.
-    const bool q8s = e->pf_q8s && n <= 32 && e->xw_buf;
-    auto x6 = [&](const float* in, int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc) {
-      if (q8s) {
-        PF(q8s_split_run(in, n, k, k, e->pf_ax, hs));
-        GemmSeg s2[kGemmMaxSeg];
-        for (int i = 0; i < nseg; ++i) {
-          s2[i] = sg[i];
-          s2[i].W = wx[i];
-        }
-        PF(gemm_run_q8s(e->pf_ax, n, k, m.gs, nseg, s2, acc, e->pf_ws, e->pf_ws_bytes, hs));
-        return;
-      }
-      PF(split3_run(in, n, k, k, e->pf_ax, hs));
-      GemmX6Planes p{};
-      p.A = e->pf_ax;
-      for (int i = 0; i < nseg; ++i) p.W[i] = wx[i];
-      PF(gemm_run_x6(p, n, k, nseg, sg, acc, e->pf_ws, e->pf_ws_bytes, hs));
-    };
-    const bool fast = e->pf_x6 || q8s;
+    // attention_rms + attention_qkv (llama3.cpp:599-639; qwen3.cpp:470-513):
+    // q, k and v in one grouped launch (k and v straight into the cache rows)
     {
       const GemmSeg sg[3] = {proj_seg(e, Ld.wq, e->pf_q, Ld.bq, Dq, D, Dq),
                              proj_seg(e, Ld.wk, krow, Ld.bk, Dkv, D, Dkv),
                              proj_seg(e, Ld.wv, vrow, Ld.bv, Dkv, D, Dkv)};
       if (fast) {
+        PF(norm_planes_run(e->pf_x, Ld.rms_att, n, D, e->eps, e->pf_ws, pend, nD, e->pf_ax, q8s, hs));
+        pend = 0;
         const void* wx[3] = {Ld.xp.q, Ld.xp.k, Ld.xp.v};
-        x6(e->pf_xn, D, 3, sg, wx, 0);
+        gemm_fast(D, 3, sg, wx, 0, nullptr);
       } else {
+        PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
         const int sp = splits_for(Dq + 2 * Dkv, D, true);
         PF(gemm_run(e->pf_xn, n, D, D, 3, sg, 0, e->pf_ws, sp, hs));
       }
@@ -1712,39 +1718,45 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq,
                           e->pf_aws, e->pf_aws_bytes, st));
-    {
-      const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
-      if (fast) {
-        x6(e->pf_att, Dq, 1, &sg, &Ld.xp.o, 1);
-      } else {
+    // feed_forward (llama3.cpp:671-719)
+    if (fast) {
+      int dwo = 1, d13 = 1, d2 = 1;
+      const GemmSeg so = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
+      PF(q8s ? q8s_split_run(e->pf_att, n, Dq, Dq, e->pf_ax, hs) : split3_run(e->pf_att, n, Dq, Dq, e->pf_ax, hs));
+      gemm_fast(Dq, 1, &so, &Ld.xp.o, 1, &dwo);
+      PF(norm_planes_run(e->pf_x, Ld.rms_ffn, n, D, e->eps, e->pf_ws, dwo > 1 ? dwo : 0, nD, e->pf_ax,
+                         q8s, hs));
+      const GemmSeg s13[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
+                              proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
+      const void* wx[2] = {Ld.xp.w1, Ld.xp.w3};
+      gemm_fast(D, 2, s13, wx, 0, &d13);
+      PF(swiglu_planes_run(e->pf_h1, e->pf_h3, n, F, e->pf_ws, d13 > 1 ? d13 : 0, 2 * nF, nF, e->pf_ax,
+                           q8s, hs));
+      const GemmSeg s2 = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
+      gemm_fast(F, 1, &s2, &Ld.xp.w2, 1, &d2);
+      pend = d2 > 1 ? d2 : 0;
+    } else {
+      {
+        const GemmSeg sg = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
         const int sp = splits_for(D, Dq, false);
         PF(gemm_run(e->pf_att, n, Dq, Dq, 1, &sg, 1, e->pf_ws, sp, hs));
       }
-    }
-    // feed_forward (llama3.cpp:671-719)
-    PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
-    {
-      const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
-                             proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
-      if (fast) {
-        const void* wx[2] = {Ld.xp.w1, Ld.xp.w3};
-        x6(e->pf_xn, D, 2, sg, wx, 0);
-      } else {
+      PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_ffn, e->pf_xn, n, D, e->eps, st));
+      {
+        const GemmSeg sg[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
+                               proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
         const int sp = splits_for(2 * F, D, true);
         PF(gemm_run(e->pf_xn, n, D, D, 2, sg, 0, e->pf_ws, sp, hs));
       }
-    }
-    PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
-    {
-      const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
-      if (fast) {
-        x6(e->pf_h1, F, 1, &sg, &Ld.xp.w2, 1);
-      } else {
+      PF(kl_swiglu(e->pf_h1, e->pf_h3, e->pf_h1, n * F, st));
+      {
+        const GemmSeg sg = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
         const int sp = splits_for(D, F, false);
         PF(gemm_run(e->pf_h1, n, F, F, 1, &sg, 1, e->pf_ws, sp, hs));
       }
     }
   }
+  if (pend) PF(partials_add_run(e->pf_x, n, D, e->pf_ws, pend, hs));  // the last layer's W2
 #undef PF
   return r;
 }

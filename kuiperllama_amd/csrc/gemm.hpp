@@ -840,6 +840,33 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
       }
 }
 
+// Stores the three bf16 planes of x[r][k .. k + 3] (k a multiple of 4): the
+// tiled plane format of k_gemm_x6 (K columns), or k_gemm_q8s's lane order
+// (q8s: r < 32).  The GEMM-input producers (row norm, SwiGLU) write through it.
+typedef __bf16 xbf4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void planes_store4(bool q8s, __bf16* out, int r, int k, int K, gf4 v) {
+  xbf4 x0, x1, x2;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x0[e] = static_cast<__bf16>(v[e]);
+    const float r1 = v[e] - static_cast<float>(x0[e]);
+    x1[e] = static_cast<__bf16>(r1);
+    x2[e] = static_cast<__bf16>(r1 - static_cast<float>(x1[e]));
+  }
+  size_t off, ps;
+  if (q8s) {
+    const int j = k >> 5, kk = k & 31;
+    off = ((static_cast<size_t>(j) * 3 * 2 + ((kk >> 3) & 1)) * 64 + (kk >> 4) * 32 + r) * 8 + (kk & 7);
+    ps = 1024;
+  } else {
+    off = x6_tile_offset(r, k, 0, K);
+    ps = 512;
+  }
+  *reinterpret_cast<xbf4*>(out + off) = x0;
+  *reinterpret_cast<xbf4*>(out + off + ps) = x1;
+  *reinterpret_cast<xbf4*>(out + off + 2 * ps) = x2;
+}
+
 // fp32 rows -> the three bf16 planes x0, x1, x2 of k_gemm_x6 in the tiled
 // plane format (x6_tile_offset); eight values per thread.
 __global__ void k_split3(const float* __restrict__ x, int rows, int cols, int ldx,

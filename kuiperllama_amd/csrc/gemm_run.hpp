@@ -79,8 +79,11 @@ int gemm_run(const float* A, int M, int K, int lda, int nseg, const GemmSeg* seg
 // Host launcher (ops.hip) of k_gemm_x6: the same products from bf16 planes
 // (segs[s].W and ldw unused).  K a multiple of 32.  Chooses the split count
 // itself (up to 8, where ws_bytes holds splits * M * (N_0 + ...) floats).
+// With `deferred`, a split-K launch leaves its partials in ws (no reduction:
+// the caller's next producer sums them) and *deferred = the split count (1:
+// C was written directly).
 int gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSeg* segs,
-                int accumulate, float* ws, size_t ws_bytes, hipStream_t st);
+                int accumulate, float* ws, size_t ws_bytes, hipStream_t st, int* deferred = nullptr);
 
 // Host launcher (ops.hip) of k_split3: rows x cols fp32 (stride ldx, cols a
 // multiple of 32) into the tiled planes (x6_plane_bytes(rows, cols) bytes).
@@ -96,7 +99,20 @@ int q8s_pack_run(const int8_t* q, const float* scales, int N, int K, int group_s
                  hipStream_t st);
 int q8s_split_run(const float* A, int M, int K, int lda, void* planes, hipStream_t st);
 int gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg, const GemmSeg* segs,
-                 int accumulate, float* ws, size_t ws_bytes, hipStream_t st);
+                 int accumulate, float* ws, size_t ws_bytes, hipStream_t st, int* deferred = nullptr);
+
+// GEMM-input producers (ops.hip) writing the operand planes directly (q8s:
+// k_gemm_q8s's lane order, rows <= 32; else the tiled format):
+// norm_planes_run: x += sum of `splits` partial slabs (ws + z ws_split, rows
+// x n; none for splits = 0), written back, then RMSNorm(x) * w into planes;
+// swiglu_planes_run: silu(h1) * h3 into planes, h1 and h3 the sums of the
+// partial slabs at ws (+ wsoff3 for h3) when splits > 0.
+int norm_planes_run(float* x, const float* w, int rows, int n, float eps, const float* ws, int splits,
+                    size_t ws_split, void* planes, bool q8s, hipStream_t st);
+int swiglu_planes_run(const float* h1, const float* h3, int rows, int F, const float* ws, int splits,
+                      size_t ws_split, size_t wsoff3, void* planes, bool q8s, hipStream_t st);
+// x[rows x n] += the sum of `splits` partial slabs of rows x n at ws (k_gemm_reduce).
+int partials_add_run(float* x, int rows, int n, const float* ws, int splits, hipStream_t st);
 
 inline size_t x6_plane_bytes(int rows, int cols) {
   return static_cast<size_t>((rows + 15) / 16) * 16 * cols * 3 * 2;

@@ -1039,7 +1039,7 @@ int x6_splits(long long tiles, int nkt, size_t mn, size_t ws_floats) {
 }  // namespace
 
 int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSeg* segs,
-                    int accumulate, float* ws, size_t ws_bytes, hipStream_t st) {
+                    int accumulate, float* ws, size_t ws_bytes, hipStream_t st, int* deferred) {
   if (!planes.A || M <= 0 || K <= 0 || nseg < 1 || nseg > kGemmMaxSeg) return KL_EINVAL;
   if (K % 32 || !aligned16(planes.A)) return KL_EUNSUPP;
   GemmArgs g{};
@@ -1071,7 +1071,8 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
   const unsigned grid = static_cast<unsigned>(8 * ((tiles + 7) / 8));
   hipLaunchKernelGGL(k_gemm_x6, dim3(grid, g.splits), dim3(256), 0, st, x);
   int r = launch_rc();
-  if (r != KL_OK || g.splits == 1) return r;
+  if (deferred) *deferred = g.splits;
+  if (r != KL_OK || g.splits == 1 || deferred) return r;
   const int rgrid = static_cast<int>(std::min<size_t>((g.ws_split + 255) / 256, 4096));
   hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, g);
   return launch_rc();
@@ -1136,7 +1137,7 @@ int kl::q8s_split_run(const float* A, int M, int K, int lda, void* planes, hipSt
 }
 
 int kl::gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg, const GemmSeg* segs,
-                     int accumulate, float* ws, size_t ws_bytes, hipStream_t st) {
+                     int accumulate, float* ws, size_t ws_bytes, hipStream_t st, int* deferred) {
   if (!planes || M <= 0 || M > 32 || nseg < 1 || nseg > kGemmMaxSeg) return KL_EINVAL;
   if (!q8s_group_ok(K, group_size) || !aligned16(planes)) return KL_EUNSUPP;
   GemmQ8sArgs g{};
@@ -1167,7 +1168,8 @@ int kl::gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg,
   else
     hipLaunchKernelGGL(k_gemm_q8s<2>, grid, dim3(512), 0, st, g);
   int r = launch_rc();
-  if (r != KL_OK || g.splits == 1) return r;
+  if (deferred) *deferred = g.splits;
+  if (r != KL_OK || g.splits == 1 || deferred) return r;
   // k_gemm_reduce reads the output list of a GemmArgs.
   GemmArgs ra{};
   ra.M = M;
@@ -1185,6 +1187,134 @@ int kl::gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg,
   }
   const int rgrid = static_cast<int>(std::min<size_t>((wsoff + 255) / 256, 4096));
   hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, ra);
+  return launch_rc();
+}
+
+// RMSNorm of one row per workgroup into GEMM-input planes (the arithmetic
+// of k_rmsnorm_rows_b), after x += the row's split-K partials summed in split
+// order (the arithmetic of k_gemm_reduce with accumulate), written back.
+template <int R>
+__global__ __launch_bounds__(256) void k_norm_planes(float* x, const float* __restrict__ w, int n,
+                                                     float eps, const float* __restrict__ ws,
+                                                     int splits, size_t ws_split, __bf16* planes,
+                                                     bool q8s) {
+  __shared__ float red[kWavesPerBlock];
+  const int row = blockIdx.x;
+  f4* xr = reinterpret_cast<f4*>(x + static_cast<size_t>(row) * n);
+  const f4* w4 = reinterpret_cast<const f4*>(w);
+  const int n4 = n / 4;
+  f4 v[R];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int i = threadIdx.x + j * 256;
+    v[j] = f4{0.f, 0.f, 0.f, 0.f};
+    if (i < n4) {
+      v[j] = xr[i];
+      if (splits > 0) {
+        const f4* p = reinterpret_cast<const f4*>(ws + static_cast<size_t>(row) * n) + i;
+        f4 sum = p[0];
+        for (int z = 1; z < splits; ++z) sum += p[z * (ws_split / 4)];
+        v[j] = v[j] + sum;
+        xr[i] = v[j];
+      }
+    }
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  ss = block_sum(ss, red);
+  const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int i = threadIdx.x + j * 256;
+    if (i < n4) planes_store4(q8s, planes, row, 4 * i, n, (r * v[j]) * w4[i]);
+  }
+}
+
+// silu(h1) * h3 (the arithmetic of k_swiglu) into GEMM-input planes, h1 and
+// h3 summed from split-K partials in split order when splits > 0.
+__global__ void k_swiglu_planes(const float* __restrict__ h1, const float* __restrict__ h3, int rows,
+                                int F, const float* __restrict__ ws, int splits, size_t ws_split,
+                                size_t wsoff3, __bf16* planes, bool q8s) {
+  const int f4n = F / 4;
+  const size_t total = static_cast<size_t>(rows) * f4n;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int r = static_cast<int>(i / f4n), c = static_cast<int>(i - static_cast<size_t>(r) * f4n) * 4;
+    const size_t o = static_cast<size_t>(r) * F + c;
+    f4 a, b;
+    if (splits > 0) {
+      a = *reinterpret_cast<const f4*>(ws + o);
+      b = *reinterpret_cast<const f4*>(ws + wsoff3 + o);
+      for (int z = 1; z < splits; ++z) {
+        a += *reinterpret_cast<const f4*>(ws + z * ws_split + o);
+        b += *reinterpret_cast<const f4*>(ws + z * ws_split + wsoff3 + o);
+      }
+    } else {
+      a = *reinterpret_cast<const f4*>(h1 + o);
+      b = *reinterpret_cast<const f4*>(h3 + o);
+    }
+    f4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float av = a[e];
+      const float sl = av * (1.0f / (1.0f + expf(-av)));
+      out[e] = sl * b[e];
+    }
+    planes_store4(q8s, planes, r, c, F, out);
+  }
+}
+
+int kl::norm_planes_run(float* x, const float* w, int rows, int n, float eps, const float* ws,
+                        int splits, size_t ws_split, void* planes, bool q8s, hipStream_t st) {
+  if (!x || !w || !planes || rows <= 0 || n <= 0 || (splits > 0 && !ws) || (q8s && rows > 32))
+    return KL_EINVAL;
+  if (n % 32 || n > 8 * 256 * 4 || ws_split % 4 || !aligned16(x) || !aligned16(w) || !aligned16(planes))
+    return KL_EUNSUPP;
+  // Few rows (one workgroup each) summing several partials: the wide
+  // reduction first (32 rows x 16 splits took 26 us in the row kernel).
+  if (splits > 1 && rows < 128) {
+    const int rr = partials_add_run(x, rows, n, ws, splits, st);
+    if (rr != KL_OK) return rr;
+    splits = 0;
+  }
+  const int r4 = (n / 4 + 255) / 256;
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(256), 0, st, x, w, n, eps, ws, splits, ws_split,
+                       static_cast<__bf16*>(planes), q8s);
+  };
+  if (r4 <= 1) launch(k_norm_planes<1>);
+  else if (r4 <= 2) launch(k_norm_planes<2>);
+  else if (r4 <= 4) launch(k_norm_planes<4>);
+  else launch(k_norm_planes<8>);
+  return launch_rc();
+}
+
+int kl::swiglu_planes_run(const float* h1, const float* h3, int rows, int F, const float* ws, int splits,
+                          size_t ws_split, size_t wsoff3, void* planes, bool q8s, hipStream_t st) {
+  if (!planes || rows <= 0 || F <= 0 || (splits > 0 ? !ws : (!h1 || !h3)) || (q8s && rows > 32))
+    return KL_EINVAL;
+  if (F % 32 || ws_split % 4 || wsoff3 % 4 || !aligned16(planes)) return KL_EUNSUPP;
+  const size_t work = static_cast<size_t>(rows) * (F / 4);
+  const int grid = static_cast<int>(std::min<size_t>((work + 255) / 256, 8192));
+  hipLaunchKernelGGL(k_swiglu_planes, dim3(grid), dim3(256), 0, st, h1, h3, rows, F, ws, splits,
+                     ws_split, wsoff3, static_cast<__bf16*>(planes), q8s);
+  return launch_rc();
+}
+
+int kl::partials_add_run(float* x, int rows, int n, const float* ws, int splits, hipStream_t st) {
+  if (!x || !ws || rows <= 0 || n <= 0 || splits < 1) return KL_EINVAL;
+  GemmArgs ra{};
+  ra.M = rows;
+  ra.accumulate = 1;
+  ra.nseg = 1;
+  ra.ws = const_cast<float*>(ws);
+  ra.ws_split = static_cast<size_t>(rows) * n;
+  ra.splits = splits;
+  ra.seg[0].C = x;
+  ra.seg[0].N = n;
+  ra.seg[0].ldc = n;
+  const int grid = static_cast<int>(std::min<size_t>((ra.ws_split + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_gemm_reduce, dim3(grid), dim3(256), 0, st, ra);
   return launch_rc();
 }
 
