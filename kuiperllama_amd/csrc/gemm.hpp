@@ -626,7 +626,11 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
 // 1.1e-7 (one K pass) against 1.3e-7 to 2.2e-7 for k_gemm_f32_dma).  bf16 MFMA
 // runs at 16x the fp32 MFMA rate, six products at 2.7x.
 //
-// Workgroup tile 128 x 128, four waves of 64 x 64 (2 x 2 blocks of 32 x 32;
+// Workgroup tile 64 WMW x 128 with WMW = 2 (128 x 128, four waves, a 3-stage
+// ring of 48 KB stages) or 4 (256 x 128, eight waves -- two per SIMD, so a
+// wave waiting on its loads leaves the matrix core to the other -- a 2-stage
+// ring of 72 KB, block k + 1 requested while block k is computed; 25% fewer
+// operand bytes per product); each wave 64 x 64 (2 x 2 blocks of 32 x 32;
 // A operand: lane l holds A[l % 32][8 k-values], B operand W[l % 32][the
 // same 8 k-values], k-values 8 (l / 32) .. + 7 of a 16-column step; result
 // register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  The
@@ -635,9 +639,9 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
 // direct-to-LDS load instruction reads 1 KB of consecutive bytes (rows of 64
 // B in row-major planes touch half of sixteen 128 B lines each: 7-11% slower
 // on the Qwen3-4B and Qwen2.5-1.5B shapes).  K advances in blocks of 32
-// columns: the six plane tiles of a block (A0 A1 A2 W0 W1 W2, 128 rows x 64 B
-// each, 48 KB) land in LDS through a 3-stage ring (144 KB: one workgroup per
-// CU), block k + 2 requested while block k is computed.  A row holds four
+// columns: the six plane tiles of a block (A0 A1 A2 W0 W1 W2, rows of 64 B)
+// land in LDS through the ring (144 KB either way: one workgroup per CU).
+// A row holds four
 // 16-byte chunks; chunk c of row r sits in slot c ^ x6_swz(r), so the 32
 // lanes of a half wave (32 consecutive rows, one chunk each) read 32 distinct
 // 16-byte slots of the 512 B bank period.  Each block runs as two 16-column steps of 24
@@ -649,7 +653,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
 // dispatch), so tile t = (b % 8) ceil(T / 8) + b / 8 gives each XCD a
 // contiguous run of tiles whose M tiles share their W tile in its L2.
 // Split-K as k_gemm_f32_dma (blockIdx.y = split, partials to ws, then
-// k_gemm_reduce).
+// k_gemm_reduce).  The launcher (gemm_run_x6) picks the tile, and may run a
+// launch as whole rounds of tiles plus a split-K launch over the remaining
+// columns of the last output, so that the partial last round is spread over
+// every CU.
 __device__ __forceinline__ int x6_swz(int r) { return (r >> 3) & 3; }
 
 // Element (r, k) of plane p of an R x K matrix (K a multiple of 32) in the
@@ -663,16 +670,20 @@ __host__ __device__ __forceinline__ size_t x6_tile_offset(int r, int k, int p, i
 
 typedef __bf16 xbf8 __attribute__((ext_vector_type(8)));
 
-__global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
-  constexpr int BM = 128, BN = 128, BK = 32, ST = 3;
-  constexpr int PT = BM * BK;  // bf16 per plane tile
-  constexpr int SS = 6 * PT;   // per stage
-  constexpr int LPW = 12;      // 1 KB load instructions per wave and block
+template <int WMW>  // waves along M: 2 (128 x 128 tiles) or 4 (256 x 128)
+__global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
+  constexpr int BM = 64 * WMW, BN = 128, BK = 32, ST = WMW == 4 ? 2 : 3;
+  constexpr int PA = BM * BK, PW = BN * BK;   // bf16 per plane tile (A, W)
+  constexpr int SS = 3 * PA + 3 * PW;         // per stage
+  constexpr int NW = 2 * WMW;                 // waves
+  constexpr int NL = 3 * BM / 16 + 3 * BN / 16;  // 1 KB loads per stage
+  constexpr int LPW = NL / NW;
+  static_assert(LPW * NW == NL, "loads per wave");
   __shared__ __align__(1024) __bf16 L[ST * SS];
   const GemmArgs& g = x.g;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WMW, wn = wave / WMW;
   const int per = static_cast<int>(gridDim.x) >> 3;
   const int b = static_cast<int>(blockIdx.x);
   const int t = (b & 7) * per + (b >> 3);
@@ -714,23 +725,27 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
   // (l % 4) ^ x6_swz(r).  Row tiles past M or N read the last one (they only
   // feed outputs that are never stored).
   const char* src[LPW];
+  int ldo[LPW];
   const int kbs = K / BK;
   const int lra = (M - 1) >> 4, lrw = (N - 1) >> 4;
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
     const int j = LPW * wave + i;
-    const int pt = j >> 3;
-    const int c = (lane & 3) ^ x6_swz(16 * (j & 7) + (lane >> 2));
-    const int rt = pt < 3 ? min((m0 >> 4) + (j & 7), lra) : min((n0 >> 4) + (j & 7), lrw);
-    src[i] = (pt < 3 ? A : W) + (static_cast<size_t>(rt) * kbs * 1536 + 512 * (pt % 3)) * 2 +
-             64 * (lane >> 2) + 16 * c;
+    const bool isa = j < 3 * BM / 16;
+    const int jj = isa ? j : j - 3 * BM / 16;
+    const int rpp = isa ? BM / 16 : BN / 16;     // row tiles per plane
+    const int pl = jj / rpp, tr = jj % rpp;
+    const int c = (lane & 3) ^ x6_swz(16 * tr + (lane >> 2));
+    const int rt = isa ? min((m0 >> 4) + tr, lra) : min((n0 >> 4) + tr, lrw);
+    src[i] = (isa ? A : W) + (static_cast<size_t>(rt) * kbs * 1536 + 512 * pl) * 2 + 64 * (lane >> 2) + 16 * c;
+    ldo[i] = isa ? pl * PA + 512 * tr : 3 * PA + pl * PW + 512 * tr;
   }
   auto request = [&](int kb, int st) {
     __bf16* base = L + st * SS;
 #pragma unroll
     for (int i = 0; i < LPW; ++i)
       __builtin_amdgcn_global_load_lds((global_void_t*)(src[i] + static_cast<size_t>(kb) * 3072),
-                                       (lds_void_t*)(base + 512 * (LPW * wave + i)), 16, 0, 0);
+                                       (lds_void_t*)(base + ldo[i]), 16, 0, 0);
   };
   // Step s of a block: lane half h = l / 32 reads chunk 2 s + h of rows
   // 64 wm + 32 q + l % 32 (A planes) and 64 wn + 32 q + l % 32 (W planes).
@@ -751,8 +766,8 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        fa[p][pl][q] = *reinterpret_cast<const xbf8*>(base + pl * PT + oa[q][s]);
-        fw[p][pl][q] = *reinterpret_cast<const xbf8*>(base + (3 + pl) * PT + ow[q][s]);
+        fa[p][pl][q] = *reinterpret_cast<const xbf8*>(base + pl * PA + oa[q][s]);
+        fw[p][pl][q] = *reinterpret_cast<const xbf8*>(base + 3 * PA + pl * PW + ow[q][s]);
       }
   };
   gf16 acc[2][2];
@@ -787,8 +802,12 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
   } while (0)
   if (kb0 < kb1) {
     request(kb0, 0);
-    request(min(kb0 + 1, kb1 - 1), 1);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    if (ST == 3) {
+      request(min(kb0 + 1, kb1 - 1), 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __builtin_amdgcn_s_barrier();
     operands(0, 0, 0);
     int st = 0;
@@ -802,12 +821,16 @@ __global__ __launch_bounds__(256) void k_gemm_x6(GemmX6Args x) {
       const int sn = st == 0 ? ST - 1 : st - 1;
       const int st1 = st == ST - 1 ? 0 : st + 1;
       __builtin_amdgcn_sched_barrier(0);
-      request(min(kt + 2, kb1 - 1), sn);
+      if (ST == 3) request(min(kt + 2, kb1 - 1), sn);
+      else request(min(kt + 1, kb1 - 1), st1);
       operands(st, 1, 1);
       step(0);
       KL_X6_INTERLEAVE(true);
       __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(LPW) : "memory");
+      if (ST == 3)
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(LPW) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       operands(st1, 0, 0);
       step(1);

@@ -1013,28 +1013,39 @@ int kl_gemm_f32_splitk(const float* A, const float* W, float* C, int M, int N, i
 namespace {
 int device_cus();
 
-// Split count of a k_gemm_x6 launch of `tiles` tiles over nkt 32-column
-// blocks and mn output floats, one workgroup per CU: the time model is the
-// grid's rounds x blocks per split x 1.45 us, plus (splits > 1) the partials
-// written and read once and the outputs written ((2 splits + 1) x mn floats)
-// at 4 TB/s; a split count must win by 3% over the next smaller one.  On the
-// Qwen3-4B (512 rows) and Qwen2.5-1.5B (1024 rows) projections it picks the
-// best measured split of 1, 2, 3, 4, 6, 8 on every shape.
-int x6_splits(long long tiles, int nkt, size_t mn, size_t ws_floats) {
+// Time model of k_gemm_x6 launches, one workgroup per CU: rounds of the grid
+// x 32-column blocks per split x the block time of the tile (1.45 us for 128
+// x 128, 2.3 us for 256 x 128: measured on the Qwen3-4B and Qwen2.5-1.5B
+// shapes), plus (splits > 1) the partials written and read once and the
+// outputs written ((2 splits + 1) x mn floats) at 4 TB/s.
+double x6_time(long long units, int kblocks, size_t mn, int splits, double blk) {
   const long long cus = device_cus();
+  return static_cast<double>((units + cus - 1) / cus) * kblocks * blk +
+         (splits > 1 ? static_cast<double>(mn) * 4.0 * (2 * splits + 1) / 4e6 : 0.0);
+}
+
+// The split count (1 .. 8, each split at least 4 blocks, partials within
+// ws_floats) with the least modelled time; a larger count must win by 3%.
+int x6_splits(long long tiles, int nkt, size_t mn, size_t ws_floats, double blk, double* t_out) {
   int best = 1;
   double tbest = 1e300;
   for (int s = 1; s <= 8 && nkt / s >= 4; ++s) {
     if (s > 1 && static_cast<size_t>(s) * mn > ws_floats) break;
-    const long long rounds = (tiles * s + cus - 1) / cus;
-    const double t = static_cast<double>(rounds) * ((nkt + s - 1) / s) * 1.45 +
-                     (s > 1 ? static_cast<double>(mn) * 4.0 * (2 * s + 1) / 4e6 : 0.0);
+    const double t = x6_time(tiles * s, (nkt + s - 1) / s, mn, s, blk);
     if (t < tbest * 0.97) {
       tbest = t;
       best = s;
     }
   }
+  if (t_out) *t_out = tbest;
   return best;
+}
+
+template <int WMW>
+int x6_launch(GemmX6Args x, int splits, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>(8 * ((x.tiles + 7) / 8));
+  hipLaunchKernelGGL(k_gemm_x6<WMW>, dim3(grid, splits), dim3(128 * WMW), 0, st, x);
+  return launch_rc();
 }
 }  // namespace
 
@@ -1042,40 +1053,101 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
                     int accumulate, float* ws, size_t ws_bytes, hipStream_t st, int* deferred) {
   if (!planes.A || M <= 0 || K <= 0 || nseg < 1 || nseg > kGemmMaxSeg) return KL_EINVAL;
   if (K % 32 || !aligned16(planes.A)) return KL_EUNSUPP;
-  GemmArgs g{};
-  g.M = M;
-  g.K = K;
-  g.accumulate = accumulate;
-  g.nseg = nseg;
-  g.ws = ws;
-  g.tiles_m = (M + 127) / 128;
-  GemmX6Args x{};
-  x.p = planes;
-  long long tiles = 0;
-  size_t wsoff = 0;
   for (int i = 0; i < nseg; ++i) {
     const GemmSeg& sg = segs[i];
     if (!planes.W[i] || !sg.C || sg.N <= 0 || sg.ldc < sg.N || sg.S) return KL_EINVAL;
     if (!aligned16(planes.W[i])) return KL_EUNSUPP;
-    g.seg[i] = sg;
-    g.seg[i].tile0 = static_cast<int>(tiles);
-    g.seg[i].wsoff = wsoff;
-    tiles += static_cast<long long>(g.tiles_m) * ((sg.N + 127) / 128);
-    wsoff += static_cast<size_t>(M) * sg.N;
   }
+  // Tile: 256 x 128 from 256 rows (KL_X6_TILE=128 keeps 128 x 128).
+  static const int force128 = [] {
+    const char* e = std::getenv("KL_X6_TILE");
+    return e && std::atoi(e) == 128;
+  }();
+  const int wmw = M >= 256 && !force128 ? 4 : 2;
+  const int bm = 64 * wmw;
+  const double blk = wmw == 4 ? 2.3 : 1.45;
+  const int nkt = K / 32;
+  const size_t ws_floats = ws ? ws_bytes / sizeof(float) : 0;
+  auto build = [&](GemmX6Args& x, int n, const GemmSeg* sgs, const void* const* W) {
+    GemmArgs g{};
+    g.M = M;
+    g.K = K;
+    g.accumulate = accumulate;
+    g.nseg = n;
+    g.ws = ws;
+    g.tiles_m = (M + bm - 1) / bm;
+    x = GemmX6Args{};
+    x.p.A = planes.A;
+    long long tiles = 0;
+    size_t wsoff = 0;
+    for (int i = 0; i < n; ++i) {
+      x.p.W[i] = W[i];
+      g.seg[i] = sgs[i];
+      g.seg[i].tile0 = static_cast<int>(tiles);
+      g.seg[i].wsoff = wsoff;
+      tiles += static_cast<long long>(g.tiles_m) * ((sgs[i].N + 127) / 128);
+      wsoff += static_cast<size_t>(M) * sgs[i].N;
+    }
+    g.ws_split = wsoff;
+    x.g = g;
+    x.tiles = static_cast<int>(std::min<long long>(tiles, INT_MAX));
+    return tiles;
+  };
+  auto run = [&](GemmX6Args& x, int splits, bool reduce) {
+    x.g.splits = splits;
+    int r = wmw == 4 ? x6_launch<4>(x, splits, st) : x6_launch<2>(x, splits, st);
+    if (r != KL_OK || splits == 1 || !reduce) return r;
+    const int rgrid = static_cast<int>(std::min<size_t>((x.g.ws_split + 255) / 256, 4096));
+    hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, x.g);
+    return launch_rc();
+  };
+  GemmX6Args x;
+  const long long tiles = build(x, nseg, segs, planes.W);
   if (tiles > INT_MAX / 2) return KL_EUNSUPP;
-  g.ws_split = wsoff;
-  g.splits = ws ? x6_splits(tiles, K / 32, wsoff, ws_bytes / sizeof(float)) : 1;
-  x.g = g;
-  x.tiles = static_cast<int>(tiles);
-  const unsigned grid = static_cast<unsigned>(8 * ((tiles + 7) / 8));
-  hipLaunchKernelGGL(k_gemm_x6, dim3(grid, g.splits), dim3(256), 0, st, x);
-  int r = launch_rc();
-  if (deferred) *deferred = g.splits;
-  if (r != KL_OK || g.splits == 1 || deferred) return r;
-  const int rgrid = static_cast<int>(std::min<size_t>((g.ws_split + 255) / 256, 4096));
-  hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, g);
-  return launch_rc();
+  const size_t mn = x.g.ws_split;
+  double t_plain = 0;
+  const int sp = ws ? x6_splits(tiles, nkt, mn, ws_floats, blk, &t_plain) : 1;
+  // Whole rounds plus a split-K tail: the tail is the last tail_tiles tiles
+  // (whole tile columns of the last output), split to fill the CUs.
+  const long long cus = device_cus();
+  const int tm = x.g.tiles_m;
+  const GemmSeg& last = segs[nseg - 1];
+  const long long last_cols = (last.N + 127) / 128;
+  long long tail_cols = (tiles % cus + tm - 1) / tm;
+  if (ws && tiles > cus && tail_cols > 0 && tail_cols < last_cols) {
+    const long long tail = tail_cols * tm, main = tiles - tail;
+    const size_t tmn = static_cast<size_t>(M) * (last.N - (last_cols - tail_cols) * 128);
+    double t_tail = 0;
+    const int tsp = x6_splits(tail, nkt, tmn, ws_floats, blk, &t_tail);
+    const double t_split = x6_time(main, nkt, 0, 1, blk) + t_tail;
+    if (t_split < t_plain * 0.97) {
+      const int c0 = static_cast<int>((last_cols - tail_cols) * 128);
+      GemmSeg hs[kGemmMaxSeg];
+      const void* hw[kGemmMaxSeg];
+      for (int i = 0; i < nseg; ++i) {
+        hs[i] = segs[i];
+        hw[i] = planes.W[i];
+      }
+      hs[nseg - 1].N = c0;  // main: the last output's first c0 columns
+      GemmX6Args xm;
+      build(xm, nseg, hs, hw);
+      int r = run(xm, 1, true);
+      // tail: columns c0 .. N of the last output (its W planes from row c0)
+      GemmSeg ts = last;
+      ts.C = last.C + c0;
+      if (ts.bias) ts.bias = last.bias + c0;
+      ts.N = last.N - c0;
+      const void* tw = static_cast<const char*>(planes.W[nseg - 1]) +
+                       static_cast<size_t>(c0 / 16) * (K / 32) * 1536 * sizeof(__bf16);
+      GemmX6Args xt;
+      build(xt, 1, &ts, &tw);
+      if (r == KL_OK) r = run(xt, tsp, true);
+      if (deferred) *deferred = 1;
+      return r;
+    }
+  }
+  if (deferred) *deferred = sp;
+  return run(x, sp, !deferred);
 }
 
 namespace {

@@ -214,11 +214,14 @@ X6_TOL = 1e-6  # |C - A W^T| <= X6_TOL * (|A| |W|^T), elementwise (fp32 GEMMs he
 
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 64, 32), (37, 200, 96), (300, 1000, 256), (513, 130, 1024),
-                                    (512, 2560, 4096), (1024, 1536, 1536), (129, 257, 64)])
+                                    (512, 2560, 4096), (1024, 1536, 1536), (129, 257, 64),
+                                    (512, 20000, 512), (300, 33000, 128)])
 def test_gemm_x6_vs_fp64(K, gpu, M, N, Kd):
     """Within an fp32 GEMM's error of the exact product, with and without the
-    split-K workspace (the launcher picks the split count; the narrow, deep
-    shapes split)."""
+    split-K workspace (the launcher picks the tile and the split count; the
+    narrow, deep shapes split; (512, 20000) and (300, 33000) have more than a
+    round of 256 x 128 tiles and run whole rounds plus a split-K launch over
+    the last columns, the latter with ragged rows and columns)."""
     rng = np.random.default_rng(M + 3 * N + Kd)
     A = rng.standard_normal((M, Kd)).astype(np.float32)
     W = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
