@@ -629,8 +629,9 @@ __global__ __launch_bounds__(256) void k_gemm_q8_dma(GemmArgs g) {
 // Workgroup tile 64 WMW x 128 with WMW = 2 (128 x 128, four waves, a 3-stage
 // ring of 48 KB stages) or 4 (256 x 128, eight waves -- two per SIMD, so a
 // wave waiting on its loads leaves the matrix core to the other -- a 2-stage
-// ring of 72 KB, block k + 1 requested while block k is computed; 25% fewer
-// operand bytes per product); each wave 64 x 64 (2 x 2 blocks of 32 x 32;
+// ring of 72 KB; 25% fewer operand bytes per product).  A stage is refilled as
+// soon as every wave holds its operands in registers (mid-block), so each
+// block's loads are in flight for ST - 1 blocks of MFMA work; each wave 64 x 64 (2 x 2 blocks of 32 x 32;
 // A operand: lane l holds A[l % 32][8 k-values], B operand W[l % 32][the
 // same 8 k-values], k-values 8 (l / 32) .. + 7 of a 16-column step; result
 // register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]).  The
@@ -801,43 +802,40 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
     __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);                   \
   } while (0)
   if (kb0 < kb1) {
-    request(kb0, 0);
-    if (ST == 3) {
-      request(min(kb0 + 1, kb1 - 1), 1);
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
+    // Prologue: blocks kb0 .. kb0 + ST - 1 requested (clamped to the last
+    // block), block kb0 waited for.
+#pragma unroll
+    for (int s = 0; s < ST; ++s) request(min(kb0 + s, kb1 - 1), s);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((ST - 1) * LPW) : "memory");
     __builtin_amdgcn_s_barrier();
     operands(0, 0, 0);
     int st = 0;
-    // Block kt in stage st, its first-step operands in buffer 0: request
-    // block kt + 2 into the stage block kt - 1 used, read the second step's
-    // operands and run the first step, wait until block kt + 1 has landed and
-    // every wave is done reading stage st, then read block kt + 1's first
-    // step while the second step runs.  The last blocks request themselves
-    // again (a stage nobody reads afterwards).
+    // Block kt in stage st, its first-step operands in register buffer 0:
+    // read the second step's operands and run the first step; wait until
+    // block kt + 1 has landed (ST - 2 later requests may still be in flight)
+    // and every wave has read its operands of stage st, which is then free:
+    // request block kt + ST into it, read block kt + 1's first step and run
+    // the second step.  Each block's loads are thus in flight for ST - 1
+    // blocks of MFMA work.  Requests past the last block load the last block
+    // again into a stage nobody reads afterwards, so every wait is an exact
+    // vmcnt; the loop ends with a full drain.
     for (int kt = kb0; kt < kb1; ++kt) {
-      const int sn = st == 0 ? ST - 1 : st - 1;
       const int st1 = st == ST - 1 ? 0 : st + 1;
       __builtin_amdgcn_sched_barrier(0);
-      if (ST == 3) request(min(kt + 2, kb1 - 1), sn);
-      else request(min(kt + 1, kb1 - 1), st1);
       operands(st, 1, 1);
       step(0);
-      KL_X6_INTERLEAVE(true);
+      KL_X6_INTERLEAVE(false);
       __builtin_amdgcn_sched_barrier(0);
-      if (ST == 3)
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(LPW) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"((ST - 2) * LPW) : "memory");
       __builtin_amdgcn_s_barrier();
+      request(min(kt + ST, kb1 - 1), st);
       operands(st1, 0, 0);
       step(1);
-      KL_X6_INTERLEAVE(false);
+      KL_X6_INTERLEAVE(true);
       __builtin_amdgcn_sched_barrier(0);
       st = st1;
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 #undef KL_X6_INTERLEAVE
   float* wsp = g.splits > 1 ? g.ws + static_cast<size_t>(blockIdx.y) * g.ws_split + wsoff : nullptr;
