@@ -171,17 +171,24 @@ def test_split_bf16x3_bit_exact(K, gpu):
     assert np.array_equal((x0 + x1 + x2)[finite], X.astype(np.float64)[finite])
 
 
-def gemm_x6(K, A, W, bias=None, C0=None, ws=True):
+def gemm_x6(K, A, W, bias=None, C0=None, ws=True, ldc=None):
+    """C (M x N, row stride ldc) = A W^T (+ bias) (+ C0); returns the M x N part."""
     M, Kd = A.shape
     N = W.shape[0]
+    ldc = ldc or N
     dA, dW = _split_dev(K, A), _split_dev(K, W)
-    dC = D(K, C0) if C0 is not None else K.DeviceArray(M * N)
+    C = np.full((M, ldc), np.nan, np.float32)
+    if C0 is not None:
+        C[:, :N] = C0
+    dC = D(K, C)
     db = D(K, bias) if bias is not None else None
     wsa = K.DeviceArray(8 * M * N) if ws else None
-    ok(K.lib.kl_gemm_x6(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, N, db.ptr if db else None,
+    ok(K.lib.kl_gemm_x6(dA.ptr, dW.ptr, dC.ptr, M, N, Kd, ldc, db.ptr if db else None,
                         int(C0 is not None), wsa.ptr if wsa else None, wsa.nbytes if wsa else 0,
                         None), "kl_gemm_x6")
-    return dC.numpy().reshape(M, N)
+    out = dC.numpy().reshape(M, ldc)
+    assert np.all(np.isnan(out[:, N:])), "columns past N of a row were written"
+    return out[:, :N]
 
 
 def test_gemm_x6_kat_six_terms_exact(K, gpu):
@@ -234,19 +241,28 @@ def test_gemm_x6_vs_fp64(K, gpu, M, N, Kd):
         assert err <= X6_TOL
 
 
-def test_gemm_x6_bias_accumulate_and_refusals(K, O, gpu):
-    rng = np.random.default_rng(21)
-    M, N, Kd = 70, 200, 96
+@pytest.mark.parametrize("M,N,Kd,ldc", [(70, 200, 96, 200), (70, 200, 96, 212), (300, 33000, 128, 33012)])
+def test_gemm_x6_bias_accumulate(K, gpu, M, N, Kd, ldc):
+    """Bias and accumulation into C with a row stride past N; (300, 33000)
+    runs whole rounds of 256 x 128 tiles plus a split-K launch over the last
+    columns, whose output, bias and weight planes start past column 0."""
+    rng = np.random.default_rng(21 + N)
     A = rng.standard_normal((M, Kd)).astype(np.float32)
     W = rng.standard_normal((N, Kd)).astype(np.float32)
     b = rng.standard_normal(N).astype(np.float32)
     C0 = rng.standard_normal((M, N)).astype(np.float32)
     exact = A.astype(np.float64) @ W.astype(np.float64).T
     mag = np.abs(A).astype(np.float64) @ np.abs(W).astype(np.float64).T
-    yb = gemm_x6(K, A, W, bias=b)
-    ya = gemm_x6(K, A, W, C0=C0)
+    yb = gemm_x6(K, A, W, bias=b, ldc=ldc)
+    ya = gemm_x6(K, A, W, bias=b, C0=C0, ldc=ldc)
     assert np.max(np.abs(yb - (exact + b)) / (mag + np.abs(b))) <= X6_TOL
-    assert np.max(np.abs(ya - (exact + C0)) / (mag + np.abs(C0))) <= X6_TOL
+    assert np.max(np.abs(ya - (exact + b + C0)) / (mag + np.abs(b) + np.abs(C0))) <= X6_TOL
+
+
+def test_gemm_x6_refusals(K, gpu):
+    rng = np.random.default_rng(21)
+    M, N, Kd = 70, 200, 96
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
     dP = _split_dev(K, A)
     dC = K.DeviceArray(M * N)
     # K not a multiple of 32; ldc < N; a missing operand (all refused before any launch)
