@@ -5,11 +5,13 @@
 // K-contiguous.  The reference has no batched path (MatmulLayer takes a 1-D
 // input, op/matmul.cpp:20; the prompt runs token by token, demo/main.cpp:20-22).
 //
-// Four kernels share the launch arguments (GemmArgs, gemm_run.hpp), four
-// waves per workgroup: k_gemm_f32_dma (fp32), k_gemm_f32 (int8 and other K),
-// k_gemm_q8_dma (int8, at most 32 rows) and k_gemm_x6 (fp32 operands as bf16
-// planes on the bf16 matrix cores); the last two are described at their
-// definitions.
+// Four kernels share the launch arguments (GemmArgs, gemm_run.hpp; k_gemm_x6
+// wraps them with its operand planes): k_gemm_f32_dma (fp32), k_gemm_f32
+// (int8 and other K) and k_gemm_q8_dma (int8, at most 32 rows), four waves per
+// workgroup, and k_gemm_x6 (fp32 operands as bf16 planes on the bf16 matrix
+// cores; four or eight waves).  k_gemm_q8s (int8 weights prepacked in lane
+// order, at most 32 rows, eight waves) has arguments of its own.  The last
+// three are described at their definitions.
 //
 // k_gemm_f32_dma<TA> (fp32 weights, K a multiple of 32; every model
 // projection): a workgroup tile of 32 TA x 64 (TA = 2: 64 x 64, three
