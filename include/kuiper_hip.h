@@ -239,8 +239,10 @@ int kl_rope_rows(int style, int dim, int kv_dim, int head_size, float* q, int ld
  * n_pos prefill rows in one pass (no reference counterpart for the fusion:
  * the reference applies the two per token).  Row r of q (q_heads heads,
  * stride ldq) and of k (kv_heads heads, stride ldk) at position pos0 + r;
- * every k head is rotated.  head_size 64 or 128 (else KL_EUNSUPP); the same
- * values as kl_rmsnorm_rows then kl_rope_rows up to float rounding. */
+ * every k head is rotated.  head_size 64 or 128, and q, k, the norm weights
+ * and the sin/cos tables 16-byte aligned with ldq, ldk multiples of 4 (else
+ * KL_EUNSUPP); the same values as kl_rmsnorm_rows then kl_rope_rows up to
+ * float rounding. */
 int kl_qk_norm_rope_rows(int style, int head_size, int q_heads, int kv_heads, float* q, int ldq,
                          float* k, int ldk, const float* q_norm, const float* k_norm, float eps,
                          int pos0, int n_pos, const float* sin_cache, const float* cos_cache,

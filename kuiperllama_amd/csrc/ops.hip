@@ -262,58 +262,68 @@ __global__ void k_rope_rows(int style, int dim, int kv_dim, int hd, float* q, in
 }
 
 // Qwen3's per-head q/k RMSNorm followed by RoPE on rows of a prefill, in one
-// pass: one wave per (row, head), q heads then k heads; lane l < HD / 4 holds
-// the head's float4 l.  The norm is the one of k_rmsnorm_rows_w (sum of
-// squares over the lanes, y = (r * x) * w); the rotation is rope_one's
-// (rotate-half pairs (j, j + HD / 2) sit HD / 8 lanes apart and are exchanged
-// across lanes; interleaved pairs lie within a float4).  Every k head is
-// rotated (they all lie below kv_dim).
+// pass: HD / 4 lanes per (row, head) -- two heads per wave for head size 128,
+// four for 64 -- q heads then k heads; lane l of a group holds the head's
+// float4 l.  The norm is the one of k_rmsnorm_rows_w (sum of squares over the
+// group's lanes in an xor butterfly, y = (r * x) * w); the rotation is
+// rope_one's (rotate-half pairs (j, j + HD / 2) sit HD / 8 lanes apart and are
+// exchanged across lanes; interleaved pairs lie within a float4), its cos/sin
+// entries read as 16-byte vectors.  Every k head is rotated (they all lie
+// below kv_dim).
 template <int HD>
 __global__ __launch_bounds__(256) void k_qk_norm_rope_rows(
     int style, int H, int KVH, float* q, int ldq, float* k, int ldk, const float* __restrict__ qn,
     const float* __restrict__ kn, float eps, int pos0, int n, const float* __restrict__ sin_t,
     const float* __restrict__ cos_t) {
-  constexpr int C4 = HD / 4;
-  static_assert(C4 <= kWave && (HD / 8) * 2 == C4, "head size");
+  constexpr int C4 = HD / 4, PPW = kWave / C4;  // lanes per head, heads per wave
+  static_assert(PPW * C4 == kWave && (HD / 8) * 2 == C4, "head size");
   const int heads = H + KVH;
-  const long long wid = static_cast<long long>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wid >= static_cast<long long>(n) * heads) return;  // whole waves
-  const int r = static_cast<int>(wid / heads), hh = static_cast<int>(wid - static_cast<long long>(r) * heads);
+  const long long total = static_cast<long long>(n) * heads;
+  const int lane = threadIdx.x & 63, ll = lane % C4;
+  const long long wid =
+      (static_cast<long long>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * PPW + lane / C4;
+  const bool ok = wid < total;  // groups past the last (row, head) compute a clamped one, store nothing
+  const long long pid = ok ? wid : total - 1;
+  const int r = static_cast<int>(pid / heads), hh = static_cast<int>(pid - static_cast<long long>(r) * heads);
   const bool isq = hh < H;
   f4* x = reinterpret_cast<f4*>(isq ? q + static_cast<size_t>(r) * ldq + static_cast<size_t>(hh) * HD
                                     : k + static_cast<size_t>(r) * ldk + static_cast<size_t>(hh - H) * HD);
   const f4* w4 = reinterpret_cast<const f4*>(isq ? qn : kn);
-  const bool live = lane < C4;
-  const f4 v = live ? x[lane] : f4{0.f, 0.f, 0.f, 0.f};
+  const f4 v = x[ll];
   float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-  ss = wave_sum(ss);
+  ss = group_sum(ss, C4);
   const float rn = 1.f / sqrtf(ss / static_cast<float>(HD) + eps);
-  f4 y = (rn * v) * w4[live ? lane : 0];
+  f4 y = (rn * v) * w4[ll];
   const size_t t0 = static_cast<size_t>(pos0 + r) * HD;
   if (style == KL_ROPE_HALF) {
     constexpr int OFF = HD / 8;  // lanes between the two halves of a pair
     const f4 pt = {__shfl_xor(y.x, OFF), __shfl_xor(y.y, OFF), __shfl_xor(y.z, OFF),
                    __shfl_xor(y.w, OFF)};
-    const bool first = lane < OFF;
-    const int jb = 4 * (first ? lane : lane - OFF);  // index of y.x within its half
+    const bool first = ll < OFF;
+    const int jb = 4 * (first ? ll : ll - OFF);  // index of y.x within its half
+    // entries t0 + 2 (jb + c), c = 0..3: the even ones of 8 consecutive floats
+    const f4* ct = reinterpret_cast<const f4*>(cos_t + t0 + 2 * jb);
+    const f4* st = reinterpret_cast<const f4*>(sin_t + t0 + 2 * jb);
+    const f4 c0 = ct[0], c1 = ct[1], s0 = st[0], s1 = st[1];
+    const float cs[4] = {c0.x, c0.z, c1.x, c1.z}, sn[4] = {s0.x, s0.z, s1.x, s1.z};
     float out[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int j = live ? jb + c : 0;
       float v0 = first ? y[c] : pt[c], v1 = first ? pt[c] : y[c];
-      rope_pair(v0, v1, cos_t[t0 + 2 * j], sin_t[t0 + 2 * j]);
+      rope_pair(v0, v1, cs[c], sn[c]);
       out[c] = first ? v0 : v1;
     }
     y = f4{out[0], out[1], out[2], out[3]};
   } else {
-    const int e = live ? 4 * lane : 0;  // element index of y.x within the head
+    const int e = 4 * ll;  // element index of y.x within the head
+    const f4 cs = *reinterpret_cast<const f4*>(cos_t + t0 + e);
+    const f4 sn = *reinterpret_cast<const f4*>(sin_t + t0 + e);
     float a0 = y.x, a1 = y.y, b0 = y.z, b1 = y.w;
-    rope_pair(a0, a1, cos_t[t0 + e], sin_t[t0 + e]);
-    rope_pair(b0, b1, cos_t[t0 + e + 2], sin_t[t0 + e + 2]);
+    rope_pair(a0, a1, cs.x, sn.x);
+    rope_pair(b0, b1, cs.z, sn.z);
     y = f4{a0, a1, b0, b1};
   }
-  if (live) x[lane] = y;
+  if (ok) x[ll] = y;
 }
 
 // ---------------------------------------------------------------------------
@@ -823,9 +833,10 @@ int kl_qk_norm_rope_rows(int style, int head_size, int q_heads, int kv_heads, fl
   if (style != KL_ROPE_INTERLEAVED && style != KL_ROPE_HALF) return KL_EINVAL;
   if (head_size != 64 && head_size != 128) return KL_EUNSUPP;
   if (ldq % 4 || ldk % 4 || !aligned16(q) || !aligned16(k) || !aligned16(q_norm) ||
-      !aligned16(k_norm))
+      !aligned16(k_norm) || !aligned16(sin_cache) || !aligned16(cos_cache))
     return KL_EUNSUPP;
-  const long long waves = static_cast<long long>(n_pos) * (q_heads + kv_heads);
+  const long long groups = static_cast<long long>(n_pos) * (q_heads + kv_heads);
+  const long long waves = (groups + kWave / (head_size / 4) - 1) / (kWave / (head_size / 4));
   const long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
   if (blocks > INT_MAX) return KL_EINVAL;
   if (head_size == 128)

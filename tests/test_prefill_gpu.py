@@ -431,11 +431,14 @@ def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
 
 @pytest.mark.parametrize("style,hd,H,KVH,pos0,n", [(1, 128, 32, 8, 0, 40), (1, 128, 16, 8, 300, 17),
                                                   (0, 128, 8, 2, 5, 9), (1, 64, 8, 4, 7, 33),
-                                                  (0, 64, 4, 4, 0, 5)])
+                                                  (0, 64, 4, 4, 0, 5), (1, 128, 3, 2, 4, 3),
+                                                  (0, 64, 3, 2, 0, 3), (1, 64, 5, 1, 2, 7)])
 def test_qk_norm_rope_rows_matches_two_step(K, O, gpu, style, hd, H, KVH, pos0, n):
     """The fused Qwen3 q/k RMSNorm + RoPE of the prefill against the two-step
     path it replaces (kl_rmsnorm_rows per head, then kl_rope_rows, both pinned
-    to the oracle): every element within a few float roundings."""
+    to the oracle): every element within a few float roundings.  The kernel
+    packs 64 / (hd / 4) (row, head) pairs per wave; the last three cases leave
+    the last wave partly empty (15, 15 and 42 pairs)."""
     rng = np.random.default_rng(hd * H + pos0 + n + style)
     S = pos0 + n + 4
     q = rng.standard_normal((n, H * hd)).astype(np.float32)
@@ -455,6 +458,10 @@ def test_qk_norm_rope_rows_matches_two_step(K, O, gpu, style, hd, H, KVH, pos0, 
     for a, b in ((dq, dq2), (dk, dk2)):
         x, y = a.numpy(), b.numpy()
         assert np.max(np.abs(x - y)) <= 4e-7 * np.max(np.abs(y)), np.max(np.abs(x - y))
+    # tables not 16-byte aligned are refused before any launch
+    assert K.lib.kl_qk_norm_rope_rows(style, hd, H, KVH, dq.ptr, H * hd, dk.ptr, KVH * hd, dqn.ptr,
+                                      dkn.ptr, 1e-6, pos0, n, C.c_void_p(sin_t.ptr.value + 4), cos_t.ptr,
+                                      None) == -4
 
 
 # ------------------------------------------------------- whole prompt -------
