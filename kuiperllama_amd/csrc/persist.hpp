@@ -1699,9 +1699,10 @@ __global__ __launch_bounds__(kPThreads) void k_decode_persistent(PArgs a) {
       const int b = static_cast<int>(blockIdx.x);
       if (b >= items) {
         trace_mark(a, slot);  // no attention item: "inputs arrived" = now
-        // Idle until the attention output arrives: pull this workgroup's WO
-        // rows into L2, and those of the attention workgroup b - 8 ceil(items / 8)
-        // (the same XCD under round-robin dispatch), which has no time to.
+        // Idle until the attention output arrives: pull this workgroup's
+        // W1/W3 rows into L2, and slices of the W1/W3 rows of the attention
+        // workgroups of the same XCD (under round-robin dispatch), which have
+        // no time to.
         const int nw = static_cast<int>(gridDim.x);
         // The attention phase, and so the window for the pull, lengthens with
         // the number of attention items: pull up to 1.5x as much then.
