@@ -1487,25 +1487,34 @@ template <int HD>
 int attn_prefill_launch(const float* q, int ldq, const float* kc, const float* vc, int kv_dim,
                         int kv_mul, int heads, float* out, int ldo, int pos0, int n, hipStream_t st,
                         float* part = nullptr) {
-  // Head sizes 64 and 128 on the matrix cores; 32 and 256 on the vector ALUs.
+  // Head sizes 64 and 128 on the matrix cores (128: split bf16 products,
+  // KL_PREFILL_ATTN=f32 keeps the fp32 products); 32 and 256 on the vector ALUs.
   constexpr bool kMfma = HD == 64 || HD == 128;
-  const void* fn = kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_fa<kMfma ? HD : 64>)
-                         : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
-  const size_t lds = kMfma ? attn_prefill_fa_lds_bytes(HD) : attn_prefill_lds_bytes(HD);
-  static bool attr_set = false;
-  if (!attr_set) {
+  const char* env = HD == 128 ? std::getenv("KL_PREFILL_ATTN") : nullptr;  // read per launch (tests switch it)
+  const bool x6 = HD == 128 && !(env && std::strcmp(env, "f32") == 0);
+  const void* fn = x6 ? reinterpret_cast<const void*>(&k_attn_prefill_x6)
+                      : kMfma ? reinterpret_cast<const void*>(&k_attn_prefill_fa<kMfma ? HD : 64>)
+                              : reinterpret_cast<const void*>(&k_attn_prefill<HD>);
+  const size_t lds = x6 ? attn_prefill_x6_lds_bytes()
+                        : kMfma ? attn_prefill_fa_lds_bytes(HD) : attn_prefill_lds_bytes(HD);
+  static bool attr_set[2] = {false, false};  // per kernel of this head size
+  if (!attr_set[x6]) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds));
     if (e != hipSuccess) return rc(e);
-    attr_set = true;
+    attr_set[x6] = true;
   }
   const float scale = 1.f / std::sqrt(static_cast<float>(HD));
   const dim3 grid((n + kPrefillQB - 1) / kPrefillQB, heads);
   if constexpr (kMfma) {
     const int workers = part ? attn_prefill_workers(pos0, n, heads) : 0;
     const unsigned blocks = workers ? workers : grid.x * grid.y;
-    hipLaunchKernelGGL(k_attn_prefill_fa<HD>, dim3(blocks), dim3(512), lds, st, q, ldq, kc, vc,
-                       kv_dim, kv_mul, out, ldo, pos0, n, scale, heads, workers ? part : nullptr);
+    if (x6)
+      hipLaunchKernelGGL(k_attn_prefill_x6, dim3(blocks), dim3(512), lds, st, q, ldq, kc, vc,
+                         kv_dim, kv_mul, out, ldo, pos0, n, scale, heads, workers ? part : nullptr);
+    else
+      hipLaunchKernelGGL(k_attn_prefill_fa<HD>, dim3(blocks), dim3(512), lds, st, q, ldq, kc, vc,
+                         kv_dim, kv_mul, out, ldo, pos0, n, scale, heads, workers ? part : nullptr);
     if (workers) {
       const int r = launch_rc();
       if (r != KL_OK) return r;

@@ -530,4 +530,317 @@ __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restr
   *reinterpret_cast<pf4*>(out + static_cast<size_t>(p) * ldo + h * HD + c) = o * (1.f / l);
 }
 
+
+// Head size 128 with the products as split bf16 terms: k_attn_prefill_fa's
+// decomposition (stream-K units, eight waves, query group w % 4 and key half
+// w / 4, S^T = K Q^T and O^T += V^T P^T in the 16 x 16 accumulator layout, the
+// key halves merged at the end, the same partial records) with each product
+// on v_mfma_f32_16x16x32_bf16 as the six terms Xi Yj, i + j <= 2, of the
+// operands split into three bf16 planes x = x0 + x1 + x2 (x0 = bf16(x),
+// x1 = bf16(x - x0), x2 = bf16(x - x0 - x1), round to nearest even; the split
+// of k_split3), which carry all 24 significand bits: the terms left out are
+// each at most 2^-24 |x y|, so scores and outputs are as accurate as on the
+// fp32 matrix cores, at 16x the rate per product.
+//
+// Per key block every thread loads 16 floats of K (key t / 8, d 16 (t % 8) ..)
+// and 16 of V (keys 4 (t / 32) .., d 4 (t % 32) ..) into registers one block
+// ahead, and after a barrier writes their planes to LDS: K key-major (rows of
+// 256 B per plane, 16-byte chunk c of key r at slot c ^ ((r >> 1) & 7) 2, so
+// the 32 lanes of a half wave -- 16 consecutive keys, chunks c and c + 1 --
+// read 32 distinct slots of 512 B), V transposed, d-major (rows of 64 keys,
+// 128 B per plane, 8-byte chunk c of row d at slot c ^ ((d >> 2) & 15)).
+// A lane's S^T operand is K row 32 kh + 16 k + l % 16, d 32 j + 8 g .. + 7
+// (g = l / 16) against its query's Q slice, split once per row block into
+// registers.  Its scores are keys 32 kh + 16 k + 4 g + i (register i of
+// sub-block k), which as P^T's B operand of one 32-key step are k-values
+// 8 g + 4 k + i; the A operand (V^T) of output block b then reads, for d =
+// 64 (b / 4) + 4 (l % 16) + b % 4, keys 32 kh + 4 g .. + 3 and 32 kh + 16 +
+// 4 g .. + 3: two 8-byte reads of the d row.  Row 4 g + i of O^T block b is
+// that d, so a lane ends holding the output columns k_attn_prefill_fa's do.
+typedef __bf16 abf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 abf4 __attribute__((ext_vector_type(4)));
+typedef float af16 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr size_t attn_prefill_x6_lds_bytes() {
+  return 2 * 3 * static_cast<size_t>(kFaKB) * 128 * 2;  // K and V^T planes
+}
+
+typedef float af2 __attribute__((ext_vector_type(2)));
+typedef __bf16 abf2 __attribute__((ext_vector_type(2)));
+
+// Two values into their three planes (packed conversions, two per instruction).
+__device__ __forceinline__ void x6_split2(af2 v, abf2& x0, abf2& x1, abf2& x2) {
+  x0 = __builtin_convertvector(v, abf2);
+  const af2 r1 = v - __builtin_convertvector(x0, af2);
+  x1 = __builtin_convertvector(r1, abf2);
+  x2 = __builtin_convertvector(r1 - __builtin_convertvector(x1, af2), abf2);
+}
+
+__device__ __forceinline__ void x6_split8(const float (&v)[8], abf8& x0, abf8& x1, abf8& x2) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    abf2 y0, y1, y2;
+    x6_split2(af2{v[e], v[e + 1]}, y0, y1, y2);
+    x0[e] = y0[0];
+    x0[e + 1] = y0[1];
+    x1[e] = y1[0];
+    x1[e + 1] = y1[1];
+    x2[e] = y2[0];
+    x2[e + 1] = y2[1];
+  }
+}
+
+__global__ __launch_bounds__(512) void k_attn_prefill_x6(const float* __restrict__ q, int ldq,
+                                                         const float* __restrict__ kc,
+                                                         const float* __restrict__ vc, int kv_dim,
+                                                         int kv_mul, float* __restrict__ out,
+                                                         int ldo, int pos0, int n, float scale,
+                                                         int heads, float* __restrict__ part) {
+  constexpr int HD = 128, QB = kPrefillQB, KB = kFaKB;
+  constexpr int NB = HD / 16;      // 16-row blocks of O^T
+  constexpr int NH = HD / 64;      // 64-column groups of the output
+  constexpr int LDO = HD + 4;      // merge record row: o[HD], m, l
+  constexpr int PK = KB * HD;      // bf16 per plane (K or V^T)
+  constexpr size_t RF = attn_prefill_part_floats(HD);
+  static_assert(QB == 64 && KB == 64, "tile");
+  static_assert(static_cast<size_t>(QB) * LDO * sizeof(float) <= attn_prefill_x6_lds_bytes(),
+                "merge records fit the plane buffers");
+  extern __shared__ __align__(1024) float sm[];
+  __bf16* Kp = reinterpret_cast<__bf16*>(sm);  // [3][KB][HD], swizzled 16-byte chunks
+  __bf16* Vt = Kp + 3 * PK;                    // [3][HD][KB], swizzled 8-byte chunks
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = wave & 3, kh = wave >> 2;  // query group, key half
+  const int lg = lane >> 4, l16 = lane & 15;
+  const FaGeom geo = fa_geom(pos0, n);
+  long long u0, u1;
+  int h, i;
+  if (part) {
+    const long long W = geo.wh * heads, G = gridDim.x;
+    u0 = blockIdx.x * W / G;
+    u1 = (blockIdx.x + 1) * W / G;
+    h = static_cast<int>(u0 / geo.wh);
+    i = fa_locate(geo, u0 - h * geo.wh);
+  } else {
+    h = static_cast<int>(blockIdx.x) / geo.nqb;
+    i = static_cast<int>(blockIdx.x) % geo.nqb;
+    u0 = h * geo.wh + fa_seg_start(geo, i);
+    u1 = u0 + fa_seg_len(geo, i);
+  }
+  long long seg = h * geo.wh + fa_seg_start(geo, i);
+  // This thread's share of a key block: K key kr, d 16 kc16 .. + 15; V keys
+  // 4 vq .. + 3, d 4 ve .. + 3.
+  const int kr = tid >> 3, kc16 = tid & 7, vq = tid >> 5, ve = tid & 31;
+  const float scale2 = scale * 1.44269504088896340736f;
+  for (long long u = u0; u < u1;) {
+    const int len = fa_seg_len(geo, i);
+    const long long e = u1 < seg + len ? u1 : seg + len;
+    const int kbA = static_cast<int>(u - seg), kbB = static_cast<int>(e - seg);
+    const int p0 = QB * i;
+    const int rows = n - p0 < QB ? n - p0 : QB;
+    const int last = pos0 + p0 + rows - 1;  // last key any row of the block attends
+    const float* kg = kc + (h / kv_mul) * HD;
+    const float* vg = vc + (h / kv_mul) * HD;
+    // Rows past `last` read row `last` (their scores are masked, p = 0).
+    pf4 kreg[4], vreg[4];
+    auto load = [&](int j0) {
+      const int rk = j0 + kr <= last ? j0 + kr : last;
+      const pf4* ks = reinterpret_cast<const pf4*>(kg + static_cast<size_t>(rk) * kv_dim + 16 * kc16);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kreg[c] = ks[c];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int rv = j0 + 4 * vq + c <= last ? j0 + 4 * vq + c : last;
+        vreg[c] = *reinterpret_cast<const pf4*>(vg + static_cast<size_t>(rv) * kv_dim + 4 * ve);
+      }
+    };
+    auto store = [&]() {
+      const int ksw = ((kr >> 1) & 7) << 1;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        float v[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = kreg[2 * hh + c / 4][c % 4];
+        abf8 x[3];
+        x6_split8(v, x[0], x[1], x[2]);
+        const int slot = (2 * kc16 + hh) ^ ksw;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<abf8*>(Kp + pl * PK + kr * HD + 8 * slot) = x[pl];
+      }
+#pragma unroll
+      for (int dj = 0; dj < 4; ++dj) {
+        const int d = 4 * ve + dj;
+        abf2 a0, a1, a2, b0, b1, b2;
+        x6_split2(af2{vreg[0][dj], vreg[1][dj]}, a0, a1, a2);
+        x6_split2(af2{vreg[2][dj], vreg[3][dj]}, b0, b1, b2);
+        __bf16* dst = Vt + d * KB + 4 * (vq ^ ((d >> 2) & 15));
+        *reinterpret_cast<abf4*>(dst) = abf4{a0[0], a0[1], b0[0], b0[1]};
+        *reinterpret_cast<abf4*>(dst + PK) = abf4{a1[0], a1[1], b1[0], b1[1]};
+        *reinterpret_cast<abf4*>(dst + 2 * PK) = abf4{a2[0], a2[1], b2[0], b2[1]};
+      }
+    };
+    load(kbA * KB);
+    const int qrow = p0 + 16 * qg + l16;  // this lane's query (rows past n: not stored)
+    const int qpos = pos0 + (qrow < n ? qrow : n - 1);
+    abf8 qx[4][3];  // Q^T operand: d 32 j + 8 g .. + 7 of the lane's query, three planes
+    {
+      const float* qp = q + static_cast<size_t>(qrow < n ? qrow : 0) * ldq + h * HD + 8 * lg;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v[8];
+        const pf4 a = qrow < n ? *reinterpret_cast<const pf4*>(qp + 32 * j) : pf4{0.f, 0.f, 0.f, 0.f};
+        const pf4 b = qrow < n ? *reinterpret_cast<const pf4*>(qp + 32 * j + 4) : pf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v[c] = a[c];
+          v[4 + c] = b[c];
+        }
+        x6_split8(v, qx[j][0], qx[j][1], qx[j][2]);
+      }
+    }
+    float m = -INFINITY, l = 0.f;  // running maximum (base 2) and sum of this key half
+    af16 oacc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) oacc[b] = af16{0.f, 0.f, 0.f, 0.f};
+    constexpr int PX[6] = {2, 1, 0, 1, 0, 0}, PY[6] = {0, 1, 2, 0, 1, 0};  // smallest terms first
+    for (int kb = kbA; kb < kbB; ++kb) {
+      const int j0 = kb * KB;
+      __syncthreads();  // every wave is done with the previous block's planes (and the records)
+      store();
+      if (kb + 1 < kbB) load(j0 + KB);
+      __syncthreads();  // this block's planes are in LDS
+      // S^T[key][query] for keys 32 kh + 16 k + 4 lg + r of the block.
+      af16 sacc[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) sacc[k] = af16{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        abf8 kf[2][3];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int r = 32 * kh + 16 * k + l16;
+          const int slot = (4 * j + lg) ^ (((r >> 1) & 7) << 1);
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl) kf[k][pl] = *reinterpret_cast<const abf8*>(Kp + pl * PK + r * HD + 8 * slot);
+        }
+#pragma unroll
+        for (int t = 0; t < 6; ++t)
+#pragma unroll
+          for (int k = 0; k < 2; ++k)
+            sacc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[k][PX[t]], qx[j][PY[t]], sacc[k], 0, 0, 0);
+      }
+      pf4 sc[2];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = j0 + 16 * (2 * kh + k) + 4 * lg + r;
+          const float v = sacc[k][r];
+          sc[k][r] = key <= qpos ? v * scale2 : -INFINITY;
+          mx = fmaxf(mx, sc[k][r]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m, mx);
+      // A key half with no key at or before the row yet keeps max -inf, sum 0.
+      const float alpha = m == -INFINITY ? 0.f : exp2f(m - mn);
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = sc[k][r];
+          const float pv = v == -INFINITY ? 0.f : exp2f(v - mn);
+          sc[k][r] = pv;
+          sum += pv;
+        }
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      l = l * alpha + sum;
+      m = mn;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) oacc[b] *= alpha;
+      // P^T operand: k-value 8 lg + 4 k + r is key 32 kh + 16 k + 4 lg + r.
+      abf8 pb[3];
+      {
+        float v[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = sc[c / 4][c % 4];
+        x6_split8(v, pb[0], pb[1], pb[2]);
+      }
+      const int c0 = 8 * kh + lg, c1 = 8 * kh + 4 + lg;  // 4-key chunks of the V^T rows
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int d = 64 * (b / 4) + 4 * l16 + (b % 4);
+        const int sw = (d >> 2) & 15;
+        abf8 vf[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+          const __bf16* row = Vt + pl * PK + d * KB;
+          const abf4 lo = *reinterpret_cast<const abf4*>(row + 4 * (c0 ^ sw));
+          const abf4 hi = *reinterpret_cast<const abf4*>(row + 4 * (c1 ^ sw));
+          vf[pl] = abf8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int t = 0; t < 6; ++t)
+          oacc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[PX[t]], pb[PY[t]], oacc[b], 0, 0, 0);
+      }
+    }
+    // Output columns 64 hb + 16 lg + 4 r .. + 3 of this lane's query.
+    auto cols = [&](int hb, int r) {
+      return pf4{oacc[4 * hb][r], oacc[4 * hb + 1][r], oacc[4 * hb + 2][r], oacc[4 * hb + 3][r]};
+    };
+    // Merge the key halves: half 1 leaves (o, m, l) in LDS, half 0 combines.
+    __syncthreads();  // the last block's planes are consumed
+    float* rec = sm + (16 * qg + l16) * LDO;
+    if (kh == 1) {
+#pragma unroll
+      for (int hb = 0; hb < NH; ++hb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<pf4*>(rec + 64 * hb + 16 * lg + 4 * r) = cols(hb, r);
+      if (lg == 0) {
+        rec[HD] = m;
+        rec[HD + 1] = l;
+      }
+    }
+    __syncthreads();
+    if (kh == 0 && qrow < n) {
+      const float m1 = rec[HD], l1 = rec[HD + 1];
+      const float mm = fmaxf(m, m1);
+      const float w0 = m == -INFINITY ? 0.f : exp2f(m - mm);
+      const float w1 = m1 == -INFINITY ? 0.f : exp2f(m1 - mm);
+      l = l * w0 + l1 * w1;
+      const bool whole = kbA == 0 && kbB == len;
+      float* dst;
+      if (whole) {
+        dst = out + static_cast<size_t>(qrow) * ldo + h * HD;
+      } else {
+        dst = part + ((2 * static_cast<size_t>(blockIdx.x) + (u == u0 ? 0 : 1)) * QB + (qrow - p0)) * RF;
+        if (lg == 0) {
+          dst[HD] = mm * 0.69314718055994530942f;  // natural units for the merge
+          dst[HD + 1] = l;
+        }
+      }
+#pragma unroll
+      for (int hb = 0; hb < NH; ++hb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 64 * hb + 16 * lg + 4 * r;
+          pf4 o = cols(hb, r) * w0 + *reinterpret_cast<const pf4*>(rec + d) * w1;
+          if (whole) o = o / l;
+          *reinterpret_cast<pf4*>(dst + d) = o;
+        }
+    }
+    u = e;
+    seg += len;
+    if (++i == geo.nqb) {
+      i = 0;
+      ++h;
+    }
+  }
+}
+
 }  // namespace kl

@@ -346,7 +346,15 @@ def test_rope_rows_bit_exact(K, O, gpu, style, dim, kv, hd, pos0, n):
                                               (4, 2, 32, 80, 17, 50), (12, 6, 128, 4096, 3900, 100),
                                               (8, 8, 64, 70, 0, 1), (8, 2, 64, 300, 130, 70),
                                               (4, 2, 256, 200, 0, 150), (2, 2, 256, 160, 37, 100)])
-def test_attn_prefill_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
+@pytest.mark.parametrize("attn", ["split", "f32"])
+def test_attn_prefill_vs_oracle(K, O, gpu, monkeypatch, attn, H, kvm, hd, S, pos0, n):
+    """Head size 128 runs the split-bf16-product kernel by default and the
+    fp32 matrix-core one with KL_PREFILL_ATTN=f32 (read per launch); both
+    against the oracle's MHA."""
+    if attn == "f32":
+        if hd != 128:
+            pytest.skip("one kernel for this head size")
+        monkeypatch.setenv("KL_PREFILL_ATTN", "f32")
     rng = np.random.default_rng(H * S + pos0 + n)
     kvd = H // kvm * hd
     kc = rng.standard_normal((1, S, kvd)).astype(np.float32)
@@ -384,7 +392,8 @@ def _fa_workers(pos0, n, H, cus=256):
                                               (32, 4, 128, 520, 0, 512), (8, 2, 64, 300, 130, 70),
                                               (6, 3, 128, 400, 30, 300), (2, 1, 128, 2100, 0, 2048),
                                               (16, 4, 64, 700, 0, 640), (64, 8, 128, 64, 0, 16)])
-def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
+@pytest.mark.parametrize("attn", ["split", "f32"])
+def test_attn_prefill_ws_vs_oracle(K, O, gpu, monkeypatch, attn, H, kvm, hd, S, pos0, n):
     """kl_attn_prefill_ws: where the causal segments (64-row block, head) are
     unequal or fewer than the CUs, equal ranges of (row block, key block)
     units per workgroup, cut segments merged afterwards; a second launch on
@@ -394,7 +403,12 @@ def test_attn_prefill_ws_vs_oracle(K, O, gpu, H, kvm, hd, S, pos0, n):
     segment), ranges crossing segment boundaries (512 rows from position 0),
     head size 64, a start off the 64 grid (pieces where a row's keys are all
     masked), 2048 rows (long segments over many workgroups), and 16 rows x
-    64 heads (one unit per segment: no split)."""
+    64 heads (one unit per segment: no split).  Head size 128 with both its
+    kernels (split bf16 products, default; fp32 products)."""
+    if attn == "f32":
+        if hd != 128:
+            pytest.skip("one kernel for this head size")
+        monkeypatch.setenv("KL_PREFILL_ATTN", "f32")
     rng = np.random.default_rng(H * S + pos0 + n + 7)
     kvd = H // kvm * hd
     kc = rng.standard_normal((1, S, kvd)).astype(np.float32)
