@@ -151,7 +151,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 }
 
 // Head sizes 64 and 128 on the matrix cores: FlashAttention-2 style on
-// v_mfma_f32_16x16x4f32 with no exchange between waves inside a key block.
+// v_mfma_f32_16x16x4f32 with no exchange between waves inside a key block
+// (head size 128 runs k_attn_prefill_x6 below unless KL_PREFILL_ATTN=f32).
 // A workgroup of eight waves takes 64 query rows of one head and walks key
 // blocks of 64: wave w computes for query rows 16 (w % 4) .. + 15 and the
 // keys of half w / 4 of every block, two waves per SIMD; the two halves'
