@@ -501,6 +501,37 @@ def test_engine_prefill_f32_gemm_path(K, O, gpu, monkeypatch):
     assert nxt == int(np.argmax(lg))
 
 
+@pytest.mark.parametrize("name", ["tiny_llama3", "tiny_qwen3", "tiny_qwen2_q8"])
+def test_engine_prefill_small_chunks_vs_oracle(K, O, gpu, monkeypatch, name):
+    """A prompt longer than a prefill pass (KL_PREFILL_CHUNK=64: passes of 64,
+    64 and 22 rows, each attending the cache rows of the passes before it)
+    against the oracle's token-by-token run: the last logits, the cache rows
+    on both sides of each pass boundary, and decoding on from the cache."""
+    monkeypatch.setenv("KL_PREFILL_CHUNK", "64")
+    cfg = K.TINY[name].with_(seq_len=256)
+    img = K.synth_image(cfg)
+    P = 150
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    eng = K.Engine(img, cfg)
+    nxt, lg, _ = eng.prefill(prompt)
+    om = O.Model(img, cfg.family, cfg.quant)
+    for pos in range(P - 1):
+        om.step(prompt[pos], pos)
+    ref = om.step(prompt[P - 1], P - 1)
+    assert rel(lg, ref) < LOGIT_RTOL
+    for layer in (0, cfg.layers - 1):
+        for pos in (0, 63, 64, 127, 128, P - 1):
+            for which_v in (False, True):
+                a, b = eng.kv_row(layer, pos, which_v), om.kv_row(layer, pos, which_v)
+                assert np.max(np.abs(a - b)) <= 1e-5 * max(np.max(np.abs(b)), 1.0), (layer, pos)
+    tok = O.argmax(ref)
+    for pos in range(P, P + 4):
+        _, lg2 = eng.step(tok, pos)
+        ref2 = om.step(tok, pos)
+        assert rel(lg2, ref2) < LOGIT_RTOL
+        tok = O.argmax(ref2)
+
+
 def _prefill_cfg(K, name):
     if name == "tiny_hd256":  # head size 256 (the VALU attention with 32-key blocks)
         return K.TINY["tiny_llama2"].with_(name="tiny_hd256", dim=512, hidden_dim=768, heads=2,
