@@ -251,7 +251,11 @@ int kl_qk_norm_rope_rows(int style, int head_size, int q_heads, int kv_heads, fl
 /* MHAKernel (KI:22-28) for query positions pos0 .. pos0+n_pos-1 at once:
  * row r of q (stride ldq, head_num*head_size floats) attends key/value rows
  * 0 .. pos0+r of one layer's caches ([seq_len][kv_dim]), causal; out row r
- * (stride ldo).  head_size 32, 64, 128 or 256 (else KL_EUNSUPP). */
+ * (stride ldo).  head_size 32, 64, 128 or 256 (else KL_EUNSUPP).  Head sizes
+ * 64 and 128 run on the matrix cores: 128 with the products as split bf16
+ * terms (x = x0 + x1 + x2, six partial products, as accurate as fp32
+ * products; KL_PREFILL_ATTN=f32 in the environment selects the fp32 products),
+ * 64 with fp32 products. */
 int kl_attn_prefill(int pos0, int n_pos, int head_num, int kv_mul, int head_size, const float* q,
                     int ldq, const float* key_cache, const float* value_cache, int kv_dim,
                     float* out, int ldo, void* stream);
