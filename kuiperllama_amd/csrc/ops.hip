@@ -1276,6 +1276,9 @@ int kl::gemm_run_q8s(const void* planes, int M, int K, int group_size, int nseg,
 // RMSNorm of one row per workgroup into GEMM-input planes (the arithmetic
 // of k_rmsnorm_rows_b), after x += the row's split-K partials summed in split
 // order (the arithmetic of k_gemm_reduce with accumulate), written back.
+// With gridDim.y > 1 (no partials), workgroup (row, c) computes the row's
+// norm the same way and stores float4 columns [c, c + 1) n4 / gridDim.y only,
+// so that a few rows still spread over many CUs (same bits).
 template <int R>
 __global__ __launch_bounds__(256) void k_norm_planes(float* x, const float* __restrict__ w, int n,
                                                      float eps, const float* __restrict__ ws,
@@ -1306,10 +1309,12 @@ __global__ __launch_bounds__(256) void k_norm_planes(float* x, const float* __re
   }
   ss = block_sum(ss, red);
   const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+  const int c0 = static_cast<int>(blockIdx.y * static_cast<long long>(n4) / gridDim.y);
+  const int c1 = static_cast<int>((blockIdx.y + 1) * static_cast<long long>(n4) / gridDim.y);
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int i = threadIdx.x + j * 256;
-    if (i < n4) planes_store4(q8s, planes, row, 4 * i, n, (r * v[j]) * w4[i]);
+    if (i >= c0 && i < c1) planes_store4(q8s, planes, row, 4 * i, n, (r * v[j]) * w4[i]);
   }
 }
 
@@ -1360,9 +1365,12 @@ int kl::norm_planes_run(float* x, const float* w, int rows, int n, float eps, co
     if (rr != KL_OK) return rr;
     splits = 0;
   }
+  // Few rows and no partials left (x is only read): the norm spread over up to
+  // 8 workgroups per row, each storing a slice.
+  const int slices = splits == 0 && rows < 128 ? std::max(1, std::min(8, 256 / rows)) : 1;
   const int r4 = (n / 4 + 255) / 256;
   auto launch = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(rows), dim3(256), 0, st, x, w, n, eps, ws, splits, ws_split,
+    hipLaunchKernelGGL(kern, dim3(rows, slices), dim3(256), 0, st, x, w, n, eps, ws, splits, ws_split,
                        static_cast<__bf16*>(planes), q8s);
   };
   if (r4 <= 1) launch(k_norm_planes<1>);
