@@ -207,6 +207,19 @@ int kl_split_bf16x3(const float* x, int rows, int cols, int ldx, void* planes, v
 int kl_gemm_x6(const void* a_planes, const void* w_planes, float* C, int M, int N, int K, int ldc,
                const float* bias, int accumulate, void* workspace, size_t workspace_bytes,
                void* stream);
+/* kl_gemm_x6 told how many of W's planes carry bits (no reference
+ * counterpart: a fast path for weights exported from bf16 checkpoints).
+ * w_planes_used 1: W's planes 1 and 2 are all zero (every weight a bf16 value,
+ * see kl_x6_weight_planes), so only the three products Ai W0^T are formed --
+ * the same values as kl_gemm_x6, whose other three terms are then exact
+ * zeros; on W with nonzero planes 1 or 2 it drops them.  3: kl_gemm_x6.  Else
+ * KL_EINVAL. */
+int kl_gemm_x6w(const void* a_planes, const void* w_planes, int w_planes_used, float* C, int M, int N,
+                int K, int ldc, const float* bias, int accumulate, void* workspace,
+                size_t workspace_bytes, void* stream);
+/* *planes_used = 1 if planes 1 and 2 of W (N x K, kl_split_bf16x3's format)
+ * are all zero, else 3; synchronous on stream (allocates one word). */
+int kl_x6_weight_planes(const void* w_planes, int N, int K, int* planes_used, void* stream);
 
 /* MatmulKernelQuant (KI:12-14; cuda/matmul_kernel.cu:111-134) for prompts of
  * at most 32 rows, bound by the int8 weight bytes: the weights prepacked once

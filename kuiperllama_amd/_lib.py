@@ -99,6 +99,8 @@ _SIGS = {
     "kl_split_bf16x3_bytes": (_sz, [_i, _i]),
     "kl_split_bf16x3": (_i, [_p, _i, _i, _i, _p, _p]),
     "kl_gemm_x6": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _i, _p, _sz, _p]),
+    "kl_gemm_x6w": (_i, [_p, _p, _i, _p, _i, _i, _i, _i, _p, _i, _p, _sz, _p]),
+    "kl_x6_weight_planes": (_i, [_p, _i, _i, C.POINTER(C.c_int), _p]),
     "kl_q8s_packed_bytes": (_sz, [_i, _i, _i]),
     "kl_q8s_pack": (_i, [_p, _p, _i, _i, _i, _p, _p]),
     "kl_gemm_q8s": (_i, [_p, _i, _i, _i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),

@@ -393,6 +393,9 @@ int parse_image(const void* image, size_t size, int family, int quant, ImageLayo
 // split-product prefill GEMM: 3 planes of N x K each.
 struct XPlanes {
   const void *q, *k, *v, *o, *w1, *w2, *w3;
+  // Bit i set: matrix i (q k v o w1 w2 w3) has all-zero planes 1 and 2 (bf16-exact
+  // weights), so its GEMMs load plane 0 only and form three products.
+  unsigned one;
 };
 
 struct LayerDev {
@@ -1636,7 +1639,29 @@ int prefill_planes(kl_engine* e, int last_rows) {
     Ld.xp.w1 = planes(Ld.w1, F, D);
     Ld.xp.w2 = planes(Ld.w2, D, F);
     Ld.xp.w3 = planes(Ld.w3, F, D);
+    Ld.xp.one = 0;
   }
+  // Which matrices are bf16-exact (planes 1 and 2 all zero): one flag word per
+  // matrix, read back once.
+  if (r != KL_OK) return r;
+  unsigned* flags = nullptr;
+  const size_t nf = 7 * static_cast<size_t>(m.L);
+  if (hipMalloc(&flags, nf * sizeof(unsigned)) != hipSuccess) return KL_ENOMEM;
+  r = rc(hipMemsetAsync(flags, 0, nf * sizeof(unsigned), hs));
+  for (int l = 0; l < m.L && r == KL_OK; ++l) {
+    const XPlanes& xp = e->layers[l].xp;
+    const void* pl[7] = {xp.q, xp.k, xp.v, xp.o, xp.w1, xp.w2, xp.w3};
+    const int rows[7] = {Dq, Dkv, Dkv, D, F, D, F}, cols[7] = {D, D, D, Dq, D, F, D};
+    for (int i = 0; i < 7 && r == KL_OK; ++i)
+      r = x6_planes_flag_run(pl[i], rows[i], cols[i], flags + 7 * l + i, hs);
+  }
+  std::vector<unsigned> h(nf, 1u);
+  if (r == KL_OK) r = rc(hipMemcpyAsync(h.data(), flags, nf * sizeof(unsigned), hipMemcpyDeviceToHost, hs));
+  if (r == KL_OK) r = rc(hipStreamSynchronize(hs));
+  hipFree(flags);
+  for (int l = 0; l < m.L && r == KL_OK; ++l)
+    for (int i = 0; i < 7; ++i)
+      if (h[7 * l + i] == 0) e->layers[l].xp.one |= 1u << i;
   return r;
 }
 
@@ -1665,7 +1690,9 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
   const bool fast = e->pf_x6 || q8s;
   const size_t nD = static_cast<size_t>(n) * D, nF = static_cast<size_t>(n) * F;
   int pend = 0;
-  auto gemm_fast = [&](int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc, int* deferred) {
+  // wone: every W of the launch is bf16-exact (plane 0 only).
+  auto gemm_fast = [&](int k, int nseg, const GemmSeg* sg, const void* const* wx, int acc, int* deferred,
+                       bool wone) {
     if (q8s) {
       GemmSeg s2[kGemmMaxSeg];
       for (int i = 0; i < nseg; ++i) {
@@ -1678,6 +1705,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     GemmX6Planes p{};
     p.A = e->pf_ax;
     for (int i = 0; i < nseg; ++i) p.W[i] = wx[i];
+    p.w_planes = wone ? 1 : 3;
     PF(gemm_run_x6(p, n, k, nseg, sg, acc, e->pf_ws, e->pf_ws_bytes, hs, deferred));
   };
   for (int l = 0; l < m.L && r == KL_OK; ++l) {
@@ -1706,7 +1734,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
         PF(norm_planes_run(e->pf_x, Ld.rms_att, n, D, e->eps, e->pf_ws, pend, nD, e->pf_ax, q8s, hs));
         pend = 0;
         const void* wx[3] = {Ld.xp.q, Ld.xp.k, Ld.xp.v};
-        gemm_fast(D, 3, sg, wx, 0, nullptr);
+        gemm_fast(D, 3, sg, wx, 0, nullptr, (Ld.xp.one & 7u) == 7u);
       } else {
         PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
         const int sp = splits_for(Dq + 2 * Dkv, D, true);
@@ -1732,17 +1760,17 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
       int dwo = 1, d13 = 1, d2 = 1;
       const GemmSeg so = proj_seg(e, Ld.wo, e->pf_x, nullptr, D, Dq, D);
       PF(q8s ? q8s_split_run(e->pf_att, n, Dq, Dq, e->pf_ax, hs) : split3_run(e->pf_att, n, Dq, Dq, e->pf_ax, hs));
-      gemm_fast(Dq, 1, &so, &Ld.xp.o, 1, &dwo);
+      gemm_fast(Dq, 1, &so, &Ld.xp.o, 1, &dwo, (Ld.xp.one >> 3) & 1u);
       PF(norm_planes_run(e->pf_x, Ld.rms_ffn, n, D, e->eps, e->pf_ws, dwo > 1 ? dwo : 0, nD, e->pf_ax,
                          q8s, hs));
       const GemmSeg s13[2] = {proj_seg(e, Ld.w1, e->pf_h1, nullptr, F, D, F),
                               proj_seg(e, Ld.w3, e->pf_h3, nullptr, F, D, F)};
       const void* wx[2] = {Ld.xp.w1, Ld.xp.w3};
-      gemm_fast(D, 2, s13, wx, 0, &d13);
+      gemm_fast(D, 2, s13, wx, 0, &d13, (Ld.xp.one & 0x50u) == 0x50u);
       PF(swiglu_planes_run(e->pf_h1, e->pf_h3, n, F, e->pf_ws, d13 > 1 ? d13 : 0, 2 * nF, nF, e->pf_ax,
                            q8s, hs));
       const GemmSeg s2 = proj_seg(e, Ld.w2, e->pf_x, nullptr, D, F, D);
-      gemm_fast(F, 1, &s2, &Ld.xp.w2, 1, &d2);
+      gemm_fast(F, 1, &s2, &Ld.xp.w2, 1, &d2, (Ld.xp.one >> 5) & 1u);
       pend = d2 > 1 ? d2 : 0;
     } else {
       {

@@ -673,13 +673,18 @@ __host__ __device__ __forceinline__ size_t x6_tile_offset(int r, int k, int p, i
 
 typedef __bf16 xbf8 __attribute__((ext_vector_type(8)));
 
-template <int WMW>  // waves along M: 2 (128 x 128 tiles) or 4 (256 x 128)
+// NPW = 1: W's planes 1 and 2 are all zero (W holds bf16 values exactly, as
+// weights exported from bf16 checkpoints do); only plane 0 is loaded and the
+// three terms Ai W0 are formed, in the order the six-term step forms them, so
+// the result is the six-term one (the other three terms are exact zeros).
+template <int WMW, int NPW>  // waves along M: 2 (128 x 128 tiles) or 4 (256 x 128); W planes
 __global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
+  static_assert(NPW == 1 || NPW == 3, "weight planes");
   constexpr int BM = 64 * WMW, BN = 128, BK = 32, ST = WMW == 4 ? 2 : 3;
   constexpr int PA = BM * BK, PW = BN * BK;   // bf16 per plane tile (A, W)
-  constexpr int SS = 3 * PA + 3 * PW;         // per stage
+  constexpr int SS = 3 * PA + NPW * PW;       // per stage
   constexpr int NW = 2 * WMW;                 // waves
-  constexpr int NL = 3 * BM / 16 + 3 * BN / 16;  // 1 KB loads per stage
+  constexpr int NL = 3 * BM / 16 + NPW * BN / 16;  // 1 KB loads per stage
   constexpr int LPW = NL / NW;
   static_assert(LPW * NW == NL, "loads per wave");
   __shared__ __align__(1024) __bf16 L[ST * SS];
@@ -720,7 +725,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
   const int kb1 = (static_cast<int>(blockIdx.y) + 1) * nkt / g.splits;
   const char* A = static_cast<const char*>(x.p.A);
 
-  // Load instruction i of this wave fills 1 KB j = 12 wave + i of a stage:
+  // Load instruction i of this wave fills 1 KB j = LPW wave + i of a stage:
   // plane (j / 8) % 3 of operand j < 24 ? A : W, rows 16 (j % 8) .. + 15 of
   // the workgroup tile (one 16-row tile of the plane format: 1 KB of
   // consecutive bytes per k block, the next k block 3 KB further on); lane l
@@ -762,7 +767,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
       oa[q][s] = ra * BK + 8 * ((2 * s + h) ^ x6_swz(ra));
       ow[q][s] = rw * BK + 8 * ((2 * s + h) ^ x6_swz(rw));
     }
-  xbf8 fa[2][3][2], fw[2][3][2];  // [register buffer][plane][block]
+  xbf8 fa[2][3][2], fw[2][NPW][2];  // [register buffer][plane][block]
   auto operands = [&](int st, int s, int p) {
     const __bf16* base = L + st * SS;
 #pragma unroll
@@ -770,7 +775,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         fa[p][pl][q] = *reinterpret_cast<const xbf8*>(base + pl * PA + oa[q][s]);
-        fw[p][pl][q] = *reinterpret_cast<const xbf8*>(base + 3 * PA + pl * PW + ow[q][s]);
+        if (pl < NPW) fw[p][pl][q] = *reinterpret_cast<const xbf8*>(base + 3 * PA + pl * PW + ow[q][s]);
       }
   };
   gf16 acc[2][2];
@@ -780,28 +785,33 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_x6(GemmX6Args x) {
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][c][r] = 0.f;
-  // The six products of one step, smallest terms first.
+  // The six products of one step, smallest terms first (NPW = 1: the three
+  // with W0, in the same relative order).
   auto step = [&](int p) {
+    constexpr int NT = NPW == 3 ? 6 : 3;
     constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PW[6] = {0, 1, 2, 0, 1, 0};
+    constexpr int PA1[3] = {2, 1, 0};
 #pragma unroll
-    for (int k = 0; k < 6; ++k)
+    for (int k = 0; k < NT; ++k)
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
-          acc[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][PA[k]][a], fw[p][PW[k]][c], acc[a][c], 0,
+          acc[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][NPW == 3 ? PA[k] : PA1[k]][a],
+                                                              fw[p][NPW == 3 ? PW[k] : 0][c], acc[a][c], 0,
                                                               0, 0);
   };
   // One LDS operand read (and, with loads, one direct-to-LDS request) after
-  // each of the first 12 MFMAs of a step.
+  // each of the first (3 + NPW) 2 MFMAs of a step.
+  constexpr int NRD = (3 + NPW) * 2, NMF = (NPW == 3 ? 6 : 3) * 4;
 #define KL_X6_INTERLEAVE(loads)                                           \
   do {                                                                    \
-    _Pragma("unroll") for (int i_ = 0; i_ < 12; ++i_) {                   \
+    _Pragma("unroll") for (int i_ = 0; i_ < NRD; ++i_) {                  \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  \
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  \
       if (loads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);       \
     }                                                                     \
-    __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);                   \
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);            \
   } while (0)
   if (kb0 < kb1) {
     // Prologue: blocks kb0 .. kb0 + ST - 1 requested (clamped to the last
@@ -892,6 +902,26 @@ __device__ __forceinline__ void planes_store4(bool q8s, __bf16* out, int r, int 
 
 // fp32 rows -> the three bf16 planes x0, x1, x2 of k_gemm_x6 in the tiled
 // plane format (x6_tile_offset); eight values per thread.
+// Whether planes 1 and 2 of a rows x K matrix in the tiled plane format hold
+// any nonzero bit in rows < rows (tiles of 1536 bf16, row-tile-major: plane 0
+// at 0, planes 1 and 2 at 512 .. 1535, rows of 32; the padding rows of the
+// last row tile are never written): *flag |= 1 if so (a bf16-exact matrix
+// splits into zero planes 1 and 2).
+__global__ void k_x6_planes_nonzero(const unsigned* __restrict__ planes, int rows, int K, size_t tiles,
+                                    unsigned* flag) {
+  unsigned acc = 0;
+  const size_t words = tiles * 512;  // 32-bit words of planes 1 and 2
+  const int kt = K / 32;             // tiles per row tile
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < words;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t t = i / 512;
+    const int w = static_cast<int>(i % 512);
+    const int row = 16 * static_cast<int>(t / kt) + (w % 256) / 16;
+    if (row < rows) acc |= planes[t * 768 + 256 + w];
+  }
+  if (acc) atomicOr(flag, 1u);
+}
+
 __global__ void k_split3(const float* __restrict__ x, int rows, int cols, int ldx,
                          __bf16* __restrict__ out) {
   const int c8 = cols / 8;

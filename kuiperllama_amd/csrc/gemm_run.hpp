@@ -43,6 +43,7 @@ struct GemmArgs {
 struct GemmX6Planes {
   const void* A;
   const void* W[kGemmMaxSeg];
+  int w_planes;  // 1: every W's planes 1 and 2 are zero (bf16-exact weights); 0 or 3: all three
 };
 
 struct GemmX6Args {
@@ -87,6 +88,10 @@ int gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const GemmSe
 
 // Host launcher (ops.hip) of k_split3: rows x cols fp32 (stride ldx, cols a
 // multiple of 32) into the tiled planes (x6_plane_bytes(rows, cols) bytes).
+// *flag |= 1 if planes 1 or 2 of a rows x K matrix in the tiled plane format
+// hold a nonzero bit (so the matrix needs all three planes; else plane 0 is
+// the matrix exactly).  Asynchronous; *flag must start at 0.
+int x6_planes_flag_run(const void* planes, int rows, int K, unsigned* flag, hipStream_t st);
 int split3_run(const float* x, int rows, int cols, int ldx, void* planes, hipStream_t st);
 
 // Short int8 prompts: bytes of a prepacked int8 matrix (q8s_pack_run) and of

@@ -1052,10 +1052,10 @@ int x6_splits(long long tiles, int nkt, size_t mn, size_t ws_floats, double blk,
   return best;
 }
 
-template <int WMW>
+template <int WMW, int NPW>
 int x6_launch(GemmX6Args x, int splits, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(8 * ((x.tiles + 7) / 8));
-  hipLaunchKernelGGL(k_gemm_x6<WMW>, dim3(grid, splits), dim3(128 * WMW), 0, st, x);
+  hipLaunchKernelGGL((k_gemm_x6<WMW, NPW>), dim3(grid, splits), dim3(128 * WMW), 0, st, x);
   return launch_rc();
 }
 }  // namespace
@@ -1075,6 +1075,9 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
     return e && std::atoi(e) == 128;
   }();
   const int wmw = M >= 256 && !force128 ? 4 : 2;
+  // W planes (1: bf16-exact weights).  The split and tail choice ignores it,
+  // so both forms sum in the same order and give the same values.
+  const int npw = planes.w_planes == 1 ? 1 : 3;
   const int bm = 64 * wmw;
   const double blk = wmw == 4 ? 2.3 : 1.45;
   const int nkt = K / 32;
@@ -1106,7 +1109,8 @@ int kl::gemm_run_x6(const GemmX6Planes& planes, int M, int K, int nseg, const Ge
   };
   auto run = [&](GemmX6Args& x, int splits, bool reduce) {
     x.g.splits = splits;
-    int r = wmw == 4 ? x6_launch<4>(x, splits, st) : x6_launch<2>(x, splits, st);
+    int r = wmw == 4 ? (npw == 1 ? x6_launch<4, 1>(x, splits, st) : x6_launch<4, 3>(x, splits, st))
+                     : (npw == 1 ? x6_launch<2, 1>(x, splits, st) : x6_launch<2, 3>(x, splits, st));
     if (r != KL_OK || splits == 1 || !reduce) return r;
     const int rgrid = static_cast<int>(std::min<size_t>((x.g.ws_split + 255) / 256, 4096));
     hipLaunchKernelGGL(k_gemm_reduce, dim3(rgrid), dim3(256), 0, st, x.g);
@@ -1409,6 +1413,16 @@ int kl::partials_add_run(float* x, int rows, int n, const float* ws, int splits,
   return launch_rc();
 }
 
+int kl::x6_planes_flag_run(const void* planes, int rows, int K, unsigned* flag, hipStream_t st) {
+  if (!planes || !flag || rows <= 0 || K <= 0) return KL_EINVAL;
+  if (K % 32 || !aligned16(planes)) return KL_EUNSUPP;
+  const size_t tiles = static_cast<size_t>((rows + 15) / 16) * (K / 32);
+  const int grid = static_cast<int>(std::min<size_t>((tiles * 512 + 255) / 256, 4096));
+  hipLaunchKernelGGL(k_x6_planes_nonzero, dim3(grid), dim3(256), 0, st,
+                     static_cast<const unsigned*>(planes), rows, K, tiles, flag);
+  return launch_rc();
+}
+
 int kl::split3_run(const float* x, int rows, int cols, int ldx, void* planes, hipStream_t st) {
   if (!x || !planes || rows <= 0 || cols <= 0 || ldx < cols) return KL_EINVAL;
   if (cols % 32 || ldx % 4 || !aligned16(x) || !aligned16(planes)) return KL_EUNSUPP;
@@ -1453,13 +1467,36 @@ int kl_gemm_q8s(const float* A, int M, int K, int lda, const void* packed, int N
 int kl_gemm_x6(const void* a_planes, const void* w_planes, float* C, int M, int N, int K, int ldc,
                const float* bias, int accumulate, void* workspace, size_t workspace_bytes,
                void* stream) {
-  if (!C || N <= 0 || ldc < N) return KL_EINVAL;
+  return kl_gemm_x6w(a_planes, w_planes, 3, C, M, N, K, ldc, bias, accumulate, workspace,
+                     workspace_bytes, stream);
+}
+
+int kl_gemm_x6w(const void* a_planes, const void* w_planes, int w_planes_used, float* C, int M, int N,
+                int K, int ldc, const float* bias, int accumulate, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (!C || N <= 0 || ldc < N || (w_planes_used != 1 && w_planes_used != 3)) return KL_EINVAL;
   GemmX6Planes p{};
   p.A = a_planes;
   p.W[0] = w_planes;
+  p.w_planes = w_planes_used;
   const GemmSeg sg{nullptr, C, bias, N, K, ldc, 0};
   return gemm_run_x6(p, M, K, 1, &sg, accumulate, static_cast<float*>(workspace), workspace_bytes,
                      as_stream(stream));
+}
+
+int kl_x6_weight_planes(const void* w_planes, int N, int K, int* planes_used, void* stream) {
+  if (!planes_used) return KL_EINVAL;
+  unsigned* flag = nullptr;
+  if (hipMalloc(&flag, sizeof(unsigned)) != hipSuccess) return KL_ENOMEM;
+  hipStream_t st = as_stream(stream);
+  unsigned h = 0;
+  int r = rc(hipMemsetAsync(flag, 0, sizeof(unsigned), st));
+  if (r == KL_OK) r = x6_planes_flag_run(w_planes, N, K, flag, st);
+  if (r == KL_OK) r = rc(hipMemcpyAsync(&h, flag, sizeof(unsigned), hipMemcpyDeviceToHost, st));
+  if (r == KL_OK) r = rc(hipStreamSynchronize(st));
+  hipFree(flag);
+  if (r == KL_OK) *planes_used = h ? 3 : 1;
+  return r;
 }
 
 }  // extern "C"

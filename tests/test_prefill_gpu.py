@@ -272,6 +272,53 @@ def test_gemm_x6_refusals(K, gpu):
     assert K.lib.kl_split_bf16x3(dC.ptr, M, 80, 80, dP.ptr, None) == -4  # cols % 32
 
 
+def _bf16_exact(x):
+    """x rounded to the nearest bf16 value (ties to even), kept as fp32."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).reshape(np.shape(x))
+
+
+@pytest.mark.parametrize("M,N,Kd", [(37, 200, 96), (512, 2560, 4096), (300, 33000, 128), (1024, 1536, 1536)])
+def test_gemm_x6w_one_plane(K, gpu, M, N, Kd):
+    """bf16-exact W (as exported from bf16 checkpoints): kl_x6_weight_planes
+    finds planes 1 and 2 zero, and the one-plane product (three terms) gives
+    exactly kl_gemm_x6's values, with and without the split-K workspace (the
+    (300, 33000) shape runs the tail launch).  On W that is not bf16-exact the
+    planes are reported as needed, and the one-plane product drops their
+    terms (about 2^-9 of each product)."""
+    rng = np.random.default_rng(M + N + Kd)
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    Wf = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float32)
+    W = _bf16_exact(Wf)
+    dA, dW, dWf = _split_dev(K, A), _split_dev(K, W), _split_dev(K, Wf)
+    used = C.c_int(0)
+    ok(K.lib.kl_x6_weight_planes(dW.ptr, N, Kd, C.byref(used), None), "kl_x6_weight_planes")
+    assert used.value == 1
+    ok(K.lib.kl_x6_weight_planes(dWf.ptr, N, Kd, C.byref(used), None), "kl_x6_weight_planes")
+    assert used.value == 3
+    for ws in (False, True):
+        wsa = K.DeviceArray(8 * M * N) if ws else None
+        outs = []
+        for fn in ("x6", "x6w"):
+            dC = K.DeviceArray(M * N)
+            args = (dC.ptr, M, N, Kd, N, None, 0, wsa.ptr if wsa else None, wsa.nbytes if wsa else 0, None)
+            if fn == "x6":
+                ok(K.lib.kl_gemm_x6(dA.ptr, dW.ptr, *args), "kl_gemm_x6")
+            else:
+                ok(K.lib.kl_gemm_x6w(dA.ptr, dW.ptr, 1, *args), "kl_gemm_x6w")
+            outs.append(dC.numpy().reshape(M, N))
+        assert np.array_equal(outs[0], outs[1]), (ws, np.max(np.abs(outs[0] - outs[1])))
+    # not bf16-exact: the one-plane product leaves out W's planes 1 and 2
+    d6, d1 = K.DeviceArray(M * N), K.DeviceArray(M * N)
+    ok(K.lib.kl_gemm_x6(dA.ptr, dWf.ptr, d6.ptr, M, N, Kd, N, None, 0, None, 0, None), "kl_gemm_x6")
+    ok(K.lib.kl_gemm_x6w(dA.ptr, dWf.ptr, 1, d1.ptr, M, N, Kd, N, None, 0, None, 0, None), "kl_gemm_x6w")
+    y6, y1 = d6.numpy().reshape(M, N), d1.numpy().reshape(M, N)
+    mag = np.abs(A).astype(np.float64) @ np.abs(Wf).astype(np.float64).T
+    assert np.max(np.abs(y1 - y6) / mag) > 1e-6 and np.max(np.abs(y1 - y6) / mag) < 2 ** -8
+    assert K.lib.kl_gemm_x6w(dA.ptr, dW.ptr, 2, d1.ptr, M, N, Kd, N, None, 0, None, 0, None) == -1
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
 def test_gemm_splitk_vs_oracle(K, O, gpu, splits):
     rng = np.random.default_rng(splits)
@@ -530,6 +577,41 @@ def test_engine_prefill_small_chunks_vs_oracle(K, O, gpu, monkeypatch, name):
         ref2 = om.step(tok, pos)
         assert rel(lg2, ref2) < LOGIT_RTOL
         tok = O.argmax(ref2)
+
+
+@pytest.mark.parametrize("name", ["tiny_llama3", "tiny_qwen3", "qwen3_shape"])
+def test_engine_prefill_bf16_exact_weights(K, O, gpu, name):
+    """An image whose weights are all bf16 values (every float past the
+    header rounded to bf16): the engine finds every projection's planes 1 and
+    2 zero and runs the one-plane products; the prompt's last logits and cache
+    rows against the oracle on the same image."""
+    if name == "qwen3_shape":
+        cfg = K.BASELINE["qwen3_4b"].with_(name="qwen3_shape_bf16", layers=2, hidden_dim=1024,
+                                           vocab=2048, norm_std=0.1)
+        P = 512
+    else:
+        cfg = K.TINY[name]
+        P = 40
+    img = K.synth_image(cfg).copy()
+    body = img[256:256 + (img.size - 256) // 4 * 4].view(np.float32)
+    img[256:256 + body.size * 4] = _bf16_exact(body).view(np.uint8)
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    eng = K.Engine(img, cfg)
+    nxt, lg, ms = eng.prefill(prompt)
+    om = O.Model(img, cfg.family, cfg.quant)
+    ref = om.prompt(prompt) if P > 64 else None
+    if ref is None:
+        for pos in range(P - 1):
+            om.step(prompt[pos], pos)
+        ref = om.step(prompt[P - 1], P - 1)
+    r = rel(lg, ref)
+    print(f"{name} bf16-exact weights: prefill P={P} in {ms:.2f} ms, logits rel err {r:.2e}", flush=True)
+    assert r < LOGIT_RTOL
+    for layer in (0, cfg.layers - 1):
+        for pos in (0, P - 1):
+            for which_v in (False, True):
+                a, b = eng.kv_row(layer, pos, which_v), om.kv_row(layer, pos, which_v)
+                assert np.max(np.abs(a - b)) <= 1e-5 * max(np.max(np.abs(b)), 1.0)
 
 
 def _prefill_cfg(K, name):
