@@ -1658,7 +1658,7 @@ int prefill_planes(kl_engine* e, int last_rows) {
   std::vector<unsigned> h(nf, 1u);
   if (r == KL_OK) r = rc(hipMemcpyAsync(h.data(), flags, nf * sizeof(unsigned), hipMemcpyDeviceToHost, hs));
   if (r == KL_OK) r = rc(hipStreamSynchronize(hs));
-  hipFree(flags);
+  (void)hipFree(flags);
   for (int l = 0; l < m.L && r == KL_OK; ++l)
     for (int i = 0; i < 7; ++i)
       if (h[7 * l + i] == 0) e->layers[l].xp.one |= 1u << i;

@@ -1494,7 +1494,7 @@ int kl_x6_weight_planes(const void* w_planes, int N, int K, int* planes_used, vo
   if (r == KL_OK) r = x6_planes_flag_run(w_planes, N, K, flag, st);
   if (r == KL_OK) r = rc(hipMemcpyAsync(&h, flag, sizeof(unsigned), hipMemcpyDeviceToHost, st));
   if (r == KL_OK) r = rc(hipStreamSynchronize(st));
-  hipFree(flag);
+  (void)hipFree(flag);
   if (r == KL_OK) *planes_used = h ? 3 : 1;
   return r;
 }
