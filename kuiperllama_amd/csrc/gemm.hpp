@@ -1234,6 +1234,24 @@ __global__ void k_q8s_split(const float* __restrict__ x, int M, int K, int ldx, 
 // C_s = sum of the split partials in split order (+ bias_s) (+ C_s), over
 // every output s of the launch: element i of a split's slab belongs to the
 // output whose [M][N_s] block (at seg[s].wsoff) holds it.
+// p[0] + p[stride] + ... + p[(splits - 1) stride], added in that order (the
+// bits of a plain loop), with the loads issued eight at a time ahead of their
+// adds: a loop that waits for each partial before requesting the next pays one
+// memory latency per split.
+template <class T>
+__device__ __forceinline__ T split_sum(const T* p, size_t stride, int splits) {
+  T v = p[0];
+  for (int z = 1; z < splits; z += 8) {
+    T t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = p[static_cast<size_t>(min(z + j, splits - 1)) * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (z + j < splits) v += t[j];
+  }
+  return v;
+}
+
 __global__ void k_gemm_reduce(GemmArgs g) {
   const size_t total = g.ws_split;
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
@@ -1251,8 +1269,7 @@ __global__ void k_gemm_reduce(GemmArgs g) {
         ldc = g.seg[k].ldc;
         off = g.seg[k].wsoff;
       }
-    float v = g.ws[i];
-    for (int z = 1; z < g.splits; ++z) v += g.ws[static_cast<size_t>(z) * total + i];
+    float v = split_sum(g.ws + i, total, g.splits);
     const size_t local = i - off;
     const int m = static_cast<int>(local / N), n = static_cast<int>(local - static_cast<size_t>(m) * N);
     if (bias) v += bias[n];

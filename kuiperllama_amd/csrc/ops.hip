@@ -1303,9 +1303,7 @@ __global__ __launch_bounds__(256) void k_norm_planes(float* x, const float* __re
       v[j] = xr[i];
       if (splits > 0) {
         const f4* p = reinterpret_cast<const f4*>(ws + static_cast<size_t>(row) * n) + i;
-        f4 sum = p[0];
-        for (int z = 1; z < splits; ++z) sum += p[z * (ws_split / 4)];
-        v[j] = v[j] + sum;
+        v[j] = v[j] + split_sum(p, ws_split / 4, splits);
         xr[i] = v[j];
       }
     }
@@ -1335,12 +1333,8 @@ __global__ void k_swiglu_planes(const float* __restrict__ h1, const float* __res
     const size_t o = static_cast<size_t>(r) * F + c;
     f4 a, b;
     if (splits > 0) {
-      a = *reinterpret_cast<const f4*>(ws + o);
-      b = *reinterpret_cast<const f4*>(ws + wsoff3 + o);
-      for (int z = 1; z < splits; ++z) {
-        a += *reinterpret_cast<const f4*>(ws + z * ws_split + o);
-        b += *reinterpret_cast<const f4*>(ws + z * ws_split + wsoff3 + o);
-      }
+      a = split_sum(reinterpret_cast<const f4*>(ws + o), ws_split / 4, splits);
+      b = split_sum(reinterpret_cast<const f4*>(ws + wsoff3 + o), ws_split / 4, splits);
     } else {
       a = *reinterpret_cast<const f4*>(h1 + o);
       b = *reinterpret_cast<const f4*>(h3 + o);
