@@ -1714,6 +1714,7 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
     float* vc = e->vcache + l * kv_layer;
     float* krow = kc + static_cast<size_t>(pos0) * Dkv;
     float* vrow = vc + static_cast<size_t>(pos0) * Dkv;
+    int dqkv = 1;  // Q/K/V splits left unsummed
     // Split-K where the launch would leave CUs idle (int8, at most 32 rows);
     // every split's partials fit pf_ws (prefill_scratch).  Groups of at least
     // 32 run the direct-to-LDS int8 kernel (5 workgroups per CU).
@@ -1734,7 +1735,9 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
         PF(norm_planes_run(e->pf_x, Ld.rms_att, n, D, e->eps, e->pf_ws, pend, nD, e->pf_ax, q8s, hs));
         pend = 0;
         const void* wx[3] = {Ld.xp.q, Ld.xp.k, Ld.xp.v};
-        gemm_fast(D, 3, sg, wx, 0, nullptr, (Ld.xp.one & 7u) == 7u);
+        // Short int8 prompts leave Q/K/V's split-K partials to the rotation
+        // (one pass summing and rotating them); Qwen3's q/k norm needs the sums first.
+        gemm_fast(D, 3, sg, wx, 0, q8s && e->transform != 2 ? &dqkv : nullptr, (Ld.xp.one & 7u) == 7u);
       } else {
         PF(kl_rmsnorm_rows(e->pf_x, Ld.rms_att, e->pf_xn, n, D, e->eps, st));
         const int sp = splits_for(Dq + 2 * Dkv, D, true);
@@ -1749,8 +1752,13 @@ int prefill_chunk(kl_engine* e, int pos0, int n) {
         PF(kl_rmsnorm_rows(e->pf_q, Ld.qn, e->pf_q, n * H, hd, 1e-6f, st));
         PF(kl_rmsnorm_rows(krow, Ld.kn, krow, n * KVH, hd, 1e-6f, st));
       }
-      PF(kl_rope_rows(e->rope_style, Dq, Dkv, hd, e->pf_q, Dq, krow, Dkv, pos0, n, e->sin_t,
-                      e->cos_t, st));
+      if (dqkv > 1)
+        PF(qkv_sum_rope_run(e->rope_style, Dq, Dkv, hd, e->pf_ws, dqkv,
+                            static_cast<size_t>(n) * (Dq + 2 * static_cast<size_t>(Dkv)), Ld.bq, Ld.bk, Ld.bv,
+                            e->pf_q, Dq, krow, Dkv, vrow, Dkv, pos0, n, e->sin_t, e->cos_t, hs));
+      else
+        PF(kl_rope_rows(e->rope_style, Dq, Dkv, hd, e->pf_q, Dq, krow, Dkv, pos0, n, e->sin_t,
+                        e->cos_t, st));
     }
     // attention_mha (llama3.cpp:651-669), then x += Wo . att
     PF(kl_attn_prefill_ws(pos0, n, H, H / KVH, hd, e->pf_q, Dq, kc, vc, Dkv, e->pf_att, Dq,

@@ -116,6 +116,14 @@ int norm_planes_run(float* x, const float* w, int rows, int n, float eps, const 
                     size_t ws_split, void* planes, bool q8s, hipStream_t st);
 int swiglu_planes_run(const float* h1, const float* h3, int rows, int F, const float* ws, int splits,
                       size_t ws_split, size_t wsoff3, void* planes, bool q8s, hipStream_t st);
+// The partials of a grouped Q/K/V launch over n rows left unsummed (segments q
+// [n x dim], k and v [n x kv_dim] at ws + z ws_split): q, k and v summed in
+// split order plus their biases (k_gemm_reduce's arithmetic), q and k rotated
+// at positions pos0 + r (kl_rope_rows's rotation), all three stored.
+int qkv_sum_rope_run(int style, int dim, int kv_dim, int hd, const float* ws, int splits, size_t ws_split,
+                     const float* bq, const float* bk, const float* bv, float* q, int ldq, float* k, int ldk,
+                     float* v, int ldv, int pos0, int n, const float* sin_t, const float* cos_t,
+                     hipStream_t st);
 // x[rows x n] += the sum of `splits` partial slabs of rows x n at ws (k_gemm_reduce).
 int partials_add_run(float* x, int rows, int n, const float* ws, int splits, hipStream_t st);
 

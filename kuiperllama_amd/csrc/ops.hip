@@ -211,12 +211,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_b(const float* __restrict_
 // ---------------------------------------------------------------------------
 // RoPE: one thread per rotated pair of q (and of k where the index < kv_dim).
 // ---------------------------------------------------------------------------
-// Rotates pair p of q (and of k where the reference does) at position pos.
-__device__ __forceinline__ void rope_one(int style, int kv_dim, int hd, float* q, float* k, int pos,
-                                         int p, const float* __restrict__ sin_t,
-                                         const float* __restrict__ cos_t) {
+// Pair p's two indices and its sin/cos table column.
+__device__ __forceinline__ void rope_index(int style, int hd, int p, int& i0, int& i1, int& tab) {
   const int half = hd / 2;
-  int i0, i1, tab;
   if (style == KL_ROPE_INTERLEAVED) {
     i0 = 2 * p;
     i1 = i0 + 1;
@@ -227,6 +224,14 @@ __device__ __forceinline__ void rope_one(int style, int kv_dim, int hd, float* q
     i1 = i0 + half;
     tab = 2 * j;
   }
+}
+
+// Rotates pair p of q (and of k where the reference does) at position pos.
+__device__ __forceinline__ void rope_one(int style, int kv_dim, int hd, float* q, float* k, int pos,
+                                         int p, const float* __restrict__ sin_t,
+                                         const float* __restrict__ cos_t) {
+  int i0, i1, tab;
+  rope_index(style, hd, p, i0, i1, tab);
   const float fci = sin_t[static_cast<size_t>(pos) * hd + tab];
   const float fcr = cos_t[static_cast<size_t>(pos) * hd + tab];
   float v0 = q[i0], v1 = q[i1];
@@ -1348,6 +1353,78 @@ __global__ void k_swiglu_planes(const float* __restrict__ h1, const float* __res
     }
     planes_store4(q8s, planes, r, c, F, out);
   }
+}
+
+// q, k and v of a grouped Q/K/V launch summed from its split-K partials
+// (ws + z ws_split, segments at 0, n dim and n (dim + kv_dim), rows of dim /
+// kv_dim / kv_dim), in split order plus the bias -- k_gemm_reduce's
+// arithmetic -- then q and k rotated as k_rope_rows rotates them, and all
+// three stored: one pass in place of the reduction and the rotation (same
+// bits).  Thread p of row r owns q's pair p, k's pair p where rope_one
+// rotates it (which covers every k element), and v elements 2p, 2p + 1.
+__global__ void k_qkv_sum_rope_rows(int style, int dim, int kv_dim, int hd, const float* __restrict__ ws,
+                                    int splits, size_t ws_split, const float* __restrict__ bq,
+                                    const float* __restrict__ bk, const float* __restrict__ bv, float* q,
+                                    int ldq, float* k, int ldk, float* v, int ldv, int pos0, int n,
+                                    const float* __restrict__ sin_t, const float* __restrict__ cos_t) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.y;
+  if (p >= dim / 2 || r >= n) return;
+  int i0, i1, tab;
+  rope_index(style, hd, p, i0, i1, tab);
+  const int pos = pos0 + r;
+  const float fci = sin_t[static_cast<size_t>(pos) * hd + tab];
+  const float fcr = cos_t[static_cast<size_t>(pos) * hd + tab];
+  const float* pq = ws + static_cast<size_t>(r) * dim;
+  float v0 = split_sum(pq + i0, ws_split, splits), v1 = split_sum(pq + i1, ws_split, splits);
+  if (bq) {
+    v0 += bq[i0];
+    v1 += bq[i1];
+  }
+  rope_pair(v0, v1, fcr, fci);
+  float* qr = q + static_cast<size_t>(r) * ldq;
+  qr[i0] = v0;
+  qr[i1] = v1;
+  const int gate = style == KL_ROPE_INTERLEAVED ? i0 : (i0 - (i0 % hd));
+  if (gate < kv_dim) {
+    const float* pk = ws + static_cast<size_t>(n) * dim + static_cast<size_t>(r) * kv_dim;
+    float w0 = split_sum(pk + i0, ws_split, splits), w1 = split_sum(pk + i1, ws_split, splits);
+    if (bk) {
+      w0 += bk[i0];
+      w1 += bk[i1];
+    }
+    rope_pair(w0, w1, fcr, fci);
+    float* kr = k + static_cast<size_t>(r) * ldk;
+    kr[i0] = w0;
+    kr[i1] = w1;
+  }
+  if (2 * p < kv_dim) {
+    const float* pv = ws + static_cast<size_t>(n) * (dim + kv_dim) + static_cast<size_t>(r) * kv_dim;
+    float* vr = v + static_cast<size_t>(r) * ldv;
+#pragma unroll
+    for (int e = 2 * p; e < 2 * p + 2; ++e) {
+      float x = split_sum(pv + e, ws_split, splits);
+      if (bv) x += bv[e];
+      vr[e] = x;
+    }
+  }
+}
+
+int kl::qkv_sum_rope_run(int style, int dim, int kv_dim, int hd, const float* ws, int splits,
+                         size_t ws_split, const float* bq, const float* bk, const float* bv, float* q,
+                         int ldq, float* k, int ldk, float* v, int ldv, int pos0, int n,
+                         const float* sin_t, const float* cos_t, hipStream_t st) {
+  if (!ws || !q || !k || !v || !sin_t || !cos_t || splits < 1 || n <= 0 || n > 65535 || pos0 < 0 ||
+      hd <= 0 || hd % 2 || dim <= 0 || kv_dim <= 0 || kv_dim > dim || dim % hd || kv_dim % hd ||
+      ldq < dim || ldk < kv_dim || ldv < kv_dim ||
+      ws_split < static_cast<size_t>(n) * (dim + 2 * static_cast<size_t>(kv_dim)))
+    return KL_EINVAL;
+  if (style != KL_ROPE_INTERLEAVED && style != KL_ROPE_HALF) return KL_EINVAL;
+  const int pairs = dim / 2;
+  hipLaunchKernelGGL(k_qkv_sum_rope_rows, dim3((pairs + 255) / 256, n), dim3(256), 0, st, style, dim,
+                     kv_dim, hd, ws, splits, ws_split, bq, bk, bv, q, ldq, k, ldk, v, ldv, pos0, n, sin_t,
+                     cos_t);
+  return launch_rc();
 }
 
 int kl::norm_planes_run(float* x, const float* w, int rows, int n, float eps, const float* ws,

@@ -656,6 +656,41 @@ def test_engine_prefill_vs_oracle(K, O, gpu, name):
         tok = O.argmax(ref2)
 
 
+@pytest.mark.parametrize("shape", ["llama2_7b_q8", "qwen25_15b"])
+def test_engine_prefill_q8_short_prompt_vs_oracle(K, O, gpu, shape):
+    """A 32-token int8 prompt (the short-prompt int8 GEMMs, split along K) on
+    two layers of a full-width shape: Llama2-7B (interleaved RoPE) and
+    Qwen2.5-1.5B with int8 weights (QKV bias, rotate-half RoPE).  Q/K/V's
+    partials are summed, biased and rotated in one pass.  Last logits, cache
+    rows and four decode steps against the oracle."""
+    cfg = K.BASELINE[shape].with_(name=f"{shape}_int8_2l", layers=2, vocab=2048, group_size=64,
+                                  norm_std=0.1, tied=False)  # int8 images keep their classifier
+    assert cfg.quant
+    img = K.synth_image(cfg)
+    P = 32
+    prompt = [int(t) for t in K.prompt_tokens(cfg, P)]
+    eng = K.Engine(img, cfg)
+    nxt, lg, ms = eng.prefill(prompt)
+    om = O.Model(img, cfg.family, cfg.quant)
+    for pos in range(P - 1):
+        om.step(prompt[pos], pos)
+    ref = om.step(prompt[P - 1], P - 1)
+    r = rel(lg, ref)
+    print(f"{cfg.name}: prefill P={P} logits rel err {r:.2e}, {ms:.3f} ms", flush=True)
+    assert r < LOGIT_RTOL
+    for layer in (0, cfg.layers - 1):
+        for pos in (0, 17, P - 1):
+            for which_v in (False, True):
+                a, b = eng.kv_row(layer, pos, which_v), om.kv_row(layer, pos, which_v)
+                assert np.max(np.abs(a - b)) <= 1e-5 * max(np.max(np.abs(b)), 1.0), (layer, pos, which_v)
+    tok = O.argmax(ref)
+    for pos in range(P, P + 4):
+        _, lg2 = eng.step(tok, pos)
+        ref2 = om.step(tok, pos)
+        assert rel(lg2, ref2) < LOGIT_RTOL
+        tok = O.argmax(ref2)
+
+
 def test_qwen3_shape_prefill_512_vs_oracle(K, O, gpu):
     """cfg 5's layer shape (Qwen3: dim 2560, 32 Q / 8 KV heads of 128, q/k
     norms) at 2 layers with non-unit norm weights: the 512-token prompt as one
